@@ -1,0 +1,216 @@
+/*
+ * qmoe.h -- C ABI of the MI355X MoE-layer library (libqmoe.so).
+ *
+ * The entry points replace the MoE layer of the reference C port:
+ *   c/src/model.c:1281-1405  moe_forward (the layer)
+ *   c/src/model.c:1301-1318  router: gemm_bf16 + kernel_topk_indices + renorm
+ *   c/src/model.c:1321-1367  unique experts + per-expert token gather
+ *   c/src/model.c:1368-1375  routed SwiGLU FFN (gemm_fp32 x3, silu, mul)
+ *   c/src/model.c:1376-1403  weighted combine + sigmoid-gated shared expert
+ * and follow the conventions of c/src/kernel.h and c/src/util.h:
+ *   - row-major tensors, y[M,N] = x[M,K] . W[N,K]^T (weight rows are
+ *     output features), caller-owned outputs that are overwritten;
+ *   - q4 weights are MLX affine 4-bit: uint32 words of 8 nibbles, low nibble
+ *     first (kernel.h:46-50), one bf16 scale and one bf16 bias per group of
+ *     `group_size` input columns, w = q*scale + bias;
+ *   - every function returns 0 on success or -1 with a message in `err`
+ *     (mirrors err_t, util.h:11-27); nothing aborts.
+ *
+ * Pointers passed to the stage and layer functions are DEVICE pointers
+ * (hipMalloc'd or torch CUDA tensors).  Work is enqueued on `stream`
+ * (a hipStream_t; NULL = the null stream) and is asynchronous: the caller
+ * synchronises.  A context is not thread-safe: calls on one context must
+ * not overlap (they share the context's scratch buffers).
+ *
+ * Weights stay resident in HBM in the checkpoint layout; there is no expert
+ * cache and no streaming (the reference's SSD path, model.c:536-674).
+ */
+#ifndef QMOE_H
+#define QMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct qmoe_ctx qmoe_ctx;
+
+/* error message buffer, as err_t (c/src/util.h:11-13) */
+typedef struct {
+    char msg[512];
+} qmoe_err;
+
+/* activation element types */
+enum { QMOE_F32 = 0, QMOE_BF16 = 1 };
+
+/* qmoe_layer_forward flags */
+enum {
+    QMOE_RESIDUAL = 1 /* out = x + moe(x) (x un-normalised) */
+};
+
+/* Layer shape, from the checkpoint's text_config (c/src/model.c:39-154).
+ * The reference requires the shared expert's intermediate size to equal
+ * moe_intermediate_size (model.c:1391-1395 passes moe_inter as N). */
+typedef struct {
+    int hidden;      /* H: hidden_size; multiple of group_size */
+    int n_experts;   /* E: num_experts, <= 1024 */
+    int top_k;       /* k: num_experts_per_tok, 1 <= k <= min(E, 64) */
+    int moe_inter;   /* I: moe_intermediate_size; multiple of group_size */
+    int group_size;  /* g: quantization group size; must be 64 */
+    int n_layers;    /* number of resident layers */
+    int max_tokens;  /* largest n accepted per call; sizes the scratch */
+    float rms_eps;   /* pre-router RMSNorm epsilon (used only when norm_w is set) */
+} qmoe_config;
+
+/* One layer's tensors in the checkpoint layout (names: model.c:541-547 and
+ * 1902-1923).  Shapes use the config letters above; G = H/g, GI = I/g. */
+typedef struct {
+    const uint16_t *router_w;   /* [E,H]     bf16  mlp.gate.weight */
+    const float *router_bias;   /* [E]       f32   optional logit bias, or NULL */
+    const uint32_t *gate_q;     /* [E,I,H/8] u32   mlp.switch_mlp.gate_proj.weight */
+    const uint16_t *gate_s;     /* [E,I,G]   bf16  .scales */
+    const uint16_t *gate_b;     /* [E,I,G]   bf16  .biases */
+    const uint32_t *up_q;       /* [E,I,H/8]       mlp.switch_mlp.up_proj.* */
+    const uint16_t *up_s;
+    const uint16_t *up_b;
+    const uint32_t *down_q;     /* [E,H,I/8]       mlp.switch_mlp.down_proj.* */
+    const uint16_t *down_s;     /* [E,H,GI] */
+    const uint16_t *down_b;
+    const uint32_t *sh_gate_q;  /* [I,H/8]         mlp.shared_expert.gate_proj.* */
+    const uint16_t *sh_gate_s;  /* [I,G] */
+    const uint16_t *sh_gate_b;
+    const uint32_t *sh_up_q;    /* [I,H/8]         mlp.shared_expert.up_proj.* */
+    const uint16_t *sh_up_s;
+    const uint16_t *sh_up_b;
+    const uint32_t *sh_down_q;  /* [H,I/8]         mlp.shared_expert.down_proj.* */
+    const uint16_t *sh_down_s;  /* [H,GI] */
+    const uint16_t *sh_down_b;
+    const uint16_t *sh_gate_w;  /* [H]       bf16  mlp.shared_expert_gate.weight */
+    const float *norm_w;        /* [H]       f32   optional pre-router RMSNorm weight, or NULL */
+} qmoe_layer_weights;
+
+/* ------------------------------------------------------------ context */
+
+/* Allocates the context, its scratch (sized by max_tokens) on the current
+ * HIP device.  Layers are empty until uploaded, bound or synthesised. */
+int qmoe_create(qmoe_ctx **ctx, const qmoe_config *cfg, qmoe_err *err);
+void qmoe_destroy(qmoe_ctx *ctx);
+
+/* Copies one layer from HOST memory (checkpoint layout) into HBM.
+ * Replaces mw_load + experts_load (model.c:213-272, 536-674). */
+int qmoe_upload_layer(qmoe_ctx *ctx, int layer, const qmoe_layer_weights *host, qmoe_err *err);
+
+/* Fills one layer in HBM with the seeded synthetic distribution used by the
+ * benchmarks: codes U{0..15}, scales N(0,0.02), biases N(0,0.01) (bf16),
+ * router and shared-expert gate N(0,0.02) (bf16), norm weight ones when
+ * with_norm.  router_bias (host, [E] f32) may be NULL.  No counterpart in
+ * the reference (which loads checkpoints); used where no checkpoint exists. */
+int qmoe_synth_layer(qmoe_ctx *ctx, int layer, uint64_t seed, int with_norm,
+                     const float *router_bias, qmoe_err *err);
+
+/* Device pointers of a resident layer (for callers that run the stage
+ * functions themselves or inspect weights). */
+int qmoe_layer_device_weights(qmoe_ctx *ctx, int layer, qmoe_layer_weights *out, qmoe_err *err);
+
+/* Fills `count` elements of device memory with the synthetic stream
+ * (seed, layer, tag) starting at element `start`: kind 0 = bf16 normal,
+ * 1 = f32 normal, 2 = u32 codes.  Bench/test helper without a reference
+ * counterpart. */
+int qmoe_synth_fill(void *dst, size_t count, int kind, uint64_t seed, uint32_t layer,
+                    uint32_t tag, uint64_t start, float stddev, void *stream, qmoe_err *err);
+
+/* synthetic stream tags */
+enum {
+    QMOE_TAG_ROUTER_W = 1,
+    QMOE_TAG_GATE_Q = 2, QMOE_TAG_GATE_S = 3, QMOE_TAG_GATE_B = 4,
+    QMOE_TAG_UP_Q = 5, QMOE_TAG_UP_S = 6, QMOE_TAG_UP_B = 7,
+    QMOE_TAG_DOWN_Q = 8, QMOE_TAG_DOWN_S = 9, QMOE_TAG_DOWN_B = 10,
+    QMOE_TAG_SH_GATE_Q = 11, QMOE_TAG_SH_GATE_S = 12, QMOE_TAG_SH_GATE_B = 13,
+    QMOE_TAG_SH_UP_Q = 14, QMOE_TAG_SH_UP_S = 15, QMOE_TAG_SH_UP_B = 16,
+    QMOE_TAG_SH_DOWN_Q = 17, QMOE_TAG_SH_DOWN_S = 18, QMOE_TAG_SH_DOWN_B = 19,
+    QMOE_TAG_SHGATE_W = 20,
+    QMOE_TAG_X = 22
+};
+
+/* ------------------------------------------------------------ stages */
+
+/* (1) Router, model.c:1301-1318 (+ the shared-expert gate dot, model.c:1396).
+ *   x [n,H] (x_dtype); when the layer has norm_w, x is RMS-normalised first
+ *   (kernel.c:10-20) and the normalised rows are written to xn_out [n,H] f32
+ *   (may be NULL).
+ *   logits_out [n,E] f32 (may be NULL): x.Wr^T (+ router_bias), reduction in
+ *   a fixed order, so selection is reproducible bit for bit.
+ *   idx_out [n,k] i32: top-k experts, value descending, ties to the lower id.
+ *   w_out [n,k] f32: softmax over the selected logits (renormalised top-k).
+ *   shared_gate_out [n] f32: sigmoid(x . w_sg). */
+int qmoe_router(qmoe_ctx *ctx, int layer, const void *x, int x_dtype, int n, float *logits_out,
+                int32_t *idx_out, float *w_out, float *shared_gate_out, float *xn_out,
+                void *stream, qmoe_err *err);
+
+/* (2) Dispatch, model.c:1321-1367: stable counting sort of the flat slots
+ *   f = t*k+s by expert.  offsets_out [E+1]: expert e's slots are
+ *   perm_out[offsets[e] .. offsets[e+1]), tokens ascending.
+ *   unique_out [1+E]: unique_out[0] = U, then the U experts that received
+ *   tokens, ascending (model.c:1321-1332 lists them first-seen). */
+int qmoe_dispatch(qmoe_ctx *ctx, const int32_t *idx, int n, int32_t *offsets_out,
+                  int32_t *perm_out, int32_t *unique_out, void *stream, qmoe_err *err);
+
+/* (3) Expert SwiGLU FFN, model.c:1368-1375 and the shared expert
+ *   model.c:1388-1395, as two grouped kernels:
+ *   gate/up:  h[p] = silu(x[t].Wg_e^T) * (x[t].Wu_e^T)   -> h_out [n*k+n, I]
+ *   down:     y[p] = h[p].Wd_e^T                         -> y_out [n*k+n, H]
+ *   Row p < n*k belongs to slot perm[p] (expert e with offsets[e] <= p <
+ *   offsets[e+1]); rows n*k+t are the shared expert on token t.
+ *   x is the router input (xn_out of qmoe_router when the layer has a norm). */
+int qmoe_expert_gateup(qmoe_ctx *ctx, int layer, const void *x, int x_dtype, int n,
+                       const int32_t *perm, const int32_t *offsets, const int32_t *unique,
+                       float *h_out, void *stream, qmoe_err *err);
+int qmoe_expert_down(qmoe_ctx *ctx, int layer, const float *h, int n, const int32_t *perm,
+                     const int32_t *offsets, const int32_t *unique, float *y_out, void *stream,
+                     qmoe_err *err);
+/* both of the above */
+int qmoe_expert_ffn(qmoe_ctx *ctx, int layer, const void *x, int x_dtype, int n,
+                    const int32_t *perm, const int32_t *offsets, const int32_t *unique,
+                    float *y_out, void *stream, qmoe_err *err);
+
+/* (4) Combine, model.c:1376-1403:
+ *   out[t] = sum over t's slots in ascending expert order of w[t,s]*y[pos]
+ *            + shared_gate[t] * y[n*k+t]   (+ x[t] with QMOE_RESIDUAL)
+ *   where pos is the position of slot t*k+s in perm. */
+int qmoe_combine(qmoe_ctx *ctx, const float *y, const int32_t *perm, const float *w,
+                 const float *shared_gate, int n, const void *x_residual, int x_dtype,
+                 float *out, void *stream, qmoe_err *err);
+
+/* The whole layer (stages 1-4) on device buffers; the drop-in for the call
+ * at model.c:1712.  x [n,H] (x_dtype), out [n,H] f32.  flags: QMOE_RESIDUAL. */
+int qmoe_layer_forward(qmoe_ctx *ctx, int layer, const void *x, int x_dtype, int n, float *out,
+                       int flags, void *stream, qmoe_err *err);
+
+/* Copies the routing of the last qmoe_layer_forward call on this context
+ * (n must be that call's token count) into caller device buffers, any of
+ * which may be NULL: idx [n,k], w [n,k], shared_gate [n], offsets [E+1],
+ * perm [n*k], unique [1+E].  An inspection hook for tests and tools; the
+ * reference keeps these in moe_forward's scratch (model.c:1288-1300). */
+int qmoe_last_routing(qmoe_ctx *ctx, int n, int32_t *idx_out, float *w_out, float *shared_gate_out,
+                      int32_t *offsets_out, int32_t *perm_out, int32_t *unique_out, void *stream,
+                      qmoe_err *err);
+
+/* Host-memory shim with moe_forward's data contract (model.c:1281-1282):
+ * x [n,H] f32 host in, out [n,H] f32 host out, synchronous.  The caller's
+ * scratch is not needed (the context owns device scratch). */
+int qmoe_moe_forward_host(qmoe_ctx *ctx, int layer, const float *x, int n, float *out,
+                          qmoe_err *err);
+
+/* Size in bytes of the context's device scratch and of one resident layer. */
+size_t qmoe_scratch_bytes(const qmoe_ctx *ctx);
+size_t qmoe_layer_bytes(const qmoe_ctx *ctx);
+
+/* Library version string. */
+const char *qmoe_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,642 @@
+/*
+ * moe_oracle.c -- CPU restatement of the reference C port's MoE layer.
+ * TEST INFRASTRUCTURE ONLY (see moe_oracle.h for scope, citations and the
+ * deliberate departures).  Built with -ffp-contract=off: every fused
+ * multiply-add below is an explicit fmaf(), so the arithmetic is the same on
+ * any x86-64 host.
+ */
+#define _POSIX_C_SOURCE 199309L
+#include "moe_oracle.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <time.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------ bf16 */
+
+/* c/src/util.h:56-61: widen by a 16-bit shift */
+float orc_bf16_to_f32(uint16_t h) {
+    uint32_t bits = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* c/src/util.h:63-71: round to nearest even on the upper 16 bits, no NaN
+ * special case */
+uint16_t orc_f32_to_bf16(float f) {
+    uint32_t bits;
+    memcpy(&bits, &f, 4);
+    uint32_t hi = bits >> 16;
+    uint32_t lo = bits & 0xffffu;
+    if (lo > 0x8000u || (lo == 0x8000u && (hi & 1u))) hi++;
+    return (uint16_t)hi;
+}
+
+/* ----------------------------------------------------------- elementwise */
+
+float orc_silu(float v) { return v / (1.0f + expf(-v)); }     /* kernel.c:38-43 */
+float orc_sigmoid(float v) { return 1.0f / (1.0f + expf(-v)); } /* kernel.c:45-47 */
+
+/* kernel.c:10-20 verbatim in arithmetic: sequential sum of squares,
+ * r = 1/sqrt(ss/n + eps), y = x*r*w (two roundings, left to right) */
+void orc_rmsnorm_seq(const float *x, const float *w, size_t n, float eps, float *y) {
+    float ss = 0.0f;
+    for (size_t i = 0; i < n; i++) ss = fmaf(x[i], x[i], ss);
+    float r = 1.0f / sqrtf(ss / (float)n + eps);
+    for (size_t i = 0; i < n; i++) y[i] = w ? (x[i] * r) * w[i] : x[i] * r;
+}
+
+/* ------------------------------------------------------------ R64 order
+ * A length-K reduction is split into 8-element chunks; chunk c belongs to
+ * leaf (c mod 64).  Each leaf is an fma chain over its chunks in ascending
+ * order starting from +0.0f.  The 64 leaves are then combined by a
+ * butterfly (p[l] += p[l^o] for o = 32,16,...,1), which is the pairwise tree
+ * over leaves in bit-reversed order.  A 64-lane wavefront that loads one
+ * 16-byte bf16 chunk per lane and reduces with xor shuffles computes exactly
+ * this value in every lane. */
+static float r64_combine(float *p) {
+    for (int o = 32; o >= 1; o >>= 1) {
+        float q[64];
+        for (int l = 0; l < 64; l++) q[l] = p[l] + p[l ^ o];
+        memcpy(p, q, sizeof(q));
+    }
+    return p[0];
+}
+
+/* chunk c covers elements [8c, min(8c+8, K)) */
+float orc_dot_r64_bf16w(const float *x, const uint16_t *w, int K) {
+    float p[64];
+    int chunks = (K + 7) / 8;
+    for (int l = 0; l < 64; l++) {
+        float acc = 0.0f;
+        for (int c = l; c < chunks; c += 64)
+            for (int j = 8 * c; j < 8 * c + 8 && j < K; j++)
+                acc = fmaf(x[j], orc_bf16_to_f32(w[j]), acc);
+        p[l] = acc;
+    }
+    return r64_combine(p);
+}
+
+float orc_sumsq_r64(const float *x, int K) {
+    float p[64];
+    int chunks = (K + 7) / 8;
+    for (int l = 0; l < 64; l++) {
+        float acc = 0.0f;
+        for (int c = l; c < chunks; c += 64)
+            for (int j = 8 * c; j < 8 * c + 8 && j < K; j++) acc = fmaf(x[j], x[j], acc);
+        p[l] = acc;
+    }
+    return r64_combine(p);
+}
+
+/* kernel.c:10-20 with the sum of squares in R64 order */
+void orc_rmsnorm_r64(const float *x, const float *w, size_t n, float eps, float *y) {
+    float ss = orc_sumsq_r64(x, (int)n);
+    float r = 1.0f / sqrtf(ss / (float)n + eps);
+    for (size_t i = 0; i < n; i++) y[i] = w ? (x[i] * r) * w[i] : x[i] * r;
+}
+
+/* ----------------------------------------------------------------- top-k */
+
+/* kernel.c:114-138: quickselect with the middle element as pivot, Lomuto
+ * partition on strict '>' so the k largest end up in idx[0..k) */
+static void quickselect_kth(const float *x, int *idx, int n, int k) {
+    int lo = 0, hi = n;
+    for (;;) {
+        int mid = lo + (hi - lo) / 2;
+        float pv = x[idx[mid]];
+        int t = idx[mid];
+        idx[mid] = idx[hi - 1];
+        idx[hi - 1] = t;
+        int store = lo;
+        for (int i = lo; i < hi - 1; i++) {
+            if (x[idx[i]] > pv) {
+                t = idx[i];
+                idx[i] = idx[store];
+                idx[store] = t;
+                store++;
+            }
+        }
+        t = idx[store];
+        idx[store] = idx[hi - 1];
+        idx[hi - 1] = t;
+        if (store == k - 1) return;
+        if (store < k - 1)
+            lo = store + 1;
+        else
+            hi = store;
+    }
+}
+
+/* kernel.c:140-150 */
+void orc_topk_quickselect(const float *x, int n, int k, int *out) {
+    if (k >= n) {
+        for (int i = 0; i < n; i++) out[i] = i;
+        return;
+    }
+    int *idx = (int *)malloc((size_t)n * sizeof(int));
+    for (int i = 0; i < n; i++) idx[i] = i;
+    quickselect_kth(x, idx, n, k);
+    memcpy(out, idx, (size_t)k * sizeof(int));
+    free(idx);
+}
+
+/* a precedes b: larger value first, equal values (with -0 == +0) by lower id */
+static int canon_before(float va, int ia, float vb, int ib) {
+    if (va > vb) return 1;
+    if (va < vb) return 0;
+    return ia < ib;
+}
+
+/* canonical top-k: k passes of "best remaining" (value desc, id asc) */
+void orc_topk_canonical(const float *x, int n, int k, int *out) {
+    if (k > n) k = n;
+    unsigned char *taken = (unsigned char *)calloc((size_t)n, 1);
+    for (int s = 0; s < k; s++) {
+        int best = -1;
+        for (int i = 0; i < n; i++) {
+            if (taken[i]) continue;
+            if (best < 0 || canon_before(x[i] + 0.0f, i, x[best] + 0.0f, best)) best = i;
+        }
+        taken[best] = 1;
+        out[s] = best;
+    }
+    free(taken);
+}
+
+/* -------------------------------------------------------------------- q4 */
+
+/* kernel.c:152-173.  The reference writes q*s + b inside one expression;
+ * Apple clang contracts it (-ffp-contract=on), so it is restated as fmaf. */
+void orc_dequant_q4_f32sb(const uint32_t *q, const float *scales, const float *biases,
+                          size_t rows, size_t cols, size_t group_size, float *out) {
+    size_t words = cols / 8, groups = cols / group_size;
+    for (size_t r = 0; r < rows; r++) {
+        const uint32_t *qr = q + r * words;
+        for (size_t c = 0; c < cols; c++) {
+            size_t g = c / group_size;
+            uint32_t v = qr[c / 8];
+            float code = (float)((v >> (4 * (c % 8))) & 0xFu);
+            out[r * cols + c] = fmaf(code, scales[r * groups + g], biases[r * groups + g]);
+        }
+    }
+}
+
+void orc_dequant_q4(const uint32_t *q, const uint16_t *scales, const uint16_t *biases,
+                    size_t rows, size_t cols, size_t group_size, float *out) {
+    size_t groups = cols / group_size;
+    float *s = (float *)malloc(rows * groups * sizeof(float));
+    float *b = (float *)malloc(rows * groups * sizeof(float));
+    for (size_t i = 0; i < rows * groups; i++) {
+        s[i] = orc_bf16_to_f32(scales[i]);
+        b[i] = orc_bf16_to_f32(biases[i]);
+    }
+    orc_dequant_q4_f32sb(q, s, b, rows, cols, group_size, out);
+    free(s);
+    free(b);
+}
+
+/* kernel.c:181-186: C[M,N] = A[M,K] W[N,K]^T, sequential fma over k */
+void orc_gemm_fp32(int M, int N, int K, const float *A, const float *W, float *C) {
+    for (int m = 0; m < M; m++)
+        for (int n = 0; n < N; n++) {
+            float acc = 0.0f;
+            for (int k = 0; k < K; k++) acc = fmaf(A[(size_t)m * K + k], W[(size_t)n * K + k], acc);
+            C[(size_t)m * N + n] = acc;
+        }
+}
+
+/* kernel.c:190-228 in naive form */
+void orc_gemm_bf16(int M, int N, int K, const float *A, const uint16_t *W, float *C) {
+    for (int m = 0; m < M; m++)
+        for (int n = 0; n < N; n++) {
+            float acc = 0.0f;
+            for (int k = 0; k < K; k++)
+                acc = fmaf(A[(size_t)m * K + k], orc_bf16_to_f32(W[(size_t)n * K + k]), acc);
+            C[(size_t)m * N + n] = acc;
+        }
+}
+
+/* One output of gemm_q4 (kernel.c:239-246, 289-305): per group
+ * xq = sum x*q (fma chain), acc += s*xq + b*xsum.  Under Apple clang's
+ * contraction the group update is acc + fma(s, xq, b*xsum). */
+static float q4_row_dot(const float *a, const float *xsum, const uint32_t *w, const float *s,
+                        const float *b, int K, int gs) {
+    int groups = K / gs, wpg = gs / 8;
+    float acc = 0.0f;
+    for (int g = 0; g < groups; g++) {
+        float xq = 0.0f;
+        const float *ag = a + (size_t)g * gs;
+        for (int wd = 0; wd < wpg; wd++) {
+            uint32_t v = w[g * wpg + wd];
+            for (int i = 0; i < 8; i++) xq = fmaf(ag[wd * 8 + i], (float)((v >> (4 * i)) & 0xFu), xq);
+        }
+        acc = acc + fmaf(s[g], xq, b[g] * xsum[g]);
+    }
+    return acc;
+}
+
+static void group_sums(const float *a, int K, int gs, float *xsum) {
+    for (int g = 0; g < K / gs; g++) {
+        float s = 0.0f;
+        for (int i = 0; i < gs; i++) s += a[(size_t)g * gs + i];
+        xsum[g] = s;
+    }
+}
+
+void orc_gemm_q4_f32sb(int M, int N, int K, const float *A, const uint32_t *W,
+                       const float *scales, const float *biases, int group_size, float *C) {
+    if (M <= 0 || N <= 0) return;
+    int groups = K / group_size;
+    float *xsum = (float *)malloc((size_t)groups * sizeof(float));
+    for (int m = 0; m < M; m++) {
+        const float *a = A + (size_t)m * K;
+        group_sums(a, K, group_size, xsum);
+        for (int n = 0; n < N; n++)
+            C[(size_t)m * N + n] = q4_row_dot(a, xsum, W + (size_t)n * (K / 8),
+                                              scales + (size_t)n * groups,
+                                              biases + (size_t)n * groups, K, group_size);
+    }
+    free(xsum);
+}
+
+void orc_gemm_q4(int M, int N, int K, const float *A, const uint32_t *W,
+                 const uint16_t *scales, const uint16_t *biases, int group_size, float *C) {
+    size_t ng = (size_t)N * (K / group_size);
+    float *s = (float *)malloc(ng * sizeof(float));
+    float *b = (float *)malloc(ng * sizeof(float));
+    for (size_t i = 0; i < ng; i++) {
+        s[i] = orc_bf16_to_f32(scales[i]);
+        b[i] = orc_bf16_to_f32(biases[i]);
+    }
+    orc_gemm_q4_f32sb(M, N, K, A, W, s, b, group_size, C);
+    free(s);
+    free(b);
+}
+
+/* -------------------------------------------------------------- dispatch */
+
+/* Stable counting sort of flat slots f = t*k + s by expert id.  Because the
+ * k experts of one token are distinct, "t ascending within an expert" and
+ * "f ascending within an expert" are the same order. */
+int orc_dispatch(const int *idx, int n, int k, int E, int *offsets, int *perm, int *pos,
+                 int *active) {
+    int *cnt = (int *)calloc((size_t)E + 1, sizeof(int));
+    for (int f = 0; f < n * k; f++) cnt[idx[f]]++;
+    offsets[0] = 0;
+    for (int e = 0; e < E; e++) offsets[e + 1] = offsets[e] + cnt[e];
+    int na = 0;
+    for (int e = 0; e < E; e++)
+        if (cnt[e]) active[na++] = e;
+    memcpy(cnt, offsets, (size_t)E * sizeof(int));
+    for (int f = 0; f < n * k; f++) {
+        int p = cnt[idx[f]]++;
+        perm[p] = f;
+        if (pos) pos[f] = p;
+    }
+    free(cnt);
+    return na;
+}
+
+/* ----------------------------------------------------------------- layer */
+
+static int check_layer(const orc_layer *L, int n, char *err) {
+    int H = L->hidden, E = L->n_experts, k = L->top_k, I = L->moe_inter, g = L->group_size;
+    if (n < 0 || H <= 0 || E <= 0 || k <= 0 || k > E || I <= 0 || g <= 0 || g % 8 ||
+        H % g || I % g || H % 8) {
+        if (err) snprintf(err, 512, "bad layer shape H=%d E=%d k=%d I=%d g=%d n=%d", H, E, k, I, g, n);
+        return -1;
+    }
+    return 0;
+}
+
+static void load_x(const void *x, int x_is_bf16, size_t count, float *dst) {
+    if (x_is_bf16) {
+        const uint16_t *xb = (const uint16_t *)x;
+        for (size_t i = 0; i < count; i++) dst[i] = orc_bf16_to_f32(xb[i]);
+    } else {
+        memcpy(dst, x, count * sizeof(float));
+    }
+}
+
+/* router for one token: model.c:1301-1318 with departures 1, 2, 4 */
+static void route_token(const orc_layer *L, const float *xn, float *logits, float *gate_logit,
+                        int *idx, float *w, float *shared_gate) {
+    int H = L->hidden, E = L->n_experts, k = L->top_k;
+    for (int e = 0; e < E; e++) {
+        float v = orc_dot_r64_bf16w(xn, L->router_w + (size_t)e * H, H);
+        if (L->router_bias) v = v + L->router_bias[e];
+        logits[e] = v;
+    }
+    float gl = orc_dot_r64_bf16w(xn, L->sh_gate_w, H);
+    if (gate_logit) *gate_logit = gl;
+    if (shared_gate) *shared_gate = orc_sigmoid(gl);
+    orc_topk_canonical(logits, E, k, idx);
+    /* model.c:1305-1318: softmax over the selected logits */
+    float mx = -1e30f;
+    for (int s = 0; s < k; s++)
+        if (logits[idx[s]] > mx) mx = logits[idx[s]];
+    float sum = 0.0f;
+    for (int s = 0; s < k; s++) {
+        w[s] = expf(logits[idx[s]] - mx);
+        sum += w[s];
+    }
+    for (int s = 0; s < k; s++) w[s] /= sum;
+}
+
+int orc_route(const orc_layer *L, const void *x, int x_is_bf16, int n, float *logits_out,
+              float *gate_logit_out, int *idx_out, float *w_out, float *shared_gate_out,
+              float *xn_out, int n_threads, char *err) {
+    if (check_layer(L, n, err)) return -1;
+    int H = L->hidden, E = L->n_experts, k = L->top_k;
+#ifdef _OPENMP
+    if (n_threads > 0) omp_set_num_threads(n_threads);
+#else
+    (void)n_threads;
+#endif
+#pragma omp parallel
+    {
+        float *xn = (float *)malloc((size_t)H * sizeof(float));
+        float *lg = (float *)malloc((size_t)E * sizeof(float));
+        int *id = (int *)malloc((size_t)k * sizeof(int));
+        float *wt = (float *)malloc((size_t)k * sizeof(float));
+#pragma omp for schedule(static)
+        for (int t = 0; t < n; t++) {
+            load_x(x_is_bf16 ? (const void *)((const uint16_t *)x + (size_t)t * H)
+                             : (const void *)((const float *)x + (size_t)t * H),
+                   x_is_bf16, (size_t)H, xn);
+            if (L->norm_w) orc_rmsnorm_r64(xn, L->norm_w, (size_t)H, L->rms_eps, xn);
+            float gl, sg;
+            route_token(L, xn, lg, &gl, id, wt, &sg);
+            if (logits_out) memcpy(logits_out + (size_t)t * E, lg, (size_t)E * sizeof(float));
+            if (gate_logit_out) gate_logit_out[t] = gl;
+            if (idx_out) memcpy(idx_out + (size_t)t * k, id, (size_t)k * sizeof(int));
+            if (w_out) memcpy(w_out + (size_t)t * k, wt, (size_t)k * sizeof(float));
+            if (shared_gate_out) shared_gate_out[t] = sg;
+            if (xn_out) memcpy(xn_out + (size_t)t * H, xn, (size_t)H * sizeof(float));
+        }
+        free(xn);
+        free(lg);
+        free(id);
+        free(wt);
+    }
+    return 0;
+}
+
+/* routed expert row dot, faithful mode: dequantise the row to fp32 with
+ * fma(q,s,b) (model.c:603-662 + kernel.c:157-172) and take the fp32 dot
+ * product (gemm_fp32, kernel.c:181-186) as one fma chain over k */
+static float faithful_row_dot(const float *a, const uint32_t *q, const uint16_t *s,
+                              const uint16_t *b, int K, int gs) {
+    float acc = 0.0f;
+    for (int c = 0; c < K; c++) {
+        int g = c / gs;
+        float code = (float)((q[c / 8] >> (4 * (c % 8))) & 0xFu);
+        float w = fmaf(code, orc_bf16_to_f32(s[g]), orc_bf16_to_f32(b[g]));
+        acc = fmaf(a[c], w, acc);
+    }
+    return acc;
+}
+
+static float q4_row_dot_bf16sb(const float *a, const float *xsum, const uint32_t *q,
+                               const uint16_t *s, const uint16_t *b, int K, int gs) {
+    float sf[1024], bf[1024];
+    int groups = K / gs;
+    float *sp = sf, *bp = bf;
+    if (groups > 1024) {
+        sp = (float *)malloc((size_t)groups * sizeof(float));
+        bp = (float *)malloc((size_t)groups * sizeof(float));
+    }
+    for (int g = 0; g < groups; g++) {
+        sp[g] = orc_bf16_to_f32(s[g]);
+        bp[g] = orc_bf16_to_f32(b[g]);
+    }
+    float r = q4_row_dot(a, xsum, q, sp, bp, K, gs);
+    if (sp != sf) {
+        free(sp);
+        free(bp);
+    }
+    return r;
+}
+
+/* One SwiGLU expert on one token row: model.c:1368-1375 (routed) or
+ * model.c:1388-1395 (shared, via linear_forward -> gemm_q4). */
+static void expert_ffn_token(const float *xrow, const float *xsum_h, int H, int I, int gs,
+                             const uint32_t *gq, const uint16_t *gsc, const uint16_t *gb,
+                             const uint32_t *uq, const uint16_t *usc, const uint16_t *ub,
+                             const uint32_t *dq, const uint16_t *dsc, const uint16_t *db,
+                             int faithful, float *hbuf, float *xsum_i, float *yrow) {
+    size_t wrow_h = (size_t)H / 8, grow_h = (size_t)H / gs;
+    size_t wrow_i = (size_t)I / 8, grow_i = (size_t)I / gs;
+    for (int r = 0; r < I; r++) {
+        float g, u;
+        if (faithful) {
+            g = faithful_row_dot(xrow, gq + r * wrow_h, gsc + r * grow_h, gb + r * grow_h, H, gs);
+            u = faithful_row_dot(xrow, uq + r * wrow_h, usc + r * grow_h, ub + r * grow_h, H, gs);
+        } else {
+            g = q4_row_dot_bf16sb(xrow, xsum_h, gq + r * wrow_h, gsc + r * grow_h, gb + r * grow_h, H, gs);
+            u = q4_row_dot_bf16sb(xrow, xsum_h, uq + r * wrow_h, usc + r * grow_h, ub + r * grow_h, H, gs);
+        }
+        hbuf[r] = orc_silu(g) * u; /* kernel_silu then kernel_mul */
+    }
+    if (!faithful) group_sums(hbuf, I, gs, xsum_i);
+    for (int c = 0; c < H; c++) {
+        if (faithful)
+            yrow[c] = faithful_row_dot(hbuf, dq + c * wrow_i, dsc + c * grow_i, db + c * grow_i, I, gs);
+        else
+            yrow[c] = q4_row_dot_bf16sb(hbuf, xsum_i, dq + c * wrow_i, dsc + c * grow_i,
+                                        db + c * grow_i, I, gs);
+    }
+}
+
+int orc_moe_forward(const orc_layer *L, const void *x, int n, float *out, const orc_opts *opt,
+                    const int *token_sel, int n_sel, float *logits_out, float *gate_logit_out,
+                    int *idx_out, float *w_out, float *shared_gate_out, float *xn_out, char *err) {
+    if (check_layer(L, n, err)) return -1;
+    orc_opts o = {0, 0, ORC_ROUTED_FAITHFUL, 0};
+    if (opt) o = *opt;
+    int H = L->hidden, E = L->n_experts, k = L->top_k, I = L->moe_inter, gs = L->group_size;
+    if (n == 0) return 0;
+    float *xn = (float *)malloc((size_t)n * H * sizeof(float));
+    float *logits = (float *)malloc((size_t)n * E * sizeof(float));
+    float *gl = (float *)malloc((size_t)n * sizeof(float));
+    int *idx = (int *)malloc((size_t)n * k * sizeof(int));
+    float *wts = (float *)malloc((size_t)n * k * sizeof(float));
+    float *sg = (float *)malloc((size_t)n * sizeof(float));
+    if (orc_route(L, x, o.x_is_bf16, n, logits, gl, idx, wts, sg, xn, o.n_threads, err)) return -1;
+    if (logits_out) memcpy(logits_out, logits, (size_t)n * E * sizeof(float));
+    if (gate_logit_out) memcpy(gate_logit_out, gl, (size_t)n * sizeof(float));
+    if (idx_out) memcpy(idx_out, idx, (size_t)n * k * sizeof(int));
+    if (w_out) memcpy(w_out, wts, (size_t)n * k * sizeof(float));
+    if (shared_gate_out) memcpy(shared_gate_out, sg, (size_t)n * sizeof(float));
+    if (xn_out) memcpy(xn_out, xn, (size_t)n * H * sizeof(float));
+
+    if (out) {
+        int nout = token_sel ? n_sel : n;
+        int faithful = o.routed_mode == ORC_ROUTED_FAITHFUL;
+        size_t eq = (size_t)I * (H / 8), es = (size_t)I * (H / gs);
+        size_t dqs = (size_t)H * (I / 8), dss = (size_t)H * (I / gs);
+        /* Each selected token is independent (the layer is per-token); its
+         * expert contributions are accumulated in ascending expert order,
+         * matching the dispatch order (departure 3), then the shared expert
+         * (model.c:1376-1403).  out += w*r is contracted to fma by Apple
+         * clang, so it is written as fmaf. */
+#pragma omp parallel
+        {
+            float *hbuf = (float *)malloc((size_t)I * sizeof(float));
+            float *yrow = (float *)malloc((size_t)H * sizeof(float));
+            float *xs_h = (float *)malloc((size_t)(H / gs) * sizeof(float));
+            float *xs_i = (float *)malloc((size_t)(I / gs) * sizeof(float));
+            int *ord = (int *)malloc((size_t)k * sizeof(int));
+#pragma omp for schedule(dynamic, 1)
+            for (int j = 0; j < nout; j++) {
+                int t = token_sel ? token_sel[j] : j;
+                const float *xr = xn + (size_t)t * H;
+                float *orow = out + (size_t)j * H;
+                for (int c = 0; c < H; c++) orow[c] = 0.0f;
+                group_sums(xr, H, gs, xs_h);
+                /* slots of token t sorted by expert id */
+                for (int s = 0; s < k; s++) ord[s] = s;
+                for (int a = 1; a < k; a++)
+                    for (int b2 = a; b2 > 0 && idx[(size_t)t * k + ord[b2 - 1]] > idx[(size_t)t * k + ord[b2]]; b2--) {
+                        int tmp = ord[b2];
+                        ord[b2] = ord[b2 - 1];
+                        ord[b2 - 1] = tmp;
+                    }
+                for (int a = 0; a < k; a++) {
+                    int s = ord[a];
+                    int e = idx[(size_t)t * k + s];
+                    expert_ffn_token(xr, xs_h, H, I, gs, L->gate_q + e * eq, L->gate_s + e * es,
+                                     L->gate_b + e * es, L->up_q + e * eq, L->up_s + e * es,
+                                     L->up_b + e * es, L->down_q + e * dqs, L->down_s + e * dss,
+                                     L->down_b + e * dss, faithful, hbuf, xs_i, yrow);
+                    float wt = wts[(size_t)t * k + s];
+                    for (int c = 0; c < H; c++) orow[c] = fmaf(wt, yrow[c], orow[c]);
+                }
+                /* shared expert: linear_forward -> gemm_q4 (model.c:1388-1395) */
+                expert_ffn_token(xr, xs_h, H, I, gs, L->sh_gate_q, L->sh_gate_s, L->sh_gate_b,
+                                 L->sh_up_q, L->sh_up_s, L->sh_up_b, L->sh_down_q, L->sh_down_s,
+                                 L->sh_down_b, 0, hbuf, xs_i, yrow);
+                float g = sg[t];
+                for (int c = 0; c < H; c++) orow[c] = fmaf(g, yrow[c], orow[c]);
+                if (o.residual) { /* the un-normalised input row plus the layer output */
+                    load_x(o.x_is_bf16 ? (const void *)((const uint16_t *)x + (size_t)t * H)
+                                       : (const void *)((const float *)x + (size_t)t * H),
+                           o.x_is_bf16, (size_t)H, yrow);
+                    for (int c = 0; c < H; c++) orow[c] = yrow[c] + orow[c];
+                }
+            }
+            free(hbuf);
+            free(yrow);
+            free(xs_h);
+            free(xs_i);
+            free(ord);
+        }
+    }
+    free(xn);
+    free(logits);
+    free(gl);
+    free(idx);
+    free(wts);
+    free(sg);
+    return 0;
+}
+
+/* ------------------------------------------------------------ generators */
+
+/* splitmix64 output function (Steele, Lea, Flood 2014; constants as
+ * published by Vigna) */
+uint64_t orc_mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+#define GOLDEN64 0x9E3779B97F4A7C15ull
+
+uint64_t orc_tensor_key(uint64_t seed, uint32_t layer, uint32_t tag) {
+    return orc_mix64(orc_mix64(seed + GOLDEN64) ^ (((uint64_t)layer << 32) | (uint64_t)tag));
+}
+
+/* element i of a stream: splitmix64 in counter mode */
+static inline uint64_t stream_u64(uint64_t key, uint64_t i) { return orc_mix64(key + (i + 1) * GOLDEN64); }
+
+/* Box-Muller in double from draws 2i and 2i+1; cosine branch only */
+static inline double stream_normal(uint64_t key, uint64_t i) {
+    uint64_t r1 = stream_u64(key, 2 * i), r2 = stream_u64(key, 2 * i + 1);
+    double u1 = (double)((r1 >> 11) + 1) * 0x1.0p-53; /* (0,1] */
+    double u2 = (double)(r2 >> 11) * 0x1.0p-53;       /* [0,1) */
+    return sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+}
+
+void orc_gen_normal_f32(float *out, size_t count, uint64_t key, uint64_t start, float stddev) {
+#pragma omp parallel for schedule(static) if (count > 65536)
+    for (size_t i = 0; i < count; i++) out[i] = (float)(stream_normal(key, start + i) * (double)stddev);
+}
+
+void orc_gen_normal_bf16(uint16_t *out, size_t count, uint64_t key, uint64_t start, float stddev) {
+#pragma omp parallel for schedule(static) if (count > 65536)
+    for (size_t i = 0; i < count; i++)
+        out[i] = orc_f32_to_bf16((float)(stream_normal(key, start + i) * (double)stddev));
+}
+
+/* eight uniform 4-bit codes per word: the high half of the stream value */
+void orc_gen_codes(uint32_t *out, size_t count, uint64_t key, uint64_t start) {
+#pragma omp parallel for schedule(static) if (count > 65536)
+    for (size_t i = 0; i < count; i++) out[i] = (uint32_t)(stream_u64(key, start + i) >> 32);
+}
+
+void orc_zipf_bias(float *bias, int E, double s, double scale, uint64_t seed) {
+    int *perm = (int *)malloc((size_t)E * sizeof(int));
+    for (int i = 0; i < E; i++) perm[i] = i;
+    uint64_t key = orc_mix64(seed ^ 0x5A17F00Dull);
+    for (int i = E - 1; i > 0; i--) {
+        int j = (int)(stream_u64(key, (uint64_t)i) % (uint64_t)(i + 1));
+        int t = perm[i];
+        perm[i] = perm[j];
+        perm[j] = t;
+    }
+    double z = 0.0;
+    for (int r = 1; r <= E; r++) z += pow((double)r, -s);
+    for (int e = 0; e < E; e++) {
+        double p = pow((double)(perm[e] + 1), -s) / z;
+        bias[e] = (float)(scale * log(p));
+    }
+    free(perm);
+}
+
+/* ------------------------------------------------------------ timing */
+
+static double now_s(void) { /* util.h:73-77 */
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + (double)ts.tv_nsec * 1e-9;
+}
+
+static int cmp_dbl(const void *a, const void *b) {
+    double x = *(const double *)a, y = *(const double *)b;
+    return (x > y) - (x < y);
+}
+
+double orc_time_forward(const orc_layer *L, const void *x, int n, float *out, const orc_opts *opt,
+                        int warmup, int iters) {
+    char err[512];
+    for (int i = 0; i < warmup; i++) orc_moe_forward(L, x, n, out, opt, NULL, 0, 0, 0, 0, 0, 0, 0, err);
+    if (iters < 1) iters = 1;
+    double *t = (double *)malloc((size_t)iters * sizeof(double));
+    for (int i = 0; i < iters; i++) {
+        double t0 = now_s();
+        orc_moe_forward(L, x, n, out, opt, NULL, 0, 0, 0, 0, 0, 0, 0, err);
+        t[i] = now_s() - t0;
+    }
+    qsort(t, (size_t)iters, sizeof(double), cmp_dbl);
+    double med = t[iters / 2];
+    free(t);
+    return med;
+}

@@ -1,0 +1,167 @@
+/*
+ * moe_oracle.h -- CPU restatement of the reference C port's MoE layer.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the HIP
+ * path and the timed CPU baseline.  Only tests/, __graft_entry__.smoke() and
+ * the cpu_baseline leg of bench.py may load it.  The product library
+ * (libqmoe.so) never links, calls or falls back to it.
+ *
+ * What it restates (reference paths relative to the reference checkout):
+ *   c/src/model.c:1281-1405   moe_forward (router, top-k, renorm, dispatch,
+ *                             per-expert SwiGLU, combine, shared expert)
+ *   c/src/kernel.c:10-20      kernel_rmsnorm
+ *   c/src/kernel.c:38-59      kernel_silu / kernel_sigmoid / kernel_mul
+ *   c/src/kernel.c:112-150    kth_largest + kernel_topk_indices (quickselect)
+ *   c/src/kernel.c:152-179    kernel_dequant_q4(_row)
+ *   c/src/kernel.c:181-186    gemm_fp32 (naive loops replace cblas_sgemm)
+ *   c/src/kernel.c:190-228    gemm_bf16 (naive loops replace BNNSMatMul)
+ *   c/src/kernel.c:230-309    gemm_q4 (per-group s*sum(xq) + b*sum(x) identity)
+ *   c/src/util.h:56-71        bf16 <-> f32 (shift widen, RNE narrow)
+ *   c/src/model.c:424-472,539-674  expert tensor layout [E,I,H/8] / [E,H,I/8]
+ *
+ * Deliberate departures (each is also a contract the GPU path keeps):
+ *   1. Router dot products use the fixed "R64" order (orc_dot_r64): 64
+ *      strided partial fma-chains over 8-element chunks, combined by a
+ *      bit-reversed pairwise tree.  The reference leaves the order to BNNS;
+ *      fixing it makes expert selection bit-exact across CPU and GPU.
+ *   2. Top-k order is canonical: value descending, ties to the lower expert
+ *      id (-0.0 counts as +0.0).  The reference quickselect returns the same
+ *      set whenever the k-th and (k+1)-th logits differ.
+ *   3. Dispatch order: experts ascending, tokens ascending within an expert
+ *      (the MLX order, src/colibri_runtime/model.py:433-441).  The C port's
+ *      first-seen expert order only changes the fp32 summation order of the
+ *      combine.
+ *   4. Optional per-expert router bias (fp32, added after the dot product,
+ *      before top-k and softmax).  NULL reproduces the reference.
+ *   5. Optional pre-router RMSNorm (kernel.c:10-20) with its sum of squares in
+ *      R64 order, and an optional residual add (out = x + moe(x)).
+ *
+ * Parity pins for every function are listed in tests/test_oracle.py.
+ */
+#ifndef MOE_ORACLE_H
+#define MOE_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- bf16 (c/src/util.h:56-71) ---- */
+float orc_bf16_to_f32(uint16_t h);
+uint16_t orc_f32_to_bf16(float f);
+
+/* ---- elementwise (c/src/kernel.c:10-20, 38-59) ---- */
+/* sequential sum of squares, exactly as kernel.c:12-14 */
+void orc_rmsnorm_seq(const float *x, const float *w, size_t n, float eps, float *y);
+/* R64-ordered sum of squares (departure 5); same formula otherwise */
+void orc_rmsnorm_r64(const float *x, const float *w, size_t n, float eps, float *y);
+float orc_silu(float v);
+float orc_sigmoid(float v);
+
+/* ---- fixed-order dot products (departure 1) ---- */
+float orc_dot_r64_bf16w(const float *x, const uint16_t *w, int K);
+float orc_sumsq_r64(const float *x, int K);
+
+/* ---- top-k ---- */
+/* faithful restatement of kth_largest / kernel_topk_indices (quickselect,
+ * middle pivot, Lomuto with strict '>'), order unspecified */
+void orc_topk_quickselect(const float *x, int n, int k, int *out);
+/* canonical order: value desc, id asc (departure 2) */
+void orc_topk_canonical(const float *x, int n, int k, int *out);
+
+/* ---- q4 (c/src/kernel.c:152-179, 230-309) ---- */
+/* scales/biases are given as bf16 (as stored on disk), widened exactly */
+void orc_dequant_q4(const uint32_t *q, const uint16_t *scales, const uint16_t *biases,
+                    size_t rows, size_t cols, size_t group_size, float *out);
+void orc_dequant_q4_f32sb(const uint32_t *q, const float *scales, const float *biases,
+                          size_t rows, size_t cols, size_t group_size, float *out);
+void orc_gemm_fp32(int M, int N, int K, const float *A, const float *W, float *C);
+void orc_gemm_bf16(int M, int N, int K, const float *A, const uint16_t *W, float *C);
+void orc_gemm_q4_f32sb(int M, int N, int K, const float *A, const uint32_t *W,
+                       const float *scales, const float *biases, int group_size, float *C);
+void orc_gemm_q4(int M, int N, int K, const float *A, const uint32_t *W,
+                 const uint16_t *scales, const uint16_t *biases, int group_size, float *C);
+
+/* ---- dispatch (departure 3) ---- */
+/* idx [n*k] -> offsets [E+1], perm [n*k] (flat t*k+s), pos [n*k] (inverse),
+ * active [E] (experts with tokens, ascending); returns the active count */
+int orc_dispatch(const int *idx, int n, int k, int E, int *offsets, int *perm, int *pos,
+                 int *active);
+
+/* ---- the layer ---- */
+typedef struct {
+    int hidden;       /* H */
+    int n_experts;    /* E */
+    int top_k;        /* k */
+    int moe_inter;    /* I (routed and shared; the C port requires equality) */
+    int group_size;   /* g */
+    float rms_eps;
+    const uint16_t *router_w;   /* [E,H] bf16   mlp.gate.weight */
+    const float *router_bias;   /* [E] f32 or NULL */
+    const uint32_t *gate_q;     /* [E,I,H/8]    switch_mlp.gate_proj.weight */
+    const uint16_t *gate_s, *gate_b;   /* [E,I,H/g] bf16 */
+    const uint32_t *up_q;
+    const uint16_t *up_s, *up_b;
+    const uint32_t *down_q;     /* [E,H,I/8]    switch_mlp.down_proj.weight */
+    const uint16_t *down_s, *down_b;   /* [E,H,I/g] */
+    const uint32_t *sh_gate_q;  /* [I,H/8]      shared_expert.gate_proj */
+    const uint16_t *sh_gate_s, *sh_gate_b;
+    const uint32_t *sh_up_q;
+    const uint16_t *sh_up_s, *sh_up_b;
+    const uint32_t *sh_down_q;  /* [H,I/8]      shared_expert.down_proj */
+    const uint16_t *sh_down_s, *sh_down_b;
+    const uint16_t *sh_gate_w;  /* [H] bf16     shared_expert_gate.weight */
+    const float *norm_w;        /* [H] f32 or NULL: pre-router RMSNorm */
+} orc_layer;
+
+enum {
+    ORC_ROUTED_FAITHFUL = 0, /* dequant to fp32 (fma(q,s,b)) + fp32 dot, as model.c:1368-1375 */
+    ORC_ROUTED_Q4 = 1        /* gemm_q4 identity for routed experts too */
+};
+
+typedef struct {
+    int x_is_bf16;   /* x element type: 0 = f32, 1 = bf16 */
+    int residual;    /* out = x + moe(x) */
+    int routed_mode; /* ORC_ROUTED_* */
+    int n_threads;   /* OpenMP threads, <= 0: runtime default */
+} orc_opts;
+
+/* Full layer for n tokens.  Any of the *_out pointers may be NULL.
+ *   logits_out [n,E] biased router logits, gate_logit_out [n],
+ *   idx_out [n,k] canonical order, w_out [n,k], shared_gate_out [n] (sigmoid),
+ *   xn_out [n,H] the router input (after RMSNorm when norm_w is set).
+ * token_sel: if non-NULL, only tokens token_sel[0..n_sel) produce an `out`
+ * row (out is then [n_sel,H]); routing outputs still cover all n tokens.
+ * Returns 0, or -1 with a message in err (512 bytes) on a shape error. */
+int orc_moe_forward(const orc_layer *L, const void *x, int n, float *out,
+                    const orc_opts *opt, const int *token_sel, int n_sel,
+                    float *logits_out, float *gate_logit_out, int *idx_out, float *w_out,
+                    float *shared_gate_out, float *xn_out, char *err);
+
+/* Router only (logits + top-k + renorm + shared gate), all n tokens. */
+int orc_route(const orc_layer *L, const void *x, int x_is_bf16, int n, float *logits_out,
+              float *gate_logit_out, int *idx_out, float *w_out, float *shared_gate_out,
+              float *xn_out, int n_threads, char *err);
+
+/* ---- seeded synthetic tensors (counter-based; the GPU generator in the
+ * product library produces the same values) ---- */
+uint64_t orc_mix64(uint64_t z);
+uint64_t orc_tensor_key(uint64_t seed, uint32_t layer, uint32_t tag);
+void orc_gen_normal_bf16(uint16_t *out, size_t count, uint64_t key, uint64_t start, float stddev);
+void orc_gen_normal_f32(float *out, size_t count, uint64_t key, uint64_t start, float stddev);
+void orc_gen_codes(uint32_t *out, size_t count, uint64_t key, uint64_t start);
+/* Zipf(s) router bias: bias[e] = ln p_{pi(e)}, p_r = r^-s / sum, pi = seeded
+ * Fisher-Yates permutation of 0..E-1, scaled by `scale` */
+void orc_zipf_bias(float *bias, int E, double s, double scale, uint64_t seed);
+
+/* ---- CPU baseline timing ---- */
+/* times `iters` forward passes after `warmup` ones; returns median seconds */
+double orc_time_forward(const orc_layer *L, const void *x, int n, float *out,
+                        const orc_opts *opt, int warmup, int iters);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,378 @@
+"""ctypes binding of liboracle.so -- the CPU restatement of the reference
+C port's MoE layer (see moe_oracle.h for what it restates and where).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+the cpu_baseline leg of bench.py, as the checker.  The product library never
+loads it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liboracle.so")
+REF_UTIL_PATH = os.path.join(_HERE, "_ref", "libref_util.so")
+
+# synthetic stream tags, identical to include/qmoe.h QMOE_TAG_*
+TAG = dict(
+    ROUTER_W=1, GATE_Q=2, GATE_S=3, GATE_B=4, UP_Q=5, UP_S=6, UP_B=7, DOWN_Q=8, DOWN_S=9,
+    DOWN_B=10, SH_GATE_Q=11, SH_GATE_S=12, SH_GATE_B=13, SH_UP_Q=14, SH_UP_S=15, SH_UP_B=16,
+    SH_DOWN_Q=17, SH_DOWN_S=18, SH_DOWN_B=19, SHGATE_W=20, X=22,
+)
+
+ROUTED_FAITHFUL, ROUTED_Q4 = 0, 1
+
+_F = ctypes.c_float
+_I = ctypes.c_int
+_P = ctypes.c_void_p
+_U64 = ctypes.c_uint64
+_SZ = ctypes.c_size_t
+
+
+class OrcLayer(ctypes.Structure):
+    _fields_ = [
+        ("hidden", _I), ("n_experts", _I), ("top_k", _I), ("moe_inter", _I), ("group_size", _I),
+        ("rms_eps", _F),
+        ("router_w", _P), ("router_bias", _P),
+        ("gate_q", _P), ("gate_s", _P), ("gate_b", _P),
+        ("up_q", _P), ("up_s", _P), ("up_b", _P),
+        ("down_q", _P), ("down_s", _P), ("down_b", _P),
+        ("sh_gate_q", _P), ("sh_gate_s", _P), ("sh_gate_b", _P),
+        ("sh_up_q", _P), ("sh_up_s", _P), ("sh_up_b", _P),
+        ("sh_down_q", _P), ("sh_down_s", _P), ("sh_down_b", _P),
+        ("sh_gate_w", _P), ("norm_w", _P),
+    ]
+
+
+class OrcOpts(ctypes.Structure):
+    _fields_ = [("x_is_bf16", _I), ("residual", _I), ("routed_mode", _I), ("n_threads", _I)]
+
+
+_SIG = {
+    "orc_bf16_to_f32": (_F, [ctypes.c_uint16]),
+    "orc_f32_to_bf16": (ctypes.c_uint16, [_F]),
+    "orc_rmsnorm_seq": (None, [_P, _P, _SZ, _F, _P]),
+    "orc_rmsnorm_r64": (None, [_P, _P, _SZ, _F, _P]),
+    "orc_silu": (_F, [_F]),
+    "orc_sigmoid": (_F, [_F]),
+    "orc_dot_r64_bf16w": (_F, [_P, _P, _I]),
+    "orc_sumsq_r64": (_F, [_P, _I]),
+    "orc_topk_quickselect": (None, [_P, _I, _I, _P]),
+    "orc_topk_canonical": (None, [_P, _I, _I, _P]),
+    "orc_dequant_q4": (None, [_P, _P, _P, _SZ, _SZ, _SZ, _P]),
+    "orc_dequant_q4_f32sb": (None, [_P, _P, _P, _SZ, _SZ, _SZ, _P]),
+    "orc_gemm_fp32": (None, [_I, _I, _I, _P, _P, _P]),
+    "orc_gemm_bf16": (None, [_I, _I, _I, _P, _P, _P]),
+    "orc_gemm_q4_f32sb": (None, [_I, _I, _I, _P, _P, _P, _P, _I, _P]),
+    "orc_gemm_q4": (None, [_I, _I, _I, _P, _P, _P, _P, _I, _P]),
+    "orc_dispatch": (_I, [_P, _I, _I, _I, _P, _P, _P, _P]),
+    "orc_moe_forward": (_I, [ctypes.POINTER(OrcLayer), _P, _I, _P, ctypes.POINTER(OrcOpts), _P, _I,
+                             _P, _P, _P, _P, _P, _P, _P]),
+    "orc_route": (_I, [ctypes.POINTER(OrcLayer), _P, _I, _I, _P, _P, _P, _P, _P, _P, _I, _P]),
+    "orc_mix64": (_U64, [_U64]),
+    "orc_tensor_key": (_U64, [_U64, ctypes.c_uint32, ctypes.c_uint32]),
+    "orc_gen_normal_bf16": (None, [_P, _SZ, _U64, _U64, _F]),
+    "orc_gen_normal_f32": (None, [_P, _SZ, _U64, _U64, _F]),
+    "orc_gen_codes": (None, [_P, _SZ, _U64, _U64]),
+    "orc_zipf_bias": (None, [_P, _I, ctypes.c_double, ctypes.c_double, _U64]),
+    "orc_time_forward": (ctypes.c_double, [ctypes.POINTER(OrcLayer), _P, _I, _P,
+                                           ctypes.POINTER(OrcOpts), _I, _I]),
+}
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} missing: run `make -C oracle`")
+        _lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIG.items():
+            fn = getattr(_lib, name)
+            fn.restype = res
+            fn.argtypes = args
+    return _lib
+
+
+def ref_util():
+    """the reference's own util.h bf16 conversions, or None when not built"""
+    if not os.path.exists(REF_UTIL_PATH):
+        return None
+    r = ctypes.CDLL(REF_UTIL_PATH)
+    r.ref_bf16_to_f32.restype = _F
+    r.ref_bf16_to_f32.argtypes = [ctypes.c_uint16]
+    r.ref_f32_to_bf16.restype = ctypes.c_uint16
+    r.ref_f32_to_bf16.argtypes = [_F]
+    return r
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+# ------------------------------------------------------------- generators
+
+def tensor_key(seed, layer, tag):
+    return lib().orc_tensor_key(seed, layer, tag)
+
+
+def gen_bf16(count, seed, layer, tag, std, start=0):
+    out = np.empty(count, dtype=np.uint16)
+    lib().orc_gen_normal_bf16(_p(out), count, tensor_key(seed, layer, TAG[tag]), start, std)
+    return out
+
+
+def gen_f32(count, seed, layer, tag, std, start=0):
+    out = np.empty(count, dtype=np.float32)
+    lib().orc_gen_normal_f32(_p(out), count, tensor_key(seed, layer, TAG[tag]), start, std)
+    return out
+
+
+def gen_codes(count, seed, layer, tag, start=0):
+    out = np.empty(count, dtype=np.uint32)
+    lib().orc_gen_codes(_p(out), count, tensor_key(seed, layer, TAG[tag]), start)
+    return out
+
+
+def zipf_bias(E, s, scale, seed):
+    out = np.empty(E, dtype=np.float32)
+    lib().orc_zipf_bias(_p(out), E, s, scale, seed)
+    return out
+
+
+def bf16_to_f32(a):
+    """exact widening of bf16 bit patterns (uint16) to float32"""
+    return (np.asarray(a, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(a):
+    """round-to-nearest-even narrowing, as c/src/util.h:63-71 (vectorised)"""
+    b = np.asarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = (b + 0x7FFF + ((b >> 16) & 1)) >> 16
+    return (r & 0xFFFF).astype(np.uint16)
+
+
+class Layer:
+    """One synthetic layer in host memory, checkpoint layout, generated from
+    the same seeded streams as qmoe_synth_layer (codes U{0..15}, scales
+    N(0,0.02), biases N(0,0.01), router and shared gate N(0,0.02))."""
+
+    def __init__(self, H, E, k, I, seed=0, layer=0, with_norm=False, router_bias=None,
+                 group_size=64, eps=1e-6, only_experts=None):
+        self.H, self.E, self.k, self.I, self.g, self.eps = H, E, k, I, group_size, eps
+        G, GI = H // group_size, I // group_size
+        s, L = seed, layer
+        self.t = {}
+        self.t["router_w"] = gen_bf16(E * H, s, L, "ROUTER_W", 0.02)
+        self.t["router_bias"] = (None if router_bias is None
+                                 else np.ascontiguousarray(router_bias, dtype=np.float32))
+        if only_experts is None:
+            self.t["gate_q"] = gen_codes(E * I * H // 8, s, L, "GATE_Q")
+            self.t["gate_s"] = gen_bf16(E * I * G, s, L, "GATE_S", 0.02)
+            self.t["gate_b"] = gen_bf16(E * I * G, s, L, "GATE_B", 0.01)
+            self.t["up_q"] = gen_codes(E * I * H // 8, s, L, "UP_Q")
+            self.t["up_s"] = gen_bf16(E * I * G, s, L, "UP_S", 0.02)
+            self.t["up_b"] = gen_bf16(E * I * G, s, L, "UP_B", 0.01)
+            self.t["down_q"] = gen_codes(E * H * I // 8, s, L, "DOWN_Q")
+            self.t["down_s"] = gen_bf16(E * H * GI, s, L, "DOWN_S", 0.02)
+            self.t["down_b"] = gen_bf16(E * H * GI, s, L, "DOWN_B", 0.01)
+        else:
+            # sparse fill: only the listed experts get their real values (the
+            # streams are counter-based), everything else stays zero
+            self.t["gate_q"] = np.zeros(E * I * H // 8, np.uint32)
+            self.t["up_q"] = np.zeros(E * I * H // 8, np.uint32)
+            self.t["down_q"] = np.zeros(E * H * I // 8, np.uint32)
+            for nm in ("gate_s", "gate_b", "up_s", "up_b"):
+                self.t[nm] = np.zeros(E * I * G, np.uint16)
+            for nm in ("down_s", "down_b"):
+                self.t[nm] = np.zeros(E * H * GI, np.uint16)
+            qn, sn, dqn, dsn = I * H // 8, I * G, H * I // 8, H * GI
+            for e in sorted(set(int(v) for v in only_experts)):
+                for nm, tg in (("gate_q", "GATE_Q"), ("up_q", "UP_Q")):
+                    self.t[nm][e * qn:(e + 1) * qn] = gen_codes(qn, s, L, tg, start=e * qn)
+                self.t["down_q"][e * dqn:(e + 1) * dqn] = gen_codes(dqn, s, L, "DOWN_Q", start=e * dqn)
+                for nm, tg, sd in (("gate_s", "GATE_S", 0.02), ("gate_b", "GATE_B", 0.01),
+                                   ("up_s", "UP_S", 0.02), ("up_b", "UP_B", 0.01)):
+                    self.t[nm][e * sn:(e + 1) * sn] = gen_bf16(sn, s, L, tg, sd, start=e * sn)
+                for nm, tg, sd in (("down_s", "DOWN_S", 0.02), ("down_b", "DOWN_B", 0.01)):
+                    self.t[nm][e * dsn:(e + 1) * dsn] = gen_bf16(dsn, s, L, tg, sd, start=e * dsn)
+        self.t["sh_gate_q"] = gen_codes(I * H // 8, s, L, "SH_GATE_Q")
+        self.t["sh_gate_s"] = gen_bf16(I * G, s, L, "SH_GATE_S", 0.02)
+        self.t["sh_gate_b"] = gen_bf16(I * G, s, L, "SH_GATE_B", 0.01)
+        self.t["sh_up_q"] = gen_codes(I * H // 8, s, L, "SH_UP_Q")
+        self.t["sh_up_s"] = gen_bf16(I * G, s, L, "SH_UP_S", 0.02)
+        self.t["sh_up_b"] = gen_bf16(I * G, s, L, "SH_UP_B", 0.01)
+        self.t["sh_down_q"] = gen_codes(H * I // 8, s, L, "SH_DOWN_Q")
+        self.t["sh_down_s"] = gen_bf16(H * GI, s, L, "SH_DOWN_S", 0.02)
+        self.t["sh_down_b"] = gen_bf16(H * GI, s, L, "SH_DOWN_B", 0.01)
+        self.t["sh_gate_w"] = gen_bf16(H, s, L, "SHGATE_W", 0.02)
+        self.t["norm_w"] = np.ones(H, np.float32) if with_norm else None
+        self._build()
+
+    @classmethod
+    def from_arrays(cls, H, E, k, I, arrays, group_size=64, eps=1e-6):
+        self = cls.__new__(cls)
+        self.H, self.E, self.k, self.I, self.g, self.eps = H, E, k, I, group_size, eps
+        self.t = {}
+        for f in ("router_w", "router_bias", "gate_q", "gate_s", "gate_b", "up_q", "up_s", "up_b",
+                  "down_q", "down_s", "down_b", "sh_gate_q", "sh_gate_s", "sh_gate_b", "sh_up_q",
+                  "sh_up_s", "sh_up_b", "sh_down_q", "sh_down_s", "sh_down_b", "sh_gate_w",
+                  "norm_w"):
+            a = arrays.get(f)
+            self.t[f] = None if a is None else np.ascontiguousarray(a)
+        self._build()
+        return self
+
+    def _build(self):
+        st = OrcLayer()
+        st.hidden, st.n_experts, st.top_k, st.moe_inter = self.H, self.E, self.k, self.I
+        st.group_size, st.rms_eps = self.g, self.eps
+        for f, a in self.t.items():
+            setattr(st, f, _p(a))
+        self.st = st
+
+    def arrays(self):
+        """dict for MoeContext.upload_layer"""
+        return dict(self.t)
+
+    # -- oracle calls
+    def route(self, x, x_is_bf16, n_threads=0):
+        n = x.shape[0]
+        logits = np.empty((n, self.E), np.float32)
+        gl = np.empty(n, np.float32)
+        idx = np.empty((n, self.k), np.int32)
+        w = np.empty((n, self.k), np.float32)
+        sg = np.empty(n, np.float32)
+        xn = np.empty((n, self.H), np.float32)
+        err = ctypes.create_string_buffer(512)
+        rc = lib().orc_route(ctypes.byref(self.st), _p(np.ascontiguousarray(x)), int(x_is_bf16), n,
+                             _p(logits), _p(gl), _p(idx), _p(w), _p(sg), _p(xn), n_threads, err)
+        if rc:
+            raise RuntimeError(err.value.decode())
+        return dict(logits=logits, gate_logit=gl, idx=idx, w=w, shared_gate=sg, xn=xn)
+
+    def forward(self, x, x_is_bf16, residual=False, routed_mode=ROUTED_FAITHFUL, token_sel=None,
+                n_threads=0):
+        x = np.ascontiguousarray(x)
+        n = x.shape[0]
+        sel = None if token_sel is None else np.ascontiguousarray(token_sel, dtype=np.int32)
+        nout = n if sel is None else len(sel)
+        out = np.empty((nout, self.H), np.float32)
+        opts = OrcOpts(int(x_is_bf16), int(residual), routed_mode, n_threads)
+        idx = np.empty((n, self.k), np.int32)
+        w = np.empty((n, self.k), np.float32)
+        sg = np.empty(n, np.float32)
+        err = ctypes.create_string_buffer(512)
+        rc = lib().orc_moe_forward(ctypes.byref(self.st), _p(x), n, _p(out), ctypes.byref(opts),
+                                   _p(sel), 0 if sel is None else len(sel), None, None, _p(idx),
+                                   _p(w), _p(sg), None, err)
+        if rc:
+            raise RuntimeError(err.value.decode())
+        return dict(out=out, idx=idx, w=w, shared_gate=sg)
+
+    def time_forward(self, x, x_is_bf16, n_threads, warmup=1, iters=3, routed_mode=ROUTED_Q4,
+                     residual=False):
+        x = np.ascontiguousarray(x)
+        out = np.empty((x.shape[0], self.H), np.float32)
+        opts = OrcOpts(int(x_is_bf16), int(residual), routed_mode, n_threads)
+        return lib().orc_time_forward(ctypes.byref(self.st), _p(x), x.shape[0], _p(out),
+                                      ctypes.byref(opts), warmup, iters)
+
+
+def gen_x(n, H, seed, bf16, layer=0, std=1.0):
+    """activations from the X stream: bf16 bits (uint16) or float32"""
+    if bf16:
+        return gen_bf16(n * H, seed, layer, "X", std).reshape(n, H)
+    return gen_f32(n * H, seed, layer, "X", std).reshape(n, H)
+
+
+def dispatch(idx, E):
+    idx = np.ascontiguousarray(idx, dtype=np.int32)
+    n, k = idx.shape
+    offsets = np.empty(E + 1, np.int32)
+    perm = np.empty(max(1, n * k), np.int32)
+    pos = np.empty(max(1, n * k), np.int32)
+    active = np.empty(E, np.int32)
+    na = lib().orc_dispatch(_p(idx), n, k, E, _p(offsets), _p(perm), _p(pos), _p(active))
+    return dict(offsets=offsets, perm=perm[: n * k], pos=pos[: n * k], unique=active[:na])
+
+
+def topk_canonical(x, k):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(k, np.int32)
+    lib().orc_topk_canonical(_p(x), len(x), k, _p(out))
+    return out
+
+
+def topk_quickselect(x, k):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(min(k, len(x)), np.int32)
+    lib().orc_topk_quickselect(_p(x), len(x), k, _p(out))
+    return out
+
+
+def dequant_q4_f32sb(q, scales, biases, rows, cols, group_size):
+    out = np.empty((rows, cols), np.float32)
+    lib().orc_dequant_q4_f32sb(_p(np.ascontiguousarray(q, dtype=np.uint32)),
+                               _p(np.ascontiguousarray(scales, dtype=np.float32)),
+                               _p(np.ascontiguousarray(biases, dtype=np.float32)), rows, cols,
+                               group_size, _p(out))
+    return out
+
+
+def gemm_q4_f32sb(A, W, scales, biases, N, K, group_size):
+    A = np.ascontiguousarray(A, dtype=np.float32)
+    M = A.shape[0]
+    C = np.empty((M, N), np.float32)
+    lib().orc_gemm_q4_f32sb(M, N, K, _p(A), _p(np.ascontiguousarray(W, dtype=np.uint32)),
+                            _p(np.ascontiguousarray(scales, dtype=np.float32)),
+                            _p(np.ascontiguousarray(biases, dtype=np.float32)), group_size, _p(C))
+    return C
+
+
+def gemm_fp32(A, W):
+    A = np.ascontiguousarray(A, dtype=np.float32)
+    W = np.ascontiguousarray(W, dtype=np.float32)
+    C = np.empty((A.shape[0], W.shape[0]), np.float32)
+    lib().orc_gemm_fp32(A.shape[0], W.shape[0], A.shape[1], _p(A), _p(W), _p(C))
+    return C
+
+
+def gemm_bf16(A, Wbits):
+    A = np.ascontiguousarray(A, dtype=np.float32)
+    Wbits = np.ascontiguousarray(Wbits, dtype=np.uint16)
+    C = np.empty((A.shape[0], Wbits.shape[0]), np.float32)
+    lib().orc_gemm_bf16(A.shape[0], Wbits.shape[0], A.shape[1], _p(A), _p(Wbits), _p(C))
+    return C
+
+
+def dot_r64(x, wbits):
+    return lib().orc_dot_r64_bf16w(_p(np.ascontiguousarray(x, dtype=np.float32)),
+                                   _p(np.ascontiguousarray(wbits, dtype=np.uint16)), len(x))
+
+
+def sumsq_r64(x):
+    return lib().orc_sumsq_r64(_p(np.ascontiguousarray(x, dtype=np.float32)), len(x))
+
+
+def rmsnorm(x, w, eps, r64=True):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    fn = lib().orc_rmsnorm_r64 if r64 else lib().orc_rmsnorm_seq
+    fn(_p(x), None if w is None else _p(np.ascontiguousarray(w, dtype=np.float32)), len(x), eps,
+       _p(y))
+    return y
+
+
+def workload_layer(w, layer=0, only_experts=None):
+    """host Layer for a qmoe Workload (same seeds/biases the bench uses)"""
+    rb = None
+    if w.zipf_s > 0:
+        rb = zipf_bias(w.n_experts, w.zipf_s, w.zipf_scale, w.seed * 1000003 + layer)
+    return Layer(w.hidden, w.n_experts, w.top_k, w.moe_inter, seed=w.seed, layer=layer,
+                 with_norm=w.rms_norm, router_bias=rb, group_size=w.group_size,
+                 only_experts=only_experts)

@@ -1,0 +1,145 @@
+/*
+ * combine.hip -- weighted combine of routed expert outputs plus the
+ * sigmoid-gated shared expert (reference C port model.c:1376-1403), and the
+ * synthetic-tensor generator used by the benchmarks.
+ */
+#include "qk_device.h"
+
+struct CombineArgs {
+    const float *y;     /* [n*k+n, H] */
+    const int32_t *pos; /* [n*k] dispatch position of slot t*k+s */
+    const float *w;     /* [n, k] */
+    const float *sg;    /* [n] */
+    const void *xres;   /* [n, H] or null */
+    float *out;         /* [n, H] */
+    int H, k, n, xbf16;
+};
+
+/*
+ * grid = (n, ceil(H/1024)); 256 threads x 4 columns.  For token t the k
+ * slots are taken in ascending dispatch position, i.e. ascending expert id
+ * (the expert loop order of model.c:1338), each as out = fma(w, y, out)
+ * from out = 0, then out = fma(g, y_shared, out), then the optional residual.
+ */
+__global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
+    __shared__ int s_pos[QK_MAX_TOPK];
+    __shared__ float s_w[QK_MAX_TOPK];
+    const int t = blockIdx.x;
+    if (threadIdx.x < 64) {
+        const int s = threadIdx.x;
+        int p = s < a.k ? a.pos[(size_t)t * a.k + s] : 0x7FFFFFFF;
+        float wt = s < a.k ? a.w[(size_t)t * a.k + s] : 0.0f;
+        if (s < a.k && (p < 0 || p >= a.n * a.k)) { /* undispatched slot: no contribution */
+            p = 0x7FFFFFFE;
+            wt = 0.0f;
+        }
+        int rank = 0;
+        for (int s2 = 0; s2 < a.k; s2++) {
+            int q = __shfl(p, s2, QK_WAVE);
+            rank += q < p ? 1 : 0;
+        }
+        if (s < a.k) {
+            s_pos[rank] = p;
+            s_w[rank] = wt;
+        }
+    }
+    __syncthreads();
+    const int c = (blockIdx.y * 256 + threadIdx.x) * 4;
+    if (c >= a.H) return;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int j = 0; j < a.k; j++) {
+        const float wt = s_w[j];
+        if (s_pos[j] >= a.n * a.k) continue;
+        const float4 v = *(const float4 *)(a.y + (size_t)s_pos[j] * a.H + c);
+        acc.x = fmaf(wt, v.x, acc.x);
+        acc.y = fmaf(wt, v.y, acc.y);
+        acc.z = fmaf(wt, v.z, acc.z);
+        acc.w = fmaf(wt, v.w, acc.w);
+    }
+    {
+        const float g = a.sg[t];
+        const float4 v = *(const float4 *)(a.y + ((size_t)a.n * a.k + t) * a.H + c);
+        acc.x = fmaf(g, v.x, acc.x);
+        acc.y = fmaf(g, v.y, acc.y);
+        acc.z = fmaf(g, v.z, acc.z);
+        acc.w = fmaf(g, v.w, acc.w);
+    }
+    if (a.xres) {
+        float4 xv;
+        if (a.xbf16) {
+            const uint2 d = *(const uint2 *)((const uint16_t *)a.xres + (size_t)t * a.H + c);
+            xv = make_float4(qk_bf16_lo(d.x), qk_bf16_hi(d.x), qk_bf16_lo(d.y), qk_bf16_hi(d.y));
+        } else {
+            xv = *(const float4 *)((const float *)a.xres + (size_t)t * a.H + c);
+        }
+        acc.x = xv.x + acc.x;
+        acc.y = xv.y + acc.y;
+        acc.z = xv.z + acc.z;
+        acc.w = xv.w + acc.w;
+    }
+    *(float4 *)(a.out + (size_t)t * a.H + c) = acc;
+}
+
+extern "C" int qk_launch_combine(qk_shape s, int n, const float *y, const int32_t *pos,
+                                 const float *w, const float *sg, const void *x_res, int x_bf16,
+                                 float *out, void *stream) {
+    if (n <= 0) return 0;
+    CombineArgs a{y, pos, w, sg, x_res, out, s.H, s.k, n, x_bf16};
+    dim3 grid(n, (s.H + 1023) / 1024);
+    hipLaunchKernelGGL(k_combine, grid, dim3(256), 0, (hipStream_t)stream, a);
+    return QK_CHECK_LAUNCH();
+}
+
+/* ------------------------------------------------------- synthetic data
+ * Counter-based streams: element i of stream `key` is splitmix64's output
+ * function applied to key + (i+1)*golden.  Normals use Box-Muller in double
+ * on draws 2i, 2i+1 (cosine branch); codes are the high 32 bits.  The host
+ * generator of the test oracle computes the same values. */
+
+#define QK_GOLDEN 0x9E3779B97F4A7C15ull
+
+__host__ __device__ __forceinline__ uint64_t qk_mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+extern "C" uint64_t qk_tensor_key(uint64_t seed, uint32_t layer, uint32_t tag) {
+    return qk_mix64(qk_mix64(seed + QK_GOLDEN) ^ (((uint64_t)layer << 32) | (uint64_t)tag));
+}
+
+__device__ __forceinline__ double qk_stream_normal(uint64_t key, uint64_t i) {
+    const uint64_t r1 = qk_mix64(key + (2 * i + 1) * QK_GOLDEN);
+    const uint64_t r2 = qk_mix64(key + (2 * i + 2) * QK_GOLDEN);
+    const double u1 = (double)((r1 >> 11) + 1) * 0x1.0p-53;
+    const double u2 = (double)(r2 >> 11) * 0x1.0p-53;
+    return sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+}
+
+__global__ void k_synth(void *dst, size_t count, int kind, uint64_t key, uint64_t start,
+                        float stddev) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const uint64_t gi = start + i;
+        if (kind == 0) {
+            float v = (float)(qk_stream_normal(key, gi) * (double)stddev);
+            ((uint16_t *)dst)[i] = (uint16_t)qk_f2bf(v);
+        } else if (kind == 1) {
+            ((float *)dst)[i] = (float)(qk_stream_normal(key, gi) * (double)stddev);
+        } else if (kind == 2) {
+            ((uint32_t *)dst)[i] = (uint32_t)(qk_mix64(key + (gi + 1) * QK_GOLDEN) >> 32);
+        } else {
+            ((float *)dst)[i] = stddev;
+        }
+    }
+}
+
+extern "C" int qk_launch_synth(void *dst, size_t count, int kind, uint64_t key, uint64_t start,
+                               float stddev, void *stream) {
+    if (count == 0) return 0;
+    size_t blocks = (count + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(k_synth, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, dst,
+                       count, kind, key, start, stddev);
+    return QK_CHECK_LAUNCH();
+}

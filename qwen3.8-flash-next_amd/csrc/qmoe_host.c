@@ -1,0 +1,670 @@
+/*
+ * qmoe_host.c -- C11 host side of libqmoe.so: context, HBM residency of the
+ * layers, argument checking and the orchestration of the HIP kernels.
+ *
+ * Mirrors the reference C port's MoE-layer call contract
+ * (c/src/model.c:1281-1405, c/src/kernel.h, c/src/util.h:11-27): plain C,
+ * caller-owned outputs, 0 / -1 + message returns, no aborts.
+ */
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <hip/hip_runtime_api.h>
+
+#include "qmoe_internal.h"
+
+#define QMOE_VERSION "qmoe 0.1 (gfx950)"
+#define ALIGN 256u
+
+typedef struct {
+    void *mem;
+    qmoe_layer_weights dev; /* pointers into mem; router_bias / norm_w NULL when absent */
+    int ready;
+} qmoe_layer_slot;
+
+struct qmoe_ctx {
+    qmoe_config cfg;
+    qk_shape shape;
+    int device;
+    void *scratch_mem;
+    size_t scratch_bytes;
+    qk_scratch sc;
+    float *host_x_dev, *host_out_dev; /* staging for qmoe_moe_forward_host */
+    qmoe_layer_slot *layers;
+    size_t layer_bytes;
+    int last_n; /* token count of the last qmoe_layer_forward, -1 if none */
+    /* byte offsets of each tensor inside a layer allocation */
+    size_t off[24];
+};
+
+/* tensor order inside a layer allocation */
+enum {
+    T_ROUTER_W, T_ROUTER_BIAS, T_GATE_Q, T_GATE_S, T_GATE_B, T_UP_Q, T_UP_S, T_UP_B,
+    T_DOWN_Q, T_DOWN_S, T_DOWN_B, T_SH_GATE_Q, T_SH_GATE_S, T_SH_GATE_B, T_SH_UP_Q, T_SH_UP_S,
+    T_SH_UP_B, T_SH_DOWN_Q, T_SH_DOWN_S, T_SH_DOWN_B, T_SHGATE_W, T_NORM_W, T_COUNT
+};
+
+static void set_err(qmoe_err *err, const char *fmt, ...) {
+    if (!err) return;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(err->msg, sizeof(err->msg), fmt, ap);
+    va_end(ap);
+}
+
+static void clear_err(qmoe_err *err) {
+    if (err) err->msg[0] = 0;
+}
+
+static int hip_fail(qmoe_err *err, int rc, const char *what) {
+    if (rc == 0) return 0;
+    set_err(err, "%s: HIP error %d (%s)", what, rc, hipGetErrorString((hipError_t)rc));
+    return -1;
+}
+
+static size_t align_up(size_t v) { return (v + ALIGN - 1) / ALIGN * ALIGN; }
+
+/* element count and element size of each tensor */
+static void tensor_shape(const qmoe_config *c, int t, size_t *count, size_t *esize) {
+    const size_t H = (size_t)c->hidden, E = (size_t)c->n_experts, I = (size_t)c->moe_inter;
+    const size_t g = (size_t)c->group_size;
+    size_t n = 0, es = 2;
+    switch (t) {
+    case T_ROUTER_W: n = E * H; break;
+    case T_ROUTER_BIAS: n = E; es = 4; break;
+    case T_GATE_Q: case T_UP_Q: n = E * I * H / 8; es = 4; break;
+    case T_GATE_S: case T_GATE_B: case T_UP_S: case T_UP_B: n = E * I * H / g; break;
+    case T_DOWN_Q: n = E * H * I / 8; es = 4; break;
+    case T_DOWN_S: case T_DOWN_B: n = E * H * I / g; break;
+    case T_SH_GATE_Q: case T_SH_UP_Q: n = I * H / 8; es = 4; break;
+    case T_SH_GATE_S: case T_SH_GATE_B: case T_SH_UP_S: case T_SH_UP_B: n = I * H / g; break;
+    case T_SH_DOWN_Q: n = H * I / 8; es = 4; break;
+    case T_SH_DOWN_S: case T_SH_DOWN_B: n = H * I / g; break;
+    case T_SHGATE_W: n = H; break;
+    case T_NORM_W: n = H; es = 4; break;
+    }
+    *count = n;
+    *esize = es;
+}
+
+static int check_config(const qmoe_config *c, qmoe_err *err) {
+    if (!c) {
+        set_err(err, "config is NULL");
+        return -1;
+    }
+    if (c->group_size != QK_GROUP) {
+        set_err(err, "group_size %d unsupported (this build needs %d)", c->group_size, QK_GROUP);
+        return -1;
+    }
+    if (c->hidden <= 0 || c->hidden % QK_GROUP || c->hidden > 8192) {
+        set_err(err, "hidden %d must be a positive multiple of %d and <= 8192", c->hidden, QK_GROUP);
+        return -1;
+    }
+    if (c->moe_inter <= 0 || c->moe_inter % QK_GROUP || c->moe_inter > 8192) {
+        set_err(err, "moe_inter %d must be a positive multiple of %d and <= 8192", c->moe_inter,
+                QK_GROUP);
+        return -1;
+    }
+    if (c->n_experts <= 0 || c->n_experts > QK_MAX_EXPERTS) {
+        set_err(err, "n_experts %d must be in [1, %d]", c->n_experts, QK_MAX_EXPERTS);
+        return -1;
+    }
+    if (c->top_k <= 0 || c->top_k > c->n_experts || c->top_k > QK_MAX_TOPK) {
+        set_err(err, "top_k %d must be in [1, min(n_experts, %d)]", c->top_k, QK_MAX_TOPK);
+        return -1;
+    }
+    if (c->n_layers <= 0) {
+        set_err(err, "n_layers %d must be positive", c->n_layers);
+        return -1;
+    }
+    if (c->max_tokens <= 0 || (long long)c->max_tokens * (c->top_k + 1) > (1LL << 30)) {
+        set_err(err, "max_tokens %d out of range", c->max_tokens);
+        return -1;
+    }
+    if (!(c->rms_eps >= 0.0f)) {
+        set_err(err, "rms_eps must be >= 0");
+        return -1;
+    }
+    return 0;
+}
+
+int qmoe_create(qmoe_ctx **out, const qmoe_config *cfg, qmoe_err *err) {
+    clear_err(err);
+    if (!out) {
+        set_err(err, "ctx pointer is NULL");
+        return -1;
+    }
+    *out = NULL;
+    if (check_config(cfg, err)) return -1;
+    qmoe_ctx *c = (qmoe_ctx *)calloc(1, sizeof(qmoe_ctx));
+    if (!c) {
+        set_err(err, "out of host memory");
+        return -1;
+    }
+    c->cfg = *cfg;
+    c->shape.H = cfg->hidden;
+    c->shape.E = cfg->n_experts;
+    c->shape.k = cfg->top_k;
+    c->shape.I = cfg->moe_inter;
+    c->shape.eps = cfg->rms_eps;
+    if (hip_fail(err, (int)hipGetDevice(&c->device), "hipGetDevice")) {
+        free(c);
+        return -1;
+    }
+    /* layer layout */
+    size_t o = 0;
+    for (int t = 0; t < T_COUNT; t++) {
+        size_t n, es;
+        tensor_shape(cfg, t, &n, &es);
+        c->off[t] = o;
+        o = align_up(o + n * es);
+    }
+    c->layer_bytes = o;
+    c->last_n = -1;
+    c->layers = (qmoe_layer_slot *)calloc((size_t)cfg->n_layers, sizeof(qmoe_layer_slot));
+    if (!c->layers) {
+        free(c);
+        set_err(err, "out of host memory");
+        return -1;
+    }
+    /* scratch */
+    const size_t n = (size_t)cfg->max_tokens, E = (size_t)cfg->n_experts, k = (size_t)cfg->top_k;
+    const size_t H = (size_t)cfg->hidden, I = (size_t)cfg->moe_inter;
+    const size_t nw = (n + 31) / 32, rows = n * k + n;
+    size_t sz[13] = {n * (E + 1) * 4, n * k * 4, n * k * 4, n * 4, (E + 1) * 4, n * k * 4,
+                     n * k * 4, (E + 1) * 4, E * nw * 4, E * nw * 4, n * H * 4, rows * I * 4,
+                     rows * H * 4};
+    size_t total = 0, offs[13];
+    for (int i = 0; i < 13; i++) {
+        offs[i] = total;
+        total = align_up(total + sz[i]);
+    }
+    c->scratch_bytes = total;
+    if (hip_fail(err, (int)hipMalloc(&c->scratch_mem, total), "hipMalloc(scratch)")) {
+        free(c->layers);
+        free(c);
+        return -1;
+    }
+    char *b = (char *)c->scratch_mem;
+    c->sc.logits = (float *)(b + offs[0]);
+    c->sc.idx = (int32_t *)(b + offs[1]);
+    c->sc.w = (float *)(b + offs[2]);
+    c->sc.sg = (float *)(b + offs[3]);
+    c->sc.offsets = (int32_t *)(b + offs[4]);
+    c->sc.perm = (int32_t *)(b + offs[5]);
+    c->sc.pos = (int32_t *)(b + offs[6]);
+    c->sc.unique = (int32_t *)(b + offs[7]);
+    c->sc.bits = (uint32_t *)(b + offs[8]);
+    c->sc.wprefix = (int32_t *)(b + offs[9]);
+    c->sc.xn = (float *)(b + offs[10]);
+    c->sc.h = (float *)(b + offs[11]);
+    c->sc.y = (float *)(b + offs[12]);
+    *out = c;
+    return 0;
+}
+
+void qmoe_destroy(qmoe_ctx *c) {
+    if (!c) return;
+    if (c->layers)
+        for (int l = 0; l < c->cfg.n_layers; l++)
+            if (c->layers[l].mem) hipFree(c->layers[l].mem);
+    if (c->scratch_mem) hipFree(c->scratch_mem);
+    if (c->host_x_dev) hipFree(c->host_x_dev);
+    if (c->host_out_dev) hipFree(c->host_out_dev);
+    free(c->layers);
+    free(c);
+}
+
+size_t qmoe_scratch_bytes(const qmoe_ctx *c) { return c ? c->scratch_bytes : 0; }
+size_t qmoe_layer_bytes(const qmoe_ctx *c) { return c ? c->layer_bytes : 0; }
+const char *qmoe_version(void) { return QMOE_VERSION; }
+
+static int check_layer_index(qmoe_ctx *c, int layer, qmoe_err *err) {
+    if (!c) {
+        set_err(err, "ctx is NULL");
+        return -1;
+    }
+    if (layer < 0 || layer >= c->cfg.n_layers) {
+        set_err(err, "layer %d out of range [0, %d)", layer, c->cfg.n_layers);
+        return -1;
+    }
+    return 0;
+}
+
+static int ensure_layer_mem(qmoe_ctx *c, int layer, qmoe_err *err) {
+    qmoe_layer_slot *L = &c->layers[layer];
+    if (L->mem) return 0;
+    if (hip_fail(err, (int)hipMalloc(&L->mem, c->layer_bytes), "hipMalloc(layer)")) return -1;
+    char *b = (char *)L->mem;
+    qmoe_layer_weights *d = &L->dev;
+    d->router_w = (const uint16_t *)(b + c->off[T_ROUTER_W]);
+    d->router_bias = NULL;
+    d->gate_q = (const uint32_t *)(b + c->off[T_GATE_Q]);
+    d->gate_s = (const uint16_t *)(b + c->off[T_GATE_S]);
+    d->gate_b = (const uint16_t *)(b + c->off[T_GATE_B]);
+    d->up_q = (const uint32_t *)(b + c->off[T_UP_Q]);
+    d->up_s = (const uint16_t *)(b + c->off[T_UP_S]);
+    d->up_b = (const uint16_t *)(b + c->off[T_UP_B]);
+    d->down_q = (const uint32_t *)(b + c->off[T_DOWN_Q]);
+    d->down_s = (const uint16_t *)(b + c->off[T_DOWN_S]);
+    d->down_b = (const uint16_t *)(b + c->off[T_DOWN_B]);
+    d->sh_gate_q = (const uint32_t *)(b + c->off[T_SH_GATE_Q]);
+    d->sh_gate_s = (const uint16_t *)(b + c->off[T_SH_GATE_S]);
+    d->sh_gate_b = (const uint16_t *)(b + c->off[T_SH_GATE_B]);
+    d->sh_up_q = (const uint32_t *)(b + c->off[T_SH_UP_Q]);
+    d->sh_up_s = (const uint16_t *)(b + c->off[T_SH_UP_S]);
+    d->sh_up_b = (const uint16_t *)(b + c->off[T_SH_UP_B]);
+    d->sh_down_q = (const uint32_t *)(b + c->off[T_SH_DOWN_Q]);
+    d->sh_down_s = (const uint16_t *)(b + c->off[T_SH_DOWN_S]);
+    d->sh_down_b = (const uint16_t *)(b + c->off[T_SH_DOWN_B]);
+    d->sh_gate_w = (const uint16_t *)(b + c->off[T_SHGATE_W]);
+    d->norm_w = NULL;
+    return 0;
+}
+
+static const void *host_tensor(const qmoe_layer_weights *h, int t) {
+    switch (t) {
+    case T_ROUTER_W: return h->router_w;
+    case T_ROUTER_BIAS: return h->router_bias;
+    case T_GATE_Q: return h->gate_q;
+    case T_GATE_S: return h->gate_s;
+    case T_GATE_B: return h->gate_b;
+    case T_UP_Q: return h->up_q;
+    case T_UP_S: return h->up_s;
+    case T_UP_B: return h->up_b;
+    case T_DOWN_Q: return h->down_q;
+    case T_DOWN_S: return h->down_s;
+    case T_DOWN_B: return h->down_b;
+    case T_SH_GATE_Q: return h->sh_gate_q;
+    case T_SH_GATE_S: return h->sh_gate_s;
+    case T_SH_GATE_B: return h->sh_gate_b;
+    case T_SH_UP_Q: return h->sh_up_q;
+    case T_SH_UP_S: return h->sh_up_s;
+    case T_SH_UP_B: return h->sh_up_b;
+    case T_SH_DOWN_Q: return h->sh_down_q;
+    case T_SH_DOWN_S: return h->sh_down_s;
+    case T_SH_DOWN_B: return h->sh_down_b;
+    case T_SHGATE_W: return h->sh_gate_w;
+    case T_NORM_W: return h->norm_w;
+    }
+    return NULL;
+}
+
+static const char *tensor_name(int t) {
+    static const char *names[T_COUNT] = {
+        "router_w", "router_bias", "gate_q", "gate_s", "gate_b", "up_q", "up_s", "up_b",
+        "down_q", "down_s", "down_b", "sh_gate_q", "sh_gate_s", "sh_gate_b", "sh_up_q",
+        "sh_up_s", "sh_up_b", "sh_down_q", "sh_down_s", "sh_down_b", "sh_gate_w", "norm_w"};
+    return names[t];
+}
+
+int qmoe_upload_layer(qmoe_ctx *c, int layer, const qmoe_layer_weights *h, qmoe_err *err) {
+    clear_err(err);
+    if (check_layer_index(c, layer, err)) return -1;
+    if (!h) {
+        set_err(err, "weights pointer is NULL");
+        return -1;
+    }
+    for (int t = 0; t < T_COUNT; t++) {
+        if (t == T_ROUTER_BIAS || t == T_NORM_W) continue;
+        if (!host_tensor(h, t)) {
+            set_err(err, "missing tensor %s for layer %d", tensor_name(t), layer);
+            return -1;
+        }
+    }
+    if (ensure_layer_mem(c, layer, err)) return -1;
+    qmoe_layer_slot *L = &c->layers[layer];
+    L->ready = 0;
+    char *b = (char *)L->mem;
+    for (int t = 0; t < T_COUNT; t++) {
+        const void *src = host_tensor(h, t);
+        if (!src) continue;
+        size_t n, es;
+        tensor_shape(&c->cfg, t, &n, &es);
+        if (hip_fail(err, (int)hipMemcpy(b + c->off[t], src, n * es, hipMemcpyHostToDevice),
+                     "hipMemcpy(upload)"))
+            return -1;
+    }
+    L->dev.router_bias = h->router_bias ? (const float *)(b + c->off[T_ROUTER_BIAS]) : NULL;
+    L->dev.norm_w = h->norm_w ? (const float *)(b + c->off[T_NORM_W]) : NULL;
+    L->ready = 1;
+    return 0;
+}
+
+int qmoe_synth_layer(qmoe_ctx *c, int layer, uint64_t seed, int with_norm, const float *router_bias,
+                     qmoe_err *err) {
+    clear_err(err);
+    if (check_layer_index(c, layer, err)) return -1;
+    if (ensure_layer_mem(c, layer, err)) return -1;
+    qmoe_layer_slot *L = &c->layers[layer];
+    L->ready = 0;
+    char *b = (char *)L->mem;
+    static const struct {
+        int t, tag, kind;
+        float sd;
+    } spec[] = {
+        {T_ROUTER_W, QMOE_TAG_ROUTER_W, 0, 0.02f},   {T_GATE_Q, QMOE_TAG_GATE_Q, 2, 0.0f},
+        {T_GATE_S, QMOE_TAG_GATE_S, 0, 0.02f},       {T_GATE_B, QMOE_TAG_GATE_B, 0, 0.01f},
+        {T_UP_Q, QMOE_TAG_UP_Q, 2, 0.0f},            {T_UP_S, QMOE_TAG_UP_S, 0, 0.02f},
+        {T_UP_B, QMOE_TAG_UP_B, 0, 0.01f},           {T_DOWN_Q, QMOE_TAG_DOWN_Q, 2, 0.0f},
+        {T_DOWN_S, QMOE_TAG_DOWN_S, 0, 0.02f},       {T_DOWN_B, QMOE_TAG_DOWN_B, 0, 0.01f},
+        {T_SH_GATE_Q, QMOE_TAG_SH_GATE_Q, 2, 0.0f},  {T_SH_GATE_S, QMOE_TAG_SH_GATE_S, 0, 0.02f},
+        {T_SH_GATE_B, QMOE_TAG_SH_GATE_B, 0, 0.01f}, {T_SH_UP_Q, QMOE_TAG_SH_UP_Q, 2, 0.0f},
+        {T_SH_UP_S, QMOE_TAG_SH_UP_S, 0, 0.02f},     {T_SH_UP_B, QMOE_TAG_SH_UP_B, 0, 0.01f},
+        {T_SH_DOWN_Q, QMOE_TAG_SH_DOWN_Q, 2, 0.0f},  {T_SH_DOWN_S, QMOE_TAG_SH_DOWN_S, 0, 0.02f},
+        {T_SH_DOWN_B, QMOE_TAG_SH_DOWN_B, 0, 0.01f}, {T_SHGATE_W, QMOE_TAG_SHGATE_W, 0, 0.02f},
+    };
+    for (size_t i = 0; i < sizeof(spec) / sizeof(spec[0]); i++) {
+        size_t n, es;
+        tensor_shape(&c->cfg, spec[i].t, &n, &es);
+        uint64_t key = qk_tensor_key(seed, (uint32_t)layer, (uint32_t)spec[i].tag);
+        if (hip_fail(err, qk_launch_synth(b + c->off[spec[i].t], n, spec[i].kind, key, 0,
+                                          spec[i].sd, NULL),
+                     "synth"))
+            return -1;
+    }
+    if (with_norm) {
+        if (hip_fail(err, qk_launch_synth(b + c->off[T_NORM_W], (size_t)c->cfg.hidden, 3, 0, 0,
+                                          1.0f, NULL),
+                     "synth(norm)"))
+            return -1;
+    }
+    if (router_bias) {
+        if (hip_fail(err, (int)hipMemcpy(b + c->off[T_ROUTER_BIAS], router_bias,
+                                         (size_t)c->cfg.n_experts * 4, hipMemcpyHostToDevice),
+                     "hipMemcpy(router_bias)"))
+            return -1;
+    }
+    if (hip_fail(err, (int)hipDeviceSynchronize(), "synth sync")) return -1;
+    L->dev.router_bias = router_bias ? (const float *)(b + c->off[T_ROUTER_BIAS]) : NULL;
+    L->dev.norm_w = with_norm ? (const float *)(b + c->off[T_NORM_W]) : NULL;
+    L->ready = 1;
+    return 0;
+}
+
+int qmoe_synth_fill(void *dst, size_t count, int kind, uint64_t seed, uint32_t layer, uint32_t tag,
+                    uint64_t start, float stddev, void *stream, qmoe_err *err) {
+    clear_err(err);
+    if (!dst && count) {
+        set_err(err, "dst is NULL");
+        return -1;
+    }
+    if (kind < 0 || kind > 2) {
+        set_err(err, "kind %d must be 0 (bf16 normal), 1 (f32 normal) or 2 (u32 codes)", kind);
+        return -1;
+    }
+    return hip_fail(err, qk_launch_synth(dst, count, kind, qk_tensor_key(seed, layer, tag), start,
+                                         stddev, stream),
+                    "synth_fill");
+}
+
+int qmoe_layer_device_weights(qmoe_ctx *c, int layer, qmoe_layer_weights *out, qmoe_err *err) {
+    clear_err(err);
+    if (check_layer_index(c, layer, err)) return -1;
+    if (!c->layers[layer].ready) {
+        set_err(err, "layer %d has no weights", layer);
+        return -1;
+    }
+    if (!out) {
+        set_err(err, "out is NULL");
+        return -1;
+    }
+    *out = c->layers[layer].dev;
+    return 0;
+}
+
+/* ------------------------------------------------------------ stages */
+
+static int check_call(qmoe_ctx *c, int layer, int n, qmoe_err *err) {
+    if (check_layer_index(c, layer, err)) return -1;
+    if (!c->layers[layer].ready) {
+        set_err(err, "layer %d has no weights", layer);
+        return -1;
+    }
+    if (n < 0 || n > c->cfg.max_tokens) {
+        set_err(err, "n = %d out of range [0, max_tokens = %d]", n, c->cfg.max_tokens);
+        return -1;
+    }
+    return 0;
+}
+
+static int check_dtype(int dt, qmoe_err *err) {
+    if (dt != QMOE_F32 && dt != QMOE_BF16) {
+        set_err(err, "x_dtype %d must be QMOE_F32 (0) or QMOE_BF16 (1)", dt);
+        return -1;
+    }
+    return 0;
+}
+
+#define NEED(p, name)                                                                          \
+    do {                                                                                       \
+        if (!(p)) {                                                                            \
+            set_err(err, "%s is NULL", name);                                                  \
+            return -1;                                                                         \
+        }                                                                                      \
+    } while (0)
+
+int qmoe_router(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n, float *logits_out,
+                int32_t *idx_out, float *w_out, float *shared_gate_out, float *xn_out,
+                void *stream, qmoe_err *err) {
+    clear_err(err);
+    if (check_call(c, layer, n, err) || check_dtype(x_dtype, err)) return -1;
+    if (n == 0) return 0;
+    NEED(x, "x");
+    NEED(idx_out, "idx_out");
+    NEED(w_out, "w_out");
+    NEED(shared_gate_out, "shared_gate_out");
+    const qmoe_layer_weights *W = &c->layers[layer].dev;
+    if (!W->norm_w && xn_out) {
+        set_err(err, "xn_out given but layer %d has no norm weight", layer);
+        return -1;
+    }
+    float *xn = W->norm_w ? (xn_out ? xn_out : c->sc.xn) : NULL;
+    if (hip_fail(err, qk_launch_router(W, c->shape, x, x_dtype == QMOE_BF16, n, c->sc.logits, xn,
+                                       stream),
+                 "router"))
+        return -1;
+    return hip_fail(err, qk_launch_topk(c->shape, n, c->sc.logits, logits_out, idx_out, w_out,
+                                        shared_gate_out, stream),
+                    "topk");
+}
+
+int qmoe_dispatch(qmoe_ctx *c, const int32_t *idx, int n, int32_t *offsets_out, int32_t *perm_out,
+                  int32_t *unique_out, void *stream, qmoe_err *err) {
+    clear_err(err);
+    if (!c) {
+        set_err(err, "ctx is NULL");
+        return -1;
+    }
+    if (n < 0 || n > c->cfg.max_tokens) {
+        set_err(err, "n = %d out of range [0, max_tokens = %d]", n, c->cfg.max_tokens);
+        return -1;
+    }
+    NEED(offsets_out, "offsets_out");
+    NEED(unique_out, "unique_out");
+    if (n == 0) {
+        /* nothing routed: all offsets 0 and an empty unique list */
+        int32_t *z = (int32_t *)calloc((size_t)c->cfg.n_experts + 1, sizeof(int32_t));
+        if (!z) {
+            set_err(err, "out of host memory");
+            return -1;
+        }
+        int rc = (int)hipMemcpyAsync(offsets_out, z, ((size_t)c->cfg.n_experts + 1) * 4,
+                                     hipMemcpyHostToDevice, (hipStream_t)stream);
+        if (!rc)
+            rc = (int)hipMemcpyAsync(unique_out, z, 4, hipMemcpyHostToDevice, (hipStream_t)stream);
+        if (!rc) rc = (int)hipStreamSynchronize((hipStream_t)stream);
+        free(z);
+        return hip_fail(err, rc, "dispatch(n=0)");
+    }
+    NEED(idx, "idx");
+    NEED(perm_out, "perm_out");
+    return hip_fail(err, qk_launch_dispatch(c->shape, n, idx, offsets_out, perm_out, c->sc.pos,
+                                            unique_out, c->sc.bits, c->sc.wprefix, stream),
+                    "dispatch");
+}
+
+int qmoe_expert_gateup(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n,
+                       const int32_t *perm, const int32_t *offsets, const int32_t *unique,
+                       float *h_out, void *stream, qmoe_err *err) {
+    clear_err(err);
+    if (check_call(c, layer, n, err) || check_dtype(x_dtype, err)) return -1;
+    if (n == 0) return 0;
+    NEED(x, "x");
+    NEED(perm, "perm");
+    NEED(offsets, "offsets");
+    NEED(unique, "unique");
+    NEED(h_out, "h_out");
+    return hip_fail(err, qk_launch_gateup(&c->layers[layer].dev, c->shape, x, x_dtype == QMOE_BF16,
+                                          n, perm, offsets, unique, h_out, stream),
+                    "gateup");
+}
+
+int qmoe_expert_down(qmoe_ctx *c, int layer, const float *h, int n, const int32_t *perm,
+                     const int32_t *offsets, const int32_t *unique, float *y_out, void *stream,
+                     qmoe_err *err) {
+    clear_err(err);
+    if (check_call(c, layer, n, err)) return -1;
+    if (n == 0) return 0;
+    NEED(h, "h");
+    NEED(perm, "perm");
+    NEED(offsets, "offsets");
+    NEED(unique, "unique");
+    NEED(y_out, "y_out");
+    return hip_fail(err, qk_launch_down(&c->layers[layer].dev, c->shape, h, n, perm, offsets, unique,
+                                        y_out, stream),
+                    "down");
+}
+
+int qmoe_expert_ffn(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n, const int32_t *perm,
+                    const int32_t *offsets, const int32_t *unique, float *y_out, void *stream,
+                    qmoe_err *err) {
+    if (qmoe_expert_gateup(c, layer, x, x_dtype, n, perm, offsets, unique, c ? c->sc.h : NULL,
+                           stream, err))
+        return -1;
+    return qmoe_expert_down(c, layer, c->sc.h, n, perm, offsets, unique, y_out, stream, err);
+}
+
+int qmoe_combine(qmoe_ctx *c, const float *y, const int32_t *perm, const float *w,
+                 const float *shared_gate, int n, const void *x_residual, int x_dtype, float *out,
+                 void *stream, qmoe_err *err) {
+    clear_err(err);
+    if (!c) {
+        set_err(err, "ctx is NULL");
+        return -1;
+    }
+    if (n < 0 || n > c->cfg.max_tokens) {
+        set_err(err, "n = %d out of range [0, max_tokens = %d]", n, c->cfg.max_tokens);
+        return -1;
+    }
+    if (x_residual && check_dtype(x_dtype, err)) return -1;
+    if (n == 0) return 0;
+    NEED(y, "y");
+    NEED(perm, "perm");
+    NEED(w, "w");
+    NEED(shared_gate, "shared_gate");
+    NEED(out, "out");
+    if (hip_fail(err, qk_launch_invert_perm(n * c->cfg.top_k, perm, c->sc.pos, stream), "invert"))
+        return -1;
+    return hip_fail(err, qk_launch_combine(c->shape, n, y, c->sc.pos, w, shared_gate, x_residual,
+                                           x_dtype == QMOE_BF16, out, stream),
+                    "combine");
+}
+
+int qmoe_layer_forward(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n, float *out,
+                       int flags, void *stream, qmoe_err *err) {
+    clear_err(err);
+    if (check_call(c, layer, n, err) || check_dtype(x_dtype, err)) return -1;
+    if (flags & ~QMOE_RESIDUAL) {
+        set_err(err, "unknown flags 0x%x", flags);
+        return -1;
+    }
+    if (n == 0) return 0;
+    NEED(x, "x");
+    NEED(out, "out");
+    c->last_n = n;
+    const qmoe_layer_weights *W = &c->layers[layer].dev;
+    const qk_shape s = c->shape;
+    qk_scratch *sc = &c->sc;
+    const int xbf = x_dtype == QMOE_BF16;
+    int rc = qk_launch_router(W, s, x, xbf, n, sc->logits, W->norm_w ? sc->xn : NULL, stream);
+    if (hip_fail(err, rc, "router")) return -1;
+    if (n <= QK_SMALL_N && n * s.k <= QK_SMALL_NK) {
+        rc = qk_launch_topk_dispatch_small(s, n, sc->logits, NULL, sc->idx, sc->w, sc->sg,
+                                           sc->offsets, sc->perm, sc->pos, sc->unique, stream);
+        if (hip_fail(err, rc, "topk+dispatch")) return -1;
+    } else {
+        rc = qk_launch_topk(s, n, sc->logits, NULL, sc->idx, sc->w, sc->sg, stream);
+        if (hip_fail(err, rc, "topk")) return -1;
+        rc = qk_launch_dispatch(s, n, sc->idx, sc->offsets, sc->perm, sc->pos, sc->unique, sc->bits,
+                                sc->wprefix, stream);
+        if (hip_fail(err, rc, "dispatch")) return -1;
+    }
+    const void *xf = W->norm_w ? (const void *)sc->xn : x;
+    const int xf_bf = W->norm_w ? 0 : xbf;
+    rc = qk_launch_gateup(W, s, xf, xf_bf, n, sc->perm, sc->offsets, sc->unique, sc->h, stream);
+    if (hip_fail(err, rc, "gateup")) return -1;
+    rc = qk_launch_down(W, s, sc->h, n, sc->perm, sc->offsets, sc->unique, sc->y, stream);
+    if (hip_fail(err, rc, "down")) return -1;
+    rc = qk_launch_combine(s, n, sc->y, sc->pos, sc->w, sc->sg,
+                           (flags & QMOE_RESIDUAL) ? x : NULL, xbf, out, stream);
+    return hip_fail(err, rc, "combine");
+}
+
+int qmoe_moe_forward_host(qmoe_ctx *c, int layer, const float *x, int n, float *out,
+                          qmoe_err *err) {
+    clear_err(err);
+    if (check_call(c, layer, n, err)) return -1;
+    if (n == 0) return 0;
+    NEED(x, "x");
+    NEED(out, "out");
+    const size_t bytes = (size_t)c->cfg.max_tokens * c->cfg.hidden * sizeof(float);
+    if (!c->host_x_dev) {
+        if (hip_fail(err, (int)hipMalloc((void **)&c->host_x_dev, bytes), "hipMalloc(x)")) return -1;
+        if (hip_fail(err, (int)hipMalloc((void **)&c->host_out_dev, bytes), "hipMalloc(out)")) {
+            hipFree(c->host_x_dev);
+            c->host_x_dev = NULL;
+            return -1;
+        }
+    }
+    const size_t nb = (size_t)n * c->cfg.hidden * sizeof(float);
+    if (hip_fail(err, (int)hipMemcpy(c->host_x_dev, x, nb, hipMemcpyHostToDevice), "copy x"))
+        return -1;
+    if (qmoe_layer_forward(c, layer, c->host_x_dev, QMOE_F32, n, c->host_out_dev, 0, NULL, err))
+        return -1;
+    if (hip_fail(err, (int)hipMemcpy(out, c->host_out_dev, nb, hipMemcpyDeviceToHost), "copy out"))
+        return -1;
+    return 0;
+}
+
+int qmoe_last_routing(qmoe_ctx *c, int n, int32_t *idx_out, float *w_out, float *shared_gate_out,
+                      int32_t *offsets_out, int32_t *perm_out, int32_t *unique_out, void *stream,
+                      qmoe_err *err) {
+    clear_err(err);
+    if (!c) {
+        set_err(err, "ctx is NULL");
+        return -1;
+    }
+    if (n <= 0 || n != c->last_n) {
+        set_err(err, "n = %d does not match the last layer_forward (n = %d)", n, c->last_n);
+        return -1;
+    }
+    const size_t nk = (size_t)n * c->cfg.top_k, E1 = (size_t)c->cfg.n_experts + 1;
+    struct {
+        void *dst;
+        const void *src;
+        size_t bytes;
+    } cp[6] = {{idx_out, c->sc.idx, nk * 4},         {w_out, c->sc.w, nk * 4},
+               {shared_gate_out, c->sc.sg, (size_t)n * 4}, {offsets_out, c->sc.offsets, E1 * 4},
+               {perm_out, c->sc.perm, nk * 4},       {unique_out, c->sc.unique, E1 * 4}};
+    for (int i = 0; i < 6; i++) {
+        if (!cp[i].dst) continue;
+        if (hip_fail(err, (int)hipMemcpyAsync(cp[i].dst, cp[i].src, cp[i].bytes,
+                                              hipMemcpyDeviceToDevice, (hipStream_t)stream),
+                     "last_routing copy"))
+            return -1;
+    }
+    return 0;
+}

@@ -1,0 +1,88 @@
+/*
+ * qmoe_internal.h -- shared between the C host code (qmoe_host.c) and the
+ * HIP kernels (*.hip).  Plain C declarations only: the launchers are
+ * extern "C" functions defined in the .hip files and called from C.
+ */
+#ifndef QMOE_INTERNAL_H
+#define QMOE_INTERNAL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "qmoe.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* limits of this implementation (checked by qmoe_create) */
+#define QK_MAX_EXPERTS 1024
+#define QK_MAX_TOPK 64
+#define QK_GROUP 64
+/* dispatch runs in one workgroup (LDS) when n <= QK_SMALL_N and
+ * n*k <= QK_SMALL_NK, else in the multi-kernel global-memory path */
+#define QK_SMALL_N 128
+#define QK_SMALL_NK 1024
+
+typedef struct {
+    int H, E, k, I;
+    float eps;
+} qk_shape;
+
+/* device scratch carved out of one allocation by the host */
+typedef struct {
+    float *logits;     /* [n, E+1]: router logits, column E = shared-gate logit */
+    int32_t *idx;      /* [n, k] */
+    float *w;          /* [n, k] */
+    float *sg;         /* [n] sigmoid(shared gate) */
+    int32_t *offsets;  /* [E+1] */
+    int32_t *perm;     /* [n*k] */
+    int32_t *pos;      /* [n*k] inverse of perm */
+    int32_t *unique;   /* [1+E] */
+    uint32_t *bits;    /* [E, ceil(n/32)] token membership bitmask (large dispatch) */
+    int32_t *wprefix;  /* [E, ceil(n/32)] per-word exclusive popcount prefix */
+    float *xn;         /* [n, H] normalised router input */
+    float *h;          /* [n*k+n, I] */
+    float *y;          /* [n*k+n, H] */
+} qk_scratch;
+
+/* All launchers return a hipError_t value (0 = hipSuccess). */
+
+/* logits[t, 0..E) = x_t . Wr^T (+bias), logits[t, E] = x_t . w_sg; with
+ * norm_w set, x is RMS-normalised first and written to xn (if non-NULL) */
+int qk_launch_router(const qmoe_layer_weights *W, qk_shape s, const void *x, int x_bf16, int n,
+                     float *logits, float *xn, void *stream);
+
+/* top-k + renorm + sigmoid; copies the first E logit columns to logits_out
+ * when non-NULL.  With dispatch outputs non-NULL and a small n, also runs
+ * the whole dispatch in the same (single-workgroup) launch. */
+int qk_launch_topk(qk_shape s, int n, const float *logits, float *logits_out, int32_t *idx,
+                   float *w, float *sg, void *stream);
+int qk_launch_topk_dispatch_small(qk_shape s, int n, const float *logits, float *logits_out,
+                                  int32_t *idx, float *w, float *sg, int32_t *offsets,
+                                  int32_t *perm, int32_t *pos, int32_t *unique, void *stream);
+/* dispatch from idx alone (any n) */
+int qk_launch_dispatch(qk_shape s, int n, const int32_t *idx, int32_t *offsets, int32_t *perm,
+                       int32_t *pos, int32_t *unique, uint32_t *bits, int32_t *wprefix,
+                       void *stream);
+/* pos[perm[p]] = p */
+int qk_launch_invert_perm(int count, const int32_t *perm, int32_t *pos, void *stream);
+
+int qk_launch_gateup(const qmoe_layer_weights *W, qk_shape s, const void *x, int x_bf16, int n,
+                     const int32_t *perm, const int32_t *offsets, const int32_t *unique,
+                     float *h, void *stream);
+int qk_launch_down(const qmoe_layer_weights *W, qk_shape s, const float *h, int n,
+                   const int32_t *perm, const int32_t *offsets, const int32_t *unique, float *y,
+                   void *stream);
+int qk_launch_combine(qk_shape s, int n, const float *y, const int32_t *pos, const float *w,
+                      const float *sg, const void *x_res, int x_bf16, float *out, void *stream);
+
+/* synthetic streams: kind 0 bf16 normal, 1 f32 normal, 2 u32 codes, 3 f32 constant (stddev) */
+int qk_launch_synth(void *dst, size_t count, int kind, uint64_t key, uint64_t start, float stddev,
+                    void *stream);
+uint64_t qk_tensor_key(uint64_t seed, uint32_t layer, uint32_t tag);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

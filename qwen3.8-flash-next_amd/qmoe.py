@@ -1,0 +1,392 @@
+"""ctypes binding of libqmoe.so, the MI355X MoE-layer library.
+
+The C ABI (include/qmoe.h) is the product boundary; this module is the thin
+Python-side caller used by the tests and the benchmark.  Device buffers are
+torch CUDA (HIP) tensors; their data pointers and torch's current HIP stream
+are handed to the library unchanged.
+
+The library is the only compute path: if libqmoe.so is missing this module
+raises at import time instead of falling back to anything else.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+from typing import Optional
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libqmoe.so")
+
+F32, BF16 = 0, 1
+RESIDUAL = 1
+
+# synthetic stream tags (include/qmoe.h QMOE_TAG_*)
+TAGS = dict(
+    ROUTER_W=1, GATE_Q=2, GATE_S=3, GATE_B=4, UP_Q=5, UP_S=6, UP_B=7, DOWN_Q=8, DOWN_S=9,
+    DOWN_B=10, SH_GATE_Q=11, SH_GATE_S=12, SH_GATE_B=13, SH_UP_Q=14, SH_UP_S=15, SH_UP_B=16,
+    SH_DOWN_Q=17, SH_DOWN_S=18, SH_DOWN_B=19, SHGATE_W=20, X=22,
+)
+
+WEIGHT_FIELDS = [
+    "router_w", "router_bias", "gate_q", "gate_s", "gate_b", "up_q", "up_s", "up_b",
+    "down_q", "down_s", "down_b", "sh_gate_q", "sh_gate_s", "sh_gate_b", "sh_up_q",
+    "sh_up_s", "sh_up_b", "sh_down_q", "sh_down_s", "sh_down_b", "sh_gate_w", "norm_w",
+]
+
+
+class QmoeConfig(ctypes.Structure):
+    _fields_ = [
+        ("hidden", ctypes.c_int), ("n_experts", ctypes.c_int), ("top_k", ctypes.c_int),
+        ("moe_inter", ctypes.c_int), ("group_size", ctypes.c_int), ("n_layers", ctypes.c_int),
+        ("max_tokens", ctypes.c_int), ("rms_eps", ctypes.c_float),
+    ]
+
+
+class QmoeErr(ctypes.Structure):
+    _fields_ = [("msg", ctypes.c_char * 512)]
+
+
+class QmoeLayerWeights(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_void_p) for f in WEIGHT_FIELDS]
+
+
+class QmoeError(RuntimeError):
+    pass
+
+
+# exported symbols and their signatures (must match include/qmoe.h)
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+SIGNATURES = {
+    "qmoe_create": (_I, [ctypes.POINTER(_P), ctypes.POINTER(QmoeConfig), ctypes.POINTER(QmoeErr)]),
+    "qmoe_destroy": (None, [_P]),
+    "qmoe_upload_layer": (_I, [_P, _I, ctypes.POINTER(QmoeLayerWeights), ctypes.POINTER(QmoeErr)]),
+    "qmoe_synth_layer": (_I, [_P, _I, ctypes.c_uint64, _I, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_layer_device_weights": (_I, [_P, _I, ctypes.POINTER(QmoeLayerWeights), ctypes.POINTER(QmoeErr)]),
+    "qmoe_synth_fill": (_I, [_P, ctypes.c_size_t, _I, ctypes.c_uint64, ctypes.c_uint32,
+                             ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float, _P,
+                             ctypes.POINTER(QmoeErr)]),
+    "qmoe_router": (_I, [_P, _I, _P, _I, _I, _P, _P, _P, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_dispatch": (_I, [_P, _P, _I, _P, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_expert_gateup": (_I, [_P, _I, _P, _I, _I, _P, _P, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_expert_down": (_I, [_P, _I, _P, _I, _P, _P, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_expert_ffn": (_I, [_P, _I, _P, _I, _I, _P, _P, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_combine": (_I, [_P, _P, _P, _P, _P, _I, _P, _I, _P, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_layer_forward": (_I, [_P, _I, _P, _I, _I, _P, _I, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_moe_forward_host": (_I, [_P, _I, _P, _I, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_last_routing": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_scratch_bytes": (ctypes.c_size_t, [_P]),
+    "qmoe_layer_bytes": (ctypes.c_size_t, [_P]),
+    "qmoe_version": (ctypes.c_char_p, []),
+}
+
+
+def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
+    if not os.path.exists(path):
+        raise QmoeError(f"{path} is missing: build it with __graft_entry__.build() "
+                        f"(make -C qwen3.8-flash-next_amd/csrc)")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        _lib = load_library()
+    return _lib
+
+
+def _ptr(t) -> Optional[int]:
+    """device pointer of a torch tensor (or None)"""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _stream(stream) -> Optional[int]:
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def _check(rc: int, err: QmoeErr, what: str):
+    if rc != 0:
+        raise QmoeError(f"{what}: {err.msg.decode(errors='replace')}")
+
+
+def _dtype_code(t) -> int:
+    import torch
+    if t.dtype == torch.bfloat16:
+        return BF16
+    if t.dtype == torch.float32:
+        return F32
+    raise QmoeError(f"activation dtype {t.dtype} unsupported (float32 or bfloat16)")
+
+
+# ---------------------------------------------------------------- workloads
+
+@dataclass(frozen=True)
+class Workload:
+    """A synthetic MoE-layer workload (shapes, token count, routing bias)."""
+    name: str
+    hidden: int
+    n_experts: int
+    top_k: int
+    moe_inter: int
+    n_tokens: int
+    x_bf16: bool
+    zipf_s: float = 0.0        # >0: per-expert Zipf(s) log-popularity bias on the router logits
+    zipf_scale: float = 1.0
+    n_layers: int = 1
+    rms_norm: bool = False     # pre-router RMSNorm (weight ones, eps 1e-6) + residual stream
+    seed: int = 0
+    group_size: int = 64
+
+
+WORKLOADS = {
+    "tiny": Workload("tiny", 256, 8, 2, 128, 4, x_bf16=False),
+    "decode": Workload("decode", 2048, 512, 10, 512, 1, x_bf16=True),
+    "batched": Workload("batched", 2048, 512, 10, 512, 64, x_bf16=True, zipf_s=1.1),
+    "prefill": Workload("prefill", 2048, 512, 10, 512, 4096, x_bf16=True),
+    "depth48": Workload("depth48", 2048, 512, 10, 512, 1, x_bf16=False, zipf_s=1.1,
+                        n_layers=48, rms_norm=True),
+}
+
+
+# ------------------------------------------------------------------ context
+
+class MoeContext:
+    """Owns a qmoe_ctx: resident layers plus device scratch."""
+
+    def __init__(self, hidden, n_experts, top_k, moe_inter, n_layers=1, max_tokens=1,
+                 rms_eps=1e-6, group_size=64):
+        self.cfg = QmoeConfig(hidden, n_experts, top_k, moe_inter, group_size, n_layers,
+                              max_tokens, rms_eps)
+        self.H, self.E, self.k, self.I = hidden, n_experts, top_k, moe_inter
+        self.n_layers, self.max_tokens = n_layers, max_tokens
+        self._h = ctypes.c_void_p()
+        err = QmoeErr()
+        _check(lib().qmoe_create(ctypes.byref(self._h), ctypes.byref(self.cfg), ctypes.byref(err)),
+               err, "qmoe_create")
+
+    @classmethod
+    def for_workload(cls, w: Workload, max_tokens: Optional[int] = None, n_layers=None):
+        return cls(w.hidden, w.n_experts, w.top_k, w.moe_inter,
+                   n_layers=n_layers or w.n_layers, max_tokens=max_tokens or w.n_tokens,
+                   group_size=w.group_size)
+
+    @property
+    def handle(self):
+        return self._h
+
+    def close(self):
+        if self._h:
+            lib().qmoe_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def scratch_bytes(self) -> int:
+        return lib().qmoe_scratch_bytes(self._h)
+
+    def layer_bytes(self) -> int:
+        return lib().qmoe_layer_bytes(self._h)
+
+    # -- weights
+    def upload_layer(self, layer: int, host: dict):
+        """host: dict of numpy arrays in checkpoint layout (keys = WEIGHT_FIELDS)"""
+        import numpy as np
+        w = QmoeLayerWeights()
+        keep = []
+        for f in WEIGHT_FIELDS:
+            a = host.get(f)
+            if a is None:
+                setattr(w, f, None)
+                continue
+            a = np.ascontiguousarray(a)
+            keep.append(a)
+            setattr(w, f, a.ctypes.data)
+        err = QmoeErr()
+        _check(lib().qmoe_upload_layer(self._h, layer, ctypes.byref(w), ctypes.byref(err)), err,
+               "qmoe_upload_layer")
+
+    def synth_layer(self, layer: int, seed: int, with_norm=False, router_bias=None):
+        import numpy as np
+        rb = None
+        if router_bias is not None:
+            rb = np.ascontiguousarray(router_bias, dtype=np.float32)
+        err = QmoeErr()
+        _check(lib().qmoe_synth_layer(self._h, layer, seed, 1 if with_norm else 0,
+                                      None if rb is None else rb.ctypes.data, ctypes.byref(err)),
+               err, "qmoe_synth_layer")
+
+    def device_weights(self, layer: int) -> dict:
+        w = QmoeLayerWeights()
+        err = QmoeErr()
+        _check(lib().qmoe_layer_device_weights(self._h, layer, ctypes.byref(w), ctypes.byref(err)),
+               err, "qmoe_layer_device_weights")
+        return {f: getattr(w, f) for f in WEIGHT_FIELDS}
+
+    # -- stages (torch CUDA tensors in, torch CUDA tensors out)
+    def router(self, layer, x, want_logits=False, stream=None):
+        import torch
+        n = x.shape[0]
+        dev = x.device
+        logits = torch.empty((n, self.E), dtype=torch.float32, device=dev) if want_logits else None
+        idx = torch.empty((n, self.k), dtype=torch.int32, device=dev)
+        w = torch.empty((n, self.k), dtype=torch.float32, device=dev)
+        sg = torch.empty((n,), dtype=torch.float32, device=dev)
+        err = QmoeErr()
+        _check(lib().qmoe_router(self._h, layer, _ptr(x), _dtype_code(x), n, _ptr(logits),
+                                 _ptr(idx), _ptr(w), _ptr(sg), None, _stream(stream),
+                                 ctypes.byref(err)), err, "qmoe_router")
+        return dict(logits=logits, idx=idx, w=w, shared_gate=sg)
+
+    def router_norm(self, layer, x, stream=None):
+        """router of a layer with a pre-router RMSNorm; also returns the normalised rows"""
+        import torch
+        n = x.shape[0]
+        dev = x.device
+        logits = torch.empty((n, self.E), dtype=torch.float32, device=dev)
+        idx = torch.empty((n, self.k), dtype=torch.int32, device=dev)
+        w = torch.empty((n, self.k), dtype=torch.float32, device=dev)
+        sg = torch.empty((n,), dtype=torch.float32, device=dev)
+        xn = torch.empty((n, self.H), dtype=torch.float32, device=dev)
+        err = QmoeErr()
+        _check(lib().qmoe_router(self._h, layer, _ptr(x), _dtype_code(x), n, _ptr(logits),
+                                 _ptr(idx), _ptr(w), _ptr(sg), _ptr(xn), _stream(stream),
+                                 ctypes.byref(err)), err, "qmoe_router")
+        return dict(logits=logits, idx=idx, w=w, shared_gate=sg, xn=xn)
+
+    def dispatch(self, idx, stream=None):
+        import torch
+        n = idx.shape[0]
+        dev = idx.device
+        offsets = torch.empty((self.E + 1,), dtype=torch.int32, device=dev)
+        perm = torch.empty((max(1, n * self.k),), dtype=torch.int32, device=dev)
+        unique = torch.empty((self.E + 1,), dtype=torch.int32, device=dev)
+        err = QmoeErr()
+        _check(lib().qmoe_dispatch(self._h, _ptr(idx), n, _ptr(offsets), _ptr(perm), _ptr(unique),
+                                   _stream(stream), ctypes.byref(err)), err, "qmoe_dispatch")
+        return dict(offsets=offsets, perm=perm[: n * self.k], unique=unique)
+
+    def expert_gateup(self, layer, x, d, stream=None):
+        import torch
+        n = x.shape[0]
+        h = torch.empty((n * self.k + n, self.I), dtype=torch.float32, device=x.device)
+        err = QmoeErr()
+        _check(lib().qmoe_expert_gateup(self._h, layer, _ptr(x), _dtype_code(x), n, _ptr(d["perm"]),
+                                        _ptr(d["offsets"]), _ptr(d["unique"]), _ptr(h),
+                                        _stream(stream), ctypes.byref(err)), err,
+               "qmoe_expert_gateup")
+        return h
+
+    def expert_down(self, layer, h, n, d, stream=None):
+        import torch
+        y = torch.empty((n * self.k + n, self.H), dtype=torch.float32, device=h.device)
+        err = QmoeErr()
+        _check(lib().qmoe_expert_down(self._h, layer, _ptr(h), n, _ptr(d["perm"]), _ptr(d["offsets"]),
+                                      _ptr(d["unique"]), _ptr(y), _stream(stream), ctypes.byref(err)),
+               err, "qmoe_expert_down")
+        return y
+
+    def expert_ffn(self, layer, x, d, stream=None):
+        import torch
+        n = x.shape[0]
+        y = torch.empty((n * self.k + n, self.H), dtype=torch.float32, device=x.device)
+        err = QmoeErr()
+        _check(lib().qmoe_expert_ffn(self._h, layer, _ptr(x), _dtype_code(x), n, _ptr(d["perm"]),
+                                     _ptr(d["offsets"]), _ptr(d["unique"]), _ptr(y),
+                                     _stream(stream), ctypes.byref(err)), err, "qmoe_expert_ffn")
+        return y
+
+    def combine(self, y, perm, w, shared_gate, n, x_residual=None, stream=None):
+        import torch
+        out = torch.empty((n, self.H), dtype=torch.float32, device=y.device)
+        err = QmoeErr()
+        xd = _dtype_code(x_residual) if x_residual is not None else F32
+        _check(lib().qmoe_combine(self._h, _ptr(y), _ptr(perm), _ptr(w), _ptr(shared_gate), n,
+                                  _ptr(x_residual), xd, _ptr(out), _stream(stream),
+                                  ctypes.byref(err)), err, "qmoe_combine")
+        return out
+
+    def layer_forward(self, layer, x, out=None, residual=False, stream=None):
+        import torch
+        n = x.shape[0]
+        if out is None:
+            out = torch.empty((n, self.H), dtype=torch.float32, device=x.device)
+        err = QmoeErr()
+        _check(lib().qmoe_layer_forward(self._h, layer, _ptr(x), _dtype_code(x), n, _ptr(out),
+                                        RESIDUAL if residual else 0, _stream(stream),
+                                        ctypes.byref(err)), err, "qmoe_layer_forward")
+        return out
+
+    def layer_forward_raw(self, layer, x_ptr, x_dtype, n, out_ptr, flags, stream_handle):
+        """no-allocation variant for timing loops; returns the rc and message"""
+        err = QmoeErr()
+        rc = lib().qmoe_layer_forward(self._h, layer, x_ptr, x_dtype, n, out_ptr, flags,
+                                      stream_handle, ctypes.byref(err))
+        return rc, err.msg.decode(errors="replace")
+
+    def last_routing(self, n, stream=None):
+        """routing of the last layer_forward call (device tensors)"""
+        import torch
+        dev = torch.device("cuda", torch.cuda.current_device())
+        r = dict(idx=torch.empty((n, self.k), dtype=torch.int32, device=dev),
+                 w=torch.empty((n, self.k), dtype=torch.float32, device=dev),
+                 shared_gate=torch.empty((n,), dtype=torch.float32, device=dev),
+                 offsets=torch.empty((self.E + 1,), dtype=torch.int32, device=dev),
+                 perm=torch.empty((n * self.k,), dtype=torch.int32, device=dev),
+                 unique=torch.empty((self.E + 1,), dtype=torch.int32, device=dev))
+        err = QmoeErr()
+        _check(lib().qmoe_last_routing(self._h, n, _ptr(r["idx"]), _ptr(r["w"]),
+                                       _ptr(r["shared_gate"]), _ptr(r["offsets"]), _ptr(r["perm"]),
+                                       _ptr(r["unique"]), _stream(stream), ctypes.byref(err)),
+               err, "qmoe_last_routing")
+        return r
+
+    def forward_host(self, layer, x):
+        """moe_forward's host contract: numpy f32 [n,H] in, numpy f32 [n,H] out"""
+        import numpy as np
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        n = x.shape[0]
+        out = np.empty((n, self.H), dtype=np.float32)
+        err = QmoeErr()
+        _check(lib().qmoe_moe_forward_host(self._h, layer, x.ctypes.data, n, out.ctypes.data,
+                                           ctypes.byref(err)), err, "qmoe_moe_forward_host")
+        return out
+
+
+def synth_fill(t, kind: int, seed: int, layer: int, tag: int, start=0, stddev=1.0, stream=None):
+    """fill a torch CUDA tensor with a synthetic stream (kind 0 bf16 normal, 1 f32 normal, 2 codes)"""
+    err = QmoeErr()
+    _check(lib().qmoe_synth_fill(_ptr(t), t.numel(), kind, seed, layer, tag, start, stddev,
+                                 _stream(stream), ctypes.byref(err)), err, "qmoe_synth_fill")
+    return t
+
+
+def version() -> str:
+    return lib().qmoe_version().decode()
