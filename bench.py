@@ -1,0 +1,313 @@
+#!/usr/bin/env python3
+"""MoE-layer benchmark on one MI355X.
+
+Default workload ("decode"): one bf16 token per step through one MoE layer
+(hidden 2048, 512 experts top-10 + a sigmoid-gated shared expert, SwiGLU
+intermediate 512, MLX affine 4-bit weights with group 64).  Consecutive
+steps use different tokens and rotate over --layers resident layers so the
+expert weights come from HBM, not from the 256 MB Infinity Cache.  Steps are
+captured in a HIP graph (one node per kernel) and replayed.
+
+Prints ONE JSON line: whole-job tokens/s, the roofline of the dominant
+kernel (measured with HIP events on the stream it runs on), and the CPU
+baseline (the oracle's C restatement of the reference C port, timed on this
+host's cores on a bounded sample).
+"""
+import argparse
+import importlib.util
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(ROOT, "qwen3.8-flash-next_amd")
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA
+METRIC = "MoE-layer tokens/sec at decode+prefill, 1 MI355X; % HBM BW / % MFMA peak"
+
+
+def load_pkg():
+    spec = importlib.util.spec_from_file_location(
+        "qmoe_amd", os.path.join(PKG_DIR, "__init__.py"), submodule_search_locations=[PKG_DIR])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["qmoe_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def q4_matrix_bytes(rows, cols, g=64):
+    """codes (4 bits/weight) + one bf16 scale and one bf16 bias per group"""
+    return rows * cols // 2 + rows * (cols // g) * 4
+
+
+def expert_bytes(w):
+    return 2 * q4_matrix_bytes(w.moe_inter, w.hidden, w.group_size) + \
+        q4_matrix_bytes(w.hidden, w.moe_inter, w.group_size)
+
+
+class Setup:
+    """resident layers + per-step token batches for one workload"""
+
+    def __init__(self, pkg, torch, w, n_layers, n_steps, seed_base=1000):
+        self.pkg, self.torch, self.w = pkg, torch, w
+        self.L = n_layers
+        self.ctx = pkg.MoeContext.for_workload(w, n_layers=n_layers, max_tokens=w.n_tokens)
+        self.bias = []
+        sys.path.insert(0, ROOT)
+        for layer in range(n_layers):
+            rb = None
+            if w.zipf_s > 0:
+                rb = zipf_bias_host(w.n_experts, w.zipf_s, w.zipf_scale, w.seed * 1000003 + layer)
+            self.ctx.synth_layer(layer, w.seed, with_norm=w.rms_norm, router_bias=rb)
+        dt = torch.bfloat16 if w.x_bf16 else torch.float32
+        kind = 0 if w.x_bf16 else 1
+        self.x = []
+        for i in range(n_steps):
+            t = torch.empty((w.n_tokens, w.hidden), dtype=dt, device="cuda")
+            pkg.synth_fill(t, kind, seed_base + i, 0, pkg.TAGS["X"], stddev=1.0)
+            self.x.append(t)
+        self.out = [torch.empty((w.n_tokens, w.hidden), dtype=torch.float32, device="cuda")
+                    for _ in range(n_steps)]
+        torch.cuda.synchronize()
+
+
+def zipf_bias_host(E, s, scale, seed):
+    """Zipf(s) router bias b_e = scale * ln p_{pi(e)} -- same definition as
+    the oracle's orc_zipf_bias, restated here so the product path does not
+    import the oracle"""
+    import numpy as np
+
+    def mix64(z):
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9 & 0xFFFFFFFFFFFFFFFF
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EB & 0xFFFFFFFFFFFFFFFF
+        return z ^ (z >> 31)
+
+    G = 0x9E3779B97F4A7C15
+    key = mix64(seed ^ 0x5A17F00D)
+    perm = list(range(E))
+    for i in range(E - 1, 0, -1):
+        j = mix64((key + (i + 1) * G) & 0xFFFFFFFFFFFFFFFF) % (i + 1)
+        perm[i], perm[j] = perm[j], perm[i]
+    r = np.arange(1, E + 1, dtype=np.float64)
+    z = (r ** -s).sum()
+    p = (np.array(perm, dtype=np.float64) + 1) ** -s / z
+    return (scale * np.log(p)).astype(np.float32)
+
+
+def capture(torch, fn):
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # warm the launch path outside capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(torch, g, reps):
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1000.0  # seconds
+
+
+def bench_layer(pkg, torch, w, n_layers, steps, warmup):
+    """whole-layer steps: returns (seconds per step, setup)"""
+    S = n_layers
+    st = Setup(pkg, torch, w, n_layers, S)
+
+    def run():
+        for i in range(S):
+            st.ctx.layer_forward(i % n_layers, st.x[i], out=st.out[i],
+                                 residual=w.rms_norm)
+    g = capture(torch, run)
+    reps_w = max(1, math.ceil(warmup / S))
+    time_graph(torch, g, reps_w)
+    reps = max(1, math.ceil(steps / S))
+    sec = time_graph(torch, g, reps)
+    return sec / (reps * S), reps * S, reps_w * S, st
+
+
+def bench_gateup(pkg, torch, st, reps_target=200):
+    """dominant kernel: grouped gate/up GEMV, one launch per step with that
+    step's routing; returns (avg seconds per launch, algorithmic bytes per
+    launch averaged over the steps)"""
+    w, ctx = st.w, st.ctx
+    S = st.L
+    routes = []
+    for i in range(S):
+        xin = st.x[i]
+        r = ctx.router(i % st.L, xin)
+        d = ctx.dispatch(r["idx"])
+        routes.append(d)
+    torch.cuda.synchronize()
+    h = [torch.empty((w.n_tokens * w.top_k + w.n_tokens, w.moe_inter), dtype=torch.float32,
+                     device="cuda") for _ in range(S)]
+    algo = []
+    mb = q4_matrix_bytes(w.moe_inter, w.hidden, w.group_size)
+    xbytes = w.hidden * (2 if w.x_bf16 else 4)
+    for i in range(S):
+        U = int(routes[i]["unique"][0].item())
+        algo.append((U + 1) * 2 * mb + w.n_tokens * xbytes +
+                    (w.n_tokens * w.top_k + w.n_tokens) * w.moe_inter * 4)
+
+    # the raw entry point writes into the preallocated h buffers, so the
+    # captured graph does no allocation
+    lib = pkg.lib()
+    import ctypes
+
+    def run_raw():
+        stream = torch.cuda.current_stream().cuda_stream
+        err = pkg.QmoeErr()
+        for i in range(S):
+            d = routes[i]
+            rc = lib.qmoe_expert_gateup(ctx.handle, i % st.L, st.x[i].data_ptr(),
+                                        pkg.BF16 if w.x_bf16 else pkg.F32, w.n_tokens,
+                                        d["perm"].data_ptr(), d["offsets"].data_ptr(),
+                                        d["unique"].data_ptr(), h[i].data_ptr(), stream,
+                                        ctypes.byref(err))
+            assert rc == 0, err.msg
+    g = capture(torch, run_raw)
+    time_graph(torch, g, 2)
+    reps = max(1, math.ceil(reps_target / S))
+    sec = time_graph(torch, g, reps)
+    return sec / (reps * S), sum(algo) / len(algo)
+
+
+def cpu_baseline(w, budget_s=12.0):
+    """the oracle (C restatement of the reference C port's CPU path, q4
+    weights resident, gemm_q4 for every expert) timed on this host"""
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as orc
+    import numpy as np
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+    t0 = time.time()
+    rb = orc.zipf_bias(w.n_experts, w.zipf_s, w.zipf_scale, w.seed * 1000003) if w.zipf_s > 0 else None
+    L = orc.Layer(w.hidden, w.n_experts, w.top_k, w.moe_inter, seed=w.seed, router_bias=rb,
+                  with_norm=w.rms_norm, group_size=w.group_size)
+    log(f"cpu baseline: host layer generated in {time.time() - t0:.1f}s")
+    ntok_batch = w.n_tokens
+    # sample: as many batches as fit the budget (at least 2)
+    x = orc.gen_x(ntok_batch, w.hidden, 4242, bf16=w.x_bf16)
+    one = L.time_forward(x, w.x_bf16, threads, warmup=1, iters=1)
+    iters = max(2, min(50, int(budget_s / max(one, 1e-6))))
+    med = L.time_forward(x, w.x_bf16, threads, warmup=1, iters=iters, residual=w.rms_norm)
+    med1 = L.time_forward(x, w.x_bf16, 1, warmup=0, iters=max(1, min(3, int(4.0 / max(med * threads, 1e-6)))))
+    return dict(value=ntok_batch / med, unit="tokens/s", cores=threads, kind="port",
+                value_1thread=ntok_batch / med1,
+                sample=f"{iters} runs of the {w.name} batch ({ntok_batch} token(s), one layer, "
+                       f"H={w.hidden} E={w.n_experts} k={w.top_k} I={w.moe_inter}) through "
+                       f"oracle/moe_oracle.c with q4-resident gemm_q4 experts; median; "
+                       f"{threads} OpenMP threads (value_1thread: 1 thread)")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=480)
+    ap.add_argument("--warmup", type=int, default=48)
+    ap.add_argument("--workload", default="decode")
+    ap.add_argument("--layers", type=int, default=48,
+                    help="resident layers rotated over (defeats the Infinity Cache)")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--extra", default="batched,prefill",
+                    help="comma list of other workloads to time (secondary results)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              f"(the MoE layer runs on a single MI355X here)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    pkg = load_pkg()
+    dev = torch.cuda.get_device_name(0)
+    log(f"device {dev}, library {pkg.version()}")
+    w = pkg.WORKLOADS[args.workload]
+    n_layers = max(1, min(args.layers, 48 if w.n_tokens <= 64 else 8))
+
+    sec_step, steps, warm, st = bench_layer(pkg, torch, w, n_layers, args.steps, args.warmup)
+    log(f"{w.name}: {sec_step * 1e6:.2f} us/step over {steps} steps, {n_layers} layers")
+    k_sec, k_bytes = bench_gateup(pkg, torch, st)
+    achieved = k_bytes / k_sec / 1e9
+    log(f"gate/up kernel: {k_sec * 1e6:.2f} us/launch, {k_bytes / 1e6:.2f} MB -> {achieved:.0f} GB/s")
+    value = w.n_tokens / sec_step
+    layer_bytes = (10 + 1) * expert_bytes(w) + w.n_experts * w.hidden * 2 + w.hidden * 2
+
+    extra = {}
+    for name in [e for e in args.extra.split(",") if e and e != w.name]:
+        we = pkg.WORKLOADS[name]
+        st.ctx.close()
+        del st
+        torch.cuda.empty_cache()
+        nl = 8 if we.n_tokens <= 64 else 2
+        s_e, k_e, _, st = bench_layer(pkg, torch, we, nl, max(16, nl * 4), nl)
+        extra[name] = dict(tokens_per_s=we.n_tokens / s_e, ms_per_step=s_e * 1e3,
+                           tokens_per_step=we.n_tokens, layers_rotated=nl, steps=k_e)
+        log(f"{name}: {s_e * 1e3:.3f} ms/step -> {we.n_tokens / s_e:.0f} tokens/s")
+    st.ctx.close()
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(w)
+        log(f"cpu baseline: {cpu['value']:.1f} tokens/s with {cpu['cores']} threads, "
+            f"{cpu['value_1thread']:.1f} with 1")
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warm,
+        "ms_per_step": round(sec_step * 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{w.name}: {w.n_tokens} token(s)/step through one MoE layer, "
+                        f"hidden {w.hidden}, {w.n_experts} experts top-{w.top_k} + shared expert, "
+                        f"SwiGLU intermediate {w.moe_inter}, q4 g{w.group_size} weights "
+                        f"(bf16 scale/bias), {'bf16' if w.x_bf16 else 'f32'} activations, "
+                        f"{n_layers} resident layers rotated",
+            "tokens_per_step": w.n_tokens,
+            "layer_algorithmic_bytes_per_token": layer_bytes if w.n_tokens == 1 else None,
+            "layer_hbm_fraction": round(layer_bytes / sec_step / 1e9 / HBM_PEAK_GBS, 4)
+            if w.n_tokens == 1 else None,
+            "device": dev,
+            "extra": extra,
+        },
+        "roofline": {
+            "kernel": "k_q4gemv<2,...> (grouped gate/up GEMV + SiLU*up)",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_launch_us": round(k_sec * 1e6, 3),
+            "algorithmic_bytes_per_launch": int(k_bytes),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -325,31 +325,6 @@ static void load_x(const void *x, int x_is_bf16, size_t count, float *dst) {
     }
 }
 
-/* router for one token: model.c:1301-1318 with departures 1, 2, 4 */
-static void route_token(const orc_layer *L, const float *xn, float *logits, float *gate_logit,
-                        int *idx, float *w, float *shared_gate) {
-    int H = L->hidden, E = L->n_experts, k = L->top_k;
-    for (int e = 0; e < E; e++) {
-        float v = orc_dot_r64_bf16w(xn, L->router_w + (size_t)e * H, H);
-        if (L->router_bias) v = v + L->router_bias[e];
-        logits[e] = v;
-    }
-    float gl = orc_dot_r64_bf16w(xn, L->sh_gate_w, H);
-    if (gate_logit) *gate_logit = gl;
-    if (shared_gate) *shared_gate = orc_sigmoid(gl);
-    orc_topk_canonical(logits, E, k, idx);
-    /* model.c:1305-1318: softmax over the selected logits */
-    float mx = -1e30f;
-    for (int s = 0; s < k; s++)
-        if (logits[idx[s]] > mx) mx = logits[idx[s]];
-    float sum = 0.0f;
-    for (int s = 0; s < k; s++) {
-        w[s] = expf(logits[idx[s]] - mx);
-        sum += w[s];
-    }
-    for (int s = 0; s < k; s++) w[s] /= sum;
-}
-
 int orc_route(const orc_layer *L, const void *x, int x_is_bf16, int n, float *logits_out,
               float *gate_logit_out, int *idx_out, float *w_out, float *shared_gate_out,
               float *xn_out, int n_threads, char *err) {
@@ -360,32 +335,55 @@ int orc_route(const orc_layer *L, const void *x, int x_is_bf16, int n, float *lo
 #else
     (void)n_threads;
 #endif
+    float *xn = (float *)malloc((size_t)n * H * sizeof(float));
+    float *lg = (float *)malloc((size_t)n * (E + 1) * sizeof(float));
+#pragma omp parallel for schedule(static)
+    for (int t = 0; t < n; t++) {
+        float *xr = xn + (size_t)t * H;
+        load_x(x_is_bf16 ? (const void *)((const uint16_t *)x + (size_t)t * H)
+                         : (const void *)((const float *)x + (size_t)t * H),
+               x_is_bf16, (size_t)H, xr);
+        if (L->norm_w) orc_rmsnorm_r64(xr, L->norm_w, (size_t)H, L->rms_eps, xr);
+    }
+    /* logits: every (token, row) dot is independent; row E is the shared gate */
+#pragma omp parallel for schedule(static)
+    for (long long q = 0; q < (long long)n * (E + 1); q++) {
+        const int t = (int)(q / (E + 1)), e = (int)(q % (E + 1));
+        const float *xr = xn + (size_t)t * H;
+        float v = orc_dot_r64_bf16w(xr, e < E ? L->router_w + (size_t)e * H : L->sh_gate_w, H);
+        if (e < E && L->router_bias) v = v + L->router_bias[e];
+        lg[q] = v;
+    }
 #pragma omp parallel
     {
-        float *xn = (float *)malloc((size_t)H * sizeof(float));
-        float *lg = (float *)malloc((size_t)E * sizeof(float));
         int *id = (int *)malloc((size_t)k * sizeof(int));
         float *wt = (float *)malloc((size_t)k * sizeof(float));
 #pragma omp for schedule(static)
         for (int t = 0; t < n; t++) {
-            load_x(x_is_bf16 ? (const void *)((const uint16_t *)x + (size_t)t * H)
-                             : (const void *)((const float *)x + (size_t)t * H),
-                   x_is_bf16, (size_t)H, xn);
-            if (L->norm_w) orc_rmsnorm_r64(xn, L->norm_w, (size_t)H, L->rms_eps, xn);
-            float gl, sg;
-            route_token(L, xn, lg, &gl, id, wt, &sg);
-            if (logits_out) memcpy(logits_out + (size_t)t * E, lg, (size_t)E * sizeof(float));
-            if (gate_logit_out) gate_logit_out[t] = gl;
+            const float *row = lg + (size_t)t * (E + 1);
+            orc_topk_canonical(row, E, k, id);
+            /* model.c:1305-1318: softmax over the selected logits */
+            float mx = -1e30f;
+            for (int s = 0; s < k; s++)
+                if (row[id[s]] > mx) mx = row[id[s]];
+            float sum = 0.0f;
+            for (int s = 0; s < k; s++) {
+                wt[s] = expf(row[id[s]] - mx);
+                sum += wt[s];
+            }
+            for (int s = 0; s < k; s++) wt[s] /= sum;
+            if (logits_out) memcpy(logits_out + (size_t)t * E, row, (size_t)E * sizeof(float));
+            if (gate_logit_out) gate_logit_out[t] = row[E];
             if (idx_out) memcpy(idx_out + (size_t)t * k, id, (size_t)k * sizeof(int));
             if (w_out) memcpy(w_out + (size_t)t * k, wt, (size_t)k * sizeof(float));
-            if (shared_gate_out) shared_gate_out[t] = sg;
-            if (xn_out) memcpy(xn_out + (size_t)t * H, xn, (size_t)H * sizeof(float));
+            if (shared_gate_out) shared_gate_out[t] = orc_sigmoid(row[E]);
         }
-        free(xn);
-        free(lg);
         free(id);
         free(wt);
     }
+    if (xn_out) memcpy(xn_out, xn, (size_t)n * H * sizeof(float));
+    free(xn);
+    free(lg);
     return 0;
 }
 
@@ -425,34 +423,28 @@ static float q4_row_dot_bf16sb(const float *a, const float *xsum, const uint32_t
     return r;
 }
 
-/* One SwiGLU expert on one token row: model.c:1368-1375 (routed) or
- * model.c:1388-1395 (shared, via linear_forward -> gemm_q4). */
-static void expert_ffn_token(const float *xrow, const float *xsum_h, int H, int I, int gs,
-                             const uint32_t *gq, const uint16_t *gsc, const uint16_t *gb,
-                             const uint32_t *uq, const uint16_t *usc, const uint16_t *ub,
-                             const uint32_t *dq, const uint16_t *dsc, const uint16_t *db,
-                             int faithful, float *hbuf, float *xsum_i, float *yrow) {
-    size_t wrow_h = (size_t)H / 8, grow_h = (size_t)H / gs;
-    size_t wrow_i = (size_t)I / 8, grow_i = (size_t)I / gs;
-    for (int r = 0; r < I; r++) {
-        float g, u;
-        if (faithful) {
-            g = faithful_row_dot(xrow, gq + r * wrow_h, gsc + r * grow_h, gb + r * grow_h, H, gs);
-            u = faithful_row_dot(xrow, uq + r * wrow_h, usc + r * grow_h, ub + r * grow_h, H, gs);
-        } else {
-            g = q4_row_dot_bf16sb(xrow, xsum_h, gq + r * wrow_h, gsc + r * grow_h, gb + r * grow_h, H, gs);
-            u = q4_row_dot_bf16sb(xrow, xsum_h, uq + r * wrow_h, usc + r * grow_h, ub + r * grow_h, H, gs);
-        }
-        hbuf[r] = orc_silu(g) * u; /* kernel_silu then kernel_mul */
+/* The expert weights of one (token, expert) pair: routed expert e, or the
+ * shared expert when e < 0. */
+typedef struct {
+    const uint32_t *gq, *uq, *dq;
+    const uint16_t *gs, *gb, *us, *ub, *ds, *db;
+} expert_ptrs;
+
+static expert_ptrs expert_of(const orc_layer *L, int e) {
+    expert_ptrs p;
+    const int H = L->hidden, I = L->moe_inter, gs = L->group_size;
+    if (e < 0) {
+        p.gq = L->sh_gate_q; p.gs = L->sh_gate_s; p.gb = L->sh_gate_b;
+        p.uq = L->sh_up_q; p.us = L->sh_up_s; p.ub = L->sh_up_b;
+        p.dq = L->sh_down_q; p.ds = L->sh_down_s; p.db = L->sh_down_b;
+        return p;
     }
-    if (!faithful) group_sums(hbuf, I, gs, xsum_i);
-    for (int c = 0; c < H; c++) {
-        if (faithful)
-            yrow[c] = faithful_row_dot(hbuf, dq + c * wrow_i, dsc + c * grow_i, db + c * grow_i, I, gs);
-        else
-            yrow[c] = q4_row_dot_bf16sb(hbuf, xsum_i, dq + c * wrow_i, dsc + c * grow_i,
-                                        db + c * grow_i, I, gs);
-    }
+    const size_t eq = (size_t)I * (H / 8), es = (size_t)I * (H / gs);
+    const size_t dqs = (size_t)H * (I / 8), dss = (size_t)H * (I / gs);
+    p.gq = L->gate_q + e * eq; p.gs = L->gate_s + e * es; p.gb = L->gate_b + e * es;
+    p.uq = L->up_q + e * eq; p.us = L->up_s + e * es; p.ub = L->up_b + e * es;
+    p.dq = L->down_q + e * dqs; p.ds = L->down_s + e * dss; p.db = L->down_b + e * dss;
+    return p;
 }
 
 int orc_moe_forward(const orc_layer *L, const void *x, int n, float *out, const orc_opts *opt,
@@ -478,66 +470,113 @@ int orc_moe_forward(const orc_layer *L, const void *x, int n, float *out, const 
     if (xn_out) memcpy(xn_out, xn, (size_t)n * H * sizeof(float));
 
     if (out) {
-        int nout = token_sel ? n_sel : n;
-        int faithful = o.routed_mode == ORC_ROUTED_FAITHFUL;
-        size_t eq = (size_t)I * (H / 8), es = (size_t)I * (H / gs);
-        size_t dqs = (size_t)H * (I / 8), dss = (size_t)H * (I / gs);
-        /* Each selected token is independent (the layer is per-token); its
-         * expert contributions are accumulated in ascending expert order,
-         * matching the dispatch order (departure 3), then the shared expert
-         * (model.c:1376-1403).  out += w*r is contracted to fma by Apple
-         * clang, so it is written as fmaf. */
-#pragma omp parallel
-        {
-            float *hbuf = (float *)malloc((size_t)I * sizeof(float));
-            float *yrow = (float *)malloc((size_t)H * sizeof(float));
-            float *xs_h = (float *)malloc((size_t)(H / gs) * sizeof(float));
-            float *xs_i = (float *)malloc((size_t)(I / gs) * sizeof(float));
-            int *ord = (int *)malloc((size_t)k * sizeof(int));
-#pragma omp for schedule(dynamic, 1)
-            for (int j = 0; j < nout; j++) {
-                int t = token_sel ? token_sel[j] : j;
-                const float *xr = xn + (size_t)t * H;
-                float *orow = out + (size_t)j * H;
-                for (int c = 0; c < H; c++) orow[c] = 0.0f;
-                group_sums(xr, H, gs, xs_h);
-                /* slots of token t sorted by expert id */
-                for (int s = 0; s < k; s++) ord[s] = s;
-                for (int a = 1; a < k; a++)
-                    for (int b2 = a; b2 > 0 && idx[(size_t)t * k + ord[b2 - 1]] > idx[(size_t)t * k + ord[b2]]; b2--) {
-                        int tmp = ord[b2];
-                        ord[b2] = ord[b2 - 1];
-                        ord[b2 - 1] = tmp;
-                    }
-                for (int a = 0; a < k; a++) {
-                    int s = ord[a];
-                    int e = idx[(size_t)t * k + s];
-                    expert_ffn_token(xr, xs_h, H, I, gs, L->gate_q + e * eq, L->gate_s + e * es,
-                                     L->gate_b + e * es, L->up_q + e * eq, L->up_s + e * es,
-                                     L->up_b + e * es, L->down_q + e * dqs, L->down_s + e * dss,
-                                     L->down_b + e * dss, faithful, hbuf, xs_i, yrow);
-                    float wt = wts[(size_t)t * k + s];
-                    for (int c = 0; c < H; c++) orow[c] = fmaf(wt, yrow[c], orow[c]);
+        /* One (token, expert) "pair" per routed slot plus one for the shared
+         * expert.  Pairs of output row j are ordered by ascending expert id
+         * (the dispatch order, departure 3) with the shared expert last, which
+         * is the combine order of model.c:1376-1403. */
+        const int nout = token_sel ? n_sel : n;
+        const int faithful = o.routed_mode == ORC_ROUTED_FAITHFUL;
+        const int per = k + 1;
+        const size_t npairs = (size_t)nout * per;
+        const int G = H / gs, GI = I / gs;
+        int *pe = (int *)malloc(npairs * sizeof(int));
+        int *pt = (int *)malloc(npairs * sizeof(int));
+        float *pw = (float *)malloc(npairs * sizeof(float));
+        float *xs_h = (float *)malloc((size_t)nout * G * sizeof(float));
+        float *xs_i = (float *)malloc(npairs * GI * sizeof(float));
+        float *hb = (float *)malloc(npairs * I * sizeof(float));
+        float *yb = (float *)malloc(npairs * H * sizeof(float));
+        for (int j = 0; j < nout; j++) {
+            const int t = token_sel ? token_sel[j] : j;
+            int *ord = pe + (size_t)j * per; /* slots sorted by expert id */
+            for (int s = 0; s < k; s++) ord[s] = s;
+            for (int a2 = 1; a2 < k; a2++)
+                for (int b2 = a2; b2 > 0 && idx[(size_t)t * k + ord[b2 - 1]] > idx[(size_t)t * k + ord[b2]]; b2--) {
+                    int tmp = ord[b2];
+                    ord[b2] = ord[b2 - 1];
+                    ord[b2 - 1] = tmp;
                 }
-                /* shared expert: linear_forward -> gemm_q4 (model.c:1388-1395) */
-                expert_ffn_token(xr, xs_h, H, I, gs, L->sh_gate_q, L->sh_gate_s, L->sh_gate_b,
-                                 L->sh_up_q, L->sh_up_s, L->sh_up_b, L->sh_down_q, L->sh_down_s,
-                                 L->sh_down_b, 0, hbuf, xs_i, yrow);
-                float g = sg[t];
-                for (int c = 0; c < H; c++) orow[c] = fmaf(g, yrow[c], orow[c]);
-                if (o.residual) { /* the un-normalised input row plus the layer output */
-                    load_x(o.x_is_bf16 ? (const void *)((const uint16_t *)x + (size_t)t * H)
-                                       : (const void *)((const float *)x + (size_t)t * H),
-                           o.x_is_bf16, (size_t)H, yrow);
-                    for (int c = 0; c < H; c++) orow[c] = yrow[c] + orow[c];
+            for (int a2 = 0; a2 < k; a2++) {
+                const int s = ord[a2];
+                pw[(size_t)j * per + a2] = wts[(size_t)t * k + s];
+                ord[a2] = idx[(size_t)t * k + s];
+            }
+            pe[(size_t)j * per + k] = -1;
+            pw[(size_t)j * per + k] = sg[t];
+            for (int a2 = 0; a2 < per; a2++) pt[(size_t)j * per + a2] = j;
+            group_sums(xn + (size_t)t * H, H, gs, xs_h + (size_t)j * G);
+        }
+#ifdef _OPENMP
+        if (o.n_threads > 0) omp_set_num_threads(o.n_threads);
+#endif
+        /* gate/up + SwiGLU: every (pair, row) independent.  Routed experts
+         * follow model.c:1368-1375 (faithful: fp32-dequantised weights) or
+         * gemm_q4 (q4 mode); the shared expert always uses gemm_q4
+         * (linear_forward, model.c:193-202, 1388-1395). */
+#pragma omp parallel for schedule(static)
+        for (long long q = 0; q < (long long)(npairs * I); q++) {
+            const size_t pr = (size_t)(q / I);
+            const int r = (int)(q % I);
+            const int e = pe[pr];
+            const int t = token_sel ? token_sel[pt[pr]] : pt[pr];
+            const float *xr = xn + (size_t)t * H;
+            const float *xs = xs_h + (size_t)pt[pr] * G;
+            const expert_ptrs P = expert_of(L, e);
+            const size_t wq = (size_t)r * (H / 8), ws = (size_t)r * G;
+            float g, u;
+            if (faithful && e >= 0) {
+                g = faithful_row_dot(xr, P.gq + wq, P.gs + ws, P.gb + ws, H, gs);
+                u = faithful_row_dot(xr, P.uq + wq, P.us + ws, P.ub + ws, H, gs);
+            } else {
+                g = q4_row_dot_bf16sb(xr, xs, P.gq + wq, P.gs + ws, P.gb + ws, H, gs);
+                u = q4_row_dot_bf16sb(xr, xs, P.uq + wq, P.us + ws, P.ub + ws, H, gs);
+            }
+            hb[pr * I + r] = orc_silu(g) * u; /* kernel_silu then kernel_mul */
+        }
+#pragma omp parallel for schedule(static)
+        for (long long pr = 0; pr < (long long)npairs; pr++) group_sums(hb + pr * I, I, gs, xs_i + pr * GI);
+#pragma omp parallel for schedule(static)
+        for (long long q = 0; q < (long long)(npairs * H); q++) {
+            const size_t pr = (size_t)(q / H);
+            const int c = (int)(q % H);
+            const int e = pe[pr];
+            const expert_ptrs P = expert_of(L, e);
+            const size_t wq = (size_t)c * (I / 8), ws = (size_t)c * GI;
+            if (faithful && e >= 0)
+                yb[pr * H + c] = faithful_row_dot(hb + pr * I, P.dq + wq, P.ds + ws, P.db + ws, I, gs);
+            else
+                yb[pr * H + c] = q4_row_dot_bf16sb(hb + pr * I, xs_i + pr * GI, P.dq + wq, P.ds + ws,
+                                                   P.db + ws, I, gs);
+        }
+        /* combine: out = 0; out = fma(w, y, out) per pair in order (the
+         * reference's out += w*r under Apple clang's contraction) */
+#pragma omp parallel for schedule(static)
+        for (int j = 0; j < nout; j++) {
+            float *orow = out + (size_t)j * H;
+            for (int c = 0; c < H; c++) orow[c] = 0.0f;
+            for (int a2 = 0; a2 < per; a2++) {
+                const size_t pr = (size_t)j * per + a2;
+                const float wt = pw[pr];
+                for (int c = 0; c < H; c++) orow[c] = fmaf(wt, yb[pr * H + c], orow[c]);
+            }
+            if (o.residual) { /* the un-normalised input row plus the layer output */
+                const int t = token_sel ? token_sel[j] : j;
+                if (o.x_is_bf16) {
+                    const uint16_t *xb = (const uint16_t *)x + (size_t)t * H;
+                    for (int c = 0; c < H; c++) orow[c] = orc_bf16_to_f32(xb[c]) + orow[c];
+                } else {
+                    const float *xf = (const float *)x + (size_t)t * H;
+                    for (int c = 0; c < H; c++) orow[c] = xf[c] + orow[c];
                 }
             }
-            free(hbuf);
-            free(yrow);
-            free(xs_h);
-            free(xs_i);
-            free(ord);
         }
+        free(pe);
+        free(pt);
+        free(pw);
+        free(xs_h);
+        free(xs_i);
+        free(hb);
+        free(yb);
     }
     free(xn);
     free(logits);
