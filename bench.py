@@ -162,7 +162,7 @@ def bench_gateup(pkg, torch, st, reps_target=200):
     mb = q4_matrix_bytes(w.moe_inter, w.hidden, w.group_size)
     xbytes = w.hidden * (2 if w.x_bf16 else 4)
     for i in range(S):
-        U = int(routes[i]["unique"][0].item())
+        U = int(routes[i]["segments"][0].item())
         algo.append((U + 1) * 2 * mb + w.n_tokens * xbytes +
                     (w.n_tokens * w.top_k + w.n_tokens) * w.moe_inter * 4)
 
@@ -178,9 +178,8 @@ def bench_gateup(pkg, torch, st, reps_target=200):
             d = routes[i]
             rc = lib.qmoe_expert_gateup(ctx.handle, i % st.L, st.x[i].data_ptr(),
                                         pkg.BF16 if w.x_bf16 else pkg.F32, w.n_tokens,
-                                        d["perm"].data_ptr(), d["offsets"].data_ptr(),
-                                        d["unique"].data_ptr(), h[i].data_ptr(), stream,
-                                        ctypes.byref(err))
+                                        d["perm"].data_ptr(), d["segments"].data_ptr(),
+                                        h[i].data_ptr(), stream, ctypes.byref(err))
             assert rc == 0, err.msg
     g = capture(torch, run_raw)
     time_graph(torch, g, 2)

@@ -152,28 +152,32 @@ int qmoe_router(qmoe_ctx *ctx, int layer, const void *x, int x_dtype, int n, flo
 /* (2) Dispatch, model.c:1321-1367: stable counting sort of the flat slots
  *   f = t*k+s by expert.  offsets_out [E+1]: expert e's slots are
  *   perm_out[offsets[e] .. offsets[e+1]), tokens ascending.
- *   unique_out [1+E]: unique_out[0] = U, then the U experts that received
- *   tokens, ascending (model.c:1321-1332 lists them first-seen). */
+ *   segments_out [1+3E]: segments_out[0] = U, the number of experts that
+ *   received tokens, then one (expert, offsets[expert], count) triple per
+ *   such expert, experts ascending.  This is the reference's `unique` list
+ *   (model.c:1321-1332, first-seen order there) with each expert's run of
+ *   dispatch positions attached. */
 int qmoe_dispatch(qmoe_ctx *ctx, const int32_t *idx, int n, int32_t *offsets_out,
-                  int32_t *perm_out, int32_t *unique_out, void *stream, qmoe_err *err);
+                  int32_t *perm_out, int32_t *segments_out, void *stream, qmoe_err *err);
 
 /* (3) Expert SwiGLU FFN, model.c:1368-1375 and the shared expert
- *   model.c:1388-1395, as two grouped kernels:
+ *   model.c:1388-1395, as two grouped kernels over the segments of
+ *   qmoe_dispatch:
  *   gate/up:  h[p] = silu(x[t].Wg_e^T) * (x[t].Wu_e^T)   -> h_out [n*k+n, I]
  *   down:     y[p] = h[p].Wd_e^T                         -> y_out [n*k+n, H]
- *   Row p < n*k belongs to slot perm[p] (expert e with offsets[e] <= p <
- *   offsets[e+1]); rows n*k+t are the shared expert on token t.
- *   x is the router input (xn_out of qmoe_router when the layer has a norm). */
+ *   Row p < n*k belongs to slot perm[p] of the segment whose run contains p;
+ *   rows n*k+t are the shared expert on token t.  x is the router input
+ *   (xn_out of qmoe_router when the layer has a norm).  Segment entries
+ *   that do not fit the layer are skipped. */
 int qmoe_expert_gateup(qmoe_ctx *ctx, int layer, const void *x, int x_dtype, int n,
-                       const int32_t *perm, const int32_t *offsets, const int32_t *unique,
-                       float *h_out, void *stream, qmoe_err *err);
-int qmoe_expert_down(qmoe_ctx *ctx, int layer, const float *h, int n, const int32_t *perm,
-                     const int32_t *offsets, const int32_t *unique, float *y_out, void *stream,
-                     qmoe_err *err);
+                       const int32_t *perm, const int32_t *segments, float *h_out, void *stream,
+                       qmoe_err *err);
+int qmoe_expert_down(qmoe_ctx *ctx, int layer, const float *h, int n, const int32_t *segments,
+                     float *y_out, void *stream, qmoe_err *err);
 /* both of the above */
 int qmoe_expert_ffn(qmoe_ctx *ctx, int layer, const void *x, int x_dtype, int n,
-                    const int32_t *perm, const int32_t *offsets, const int32_t *unique,
-                    float *y_out, void *stream, qmoe_err *err);
+                    const int32_t *perm, const int32_t *segments, float *y_out, void *stream,
+                    qmoe_err *err);
 
 /* (4) Combine, model.c:1376-1403:
  *   out[t] = sum over t's slots in ascending expert order of w[t,s]*y[pos]
@@ -191,10 +195,10 @@ int qmoe_layer_forward(qmoe_ctx *ctx, int layer, const void *x, int x_dtype, int
 /* Copies the routing of the last qmoe_layer_forward call on this context
  * (n must be that call's token count) into caller device buffers, any of
  * which may be NULL: idx [n,k], w [n,k], shared_gate [n], offsets [E+1],
- * perm [n*k], unique [1+E].  An inspection hook for tests and tools; the
+ * perm [n*k], segments [1+3E].  An inspection hook for tests and tools; the
  * reference keeps these in moe_forward's scratch (model.c:1288-1300). */
 int qmoe_last_routing(qmoe_ctx *ctx, int n, int32_t *idx_out, float *w_out, float *shared_gate_out,
-                      int32_t *offsets_out, int32_t *perm_out, int32_t *unique_out, void *stream,
+                      int32_t *offsets_out, int32_t *perm_out, int32_t *segments_out, void *stream,
                       qmoe_err *err);
 
 /* Host-memory shim with moe_forward's data contract (model.c:1281-1282):

@@ -56,12 +56,12 @@ void orc_rmsnorm_seq(const float *x, const float *w, size_t n, float eps, float 
  * A length-K reduction is split into 8-element chunks; chunk c belongs to
  * leaf (c mod 64).  Each leaf is an fma chain over its chunks in ascending
  * order starting from +0.0f.  The 64 leaves are then combined by a
- * butterfly (p[l] += p[l^o] for o = 32,16,...,1), which is the pairwise tree
- * over leaves in bit-reversed order.  A 64-lane wavefront that loads one
- * 16-byte bf16 chunk per lane and reduces with xor shuffles computes exactly
- * this value in every lane. */
+ * butterfly (p[l] += p[l^o] for o = 1,2,4,...,32), which is the pairwise
+ * tree over the leaves in natural order.  A 64-lane wavefront that loads one
+ * 16-byte bf16 chunk per lane and reduces across lanes in that order
+ * computes exactly this value in every lane. */
 static float r64_combine(float *p) {
-    for (int o = 32; o >= 1; o >>= 1) {
+    for (int o = 1; o <= 32; o <<= 1) {
         float q[64];
         for (int l = 0; l < 64; l++) q[l] = p[l] + p[l ^ o];
         memcpy(p, q, sizeof(q));

@@ -22,7 +22,7 @@
  * Deliberate departures (each is also a contract the GPU path keeps):
  *   1. Router dot products use the fixed "R64" order (orc_dot_r64): 64
  *      strided partial fma-chains over 8-element chunks, combined by a
- *      bit-reversed pairwise tree.  The reference leaves the order to BNNS;
+ *      pairwise tree over the chunks' lanes in natural order.  The reference leaves the order to BNNS;
  *      fixing it makes expert selection bit-exact across CPU and GPU.
  *   2. Top-k order is canonical: value descending, ties to the lower expert
  *      id (-0.0 counts as +0.0).  The reference quickselect returns the same

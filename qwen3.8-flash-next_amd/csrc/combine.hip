@@ -46,24 +46,35 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
     __syncthreads();
     const int c = (blockIdx.y * 256 + threadIdx.x) * 4;
     if (c >= a.H) return;
+    const float g = qk_ld(a.sg + t);
+    const float4 vs = qk_ld((const float4 *)(a.y + ((size_t)a.n * a.k + t) * a.H + c));
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int j = 0; j < a.k; j++) {
-        const float wt = s_w[j];
-        if (s_pos[j] >= a.n * a.k) continue;
-        const float4 v = *(const float4 *)(a.y + (size_t)s_pos[j] * a.H + c);
-        acc.x = fmaf(wt, v.x, acc.x);
-        acc.y = fmaf(wt, v.y, acc.y);
-        acc.z = fmaf(wt, v.z, acc.z);
-        acc.w = fmaf(wt, v.w, acc.w);
+    /* issue eight independent row loads (clamped rows, no branches) before
+     * the dependent fma chain */
+    for (int j0 = 0; j0 < a.k; j0 += 8) {
+        float4 v[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; jj++) {
+            const int j = min(j0 + jj, a.k - 1);
+            const int p = s_pos[j] < a.n * a.k ? s_pos[j] : 0;
+            v[jj] = qk_ld((const float4 *)(a.y + (size_t)p * a.H + c));
+        }
+#pragma unroll
+        for (int jj = 0; jj < 8; jj++) {
+            const int j = j0 + jj;
+            if (j < a.k && s_pos[j] < a.n * a.k) {
+                const float wt = s_w[j];
+                acc.x = fmaf(wt, v[jj].x, acc.x);
+                acc.y = fmaf(wt, v[jj].y, acc.y);
+                acc.z = fmaf(wt, v[jj].z, acc.z);
+                acc.w = fmaf(wt, v[jj].w, acc.w);
+            }
+        }
     }
-    {
-        const float g = a.sg[t];
-        const float4 v = *(const float4 *)(a.y + ((size_t)a.n * a.k + t) * a.H + c);
-        acc.x = fmaf(g, v.x, acc.x);
-        acc.y = fmaf(g, v.y, acc.y);
-        acc.z = fmaf(g, v.z, acc.z);
-        acc.w = fmaf(g, v.w, acc.w);
-    }
+    acc.x = fmaf(g, vs.x, acc.x);
+    acc.y = fmaf(g, vs.y, acc.y);
+    acc.z = fmaf(g, vs.z, acc.z);
+    acc.w = fmaf(g, vs.w, acc.w);
     if (a.xres) {
         float4 xv;
         if (a.xbf16) {

@@ -13,6 +13,46 @@ typedef __bf16 qk_bf16x2 __attribute__((ext_vector_type(2)));
 
 #define QK_WAVE 64
 
+/* Loads through pointers known to be in global memory.  Pointers that
+ * travel in argument structs are generic to the compiler, which then emits
+ * flat loads; the cast gives global_load_* (vector memory counter only).
+ * Hot loops issue these unconditionally from clamped addresses and select
+ * the result afterwards, so independent loads are not serialised behind
+ * per-load branches. */
+#define QK_GLOBAL __attribute__((address_space(1)))
+typedef unsigned int qk_u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int qk_u32x2 __attribute__((ext_vector_type(2)));
+typedef float qk_f32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ __forceinline__ T qk_ld(const T *p) {
+    return *(const QK_GLOBAL T *)p;
+}
+__device__ __forceinline__ uint4 qk_ld(const uint4 *p) {
+    const qk_u32x4 v = *(const QK_GLOBAL qk_u32x4 *)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 qk_ld(const uint2 *p) {
+    const qk_u32x2 v = *(const QK_GLOBAL qk_u32x2 *)p;
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ int2 qk_ld(const int2 *p) {
+    const qk_u32x2 v = *(const QK_GLOBAL qk_u32x2 *)p;
+    return make_int2((int)v.x, (int)v.y);
+}
+__device__ __forceinline__ float4 qk_ld(const float4 *p) {
+    const qk_f32x4 v = *(const QK_GLOBAL qk_f32x4 *)p;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+template <typename T>
+__device__ __forceinline__ void qk_st(T *p, T v) {
+    *(QK_GLOBAL T *)p = v;
+}
+__device__ __forceinline__ void qk_st(float4 *p, float4 v) {
+    qk_f32x4 w = {v.x, v.y, v.z, v.w};
+    *(QK_GLOBAL qk_f32x4 *)p = w;
+}
+
 /* bf16 bits -> f32 (exact widening, c/src/util.h:56-61) */
 __device__ __forceinline__ float qk_bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ float qk_bf16_hi(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
@@ -79,12 +119,58 @@ __device__ __forceinline__ void qk_f32x8_to_pairs(const float x[8], uint32_t hi[
 __device__ __forceinline__ float qk_silu(float v) { return v / (1.0f + expf(-v)); }
 __device__ __forceinline__ float qk_sigmoid(float v) { return 1.0f / (1.0f + expf(-v)); }
 
-/* butterfly sum over aligned groups of `width` lanes (width a power of 2) */
+/* ------------------------------------------------ cross-lane reductions
+ * DPP moves within a 16-lane row (no LDS round trip), ds_bpermute for the
+ * two cross-row steps.  The sum is the pairwise tree over lanes in natural
+ * order: partner l^1, then l^2, l^4, l^8, l^16, l^32.  After the two quad
+ * steps every lane of a quad holds the same value, so the half-row mirror
+ * (lane l <- 7-l) delivers exactly the l^4 partial, and the row mirror
+ * (l <- 15-l) the l^8 partial.  Every lane of a group ends with the same
+ * bits. */
+template <int CTRL>
+__device__ __forceinline__ float qk_dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t qk_dpp_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, false);
+}
+#define QK_DPP_XOR1 0xB1       /* quad_perm [1,0,3,2] */
+#define QK_DPP_XOR2 0x4E       /* quad_perm [2,3,0,1] */
+#define QK_DPP_HALF_MIRROR 0x141
+#define QK_DPP_MIRROR 0x140
+
+/* sum over aligned groups of WIDTH lanes (WIDTH a power of 2, <= 64) */
 template <int WIDTH>
 __device__ __forceinline__ float qk_group_sum(float v) {
-#pragma unroll
-    for (int o = WIDTH / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, QK_WAVE);
+    if (WIDTH >= 2) v = v + qk_dpp<QK_DPP_XOR1>(v);
+    if (WIDTH >= 4) v = v + qk_dpp<QK_DPP_XOR2>(v);
+    if (WIDTH >= 8) v = v + qk_dpp<QK_DPP_HALF_MIRROR>(v);
+    if (WIDTH >= 16) v = v + qk_dpp<QK_DPP_MIRROR>(v);
+    if (WIDTH >= 32) v = v + __shfl_xor(v, 16, QK_WAVE);
+    if (WIDTH >= 64) v = v + __shfl_xor(v, 32, QK_WAVE);
     return v;
+}
+
+/* wave-wide max / min of a u32, result uniform (every lane of a row holds
+ * the row's extreme after the DPP steps; the four rows meet in scalars) */
+__device__ __forceinline__ uint32_t qk_wave_max_u32(uint32_t v) {
+    v = max(v, qk_dpp_u<QK_DPP_XOR1>(v));
+    v = max(v, qk_dpp_u<QK_DPP_XOR2>(v));
+    v = max(v, qk_dpp_u<QK_DPP_HALF_MIRROR>(v));
+    v = max(v, qk_dpp_u<QK_DPP_MIRROR>(v));
+    uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+    uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+    return max(max(a, b), max(c, d));
+}
+__device__ __forceinline__ uint32_t qk_wave_min_u32(uint32_t v) {
+    v = min(v, qk_dpp_u<QK_DPP_XOR1>(v));
+    v = min(v, qk_dpp_u<QK_DPP_XOR2>(v));
+    v = min(v, qk_dpp_u<QK_DPP_HALF_MIRROR>(v));
+    v = min(v, qk_dpp_u<QK_DPP_MIRROR>(v));
+    uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+    uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+    return min(min(a, b), min(c, d));
 }
 
 #define QK_CHECK_LAUNCH() ((int)hipGetLastError())

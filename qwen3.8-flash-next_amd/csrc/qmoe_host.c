@@ -173,11 +173,12 @@ int qmoe_create(qmoe_ctx **out, const qmoe_config *cfg, qmoe_err *err) {
     const size_t n = (size_t)cfg->max_tokens, E = (size_t)cfg->n_experts, k = (size_t)cfg->top_k;
     const size_t H = (size_t)cfg->hidden, I = (size_t)cfg->moe_inter;
     const size_t nw = (n + 31) / 32, rows = n * k + n;
-    size_t sz[13] = {n * (E + 1) * 4, n * k * 4, n * k * 4, n * 4, (E + 1) * 4, n * k * 4,
+    const size_t ntasks = (size_t)qk_mfma_max_tasks(c->shape, (int)n);
+    size_t sz[15] = {n * (E + 1) * 4, n * k * 4, n * k * 4, n * 4, (E + 1) * 4, n * k * 4,
                      n * k * 4, (E + 1) * 4, E * nw * 4, E * nw * 4, n * H * 4, rows * I * 4,
-                     rows * H * 4};
-    size_t total = 0, offs[13];
-    for (int i = 0; i < 13; i++) {
+                     rows * H * 4, (3 * E + 1) * 4, (2 + 2 * ntasks) * 4};
+    size_t total = 0, offs[15];
+    for (int i = 0; i < 15; i++) {
         offs[i] = total;
         total = align_up(total + sz[i]);
     }
@@ -201,6 +202,8 @@ int qmoe_create(qmoe_ctx **out, const qmoe_config *cfg, qmoe_err *err) {
     c->sc.xn = (float *)(b + offs[10]);
     c->sc.h = (float *)(b + offs[11]);
     c->sc.y = (float *)(b + offs[12]);
+    c->sc.segtab = (int32_t *)(b + offs[13]);
+    c->sc.tasks = (int32_t *)(b + offs[14]);
     *out = c;
     return 0;
 }
@@ -471,8 +474,53 @@ int qmoe_router(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n, float
                     "topk");
 }
 
+/* Grouped expert stages.  Segments with at least QK_MFMA_MIN_M rows run on
+ * the MFMA kernels (gate/up only for bf16 activations; down always, h is
+ * f32), the others on the GEMV kernels.  The MFMA task list is built from
+ * the segment table unless the caller says it is already current. */
+static int mfma_usable(const qmoe_ctx *c, int n) {
+    const qk_shape s = c->shape;
+    return s.I % 128 == 0 && s.H % 128 == 0 && n * (s.k + 1) >= QK_MFMA_MIN_M;
+}
+
+static int run_gateup(qmoe_ctx *c, const qmoe_layer_weights *W, const void *x, int xbf, int n,
+                      const int32_t *perm, const int32_t *segtab, float *h, void *stream,
+                      qmoe_err *err) {
+    const int mm = mfma_usable(c, n) && xbf;
+    int rc;
+    if (mm) {
+        rc = qk_launch_mfma_tasks(c->shape, n, segtab, QK_MFMA_MIN_M, c->sc.tasks, stream);
+        if (hip_fail(err, rc, "mfma tasks")) return -1;
+    }
+    rc = qk_launch_gateup(W, c->shape, x, xbf, n, perm, segtab, mm ? QK_MFMA_MIN_M : 0, h, stream);
+    if (hip_fail(err, rc, "gateup")) return -1;
+    if (mm) {
+        rc = qk_launch_gateup_mfma(W, c->shape, (const uint16_t *)x, n, perm, segtab, c->sc.tasks, h,
+                                   stream);
+        if (hip_fail(err, rc, "gateup mfma")) return -1;
+    }
+    return 0;
+}
+
+static int run_down(qmoe_ctx *c, const qmoe_layer_weights *W, const float *h, int n,
+                    const int32_t *segtab, int tasks_ready, float *y, void *stream, qmoe_err *err) {
+    const int mm = mfma_usable(c, n);
+    int rc;
+    if (mm && !tasks_ready) {
+        rc = qk_launch_mfma_tasks(c->shape, n, segtab, QK_MFMA_MIN_M, c->sc.tasks, stream);
+        if (hip_fail(err, rc, "mfma tasks")) return -1;
+    }
+    rc = qk_launch_down(W, c->shape, h, n, segtab, mm ? QK_MFMA_MIN_M : 0, y, stream);
+    if (hip_fail(err, rc, "down")) return -1;
+    if (mm) {
+        rc = qk_launch_down_mfma(W, c->shape, h, n, segtab, c->sc.tasks, y, stream);
+        if (hip_fail(err, rc, "down mfma")) return -1;
+    }
+    return 0;
+}
+
 int qmoe_dispatch(qmoe_ctx *c, const int32_t *idx, int n, int32_t *offsets_out, int32_t *perm_out,
-                  int32_t *unique_out, void *stream, qmoe_err *err) {
+                  int32_t *segments_out, void *stream, qmoe_err *err) {
     clear_err(err);
     if (!c) {
         set_err(err, "ctx is NULL");
@@ -483,9 +531,9 @@ int qmoe_dispatch(qmoe_ctx *c, const int32_t *idx, int n, int32_t *offsets_out, 
         return -1;
     }
     NEED(offsets_out, "offsets_out");
-    NEED(unique_out, "unique_out");
+    NEED(segments_out, "segments_out");
     if (n == 0) {
-        /* nothing routed: all offsets 0 and an empty unique list */
+        /* nothing routed: all offsets 0 and no segments */
         int32_t *z = (int32_t *)calloc((size_t)c->cfg.n_experts + 1, sizeof(int32_t));
         if (!z) {
             set_err(err, "out of host memory");
@@ -494,7 +542,7 @@ int qmoe_dispatch(qmoe_ctx *c, const int32_t *idx, int n, int32_t *offsets_out, 
         int rc = (int)hipMemcpyAsync(offsets_out, z, ((size_t)c->cfg.n_experts + 1) * 4,
                                      hipMemcpyHostToDevice, (hipStream_t)stream);
         if (!rc)
-            rc = (int)hipMemcpyAsync(unique_out, z, 4, hipMemcpyHostToDevice, (hipStream_t)stream);
+            rc = (int)hipMemcpyAsync(segments_out, z, 4, hipMemcpyHostToDevice, (hipStream_t)stream);
         if (!rc) rc = (int)hipStreamSynchronize((hipStream_t)stream);
         free(z);
         return hip_fail(err, rc, "dispatch(n=0)");
@@ -502,49 +550,41 @@ int qmoe_dispatch(qmoe_ctx *c, const int32_t *idx, int n, int32_t *offsets_out, 
     NEED(idx, "idx");
     NEED(perm_out, "perm_out");
     return hip_fail(err, qk_launch_dispatch(c->shape, n, idx, offsets_out, perm_out, c->sc.pos,
-                                            unique_out, c->sc.bits, c->sc.wprefix, stream),
+                                            c->sc.unique, segments_out, c->sc.bits, c->sc.wprefix,
+                                            stream),
                     "dispatch");
 }
 
 int qmoe_expert_gateup(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n,
-                       const int32_t *perm, const int32_t *offsets, const int32_t *unique,
-                       float *h_out, void *stream, qmoe_err *err) {
+                       const int32_t *perm, const int32_t *segments, float *h_out, void *stream,
+                       qmoe_err *err) {
     clear_err(err);
     if (check_call(c, layer, n, err) || check_dtype(x_dtype, err)) return -1;
     if (n == 0) return 0;
     NEED(x, "x");
     NEED(perm, "perm");
-    NEED(offsets, "offsets");
-    NEED(unique, "unique");
+    NEED(segments, "segments");
     NEED(h_out, "h_out");
-    return hip_fail(err, qk_launch_gateup(&c->layers[layer].dev, c->shape, x, x_dtype == QMOE_BF16,
-                                          n, perm, offsets, unique, h_out, stream),
-                    "gateup");
+    return run_gateup(c, &c->layers[layer].dev, x, x_dtype == QMOE_BF16, n, perm, segments, h_out,
+                      stream, err);
 }
 
-int qmoe_expert_down(qmoe_ctx *c, int layer, const float *h, int n, const int32_t *perm,
-                     const int32_t *offsets, const int32_t *unique, float *y_out, void *stream,
-                     qmoe_err *err) {
+int qmoe_expert_down(qmoe_ctx *c, int layer, const float *h, int n, const int32_t *segments,
+                     float *y_out, void *stream, qmoe_err *err) {
     clear_err(err);
     if (check_call(c, layer, n, err)) return -1;
     if (n == 0) return 0;
     NEED(h, "h");
-    NEED(perm, "perm");
-    NEED(offsets, "offsets");
-    NEED(unique, "unique");
+    NEED(segments, "segments");
     NEED(y_out, "y_out");
-    return hip_fail(err, qk_launch_down(&c->layers[layer].dev, c->shape, h, n, perm, offsets, unique,
-                                        y_out, stream),
-                    "down");
+    return run_down(c, &c->layers[layer].dev, h, n, segments, 0, y_out, stream, err);
 }
 
 int qmoe_expert_ffn(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n, const int32_t *perm,
-                    const int32_t *offsets, const int32_t *unique, float *y_out, void *stream,
-                    qmoe_err *err) {
-    if (qmoe_expert_gateup(c, layer, x, x_dtype, n, perm, offsets, unique, c ? c->sc.h : NULL,
-                           stream, err))
+                    const int32_t *segments, float *y_out, void *stream, qmoe_err *err) {
+    if (qmoe_expert_gateup(c, layer, x, x_dtype, n, perm, segments, c ? c->sc.h : NULL, stream, err))
         return -1;
-    return qmoe_expert_down(c, layer, c->sc.h, n, perm, offsets, unique, y_out, stream, err);
+    return qmoe_expert_down(c, layer, c->sc.h, n, segments, y_out, stream, err);
 }
 
 int qmoe_combine(qmoe_ctx *c, const float *y, const int32_t *perm, const float *w,
@@ -589,25 +629,26 @@ int qmoe_layer_forward(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n
     const qk_shape s = c->shape;
     qk_scratch *sc = &c->sc;
     const int xbf = x_dtype == QMOE_BF16;
-    int rc = qk_launch_router(W, s, x, xbf, n, sc->logits, W->norm_w ? sc->xn : NULL, stream);
+    int rc;
+    float *xn = W->norm_w ? sc->xn : NULL;
+    rc = qk_launch_router(W, s, x, xbf, n, sc->logits, xn, stream);
     if (hip_fail(err, rc, "router")) return -1;
     if (n <= QK_SMALL_N && n * s.k <= QK_SMALL_NK) {
         rc = qk_launch_topk_dispatch_small(s, n, sc->logits, NULL, sc->idx, sc->w, sc->sg,
-                                           sc->offsets, sc->perm, sc->pos, sc->unique, stream);
+                                           sc->offsets, sc->perm, sc->pos, sc->unique, sc->segtab,
+                                           stream);
         if (hip_fail(err, rc, "topk+dispatch")) return -1;
     } else {
         rc = qk_launch_topk(s, n, sc->logits, NULL, sc->idx, sc->w, sc->sg, stream);
         if (hip_fail(err, rc, "topk")) return -1;
-        rc = qk_launch_dispatch(s, n, sc->idx, sc->offsets, sc->perm, sc->pos, sc->unique, sc->bits,
-                                sc->wprefix, stream);
+        rc = qk_launch_dispatch(s, n, sc->idx, sc->offsets, sc->perm, sc->pos, sc->unique,
+                                sc->segtab, sc->bits, sc->wprefix, stream);
         if (hip_fail(err, rc, "dispatch")) return -1;
     }
     const void *xf = W->norm_w ? (const void *)sc->xn : x;
     const int xf_bf = W->norm_w ? 0 : xbf;
-    rc = qk_launch_gateup(W, s, xf, xf_bf, n, sc->perm, sc->offsets, sc->unique, sc->h, stream);
-    if (hip_fail(err, rc, "gateup")) return -1;
-    rc = qk_launch_down(W, s, sc->h, n, sc->perm, sc->offsets, sc->unique, sc->y, stream);
-    if (hip_fail(err, rc, "down")) return -1;
+    if (run_gateup(c, W, xf, xf_bf, n, sc->perm, sc->segtab, sc->h, stream, err)) return -1;
+    if (run_down(c, W, sc->h, n, sc->segtab, xf_bf, sc->y, stream, err)) return -1;
     rc = qk_launch_combine(s, n, sc->y, sc->pos, sc->w, sc->sg,
                            (flags & QMOE_RESIDUAL) ? x : NULL, xbf, out, stream);
     return hip_fail(err, rc, "combine");
@@ -640,7 +681,7 @@ int qmoe_moe_forward_host(qmoe_ctx *c, int layer, const float *x, int n, float *
 }
 
 int qmoe_last_routing(qmoe_ctx *c, int n, int32_t *idx_out, float *w_out, float *shared_gate_out,
-                      int32_t *offsets_out, int32_t *perm_out, int32_t *unique_out, void *stream,
+                      int32_t *offsets_out, int32_t *perm_out, int32_t *segments_out, void *stream,
                       qmoe_err *err) {
     clear_err(err);
     if (!c) {
@@ -658,7 +699,8 @@ int qmoe_last_routing(qmoe_ctx *c, int n, int32_t *idx_out, float *w_out, float 
         size_t bytes;
     } cp[6] = {{idx_out, c->sc.idx, nk * 4},         {w_out, c->sc.w, nk * 4},
                {shared_gate_out, c->sc.sg, (size_t)n * 4}, {offsets_out, c->sc.offsets, E1 * 4},
-               {perm_out, c->sc.perm, nk * 4},       {unique_out, c->sc.unique, E1 * 4}};
+               {perm_out, c->sc.perm, nk * 4},
+               {segments_out, c->sc.segtab, (3 * E1 - 2) * 4}};
     for (int i = 0; i < 6; i++) {
         if (!cp[i].dst) continue;
         if (hip_fail(err, (int)hipMemcpyAsync(cp[i].dst, cp[i].src, cp[i].bytes,

@@ -39,6 +39,8 @@ typedef struct {
     int32_t *perm;     /* [n*k] */
     int32_t *pos;      /* [n*k] inverse of perm */
     int32_t *unique;   /* [1+E] */
+    int32_t *segtab;   /* [1+3E]: U, then (expert, first position, count) per routed segment */
+    int32_t *tasks;    /* [2+2*max_tasks]: MFMA (segment, chunk) task list */
     uint32_t *bits;    /* [E, ceil(n/32)] token membership bitmask (large dispatch) */
     int32_t *wprefix;  /* [E, ceil(n/32)] per-word exclusive popcount prefix */
     float *xn;         /* [n, H] normalised router input */
@@ -60,20 +62,33 @@ int qk_launch_topk(qk_shape s, int n, const float *logits, float *logits_out, in
                    float *w, float *sg, void *stream);
 int qk_launch_topk_dispatch_small(qk_shape s, int n, const float *logits, float *logits_out,
                                   int32_t *idx, float *w, float *sg, int32_t *offsets,
-                                  int32_t *perm, int32_t *pos, int32_t *unique, void *stream);
+                                  int32_t *perm, int32_t *pos, int32_t *unique, int32_t *segtab,
+                                  void *stream);
 /* dispatch from idx alone (any n) */
 int qk_launch_dispatch(qk_shape s, int n, const int32_t *idx, int32_t *offsets, int32_t *perm,
-                       int32_t *pos, int32_t *unique, uint32_t *bits, int32_t *wprefix,
-                       void *stream);
+                       int32_t *pos, int32_t *unique, int32_t *segtab, uint32_t *bits,
+                       int32_t *wprefix, void *stream);
 /* pos[perm[p]] = p */
 int qk_launch_invert_perm(int count, const int32_t *perm, int32_t *pos, void *stream);
 
+/* grouped expert kernels over the segment table (segment 0 = shared expert
+ * on all n tokens at rows n*k.., segment i >= 1 = segtab entry i-1).
+ * The GEMV kernels take segments with fewer than max_m rows (0 = all);
+ * the MFMA kernels take the (segment, row chunk) tasks built by
+ * qk_launch_mfma_tasks for segments with at least min_m rows. */
+#define QK_MFMA_MIN_M 16
 int qk_launch_gateup(const qmoe_layer_weights *W, qk_shape s, const void *x, int x_bf16, int n,
-                     const int32_t *perm, const int32_t *offsets, const int32_t *unique,
-                     float *h, void *stream);
+                     const int32_t *perm, const int32_t *segtab, int max_m, float *h, void *stream);
 int qk_launch_down(const qmoe_layer_weights *W, qk_shape s, const float *h, int n,
-                   const int32_t *perm, const int32_t *offsets, const int32_t *unique, float *y,
-                   void *stream);
+                   const int32_t *segtab, int max_m, float *y, void *stream);
+int qk_mfma_max_tasks(qk_shape s, int n);
+int qk_launch_mfma_tasks(qk_shape s, int n, const int32_t *segtab, int min_m, int32_t *tasks,
+                         void *stream);
+int qk_launch_gateup_mfma(const qmoe_layer_weights *W, qk_shape s, const uint16_t *x, int n,
+                          const int32_t *perm, const int32_t *segtab, const int32_t *tasks,
+                          float *h, void *stream);
+int qk_launch_down_mfma(const qmoe_layer_weights *W, qk_shape s, const float *h, int n,
+                        const int32_t *segtab, const int32_t *tasks, float *y, void *stream);
 int qk_launch_combine(qk_shape s, int n, const float *y, const int32_t *pos, const float *w,
                       const float *sg, const void *x_res, int x_bf16, float *out, void *stream);
 

@@ -6,8 +6,8 @@
  * Router reduction order ("R64", bit-exact with the oracle): for one
  * (token, expert) dot product the K axis is cut into 8-element chunks, chunk
  * c goes to lane c%64 of a wavefront, each lane runs an fma chain over its
- * chunks in ascending order starting at +0.0f, and the wave combines lanes
- * with xor butterflies 32,16,...,1.  Every lane ends with the same value.
+ * chunks in ascending order starting at +0.0f, and the wave combines its
+ * lanes with the pairwise tree of qk_group_sum<64> (partners l^1 ... l^32).
  */
 #include "qk_device.h"
 
@@ -25,96 +25,94 @@ struct RouterArgs {
     float eps;
 };
 
-/* load the 8 activations of chunk c of token row t as f32 */
+/* load the 8 activations of chunk c of a token row as f32 */
 template <bool XBF16>
 __device__ __forceinline__ void load_x8(const void *x, size_t row_off, int c, float v[8]) {
     if (XBF16) {
-        uint4 d = *((const uint4 *)((const uint16_t *)x + row_off) + c);
+        uint4 d = qk_ld((const uint4 *)((const uint16_t *)x + row_off) + c);
         v[0] = qk_bf16_lo(d.x); v[1] = qk_bf16_hi(d.x);
         v[2] = qk_bf16_lo(d.y); v[3] = qk_bf16_hi(d.y);
         v[4] = qk_bf16_lo(d.z); v[5] = qk_bf16_hi(d.z);
         v[6] = qk_bf16_lo(d.w); v[7] = qk_bf16_hi(d.w);
     } else {
         const float4 *p = (const float4 *)((const float *)x + row_off) + 2 * c;
-        float4 a = p[0], b = p[1];
+        float4 a = qk_ld(p), b = qk_ld(p + 1);
         v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
         v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
     }
 }
 
-#define RT_MAXCH 16 /* chunks per lane: H <= 8192 */
+#define RT_TB 8 /* tokens per wave */
 
 /*
- * One wavefront per (row, token block).  Rows 0..E-1 are the router,
- * row E is the shared-expert gate.  grid.x = ceil((E+1)/4), grid.y = token
- * blocks of RT_TB tokens.  With NORM, every wave RMS-normalises its tokens
- * itself (R64 sum of squares, r = 1/sqrt(ss/H + eps), (x*r)*w as
+ * One wavefront per (row, token block); NCH = chunks per lane (a power of
+ * two >= ceil(H/512)).  Rows 0..E-1 are the router, row E is the
+ * shared-expert gate.  Lanes whose chunk lies past the row load a valid
+ * address and keep their partial unchanged (a select, not a branch), so
+ * all loads issue back to back.  With NORM, every wave RMS-normalises its
+ * tokens itself (R64 sum of squares, r = 1/sqrt(ss/H + eps), (x*r)*w as
  * kernel.c:10-20) and the wave of row 0 writes the normalised rows.
  */
-#define RT_TB 8
-template <bool XBF16, bool NORM>
-__global__ __launch_bounds__(256) void k_router(RouterArgs a) {
+template <bool XBF16, bool NORM, int NCH>
+__device__ __forceinline__ void router_rows(const RouterArgs &a, int row, int t0, int t1) {
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row > a.E) return;
     const int chunks = a.H >> 3;
     const uint16_t *wrow = row < a.E ? a.router_w + (size_t)row * a.H : a.sh_gate_w;
-    uint4 wv[RT_MAXCH];
+    uint4 wv[NCH];
+    bool cv[NCH];
+    int cc[NCH];
 #pragma unroll
-    for (int i = 0; i < RT_MAXCH; i++) {
-        int c = lane + 64 * i;
-        if (c < chunks) wv[i] = ((const uint4 *)wrow)[c];
+    for (int i = 0; i < NCH; i++) {
+        const int c = lane + 64 * i;
+        cv[i] = c < chunks;
+        cc[i] = cv[i] ? c : 0;
+        wv[i] = qk_ld((const uint4 *)wrow + cc[i]);
     }
     const float bias = (row < a.E && a.router_bias) ? a.router_bias[row] : 0.0f;
-    const int t0 = blockIdx.y * RT_TB;
-    const int t1 = min(a.n, t0 + RT_TB);
     for (int t = t0; t < t1; t++) {
         const size_t roff = (size_t)t * a.H;
-        float r = 1.0f;
+        float v[NCH][8];
+#pragma unroll
+        for (int i = 0; i < NCH; i++) load_x8<XBF16>(a.x, roff, cc[i], v[i]);
         if (NORM) {
             float ss = 0.0f;
 #pragma unroll
-            for (int i = 0; i < RT_MAXCH; i++) {
-                int c = lane + 64 * i;
-                if (c < chunks) {
-                    float v[8];
-                    load_x8<XBF16>(a.x, roff, c, v);
+            for (int i = 0; i < NCH; i++) {
+                float s2 = ss;
 #pragma unroll
-                    for (int j = 0; j < 8; j++) ss = fmaf(v[j], v[j], ss);
-                }
+                for (int j = 0; j < 8; j++) s2 = fmaf(v[i][j], v[i][j], s2);
+                ss = cv[i] ? s2 : ss;
             }
             ss = qk_group_sum<64>(ss);
-            r = 1.0f / sqrtf(ss / (float)a.H + a.eps);
+            const float r = 1.0f / sqrtf(ss / (float)a.H + a.eps);
+#pragma unroll
+            for (int i = 0; i < NCH; i++) {
+                const float4 *nw = (const float4 *)a.norm_w + 2 * cc[i];
+                const float4 w0 = qk_ld(nw), w1 = qk_ld(nw + 1);
+                const float wn[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[i][j] = (v[i][j] * r) * wn[j];
+                if (row == 0 && a.xn && cv[i]) {
+                    float4 *o = (float4 *)(a.xn + roff) + 2 * cc[i];
+                    o[0] = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
+                    o[1] = make_float4(v[i][4], v[i][5], v[i][6], v[i][7]);
+                }
+            }
         }
         float acc = 0.0f;
 #pragma unroll
-        for (int i = 0; i < RT_MAXCH; i++) {
-            int c = lane + 64 * i;
-            if (c < chunks) {
-                float v[8];
-                load_x8<XBF16>(a.x, roff, c, v);
-                if (NORM) {
-                    const float4 *nw = (const float4 *)a.norm_w + 2 * c;
-                    float4 w0 = nw[0], w1 = nw[1];
-                    float wn[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-                    for (int j = 0; j < 8; j++) v[j] = (v[j] * r) * wn[j];
-                    if (row == 0 && a.xn) {
-                        float4 *o = (float4 *)(a.xn + roff) + 2 * c;
-                        o[0] = make_float4(v[0], v[1], v[2], v[3]);
-                        o[1] = make_float4(v[4], v[5], v[6], v[7]);
-                    }
-                }
-                const uint4 d = wv[i];
-                acc = fmaf(v[0], qk_bf16_lo(d.x), acc);
-                acc = fmaf(v[1], qk_bf16_hi(d.x), acc);
-                acc = fmaf(v[2], qk_bf16_lo(d.y), acc);
-                acc = fmaf(v[3], qk_bf16_hi(d.y), acc);
-                acc = fmaf(v[4], qk_bf16_lo(d.z), acc);
-                acc = fmaf(v[5], qk_bf16_hi(d.z), acc);
-                acc = fmaf(v[6], qk_bf16_lo(d.w), acc);
-                acc = fmaf(v[7], qk_bf16_hi(d.w), acc);
-            }
+        for (int i = 0; i < NCH; i++) {
+            const uint4 d = wv[i];
+            float a2 = acc;
+            a2 = fmaf(v[i][0], qk_bf16_lo(d.x), a2);
+            a2 = fmaf(v[i][1], qk_bf16_hi(d.x), a2);
+            a2 = fmaf(v[i][2], qk_bf16_lo(d.y), a2);
+            a2 = fmaf(v[i][3], qk_bf16_hi(d.y), a2);
+            a2 = fmaf(v[i][4], qk_bf16_lo(d.z), a2);
+            a2 = fmaf(v[i][5], qk_bf16_hi(d.z), a2);
+            a2 = fmaf(v[i][6], qk_bf16_lo(d.w), a2);
+            a2 = fmaf(v[i][7], qk_bf16_hi(d.w), a2);
+            acc = cv[i] ? a2 : acc;
         }
         acc = qk_group_sum<64>(acc);
         if (lane == 0) {
@@ -123,6 +121,42 @@ __global__ __launch_bounds__(256) void k_router(RouterArgs a) {
         }
     }
 }
+
+template <bool XBF16, bool NORM, int NCH>
+__global__ __launch_bounds__(256) void k_router(RouterArgs a) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row > a.E) return;
+    const int t0 = blockIdx.y * RT_TB;
+    router_rows<XBF16, NORM, NCH>(a, row, t0, min(a.n, t0 + RT_TB));
+}
+
+/* chunks per lane rounded up to a power of two */
+static int router_nch(int H) {
+    const int per = (H / 8 + 63) / 64;
+    int p = 1;
+    while (p < per) p <<= 1;
+    return p;
+}
+
+#define RT_DISPATCH(KERNEL, XB, NORM, NCH, GRID, ARGS)                                         \
+    do {                                                                                       \
+        if (NCH == 1) hipLaunchKernelGGL((KERNEL<XB, NORM, 1>), GRID, dim3(256), 0, st, ARGS);  \
+        else if (NCH == 2) hipLaunchKernelGGL((KERNEL<XB, NORM, 2>), GRID, dim3(256), 0, st, ARGS); \
+        else if (NCH == 4) hipLaunchKernelGGL((KERNEL<XB, NORM, 4>), GRID, dim3(256), 0, st, ARGS); \
+        else if (NCH == 8) hipLaunchKernelGGL((KERNEL<XB, NORM, 8>), GRID, dim3(256), 0, st, ARGS); \
+        else hipLaunchKernelGGL((KERNEL<XB, NORM, 16>), GRID, dim3(256), 0, st, ARGS);          \
+    } while (0)
+
+#define RT_DISPATCH4(KERNEL, XBF, NRM, NCH, GRID, ARGS)                                         \
+    do {                                                                                       \
+        if (XBF) {                                                                             \
+            if (NRM) RT_DISPATCH(KERNEL, true, true, NCH, GRID, ARGS);                          \
+            else RT_DISPATCH(KERNEL, true, false, NCH, GRID, ARGS);                             \
+        } else {                                                                               \
+            if (NRM) RT_DISPATCH(KERNEL, false, true, NCH, GRID, ARGS);                         \
+            else RT_DISPATCH(KERNEL, false, false, NCH, GRID, ARGS);                            \
+        }                                                                                      \
+    } while (0)
 
 extern "C" int qk_launch_router(const qmoe_layer_weights *W, qk_shape s, const void *x, int x_bf16,
                                 int n, float *logits, float *xn, void *stream) {
@@ -141,14 +175,8 @@ extern "C" int qk_launch_router(const qmoe_layer_weights *W, qk_shape s, const v
     a.eps = s.eps;
     dim3 grid((s.E + 1 + 3) / 4, (n + RT_TB - 1) / RT_TB);
     hipStream_t st = (hipStream_t)stream;
-    bool norm = W->norm_w != nullptr;
-    if (x_bf16) {
-        if (norm) hipLaunchKernelGGL((k_router<true, true>), grid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((k_router<true, false>), grid, dim3(256), 0, st, a);
-    } else {
-        if (norm) hipLaunchKernelGGL((k_router<false, true>), grid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((k_router<false, false>), grid, dim3(256), 0, st, a);
-    }
+    const int nch = router_nch(s.H);
+    RT_DISPATCH4(k_router, x_bf16, W->norm_w != nullptr, nch, grid, a);
     return QK_CHECK_LAUNCH();
 }
 
@@ -159,64 +187,126 @@ __device__ __forceinline__ uint32_t qk_ordkey(float v) {
     uint32_t b = __float_as_uint(v + 0.0f);
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
-
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int o) {
-    uint32_t lo = __shfl_xor((uint32_t)v, o, QK_WAVE);
-    uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o, QK_WAVE);
-    return ((uint64_t)hi << 32) | lo;
+__device__ __forceinline__ float qk_ordkey_value(uint32_t o) {
+    return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
 }
 
 #define TK_MAXPL (QK_MAX_EXPERTS / 64)
 
+/* per-wave LDS for the top-k ranking */
+struct TopkLds {
+    uint32_t key[QK_MAX_TOPK];
+    int32_t id[QK_MAX_TOPK];
+    uint32_t skey[QK_MAX_TOPK];
+    int32_t sid[QK_MAX_TOPK];
+};
+
+__device__ __forceinline__ int qk_lanes_below(uint64_t mask) {
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                          __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
 /*
- * One wavefront selects the top k of row[0..E): k rounds of a wave-wide
- * max over keys (ordered value, ~id), so larger logits win and equal logits
- * go to the lower expert id.  Then w_s = exp(v_s - v_0) / sum (the selected
- * values are in descending order, so v_0 is their max; model.c:1305-1318).
- * Lane s < k returns slot s.
+ * One wavefront selects the top k of row[0..E) (all 64 lanes active).
+ * (1) Radix select on the order-preserving keys: from the top bit down,
+ *     keep a bit if at least k keys reach the candidate prefix (counted
+ *     with ballots); stop early once exactly k keys reach it.  (2) The
+ *     selected set is every key above the threshold plus, if the threshold
+ *     is shared, the lowest ids among the keys equal to it.  (3) The k
+ *     entries are ranked by (value desc, id asc) in LDS.  Then
+ *     w_s = exp(v_s - v_0) / sum over the sorted slots (model.c:1305-1318).
+ * Lane s < k returns slot s.  The set and order are exactly the oracle's
+ * canonical top-k; -0 and +0 tie.
  */
-__device__ __forceinline__ void wave_topk(const float *row, int E, int k, int lane, int &my_id,
-                                          float &my_w) {
-    uint64_t key[TK_MAXPL];
+__device__ __forceinline__ void wave_topk(const float *row, int E, int k, int lane, TopkLds *L,
+                                          int &my_id, float &my_w) {
+    uint32_t key[TK_MAXPL];
+    const int PL = (E + 63) >> 6;
 #pragma unroll
     for (int i = 0; i < TK_MAXPL; i++) {
-        int e = lane + 64 * i;
-        key[i] = e < E ? (((uint64_t)qk_ordkey(row[e]) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e))
-                       : 0ull;
+        const int e = lane + 64 * i;
+        const float v = qk_ld(row + (e < E ? e : E - 1));
+        key[i] = qk_ordkey(v);
     }
-    float vmax = 0.0f, sum = 0.0f, my_e = 0.0f;
-    my_id = 0;
-    for (int s = 0; s < k; s++) {
-        uint64_t best = key[0];
-        int bi = 0;
+    auto count_ge = [&](uint32_t cand) -> int {
+        int c = 0;
 #pragma unroll
-        for (int i = 1; i < TK_MAXPL; i++)
-            if (key[i] > best) {
-                best = key[i];
-                bi = i;
+        for (int i = 0; i < TK_MAXPL; i++)
+            if (i < PL) c += __popcll(__ballot(key[i] >= cand && lane + 64 * i < E));
+        return c;
+    };
+    uint32_t T = 0u;
+    int cge = E;
+    for (int b = 31; b >= 0 && cge != k; b--) {
+        const uint32_t cand = T | (1u << b);
+        const int c = count_ge(cand);
+        if (c >= k) {
+            T = cand;
+            cge = c;
+        }
+    }
+    /* selection flags: key > T, or key == T taken in id order until k */
+    int need = k;
+    if (cge != k) need = k - (T == 0xFFFFFFFFu ? 0 : count_ge(T + 1u)); /* ties at T to take */
+    uint32_t sel = 0u;
+#pragma unroll
+    for (int i = 0; i < TK_MAXPL; i++) {
+        if (i < PL) {
+            const bool valid = lane + 64 * i < E;
+            const bool gt = valid && (cge == k ? key[i] >= T : key[i] > T);
+            bool take = gt;
+            if (cge != k) {
+                const uint64_t eq = __ballot(valid && key[i] == T);
+                const int r = qk_lanes_below(eq);
+                if (valid && key[i] == T && r < need) take = true;
+                need -= min(need, (int)__popcll(eq));
             }
-        uint64_t m = best;
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            uint64_t other = shfl_xor_u64(m, o);
-            m = other > m ? other : m;
-        }
-        if (best == m) {
-#pragma unroll
-            for (int i = 0; i < TK_MAXPL; i++)
-                if (i == bi) key[i] = 0ull;
-        }
-        const int id = (int)(0xFFFFFFFFu - (uint32_t)m);
-        const float v = row[id];
-        if (s == 0) vmax = v;
-        const float ev = expf(v - vmax);
-        sum += ev;
-        if (lane == s) {
-            my_id = id;
-            my_e = ev;
+            if (take) sel |= 1u << i;
         }
     }
+    /* compact the k entries into LDS */
+    int base = 0;
+#pragma unroll
+    for (int i = 0; i < TK_MAXPL; i++) {
+        if (i < PL) {
+            const bool t = (sel >> i) & 1u;
+            const uint64_t m = __ballot(t);
+            if (t) {
+                const int pos = base + qk_lanes_below(m);
+                L->key[pos] = key[i];
+                L->id[pos] = lane + 64 * i;
+            }
+            base += (int)__popcll(m);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f); /* lgkmcnt(0): LDS writes done */
+    __builtin_amdgcn_wave_barrier();
+    /* rank: value desc, id asc */
+    if (lane < k) {
+        const uint32_t mk = L->key[lane];
+        const int mi = L->id[lane];
+        int rank = 0;
+        for (int j = 0; j < k; j++) {
+            const uint32_t kj = L->key[j];
+            const int ij = L->id[j];
+            rank += (kj > mk || (kj == mk && ij < mi)) ? 1 : 0;
+        }
+        L->skey[rank] = mk;
+        L->sid[rank] = mi;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    /* softmax over the selected logits in slot order */
+    const float vmax = qk_ordkey_value(L->skey[0]);
+    float sum = 0.0f, my_e = 0.0f;
+    for (int j = 0; j < k; j++) {
+        const float ev = expf(qk_ordkey_value(L->skey[j]) - vmax);
+        sum += ev;
+        if (j == lane) my_e = ev;
+    }
+    my_id = lane < k ? L->sid[lane] : 0;
     my_w = my_e / sum;
+    __builtin_amdgcn_wave_barrier();
 }
 
 struct TopkArgs {
@@ -228,11 +318,12 @@ struct TopkArgs {
     int E, k, n;
 };
 
-__device__ __forceinline__ void topk_token(const TopkArgs &a, int t, int lane, int32_t *lds_idx) {
+__device__ __forceinline__ void topk_token(const TopkArgs &a, int t, int lane, TopkLds *L,
+                                           int32_t *lds_idx) {
     const float *row = a.logits + (size_t)t * (a.E + 1);
     int id;
     float wt;
-    wave_topk(row, a.E, a.k, lane, id, wt);
+    wave_topk(row, a.E, a.k, lane, L, id, wt);
     if (lane < a.k) {
         a.idx[(size_t)t * a.k + lane] = id;
         a.w[(size_t)t * a.k + lane] = wt;
@@ -244,9 +335,10 @@ __device__ __forceinline__ void topk_token(const TopkArgs &a, int t, int lane, i
 }
 
 __global__ __launch_bounds__(256) void k_topk(TopkArgs a) {
+    __shared__ TopkLds s_tk[4];
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= a.n) return;
-    topk_token(a, t, threadIdx.x & 63, nullptr);
+    topk_token(a, t, threadIdx.x & 63, &s_tk[threadIdx.x >> 6], nullptr);
 }
 
 extern "C" int qk_launch_topk(qk_shape s, int n, const float *logits, float *logits_out,
@@ -265,10 +357,15 @@ extern "C" int qk_launch_topk(qk_shape s, int n, const float *logits, float *log
  * popcount of B[e] below bit t, which is exactly the number of earlier
  * tokens that chose e.  So the result equals the oracle's sequential
  * counting sort with no ordering dependence on the hardware.
+ *
+ * Outputs: offsets [E+1], perm [n*k], pos [n*k] (inverse), unique [1+E]
+ * (count, then the experts with tokens ascending) and the segment table
+ * segtab [1+3E] (count, then (expert, offsets[e], count[e]) per segment).
  */
 
-/* block-wide exclusive scan of one int per thread (blockDim = 1024) */
-__device__ int block_exscan_1024(int v, int *lds /* >= 16 ints */, int &total) {
+/* block-wide exclusive scan of NT/64 waves, one int per thread */
+template <int NT>
+__device__ int block_exscan(int v, int *lds /* >= NT/64 ints */, int &total) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     int inc = v;
 #pragma unroll
@@ -279,7 +376,7 @@ __device__ int block_exscan_1024(int v, int *lds /* >= 16 ints */, int &total) {
     if (lane == 63) lds[wave] = inc;
     __syncthreads();
     int wbase = 0, tot = 0;
-    for (int i = 0; i < 16; i++) {
+    for (int i = 0; i < NT / 64; i++) {
         int s = lds[i];
         if (i < wave) wbase += s;
         tot += s;
@@ -289,71 +386,160 @@ __device__ int block_exscan_1024(int v, int *lds /* >= 16 ints */, int &total) {
     return wbase + inc - v;
 }
 
-/* offsets + unique list from per-expert counts held one per thread */
-__device__ void counts_to_offsets(int e, int E, int cnt, int *lds_scan, int32_t *offsets,
-                                  int32_t *unique, int *lds_off) {
-    int total;
-    int off = block_exscan_1024(e < E ? cnt : 0, lds_scan, total);
-    int ntot;
-    int uoff = block_exscan_1024((e < E && cnt > 0) ? 1 : 0, lds_scan, ntot);
-    if (e < E) {
-        offsets[e] = off;
-        if (lds_off) lds_off[e] = off;
-        if (cnt > 0) unique[1 + uoff] = e;
+/* per-expert counts (cnt[j] for experts e = threadIdx.x + j*NT) -> offsets,
+ * unique, segtab; lds_off gets offsets when non-null */
+template <int NT>
+__device__ void counts_to_offsets(const int *cnt, int E, int *lds_scan, int32_t *offsets,
+                                  int32_t *unique, int32_t *segtab, int *lds_off) {
+    constexpr int PER = QK_MAX_EXPERTS / NT;
+    int csum = 0, asum = 0;
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int e = threadIdx.x * PER + j;
+        if (e < E) {
+            csum += cnt[j];
+            asum += cnt[j] > 0 ? 1 : 0;
+        }
     }
-    if (e == 0) {
+    int total, ntot;
+    int off = block_exscan<NT>(csum, lds_scan, total);
+    int uoff = block_exscan<NT>(asum, lds_scan, ntot);
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int e = threadIdx.x * PER + j;
+        if (e < E) {
+            offsets[e] = off;
+            if (lds_off) lds_off[e] = off;
+            if (cnt[j] > 0) {
+                unique[1 + uoff] = e;
+                segtab[1 + 3 * uoff] = e;
+                segtab[2 + 3 * uoff] = off;
+                segtab[3 + 3 * uoff] = cnt[j];
+                uoff++;
+            }
+            off += cnt[j];
+        }
+    }
+    if (threadIdx.x == 0) {
         offsets[E] = total;
         unique[0] = ntot;
+        segtab[0] = ntot;
+    }
+}
+
+/* dispatch of n <= QK_SMALL_N tokens whose expert ids are in LDS (s_idx),
+ * run by one NT-thread workgroup */
+template <int NT>
+__device__ void dispatch_block(const int32_t *s_idx, int n, int k, int E, int32_t *offsets,
+                               int32_t *perm, int32_t *pos, int32_t *unique, int32_t *segtab) {
+    __shared__ uint32_t s_bits[QK_MAX_EXPERTS * (QK_SMALL_N / 32)];
+    __shared__ int32_t s_wpre[QK_MAX_EXPERTS * (QK_SMALL_N / 32)];
+    __shared__ int32_t s_off[QK_MAX_EXPERTS];
+    __shared__ int s_scan[NT / 64];
+    constexpr int PER = QK_MAX_EXPERTS / NT;
+    const int tid = threadIdx.x;
+    const int NW = (n + 31) >> 5;
+    for (int i = tid; i < E * NW; i += NT) s_bits[i] = 0u;
+    __syncthreads();
+    for (int f = tid; f < n * k; f += NT) {
+        const int t = f / k, e = s_idx[f];
+        if (e >= 0 && e < E) atomicOr(&s_bits[e * NW + (t >> 5)], 1u << (t & 31));
+    }
+    __syncthreads();
+    int cnt[PER];
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int e = tid * PER + j;
+        cnt[j] = 0;
+        if (e < E)
+            for (int wd = 0; wd < NW; wd++) {
+                s_wpre[e * NW + wd] = cnt[j];
+                cnt[j] += __popc(s_bits[e * NW + wd]);
+            }
+    }
+    counts_to_offsets<NT>(cnt, E, s_scan, offsets, unique, segtab, s_off);
+    __syncthreads();
+    for (int f = tid; f < n * k; f += NT) {
+        const int t = f / k, e = s_idx[f], wd = t >> 5;
+        if (e < 0 || e >= E) {
+            if (pos) pos[f] = -1;
+            continue;
+        }
+        const int rank = s_wpre[e * NW + wd] + __popc(s_bits[e * NW + wd] & ((1u << (t & 31)) - 1u));
+        const int p = s_off[e] + rank;
+        perm[p] = f;
+        if (pos) pos[f] = p;
     }
 }
 
 struct SmallDispArgs {
     TopkArgs tk;
-    int32_t *offsets, *perm, *pos, *unique;
+    int32_t *offsets, *perm, *pos, *unique, *segtab;
 };
 
-/* n <= QK_SMALL_N, n*k <= QK_SMALL_NK, E <= 1024: top-k and the whole
- * dispatch in one 1024-thread workgroup */
+/* dispatch of a single token by one wavefront: its k distinct experts,
+ * sorted ascending, are the segments, one slot each */
+__device__ __forceinline__ void dispatch_one_token(const SmallDispArgs &d, int lane, int my_id) {
+    const int k = d.tk.k, E = d.tk.E;
+    int rank = 0;
+    for (int s2 = 0; s2 < k; s2++) {
+        const int o = __shfl(my_id, s2, QK_WAVE);
+        rank += o < my_id ? 1 : 0;
+    }
+    if (lane < k) {
+        d.perm[rank] = lane;
+        d.pos[lane] = rank;
+        d.unique[1 + rank] = my_id;
+        d.segtab[1 + 3 * rank] = my_id;
+        d.segtab[2 + 3 * rank] = rank;
+        d.segtab[3 + 3 * rank] = 1;
+    }
+    for (int e = lane; e <= E; e += 64) {
+        int c = 0;
+        for (int s2 = 0; s2 < k; s2++) c += __shfl(my_id, s2, QK_WAVE) < e ? 1 : 0;
+        d.offsets[e] = c;
+    }
+    if (lane == 0) {
+        d.unique[0] = k;
+        d.segtab[0] = k;
+    }
+}
+
+/* n <= QK_SMALL_N, n*k <= QK_SMALL_NK: top-k (one wave per token) and the
+ * whole dispatch in one 1024-thread workgroup */
 __global__ __launch_bounds__(1024) void k_topk_dispatch_small(SmallDispArgs a) {
     __shared__ int32_t s_idx[QK_SMALL_NK];
-    __shared__ uint32_t s_bits[QK_MAX_EXPERTS * (QK_SMALL_N / 32)];
-    __shared__ int32_t s_wpre[QK_MAX_EXPERTS * (QK_SMALL_N / 32)];
-    __shared__ int32_t s_off[QK_MAX_EXPERTS];
-    __shared__ int s_scan[16];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int E = a.tk.E, k = a.tk.k, n = a.tk.n;
-    const int NW = (n + 31) >> 5;
-    for (int i = tid; i < E * NW; i += 1024) s_bits[i] = 0u;
-    for (int t = wave; t < n; t += 16) topk_token(a.tk, t, lane, s_idx);
-    __syncthreads();
-    for (int f = tid; f < n * k; f += 1024) {
-        int t = f / k;
-        atomicOr(&s_bits[s_idx[f] * NW + (t >> 5)], 1u << (t & 31));
-    }
-    __syncthreads();
-    int cnt = 0;
-    if (tid < E)
-        for (int wd = 0; wd < NW; wd++) {
-            s_wpre[tid * NW + wd] = cnt;
-            cnt += __popc(s_bits[tid * NW + wd]);
+    __shared__ TopkLds s_tk[16];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (a.tk.n == 1) { /* one token: one wave does everything, no barriers */
+        if (wave == 0) {
+            const float *row0 = a.tk.logits;
+            int id;
+            float wt;
+            wave_topk(row0, a.tk.E, a.tk.k, lane, &s_tk[0], id, wt);
+            if (lane < a.tk.k) {
+                a.tk.idx[lane] = id;
+                a.tk.w[lane] = wt;
+            }
+            if (lane == 0) a.tk.sg[0] = qk_sigmoid(qk_ld(row0 + a.tk.E));
+            if (a.tk.logits_out)
+                for (int e = lane; e < a.tk.E; e += 64) a.tk.logits_out[e] = row0[e];
+            dispatch_one_token(a, lane, lane < a.tk.k ? id : 0x7FFFFFFF);
         }
-    counts_to_offsets(tid, E, cnt, s_scan, a.offsets, a.unique, s_off);
-    __syncthreads();
-    for (int f = tid; f < n * k; f += 1024) {
-        int t = f / k, e = s_idx[f], wd = t >> 5;
-        int rank = s_wpre[e * NW + wd] + __popc(s_bits[e * NW + wd] & ((1u << (t & 31)) - 1u));
-        int p = s_off[e] + rank;
-        a.perm[p] = f;
-        a.pos[f] = p;
+        return;
     }
+    for (int t = wave; t < a.tk.n; t += 16) topk_token(a.tk, t, lane, &s_tk[wave], s_idx);
+    __syncthreads();
+    dispatch_block<1024>(s_idx, a.tk.n, a.tk.k, a.tk.E, a.offsets, a.perm, a.pos, a.unique,
+                         a.segtab);
 }
 
 extern "C" int qk_launch_topk_dispatch_small(qk_shape s, int n, const float *logits,
                                              float *logits_out, int32_t *idx, float *w, float *sg,
                                              int32_t *offsets, int32_t *perm, int32_t *pos,
-                                             int32_t *unique, void *stream) {
+                                             int32_t *unique, int32_t *segtab, void *stream) {
     if (n <= 0) return 0;
-    SmallDispArgs a{{logits, logits_out, idx, w, sg, s.E, s.k, n}, offsets, perm, pos, unique};
+    SmallDispArgs a{{logits, logits_out, idx, w, sg, s.E, s.k, n}, offsets, perm, pos, unique, segtab};
     hipLaunchKernelGGL(k_topk_dispatch_small, dim3(1), dim3(1024), 0, (hipStream_t)stream, a);
     return QK_CHECK_LAUNCH();
 }
@@ -377,7 +563,7 @@ __global__ void k_setbits(const int32_t *idx, int n, int k, int E, int NW, uint3
 /* one workgroup: per-expert word prefixes (wave per expert) + offsets */
 __global__ __launch_bounds__(1024) void k_count_offsets(const uint32_t *bits, int32_t *wprefix,
                                                         int E, int NW, int32_t *offsets,
-                                                        int32_t *unique) {
+                                                        int32_t *unique, int32_t *segtab) {
     __shared__ int s_cnt[QK_MAX_EXPERTS];
     __shared__ int s_scan[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -398,7 +584,8 @@ __global__ __launch_bounds__(1024) void k_count_offsets(const uint32_t *bits, in
         if (lane == 0) s_cnt[e] = base;
     }
     __syncthreads();
-    counts_to_offsets(tid, E, tid < E ? s_cnt[tid] : 0, s_scan, offsets, unique, nullptr);
+    int cnt[1] = {tid < E ? s_cnt[tid] : 0};
+    counts_to_offsets<1024>(cnt, E, s_scan, offsets, unique, segtab, nullptr);
 }
 
 __global__ void k_scatter(const int32_t *idx, int n, int k, int E, int NW, const uint32_t *bits,
@@ -418,8 +605,8 @@ __global__ void k_scatter(const int32_t *idx, int n, int k, int E, int NW, const
 }
 
 extern "C" int qk_launch_dispatch(qk_shape s, int n, const int32_t *idx, int32_t *offsets,
-                                  int32_t *perm, int32_t *pos, int32_t *unique, uint32_t *bits,
-                                  int32_t *wprefix, void *stream) {
+                                  int32_t *perm, int32_t *pos, int32_t *unique, int32_t *segtab,
+                                  uint32_t *bits, int32_t *wprefix, void *stream) {
     hipStream_t st = (hipStream_t)stream;
     if (n <= 0) return 0;
     const int NW = (n + 31) / 32;
@@ -429,7 +616,7 @@ extern "C" int qk_launch_dispatch(qk_shape s, int n, const int32_t *idx, int32_t
     hipLaunchKernelGGL(k_setbits, dim3((nk + 255) / 256), dim3(256), 0, st, idx, n, s.k, s.E, NW,
                        bits);
     hipLaunchKernelGGL(k_count_offsets, dim3(1), dim3(1024), 0, st, (const uint32_t *)bits, wprefix,
-                       s.E, NW, offsets, unique);
+                       s.E, NW, offsets, unique, segtab);
     hipLaunchKernelGGL(k_scatter, dim3((nk + 255) / 256), dim3(256), 0, st, idx, n, s.k, s.E, NW,
                        (const uint32_t *)bits, (const int32_t *)wprefix, (const int32_t *)offsets,
                        perm, pos);

@@ -69,9 +69,9 @@ SIGNATURES = {
                              ctypes.POINTER(QmoeErr)]),
     "qmoe_router": (_I, [_P, _I, _P, _I, _I, _P, _P, _P, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_dispatch": (_I, [_P, _P, _I, _P, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
-    "qmoe_expert_gateup": (_I, [_P, _I, _P, _I, _I, _P, _P, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
-    "qmoe_expert_down": (_I, [_P, _I, _P, _I, _P, _P, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
-    "qmoe_expert_ffn": (_I, [_P, _I, _P, _I, _I, _P, _P, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_expert_gateup": (_I, [_P, _I, _P, _I, _I, _P, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_expert_down": (_I, [_P, _I, _P, _I, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_expert_ffn": (_I, [_P, _I, _P, _I, _I, _P, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_combine": (_I, [_P, _P, _P, _P, _P, _I, _P, _I, _P, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_layer_forward": (_I, [_P, _I, _P, _I, _I, _P, _I, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_moe_forward_host": (_I, [_P, _I, _P, _I, _P, ctypes.POINTER(QmoeErr)]),
@@ -287,11 +287,12 @@ class MoeContext:
         dev = idx.device
         offsets = torch.empty((self.E + 1,), dtype=torch.int32, device=dev)
         perm = torch.empty((max(1, n * self.k),), dtype=torch.int32, device=dev)
-        unique = torch.empty((self.E + 1,), dtype=torch.int32, device=dev)
+        segments = torch.empty((3 * self.E + 1,), dtype=torch.int32, device=dev)
         err = QmoeErr()
-        _check(lib().qmoe_dispatch(self._h, _ptr(idx), n, _ptr(offsets), _ptr(perm), _ptr(unique),
-                                   _stream(stream), ctypes.byref(err)), err, "qmoe_dispatch")
-        return dict(offsets=offsets, perm=perm[: n * self.k], unique=unique)
+        _check(lib().qmoe_dispatch(self._h, _ptr(idx), n, _ptr(offsets), _ptr(perm),
+                                   _ptr(segments), _stream(stream), ctypes.byref(err)), err,
+               "qmoe_dispatch")
+        return dict(offsets=offsets, perm=perm[: n * self.k], segments=segments)
 
     def expert_gateup(self, layer, x, d, stream=None):
         import torch
@@ -299,18 +300,16 @@ class MoeContext:
         h = torch.empty((n * self.k + n, self.I), dtype=torch.float32, device=x.device)
         err = QmoeErr()
         _check(lib().qmoe_expert_gateup(self._h, layer, _ptr(x), _dtype_code(x), n, _ptr(d["perm"]),
-                                        _ptr(d["offsets"]), _ptr(d["unique"]), _ptr(h),
-                                        _stream(stream), ctypes.byref(err)), err,
-               "qmoe_expert_gateup")
+                                        _ptr(d["segments"]), _ptr(h), _stream(stream),
+                                        ctypes.byref(err)), err, "qmoe_expert_gateup")
         return h
 
     def expert_down(self, layer, h, n, d, stream=None):
         import torch
         y = torch.empty((n * self.k + n, self.H), dtype=torch.float32, device=h.device)
         err = QmoeErr()
-        _check(lib().qmoe_expert_down(self._h, layer, _ptr(h), n, _ptr(d["perm"]), _ptr(d["offsets"]),
-                                      _ptr(d["unique"]), _ptr(y), _stream(stream), ctypes.byref(err)),
-               err, "qmoe_expert_down")
+        _check(lib().qmoe_expert_down(self._h, layer, _ptr(h), n, _ptr(d["segments"]), _ptr(y),
+                                      _stream(stream), ctypes.byref(err)), err, "qmoe_expert_down")
         return y
 
     def expert_ffn(self, layer, x, d, stream=None):
@@ -319,8 +318,8 @@ class MoeContext:
         y = torch.empty((n * self.k + n, self.H), dtype=torch.float32, device=x.device)
         err = QmoeErr()
         _check(lib().qmoe_expert_ffn(self._h, layer, _ptr(x), _dtype_code(x), n, _ptr(d["perm"]),
-                                     _ptr(d["offsets"]), _ptr(d["unique"]), _ptr(y),
-                                     _stream(stream), ctypes.byref(err)), err, "qmoe_expert_ffn")
+                                     _ptr(d["segments"]), _ptr(y), _stream(stream),
+                                     ctypes.byref(err)), err, "qmoe_expert_ffn")
         return y
 
     def combine(self, y, perm, w, shared_gate, n, x_residual=None, stream=None):
@@ -360,11 +359,11 @@ class MoeContext:
                  shared_gate=torch.empty((n,), dtype=torch.float32, device=dev),
                  offsets=torch.empty((self.E + 1,), dtype=torch.int32, device=dev),
                  perm=torch.empty((n * self.k,), dtype=torch.int32, device=dev),
-                 unique=torch.empty((self.E + 1,), dtype=torch.int32, device=dev))
+                 segments=torch.empty((3 * self.E + 1,), dtype=torch.int32, device=dev))
         err = QmoeErr()
         _check(lib().qmoe_last_routing(self._h, n, _ptr(r["idx"]), _ptr(r["w"]),
                                        _ptr(r["shared_gate"]), _ptr(r["offsets"]), _ptr(r["perm"]),
-                                       _ptr(r["unique"]), _stream(stream), ctypes.byref(err)),
+                                       _ptr(r["segments"]), _stream(stream), ctypes.byref(err)),
                err, "qmoe_last_routing")
         return r
 

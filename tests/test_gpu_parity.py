@@ -35,6 +35,16 @@ def assert_out_close(got, ref, what):
     assert err < MAX_ABS and rel < REL_L2, (what, err, rel)
 
 
+def check_segments(seg, ref):
+    """segment table = (U, then expert, first dispatch position, count)"""
+    U = int(seg[0])
+    assert U == len(ref["unique"])
+    tab = seg[1:1 + 3 * U].reshape(U, 3)
+    np.testing.assert_array_equal(tab[:, 0], ref["unique"])
+    np.testing.assert_array_equal(tab[:, 1], ref["offsets"][ref["unique"]])
+    np.testing.assert_array_equal(tab[:, 2], np.diff(ref["offsets"])[ref["unique"]])
+
+
 def to_dev(a, torch, dev):
     if a.dtype == np.uint16:  # bf16 bit patterns
         return torch.from_numpy(a.view(np.int16)).to(dev).view(torch.bfloat16)
@@ -155,9 +165,7 @@ def test_dispatch_bitexact(torch_dev, n, k, E):
         torch.cuda.synchronize()
         np.testing.assert_array_equal(d["offsets"].cpu().numpy(), ref["offsets"])
         np.testing.assert_array_equal(d["perm"].cpu().numpy(), ref["perm"])
-        u = d["unique"].cpu().numpy()
-        assert u[0] == len(ref["unique"])
-        np.testing.assert_array_equal(u[1:1 + u[0]], ref["unique"])
+        check_segments(d["segments"].cpu().numpy(), ref)
 
 
 # ------------------------------------------------------------ full shapes
@@ -191,8 +199,8 @@ def _layer_case(torch, dev, wname, n=None, n_check=16, seed_x=None):
         dref = orc.dispatch(route["idx"], w.n_experts)
         np.testing.assert_array_equal(lr["offsets"].cpu().numpy(), dref["offsets"])
         np.testing.assert_array_equal(lr["perm"].cpu().numpy(), dref["perm"])
-        u = lr["unique"].cpu().numpy()
-        np.testing.assert_array_equal(u[1:1 + u[0]], dref["unique"])
+        check_segments(lr["segments"].cpu().numpy(), dref)
+        u = lr["segments"].cpu().numpy()
         say(f"{wname}: n={n} distinct experts U={u[0]}, max segment "
             f"{np.diff(dref['offsets']).max()}")
         assert_out_close(out.cpu().numpy()[sel], ref["out"], f"{wname} layer")
