@@ -26,6 +26,9 @@ PKG_DIR = os.path.join(ROOT, "qwen3.8-flash-next_amd")
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA
+# symbol of the gate/up GEMV instance that hidden 2048 selects (64 lanes
+# per weight row, one chunk per lane), by activation type
+GATEUP_SYMBOL = {True: "k_q4gemv<2, 64, 1, true>", False: "k_q4gemv<2, 64, 1, false>"}
 METRIC = "MoE-layer tokens/sec at decode+prefill, 1 MI355X; % HBM BW / % MFMA peak"
 
 
@@ -215,6 +218,38 @@ def cpu_baseline(w, budget_s=12.0):
                        f"{threads} OpenMP threads (value_1thread: 1 thread)")
 
 
+def copy_calibration(torch, mib):
+    """a plain device copy of known size, run under rocprofv3 --pmc to
+    calibrate FETCH_SIZE / WRITE_SIZE (bytes moved per dispatch are known)"""
+    n = mib * 1024 * 1024 // 4
+    a = torch.randn(n, device="cuda")
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(8):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "copies": 8}),
+          flush=True)
+
+
+def measured_traffic(kernel_symbol, workload):
+    """HBM traffic per launch of the roofline kernel, as measured by the two
+    rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) recorded in
+    profiles/traffic.json, scaled by the copy-kernel calibration factors
+    stored beside them; None when no measurement of this kernel/workload is
+    recorded"""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    for r in rec.get("kernels", []):
+        if r.get("kernel") == kernel_symbol and r.get("workload") == workload:
+            return int(r["traffic_bytes_per_launch"])
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -226,6 +261,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--extra", default="batched,prefill",
                     help="comma list of other workloads to time (secondary results)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 8 plain copies of MIB MiB (counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -233,6 +270,9 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.copy_calibration > 0:
+        copy_calibration(torch, args.copy_calibration)
+        return
     pkg = load_pkg()
     dev = torch.cuda.get_device_name(0)
     log(f"device {dev}, library {pkg.version()}")
@@ -293,13 +333,13 @@ def main():
             "extra": extra,
         },
         "roofline": {
-            "kernel": "k_q4gemv<2,...> (grouped gate/up GEMV + SiLU*up)",
+            "kernel": GATEUP_SYMBOL[w.x_bf16] + " (grouped gate/up GEMV + SiLU*up)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(GATEUP_SYMBOL[w.x_bf16], w.name),
             "avg_launch_us": round(k_sec * 1e6, 3),
             "algorithmic_bytes_per_launch": int(k_bytes),
         },
