@@ -33,10 +33,11 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
             p = 0x7FFFFFFE;
             wt = 0.0f;
         }
+        /* rank by (position, slot): invalid slots share one position */
         int rank = 0;
         for (int s2 = 0; s2 < a.k; s2++) {
-            int q = __shfl(p, s2, QK_WAVE);
-            rank += q < p ? 1 : 0;
+            const int q = __shfl(p, s2, QK_WAVE);
+            rank += (q < p || (q == p && s2 < s)) ? 1 : 0;
         }
         if (s < a.k) {
             s_pos[rank] = p;

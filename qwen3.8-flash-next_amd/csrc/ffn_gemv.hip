@@ -21,6 +21,7 @@
  * are split into hi+lo bf16 pairs (16 significant bits).
  */
 #include "qk_device.h"
+#include "gemv_decode.h"
 
 struct GemvArgs {
     const uint32_t *q[2];   /* routed [E, N, K/8] */
@@ -89,12 +90,8 @@ __device__ __forceinline__ void convert_xraw(const XRaw<P, XBF16> &xr, int K, in
                 uint4 d = xr.d[XBF16 ? ps : 0][w];
                 if (!ok) d = make_uint4(0u, 0u, 0u, 0u);
                 qk_bf16x8_to_pairs(d, &xp.hi[ps][4 * w]);
-                float s = 0.0f;
-                s += qk_bf16_lo(d.x) + qk_bf16_hi(d.x);
-                s += qk_bf16_lo(d.y) + qk_bf16_hi(d.y);
-                s += qk_bf16_lo(d.z) + qk_bf16_hi(d.z);
-                s += qk_bf16_lo(d.w) + qk_bf16_hi(d.w);
-                xp.xs[ps] += s;
+#pragma unroll
+                for (int i = 0; i < 4; i++) xp.xs[ps] = qk_dot2(xp.hi[ps][4 * w + i], QK_BF16_ONES, xp.xs[ps]);
             }
         } else {
 #pragma unroll
@@ -129,6 +126,22 @@ __device__ __forceinline__ float chunk_dot(uint4 q4, const XPairs<LPR, P, XBF16>
     return d;
 }
 
+/* this lane's share of one output row: sum over its chunks of the group
+ * update s*(D - 128*xs) + b*xs (a group is two chunks; the lanes of a row
+ * are summed by qk_group_sum afterwards) */
+template <int LPR, int P, bool XBF16>
+__device__ __forceinline__ float row_part(const uint4 (&wq)[P], const float (&ws)[P],
+                                          const float (&wb)[P], const XPairs<LPR, P, XBF16> &xp) {
+    float part = 0.0f;
+#pragma unroll
+    for (int ps = 0; ps < P; ps++) {
+        const float d = chunk_dot<LPR, P, XBF16>(wq[ps], xp, ps);
+        const float dq = fmaf(-128.0f, xp.xs[ps], d);
+        part = fmaf(ws[ps], dq, fmaf(wb[ps], xp.xs[ps], part));
+    }
+    return part;
+}
+
 template <int NMAT, int LPR, int P, bool XBF16>
 __global__ __launch_bounds__(256) void k_q4gemv(GemvArgs a) {
     constexpr int RPW = 64 / LPR;
@@ -139,18 +152,21 @@ __global__ __launch_bounds__(256) void k_q4gemv(GemvArgs a) {
     const int CH = a.K >> 5, G = a.K >> 6;
     const size_t wrow = (size_t)a.K >> 3; /* u32 words per weight row */
     const int tps = (a.N + RB - 1) / RB;
-    const int U = min(max(a.segtab[0], 0), a.E); /* first used by routed tasks */
+    const int u_raw = a.segtab[0];
     for (int task = blockIdx.x;; task += gridDim.x) {
         const int seg = task / tps, rb = task - seg * tps;
         const bool shared = seg == 0;
-        if (!shared && seg > U) break;
+        if (seg > a.E) break;
         int p0, m;
         const uint32_t *q[NMAT];
         const uint16_t *sc[NMAT], *bi[NMAT];
         if (!shared) {
+            /* the entry is read before the segment count is known (the table
+             * has room for E entries), so both loads are in flight at once */
             const int e = a.segtab[3 * seg - 2];
             p0 = a.segtab[3 * seg - 1];
             m = a.segtab[3 * seg];
+            if (seg > min(max(u_raw, 0), a.E)) break;
             if (e < 0 || e >= a.E || p0 < 0 || m < 0 || p0 + m > a.n * a.k) continue;
 #pragma unroll
             for (int mt = 0; mt < NMAT; mt++) {
@@ -237,16 +253,9 @@ __global__ __launch_bounds__(256) void k_q4gemv(GemvArgs a) {
             for (int it = 0; it < GV_RITER; it++) {
                 float acc[NMAT];
 #pragma unroll
-                for (int mt = 0; mt < NMAT; mt++) {
-                    float part = 0.0f;
-#pragma unroll
-                    for (int ps = 0; ps < P; ps++) {
-                        const float d = chunk_dot<LPR, P, XBF16>(wq[mt][it][ps], xp, ps);
-                        const float dq = fmaf(-128.0f, xp.xs[ps], d);
-                        part = fmaf(ws[mt][it][ps], dq, fmaf(wb[mt][it][ps], xp.xs[ps], part));
-                    }
-                    acc[mt] = qk_group_sum<LPR>(part);
-                }
+                for (int mt = 0; mt < NMAT; mt++)
+                    acc[mt] = qk_group_sum<LPR>(
+                        row_part<LPR, P, XBF16>(wq[mt][it], ws[mt][it], wb[mt][it], xp));
                 const int r = rbase + it * RPW + rsub;
                 if (sub == 0 && r < a.N) {
                     float v = NMAT == 2 ? qk_silu(acc[0]) * acc[NMAT - 1] : acc[0];
@@ -257,11 +266,253 @@ __global__ __launch_bounds__(256) void k_q4gemv(GemvArgs a) {
     }
 }
 
+/*
+ * Down projection fused with the combine, for a few tokens (decode).  A
+ * workgroup owns RB = 2*(64/LPR) output rows of every token and computes
+ * y for those rows for every segment (the waves take segments in turn),
+ * keeping y in LDS; then each (token, row) is combined exactly as
+ * k_combine does: out = 0, out = fma(w, y, out) over the token's slots in
+ * ascending dispatch position (ascending expert id), out = fma(g, y_shared,
+ * out), then the optional residual x + out.  The y values are computed with
+ * the lane mapping and arithmetic of k_q4gemv<1, LPR, P, false>, so the
+ * result is bit-identical to qk_launch_down followed by qk_launch_combine.
+ */
+struct DcArgs {
+    const uint32_t *q, *sq;       /* routed [E, N, K/8], shared [N, K/8] */
+    const uint16_t *s, *b, *ss, *sb;
+    const float *h;               /* [n*k+n, K], rows in dispatch order */
+    const int32_t *segtab, *pos;  /* pos [n*k]: dispatch position of slot t*k+s */
+    const float *w, *sg;          /* [n, k], [n] */
+    const void *xres;             /* [n, N] or null */
+    float *out;                   /* [n, N] */
+    int K, N, n, k, E, xbf16;
+};
+
+#define DC_WAVES 16
+
+template <int LPR, int P>
+__global__ __launch_bounds__(64 * DC_WAVES) void k_down_combine(DcArgs a,
+                                                                const int32_t *__restrict__ segtab) {
+    constexpr int RPW = 64 / LPR;
+    constexpr int RB = RPW * GV_RITER;
+    extern __shared__ float dc_lds[];
+    const int nk = a.n * a.k;
+    float *s_y = dc_lds;                              /* [(nk + n) * RB] */
+    float *s_w = s_y + (nk + a.n) * RB;               /* [nk] slot weights, position order */
+    int *s_p = (int *)(s_w + nk);                     /* [nk] slot positions, ascending */
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane % LPR, rsub = lane / LPR;
+    const int CH = a.K >> 5, G = a.K >> 6;
+    const size_t wrow = (size_t)a.K >> 3;
+    const int r0 = blockIdx.x * RB;
+    const int u_raw = segtab[0];
+
+    /* each token's slots ranked by dispatch position (invalid last) */
+    for (int t = wave; t < a.n; t += DC_WAVES) {
+        int p = 0x7FFFFFFF;
+        float wt = 0.0f;
+        if (lane < a.k) {
+            p = a.pos[(size_t)t * a.k + lane];
+            wt = a.w[(size_t)t * a.k + lane];
+            if (p < 0 || p >= nk) {
+                p = 0x7FFFFFFE;
+                wt = 0.0f;
+            }
+        }
+        /* rank by (position, slot): invalid slots share one position */
+        int rank = 0;
+        for (int s2 = 0; s2 < a.k; s2++) {
+            const int q = __builtin_amdgcn_readlane(p, s2);
+            rank += (q < p || (q == p && s2 < lane)) ? 1 : 0;
+        }
+        if (lane < a.k) {
+            s_p[t * a.k + rank] = p;
+            s_w[t * a.k + rank] = wt;
+        }
+    }
+
+    /* y for this workgroup's rows, one segment per wave at a time */
+    for (int seg = wave; seg <= a.E; seg += DC_WAVES) {
+        const bool shared = seg == 0;
+        int p0, m;
+        const uint32_t *q;
+        const uint16_t *sc, *bi;
+        if (!shared) {
+            /* entry and count are read together (the table has room for E) */
+            const int e = segtab[3 * seg - 2];
+            p0 = segtab[3 * seg - 1];
+            m = segtab[3 * seg];
+            if (seg > min(max(u_raw, 0), a.E)) break;
+            if (e < 0 || e >= a.E || p0 < 0 || m < 0 || p0 + m > nk) continue;
+            q = a.q + (size_t)e * a.N * wrow;
+            sc = a.s + (size_t)e * a.N * G;
+            bi = a.b + (size_t)e * a.N * G;
+        } else {
+            p0 = nk;
+            m = a.n;
+            q = a.sq;
+            sc = a.ss;
+            bi = a.sb;
+        }
+        XRaw<P, false> xr;
+        if (m > 0) load_xraw<LPR, P, false>(a.h, (size_t)p0, a.K, sub, xr);
+        uint4 wq[GV_RITER][P];
+        uint16_t rs[GV_RITER][P], rbi[GV_RITER][P];
+        float ws[GV_RITER][P], wb[GV_RITER][P];
+#pragma unroll
+        for (int it = 0; it < GV_RITER; it++) {
+            const int rr = r0 + it * RPW + rsub;
+            const int r = rr < a.N ? rr : 0;
+#pragma unroll
+            for (int ps = 0; ps < P; ps++) {
+                const int c0 = ps * LPR + sub;
+                const int c = c0 < CH ? c0 : 0;
+                wq[it][ps] = qk_ld((const uint4 *)(q + (size_t)r * wrow) + c);
+                rs[it][ps] = qk_ld(sc + (size_t)r * G + (c >> 1));
+                rbi[it][ps] = qk_ld(bi + (size_t)r * G + (c >> 1));
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int it = 0; it < GV_RITER; it++) {
+            const bool rok = r0 + it * RPW + rsub < a.N;
+#pragma unroll
+            for (int ps = 0; ps < P; ps++) {
+                const bool ok = rok && ps * LPR + sub < CH;
+                ws[it][ps] = ok ? qk_bf16(rs[it][ps]) : 0.0f;
+                wb[it][ps] = ok ? qk_bf16(rbi[it][ps]) : 0.0f;
+                if (!ok) wq[it][ps] = make_uint4(0u, 0u, 0u, 0u);
+            }
+        }
+        for (int j = 0; j < m; j++) {
+            const int p = p0 + j;
+            XPairs<LPR, P, false> xp;
+            convert_xraw<LPR, P, false>(xr, a.K, sub, xp);
+            if (j + 1 < m) load_xraw<LPR, P, false>(a.h, (size_t)(p + 1), a.K, sub, xr);
+#pragma unroll
+            for (int it = 0; it < GV_RITER; it++) {
+                const float v = qk_group_sum<LPR>(row_part<LPR, P, false>(wq[it], ws[it], wb[it], xp));
+                if (sub == 0) s_y[p * RB + it * RPW + rsub] = v;
+            }
+        }
+    }
+    __syncthreads();
+
+    /* combine */
+    for (int i = threadIdx.x; i < a.n * RB; i += 64 * DC_WAVES) {
+        const int t = i / RB, rl = i - t * RB, r = r0 + rl;
+        if (r >= a.N) continue;
+        float acc = 0.0f;
+        for (int s2 = 0; s2 < a.k; s2++) {
+            const int p = s_p[t * a.k + s2];
+            if (p < nk) acc = fmaf(s_w[t * a.k + s2], s_y[p * RB + rl], acc);
+        }
+        acc = fmaf(qk_ld(a.sg + t), s_y[(nk + t) * RB + rl], acc);
+        if (a.xres) {
+            const float xv = a.xbf16 ? qk_bf16(((const uint16_t *)a.xres)[(size_t)t * a.N + r])
+                                     : ((const float *)a.xres)[(size_t)t * a.N + r];
+            acc = xv + acc;
+        }
+        a.out[(size_t)t * a.N + r] = acc;
+    }
+}
+
+static int pick_lpr(int K);
+
+/* LDS bytes of k_down_combine for n tokens, or 0 when the fused path does
+ * not apply (too many tokens for one workgroup's LDS) */
+extern "C" size_t qk_down_combine_lds(qk_shape s, int n) {
+    if (n <= 0 || n > QK_DC_MAX_N) return 0;
+    const int rb = (64 / pick_lpr(s.I)) * GV_RITER;
+    const size_t nk = (size_t)n * s.k;
+    const size_t bytes = ((nk + n) * rb + 2 * nk) * 4;
+    return bytes <= QK_DC_MAX_LDS ? bytes : 0;
+}
+
+extern "C" int qk_launch_down_combine(const qmoe_layer_weights *W, qk_shape s, const float *h,
+                                      int n, const int32_t *segtab, const int32_t *pos,
+                                      const float *w, const float *sg, const void *x_res,
+                                      int x_bf16, float *out, void *stream) {
+    const size_t lds = qk_down_combine_lds(s, n);
+    if (lds == 0) return (int)hipErrorInvalidValue;
+    DcArgs a;
+    a.q = W->down_q; a.s = W->down_s; a.b = W->down_b;
+    a.sq = W->sh_down_q; a.ss = W->sh_down_s; a.sb = W->sh_down_b;
+    a.h = h;
+    a.segtab = segtab;
+    a.pos = pos;
+    a.w = w;
+    a.sg = sg;
+    a.xres = x_res;
+    a.xbf16 = x_bf16;
+    a.out = out;
+    a.K = s.I;
+    a.N = s.H;
+    a.n = n;
+    a.k = s.k;
+    a.E = s.E;
+    const int lpr = pick_lpr(s.I);
+    const int ch = s.I / 32;
+    const int P = (ch + lpr - 1) / lpr;
+    const int rb = (64 / lpr) * GV_RITER;
+    const dim3 grid((s.H + rb - 1) / rb);
+    hipStream_t st = (hipStream_t)stream;
+#define DC_LAUNCH(L, PP) \
+    hipLaunchKernelGGL((k_down_combine<L, PP>), grid, dim3(64 * DC_WAVES), lds, st, a, a.segtab)
+    if (lpr == 64) {
+        if (P == 1) DC_LAUNCH(64, 1);
+        else if (P == 2) DC_LAUNCH(64, 2);
+        else if (P <= 4) DC_LAUNCH(64, 4);
+        else return (int)hipErrorInvalidValue;
+    } else if (lpr == 32) DC_LAUNCH(32, 1);
+    else if (lpr == 16) DC_LAUNCH(16, 1);
+    else if (lpr == 8) DC_LAUNCH(8, 1);
+    else if (lpr == 4) DC_LAUNCH(4, 1);
+    else DC_LAUNCH(2, 1);
+#undef DC_LAUNCH
+    return QK_CHECK_LAUNCH();
+}
+
 static int pick_lpr(int K) {
     int ch = K / 32;
     int l = 2;
     while (l < ch && l < 64) l <<= 1;
     return l;
+}
+
+/* one token: the straight-line decode kernel when K/32 is a power of two
+ * (<= 256 chunks); returns -1 when it does not apply */
+template <bool XBF16>
+static int launch_gateup_dec(const GemvArgs &g, hipStream_t st) {
+    const int ch = g.K / 32;
+    if (ch < 2 || ch > 256 || (ch & (ch - 1)) != 0) return -1;
+    DecArgs a;
+    for (int mt = 0; mt < 2; mt++) {
+        a.q[mt] = g.q[mt]; a.s[mt] = g.s[mt]; a.b[mt] = g.b[mt];
+        a.sq[mt] = g.sq[mt]; a.ss[mt] = g.ss[mt]; a.sb[mt] = g.sb[mt];
+    }
+    a.x = g.x;
+    a.out = g.out;
+    a.K = g.K;
+    a.N = g.N;
+    a.k = g.k;
+    a.E = g.E;
+    const int lpr = ch < 64 ? ch : 64, cpl = ch / lpr;
+    const int rb = 4 * (64 / lpr) * 2;
+    const dim3 grid((g.k + 1) * ((g.N + rb - 1) / rb));
+#define GD_LAUNCH(L, C) \
+    hipLaunchKernelGGL((k_gateup_dec<L, C, 2, XBF16>), grid, dim3(256), 0, st, a, g.segtab)
+    if (lpr == 64) {
+        if (cpl == 1) GD_LAUNCH(64, 1);
+        else if (cpl == 2) GD_LAUNCH(64, 2);
+        else GD_LAUNCH(64, 4);
+    } else if (lpr == 32) GD_LAUNCH(32, 1);
+    else if (lpr == 16) GD_LAUNCH(16, 1);
+    else if (lpr == 8) GD_LAUNCH(8, 1);
+    else if (lpr == 4) GD_LAUNCH(4, 1);
+    else GD_LAUNCH(2, 1);
+#undef GD_LAUNCH
+    return QK_CHECK_LAUNCH();
 }
 
 template <int NMAT, bool XBF16>
@@ -313,6 +564,10 @@ extern "C" int qk_launch_gateup(const qmoe_layer_weights *W, qk_shape s, const v
     a.in_by_pos = 0;
     const int max_seg = n * s.k < s.E ? n * s.k : s.E;
     hipStream_t st = (hipStream_t)stream;
+    if (n == 1) {
+        const int rc = x_bf16 ? launch_gateup_dec<true>(a, st) : launch_gateup_dec<false>(a, st);
+        if (rc >= 0) return rc;
+    }
     return x_bf16 ? launch_gemv<2, true>(a, max_seg, st) : launch_gemv<2, false>(a, max_seg, st);
 }
 

@@ -1,0 +1,179 @@
+/*
+ * gemv_decode.h -- grouped gate/up GEMV for one token (decode), gfx950.
+ *
+ * One workgroup per (segment, block of RB rows), no task loop: with one
+ * token every segment has one row and there are at most k routed segments,
+ * so the grid is (k+1) x blocks.  Segment 0 is the shared expert (output
+ * row k); segment j >= 1 is entry j-1 of the segment table.
+ *
+ * Lane mapping: LPR lanes share a weight row and lane `sub` owns the CPL
+ * consecutive 32-code chunks sub*CPL .. sub*CPL+CPL-1 (K = 32*LPR*CPL), so
+ * its scales and biases are CPL/2 consecutive bf16 values and its
+ * activations one contiguous run.  Per chunk the lane accumulates
+ * D = sum x*(128+q) with v_dot2c_f32_bf16 on (code i, code i+4) pairs and
+ * applies the gemm_q4 group identity (kernel.c:279-282) as
+ *     acc = s*D + (b - 128*s)*xs,        xs = sum x over the chunk,
+ * then the row is summed over its LPR lanes.  All loads are issued before
+ * any test on the segment entry; an invalid entry reads expert 0 and
+ * stores nothing.
+ */
+#ifndef GEMV_DECODE_H
+#define GEMV_DECODE_H
+
+#include "qk_device.h"
+
+struct DecArgs {
+    const uint32_t *q[2];  /* routed gate, up [E, N, K/8] */
+    const uint16_t *s[2];  /* [E, N, K/64] */
+    const uint16_t *b[2];
+    const uint32_t *sq[2]; /* shared gate, up [N, K/8] */
+    const uint16_t *ss[2];
+    const uint16_t *sb[2];
+    const void *x;         /* [1, K] bf16 or f32 */
+    float *out;            /* [k+1, N]: h = silu(g) * u, rows in dispatch order */
+    int K, N, k, E;
+};
+
+/* GPL consecutive bf16 values starting at p (GPL = 1, 2 or 4) */
+template <int GPL>
+__device__ __forceinline__ void dec_ld_bf16(const uint16_t *p, float v[GPL]) {
+    if (GPL == 1) {
+        v[0] = qk_bf16(qk_ld(p));
+    } else if (GPL == 2) {
+        const uint32_t w = qk_ld((const uint32_t *)p);
+        v[0] = qk_bf16_lo(w);
+        v[GPL > 1 ? 1 : 0] = qk_bf16_hi(w);
+    } else {
+        const uint2 w = qk_ld((const uint2 *)p);
+        v[0] = qk_bf16_lo(w.x);
+        v[GPL > 1 ? 1 : 0] = qk_bf16_hi(w.x);
+        v[GPL > 2 ? 2 : 0] = qk_bf16_lo(w.y);
+        v[GPL > 3 ? 3 : 0] = qk_bf16_hi(w.y);
+    }
+}
+
+template <int LPR, int CPL, int RIT, bool XBF16>
+__global__ __launch_bounds__(256) void k_gateup_dec(DecArgs a, const int32_t *__restrict__ segtab) {
+    constexpr int RPW = 64 / LPR;
+    constexpr int RB = 4 * RPW * RIT;
+    constexpr int GPL = CPL >= 2 ? CPL / 2 : 1; /* scale groups per lane */
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane % LPR, rsub = lane / LPR;
+    const int G = a.K >> 6;
+    const size_t wrow = (size_t)a.K >> 3;
+    const int tps = (a.N + RB - 1) / RB;
+    const int seg = blockIdx.x / tps, rb = blockIdx.x - seg * tps;
+    const int c0 = sub * CPL;     /* first chunk of this lane */
+    const int g0 = (c0 >> 1);     /* first scale group of this lane */
+
+    /* activations: no routing dependence, issued first */
+    uint4 xd[XBF16 ? CPL : 1][4];
+    float4 xf[XBF16 ? 1 : CPL][8];
+#pragma unroll
+    for (int c = 0; c < CPL; c++) {
+        if (XBF16) {
+            const uint4 *src = (const uint4 *)((const uint16_t *)a.x) + 4 * (c0 + c);
+#pragma unroll
+            for (int w = 0; w < 4; w++) xd[XBF16 ? c : 0][w] = qk_ld(src + w);
+        } else {
+            const float4 *src = (const float4 *)((const float *)a.x) + 8 * (c0 + c);
+#pragma unroll
+            for (int w = 0; w < 8; w++) xf[XBF16 ? 0 : c][w] = qk_ld(src + w);
+        }
+    }
+
+    /* segment entry and count, read together; bitwise tests (no branches) */
+    const bool shared = seg == 0;
+    const int s1 = shared ? 1 : seg;
+    const int u = segtab[0];
+    const int e_raw = segtab[3 * s1 - 2], p_raw = segtab[3 * s1 - 1], m_raw = segtab[3 * s1];
+    const bool valid = shared | ((seg <= u) & (e_raw >= 0) & (e_raw < a.E) & (p_raw >= 0) &
+                                 (p_raw < a.k) & (m_raw == 1));
+    const int e = (valid && !shared) ? e_raw : 0;
+    const int p0 = shared ? a.k : p_raw;
+    const uint32_t *q[2];
+    const uint16_t *sc[2], *bi[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++) {
+        q[mt] = shared ? a.sq[mt] : a.q[mt] + (size_t)e * a.N * wrow;
+        sc[mt] = shared ? a.ss[mt] : a.s[mt] + (size_t)e * a.N * G;
+        bi[mt] = shared ? a.sb[mt] : a.b[mt] + (size_t)e * a.N * G;
+    }
+
+    const int rbase = rb * RB + wave * (RPW * RIT);
+    uint4 wq[RIT][2][CPL];
+    float ws[RIT][2][GPL], wb[RIT][2][GPL];
+#pragma unroll
+    for (int it = 0; it < RIT; it++) {
+        const int r0 = rbase + it * RPW + rsub;
+        const int r = r0 < a.N ? r0 : 0;
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++) {
+            const uint4 *src = (const uint4 *)(q[mt] + (size_t)r * wrow) + c0;
+#pragma unroll
+            for (int c = 0; c < CPL; c++) wq[it][mt][c] = qk_ld(src + c);
+            dec_ld_bf16<GPL>(sc[mt] + (size_t)r * G + g0, ws[it][mt]);
+            dec_ld_bf16<GPL>(bi[mt] + (size_t)r * G + g0, wb[it][mt]);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    /* activation pairs (x_i, x_{i+4}) per 8 columns, and chunk sums */
+    uint32_t hp[CPL][16];
+    uint32_t lp[XBF16 ? 1 : CPL][XBF16 ? 1 : 16];
+    float xs[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; c++) {
+        if (XBF16) {
+#pragma unroll
+            for (int w = 0; w < 4; w++) qk_bf16x8_to_pairs(xd[XBF16 ? c : 0][w], &hp[c][4 * w]);
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) s = qk_dot2(hp[c][i], QK_BF16_ONES, s);
+            xs[c] = s;
+        } else {
+            xs[c] = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const float4 a0 = xf[XBF16 ? 0 : c][2 * w], a1 = xf[XBF16 ? 0 : c][2 * w + 1];
+                const float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+                qk_f32x8_to_pairs(v, &hp[c][4 * w], &lp[XBF16 ? 0 : c][XBF16 ? 0 : 4 * w], xs[c]);
+            }
+        }
+    }
+
+#pragma unroll
+    for (int it = 0; it < RIT; it++) {
+        float acc[2];
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++) {
+            float part = 0.0f;
+#pragma unroll
+            for (int c = 0; c < CPL; c++) {
+                const int gl = CPL >= 2 ? c >> 1 : 0;
+                const float s = ws[it][mt][gl];
+                const float bp = fmaf(-128.0f, s, wb[it][mt][gl]);
+                const uint4 q4 = wq[it][mt][c];
+                const uint32_t words[4] = {q4.x, q4.y, q4.z, q4.w};
+                float d = 0.0f;
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    uint32_t pr[4];
+                    qk_codes_to_pairs(words[w], pr);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        d = qk_dot2(hp[c][4 * w + i], pr[i], d);
+                        if (!XBF16) d = qk_dot2(lp[XBF16 ? 0 : c][XBF16 ? 0 : 4 * w + i], pr[i], d);
+                    }
+                }
+                part = fmaf(s, d, fmaf(bp, xs[c], part));
+            }
+            acc[mt] = qk_group_sum<LPR>(part);
+        }
+        const int r = rbase + it * RPW + rsub;
+        if (valid && sub == 0 && r < a.N)
+            qk_st(a.out + (size_t)p0 * a.N + r, qk_silu(acc[0]) * acc[1]);
+    }
+}
+
+#endif

@@ -96,23 +96,32 @@ __device__ __forceinline__ void qk_bf16x8_to_pairs(uint4 d, uint32_t p[4]) {
 
 __device__ __forceinline__ uint32_t qk_pack2(uint32_t lo, uint32_t hi) { return (lo & 0xFFFFu) | (hi << 16); }
 
-/* eight f32 activations -> hi and lo bf16 pair sets with x ~= hi + lo
- * (hi = RNE(x), lo = RNE(x - hi); relative residual <= 2^-17); xsum gets
- * the sum of (hi + lo) so that the +128 code offset cancels exactly. */
+/* two f32 -> a bf16 pair (a in the low half), round to nearest even:
+ * v_cvt_pk_bf16_f32; same bits as qk_f2bf for finite values */
+typedef __bf16 qk_bf16x2v __attribute__((ext_vector_type(2)));
+typedef float qk_f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t qk_cvt_pk_bf16(float a, float b) {
+    const qk_f32x2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, qk_bf16x2v));
+}
+
+#define QK_BF16_ONES 0x3F803F80u /* the bf16 pair (1.0, 1.0) */
+
+/* eight f32 activations -> hi and lo bf16 pair sets in (x_i, x_{i+4})
+ * order with x ~= hi + lo (hi = RNE(x), lo = RNE(x - hi); x - hi is exact;
+ * relative residual <= 2^-17); xsum accumulates sum (hi + lo) with
+ * v_dot2 against (1, 1), hi pairs then lo pairs, i = 0..3 */
 __device__ __forceinline__ void qk_f32x8_to_pairs(const float x[8], uint32_t hi[4], uint32_t lo[4],
                                                   float &xsum) {
-    uint32_t h[8], l[8];
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        h[j] = qk_f2bf(x[j]);
-        float hf = __uint_as_float(h[j] << 16);
-        l[j] = qk_f2bf(x[j] - hf);
-        xsum += hf + __uint_as_float(l[j] << 16);
+    for (int i = 0; i < 4; i++) {
+        hi[i] = qk_cvt_pk_bf16(x[i], x[i + 4]);
+        lo[i] = qk_cvt_pk_bf16(x[i] - qk_bf16_lo(hi[i]), x[i + 4] - qk_bf16_hi(hi[i]));
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        hi[i] = qk_pack2(h[i], h[i + 4]);
-        lo[i] = qk_pack2(l[i], l[i + 4]);
+        xsum = qk_dot2(hi[i], QK_BF16_ONES, xsum);
+        xsum = qk_dot2(lo[i], QK_BF16_ONES, xsum);
     }
 }
 
@@ -152,25 +161,30 @@ __device__ __forceinline__ float qk_group_sum(float v) {
     return v;
 }
 
-/* wave-wide max / min of a u32, result uniform (every lane of a row holds
- * the row's extreme after the DPP steps; the four rows meet in scalars) */
+/* wave-wide max / min of a u32, result uniform.  After the four in-row
+ * DPP steps every lane of a row holds the row's extreme; row_bcast:15 then
+ * carries row r's lane 15 into row r+1 (rows 1 and 3 written) and
+ * row_bcast:31 carries lane 31 into rows 2 and 3, so lane 63 ends with the
+ * extreme of the wave. */
+#define QK_DPP_ROW_BCAST15 0x142
+#define QK_DPP_ROW_BCAST31 0x143
 __device__ __forceinline__ uint32_t qk_wave_max_u32(uint32_t v) {
     v = max(v, qk_dpp_u<QK_DPP_XOR1>(v));
     v = max(v, qk_dpp_u<QK_DPP_XOR2>(v));
     v = max(v, qk_dpp_u<QK_DPP_HALF_MIRROR>(v));
     v = max(v, qk_dpp_u<QK_DPP_MIRROR>(v));
-    uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
-    uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
-    return max(max(a, b), max(c, d));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, QK_DPP_ROW_BCAST15, 0xA, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, QK_DPP_ROW_BCAST31, 0xC, 0xF, false));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 __device__ __forceinline__ uint32_t qk_wave_min_u32(uint32_t v) {
     v = min(v, qk_dpp_u<QK_DPP_XOR1>(v));
     v = min(v, qk_dpp_u<QK_DPP_XOR2>(v));
     v = min(v, qk_dpp_u<QK_DPP_HALF_MIRROR>(v));
     v = min(v, qk_dpp_u<QK_DPP_MIRROR>(v));
-    uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
-    uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
-    return min(min(a, b), min(c, d));
+    v = min(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, QK_DPP_ROW_BCAST15, 0xA, 0xF, false));
+    v = min(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, QK_DPP_ROW_BCAST31, 0xC, 0xF, false));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
 #define QK_CHECK_LAUNCH() ((int)hipGetLastError())

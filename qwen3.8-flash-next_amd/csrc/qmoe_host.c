@@ -174,11 +174,11 @@ int qmoe_create(qmoe_ctx **out, const qmoe_config *cfg, qmoe_err *err) {
     const size_t H = (size_t)cfg->hidden, I = (size_t)cfg->moe_inter;
     const size_t nw = (n + 31) / 32, rows = n * k + n;
     const size_t ntasks = (size_t)qk_mfma_max_tasks(c->shape, (int)n);
-    size_t sz[15] = {n * (E + 1) * 4, n * k * 4, n * k * 4, n * 4, (E + 1) * 4, n * k * 4,
-                     n * k * 4, (E + 1) * 4, E * nw * 4, E * nw * 4, n * H * 4, rows * I * 4,
+    size_t sz[14] = {n * (E + 1) * 4, n * k * 4, n * k * 4, n * 4, (E + 1) * 4, n * k * 4,
+                     n * k * 4, E * nw * 4, E * nw * 4, n * H * 4, rows * I * 4,
                      rows * H * 4, (3 * E + 1) * 4, (2 + 2 * ntasks) * 4};
-    size_t total = 0, offs[15];
-    for (int i = 0; i < 15; i++) {
+    size_t total = 0, offs[14];
+    for (int i = 0; i < 14; i++) {
         offs[i] = total;
         total = align_up(total + sz[i]);
     }
@@ -196,14 +196,13 @@ int qmoe_create(qmoe_ctx **out, const qmoe_config *cfg, qmoe_err *err) {
     c->sc.offsets = (int32_t *)(b + offs[4]);
     c->sc.perm = (int32_t *)(b + offs[5]);
     c->sc.pos = (int32_t *)(b + offs[6]);
-    c->sc.unique = (int32_t *)(b + offs[7]);
-    c->sc.bits = (uint32_t *)(b + offs[8]);
-    c->sc.wprefix = (int32_t *)(b + offs[9]);
-    c->sc.xn = (float *)(b + offs[10]);
-    c->sc.h = (float *)(b + offs[11]);
-    c->sc.y = (float *)(b + offs[12]);
-    c->sc.segtab = (int32_t *)(b + offs[13]);
-    c->sc.tasks = (int32_t *)(b + offs[14]);
+    c->sc.bits = (uint32_t *)(b + offs[7]);
+    c->sc.wprefix = (int32_t *)(b + offs[8]);
+    c->sc.xn = (float *)(b + offs[9]);
+    c->sc.h = (float *)(b + offs[10]);
+    c->sc.y = (float *)(b + offs[11]);
+    c->sc.segtab = (int32_t *)(b + offs[12]);
+    c->sc.tasks = (int32_t *)(b + offs[13]);
     *out = c;
     return 0;
 }
@@ -550,7 +549,7 @@ int qmoe_dispatch(qmoe_ctx *c, const int32_t *idx, int n, int32_t *offsets_out, 
     NEED(idx, "idx");
     NEED(perm_out, "perm_out");
     return hip_fail(err, qk_launch_dispatch(c->shape, n, idx, offsets_out, perm_out, c->sc.pos,
-                                            c->sc.unique, segments_out, c->sc.bits, c->sc.wprefix,
+                                            segments_out, c->sc.bits, c->sc.wprefix,
                                             stream),
                     "dispatch");
 }
@@ -634,20 +633,26 @@ int qmoe_layer_forward(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n
     rc = qk_launch_router(W, s, x, xbf, n, sc->logits, xn, stream);
     if (hip_fail(err, rc, "router")) return -1;
     if (n <= QK_SMALL_N && n * s.k <= QK_SMALL_NK) {
+        /* offsets are not used by the layer; qmoe_last_routing derives them */
         rc = qk_launch_topk_dispatch_small(s, n, sc->logits, NULL, sc->idx, sc->w, sc->sg,
-                                           sc->offsets, sc->perm, sc->pos, sc->unique, sc->segtab,
-                                           stream);
+                                           n == 1 ? NULL : sc->offsets, sc->perm, sc->pos,
+                                           sc->segtab, stream);
         if (hip_fail(err, rc, "topk+dispatch")) return -1;
     } else {
         rc = qk_launch_topk(s, n, sc->logits, NULL, sc->idx, sc->w, sc->sg, stream);
         if (hip_fail(err, rc, "topk")) return -1;
-        rc = qk_launch_dispatch(s, n, sc->idx, sc->offsets, sc->perm, sc->pos, sc->unique,
-                                sc->segtab, sc->bits, sc->wprefix, stream);
+        rc = qk_launch_dispatch(s, n, sc->idx, sc->offsets, sc->perm, sc->pos, sc->segtab,
+                                sc->bits, sc->wprefix, stream);
         if (hip_fail(err, rc, "dispatch")) return -1;
     }
     const void *xf = W->norm_w ? (const void *)sc->xn : x;
     const int xf_bf = W->norm_w ? 0 : xbf;
     if (run_gateup(c, W, xf, xf_bf, n, sc->perm, sc->segtab, sc->h, stream, err)) return -1;
+    if (!mfma_usable(c, n) && qk_down_combine_lds(s, n) > 0) {
+        rc = qk_launch_down_combine(W, s, sc->h, n, sc->segtab, sc->pos, sc->w, sc->sg,
+                                    (flags & QMOE_RESIDUAL) ? x : NULL, xbf, out, stream);
+        return hip_fail(err, rc, "down+combine");
+    }
     if (run_down(c, W, sc->h, n, sc->segtab, xf_bf, sc->y, stream, err)) return -1;
     rc = qk_launch_combine(s, n, sc->y, sc->pos, sc->w, sc->sg,
                            (flags & QMOE_RESIDUAL) ? x : NULL, xbf, out, stream);
@@ -693,6 +698,10 @@ int qmoe_last_routing(qmoe_ctx *c, int n, int32_t *idx_out, float *w_out, float 
         return -1;
     }
     const size_t nk = (size_t)n * c->cfg.top_k, E1 = (size_t)c->cfg.n_experts + 1;
+    if (offsets_out &&
+        hip_fail(err, qk_launch_offsets_from_segtab(c->shape, c->sc.segtab, c->sc.offsets, stream),
+                 "last_routing offsets"))
+        return -1;
     struct {
         void *dst;
         const void *src;

@@ -38,7 +38,6 @@ typedef struct {
     int32_t *offsets;  /* [E+1] */
     int32_t *perm;     /* [n*k] */
     int32_t *pos;      /* [n*k] inverse of perm */
-    int32_t *unique;   /* [1+E] */
     int32_t *segtab;   /* [1+3E]: U, then (expert, first position, count) per routed segment */
     int32_t *tasks;    /* [2+2*max_tasks]: MFMA (segment, chunk) task list */
     uint32_t *bits;    /* [E, ceil(n/32)] token membership bitmask (large dispatch) */
@@ -56,18 +55,22 @@ int qk_launch_router(const qmoe_layer_weights *W, qk_shape s, const void *x, int
                      float *logits, float *xn, void *stream);
 
 /* top-k + renorm + sigmoid; copies the first E logit columns to logits_out
- * when non-NULL.  With dispatch outputs non-NULL and a small n, also runs
- * the whole dispatch in the same (single-workgroup) launch. */
+ * when non-NULL. */
 int qk_launch_topk(qk_shape s, int n, const float *logits, float *logits_out, int32_t *idx,
                    float *w, float *sg, void *stream);
+/* top-k and the whole dispatch in one single-workgroup launch, for
+ * n <= QK_SMALL_N and n*k <= QK_SMALL_NK; offsets may be NULL only for
+ * n == 1 */
 int qk_launch_topk_dispatch_small(qk_shape s, int n, const float *logits, float *logits_out,
                                   int32_t *idx, float *w, float *sg, int32_t *offsets,
-                                  int32_t *perm, int32_t *pos, int32_t *unique, int32_t *segtab,
-                                  void *stream);
+                                  int32_t *perm, int32_t *pos, int32_t *segtab, void *stream);
 /* dispatch from idx alone (any n) */
 int qk_launch_dispatch(qk_shape s, int n, const int32_t *idx, int32_t *offsets, int32_t *perm,
-                       int32_t *pos, int32_t *unique, int32_t *segtab, uint32_t *bits,
-                       int32_t *wprefix, void *stream);
+                       int32_t *pos, int32_t *segtab, uint32_t *bits, int32_t *wprefix,
+                       void *stream);
+/* offsets [E+1] from a segment table */
+int qk_launch_offsets_from_segtab(qk_shape s, const int32_t *segtab, int32_t *offsets,
+                                  void *stream);
 /* pos[perm[p]] = p */
 int qk_launch_invert_perm(int count, const int32_t *perm, int32_t *pos, void *stream);
 
@@ -89,6 +92,16 @@ int qk_launch_gateup_mfma(const qmoe_layer_weights *W, qk_shape s, const uint16_
                           float *h, void *stream);
 int qk_launch_down_mfma(const qmoe_layer_weights *W, qk_shape s, const float *h, int n,
                         const int32_t *segtab, const int32_t *tasks, float *y, void *stream);
+/* down projection fused with the combine for n <= QK_DC_MAX_N tokens;
+ * bit-identical to qk_launch_down + qk_launch_combine.  qk_down_combine_lds
+ * returns its LDS bytes, 0 when it does not apply. */
+#define QK_DC_MAX_N 8
+#define QK_DC_MAX_LDS 32768
+size_t qk_down_combine_lds(qk_shape s, int n);
+int qk_launch_down_combine(const qmoe_layer_weights *W, qk_shape s, const float *h, int n,
+                           const int32_t *segtab, const int32_t *pos, const float *w,
+                           const float *sg, const void *x_res, int x_bf16, float *out,
+                           void *stream);
 int qk_launch_combine(qk_shape s, int n, const float *y, const int32_t *pos, const float *w,
                       const float *sg, const void *x_res, int x_bf16, float *out, void *stream);
 

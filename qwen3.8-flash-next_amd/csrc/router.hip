@@ -1,7 +1,7 @@
 /*
  * router.hip -- router logits, top-k + renormalise, and token dispatch for
  * gfx950.  Replaces model.c:1301-1332 and 1354-1367 of the reference C port
- * (gemm_bf16 + kernel_topk_indices + softmax-over-selected + unique/gather).
+ * (gemm_bf16 + kernel_topk_indices + softmax-over-selected + expert gather).
  *
  * Router reduction order ("R64", bit-exact with the oracle): for one
  * (token, expert) dot product the K axis is cut into 8-element chunks, chunk
@@ -191,123 +191,101 @@ __device__ __forceinline__ float qk_ordkey_value(uint32_t o) {
     return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
 }
 
-#define TK_MAXPL (QK_MAX_EXPERTS / 64)
-
-/* per-wave LDS for the top-k ranking */
-struct TopkLds {
-    uint32_t key[QK_MAX_TOPK];
-    int32_t id[QK_MAX_TOPK];
-    uint32_t skey[QK_MAX_TOPK];
-    int32_t sid[QK_MAX_TOPK];
-};
-
-__device__ __forceinline__ int qk_lanes_below(uint64_t mask) {
-    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
-                                          __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
-}
-
 /*
- * One wavefront selects the top k of row[0..E) (all 64 lanes active).
- * (1) Radix select on the order-preserving keys: from the top bit down,
- *     keep a bit if at least k keys reach the candidate prefix (counted
- *     with ballots); stop early once exactly k keys reach it.  (2) The
- *     selected set is every key above the threshold plus, if the threshold
- *     is shared, the lowest ids among the keys equal to it.  (3) The k
- *     entries are ranked by (value desc, id asc) in LDS.  Then
- *     w_s = exp(v_s - v_0) / sum over the sorted slots (model.c:1305-1318).
- * Lane s < k returns slot s.  The set and order are exactly the oracle's
- * canonical top-k; -0 and +0 tie.
+ * One wavefront selects the top k of row[0..E) in canonical order: value
+ * descending, ties to the lower expert id, -0 equal to +0.  Lane l holds
+ * the PL experts e = l*PL + i (E <= 64*PL) and sorts them descending with
+ * an odd-even transposition network; it swaps neighbours only on strict
+ * inequality, so equal keys keep ascending e.  Then k rounds: the wave
+ * maximum of the lane heads; the lowest lane holding it wins (lane order is
+ * e order, so that is the lowest e among equal keys) and pops its head.
+ * Round s yields slot s.  Lane s < k returns slot s's expert and weight
+ * w_s = exp(v_s - v_0) / sum_j exp(v_j - v_0), summed in slot order
+ * (model.c:1305-1318).  Padding entries (e >= E) carry key 0 and valid
+ * keys are at least 1, so padding is never chosen while E >= k.
  */
-__device__ __forceinline__ void wave_topk(const float *row, int E, int k, int lane, TopkLds *L,
-                                          int &my_id, float &my_w) {
-    uint32_t key[TK_MAXPL];
-    const int PL = (E + 63) >> 6;
+template <int PL>
+__device__ __forceinline__ void wave_topk(const float *row, int E, int k, int lane, int &my_id,
+                                          float &my_w) {
+    static_assert(PL <= 16, "at most 16 experts per lane");
+    uint32_t kk[PL];
+    int ii[PL]; /* local index i of each sorted entry */
 #pragma unroll
-    for (int i = 0; i < TK_MAXPL; i++) {
-        const int e = lane + 64 * i;
+    for (int i = 0; i < PL; i++) {
+        const int e = lane * PL + i;
         const float v = qk_ld(row + (e < E ? e : E - 1));
-        key[i] = qk_ordkey(v);
+        kk[i] = e < E ? max(qk_ordkey(v), 1u) : 0u;
+        ii[i] = i;
     }
-    auto count_ge = [&](uint32_t cand) -> int {
-        int c = 0;
 #pragma unroll
-        for (int i = 0; i < TK_MAXPL; i++)
-            if (i < PL) c += __popcll(__ballot(key[i] >= cand && lane + 64 * i < E));
-        return c;
-    };
-    uint32_t T = 0u;
-    int cge = E;
-    for (int b = 31; b >= 0 && cge != k; b--) {
-        const uint32_t cand = T | (1u << b);
-        const int c = count_ge(cand);
-        if (c >= k) {
-            T = cand;
-            cge = c;
+    for (int pass = 0; pass < PL; pass++) {
+#pragma unroll
+        for (int i = pass & 1; i + 1 < PL; i += 2) {
+            const bool sw = kk[i + 1] > kk[i];
+            const uint32_t ka = kk[i], kb = kk[i + 1];
+            const int ia = ii[i], ib = ii[i + 1];
+            kk[i] = sw ? kb : ka;
+            kk[i + 1] = sw ? ka : kb;
+            ii[i] = sw ? ib : ia;
+            ii[i + 1] = sw ? ia : ib;
         }
     }
-    /* selection flags: key > T, or key == T taken in id order until k */
-    int need = k;
-    if (cge != k) need = k - (T == 0xFFFFFFFFu ? 0 : count_ge(T + 1u)); /* ties at T to take */
-    uint32_t sel = 0u;
+    /* sorted local indices packed 4 bits each (entries beyond 8 in a second
+     * word), so a pop shifts one or two registers */
+    uint32_t pk0 = 0u, pk1 = 0u;
 #pragma unroll
-    for (int i = 0; i < TK_MAXPL; i++) {
-        if (i < PL) {
-            const bool valid = lane + 64 * i < E;
-            const bool gt = valid && (cge == k ? key[i] >= T : key[i] > T);
-            bool take = gt;
-            if (cge != k) {
-                const uint64_t eq = __ballot(valid && key[i] == T);
-                const int r = qk_lanes_below(eq);
-                if (valid && key[i] == T && r < need) take = true;
-                need -= min(need, (int)__popcll(eq));
+    for (int i = 0; i < PL; i++) {
+        if (i < 8) pk0 |= (uint32_t)ii[i] << (4 * i);
+        else pk1 |= (uint32_t)ii[i] << (4 * (i - 8));
+    }
+    uint32_t my_key = 0u;
+    my_id = 0;
+    for (int r = 0; r < k; r++) {
+        const uint32_t m = qk_wave_max_u32(kk[0]);
+        const uint64_t ball = __ballot(kk[0] == m);
+        const int wl = (int)__builtin_ctzll(ball);
+        const int e = wl * PL + (int)(__builtin_amdgcn_readlane((int)pk0, wl) & 15u);
+        if (lane == r) {
+            my_key = m;
+            my_id = e;
+        }
+        if (lane == wl) {
+#pragma unroll
+            for (int i = 0; i + 1 < PL; i++) kk[i] = kk[i + 1];
+            kk[PL - 1] = 0u;
+            if (PL > 8) {
+                pk0 = (pk0 >> 4) | (pk1 << 28);
+                pk1 >>= 4;
+            } else {
+                pk0 >>= 4;
             }
-            if (take) sel |= 1u << i;
         }
     }
-    /* compact the k entries into LDS */
-    int base = 0;
-#pragma unroll
-    for (int i = 0; i < TK_MAXPL; i++) {
-        if (i < PL) {
-            const bool t = (sel >> i) & 1u;
-            const uint64_t m = __ballot(t);
-            if (t) {
-                const int pos = base + qk_lanes_below(m);
-                L->key[pos] = key[i];
-                L->id[pos] = lane + 64 * i;
-            }
-            base += (int)__popcll(m);
-        }
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f); /* lgkmcnt(0): LDS writes done */
-    __builtin_amdgcn_wave_barrier();
-    /* rank: value desc, id asc */
-    if (lane < k) {
-        const uint32_t mk = L->key[lane];
-        const int mi = L->id[lane];
-        int rank = 0;
-        for (int j = 0; j < k; j++) {
-            const uint32_t kj = L->key[j];
-            const int ij = L->id[j];
-            rank += (kj > mk || (kj == mk && ij < mi)) ? 1 : 0;
-        }
-        L->skey[rank] = mk;
-        L->sid[rank] = mi;
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
-    /* softmax over the selected logits in slot order */
-    const float vmax = qk_ordkey_value(L->skey[0]);
-    float sum = 0.0f, my_e = 0.0f;
-    for (int j = 0; j < k; j++) {
-        const float ev = expf(qk_ordkey_value(L->skey[j]) - vmax);
-        sum += ev;
-        if (j == lane) my_e = ev;
-    }
-    my_id = lane < k ? L->sid[lane] : 0;
-    my_w = my_e / sum;
-    __builtin_amdgcn_wave_barrier();
+    const float v = qk_ordkey_value(my_key);
+    const float v0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float ev = lane < k ? expf(v - v0) : 0.0f;
+    float sum = 0.0f;
+    for (int j = 0; j < k; j++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), j));
+    my_w = ev / sum;
 }
+
+/* experts per lane for E experts: the power of two >= ceil(E/64) */
+static int topk_pl(int E) {
+    int pl = 1;
+    while (pl * 64 < E) pl <<= 1;
+    return pl;
+}
+
+#define TK_DISPATCH(KERNEL, PL, GRID, BLOCK, ARGS)                                              \
+    do {                                                                                       \
+        switch (PL) {                                                                          \
+        case 1: hipLaunchKernelGGL(KERNEL<1>, GRID, BLOCK, 0, st, ARGS); break;                \
+        case 2: hipLaunchKernelGGL(KERNEL<2>, GRID, BLOCK, 0, st, ARGS); break;                \
+        case 4: hipLaunchKernelGGL(KERNEL<4>, GRID, BLOCK, 0, st, ARGS); break;                \
+        case 8: hipLaunchKernelGGL(KERNEL<8>, GRID, BLOCK, 0, st, ARGS); break;                \
+        default: hipLaunchKernelGGL(KERNEL<16>, GRID, BLOCK, 0, st, ARGS); break;              \
+        }                                                                                      \
+    } while (0)
 
 struct TopkArgs {
     const float *logits; /* [n, E+1] */
@@ -318,34 +296,35 @@ struct TopkArgs {
     int E, k, n;
 };
 
-__device__ __forceinline__ void topk_token(const TopkArgs &a, int t, int lane, TopkLds *L,
-                                           int32_t *lds_idx) {
+template <int PL>
+__device__ __forceinline__ void topk_token(const TopkArgs &a, int t, int lane, int32_t *lds_idx) {
     const float *row = a.logits + (size_t)t * (a.E + 1);
     int id;
     float wt;
-    wave_topk(row, a.E, a.k, lane, L, id, wt);
+    wave_topk<PL>(row, a.E, a.k, lane, id, wt);
     if (lane < a.k) {
         a.idx[(size_t)t * a.k + lane] = id;
         a.w[(size_t)t * a.k + lane] = wt;
         if (lds_idx) lds_idx[t * a.k + lane] = id;
     }
-    if (lane == 0) a.sg[t] = qk_sigmoid(row[a.E]);
+    if (lane == 0) a.sg[t] = qk_sigmoid(qk_ld(row + a.E));
     if (a.logits_out)
         for (int e = lane; e < a.E; e += 64) a.logits_out[(size_t)t * a.E + e] = row[e];
 }
 
+template <int PL>
 __global__ __launch_bounds__(256) void k_topk(TopkArgs a) {
-    __shared__ TopkLds s_tk[4];
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= a.n) return;
-    topk_token(a, t, threadIdx.x & 63, &s_tk[threadIdx.x >> 6], nullptr);
+    topk_token<PL>(a, t, threadIdx.x & 63, nullptr);
 }
 
 extern "C" int qk_launch_topk(qk_shape s, int n, const float *logits, float *logits_out,
                               int32_t *idx, float *w, float *sg, void *stream) {
     if (n <= 0) return 0;
     TopkArgs a{logits, logits_out, idx, w, sg, s.E, s.k, n};
-    hipLaunchKernelGGL(k_topk, dim3((n + 3) / 4), dim3(256), 0, (hipStream_t)stream, a);
+    hipStream_t st = (hipStream_t)stream;
+    TK_DISPATCH(k_topk, topk_pl(s.E), dim3((n + 3) / 4), dim3(256), a);
     return QK_CHECK_LAUNCH();
 }
 
@@ -358,9 +337,9 @@ extern "C" int qk_launch_topk(qk_shape s, int n, const float *logits, float *log
  * tokens that chose e.  So the result equals the oracle's sequential
  * counting sort with no ordering dependence on the hardware.
  *
- * Outputs: offsets [E+1], perm [n*k], pos [n*k] (inverse), unique [1+E]
- * (count, then the experts with tokens ascending) and the segment table
- * segtab [1+3E] (count, then (expert, offsets[e], count[e]) per segment).
+ * Outputs: offsets [E+1], perm [n*k], pos [n*k] (inverse) and the segment
+ * table segtab [1+3E] (count U, then (expert, offsets[e], count[e]) for the
+ * U experts with tokens, ascending).
  */
 
 /* block-wide exclusive scan of NT/64 waves, one int per thread */
@@ -386,11 +365,12 @@ __device__ int block_exscan(int v, int *lds /* >= NT/64 ints */, int &total) {
     return wbase + inc - v;
 }
 
-/* per-expert counts (cnt[j] for experts e = threadIdx.x + j*NT) -> offsets,
- * unique, segtab; lds_off gets offsets when non-null */
+/* per-expert counts (cnt[j] for experts e = threadIdx.x*PER + j) ->
+ * offsets and segtab; lds_off gets offsets when non-null; returns the
+ * total count (in every thread) */
 template <int NT>
-__device__ void counts_to_offsets(const int *cnt, int E, int *lds_scan, int32_t *offsets,
-                                  int32_t *unique, int32_t *segtab, int *lds_off) {
+__device__ int counts_to_offsets(const int *cnt, int E, int *lds_scan, int32_t *offsets,
+                                  int32_t *segtab, int *lds_off) {
     constexpr int PER = QK_MAX_EXPERTS / NT;
     int csum = 0, asum = 0;
 #pragma unroll
@@ -411,7 +391,6 @@ __device__ void counts_to_offsets(const int *cnt, int E, int *lds_scan, int32_t 
             offsets[e] = off;
             if (lds_off) lds_off[e] = off;
             if (cnt[j] > 0) {
-                unique[1 + uoff] = e;
                 segtab[1 + 3 * uoff] = e;
                 segtab[2 + 3 * uoff] = off;
                 segtab[3 + 3 * uoff] = cnt[j];
@@ -422,16 +401,16 @@ __device__ void counts_to_offsets(const int *cnt, int E, int *lds_scan, int32_t 
     }
     if (threadIdx.x == 0) {
         offsets[E] = total;
-        unique[0] = ntot;
         segtab[0] = ntot;
     }
+    return total;
 }
 
 /* dispatch of n <= QK_SMALL_N tokens whose expert ids are in LDS (s_idx),
  * run by one NT-thread workgroup */
 template <int NT>
 __device__ void dispatch_block(const int32_t *s_idx, int n, int k, int E, int32_t *offsets,
-                               int32_t *perm, int32_t *pos, int32_t *unique, int32_t *segtab) {
+                               int32_t *perm, int32_t *pos, int32_t *segtab) {
     __shared__ uint32_t s_bits[QK_MAX_EXPERTS * (QK_SMALL_N / 32)];
     __shared__ int32_t s_wpre[QK_MAX_EXPERTS * (QK_SMALL_N / 32)];
     __shared__ int32_t s_off[QK_MAX_EXPERTS];
@@ -457,7 +436,7 @@ __device__ void dispatch_block(const int32_t *s_idx, int n, int k, int E, int32_
                 cnt[j] += __popc(s_bits[e * NW + wd]);
             }
     }
-    counts_to_offsets<NT>(cnt, E, s_scan, offsets, unique, segtab, s_off);
+    counts_to_offsets<NT>(cnt, E, s_scan, offsets, segtab, s_off);
     __syncthreads();
     for (int f = tid; f < n * k; f += NT) {
         const int t = f / k, e = s_idx[f], wd = t >> 5;
@@ -474,73 +453,73 @@ __device__ void dispatch_block(const int32_t *s_idx, int n, int k, int E, int32_
 
 struct SmallDispArgs {
     TopkArgs tk;
-    int32_t *offsets, *perm, *pos, *unique, *segtab;
+    int32_t *offsets, *perm, *pos, *segtab;
 };
 
-/* dispatch of a single token by one wavefront: its k distinct experts,
- * sorted ascending, are the segments, one slot each */
-__device__ __forceinline__ void dispatch_one_token(const SmallDispArgs &d, int lane, int my_id) {
-    const int k = d.tk.k, E = d.tk.E;
+/*
+ * One token, one wavefront: top-k, then its k distinct experts sorted
+ * ascending are the segments, one slot each (rank = number of selected
+ * experts with a lower id).  Offsets are written only when asked for.
+ */
+template <int PL>
+__global__ __launch_bounds__(64) void k_topk_dispatch_one(SmallDispArgs a) {
+    const int lane = threadIdx.x;
+    const int k = a.tk.k, E = a.tk.E;
+    const float *row = a.tk.logits;
+    int id;
+    float wt;
+    wave_topk<PL>(row, E, k, lane, id, wt);
+    const int my_id = lane < k ? id : 0x7FFFFFFF;
     int rank = 0;
-    for (int s2 = 0; s2 < k; s2++) {
-        const int o = __shfl(my_id, s2, QK_WAVE);
-        rank += o < my_id ? 1 : 0;
-    }
+    for (int s2 = 0; s2 < k; s2++) rank += __builtin_amdgcn_readlane(my_id, s2) < my_id ? 1 : 0;
     if (lane < k) {
-        d.perm[rank] = lane;
-        d.pos[lane] = rank;
-        d.unique[1 + rank] = my_id;
-        d.segtab[1 + 3 * rank] = my_id;
-        d.segtab[2 + 3 * rank] = rank;
-        d.segtab[3 + 3 * rank] = 1;
-    }
-    for (int e = lane; e <= E; e += 64) {
-        int c = 0;
-        for (int s2 = 0; s2 < k; s2++) c += __shfl(my_id, s2, QK_WAVE) < e ? 1 : 0;
-        d.offsets[e] = c;
+        a.tk.idx[lane] = id;
+        a.tk.w[lane] = wt;
+        a.perm[rank] = lane;
+        a.pos[lane] = rank;
+        a.segtab[1 + 3 * rank] = id;
+        a.segtab[2 + 3 * rank] = rank;
+        a.segtab[3 + 3 * rank] = 1;
     }
     if (lane == 0) {
-        d.unique[0] = k;
-        d.segtab[0] = k;
+        a.segtab[0] = k;
+        a.tk.sg[0] = qk_sigmoid(qk_ld(row + E));
     }
+    if (a.tk.logits_out)
+        for (int e = lane; e < E; e += 64) a.tk.logits_out[e] = row[e];
+    if (a.offsets)
+        for (int e = lane; e <= E; e += 64) {
+            int c = 0;
+            for (int s2 = 0; s2 < k; s2++) c += __builtin_amdgcn_readlane(my_id, s2) < e ? 1 : 0;
+            a.offsets[e] = c;
+        }
 }
 
-/* n <= QK_SMALL_N, n*k <= QK_SMALL_NK: top-k (one wave per token) and the
- * whole dispatch in one 1024-thread workgroup */
+/* 2 <= n <= QK_SMALL_N, n*k <= QK_SMALL_NK: top-k (one wave per token) and
+ * the whole dispatch in one 1024-thread workgroup */
+template <int PL>
 __global__ __launch_bounds__(1024) void k_topk_dispatch_small(SmallDispArgs a) {
     __shared__ int32_t s_idx[QK_SMALL_NK];
-    __shared__ TopkLds s_tk[16];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (a.tk.n == 1) { /* one token: one wave does everything, no barriers */
-        if (wave == 0) {
-            const float *row0 = a.tk.logits;
-            int id;
-            float wt;
-            wave_topk(row0, a.tk.E, a.tk.k, lane, &s_tk[0], id, wt);
-            if (lane < a.tk.k) {
-                a.tk.idx[lane] = id;
-                a.tk.w[lane] = wt;
-            }
-            if (lane == 0) a.tk.sg[0] = qk_sigmoid(qk_ld(row0 + a.tk.E));
-            if (a.tk.logits_out)
-                for (int e = lane; e < a.tk.E; e += 64) a.tk.logits_out[e] = row0[e];
-            dispatch_one_token(a, lane, lane < a.tk.k ? id : 0x7FFFFFFF);
-        }
-        return;
-    }
-    for (int t = wave; t < a.tk.n; t += 16) topk_token(a.tk, t, lane, &s_tk[wave], s_idx);
+    for (int t = wave; t < a.tk.n; t += 16) topk_token<PL>(a.tk, t, lane, s_idx);
     __syncthreads();
-    dispatch_block<1024>(s_idx, a.tk.n, a.tk.k, a.tk.E, a.offsets, a.perm, a.pos, a.unique,
-                         a.segtab);
+    dispatch_block<1024>(s_idx, a.tk.n, a.tk.k, a.tk.E, a.offsets, a.perm, a.pos, a.segtab);
 }
 
 extern "C" int qk_launch_topk_dispatch_small(qk_shape s, int n, const float *logits,
                                              float *logits_out, int32_t *idx, float *w, float *sg,
                                              int32_t *offsets, int32_t *perm, int32_t *pos,
-                                             int32_t *unique, int32_t *segtab, void *stream) {
+                                             int32_t *segtab, void *stream) {
     if (n <= 0) return 0;
-    SmallDispArgs a{{logits, logits_out, idx, w, sg, s.E, s.k, n}, offsets, perm, pos, unique, segtab};
-    hipLaunchKernelGGL(k_topk_dispatch_small, dim3(1), dim3(1024), 0, (hipStream_t)stream, a);
+    if (n > QK_SMALL_N || n * s.k > QK_SMALL_NK) return (int)hipErrorInvalidValue;
+    SmallDispArgs a{{logits, logits_out, idx, w, sg, s.E, s.k, n}, offsets, perm, pos, segtab};
+    hipStream_t st = (hipStream_t)stream;
+    if (n == 1) {
+        TK_DISPATCH(k_topk_dispatch_one, topk_pl(s.E), dim3(1), dim3(64), a);
+    } else {
+        if (!offsets) return (int)hipErrorInvalidValue;
+        TK_DISPATCH(k_topk_dispatch_small, topk_pl(s.E), dim3(1), dim3(1024), a);
+    }
     return QK_CHECK_LAUNCH();
 }
 
@@ -560,10 +539,12 @@ __global__ void k_setbits(const int32_t *idx, int n, int k, int E, int NW, uint3
     atomicOr(&bits[(size_t)e * NW + (t >> 5)], 1u << (t & 31));
 }
 
-/* one workgroup: per-expert word prefixes (wave per expert) + offsets */
+/* one workgroup: per-expert word prefixes (wave per expert) + offsets;
+ * perm entries past the dispatched total (slots with invalid expert ids)
+ * are set to -1 */
 __global__ __launch_bounds__(1024) void k_count_offsets(const uint32_t *bits, int32_t *wprefix,
                                                         int E, int NW, int32_t *offsets,
-                                                        int32_t *unique, int32_t *segtab) {
+                                                        int32_t *segtab, int32_t *perm, int nk) {
     __shared__ int s_cnt[QK_MAX_EXPERTS];
     __shared__ int s_scan[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -585,7 +566,8 @@ __global__ __launch_bounds__(1024) void k_count_offsets(const uint32_t *bits, in
     }
     __syncthreads();
     int cnt[1] = {tid < E ? s_cnt[tid] : 0};
-    counts_to_offsets<1024>(cnt, E, s_scan, offsets, unique, segtab, nullptr);
+    const int total = counts_to_offsets<1024>(cnt, E, s_scan, offsets, segtab, nullptr);
+    for (int i = total + tid; i < nk; i += 1024) perm[i] = -1;
 }
 
 __global__ void k_scatter(const int32_t *idx, int n, int k, int E, int NW, const uint32_t *bits,
@@ -605,7 +587,7 @@ __global__ void k_scatter(const int32_t *idx, int n, int k, int E, int NW, const
 }
 
 extern "C" int qk_launch_dispatch(qk_shape s, int n, const int32_t *idx, int32_t *offsets,
-                                  int32_t *perm, int32_t *pos, int32_t *unique, int32_t *segtab,
+                                  int32_t *perm, int32_t *pos, int32_t *segtab,
                                   uint32_t *bits, int32_t *wprefix, void *stream) {
     hipStream_t st = (hipStream_t)stream;
     if (n <= 0) return 0;
@@ -616,7 +598,7 @@ extern "C" int qk_launch_dispatch(qk_shape s, int n, const int32_t *idx, int32_t
     hipLaunchKernelGGL(k_setbits, dim3((nk + 255) / 256), dim3(256), 0, st, idx, n, s.k, s.E, NW,
                        bits);
     hipLaunchKernelGGL(k_count_offsets, dim3(1), dim3(1024), 0, st, (const uint32_t *)bits, wprefix,
-                       s.E, NW, offsets, unique, segtab);
+                       s.E, NW, offsets, segtab, perm, nk);
     hipLaunchKernelGGL(k_scatter, dim3((nk + 255) / 256), dim3(256), 0, st, idx, n, s.k, s.E, NW,
                        (const uint32_t *)bits, (const int32_t *)wprefix, (const int32_t *)offsets,
                        perm, pos);
@@ -642,5 +624,31 @@ extern "C" int qk_launch_invert_perm(int count, const int32_t *perm, int32_t *po
                        pos, count, -1);
     hipLaunchKernelGGL(k_invert_perm, dim3((count + 255) / 256), dim3(256), 0, (hipStream_t)stream,
                        count, perm, pos);
+    return QK_CHECK_LAUNCH();
+}
+
+/* offsets[e] (e = 0..E) from a segment table whose experts ascend: the
+ * first dispatch position of the first segment with expert >= e, or the
+ * total count when there is none */
+__global__ void k_offsets_from_segtab(const int32_t *segtab, int E, int32_t *offsets) {
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e > E) return;
+    const int U = min(max(segtab[0], 0), E);
+    int lo = 0, hi = U; /* first segment index with expert >= e */
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (segtab[1 + 3 * mid] < e) lo = mid + 1;
+        else hi = mid;
+    }
+    int v;
+    if (lo < U) v = segtab[2 + 3 * lo];
+    else v = U > 0 ? segtab[2 + 3 * (U - 1)] + segtab[3 + 3 * (U - 1)] : 0;
+    offsets[e] = v;
+}
+
+extern "C" int qk_launch_offsets_from_segtab(qk_shape s, const int32_t *segtab, int32_t *offsets,
+                                             void *stream) {
+    hipLaunchKernelGGL(k_offsets_from_segtab, dim3((s.E + 1 + 255) / 256), dim3(256), 0,
+                       (hipStream_t)stream, segtab, s.E, offsets);
     return QK_CHECK_LAUNCH();
 }

@@ -263,26 +263,63 @@ def test_depth_stack_norm_residual(torch_dev):
             hd = to_dev(h, torch, dev)
 
 
-def test_stages_compose_to_layer(torch_dev):
+@pytest.mark.parametrize("n,residual", [(64, False), (1, False), (1, True), (5, True)])
+def test_stages_compose_to_layer(torch_dev, n, residual):
+    """the stage entry points chained by hand give the layer's bits (n <= 8
+    exercises the layer's fused down+combine kernel, n = 64 the separate
+    down and combine kernels)"""
     torch, dev = torch_dev
     pkg = load_pkg()
-    say("case: router -> dispatch -> ffn -> combine == layer_forward")
+    say(f"case: router -> dispatch -> ffn -> combine == layer_forward, n={n} residual={residual}")
     w = pkg.WORKLOADS["batched"]
     rb = orc.zipf_bias(w.n_experts, w.zipf_s, w.zipf_scale, 0)
-    x = orc.gen_x(w.n_tokens, w.hidden, 1, bf16=True)
-    with pkg.MoeContext.for_workload(w) as ctx:
+    x = orc.gen_x(n, w.hidden, 1, bf16=True)
+    with pkg.MoeContext.for_workload(w, max_tokens=n) as ctx:
         ctx.synth_layer(0, 0, router_bias=rb)
         xt = to_dev(x, torch, dev)
-        full = ctx.layer_forward(0, xt)
+        full = ctx.layer_forward(0, xt, residual=residual)
         rt = ctx.router(0, xt)
         d = ctx.dispatch(rt["idx"])
         h = ctx.expert_gateup(0, xt, d)
-        y = ctx.expert_down(0, h, w.n_tokens, d)
+        y = ctx.expert_down(0, h, n, d)
         y2 = ctx.expert_ffn(0, xt, d)
-        out = ctx.combine(y, d["perm"], rt["w"], rt["shared_gate"], w.n_tokens)
+        out = ctx.combine(y, d["perm"], rt["w"], rt["shared_gate"], n,
+                          x_residual=xt if residual else None)
         torch.cuda.synchronize()
         assert torch.equal(y, y2)
         assert torch.equal(out, full)
+
+
+def test_combine_skips_undispatched_slots(torch_dev):
+    """slots whose expert id is invalid are left out of the dispatch; the
+    combine must then add nothing for them (several such slots share one
+    sentinel position)"""
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    say("case: combine with undispatched slots")
+    n, k, E, H, I = 3, 4, 8, 128, 64
+    idx = np.array([[0, 9, 3, -1], [2, 3, 11, 12], [5, 6, 7, 1]], dtype=np.int32)
+    rng = np.random.default_rng(3)
+    wts = rng.random((n, k)).astype(np.float32)
+    sg = rng.random(n).astype(np.float32)
+    with pkg.MoeContext(H, E, k, I, max_tokens=n) as ctx:
+        d = ctx.dispatch(to_dev(idx, torch, dev))
+        perm = d["perm"].cpu().numpy()
+        nk_valid = int(d["offsets"].cpu().numpy()[E])
+        assert nk_valid == int(((idx >= 0) & (idx < E)).sum())
+        y = rng.standard_normal((n * k + n, H)).astype(np.float32)
+        out = ctx.combine(to_dev(y, torch, dev), d["perm"], to_dev(wts, torch, dev),
+                          to_dev(sg, torch, dev), n)
+        torch.cuda.synchronize()
+        ref = np.zeros((n, H), np.float32)
+        pos = {int(f): p for p, f in enumerate(perm[:nk_valid])}
+        for t in range(n):
+            order = sorted((pos[t * k + s], s) for s in range(k) if t * k + s in pos)
+            acc = np.zeros(H, np.float32)
+            for p, s in order:
+                acc = (np.float32(wts[t, s]) * y[p] + acc).astype(np.float32)
+            ref[t] = (np.float32(sg[t]) * y[n * k + t] + acc).astype(np.float32)
+        np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-6, atol=1e-6)
 
 
 # ------------------------------------------------------------ edges
