@@ -419,6 +419,58 @@ __global__ __launch_bounds__(64 * DC_WAVES) void k_down_combine(DcArgs a,
 
 static int pick_lpr(int K);
 
+/* one token, layer path: gate/up with the top-k fused in (H/32 a power of
+ * two >= 64, i.e. 64 lanes per weight row); returns -1 when the shape is
+ * not covered */
+template <bool XBF16, int PL>
+static int launch_gateup_topk_pl(const DecArgs &a, int cpl, dim3 grid, const DecRouteOut &ro,
+                                 hipStream_t st) {
+    if (cpl == 1) hipLaunchKernelGGL((k_gateup_dec<64, 1, 2, XBF16, PL>), grid, dim3(256), 0, st, a, nullptr, ro);
+    else if (cpl == 2) hipLaunchKernelGGL((k_gateup_dec<64, 2, 2, XBF16, PL>), grid, dim3(256), 0, st, a, nullptr, ro);
+    else hipLaunchKernelGGL((k_gateup_dec<64, 4, 2, XBF16, PL>), grid, dim3(256), 0, st, a, nullptr, ro);
+    return QK_CHECK_LAUNCH();
+}
+
+extern "C" int qk_gateup_topk_supported(qk_shape s) {
+    const int ch = s.H / 32;
+    return ch >= 64 && ch <= 256 && (ch & (ch - 1)) == 0 && s.E <= 64 * 16 && s.k <= QK_MAX_TOPK;
+}
+
+extern "C" int qk_launch_gateup_topk(const qmoe_layer_weights *W, qk_shape s, const void *x,
+                                     int x_bf16, const float *logits, int32_t *idx, float *w,
+                                     float *sg, int32_t *perm, int32_t *pos, int32_t *segtab,
+                                     float *h, void *stream) {
+    if (!qk_gateup_topk_supported(s)) return (int)hipErrorInvalidValue;
+    DecArgs a;
+    a.q[0] = W->gate_q; a.s[0] = W->gate_s; a.b[0] = W->gate_b;
+    a.q[1] = W->up_q;   a.s[1] = W->up_s;   a.b[1] = W->up_b;
+    a.sq[0] = W->sh_gate_q; a.ss[0] = W->sh_gate_s; a.sb[0] = W->sh_gate_b;
+    a.sq[1] = W->sh_up_q;   a.ss[1] = W->sh_up_s;   a.sb[1] = W->sh_up_b;
+    a.x = x;
+    a.out = h;
+    a.K = s.H;
+    a.N = s.I;
+    a.k = s.k;
+    a.E = s.E;
+    const DecRouteOut ro{logits, idx, w, sg, perm, pos, segtab};
+    const int cpl = s.H / 32 / 64;
+    const int rb = 4 * 1 * 2;
+    const dim3 grid((s.k + 1) * ((s.I + rb - 1) / rb));
+    hipStream_t st = (hipStream_t)stream;
+    int pl = 1;
+    while (pl * 64 < s.E) pl <<= 1;
+#define GT_PL(P) return x_bf16 ? launch_gateup_topk_pl<true, P>(a, cpl, grid, ro, st) \
+                               : launch_gateup_topk_pl<false, P>(a, cpl, grid, ro, st)
+    switch (pl) {
+    case 1: GT_PL(1);
+    case 2: GT_PL(2);
+    case 4: GT_PL(4);
+    case 8: GT_PL(8);
+    default: GT_PL(16);
+    }
+#undef GT_PL
+}
+
 /* LDS bytes of k_down_combine for n tokens, or 0 when the fused path does
  * not apply (too many tokens for one workgroup's LDS) */
 extern "C" size_t qk_down_combine_lds(qk_shape s, int n) {
@@ -500,8 +552,9 @@ static int launch_gateup_dec(const GemvArgs &g, hipStream_t st) {
     const int lpr = ch < 64 ? ch : 64, cpl = ch / lpr;
     const int rb = 4 * (64 / lpr) * 2;
     const dim3 grid((g.k + 1) * ((g.N + rb - 1) / rb));
+    const DecRouteOut none{};
 #define GD_LAUNCH(L, C) \
-    hipLaunchKernelGGL((k_gateup_dec<L, C, 2, XBF16>), grid, dim3(256), 0, st, a, g.segtab)
+    hipLaunchKernelGGL((k_gateup_dec<L, C, 2, XBF16>), grid, dim3(256), 0, st, a, g.segtab, none)
     if (lpr == 64) {
         if (cpl == 1) GD_LAUNCH(64, 1);
         else if (cpl == 2) GD_LAUNCH(64, 2);

@@ -21,6 +21,7 @@
 #define GEMV_DECODE_H
 
 #include "qk_device.h"
+#include "topk_wave.h"
 
 struct DecArgs {
     const uint32_t *q[2];  /* routed gate, up [E, N, K/8] */
@@ -52,8 +53,30 @@ __device__ __forceinline__ void dec_ld_bf16(const uint16_t *p, float v[GPL]) {
     }
 }
 
-template <int LPR, int CPL, int RIT, bool XBF16>
-__global__ __launch_bounds__(256) void k_gateup_dec(DecArgs a, const int32_t *__restrict__ segtab) {
+/* routing outputs written by the fused top-k variant (one workgroup) */
+struct DecRouteOut {
+    const float *logits; /* [E+1]: router logits, then the shared-gate logit */
+    int32_t *idx;        /* [k] */
+    float *w;            /* [k] */
+    float *sg;           /* [1] */
+    int32_t *perm, *pos; /* [k] */
+    int32_t *segtab;     /* [1+3k] */
+};
+
+/*
+ * TK = 0: segment j >= 1 is entry j-1 of `segtab` (any table made by the
+ *         dispatch for one token).
+ * TK = PL > 0: the workgroups of routed segments select the top k of the
+ *         router logits themselves (wave 0, wave_topk<PL>, broadcast through
+ *         LDS) instead of waiting for a separate top-k launch; segment j is
+ *         the j-th smallest selected expert id, at dispatch position j-1.
+ *         Workgroup (segment 1, block 0) writes the routing (idx, w,
+ *         sigmoid gate, perm, pos, segment table) for the down projection
+ *         and the combine, in the form the dispatch produces.
+ */
+template <int LPR, int CPL, int RIT, bool XBF16, int TK = 0>
+__global__ __launch_bounds__(256) void k_gateup_dec(DecArgs a, const int32_t *__restrict__ segtab,
+                                                    DecRouteOut ro) {
     constexpr int RPW = 64 / LPR;
     constexpr int RB = 4 * RPW * RIT;
     constexpr int GPL = CPL >= 2 ? CPL / 2 : 1; /* scale groups per lane */
@@ -82,15 +105,52 @@ __global__ __launch_bounds__(256) void k_gateup_dec(DecArgs a, const int32_t *__
         }
     }
 
-    /* segment entry and count, read together; bitwise tests (no branches) */
     const bool shared = seg == 0;
-    const int s1 = shared ? 1 : seg;
-    const int u = segtab[0];
-    const int e_raw = segtab[3 * s1 - 2], p_raw = segtab[3 * s1 - 1], m_raw = segtab[3 * s1];
-    const bool valid = shared | ((seg <= u) & (e_raw >= 0) & (e_raw < a.E) & (p_raw >= 0) &
-                                 (p_raw < a.k) & (m_raw == 1));
-    const int e = (valid && !shared) ? e_raw : 0;
-    const int p0 = shared ? a.k : p_raw;
+    bool valid;
+    int e, p0;
+    if (TK > 0) {
+        /* fused top-k: the expert of this segment */
+        __shared__ int s_e[QK_MAX_TOPK];
+        if (!shared) {
+            if (wave == 0) {
+                int id;
+                float wt;
+                wave_topk<(TK > 0 ? TK : 1)>(ro.logits, a.E, a.k, lane, id, wt);
+                const int my_id = lane < a.k ? id : 0x7FFFFFFF;
+                int rank = 0;
+                for (int s2 = 0; s2 < a.k; s2++) rank += __builtin_amdgcn_readlane(my_id, s2) < my_id ? 1 : 0;
+                if (lane < a.k) s_e[rank] = id;
+                if (seg == 1 && rb == 0) {
+                    if (lane < a.k) {
+                        ro.idx[lane] = id;
+                        ro.w[lane] = wt;
+                        ro.perm[rank] = lane;
+                        ro.pos[lane] = rank;
+                        ro.segtab[1 + 3 * rank] = id;
+                        ro.segtab[2 + 3 * rank] = rank;
+                        ro.segtab[3 + 3 * rank] = 1;
+                    }
+                    if (lane == 0) {
+                        ro.segtab[0] = a.k;
+                        ro.sg[0] = qk_sigmoid(qk_ld(ro.logits + a.E));
+                    }
+                }
+            }
+            __syncthreads();
+        }
+        valid = true;
+        e = shared ? 0 : s_e[seg - 1];
+        p0 = shared ? a.k : seg - 1;
+    } else {
+        /* segment entry and count, read together; bitwise tests (no branches) */
+        const int s1 = shared ? 1 : seg;
+        const int u = segtab[0];
+        const int e_raw = segtab[3 * s1 - 2], p_raw = segtab[3 * s1 - 1], m_raw = segtab[3 * s1];
+        valid = shared | ((seg <= u) & (e_raw >= 0) & (e_raw < a.E) & (p_raw >= 0) & (p_raw < a.k) &
+                          (m_raw == 1));
+        e = (valid && !shared) ? e_raw : 0;
+        p0 = shared ? a.k : p_raw;
+    }
     const uint32_t *q[2];
     const uint16_t *sc[2], *bi[2];
 #pragma unroll

@@ -632,6 +632,17 @@ int qmoe_layer_forward(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n
     float *xn = W->norm_w ? sc->xn : NULL;
     rc = qk_launch_router(W, s, x, xbf, n, sc->logits, xn, stream);
     if (hip_fail(err, rc, "router")) return -1;
+    const void *xf = W->norm_w ? (const void *)sc->xn : x;
+    const int xf_bf = W->norm_w ? 0 : xbf;
+    if (n == 1 && qk_gateup_topk_supported(s) && qk_down_combine_lds(s, n) > 0) {
+        /* one token: top-k inside the gate/up launch, then down + combine */
+        rc = qk_launch_gateup_topk(W, s, xf, xf_bf, sc->logits, sc->idx, sc->w, sc->sg, sc->perm,
+                                   sc->pos, sc->segtab, sc->h, stream);
+        if (hip_fail(err, rc, "gate/up + top-k")) return -1;
+        rc = qk_launch_down_combine(W, s, sc->h, n, sc->segtab, sc->pos, sc->w, sc->sg,
+                                    (flags & QMOE_RESIDUAL) ? x : NULL, xbf, out, stream);
+        return hip_fail(err, rc, "down+combine");
+    }
     if (n <= QK_SMALL_N && n * s.k <= QK_SMALL_NK) {
         /* offsets are not used by the layer; qmoe_last_routing derives them */
         rc = qk_launch_topk_dispatch_small(s, n, sc->logits, NULL, sc->idx, sc->w, sc->sg,
@@ -645,8 +656,6 @@ int qmoe_layer_forward(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n
                                 sc->bits, sc->wprefix, stream);
         if (hip_fail(err, rc, "dispatch")) return -1;
     }
-    const void *xf = W->norm_w ? (const void *)sc->xn : x;
-    const int xf_bf = W->norm_w ? 0 : xbf;
     if (run_gateup(c, W, xf, xf_bf, n, sc->perm, sc->segtab, sc->h, stream, err)) return -1;
     if (!mfma_usable(c, n) && qk_down_combine_lds(s, n) > 0) {
         rc = qk_launch_down_combine(W, s, sc->h, n, sc->segtab, sc->pos, sc->w, sc->sg,

@@ -92,6 +92,13 @@ int qk_launch_gateup_mfma(const qmoe_layer_weights *W, qk_shape s, const uint16_
                           float *h, void *stream);
 int qk_launch_down_mfma(const qmoe_layer_weights *W, qk_shape s, const float *h, int n,
                         const int32_t *segtab, const int32_t *tasks, float *y, void *stream);
+/* one token, layer path: gate/up with the top-k of `logits` selected inside
+ * the kernel, which also writes idx, w, sg, perm, pos and the segment
+ * table (the form the dispatch produces for one token) */
+int qk_gateup_topk_supported(qk_shape s);
+int qk_launch_gateup_topk(const qmoe_layer_weights *W, qk_shape s, const void *x, int x_bf16,
+                          const float *logits, int32_t *idx, float *w, float *sg, int32_t *perm,
+                          int32_t *pos, int32_t *segtab, float *h, void *stream);
 /* down projection fused with the combine for n <= QK_DC_MAX_N tokens;
  * bit-identical to qk_launch_down + qk_launch_combine.  qk_down_combine_lds
  * returns its LDS bytes, 0 when it does not apply. */

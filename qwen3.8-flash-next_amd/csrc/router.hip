@@ -182,92 +182,7 @@ extern "C" int qk_launch_router(const qmoe_layer_weights *W, qk_shape s, const v
 
 /* ------------------------------------------------------------- top-k */
 
-/* order-preserving map f32 -> u32; -0 is first made +0 so it ties with +0 */
-__device__ __forceinline__ uint32_t qk_ordkey(float v) {
-    uint32_t b = __float_as_uint(v + 0.0f);
-    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-__device__ __forceinline__ float qk_ordkey_value(uint32_t o) {
-    return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
-}
-
-/*
- * One wavefront selects the top k of row[0..E) in canonical order: value
- * descending, ties to the lower expert id, -0 equal to +0.  Lane l holds
- * the PL experts e = l*PL + i (E <= 64*PL) and sorts them descending with
- * an odd-even transposition network; it swaps neighbours only on strict
- * inequality, so equal keys keep ascending e.  Then k rounds: the wave
- * maximum of the lane heads; the lowest lane holding it wins (lane order is
- * e order, so that is the lowest e among equal keys) and pops its head.
- * Round s yields slot s.  Lane s < k returns slot s's expert and weight
- * w_s = exp(v_s - v_0) / sum_j exp(v_j - v_0), summed in slot order
- * (model.c:1305-1318).  Padding entries (e >= E) carry key 0 and valid
- * keys are at least 1, so padding is never chosen while E >= k.
- */
-template <int PL>
-__device__ __forceinline__ void wave_topk(const float *row, int E, int k, int lane, int &my_id,
-                                          float &my_w) {
-    static_assert(PL <= 16, "at most 16 experts per lane");
-    uint32_t kk[PL];
-    int ii[PL]; /* local index i of each sorted entry */
-#pragma unroll
-    for (int i = 0; i < PL; i++) {
-        const int e = lane * PL + i;
-        const float v = qk_ld(row + (e < E ? e : E - 1));
-        kk[i] = e < E ? max(qk_ordkey(v), 1u) : 0u;
-        ii[i] = i;
-    }
-#pragma unroll
-    for (int pass = 0; pass < PL; pass++) {
-#pragma unroll
-        for (int i = pass & 1; i + 1 < PL; i += 2) {
-            const bool sw = kk[i + 1] > kk[i];
-            const uint32_t ka = kk[i], kb = kk[i + 1];
-            const int ia = ii[i], ib = ii[i + 1];
-            kk[i] = sw ? kb : ka;
-            kk[i + 1] = sw ? ka : kb;
-            ii[i] = sw ? ib : ia;
-            ii[i + 1] = sw ? ia : ib;
-        }
-    }
-    /* sorted local indices packed 4 bits each (entries beyond 8 in a second
-     * word), so a pop shifts one or two registers */
-    uint32_t pk0 = 0u, pk1 = 0u;
-#pragma unroll
-    for (int i = 0; i < PL; i++) {
-        if (i < 8) pk0 |= (uint32_t)ii[i] << (4 * i);
-        else pk1 |= (uint32_t)ii[i] << (4 * (i - 8));
-    }
-    uint32_t my_key = 0u;
-    my_id = 0;
-    for (int r = 0; r < k; r++) {
-        const uint32_t m = qk_wave_max_u32(kk[0]);
-        const uint64_t ball = __ballot(kk[0] == m);
-        const int wl = (int)__builtin_ctzll(ball);
-        const int e = wl * PL + (int)(__builtin_amdgcn_readlane((int)pk0, wl) & 15u);
-        if (lane == r) {
-            my_key = m;
-            my_id = e;
-        }
-        if (lane == wl) {
-#pragma unroll
-            for (int i = 0; i + 1 < PL; i++) kk[i] = kk[i + 1];
-            kk[PL - 1] = 0u;
-            if (PL > 8) {
-                pk0 = (pk0 >> 4) | (pk1 << 28);
-                pk1 >>= 4;
-            } else {
-                pk0 >>= 4;
-            }
-        }
-    }
-    const float v = qk_ordkey_value(my_key);
-    const float v0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-    const float ev = lane < k ? expf(v - v0) : 0.0f;
-    float sum = 0.0f;
-    for (int j = 0; j < k; j++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev), j));
-    my_w = ev / sum;
-}
+#include "topk_wave.h"
 
 /* experts per lane for E experts: the power of two >= ceil(E/64) */
 static int topk_pl(int E) {
