@@ -26,9 +26,10 @@ PKG_DIR = os.path.join(ROOT, "qwen3.8-flash-next_amd")
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA
-# symbol of the gate/up GEMV instance that hidden 2048 selects (64 lanes
-# per weight row, one chunk per lane), by activation type
-GATEUP_SYMBOL = {True: "k_q4gemv<2, 64, 1, true>", False: "k_q4gemv<2, 64, 1, false>"}
+# symbol of the one-token gate/up launch (top-k inside) that hidden 2048 and
+# 512 experts select (64 lanes per weight row, one chunk per lane, 8 experts
+# per lane in the top-k), by activation type
+GATEUP_SYMBOL = {True: "k_gateup_dec<64, 1, 2, true, 8>", False: "k_gateup_dec<64, 1, 2, false, 8>"}
 METRIC = "MoE-layer tokens/sec at decode+prefill, 1 MI355X; % HBM BW / % MFMA peak"
 
 
@@ -147,43 +148,34 @@ def bench_layer(pkg, torch, w, n_layers, steps, warmup):
 
 
 def bench_gateup(pkg, torch, st, reps_target=200):
-    """dominant kernel: grouped gate/up GEMV, one launch per step with that
-    step's routing; returns (avg seconds per launch, algorithmic bytes per
-    launch averaged over the steps)"""
+    """dominant kernel of the one-token layer step: the launch that selects
+    the top-k from the router logits and runs the grouped gate/up GEMV
+    (qmoe_expert_gateup_topk, the launch qmoe_layer_forward makes for one
+    token), one launch per resident layer with that layer's router logits;
+    returns (avg seconds per launch, algorithmic bytes per launch averaged
+    over the launches)"""
     w, ctx = st.w, st.ctx
     S = st.L
-    routes = []
+    logits, outs = [], []
     for i in range(S):
-        xin = st.x[i]
-        r = ctx.router(i % st.L, xin)
-        d = ctx.dispatch(r["idx"])
-        routes.append(d)
+        r = ctx.router(i % st.L, st.x[i], want_logits=True)
+        # [E+1]: the router logits, then a shared-gate logit (its value does
+        # not change the work)
+        logits.append(torch.cat([r["logits"][0], torch.zeros(1, device="cuda")]).contiguous())
+        outs.append(ctx.expert_gateup_topk(i % st.L, st.x[i], logits[-1]))
     torch.cuda.synchronize()
-    h = [torch.empty((w.n_tokens * w.top_k + w.n_tokens, w.moe_inter), dtype=torch.float32,
-                     device="cuda") for _ in range(S)]
-    algo = []
     mb = q4_matrix_bytes(w.moe_inter, w.hidden, w.group_size)
     xbytes = w.hidden * (2 if w.x_bf16 else 4)
+    algo = []
     for i in range(S):
-        U = int(routes[i]["segments"][0].item())
-        algo.append((U + 1) * 2 * mb + w.n_tokens * xbytes +
-                    (w.n_tokens * w.top_k + w.n_tokens) * w.moe_inter * 4)
-
-    # the raw entry point writes into the preallocated h buffers, so the
-    # captured graph does no allocation
-    lib = pkg.lib()
-    import ctypes
+        U = int(outs[i]["segments"][0].item())
+        algo.append((U + 1) * 2 * mb + xbytes + (w.n_experts + 1) * 4 +
+                    (w.top_k + 1) * w.moe_inter * 4)
 
     def run_raw():
         stream = torch.cuda.current_stream().cuda_stream
-        err = pkg.QmoeErr()
         for i in range(S):
-            d = routes[i]
-            rc = lib.qmoe_expert_gateup(ctx.handle, i % st.L, st.x[i].data_ptr(),
-                                        pkg.BF16 if w.x_bf16 else pkg.F32, w.n_tokens,
-                                        d["perm"].data_ptr(), d["segments"].data_ptr(),
-                                        h[i].data_ptr(), stream, ctypes.byref(err))
-            assert rc == 0, err.msg
+            ctx.expert_gateup_topk_raw(i % st.L, st.x[i], logits[i], outs[i], stream)
     g = capture(torch, run_raw)
     time_graph(torch, g, 2)
     reps = max(1, math.ceil(reps_target / S))
@@ -281,9 +273,22 @@ def main():
 
     sec_step, steps, warm, st = bench_layer(pkg, torch, w, n_layers, args.steps, args.warmup)
     log(f"{w.name}: {sec_step * 1e6:.2f} us/step over {steps} steps, {n_layers} layers")
-    k_sec, k_bytes = bench_gateup(pkg, torch, st)
-    achieved = k_bytes / k_sec / 1e9
-    log(f"gate/up kernel: {k_sec * 1e6:.2f} us/launch, {k_bytes / 1e6:.2f} MB -> {achieved:.0f} GB/s")
+    roof = None
+    if w.n_tokens == 1:
+        k_sec, k_bytes = bench_gateup(pkg, torch, st)
+        achieved = k_bytes / k_sec / 1e9
+        log(f"gate/up kernel: {k_sec * 1e6:.2f} us/launch, {k_bytes / 1e6:.2f} MB -> {achieved:.0f} GB/s")
+        roof = {
+            "kernel": GATEUP_SYMBOL[w.x_bf16] + " (top-k + grouped gate/up GEMV + SiLU*up, one token)",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic(GATEUP_SYMBOL[w.x_bf16], w.name),
+            "avg_launch_us": round(k_sec * 1e6, 3),
+            "algorithmic_bytes_per_launch": int(k_bytes),
+        }
     value = w.n_tokens / sec_step
     layer_bytes = (10 + 1) * expert_bytes(w) + w.n_experts * w.hidden * 2 + w.hidden * 2
 
@@ -332,17 +337,7 @@ def main():
             "device": dev,
             "extra": extra,
         },
-        "roofline": {
-            "kernel": GATEUP_SYMBOL[w.x_bf16] + " (grouped gate/up GEMV + SiLU*up)",
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(GATEUP_SYMBOL[w.x_bf16], w.name),
-            "avg_launch_us": round(k_sec * 1e6, 3),
-            "algorithmic_bytes_per_launch": int(k_bytes),
-        },
+        "roofline": roof,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -174,6 +174,20 @@ int qmoe_expert_gateup(qmoe_ctx *ctx, int layer, const void *x, int x_dtype, int
                        qmoe_err *err);
 int qmoe_expert_down(qmoe_ctx *ctx, int layer, const float *h, int n, const int32_t *segments,
                      float *y_out, void *stream, qmoe_err *err);
+
+/* (2+3) One token (decode): top-k, renormalisation, dispatch and gate/up in
+ *   one launch; model.c:1303-1375 for n = 1.  This is the launch
+ *   qmoe_layer_forward uses for one token when hidden/32 is a power of two
+ *   >= 64.  logits [E+1] f32: the router output before top-k, i.e.
+ *   x.Wr^T (+ router_bias) for the E experts followed by the shared-expert
+ *   gate logit x.w_sg.  Outputs, as qmoe_router + qmoe_dispatch +
+ *   qmoe_expert_gateup would give them for n = 1: idx_out [k], w_out [k],
+ *   shared_gate_out [1], perm_out [k], segments_out [1+3k], h_out [k+1, I].
+ *   Returns -1 for other shapes (use the separate stages). */
+int qmoe_expert_gateup_topk(qmoe_ctx *ctx, int layer, const void *x, int x_dtype,
+                            const float *logits, int32_t *idx_out, float *w_out,
+                            float *shared_gate_out, int32_t *perm_out, int32_t *segments_out,
+                            float *h_out, void *stream, qmoe_err *err);
 /* both of the above */
 int qmoe_expert_ffn(qmoe_ctx *ctx, int layer, const void *x, int x_dtype, int n,
                     const int32_t *perm, const int32_t *segments, float *y_out, void *stream,

@@ -568,6 +568,32 @@ int qmoe_expert_gateup(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n
                       stream, err);
 }
 
+int qmoe_expert_gateup_topk(qmoe_ctx *c, int layer, const void *x, int x_dtype,
+                            const float *logits, int32_t *idx_out, float *w_out,
+                            float *shared_gate_out, int32_t *perm_out, int32_t *segments_out,
+                            float *h_out, void *stream, qmoe_err *err) {
+    clear_err(err);
+    if (check_call(c, layer, 1, err) || check_dtype(x_dtype, err)) return -1;
+    if (!qk_gateup_topk_supported(c->shape)) {
+        set_err(err, "one-token gate/up with top-k needs hidden/32 a power of two >= 64 (hidden = %d)",
+                c->cfg.hidden);
+        return -1;
+    }
+    NEED(x, "x");
+    NEED(logits, "logits");
+    NEED(idx_out, "idx_out");
+    NEED(w_out, "w_out");
+    NEED(shared_gate_out, "shared_gate_out");
+    NEED(perm_out, "perm_out");
+    NEED(segments_out, "segments_out");
+    NEED(h_out, "h_out");
+    return hip_fail(err, qk_launch_gateup_topk(&c->layers[layer].dev, c->shape, x,
+                                               x_dtype == QMOE_BF16, logits, idx_out, w_out,
+                                               shared_gate_out, perm_out, c->sc.pos, segments_out,
+                                               h_out, stream),
+                    "gate/up + top-k");
+}
+
 int qmoe_expert_down(qmoe_ctx *c, int layer, const float *h, int n, const int32_t *segments,
                      float *y_out, void *stream, qmoe_err *err) {
     clear_err(err);

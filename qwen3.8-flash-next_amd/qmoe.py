@@ -71,6 +71,8 @@ SIGNATURES = {
     "qmoe_dispatch": (_I, [_P, _P, _I, _P, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_expert_gateup": (_I, [_P, _I, _P, _I, _I, _P, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_expert_down": (_I, [_P, _I, _P, _I, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_expert_gateup_topk": (_I, [_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P,
+                                     ctypes.POINTER(QmoeErr)]),
     "qmoe_expert_ffn": (_I, [_P, _I, _P, _I, _I, _P, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_combine": (_I, [_P, _P, _P, _P, _P, _I, _P, _I, _P, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_layer_forward": (_I, [_P, _I, _P, _I, _I, _P, _I, _P, ctypes.POINTER(QmoeErr)]),
@@ -303,6 +305,31 @@ class MoeContext:
                                         _ptr(d["segments"]), _ptr(h), _stream(stream),
                                         ctypes.byref(err)), err, "qmoe_expert_gateup")
         return h
+
+    def expert_gateup_topk(self, layer, x, logits, stream=None):
+        """one token: top-k of `logits` ([E+1]: router logits, then the
+        shared-expert gate logit), dispatch and gate/up in one launch"""
+        import torch
+        dev = x.device
+        k = self.k
+        out = dict(idx=torch.empty((1, k), dtype=torch.int32, device=dev),
+                   w=torch.empty((1, k), dtype=torch.float32, device=dev),
+                   shared_gate=torch.empty((1,), dtype=torch.float32, device=dev),
+                   perm=torch.empty((k,), dtype=torch.int32, device=dev),
+                   segments=torch.zeros((3 * self.E + 1,), dtype=torch.int32, device=dev),
+                   h=torch.empty((k + 1, self.I), dtype=torch.float32, device=dev))
+        self.expert_gateup_topk_raw(layer, x, logits, out, stream)
+        return out
+
+    def expert_gateup_topk_raw(self, layer, x, logits, out, stream=None):
+        """as expert_gateup_topk, into preallocated buffers (graph capture)"""
+        err = QmoeErr()
+        _check(lib().qmoe_expert_gateup_topk(self._h, layer, _ptr(x), _dtype_code(x), _ptr(logits),
+                                             _ptr(out["idx"]), _ptr(out["w"]),
+                                             _ptr(out["shared_gate"]), _ptr(out["perm"]),
+                                             _ptr(out["segments"]), _ptr(out["h"]),
+                                             _stream(stream), ctypes.byref(err)), err,
+               "qmoe_expert_gateup_topk")
 
     def expert_down(self, layer, h, n, d, stream=None):
         import torch

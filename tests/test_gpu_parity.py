@@ -290,6 +290,38 @@ def test_stages_compose_to_layer(torch_dev, n, residual):
         assert torch.equal(out, full)
 
 
+def test_gateup_topk_one_token(torch_dev):
+    """one-token launch that selects the top-k itself: same routing as the
+    oracle (bit-exact ids, dispatch), and the same h as router -> dispatch ->
+    expert_gateup"""
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    w = pkg.WORKLOADS["batched"]
+    say("case: one-token gate/up with in-kernel top-k (decode shape, Zipf bias)")
+    rb = orc.zipf_bias(w.n_experts, w.zipf_s, w.zipf_scale, 0)
+    for seed in (3, 4):
+        x = orc.gen_x(1, w.hidden, seed, bf16=True)
+        L = orc.Layer(w.hidden, w.n_experts, w.top_k, w.moe_inter, seed=w.seed, router_bias=rb,
+                      only_experts=[])
+        rt = L.route(x, True)
+        logits = np.concatenate([rt["logits"][0], rt["gate_logit"]]).astype(np.float32)
+        dref = orc.dispatch(rt["idx"], w.n_experts)
+        with pkg.MoeContext.for_workload(w, max_tokens=1) as ctx:
+            ctx.synth_layer(0, w.seed, router_bias=rb)
+            xt = to_dev(x, torch, dev)
+            got = ctx.expert_gateup_topk(0, xt, to_dev(logits, torch, dev))
+            st = ctx.router(0, xt)
+            d = ctx.dispatch(st["idx"])
+            h = ctx.expert_gateup(0, xt, d)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(got["idx"].cpu().numpy(), rt["idx"])
+            np.testing.assert_allclose(got["w"].cpu().numpy(), rt["w"], rtol=1e-6)
+            np.testing.assert_allclose(got["shared_gate"].cpu().numpy(), rt["shared_gate"], rtol=1e-6)
+            np.testing.assert_array_equal(got["perm"].cpu().numpy(), dref["perm"])
+            check_segments(got["segments"].cpu().numpy(), dref)
+            assert torch.equal(got["h"], h)
+
+
 def test_combine_skips_undispatched_slots(torch_dev):
     """slots whose expert id is invalid are left out of the dispatch; the
     combine must then add nothing for them (several such slots share one
