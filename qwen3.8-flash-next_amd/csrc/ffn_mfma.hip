@@ -1,311 +1,378 @@
 /*
- * ffn_mfma.hip -- grouped expert GEMM on bf16 MFMA for prefill-shaped
- * segments (many tokens per expert).  Same arithmetic contract as the GEMV
- * path (ffn_gemv.hip) and as gemm_q4 in the reference (kernel.c:239-246,
- * 279-282): per 64-column group, MFMA accumulates x * (128 + q) exactly from
- * bf16 activations and integer codes, and an fp32 epilogue applies
- *     acc += s * (D - 128 * sum(x)) + b * sum(x).
- * Weights are never rounded: codes are exact in bf16, scales/biases enter
- * only the fp32 epilogue.
+ * ffn_mfma.hip -- grouped expert GEMM on bf16 MFMA (v_mfma_f32_16x16x32_bf16)
+ * for segments with many rows (prefill, batched decode).  Same arithmetic
+ * contract as the GEMV path (ffn_gemv.hip) and as gemm_q4 in the reference
+ * (kernel.c:239-246, 279-282): per 64-column group g the exact integer-code
+ * products are accumulated and the affine terms are applied in fp32,
+ *     y = sum_g s_g * (sum_k x_k q_k) + sum_g b_g * X_g,   X_g = sum_k x_k.
  *
- * Tiles.  A task is (segment, chunk of up to 128 rows of that segment, tile
- * of 128 output columns).  The workgroup's 4 waves split the columns (32
- * each); every wave runs all row subtiles (32 rows each) of the chunk.  The
- * activation rows (gathered through the dispatch permutation) are staged
- * per 64-column group in LDS, double buffered, already in the (x_i, x_{i+4})
- * pair order that matches the code-word pairs.
+ * Operands.  Codes enter MFMA exactly as the bf16 numbers 128+q
+ * (qk_codes_to_pairs); activations enter as bf16 planes in (x_i, x_{i+4})
+ * pair order per 8 columns -- one plane for bf16 input, hi + lo planes for
+ * f32 (x = hi + lo to 2^-17) -- written by k_pack_rows together with
+ * P_g = -128 * X_g per row and group.  For one group the accumulator is
+ * initialised with P_g (the MFMA C operand), so the two K-steps leave
+ *     t = sum_k x_k (128 + q_k) - 128 X_g = sum_k x_k q_k
+ * and one fp32 FMA per output adds s_g * t.  The bias term sum_g b_g X_g
+ * is a K = G product done once per tile on MFMA: b is exact in bf16 and
+ * X_g = P_g / -128 is split into bf16 hi + lo.  Weights are never rounded.
  *
- * v_mfma_f32_32x32x16_bf16 lane layout (probed on gfx950): A lane l holds
- * row l%32, B lane l column l%32, both with K elements [8*(l/32), +8); D
- * lane l holds column l%32, rows 8*(r/4) + 4*(l/32) + (r%4), r = 0..15.
+ * Tiles.  A task is (segment, chunk of up to MM_BM rows); the grid is tasks
+ * x column tiles.  The workgroup's 4 waves each own 4 column tiles of 16
+ * (gate/up: 32 columns of Wg and the same 32 of Wu, so h = silu(g)*u is
+ * formed in registers; down: 64 columns of Wd) and every 16-row tile of
+ * the chunk.  Per group the chunk's activation rows are staged in LDS
+ * (double buffered, XOR-swizzled 16-byte chunks), the code words come from
+ * a register ring MM_WD groups ahead, and the scales of the whole tile sit
+ * in LDS.  The kernel body is specialised on the number of 16-row tiles.
  *
- * Gate/up: columns are rows of Wg and Wu; each wave holds both for the same
- * output column, so h = silu(g) * u is formed in registers.
- * Down:    the A operand is h (f32), split into bf16 hi + lo terms that
- *          accumulate into the same group result.
+ * 16x16x32 lane layout: A lane l holds row l%16, B lane l column l%16, both
+ * with K elements [8*(l/16), +8); D lane l holds column l%16, rows
+ * 4*(l/16) + i.  Here the K-step j of a group gives lane quarter kq the code
+ * word 2*kq + j of the group (8 columns), and the A chunk with the same
+ * columns, so one 8-byte load per lane fetches both K-steps' codes.
  */
 #include "qk_device.h"
 
-typedef __bf16 qk_bf16x8 __attribute__((ext_vector_type(8)));
-typedef float qk_f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 qm_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float qm_f32x4 __attribute__((ext_vector_type(4)));
 
-#define MM_BM 128     /* rows per chunk */
-#define MM_MSUB 4     /* 32-row subtiles per chunk */
-#define MM_BN 128     /* output columns per tile (32 per wave) */
-#define MM_ROWB 144   /* LDS bytes per staged row of one term (128 B data + pad) */
+#define MM_MT 6              /* 16-row tiles per chunk */
+#define MM_BM (16 * MM_MT)   /* rows per chunk */
+#define MM_WD 2              /* code-word prefetch depth, groups */
+#define MM_TASK_HDR 4        /* int32 header before the int4 task entries */
 
-struct MfmaArgs {
-    const uint32_t *q[2];  /* routed [E, N, K/8]: gate, up (or down, down) */
+struct MmArgs {
+    const uint32_t *q[2]; /* routed [E, N, K/8]: gate, up (down: both Wd) */
     const uint16_t *s[2], *b[2];
     const uint32_t *sq[2]; /* shared expert [N, K/8] */
     const uint16_t *ss[2], *sb[2];
-    const void *x;         /* gate/up: bf16 [n, K] tokens; down: f32 [n*k+n, K] rows */
-    float *out;            /* [n*k+n, N] */
-    const int32_t *perm, *segtab, *tasks;
-    int K, N, n, k, E;
-    int ntile;             /* N / MM_BN */
+    const uint16_t *ap[2]; /* activation planes [rows, K] (hi, lo) */
+    const float *ag;       /* [rows, G]: -128 * group sums */
+    float *out;            /* gate/up: h [n*k+n, N]; down: y [n*k+n, N] */
+    const int32_t *perm;   /* gate/up: dispatch permutation */
+    const int32_t *tasks;
+    int K, N, n, k, ntile;
 };
 
-__device__ __forceinline__ qk_bf16x8 qk_as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-    const uint4 v = make_uint4(a, b, c, d);
-    return __builtin_bit_cast(qk_bf16x8, v);
-}
+template <int TERMS, int MAXG>
+struct MmSmem {
+    uint4 a[2][TERMS][MM_BM * 8];
+    float p[2][MM_BM];
+    uint16_t s[MAXG][4][16][4]; /* [group][wave][column][tile] */
+    int row[MM_BM];
+};
 
-/* one code word -> the B operand (128+q as bf16, pair order) */
-__device__ __forceinline__ qk_bf16x8 qk_codes_operand(uint32_t w) {
+__device__ __forceinline__ qm_bf16x8 qm_codes(uint32_t w) {
     uint32_t p[4];
     qk_codes_to_pairs(w, p);
-    return qk_as_bf16x8(p[0], p[1], p[2], p[3]);
+    return __builtin_bit_cast(qm_bf16x8, make_uint4(p[0], p[1], p[2], p[3]));
 }
 
-/* 8 bf16 activations in natural order -> pair order */
-__device__ __forceinline__ uint4 qk_pair_order(uint4 d) {
-    uint32_t p[4];
-    qk_bf16x8_to_pairs(d, p);
-    return make_uint4(p[0], p[1], p[2], p[3]);
-}
-
-/*
- * DOWN = false: gate/up (NMAT 2, activations bf16 tokens, output silu(g)*u)
- * DOWN = true : down    (NMAT 1, activations f32 rows by dispatch position,
- *                        hi/lo terms, output y)
- */
+/* column of tile ct for this lane: gate/up tiles 0,1 = gate, 2,3 = up */
 template <bool DOWN>
-__global__ __launch_bounds__(256, 1) void k_mfma(MfmaArgs a) {
-    constexpr int NMAT = DOWN ? 1 : 2;
-    constexpr int TERMS = DOWN ? 2 : 1;
-    __shared__ __attribute__((aligned(16))) uint8_t s_x[2][TERMS][MM_BM * MM_ROWB];
-    __shared__ float s_xs[2][MM_BM];
-    __shared__ int s_row[MM_BM];
+__device__ __forceinline__ int mm_col(int nt, int wave, int ct, int c) {
+    return DOWN ? nt * 256 + 64 * wave + 16 * ct + c : nt * 128 + 32 * wave + 16 * (ct & 1) + c;
+}
 
-    /* task decode: consecutive column tiles of one chunk go to one XCD
-     * (workgroups are dealt round-robin over the 8 XCDs) */
+template <bool DOWN, int TERMS, int MAXG, int MS>
+__device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, MAXG> &sm, int e, int p0,
+                                        int mstart, int mrows, int nt) {
+    constexpr int ACH = (MM_BM * 8 + 255) / 256; /* staged 16-byte chunks per thread */
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c = lane & 15, kq = lane >> 4;
+    const int G = a.K >> 6;
+    const size_t wrow = (size_t)a.K >> 3;
+    const bool shared = e < 0;
+
+    const uint32_t *wq[4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ct++) {
+        const int mat = DOWN ? 0 : ct >> 1;
+        const uint32_t *base = shared ? a.sq[mat] : a.q[mat] + (size_t)e * a.N * wrow;
+        wq[ct] = base + (size_t)mm_col<DOWN>(nt, wave, ct, c) * wrow + 2 * kq;
+    }
+    /* scales of the tile: thread -> (wave', tile', column') */
+    {
+        const int w2 = tid >> 6, ct2 = (tid >> 4) & 3, c2 = tid & 15;
+        const int mat = DOWN ? 0 : ct2 >> 1;
+        const uint16_t *sp = (shared ? a.ss[mat] : a.s[mat] + (size_t)e * a.N * G) +
+                             (size_t)mm_col<DOWN>(nt, w2, ct2, c2) * G;
+        for (int g8 = 0; g8 < G; g8 += 8) {
+            const uint4 v = qk_ld((const uint4 *)(sp + g8));
+            const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                sm.s[g8 + 2 * j][w2][c2][ct2] = (uint16_t)(wv[j] & 0xFFFFu);
+                sm.s[g8 + 2 * j + 1][w2][c2][ct2] = (uint16_t)(wv[j] >> 16);
+            }
+        }
+    }
+    __syncthreads(); /* sm.row (written by the caller) and sm.s */
+
+    uint4 ar[TERMS][ACH];
+    float pr = 0.0f;
+    auto load_a = [&](int g) {
+#pragma unroll
+        for (int i = 0; i < ACH; i++) {
+            const int ci = tid + 256 * i;
+            if (ci < MM_BM * 8) {
+                const size_t off = (size_t)sm.row[ci >> 3] * a.K + g * 64 + (ci & 7) * 8;
+#pragma unroll
+                for (int tm = 0; tm < TERMS; tm++) ar[tm][i] = qk_ld((const uint4 *)(a.ap[tm] + off));
+            }
+        }
+        if (tid < MM_BM) pr = qk_ld(a.ag + (size_t)sm.row[tid] * G + g);
+    };
+    auto store_a = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < ACH; i++) {
+            const int ci = tid + 256 * i;
+            if (ci < MM_BM * 8) {
+                const int row = ci >> 3, kc = ci & 7;
+#pragma unroll
+                for (int tm = 0; tm < TERMS; tm++) sm.a[buf][tm][row * 8 + (kc ^ (row & 7))] = ar[tm][i];
+            }
+        }
+        if (tid < MM_BM) sm.p[buf][tid] = pr;
+    };
+
+    uint2 wr[MM_WD][4];
+    auto load_w = [&](int slot, int g) {
+#pragma unroll
+        for (int ct = 0; ct < 4; ct++) wr[slot][ct] = qk_ld((const uint2 *)(wq[ct] + 8 * g));
+    };
+
+    qm_f32x4 acc[MS][4];
+#pragma unroll
+    for (int rt = 0; rt < MS; rt++)
+#pragma unroll
+        for (int ct = 0; ct < 4; ct++) acc[rt][ct] = qm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+#pragma unroll
+    for (int u = 0; u < MM_WD; u++)
+        if (u < G) load_w(u, u);
+    load_a(0);
+    store_a(0);
+    if (G > 1) load_a(1);
+    __syncthreads();
+
+    for (int g0 = 0; g0 < G; g0 += MM_WD) {
+#pragma unroll
+        for (int u = 0; u < MM_WD; u++) {
+            const int g = g0 + u;
+            if (g < G) {
+                const int buf = g & 1;
+                /* buffer buf^1 was last read in group g-1, before the barrier ending it */
+                if (g + 1 < G) store_a(buf ^ 1);
+                if (g + 2 < G) load_a(g + 2);
+                qm_bf16x8 bop[4][2];
+#pragma unroll
+                for (int ct = 0; ct < 4; ct++) {
+                    bop[ct][0] = qm_codes(wr[u][ct].x);
+                    bop[ct][1] = qm_codes(wr[u][ct].y);
+                }
+                if (g + MM_WD < G) load_w(u, g + MM_WD);
+                const uint2 sv = *(const uint2 *)&sm.s[g][wave][c][0];
+                const float sc[4] = {qk_bf16_lo(sv.x), qk_bf16_hi(sv.x), qk_bf16_lo(sv.y), qk_bf16_hi(sv.y)};
+                /* LDS reads run one row tile ahead with one activation plane;
+                 * with two the registers are not there */
+                constexpr int PF = TERMS == 1 ? 2 : 1;
+                qm_bf16x8 A[PF][TERMS][2];
+                qm_f32x4 xi[PF];
+                auto lds_a = [&](int rt, int sl) {
+                    xi[sl] = *(const qm_f32x4 *)&sm.p[buf][16 * rt + 4 * kq];
+                    const int row = 16 * rt + c;
+#pragma unroll
+                    for (int tm = 0; tm < TERMS; tm++)
+#pragma unroll
+                        for (int j = 0; j < 2; j++)
+                            A[sl][tm][j] = __builtin_bit_cast(qm_bf16x8, sm.a[buf][tm][row * 8 + ((2 * kq + j) ^ (c & 7))]);
+                };
+                if (PF == 2) lds_a(0, 0);
+#pragma unroll
+                for (int rt = 0; rt < MS; rt++) {
+                    const int sl = PF == 2 ? rt & 1 : 0;
+                    if (PF == 1) lds_a(rt, 0);
+                    else if (rt + 1 < MS) lds_a(rt + 1, (rt + 1) & (PF - 1));
+                    qm_f32x4 t[4];
+#pragma unroll
+                    for (int ct = 0; ct < 4; ct++)
+                        t[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[sl][0][0], bop[ct][0], xi[sl], 0, 0, 0);
+#pragma unroll
+                    for (int tm = 0; tm < TERMS; tm++)
+#pragma unroll
+                        for (int j = 0; j < 2; j++) {
+                            if (tm == 0 && j == 0) continue;
+#pragma unroll
+                            for (int ct = 0; ct < 4; ct++)
+                                t[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[sl][tm][j], bop[ct][j], t[ct], 0, 0, 0);
+                        }
+#pragma unroll
+                    for (int ct = 0; ct < 4; ct++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++) acc[rt][ct][i] = fmaf(sc[ct], t[ct][i], acc[rt][ct][i]);
+                }
+                __syncthreads();
+            }
+        }
+    }
+
+    /* bias term: acc += sum_g b[col][g] * X[row][g], X = P / -128 as bf16 hi + lo */
+    for (int k0 = 0; k0 < G; k0 += 32) {
+        const int gk = k0 + 8 * kq;
+        qm_bf16x8 bb[4];
+#pragma unroll
+        for (int ct = 0; ct < 4; ct++) {
+            const int mat = DOWN ? 0 : ct >> 1;
+            const uint16_t *bp = (shared ? a.sb[mat] : a.b[mat] + (size_t)e * a.N * G) +
+                                 (size_t)mm_col<DOWN>(nt, wave, ct, c) * G;
+            const uint4 v = gk < G ? qk_ld((const uint4 *)(bp + gk)) : make_uint4(0, 0, 0, 0);
+            bb[ct] = __builtin_bit_cast(qm_bf16x8, v);
+        }
+#pragma unroll
+        for (int rt = 0; rt < MS; rt++) {
+            float xv[8];
+            if (gk < G) {
+                const float *src = a.ag + (size_t)sm.row[16 * rt + c] * G + gk;
+                const float4 v0 = qk_ld((const float4 *)src), v1 = qk_ld((const float4 *)(src + 4));
+                xv[0] = v0.x; xv[1] = v0.y; xv[2] = v0.z; xv[3] = v0.w;
+                xv[4] = v1.x; xv[5] = v1.y; xv[6] = v1.z; xv[7] = v1.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; j++) xv[j] = 0.0f;
+            }
+            uint32_t hi[4], lo[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float x0 = xv[2 * j] * (-1.0f / 128.0f), x1 = xv[2 * j + 1] * (-1.0f / 128.0f);
+                hi[j] = qk_cvt_pk_bf16(x0, x1);
+                lo[j] = qk_cvt_pk_bf16(x0 - qk_bf16_lo(hi[j]), x1 - qk_bf16_hi(hi[j]));
+            }
+            const qm_bf16x8 AH = __builtin_bit_cast(qm_bf16x8, make_uint4(hi[0], hi[1], hi[2], hi[3]));
+            const qm_bf16x8 AL = __builtin_bit_cast(qm_bf16x8, make_uint4(lo[0], lo[1], lo[2], lo[3]));
+#pragma unroll
+            for (int ct = 0; ct < 4; ct++) {
+                acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(AH, bb[ct], acc[rt][ct], 0, 0, 0);
+                acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(AL, bb[ct], acc[rt][ct], 0, 0, 0);
+            }
+        }
+    }
+
+    /* store rows of this chunk */
+#pragma unroll
+    for (int rt = 0; rt < MS; rt++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int row = 16 * rt + 4 * kq + i;
+            if (row < mrows) {
+                float *o = a.out + (size_t)(p0 + mstart + row) * a.N;
+                if (DOWN) {
+#pragma unroll
+                    for (int ct = 0; ct < 4; ct++) qk_st(o + mm_col<true>(nt, wave, ct, c), acc[rt][ct][i]);
+                } else {
+#pragma unroll
+                    for (int h2 = 0; h2 < 2; h2++)
+                        qk_st(o + mm_col<false>(nt, wave, h2, c), qk_silu(acc[rt][h2][i]) * acc[rt][2 + h2][i]);
+                }
+            }
+        }
+    }
+}
+
+template <bool DOWN, int TERMS>
+__global__ __launch_bounds__(256, 2) void k_mm(MmArgs a) {
+    constexpr int MAXG = TERMS == 1 ? 64 : 32;
+    __shared__ __attribute__((aligned(16))) MmSmem<TERMS, MAXG> sm;
+    /* consecutive column tiles of one task go to one XCD (workgroups are
+     * dealt round-robin over the 8 XCDs), so they share its L2 */
     const int L = blockIdx.x;
     const int per_xcd = gridDim.x >> 3;
     const int lin = (L & 7) * per_xcd + (L >> 3);
-    const int ntask = qk_ld(a.tasks);
     const int mt = lin / a.ntile, nt = lin - mt * a.ntile;
-    if (mt >= ntask) return;
-    const int2 tk = qk_ld((const int2 *)(a.tasks + 2) + mt);
-    const int seg = tk.x, chunk = tk.y;
-    int e = -1, p0, m;
-    if (seg == 0) {
-        p0 = a.n * a.k;
-        m = a.n;
-    } else {
-        e = qk_ld(a.segtab + 3 * seg - 2);
-        p0 = qk_ld(a.segtab + 3 * seg - 1);
-        m = qk_ld(a.segtab + 3 * seg);
-    }
-    const int mstart = chunk * MM_BM;
+    if (mt >= qk_ld(a.tasks)) return;
+    const int4 tk = qk_ld((const int4 *)(a.tasks + MM_TASK_HDR) + mt);
+    const int e = tk.x, p0 = tk.y, m = tk.z, mstart = tk.w * MM_BM;
     const int mrows = min(MM_BM, m - mstart);
     if (mrows <= 0) return;
-    const int msub = (mrows + 31) >> 5;
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int c = lane & 31, g = lane >> 5;
-    const int G = a.K >> 6;
-
-    /* staged row i -> source row of the activations */
+    const int tid = threadIdx.x;
     if (tid < MM_BM) {
+        /* activation row of chunk row tid (rows past the end repeat the last) */
         const int i = min(tid, mrows - 1);
         int r;
         if (DOWN) r = p0 + mstart + i;
-        else if (seg == 0) r = mstart + i;
+        else if (e < 0) r = mstart + i;
         else r = qk_ld(a.perm + p0 + mstart + i) / a.k;
-        s_row[tid] = r;
+        sm.row[tid] = r;
     }
-
-    /* weight rows of this lane: column n of the tile */
-    const int n = nt * MM_BN + wave * 32 + c;
-    const uint32_t *wq[NMAT];
-    const uint16_t *ws[NMAT], *wb[NMAT];
-    const size_t wrow = (size_t)a.K >> 3;
-#pragma unroll
-    for (int mt2 = 0; mt2 < NMAT; mt2++) {
-        if (seg == 0) {
-            wq[mt2] = a.sq[mt2] + (size_t)n * wrow;
-            ws[mt2] = a.ss[mt2] + (size_t)n * G;
-            wb[mt2] = a.sb[mt2] + (size_t)n * G;
-        } else {
-            wq[mt2] = a.q[mt2] + ((size_t)e * a.N + n) * wrow;
-            ws[mt2] = a.s[mt2] + ((size_t)e * a.N + n) * G;
-            wb[mt2] = a.b[mt2] + ((size_t)e * a.N + n) * G;
-        }
-    }
-    __syncthreads();
-
-    /* staging thread map: row si = tid/2, half sh = tid&1 (32 columns) */
-    const int si = tid >> 1, sh = tid & 1;
-    const int srow = s_row[si];
-
-    /* raw activations of one group for this thread */
-    uint4 xr_b[4];  /* bf16: 32 values */
-    float4 xr_f[8]; /* f32: 32 values */
-    auto load_x = [&](int gi) {
-        if (DOWN) {
-            const float4 *src = (const float4 *)((const float *)a.x + (size_t)srow * a.K + gi * 64 + sh * 32);
-#pragma unroll
-            for (int j = 0; j < 8; j++) xr_f[j] = qk_ld(src + j);
-        } else {
-            const uint4 *src = (const uint4 *)((const uint16_t *)a.x + (size_t)srow * a.K + gi * 64 + sh * 32);
-#pragma unroll
-            for (int j = 0; j < 4; j++) xr_b[j] = qk_ld(src + j);
-        }
-    };
-    /* convert + store one group into LDS buffer `buf`, with the row sum */
-    auto stage_x = [&](int buf) {
-        float sum = 0.0f;
-        uint8_t *dst0 = &s_x[buf][0][si * MM_ROWB + sh * 64];
-        if (DOWN) {
-            uint8_t *dst1 = &s_x[buf][TERMS - 1][si * MM_ROWB + sh * 64];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float v[8] = {xr_f[2 * j].x, xr_f[2 * j].y, xr_f[2 * j].z, xr_f[2 * j].w,
-                                    xr_f[2 * j + 1].x, xr_f[2 * j + 1].y, xr_f[2 * j + 1].z,
-                                    xr_f[2 * j + 1].w};
-                uint32_t hi[4], lo[4];
-                qk_f32x8_to_pairs(v, hi, lo, sum);
-                *(uint4 *)(dst0 + 16 * j) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-                *(uint4 *)(dst1 + 16 * j) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint4 d = xr_b[j];
-                sum += (qk_bf16_lo(d.x) + qk_bf16_hi(d.x)) + (qk_bf16_lo(d.y) + qk_bf16_hi(d.y)) +
-                       (qk_bf16_lo(d.z) + qk_bf16_hi(d.z)) + (qk_bf16_lo(d.w) + qk_bf16_hi(d.w));
-                *(uint4 *)(dst0 + 16 * j) = qk_pair_order(d);
-            }
-        }
-        sum += qk_dpp<QK_DPP_XOR1>(sum); /* the other half of the row */
-        if (sh == 0) s_xs[buf][si] = sum;
-    };
-
-    /* weights of one group: this lane's 4 code words + scale/bias */
-    uint4 bq[NMAT];
-    uint16_t bs[NMAT], bb[NMAT];
-    auto load_w = [&](int gi) {
-#pragma unroll
-        for (int mt2 = 0; mt2 < NMAT; mt2++) {
-            bq[mt2] = qk_ld((const uint4 *)(wq[mt2] + gi * 8 + g * 4));
-            bs[mt2] = qk_ld(ws[mt2] + gi);
-            bb[mt2] = qk_ld(wb[mt2] + gi);
-        }
-    };
-
-    qk_f32x16 acc[NMAT][MM_MSUB];
-#pragma unroll
-    for (int mt2 = 0; mt2 < NMAT; mt2++)
-#pragma unroll
-        for (int ms = 0; ms < MM_MSUB; ms++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[mt2][ms][r] = 0.0f;
-
-    load_x(0);
-    load_w(0);
-    stage_x(0);
-    __syncthreads();
-    for (int gi = 0; gi < G; gi++) {
-        const int buf = gi & 1;
-        /* this group's weights into registers; prefetch the next group */
-        uint4 cq[NMAT];
-        float cs[NMAT], cb[NMAT];
-#pragma unroll
-        for (int mt2 = 0; mt2 < NMAT; mt2++) {
-            cq[mt2] = bq[mt2];
-            cs[mt2] = qk_bf16(bs[mt2]);
-            cb[mt2] = qk_bf16(bb[mt2]);
-        }
-        if (gi + 1 < G) {
-            load_x(gi + 1);
-            load_w(gi + 1);
-        }
-        qk_bf16x8 bop[NMAT][4];
-#pragma unroll
-        for (int mt2 = 0; mt2 < NMAT; mt2++) {
-            bop[mt2][0] = qk_codes_operand(cq[mt2].x);
-            bop[mt2][1] = qk_codes_operand(cq[mt2].y);
-            bop[mt2][2] = qk_codes_operand(cq[mt2].z);
-            bop[mt2][3] = qk_codes_operand(cq[mt2].w);
-        }
-#pragma unroll
-        for (int ms = 0; ms < MM_MSUB; ms++) {
-            if (ms < msub) {
-                qk_f32x16 t[NMAT];
-#pragma unroll
-                for (int mt2 = 0; mt2 < NMAT; mt2++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) t[mt2][r] = 0.0f;
-#pragma unroll
-                for (int tm = 0; tm < TERMS; tm++) {
-                    const uint8_t *arow = &s_x[buf][tm][(32 * ms + c) * MM_ROWB];
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const uint4 av = *(const uint4 *)(arow + (4 * g + j) * 16);
-                        const qk_bf16x8 aop = __builtin_bit_cast(qk_bf16x8, av);
-#pragma unroll
-                        for (int mt2 = 0; mt2 < NMAT; mt2++)
-                            t[mt2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aop, bop[mt2][j], t[mt2], 0, 0, 0);
-                    }
-                }
-                /* group epilogue: acc += s*(D - 128*xs) + b*xs */
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = 32 * ms + 8 * (r >> 2) + 4 * g + (r & 3);
-                    const float xs = s_xs[buf][row];
-#pragma unroll
-                    for (int mt2 = 0; mt2 < NMAT; mt2++) {
-                        const float dq = fmaf(-128.0f, xs, t[mt2][r]);
-                        acc[mt2][ms][r] = fmaf(cs[mt2], dq, fmaf(cb[mt2], xs, acc[mt2][ms][r]));
-                    }
-                }
-            }
-        }
-        if (gi + 1 < G) {
-            /* buffer buf^1 was last read in group gi-1, before the barrier
-             * that ended it; one barrier per group suffices */
-            stage_x(buf ^ 1);
-            __syncthreads();
-        }
-    }
-
-    /* store */
-#pragma unroll
-    for (int ms = 0; ms < MM_MSUB; ms++) {
-        if (ms < msub) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int row = 32 * ms + 8 * (r >> 2) + 4 * g + (r & 3);
-                if (row < mrows) {
-                    const float v = DOWN ? acc[0][ms][r] : qk_silu(acc[0][ms][r]) * acc[NMAT - 1][ms][r];
-                    qk_st(a.out + (size_t)(p0 + mstart + row) * a.N + n, v);
-                }
-            }
-        }
+    switch ((mrows + 15) >> 4) {
+    case 1: mm_body<DOWN, TERMS, MAXG, 1>(a, sm, e, p0, mstart, mrows, nt); break;
+    case 2: mm_body<DOWN, TERMS, MAXG, 2>(a, sm, e, p0, mstart, mrows, nt); break;
+    case 3: mm_body<DOWN, TERMS, MAXG, 3>(a, sm, e, p0, mstart, mrows, nt); break;
+    case 4: mm_body<DOWN, TERMS, MAXG, 4>(a, sm, e, p0, mstart, mrows, nt); break;
+    case 5: mm_body<DOWN, TERMS, MAXG, 5>(a, sm, e, p0, mstart, mrows, nt); break;
+    default: mm_body<DOWN, TERMS, MAXG, MM_MT>(a, sm, e, p0, mstart, mrows, nt); break;
     }
 }
 
-/* ---- task list: (segment, chunk) for every segment with at least
- * `min_m` rows; segment 0 is the shared expert over all n tokens.
- * tasks[0] = count, then int2 pairs from tasks[2]. */
-__global__ __launch_bounds__(1024) void k_mfma_tasks(const int32_t *segtab, int n, int E, int min_m,
-                                                     int32_t *tasks) {
+/*
+ * Activation rows -> MFMA planes.  One thread per 8 columns: the pair-order
+ * bf16 plane (hi = RNE(x), and lo = RNE(x - hi) for f32 input) and, per row
+ * and 64-column group, P = -128 * sum(hi + lo) summed in a fixed order
+ * (8 columns with v_dot2 against ones, then the 8 threads of the group by a
+ * butterfly).
+ */
+template <bool F32>
+__global__ __launch_bounds__(256) void k_pack_rows(const void *x, size_t nchunks, uint16_t *hi,
+                                                   uint16_t *lo, float *gsum) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= nchunks) return; /* nchunks is a multiple of 8: whole groups leave together */
+    uint32_t ph[4], pl[4];
+    float s = 0.0f;
+    if (F32) {
+        const float4 a0 = qk_ld((const float4 *)x + 2 * i), a1 = qk_ld((const float4 *)x + 2 * i + 1);
+        const float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        qk_f32x8_to_pairs(v, ph, pl, s);
+        ((uint4 *)lo)[i] = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+    } else {
+        qk_bf16x8_to_pairs(qk_ld((const uint4 *)x + i), ph);
+#pragma unroll
+        for (int j = 0; j < 4; j++) s = qk_dot2(ph[j], QK_BF16_ONES, s);
+    }
+    ((uint4 *)hi)[i] = make_uint4(ph[0], ph[1], ph[2], ph[3]);
+    s += qk_dpp<QK_DPP_XOR1>(s);
+    s += qk_dpp<QK_DPP_XOR2>(s);
+    s += __shfl_xor(s, 4, QK_WAVE);
+    if ((i & 7) == 0) gsum[i >> 3] = -128.0f * s;
+}
+
+/* ---- task list: {expert (-1 = shared), first position, rows, chunk} for
+ * every segment with at least min_m rows; the shared expert covers all n
+ * tokens at positions n*k.. .  tasks[0] = count; entries from
+ * tasks + MM_TASK_HDR. */
+__global__ __launch_bounds__(1024) void k_mm_tasks(const int32_t *segtab, int n, int k, int E,
+                                                   int min_m, int32_t *tasks) {
     __shared__ int s_scan[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int U = min(max(qk_ld(segtab), 0), E);
+    int4 *out = (int4 *)(tasks + MM_TASK_HDR);
     int base = 0;
-    /* segments 0..U in blocks of 1024 */
+    /* segments 0..U in blocks of 1024; segment 0 is the shared expert */
     for (int s0 = 0; s0 <= U; s0 += 1024) {
         const int sg = s0 + tid;
-        int m = 0;
-        if (sg == 0) m = n;
-        else if (sg <= U) m = qk_ld(segtab + 3 * sg);
+        int e = -1, p0 = n * k, m = 0;
+        if (sg == 0) {
+            m = n;
+        } else if (sg <= U) {
+            e = qk_ld(segtab + 3 * sg - 2);
+            p0 = qk_ld(segtab + 3 * sg - 1);
+            m = qk_ld(segtab + 3 * sg);
+        }
         const int cnt = m >= min_m && m > 0 ? (m + MM_BM - 1) / MM_BM : 0;
         int inc = cnt;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
-            int u = __shfl_up(inc, o, QK_WAVE);
+            const int u = __shfl_up(inc, o, QK_WAVE);
             if (lane >= o) inc += u;
         }
         if (lane == 63) s_scan[wave] = inc;
@@ -318,83 +385,120 @@ __global__ __launch_bounds__(1024) void k_mfma_tasks(const int32_t *segtab, int 
         __syncthreads();
         const int off = base + wbase + inc - cnt;
         for (int ch = 0; ch < cnt; ch++) {
-            tasks[2 + 2 * (off + ch)] = sg;
-            tasks[3 + 2 * (off + ch)] = ch;
+            int *o = (int *)(out + off + ch);
+            o[0] = e;
+            o[1] = p0;
+            o[2] = m;
+            o[3] = ch;
         }
         base += tot;
     }
     if (tid == 0) tasks[0] = base;
 }
 
-static int mfma_launch(const MfmaArgs &a, bool down, int max_tasks, hipStream_t st) {
+static int mm_launch(const MmArgs &a, bool down, int terms, int max_tasks, hipStream_t st) {
     long long wgs = (long long)max_tasks * a.ntile;
     wgs = (wgs + 7) / 8 * 8;
     if (wgs <= 0) return 0;
-    if (down) hipLaunchKernelGGL((k_mfma<true>), dim3((unsigned)wgs), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((k_mfma<false>), dim3((unsigned)wgs), dim3(256), 0, st, a);
+    if (down) {
+        if (terms == 2) hipLaunchKernelGGL((k_mm<true, 2>), dim3((unsigned)wgs), dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((k_mm<true, 1>), dim3((unsigned)wgs), dim3(256), 0, st, a);
+    } else {
+        if (terms == 2) hipLaunchKernelGGL((k_mm<false, 2>), dim3((unsigned)wgs), dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((k_mm<false, 1>), dim3((unsigned)wgs), dim3(256), 0, st, a);
+    }
     return QK_CHECK_LAUNCH();
 }
 
 extern "C" int qk_mfma_max_tasks(qk_shape s, int n) {
     /* routed segments: at most min(E, n*k), plus their extra chunks; shared: ceil(n/BM) */
     const long long nk = (long long)n * s.k;
-    long long t = (nk < s.E ? nk : s.E) + nk / MM_BM + (n + MM_BM - 1) / MM_BM + 1;
+    const long long t = (nk < s.E ? nk : s.E) + nk / MM_BM + (n + MM_BM - 1) / MM_BM + 1;
     return (int)t;
+}
+
+extern "C" size_t qk_mfma_task_bytes(qk_shape s, int n) {
+    return ((size_t)MM_TASK_HDR + 4 * (size_t)qk_mfma_max_tasks(s, n)) * 4;
+}
+
+/* gate/up: K = H, N = I in tiles of 128 columns; down: K = I, N = H in
+ * tiles of 256.  K/64 groups: a multiple of 8, at most the LDS scale table
+ * (64 groups with one activation plane, 32 with two). */
+extern "C" int qk_mfma_gateup_ok(qk_shape s, int x_bf16) {
+    const int G = s.H / 64;
+    return s.H % 512 == 0 && s.I % 128 == 0 && G <= (x_bf16 ? 64 : 32);
+}
+
+extern "C" int qk_mfma_down_ok(qk_shape s) {
+    const int G = s.I / 64;
+    return s.I % 512 == 0 && s.H % 256 == 0 && G <= 32;
 }
 
 extern "C" int qk_launch_mfma_tasks(qk_shape s, int n, const int32_t *segtab, int min_m,
                                     int32_t *tasks, void *stream) {
-    hipLaunchKernelGGL(k_mfma_tasks, dim3(1), dim3(1024), 0, (hipStream_t)stream, segtab, n, s.E,
+    hipLaunchKernelGGL(k_mm_tasks, dim3(1), dim3(1024), 0, (hipStream_t)stream, segtab, n, s.k, s.E,
                        min_m, tasks);
     return QK_CHECK_LAUNCH();
 }
 
-extern "C" int qk_launch_gateup_mfma(const qmoe_layer_weights *W, qk_shape s, const uint16_t *x,
-                                     int n, const int32_t *perm, const int32_t *segtab,
-                                     const int32_t *tasks, float *h, void *stream) {
+extern "C" int qk_launch_pack_rows(const void *x, int x_bf16, size_t rows, int K, uint16_t *hi,
+                                   uint16_t *lo, float *gsum, void *stream) {
+    if (rows == 0) return 0;
+    if (K % 64) return (int)hipErrorInvalidValue;
+    const size_t nch = rows * (size_t)(K / 8);
+    const unsigned grid = (unsigned)((nch + 255) / 256);
+    if (x_bf16) hipLaunchKernelGGL(k_pack_rows<false>, dim3(grid), dim3(256), 0, (hipStream_t)stream, x, nch, hi, lo, gsum);
+    else hipLaunchKernelGGL(k_pack_rows<true>, dim3(grid), dim3(256), 0, (hipStream_t)stream, x, nch, hi, lo, gsum);
+    return QK_CHECK_LAUNCH();
+}
+
+extern "C" int qk_launch_gateup_mfma(const qmoe_layer_weights *W, qk_shape s, const uint16_t *xhi,
+                                     const uint16_t *xlo, const float *xg, int n,
+                                     const int32_t *perm, const int32_t *tasks, float *h,
+                                     void *stream) {
     if (n <= 0) return 0;
-    if (s.I % MM_BN || s.H % 64) return (int)hipErrorInvalidValue;
-    MfmaArgs a;
+    if (!qk_mfma_gateup_ok(s, xlo == NULL)) return (int)hipErrorInvalidValue;
+    MmArgs a;
     a.q[0] = W->gate_q; a.s[0] = W->gate_s; a.b[0] = W->gate_b;
     a.q[1] = W->up_q;   a.s[1] = W->up_s;   a.b[1] = W->up_b;
     a.sq[0] = W->sh_gate_q; a.ss[0] = W->sh_gate_s; a.sb[0] = W->sh_gate_b;
     a.sq[1] = W->sh_up_q;   a.ss[1] = W->sh_up_s;   a.sb[1] = W->sh_up_b;
-    a.x = x;
+    a.ap[0] = xhi;
+    a.ap[1] = xlo ? xlo : xhi;
+    a.ag = xg;
     a.out = h;
     a.perm = perm;
-    a.segtab = segtab;
     a.tasks = tasks;
     a.K = s.H;
     a.N = s.I;
     a.n = n;
     a.k = s.k;
-    a.E = s.E;
-    a.ntile = s.I / MM_BN;
-    return mfma_launch(a, false, qk_mfma_max_tasks(s, n), (hipStream_t)stream);
+    a.ntile = s.I / 128;
+    return mm_launch(a, false, xlo ? 2 : 1, qk_mfma_max_tasks(s, n), (hipStream_t)stream);
 }
 
-extern "C" int qk_launch_down_mfma(const qmoe_layer_weights *W, qk_shape s, const float *h, int n,
-                                   const int32_t *segtab, const int32_t *tasks, float *y,
-                                   void *stream) {
+extern "C" int qk_launch_down_mfma(const qmoe_layer_weights *W, qk_shape s, const uint16_t *hhi,
+                                   const uint16_t *hlo, const float *hg, int n,
+                                   const int32_t *tasks, float *y, void *stream) {
     if (n <= 0) return 0;
-    if (s.H % MM_BN || s.I % 64) return (int)hipErrorInvalidValue;
-    MfmaArgs a;
+    if (!qk_mfma_down_ok(s)) return (int)hipErrorInvalidValue;
+    MmArgs a;
     a.q[0] = a.q[1] = W->down_q;
     a.s[0] = a.s[1] = W->down_s;
     a.b[0] = a.b[1] = W->down_b;
     a.sq[0] = a.sq[1] = W->sh_down_q;
     a.ss[0] = a.ss[1] = W->sh_down_s;
     a.sb[0] = a.sb[1] = W->sh_down_b;
-    a.x = h;
+    a.ap[0] = hhi;
+    a.ap[1] = hlo;
+    a.ag = hg;
     a.out = y;
     a.perm = nullptr;
-    a.segtab = segtab;
     a.tasks = tasks;
     a.K = s.I;
     a.N = s.H;
     a.n = n;
     a.k = s.k;
-    a.E = s.E;
-    a.ntile = s.H / MM_BN;
-    return mfma_launch(a, true, qk_mfma_max_tasks(s, n), (hipStream_t)stream);
+    a.ntile = s.H / 256;
+    return mm_launch(a, true, 2, qk_mfma_max_tasks(s, n), (hipStream_t)stream);
 }

@@ -40,6 +40,10 @@ __device__ __forceinline__ int2 qk_ld(const int2 *p) {
     const qk_u32x2 v = *(const QK_GLOBAL qk_u32x2 *)p;
     return make_int2((int)v.x, (int)v.y);
 }
+__device__ __forceinline__ int4 qk_ld(const int4 *p) {
+    const qk_u32x4 v = *(const QK_GLOBAL qk_u32x4 *)p;
+    return make_int4((int)v.x, (int)v.y, (int)v.z, (int)v.w);
+}
 __device__ __forceinline__ float4 qk_ld(const float4 *p) {
     const qk_f32x4 v = *(const QK_GLOBAL qk_f32x4 *)p;
     return make_float4(v.x, v.y, v.z, v.w);

@@ -173,12 +173,13 @@ int qmoe_create(qmoe_ctx **out, const qmoe_config *cfg, qmoe_err *err) {
     const size_t n = (size_t)cfg->max_tokens, E = (size_t)cfg->n_experts, k = (size_t)cfg->top_k;
     const size_t H = (size_t)cfg->hidden, I = (size_t)cfg->moe_inter;
     const size_t nw = (n + 31) / 32, rows = n * k + n;
-    const size_t ntasks = (size_t)qk_mfma_max_tasks(c->shape, (int)n);
-    size_t sz[14] = {n * (E + 1) * 4, n * k * 4, n * k * 4, n * 4, (E + 1) * 4, n * k * 4,
+    const size_t plane = n * H > rows * I ? n * H : rows * I;
+    size_t sz[17] = {n * (E + 1) * 4, n * k * 4, n * k * 4, n * 4, (E + 1) * 4, n * k * 4,
                      n * k * 4, E * nw * 4, E * nw * 4, n * H * 4, rows * I * 4,
-                     rows * H * 4, (3 * E + 1) * 4, (2 + 2 * ntasks) * 4};
-    size_t total = 0, offs[14];
-    for (int i = 0; i < 14; i++) {
+                     rows * H * 4, (3 * E + 1) * 4, qk_mfma_task_bytes(c->shape, (int)n),
+                     plane * 2, plane * 2, plane / 64 * 4};
+    size_t total = 0, offs[17];
+    for (int i = 0; i < 17; i++) {
         offs[i] = total;
         total = align_up(total + sz[i]);
     }
@@ -203,6 +204,9 @@ int qmoe_create(qmoe_ctx **out, const qmoe_config *cfg, qmoe_err *err) {
     c->sc.y = (float *)(b + offs[11]);
     c->sc.segtab = (int32_t *)(b + offs[12]);
     c->sc.tasks = (int32_t *)(b + offs[13]);
+    c->sc.ahi = (uint16_t *)(b + offs[14]);
+    c->sc.alo = (uint16_t *)(b + offs[15]);
+    c->sc.ag = (float *)(b + offs[16]);
     *out = c;
     return 0;
 }
@@ -474,28 +478,33 @@ int qmoe_router(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n, float
 }
 
 /* Grouped expert stages.  Segments with at least QK_MFMA_MIN_M rows run on
- * the MFMA kernels (gate/up only for bf16 activations; down always, h is
- * f32), the others on the GEMV kernels.  The MFMA task list is built from
- * the segment table unless the caller says it is already current. */
-static int mfma_usable(const qmoe_ctx *c, int n) {
-    const qk_shape s = c->shape;
-    return s.I % 128 == 0 && s.H % 128 == 0 && n * (s.k + 1) >= QK_MFMA_MIN_M;
+ * the MFMA kernels, the others on the GEMV kernels.  The MFMA kernels read
+ * their activations as packed operand planes (qk_launch_pack_rows).  The
+ * MFMA task list is built from the segment table unless the caller says it
+ * is already current. */
+static int mfma_usable(const qmoe_ctx *c, int n, int stage) {
+    const int ok = stage == 2 ? qk_mfma_down_ok(c->shape) : qk_mfma_gateup_ok(c->shape, stage == 0);
+    return ok && n * (c->shape.k + 1) >= QK_MFMA_MIN_M;
 }
 
 static int run_gateup(qmoe_ctx *c, const qmoe_layer_weights *W, const void *x, int xbf, int n,
                       const int32_t *perm, const int32_t *segtab, float *h, void *stream,
                       qmoe_err *err) {
-    const int mm = mfma_usable(c, n) && xbf;
+    const int mm = mfma_usable(c, n, xbf ? 0 : 1);
+    const qk_shape s = c->shape;
     int rc;
     if (mm) {
-        rc = qk_launch_mfma_tasks(c->shape, n, segtab, QK_MFMA_MIN_M, c->sc.tasks, stream);
+        rc = qk_launch_mfma_tasks(s, n, segtab, QK_MFMA_MIN_M, c->sc.tasks, stream);
         if (hip_fail(err, rc, "mfma tasks")) return -1;
+        rc = qk_launch_pack_rows(x, xbf, (size_t)n, s.H, c->sc.ahi, xbf ? NULL : c->sc.alo, c->sc.ag,
+                                 stream);
+        if (hip_fail(err, rc, "pack x")) return -1;
     }
-    rc = qk_launch_gateup(W, c->shape, x, xbf, n, perm, segtab, mm ? QK_MFMA_MIN_M : 0, h, stream);
+    rc = qk_launch_gateup(W, s, x, xbf, n, perm, segtab, mm ? QK_MFMA_MIN_M : 0, h, stream);
     if (hip_fail(err, rc, "gateup")) return -1;
     if (mm) {
-        rc = qk_launch_gateup_mfma(W, c->shape, (const uint16_t *)x, n, perm, segtab, c->sc.tasks, h,
-                                   stream);
+        rc = qk_launch_gateup_mfma(W, s, c->sc.ahi, xbf ? NULL : c->sc.alo, c->sc.ag, n, perm,
+                                   c->sc.tasks, h, stream);
         if (hip_fail(err, rc, "gateup mfma")) return -1;
     }
     return 0;
@@ -503,16 +512,22 @@ static int run_gateup(qmoe_ctx *c, const qmoe_layer_weights *W, const void *x, i
 
 static int run_down(qmoe_ctx *c, const qmoe_layer_weights *W, const float *h, int n,
                     const int32_t *segtab, int tasks_ready, float *y, void *stream, qmoe_err *err) {
-    const int mm = mfma_usable(c, n);
+    const int mm = mfma_usable(c, n, 2);
+    const qk_shape s = c->shape;
     int rc;
-    if (mm && !tasks_ready) {
-        rc = qk_launch_mfma_tasks(c->shape, n, segtab, QK_MFMA_MIN_M, c->sc.tasks, stream);
-        if (hip_fail(err, rc, "mfma tasks")) return -1;
+    if (mm) {
+        if (!tasks_ready) {
+            rc = qk_launch_mfma_tasks(s, n, segtab, QK_MFMA_MIN_M, c->sc.tasks, stream);
+            if (hip_fail(err, rc, "mfma tasks")) return -1;
+        }
+        rc = qk_launch_pack_rows(h, 0, (size_t)n * (s.k + 1), s.I, c->sc.ahi, c->sc.alo, c->sc.ag,
+                                 stream);
+        if (hip_fail(err, rc, "pack h")) return -1;
     }
-    rc = qk_launch_down(W, c->shape, h, n, segtab, mm ? QK_MFMA_MIN_M : 0, y, stream);
+    rc = qk_launch_down(W, s, h, n, segtab, mm ? QK_MFMA_MIN_M : 0, y, stream);
     if (hip_fail(err, rc, "down")) return -1;
     if (mm) {
-        rc = qk_launch_down_mfma(W, c->shape, h, n, segtab, c->sc.tasks, y, stream);
+        rc = qk_launch_down_mfma(W, s, c->sc.ahi, c->sc.alo, c->sc.ag, n, c->sc.tasks, y, stream);
         if (hip_fail(err, rc, "down mfma")) return -1;
     }
     return 0;
@@ -683,12 +698,13 @@ int qmoe_layer_forward(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n
         if (hip_fail(err, rc, "dispatch")) return -1;
     }
     if (run_gateup(c, W, xf, xf_bf, n, sc->perm, sc->segtab, sc->h, stream, err)) return -1;
-    if (!mfma_usable(c, n) && qk_down_combine_lds(s, n) > 0) {
+    if (!mfma_usable(c, n, 2) && qk_down_combine_lds(s, n) > 0) {
         rc = qk_launch_down_combine(W, s, sc->h, n, sc->segtab, sc->pos, sc->w, sc->sg,
                                     (flags & QMOE_RESIDUAL) ? x : NULL, xbf, out, stream);
         return hip_fail(err, rc, "down+combine");
     }
-    if (run_down(c, W, sc->h, n, sc->segtab, xf_bf, sc->y, stream, err)) return -1;
+    if (run_down(c, W, sc->h, n, sc->segtab, mfma_usable(c, n, xf_bf ? 0 : 1), sc->y, stream, err))
+        return -1;
     rc = qk_launch_combine(s, n, sc->y, sc->pos, sc->w, sc->sg,
                            (flags & QMOE_RESIDUAL) ? x : NULL, xbf, out, stream);
     return hip_fail(err, rc, "combine");

@@ -39,7 +39,10 @@ typedef struct {
     int32_t *perm;     /* [n*k] */
     int32_t *pos;      /* [n*k] inverse of perm */
     int32_t *segtab;   /* [1+3E]: U, then (expert, first position, count) per routed segment */
-    int32_t *tasks;    /* [2+2*max_tasks]: MFMA (segment, chunk) task list */
+    int32_t *tasks;    /* MFMA task list (qk_mfma_task_bytes) */
+    uint16_t *ahi;     /* MFMA activation planes: max(n*H, (n*k+n)*I) bf16 each */
+    uint16_t *alo;
+    float *ag;         /* their group sums: max(n*H, (n*k+n)*I) / 64 */
     uint32_t *bits;    /* [E, ceil(n/32)] token membership bitmask (large dispatch) */
     int32_t *wprefix;  /* [E, ceil(n/32)] per-word exclusive popcount prefix */
     float *xn;         /* [n, H] normalised router input */
@@ -85,13 +88,22 @@ int qk_launch_gateup(const qmoe_layer_weights *W, qk_shape s, const void *x, int
 int qk_launch_down(const qmoe_layer_weights *W, qk_shape s, const float *h, int n,
                    const int32_t *segtab, int max_m, float *y, void *stream);
 int qk_mfma_max_tasks(qk_shape s, int n);
+size_t qk_mfma_task_bytes(qk_shape s, int n);
+/* shapes the MFMA kernels take (x_bf16: gate/up activations are bf16) */
+int qk_mfma_gateup_ok(qk_shape s, int x_bf16);
+int qk_mfma_down_ok(qk_shape s);
 int qk_launch_mfma_tasks(qk_shape s, int n, const int32_t *segtab, int min_m, int32_t *tasks,
                          void *stream);
-int qk_launch_gateup_mfma(const qmoe_layer_weights *W, qk_shape s, const uint16_t *x, int n,
-                          const int32_t *perm, const int32_t *segtab, const int32_t *tasks,
-                          float *h, void *stream);
-int qk_launch_down_mfma(const qmoe_layer_weights *W, qk_shape s, const float *h, int n,
-                        const int32_t *segtab, const int32_t *tasks, float *y, void *stream);
+/* activation rows [rows, K] (bf16 or f32) -> MFMA operand planes: hi (and
+ * lo for f32) bf16 in pair order, gsum [rows, K/64] = -128 * group sums */
+int qk_launch_pack_rows(const void *x, int x_bf16, size_t rows, int K, uint16_t *hi, uint16_t *lo,
+                        float *gsum, void *stream);
+int qk_launch_gateup_mfma(const qmoe_layer_weights *W, qk_shape s, const uint16_t *xhi,
+                          const uint16_t *xlo, const float *xg, int n, const int32_t *perm,
+                          const int32_t *tasks, float *h, void *stream);
+int qk_launch_down_mfma(const qmoe_layer_weights *W, qk_shape s, const uint16_t *hhi,
+                        const uint16_t *hlo, const float *hg, int n, const int32_t *tasks,
+                        float *y, void *stream);
 /* one token, layer path: gate/up with the top-k of `logits` selected inside
  * the kernel, which also writes idx, w, sg, perm, pos and the segment
  * table (the form the dispatch produces for one token) */

@@ -170,19 +170,20 @@ def test_dispatch_bitexact(torch_dev, n, k, E):
 
 # ------------------------------------------------------------ full shapes
 
-def _layer_case(torch, dev, wname, n=None, n_check=16, seed_x=None):
+def _layer_case(torch, dev, wname, n=None, n_check=16, seed_x=None, x_bf16=None):
     pkg = load_pkg()
     w = pkg.WORKLOADS[wname]
     n = n or w.n_tokens
+    xbf = w.x_bf16 if x_bf16 is None else x_bf16
     rb = orc.zipf_bias(w.n_experts, w.zipf_s, w.zipf_scale, w.seed * 1000003) if w.zipf_s > 0 else None
-    x = orc.gen_x(n, w.hidden, w.seed if seed_x is None else seed_x, bf16=w.x_bf16)
+    x = orc.gen_x(n, w.hidden, w.seed if seed_x is None else seed_x, bf16=xbf)
     Lr = orc.Layer(w.hidden, w.n_experts, w.top_k, w.moe_inter, seed=w.seed, router_bias=rb,
                    only_experts=[])
-    route = Lr.route(x, w.x_bf16)
+    route = Lr.route(x, xbf)
     sel = np.unique(np.linspace(0, n - 1, min(n, n_check)).astype(np.int32))
     L = orc.Layer(w.hidden, w.n_experts, w.top_k, w.moe_inter, seed=w.seed, router_bias=rb,
                   only_experts=route["idx"][sel].reshape(-1))
-    ref = L.forward(x, w.x_bf16, token_sel=sel)
+    ref = L.forward(x, xbf, token_sel=sel)
     with pkg.MoeContext.for_workload(w, max_tokens=n, n_layers=1) as ctx:
         ctx.synth_layer(0, w.seed, router_bias=rb)
         xt = to_dev(x, torch, dev)
@@ -230,6 +231,14 @@ def test_layer_small_and_large_dispatch_paths(torch_dev, n):
     torch, dev = torch_dev
     say(f"case: decode-shape layer n={n} (dispatch path boundary)")
     _layer_case(torch, dev, "decode", n=n, n_check=6, seed_x=11)
+
+
+def test_layer_f32_activations(torch_dev):
+    """f32 activations on a many-token layer: the grouped GEMM takes the
+    activations as bf16 hi + lo planes"""
+    torch, dev = torch_dev
+    say("case: decode-shape layer n=160, f32 activations")
+    _layer_case(torch, dev, "decode", n=160, n_check=6, seed_x=13, x_bf16=False)
 
 
 def test_depth_stack_norm_residual(torch_dev):
