@@ -35,6 +35,7 @@ struct GemvArgs {
     const int32_t *perm, *segtab;
     int K, N, n, k, E;
     int max_m;              /* skip segments with >= max_m rows (0: none skipped) */
+    const int32_t *seglist; /* null, or [count, segment...]: only these segments */
     int in_by_pos;          /* input row = dispatch position (down) instead of token */
 };
 
@@ -153,8 +154,14 @@ __global__ __launch_bounds__(256) void k_q4gemv(GemvArgs a) {
     const size_t wrow = (size_t)a.K >> 3; /* u32 words per weight row */
     const int tps = (a.N + RB - 1) / RB;
     const int u_raw = a.segtab[0];
+    const int nlist = a.seglist ? qk_ld(a.seglist) : 0;
     for (int task = blockIdx.x;; task += gridDim.x) {
-        const int seg = task / tps, rb = task - seg * tps;
+        int seg = task / tps;
+        const int rb = task - seg * tps;
+        if (a.seglist) {
+            if (seg >= nlist) break;
+            seg = qk_ld(a.seglist + 1 + seg);
+        }
         const bool shared = seg == 0;
         if (seg > a.E) break;
         int p0, m;
@@ -597,7 +604,7 @@ static int launch_gemv(const GemvArgs &a, int max_seg, hipStream_t st) {
 
 extern "C" int qk_launch_gateup(const qmoe_layer_weights *W, qk_shape s, const void *x, int x_bf16,
                                 int n, const int32_t *perm, const int32_t *segtab, int max_m,
-                                float *h, void *stream) {
+                                const int32_t *seglist, float *h, void *stream) {
     if (n <= 0) return 0;
     GemvArgs a;
     a.q[0] = W->gate_q; a.s[0] = W->gate_s; a.b[0] = W->gate_b;
@@ -614,6 +621,7 @@ extern "C" int qk_launch_gateup(const qmoe_layer_weights *W, qk_shape s, const v
     a.k = s.k;
     a.E = s.E;
     a.max_m = max_m;
+    a.seglist = seglist;
     a.in_by_pos = 0;
     const int max_seg = n * s.k < s.E ? n * s.k : s.E;
     hipStream_t st = (hipStream_t)stream;
@@ -625,7 +633,8 @@ extern "C" int qk_launch_gateup(const qmoe_layer_weights *W, qk_shape s, const v
 }
 
 extern "C" int qk_launch_down(const qmoe_layer_weights *W, qk_shape s, const float *h, int n,
-                              const int32_t *segtab, int max_m, float *y, void *stream) {
+                              const int32_t *segtab, int max_m, const int32_t *seglist, float *y,
+                              void *stream) {
     if (n <= 0) return 0;
     GemvArgs a;
     a.q[0] = a.q[1] = W->down_q;
@@ -644,6 +653,7 @@ extern "C" int qk_launch_down(const qmoe_layer_weights *W, qk_shape s, const flo
     a.k = s.k;
     a.E = s.E;
     a.max_m = max_m;
+    a.seglist = seglist;
     a.in_by_pos = 1;
     const int max_seg = n * s.k < s.E ? n * s.k : s.E;
     return launch_gemv<1, false>(a, max_seg, (hipStream_t)stream);

@@ -55,11 +55,13 @@ struct MmArgs {
     int K, N, n, k, ntile;
 };
 
-template <int TERMS, int MAXG>
+#define MM_MAXG 32 /* K/64 groups held in LDS (scales, group sums) */
+
+template <int TERMS>
 struct MmSmem {
-    uint4 a[2][TERMS][MM_BM * 8];
-    float p[2][MM_BM];
-    uint16_t s[MAXG][4][16][4]; /* [group][wave][column][tile] */
+    uint4 a[2][TERMS][MM_BM * 8];   /* activation chunks, double buffered */
+    float p[MM_MAXG][MM_BM];        /* P of the chunk's rows, [group][row] */
+    uint16_t s[MM_MAXG][4][16][4];  /* scales, [group][wave][column][tile] */
     int row[MM_BM];
 };
 
@@ -75,8 +77,8 @@ __device__ __forceinline__ int mm_col(int nt, int wave, int ct, int c) {
     return DOWN ? nt * 256 + 64 * wave + 16 * ct + c : nt * 128 + 32 * wave + 16 * (ct & 1) + c;
 }
 
-template <bool DOWN, int TERMS, int MAXG, int MS>
-__device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, MAXG> &sm, int e, int p0,
+template <bool DOWN, int TERMS, int MS>
+__device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS> &sm, int e, int p0,
                                         int mstart, int mrows, int nt) {
     constexpr int ACH = (MM_BM * 8 + 255) / 256; /* staged 16-byte chunks per thread */
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -92,26 +94,41 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, MAXG> &sm
         const uint32_t *base = shared ? a.sq[mat] : a.q[mat] + (size_t)e * a.N * wrow;
         wq[ct] = base + (size_t)mm_col<DOWN>(nt, wave, ct, c) * wrow + 2 * kq;
     }
-    /* scales of the tile: thread -> (wave', tile', column') */
+    uint2 wr[MM_WD][4];
+    auto load_w = [&](int slot, int g) {
+#pragma unroll
+        for (int ct = 0; ct < 4; ct++) wr[slot][ct] = qk_ld((const uint2 *)(wq[ct] + 8 * g));
+    };
+#pragma unroll
+    for (int u = 0; u < MM_WD; u++)
+        if (u < G) load_w(u, u);
+
+    /* scales of the tile: thread -> (wave', tile', column'), G/8 loads of 8 */
+    const int w2 = tid >> 6, ct2 = (tid >> 4) & 3, c2 = tid & 15;
+    uint4 sv[MM_MAXG / 8];
     {
-        const int w2 = tid >> 6, ct2 = (tid >> 4) & 3, c2 = tid & 15;
         const int mat = DOWN ? 0 : ct2 >> 1;
         const uint16_t *sp = (shared ? a.ss[mat] : a.s[mat] + (size_t)e * a.N * G) +
                              (size_t)mm_col<DOWN>(nt, w2, ct2, c2) * G;
-        for (int g8 = 0; g8 < G; g8 += 8) {
-            const uint4 v = qk_ld((const uint4 *)(sp + g8));
-            const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                sm.s[g8 + 2 * j][w2][c2][ct2] = (uint16_t)(wv[j] & 0xFFFFu);
-                sm.s[g8 + 2 * j + 1][w2][c2][ct2] = (uint16_t)(wv[j] >> 16);
-            }
+        for (int i = 0; i < MM_MAXG / 8; i++)
+            if (8 * i < G) sv[i] = qk_ld((const uint4 *)(sp + 8 * i));
+    }
+    __syncthreads(); /* sm.row, written by the caller */
+
+    /* P of the chunk's rows: 16-byte chunk ci -> row ci / (G/4), groups 4*(ci % (G/4)).. */
+    constexpr int PCH = (MM_BM * MM_MAXG / 4 + 255) / 256;
+    float4 pv[PCH];
+#pragma unroll
+    for (int i = 0; i < PCH; i++) {
+        const int ci = tid + 256 * i;
+        if (ci < MM_BM * (G >> 2)) {
+            const int row = ci / (G >> 2), g4 = ci - row * (G >> 2);
+            pv[i] = qk_ld((const float4 *)(a.ag + (size_t)sm.row[row] * G) + g4);
         }
     }
-    __syncthreads(); /* sm.row (written by the caller) and sm.s */
 
     uint4 ar[TERMS][ACH];
-    float pr = 0.0f;
     auto load_a = [&](int g) {
 #pragma unroll
         for (int i = 0; i < ACH; i++) {
@@ -122,7 +139,6 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, MAXG> &sm
                 for (int tm = 0; tm < TERMS; tm++) ar[tm][i] = qk_ld((const uint4 *)(a.ap[tm] + off));
             }
         }
-        if (tid < MM_BM) pr = qk_ld(a.ag + (size_t)sm.row[tid] * G + g);
     };
     auto store_a = [&](int buf) {
 #pragma unroll
@@ -134,14 +150,31 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, MAXG> &sm
                 for (int tm = 0; tm < TERMS; tm++) sm.a[buf][tm][row * 8 + (kc ^ (row & 7))] = ar[tm][i];
             }
         }
-        if (tid < MM_BM) sm.p[buf][tid] = pr;
     };
+    load_a(0);
 
-    uint2 wr[MM_WD][4];
-    auto load_w = [&](int slot, int g) {
 #pragma unroll
-        for (int ct = 0; ct < 4; ct++) wr[slot][ct] = qk_ld((const uint2 *)(wq[ct] + 8 * g));
-    };
+    for (int i = 0; i < MM_MAXG / 8; i++) {
+        if (8 * i < G) {
+            const uint32_t wv[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                sm.s[8 * i + 2 * j][w2][c2][ct2] = (uint16_t)(wv[j] & 0xFFFFu);
+                sm.s[8 * i + 2 * j + 1][w2][c2][ct2] = (uint16_t)(wv[j] >> 16);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < PCH; i++) {
+        const int ci = tid + 256 * i;
+        if (ci < MM_BM * (G >> 2)) {
+            const int row = ci / (G >> 2), g4 = ci - row * (G >> 2);
+            sm.p[4 * g4][row] = pv[i].x;
+            sm.p[4 * g4 + 1][row] = pv[i].y;
+            sm.p[4 * g4 + 2][row] = pv[i].z;
+            sm.p[4 * g4 + 3][row] = pv[i].w;
+        }
+    }
 
     qm_f32x4 acc[MS][4];
 #pragma unroll
@@ -149,10 +182,6 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, MAXG> &sm
 #pragma unroll
         for (int ct = 0; ct < 4; ct++) acc[rt][ct] = qm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-#pragma unroll
-    for (int u = 0; u < MM_WD; u++)
-        if (u < G) load_w(u, u);
-    load_a(0);
     store_a(0);
     if (G > 1) load_a(1);
     __syncthreads();
@@ -181,7 +210,7 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, MAXG> &sm
                 qm_bf16x8 A[PF][TERMS][2];
                 qm_f32x4 xi[PF];
                 auto lds_a = [&](int rt, int sl) {
-                    xi[sl] = *(const qm_f32x4 *)&sm.p[buf][16 * rt + 4 * kq];
+                    xi[sl] = *(const qm_f32x4 *)&sm.p[g][16 * rt + 4 * kq];
                     const int row = 16 * rt + c;
 #pragma unroll
                     for (int tm = 0; tm < TERMS; tm++)
@@ -233,15 +262,8 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, MAXG> &sm
 #pragma unroll
         for (int rt = 0; rt < MS; rt++) {
             float xv[8];
-            if (gk < G) {
-                const float *src = a.ag + (size_t)sm.row[16 * rt + c] * G + gk;
-                const float4 v0 = qk_ld((const float4 *)src), v1 = qk_ld((const float4 *)(src + 4));
-                xv[0] = v0.x; xv[1] = v0.y; xv[2] = v0.z; xv[3] = v0.w;
-                xv[4] = v1.x; xv[5] = v1.y; xv[6] = v1.z; xv[7] = v1.w;
-            } else {
 #pragma unroll
-                for (int j = 0; j < 8; j++) xv[j] = 0.0f;
-            }
+            for (int j = 0; j < 8; j++) xv[j] = gk + j < G ? sm.p[gk + j][16 * rt + c] : 0.0f;
             uint32_t hi[4], lo[4];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
@@ -282,8 +304,7 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, MAXG> &sm
 
 template <bool DOWN, int TERMS>
 __global__ __launch_bounds__(256, 2) void k_mm(MmArgs a) {
-    constexpr int MAXG = TERMS == 1 ? 64 : 32;
-    __shared__ __attribute__((aligned(16))) MmSmem<TERMS, MAXG> sm;
+    __shared__ __attribute__((aligned(16))) MmSmem<TERMS> sm;
     /* consecutive column tiles of one task go to one XCD (workgroups are
      * dealt round-robin over the 8 XCDs), so they share its L2 */
     const int L = blockIdx.x;
@@ -306,12 +327,12 @@ __global__ __launch_bounds__(256, 2) void k_mm(MmArgs a) {
         sm.row[tid] = r;
     }
     switch ((mrows + 15) >> 4) {
-    case 1: mm_body<DOWN, TERMS, MAXG, 1>(a, sm, e, p0, mstart, mrows, nt); break;
-    case 2: mm_body<DOWN, TERMS, MAXG, 2>(a, sm, e, p0, mstart, mrows, nt); break;
-    case 3: mm_body<DOWN, TERMS, MAXG, 3>(a, sm, e, p0, mstart, mrows, nt); break;
-    case 4: mm_body<DOWN, TERMS, MAXG, 4>(a, sm, e, p0, mstart, mrows, nt); break;
-    case 5: mm_body<DOWN, TERMS, MAXG, 5>(a, sm, e, p0, mstart, mrows, nt); break;
-    default: mm_body<DOWN, TERMS, MAXG, MM_MT>(a, sm, e, p0, mstart, mrows, nt); break;
+    case 1: mm_body<DOWN, TERMS, 1>(a, sm, e, p0, mstart, mrows, nt); break;
+    case 2: mm_body<DOWN, TERMS, 2>(a, sm, e, p0, mstart, mrows, nt); break;
+    case 3: mm_body<DOWN, TERMS, 3>(a, sm, e, p0, mstart, mrows, nt); break;
+    case 4: mm_body<DOWN, TERMS, 4>(a, sm, e, p0, mstart, mrows, nt); break;
+    case 5: mm_body<DOWN, TERMS, 5>(a, sm, e, p0, mstart, mrows, nt); break;
+    default: mm_body<DOWN, TERMS, MM_MT>(a, sm, e, p0, mstart, mrows, nt); break;
     }
 }
 
@@ -349,14 +370,15 @@ __global__ __launch_bounds__(256) void k_pack_rows(const void *x, size_t nchunks
 /* ---- task list: {expert (-1 = shared), first position, rows, chunk} for
  * every segment with at least min_m rows; the shared expert covers all n
  * tokens at positions n*k.. .  tasks[0] = count; entries from
- * tasks + MM_TASK_HDR. */
+ * tasks + MM_TASK_HDR.  The segments with 1..min_m-1 rows (0 = shared) are
+ * listed for the GEMV kernels at `small`: small[0] = count, then ids. */
 __global__ __launch_bounds__(1024) void k_mm_tasks(const int32_t *segtab, int n, int k, int E,
-                                                   int min_m, int32_t *tasks) {
+                                                   int min_m, int32_t *tasks, int32_t *small) {
     __shared__ int s_scan[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int U = min(max(qk_ld(segtab), 0), E);
     int4 *out = (int4 *)(tasks + MM_TASK_HDR);
-    int base = 0;
+    int base = 0, sbase = 0;
     /* segments 0..U in blocks of 1024; segment 0 is the shared expert */
     for (int s0 = 0; s0 <= U; s0 += 1024) {
         const int sg = s0 + tid;
@@ -369,7 +391,10 @@ __global__ __launch_bounds__(1024) void k_mm_tasks(const int32_t *segtab, int n,
             m = qk_ld(segtab + 3 * sg);
         }
         const int cnt = m >= min_m && m > 0 ? (m + MM_BM - 1) / MM_BM : 0;
-        int inc = cnt;
+        const int sm = m > 0 && m < min_m ? 1 : 0;
+        /* both counts in one scan: chunks in bits 0..19, small segments above */
+        const int own = cnt + (sm << 20);
+        int inc = own;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
             const int u = __shfl_up(inc, o, QK_WAVE);
@@ -383,7 +408,8 @@ __global__ __launch_bounds__(1024) void k_mm_tasks(const int32_t *segtab, int n,
             tot += s_scan[i];
         }
         __syncthreads();
-        const int off = base + wbase + inc - cnt;
+        const int ex = wbase + inc - own;
+        const int off = base + (ex & 0xFFFFF), soff = sbase + (ex >> 20);
         for (int ch = 0; ch < cnt; ch++) {
             int *o = (int *)(out + off + ch);
             o[0] = e;
@@ -391,9 +417,14 @@ __global__ __launch_bounds__(1024) void k_mm_tasks(const int32_t *segtab, int n,
             o[2] = m;
             o[3] = ch;
         }
-        base += tot;
+        if (sm) small[1 + soff] = sg;
+        base += tot & 0xFFFFF;
+        sbase += tot >> 20;
     }
-    if (tid == 0) tasks[0] = base;
+    if (tid == 0) {
+        tasks[0] = base;
+        small[0] = sbase;
+    }
 }
 
 static int mm_launch(const MmArgs &a, bool down, int terms, int max_tasks, hipStream_t st) {
@@ -418,26 +449,30 @@ extern "C" int qk_mfma_max_tasks(qk_shape s, int n) {
 }
 
 extern "C" size_t qk_mfma_task_bytes(qk_shape s, int n) {
-    return ((size_t)MM_TASK_HDR + 4 * (size_t)qk_mfma_max_tasks(s, n)) * 4;
+    return ((size_t)MM_TASK_HDR + 4 * (size_t)qk_mfma_max_tasks(s, n) + 2 + (size_t)s.E) * 4;
+}
+
+extern "C" int32_t *qk_mfma_small_list(qk_shape s, int n, int32_t *tasks) {
+    return tasks + MM_TASK_HDR + 4 * (size_t)qk_mfma_max_tasks(s, n);
 }
 
 /* gate/up: K = H, N = I in tiles of 128 columns; down: K = I, N = H in
- * tiles of 256.  K/64 groups: a multiple of 8, at most the LDS scale table
- * (64 groups with one activation plane, 32 with two). */
+ * tiles of 256.  K/64 groups: a multiple of 8, at most MM_MAXG (the LDS
+ * tables of scales and group sums). */
 extern "C" int qk_mfma_gateup_ok(qk_shape s, int x_bf16) {
     const int G = s.H / 64;
-    return s.H % 512 == 0 && s.I % 128 == 0 && G <= (x_bf16 ? 64 : 32);
+    return s.H % 512 == 0 && s.I % 128 == 0 && G <= MM_MAXG;
 }
 
 extern "C" int qk_mfma_down_ok(qk_shape s) {
     const int G = s.I / 64;
-    return s.I % 512 == 0 && s.H % 256 == 0 && G <= 32;
+    return s.I % 512 == 0 && s.H % 256 == 0 && G <= MM_MAXG;
 }
 
 extern "C" int qk_launch_mfma_tasks(qk_shape s, int n, const int32_t *segtab, int min_m,
                                     int32_t *tasks, void *stream) {
     hipLaunchKernelGGL(k_mm_tasks, dim3(1), dim3(1024), 0, (hipStream_t)stream, segtab, n, s.k, s.E,
-                       min_m, tasks);
+                       min_m, tasks, qk_mfma_small_list(s, n, tasks));
     return QK_CHECK_LAUNCH();
 }
 

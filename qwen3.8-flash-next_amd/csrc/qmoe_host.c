@@ -500,7 +500,8 @@ static int run_gateup(qmoe_ctx *c, const qmoe_layer_weights *W, const void *x, i
                                  stream);
         if (hip_fail(err, rc, "pack x")) return -1;
     }
-    rc = qk_launch_gateup(W, s, x, xbf, n, perm, segtab, mm ? QK_MFMA_MIN_M : 0, h, stream);
+    rc = qk_launch_gateup(W, s, x, xbf, n, perm, segtab, mm ? QK_MFMA_MIN_M : 0,
+                          mm ? qk_mfma_small_list(s, n, c->sc.tasks) : NULL, h, stream);
     if (hip_fail(err, rc, "gateup")) return -1;
     if (mm) {
         rc = qk_launch_gateup_mfma(W, s, c->sc.ahi, xbf ? NULL : c->sc.alo, c->sc.ag, n, perm,
@@ -524,7 +525,8 @@ static int run_down(qmoe_ctx *c, const qmoe_layer_weights *W, const float *h, in
                                  stream);
         if (hip_fail(err, rc, "pack h")) return -1;
     }
-    rc = qk_launch_down(W, s, h, n, segtab, mm ? QK_MFMA_MIN_M : 0, y, stream);
+    rc = qk_launch_down(W, s, h, n, segtab, mm ? QK_MFMA_MIN_M : 0,
+                        mm ? qk_mfma_small_list(s, n, c->sc.tasks) : NULL, y, stream);
     if (hip_fail(err, rc, "down")) return -1;
     if (mm) {
         rc = qk_launch_down_mfma(W, s, c->sc.ahi, c->sc.alo, c->sc.ag, n, c->sc.tasks, y, stream);

@@ -84,11 +84,16 @@ int qk_launch_invert_perm(int count, const int32_t *perm, int32_t *pos, void *st
  * qk_launch_mfma_tasks for segments with at least min_m rows. */
 #define QK_MFMA_MIN_M 16
 int qk_launch_gateup(const qmoe_layer_weights *W, qk_shape s, const void *x, int x_bf16, int n,
-                     const int32_t *perm, const int32_t *segtab, int max_m, float *h, void *stream);
+                     const int32_t *perm, const int32_t *segtab, int max_m,
+                     const int32_t *seglist, float *h, void *stream);
 int qk_launch_down(const qmoe_layer_weights *W, qk_shape s, const float *h, int n,
-                   const int32_t *segtab, int max_m, float *y, void *stream);
+                   const int32_t *segtab, int max_m, const int32_t *seglist, float *y,
+                   void *stream);
 int qk_mfma_max_tasks(qk_shape s, int n);
 size_t qk_mfma_task_bytes(qk_shape s, int n);
+/* the list of segments below min_m rows that the task kernel writes beside
+ * the tasks (for the GEMV kernels): [count, segment...] */
+int32_t *qk_mfma_small_list(qk_shape s, int n, int32_t *tasks);
 /* shapes the MFMA kernels take (x_bf16: gate/up activations are bf16) */
 int qk_mfma_gateup_ok(qk_shape s, int x_bf16);
 int qk_mfma_down_ok(qk_shape s);

@@ -130,6 +130,128 @@ __global__ __launch_bounds__(256) void k_router(RouterArgs a) {
     router_rows<XBF16, NORM, NCH>(a, row, t0, min(a.n, t0 + RT_TB));
 }
 
+/*
+ * Many tokens: one workgroup per (block of RTT_TOK*4 tokens, slice of rows).
+ * Each wave keeps RTT_TOK token rows in registers as f32 (lane l holds the
+ * chunks l, l+64, ..; H = 512*NCH) and the workgroup streams its weight rows
+ * through LDS, RTT_EB rows per stage, converted to f32 once and read by all
+ * four waves, double buffered.  The arithmetic per (token, row) is the R64
+ * order above (same chains, same tree), so logits are identical to k_router.
+ */
+#define RTT_TOK 4
+#define RTT_MIN_N 16
+#define RTT_EB 4
+
+template <bool XBF16, bool NORM, int NCH>
+__global__ __launch_bounds__(256, 2) void k_router_tile(RouterArgs a, int rows_per_wg) {
+    constexpr int H = 512 * NCH;
+    __shared__ __attribute__((aligned(16))) float s_w[2][RTT_EB][H];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r0 = blockIdx.y * rows_per_wg;
+    const int r1 = min(a.E + 1, r0 + rows_per_wg);
+    if (r0 >= r1) return;
+    const int tb = blockIdx.x * (4 * RTT_TOK) + wave * RTT_TOK;
+
+    /* this wave's tokens (rows past n repeat token n-1; they are not stored) */
+    float v[RTT_TOK][NCH][8];
+#pragma unroll
+    for (int t = 0; t < RTT_TOK; t++) {
+        const size_t roff = (size_t)min(tb + t, a.n - 1) * H;
+#pragma unroll
+        for (int i = 0; i < NCH; i++) load_x8<XBF16>(a.x, roff, lane + 64 * i, v[t][i]);
+        if (NORM) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NCH; i++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) ss = fmaf(v[t][i][j], v[t][i][j], ss);
+            ss = qk_group_sum<64>(ss);
+            const float r = 1.0f / sqrtf(ss / (float)H + a.eps);
+#pragma unroll
+            for (int i = 0; i < NCH; i++) {
+                const float4 *nw = (const float4 *)a.norm_w + 2 * (lane + 64 * i);
+                const float4 w0 = qk_ld(nw), w1 = qk_ld(nw + 1);
+                const float wn[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[t][i][j] = (v[t][i][j] * r) * wn[j];
+                if (blockIdx.y == 0 && a.xn && tb + t < a.n) {
+                    float4 *o = (float4 *)(a.xn + (size_t)(tb + t) * H) + 2 * (lane + 64 * i);
+                    o[0] = make_float4(v[t][i][0], v[t][i][1], v[t][i][2], v[t][i][3]);
+                    o[1] = make_float4(v[t][i][4], v[t][i][5], v[t][i][6], v[t][i][7]);
+                }
+            }
+        }
+    }
+
+    /* weight staging: stage row rr, 16-byte chunk q of the row, per thread
+     * RTT_EB*H/8/256 chunks */
+    constexpr int SCH = RTT_EB * H / 8 / 256;
+    uint4 wst[SCH];
+    auto load_rows = [&](int rb) {
+#pragma unroll
+        for (int i = 0; i < SCH; i++) {
+            const int ci = tid + 256 * i;
+            const int rr = ci / (H / 8), q = ci - rr * (H / 8);
+            const int row = min(rb + rr, r1 - 1);
+            const uint16_t *wrow = row < a.E ? a.router_w + (size_t)row * H : a.sh_gate_w;
+            wst[i] = qk_ld((const uint4 *)wrow + q);
+        }
+    };
+    auto store_rows = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < SCH; i++) {
+            const int ci = tid + 256 * i;
+            const int rr = ci / (H / 8), q = ci - rr * (H / 8);
+            const uint4 d = wst[i];
+            float4 *o = (float4 *)&s_w[buf][rr][8 * q];
+            o[0] = make_float4(qk_bf16_lo(d.x), qk_bf16_hi(d.x), qk_bf16_lo(d.y), qk_bf16_hi(d.y));
+            o[1] = make_float4(qk_bf16_lo(d.z), qk_bf16_hi(d.z), qk_bf16_lo(d.w), qk_bf16_hi(d.w));
+        }
+    };
+
+    load_rows(r0);
+    store_rows(0);
+    if (r0 + RTT_EB < r1) load_rows(r0 + RTT_EB);
+    __syncthreads();
+    for (int rb = r0, it = 0; rb < r1; rb += RTT_EB, it++) {
+        const int buf = it & 1;
+#pragma unroll 1
+        for (int rr = 0; rr < RTT_EB; rr++) {
+            float acc[RTT_TOK];
+#pragma unroll
+            for (int t = 0; t < RTT_TOK; t++) acc[t] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NCH; i++) {
+                const float4 *wp = (const float4 *)&s_w[buf][rr][8 * (lane + 64 * i)];
+                const float4 w0 = wp[0], w1 = wp[1];
+                const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+#pragma unroll
+                    for (int t = 0; t < RTT_TOK; t++) acc[t] = fmaf(v[t][i][j], w[j], acc[t]);
+            }
+#pragma unroll
+            for (int t = 0; t < RTT_TOK; t++) acc[t] = qk_group_sum<64>(acc[t]);
+            const int row = rb + rr;
+            if (lane < RTT_TOK && row < r1) {
+                float val = acc[0];
+#pragma unroll
+                for (int t = 1; t < RTT_TOK; t++) val = lane == t ? acc[t] : val;
+                if (tb + lane < a.n) {
+                    if (row < a.E && a.router_bias) val = val + a.router_bias[row];
+                    a.logits[(size_t)(tb + lane) * (a.E + 1) + row] = val;
+                }
+            }
+        }
+        /* the next stage goes into the other buffer, last read one stage ago */
+        if (rb + RTT_EB < r1) {
+            store_rows(buf ^ 1);
+            if (rb + 2 * RTT_EB < r1) load_rows(rb + 2 * RTT_EB);
+        }
+        __syncthreads();
+    }
+}
+
 /* chunks per lane rounded up to a power of two */
 static int router_nch(int H) {
     const int per = (H / 8 + 63) / 64;
@@ -173,8 +295,33 @@ extern "C" int qk_launch_router(const qmoe_layer_weights *W, qk_shape s, const v
     a.E = s.E;
     a.n = n;
     a.eps = s.eps;
-    dim3 grid((s.E + 1 + 3) / 4, (n + RT_TB - 1) / RT_TB);
     hipStream_t st = (hipStream_t)stream;
+    if (n >= RTT_MIN_N && s.H % 512 == 0 && s.H <= 2048) {
+        /* tiled: about two workgroups per CU, rows split into slices of whole stages */
+        const int tblocks = (n + 4 * RTT_TOK - 1) / (4 * RTT_TOK);
+        const int stages = (s.E + 1 + RTT_EB - 1) / RTT_EB;
+        int slices = 512 / tblocks;
+        slices = slices < 1 ? 1 : (slices > stages ? stages : slices);
+        const int rows = (stages + slices - 1) / slices * RTT_EB;
+        slices = (s.E + 1 + rows - 1) / rows;
+        dim3 grid(tblocks, slices);
+        const int nch = s.H / 512;
+        const bool nrm = W->norm_w != nullptr;
+#define RTT_L(XB, NR, NC) hipLaunchKernelGGL((k_router_tile<XB, NR, NC>), grid, dim3(256), 0, st, a, rows)
+#define RTT_N(XB, NR) \
+    do { if (nch == 1) RTT_L(XB, NR, 1); else if (nch == 2) RTT_L(XB, NR, 2); else RTT_L(XB, NR, 4); } while (0)
+        if (x_bf16) {
+            if (nrm) RTT_N(true, true);
+            else RTT_N(true, false);
+        } else {
+            if (nrm) RTT_N(false, true);
+            else RTT_N(false, false);
+        }
+#undef RTT_N
+#undef RTT_L
+        return QK_CHECK_LAUNCH();
+    }
+    dim3 grid((s.E + 1 + 3) / 4, (n + RT_TB - 1) / RT_TB);
     const int nch = router_nch(s.H);
     RT_DISPATCH4(k_router, x_bf16, W->norm_w != nullptr, nch, grid, a);
     return QK_CHECK_LAUNCH();
@@ -454,33 +601,38 @@ __global__ void k_setbits(const int32_t *idx, int n, int k, int E, int NW, uint3
     atomicOr(&bits[(size_t)e * NW + (t >> 5)], 1u << (t & 31));
 }
 
-/* one workgroup: per-expert word prefixes (wave per expert) + offsets;
- * perm entries past the dispatched total (slots with invalid expert ids)
- * are set to -1 */
-__global__ __launch_bounds__(1024) void k_count_offsets(const uint32_t *bits, int32_t *wprefix,
-                                                        int E, int NW, int32_t *offsets,
-                                                        int32_t *segtab, int32_t *perm, int nk) {
-    __shared__ int s_cnt[QK_MAX_EXPERTS];
-    __shared__ int s_scan[16];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int e = wave; e < E; e += 16) {
-        int base = 0;
-        for (int w0 = 0; w0 < NW; w0 += 64) {
-            int wd = w0 + lane;
-            int c = wd < NW ? __popc(bits[(size_t)e * NW + wd]) : 0;
-            int inc = c;
+/* per-expert word prefixes, one wave per expert; the expert's token count
+ * goes to cnt[e] */
+__global__ __launch_bounds__(1024) void k_word_prefix(const uint32_t *bits, int32_t *wprefix, int E,
+                                                      int NW, int32_t *cnt) {
+    const int lane = threadIdx.x & 63;
+    const int e = blockIdx.x * 16 + (threadIdx.x >> 6);
+    if (e >= E) return;
+    int base = 0;
+    for (int w0 = 0; w0 < NW; w0 += 64) {
+        const int wd = w0 + lane;
+        const int c = wd < NW ? __popc(bits[(size_t)e * NW + wd]) : 0;
+        int inc = c;
 #pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                int u = __shfl_up(inc, o, QK_WAVE);
-                if (lane >= o) inc += u;
-            }
-            if (wd < NW) wprefix[(size_t)e * NW + wd] = base + inc - c;
-            base += __shfl(inc, 63, QK_WAVE);
+        for (int o = 1; o < 64; o <<= 1) {
+            const int u = __shfl_up(inc, o, QK_WAVE);
+            if (lane >= o) inc += u;
         }
-        if (lane == 0) s_cnt[e] = base;
+        if (wd < NW) wprefix[(size_t)e * NW + wd] = base + inc - c;
+        base += __shfl(inc, 63, QK_WAVE);
     }
+    if (lane == 0) cnt[e] = base;
+}
+
+/* one workgroup: counts (held in `offsets` on entry) -> offsets and the
+ * segment table; perm entries past the dispatched total (slots with invalid
+ * expert ids) are set to -1 */
+__global__ __launch_bounds__(1024) void k_count_offsets(int E, int32_t *offsets, int32_t *segtab,
+                                                        int32_t *perm, int nk) {
+    __shared__ int s_scan[16];
+    const int tid = threadIdx.x;
+    int cnt[1] = {tid < E ? offsets[tid] : 0};
     __syncthreads();
-    int cnt[1] = {tid < E ? s_cnt[tid] : 0};
     const int total = counts_to_offsets<1024>(cnt, E, s_scan, offsets, segtab, nullptr);
     for (int i = total + tid; i < nk; i += 1024) perm[i] = -1;
 }
@@ -512,8 +664,9 @@ extern "C" int qk_launch_dispatch(qk_shape s, int n, const int32_t *idx, int32_t
     const int nk = n * s.k;
     hipLaunchKernelGGL(k_setbits, dim3((nk + 255) / 256), dim3(256), 0, st, idx, n, s.k, s.E, NW,
                        bits);
-    hipLaunchKernelGGL(k_count_offsets, dim3(1), dim3(1024), 0, st, (const uint32_t *)bits, wprefix,
-                       s.E, NW, offsets, segtab, perm, nk);
+    hipLaunchKernelGGL(k_word_prefix, dim3((s.E + 15) / 16), dim3(1024), 0, st, (const uint32_t *)bits,
+                       wprefix, s.E, NW, offsets);
+    hipLaunchKernelGGL(k_count_offsets, dim3(1), dim3(1024), 0, st, s.E, offsets, segtab, perm, nk);
     hipLaunchKernelGGL(k_scatter, dim3((nk + 255) / 256), dim3(256), 0, st, idx, n, s.k, s.E, NW,
                        (const uint32_t *)bits, (const int32_t *)wprefix, (const int32_t *)offsets,
                        perm, pos);

@@ -241,6 +241,28 @@ def test_layer_f32_activations(torch_dev):
     _layer_case(torch, dev, "decode", n=160, n_check=6, seed_x=13, x_bf16=False)
 
 
+@pytest.mark.parametrize("n,bf16", [(40, False), (37, True)])
+def test_router_norm_many_tokens(torch_dev, n, bf16):
+    """RMSNorm + router for a block of tokens (the tiled router): normalised
+    rows, logits and top-k bit-exact with the oracle"""
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    w = pkg.WORKLOADS["depth48"]
+    say(f"case: RMSNorm + router, n={n}, bf16={bf16}")
+    h = orc.gen_x(n, w.hidden, 21, bf16=bf16)
+    rb = orc.zipf_bias(w.n_experts, w.zipf_s, w.zipf_scale, w.seed * 1000003)
+    with pkg.MoeContext.for_workload(w, max_tokens=n, n_layers=1) as ctx:
+        ctx.synth_layer(0, w.seed, with_norm=True, router_bias=rb)
+        Lr = orc.Layer(w.hidden, w.n_experts, w.top_k, w.moe_inter, seed=w.seed, layer=0,
+                       with_norm=True, router_bias=rb, only_experts=[])
+        rt = Lr.route(h, bf16)
+        g = ctx.router_norm(0, to_dev(h, torch, dev))
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(g["xn"].cpu().numpy(), rt["xn"])
+        np.testing.assert_array_equal(g["logits"].cpu().numpy(), rt["logits"])
+        np.testing.assert_array_equal(g["idx"].cpu().numpy(), rt["idx"])
+
+
 def test_depth_stack_norm_residual(torch_dev):
     """four stacked layers of the depth workload: h <- h + MoE(RMSNorm(h))"""
     torch, dev = torch_dev
