@@ -153,6 +153,18 @@ __device__ __forceinline__ uint32_t qk_dpp_u(uint32_t v) {
 #define QK_DPP_HALF_MIRROR 0x141
 #define QK_DPP_MIRROR 0x140
 
+/* the value of lane l^16 (l^32): v_permlane16_swap (32_swap) with both
+ * operands v leaves own and partner rows in its two results, so their xor
+ * with v is the partner */
+__device__ __forceinline__ uint32_t qk_xor16_u(uint32_t v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return r[0] ^ r[1] ^ v;
+}
+__device__ __forceinline__ uint32_t qk_xor32_u(uint32_t v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return r[0] ^ r[1] ^ v;
+}
+
 /* sum over aligned groups of WIDTH lanes (WIDTH a power of 2, <= 64) */
 template <int WIDTH>
 __device__ __forceinline__ float qk_group_sum(float v) {
@@ -160,8 +172,8 @@ __device__ __forceinline__ float qk_group_sum(float v) {
     if (WIDTH >= 4) v = v + qk_dpp<QK_DPP_XOR2>(v);
     if (WIDTH >= 8) v = v + qk_dpp<QK_DPP_HALF_MIRROR>(v);
     if (WIDTH >= 16) v = v + qk_dpp<QK_DPP_MIRROR>(v);
-    if (WIDTH >= 32) v = v + __shfl_xor(v, 16, QK_WAVE);
-    if (WIDTH >= 64) v = v + __shfl_xor(v, 32, QK_WAVE);
+    if (WIDTH >= 32) v = v + __uint_as_float(qk_xor16_u(__float_as_uint(v)));
+    if (WIDTH >= 64) v = v + __uint_as_float(qk_xor32_u(__float_as_uint(v)));
     return v;
 }
 

@@ -24,10 +24,10 @@ __device__ __forceinline__ float qk_ordkey_value(uint32_t o) {
  * inequality, so equal keys keep ascending e.  Then k rounds: the wave
  * maximum of the lane heads; the lowest lane holding it wins (lane order is
  * e order, so that is the lowest e among equal keys) and pops its head.
- * Round s yields slot s.  Lane s < k returns slot s's expert and weight
- * w_s = exp(v_s - v_0) / sum_j exp(v_j - v_0), summed in slot order
- * (model.c:1305-1318).  Padding entries (e >= E) carry key 0 and valid
- * keys are at least 1, so padding is never chosen while E >= k.
+ * Round s yields slot s.  Lane s < k returns slot s's expert
+ * and weight w_s = exp(v_s - v_0) / sum_j exp(v_j - v_0), summed in slot
+ * order (model.c:1305-1318).  Padding entries (e >= E) carry key 0 and
+ * valid keys are at least 1, so padding is never chosen while E >= k.
  */
 template <int PL>
 __device__ __forceinline__ void wave_topk(const float *row, int E, int k, int lane, int &my_id,
@@ -35,11 +35,29 @@ __device__ __forceinline__ void wave_topk(const float *row, int E, int k, int la
     static_assert(PL <= 16, "at most 16 experts per lane");
     uint32_t kk[PL];
     int ii[PL]; /* local index i of each sorted entry */
+    float lv[PL];
+    if (PL % 4 == 0 && E % PL == 0) {
+        /* whole float4s; lanes past the row read its last PL values (unused) */
+        const int e0 = min(lane * PL, E - PL);
+#pragma unroll
+        for (int i = 0; i < PL; i += 4) {
+            const float4 q = qk_ld((const float4 *)(row + e0 + i));
+            lv[i] = q.x;
+            lv[(i + 1) % PL] = q.y;
+            lv[(i + 2) % PL] = q.z;
+            lv[(i + 3) % PL] = q.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < PL; i++) {
+            const int e = lane * PL + i;
+            lv[i] = qk_ld(row + (e < E ? e : E - 1));
+        }
+    }
 #pragma unroll
     for (int i = 0; i < PL; i++) {
         const int e = lane * PL + i;
-        const float v = qk_ld(row + (e < E ? e : E - 1));
-        kk[i] = e < E ? max(qk_ordkey(v), 1u) : 0u;
+        kk[i] = e < E ? max(qk_ordkey(lv[i]), 1u) : 0u;
         ii[i] = i;
     }
 #pragma unroll
