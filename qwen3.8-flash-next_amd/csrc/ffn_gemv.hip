@@ -161,6 +161,9 @@ __global__ __launch_bounds__(256) void k_q4gemv(GemvArgs a) {
         if (a.seglist) {
             if (seg >= nlist) break;
             seg = qk_ld(a.seglist + 1 + seg);
+        } else if (task >= (int)gridDim.x && seg > min(max(u_raw, 0), a.E)) {
+            /* past the first task the segment count is known */
+            break;
         }
         const bool shared = seg == 0;
         if (seg > a.E) break;
@@ -341,6 +344,9 @@ __global__ __launch_bounds__(64 * DC_WAVES) void k_down_combine(DcArgs a,
     /* y for this workgroup's rows, one segment per wave at a time */
     for (int seg = wave; seg <= a.E; seg += DC_WAVES) {
         const bool shared = seg == 0;
+        /* past the first round the segment count is known: stop before
+         * reading an entry that does not exist */
+        if (seg >= DC_WAVES && seg > min(max(u_raw, 0), a.E)) break;
         int p0, m;
         const uint32_t *q;
         const uint16_t *sc, *bi;

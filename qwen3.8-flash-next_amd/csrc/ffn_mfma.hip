@@ -305,12 +305,14 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS> &sm, int 
 template <bool DOWN, int TERMS>
 __global__ __launch_bounds__(256, 2) void k_mm(MmArgs a) {
     __shared__ __attribute__((aligned(16))) MmSmem<TERMS> sm;
-    /* consecutive column tiles of one task go to one XCD (workgroups are
-     * dealt round-robin over the 8 XCDs), so they share its L2 */
+    /* workgroups are dealt round-robin over the 8 XCDs: workgroup L runs on
+     * XCD L%8.  Tasks are interleaved over the XCDs (task 8j+x on XCD x) so
+     * the real tasks, fewer than the grid allows for, spread over all of
+     * them, and the column tiles of one task are consecutive workgroups of
+     * one XCD, sharing its L2 */
     const int L = blockIdx.x;
-    const int per_xcd = gridDim.x >> 3;
-    const int lin = (L & 7) * per_xcd + (L >> 3);
-    const int mt = lin / a.ntile, nt = lin - mt * a.ntile;
+    const int i8 = L >> 3;
+    const int mt = (i8 / a.ntile) * 8 + (L & 7), nt = i8 - (i8 / a.ntile) * a.ntile;
     if (mt >= qk_ld(a.tasks)) return;
     const int4 tk = qk_ld((const int4 *)(a.tasks + MM_TASK_HDR) + mt);
     const int e = tk.x, p0 = tk.y, m = tk.z, mstart = tk.w * MM_BM;
@@ -428,8 +430,8 @@ __global__ __launch_bounds__(1024) void k_mm_tasks(const int32_t *segtab, int n,
 }
 
 static int mm_launch(const MmArgs &a, bool down, int terms, int max_tasks, hipStream_t st) {
-    long long wgs = (long long)max_tasks * a.ntile;
-    wgs = (wgs + 7) / 8 * 8;
+    /* every (task, column tile) once: 8 * ceil(max_tasks / 8) tasks */
+    const long long wgs = (long long)(max_tasks + 7) / 8 * 8 * a.ntile;
     if (wgs <= 0) return 0;
     if (down) {
         if (terms == 2) hipLaunchKernelGGL((k_mm<true, 2>), dim3((unsigned)wgs), dim3(256), 0, st, a);
