@@ -177,6 +177,43 @@ __device__ __forceinline__ float qk_group_sum(float v) {
     return v;
 }
 
+/*
+ * Wave sums of 16 per-lane partials v[0..15] at once, with the pairing of
+ * qk_group_sum<64> (partners l^1, l^2, l^4, l^8, l^16, l^32 in that order),
+ * so every sum has the same bits as qk_group_sum<64> of that partial.  At
+ * the level of partner l^(2^b) a lane keeps the half of its values selected
+ * by lane bit b and adds the partner's copy of that half (the partner keeps
+ * the other half), so after four levels lane l holds partial
+ * d = qk_rs16_index(l) summed over its 16-lane row, and the l^16 and l^32
+ * levels add the other rows' sums of the same d.
+ */
+__device__ __forceinline__ int qk_rs16_index(int lane) {
+    return ((lane & 1) << 3) | ((lane & 2) << 1) | ((lane & 4) >> 1) | ((lane & 8) >> 3);
+}
+template <int N, typename XCH>
+__device__ __forceinline__ void qk_rs_level(const float *in, float *out, bool hi, XCH xch) {
+#pragma unroll
+    for (int i = 0; i < N / 2; i++) {
+        const float keep = hi ? in[i + N / 2] : in[i];
+        const float send = hi ? in[i] : in[i + N / 2];
+        out[i] = keep + xch(send);
+    }
+}
+__device__ __forceinline__ float qk_reduce_scatter16(const float v[16], int lane) {
+    float a8[8], a4[4], a2[2], a1[1];
+    qk_rs_level<16>(v, a8, lane & 1, [](float x) { return qk_dpp<QK_DPP_XOR1>(x); });
+    qk_rs_level<8>(a8, a4, lane & 2, [](float x) { return qk_dpp<QK_DPP_XOR2>(x); });
+    qk_rs_level<4>(a4, a2, lane & 4, [](float x) {
+        /* ds_swizzle bit mode: and 0x1f, or 0, xor 4 (within 32 lanes) */
+        return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x101F));
+    });
+    qk_rs_level<2>(a2, a1, lane & 8, [](float x) { return qk_dpp<0x128>(x); /* row_ror:8 = l^8 in a row */ });
+    float s = a1[0];
+    s = s + __uint_as_float(qk_xor16_u(__float_as_uint(s)));
+    s = s + __uint_as_float(qk_xor32_u(__float_as_uint(s)));
+    return s;
+}
+
 /* wave-wide max / min of a u32, result uniform.  After the four in-row
  * DPP steps every lane of a row holds the row's extreme; row_bcast:15 then
  * carries row r's lane 15 into row r+1 (rows 1 and 3 written) and

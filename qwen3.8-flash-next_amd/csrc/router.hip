@@ -141,6 +141,7 @@ __global__ __launch_bounds__(256) void k_router(RouterArgs a) {
 #define RTT_TOK 4
 #define RTT_MIN_N 16
 #define RTT_EB 4
+static_assert(RTT_TOK * RTT_EB == 16, "the tile router reduces 16 partials per lane");
 
 template <bool XBF16, bool NORM, int NCH>
 __global__ __launch_bounds__(256, 2) void k_router_tile(RouterArgs a, int rows_per_wg) {
@@ -215,7 +216,9 @@ __global__ __launch_bounds__(256, 2) void k_router_tile(RouterArgs a, int rows_p
     __syncthreads();
     for (int rb = r0, it = 0; rb < r1; rb += RTT_EB, it++) {
         const int buf = it & 1;
-#pragma unroll 1
+        /* partial sums of this lane, d = t*RTT_EB + rr */
+        float part[RTT_TOK * RTT_EB];
+#pragma unroll
         for (int rr = 0; rr < RTT_EB; rr++) {
             float acc[RTT_TOK];
 #pragma unroll
@@ -231,16 +234,18 @@ __global__ __launch_bounds__(256, 2) void k_router_tile(RouterArgs a, int rows_p
                     for (int t = 0; t < RTT_TOK; t++) acc[t] = fmaf(v[t][i][j], w[j], acc[t]);
             }
 #pragma unroll
-            for (int t = 0; t < RTT_TOK; t++) acc[t] = qk_group_sum<64>(acc[t]);
-            const int row = rb + rr;
-            if (lane < RTT_TOK && row < r1) {
-                float val = acc[0];
-#pragma unroll
-                for (int t = 1; t < RTT_TOK; t++) val = lane == t ? acc[t] : val;
-                if (tb + lane < a.n) {
-                    if (row < a.E && a.router_bias) val = val + a.router_bias[row];
-                    a.logits[(size_t)(tb + lane) * (a.E + 1) + row] = val;
-                }
+            for (int t = 0; t < RTT_TOK; t++) part[t * RTT_EB + rr] = acc[t];
+            __builtin_amdgcn_sched_barrier(0); /* one row's LDS reads at a time */
+        }
+        /* the 16 wave sums, each in the R64 tree's pairing, spread over lanes */
+        const float val = qk_reduce_scatter16(part, lane);
+        {
+            const int d = qk_rs16_index(lane);
+            const int t = d / RTT_EB, row = rb + d % RTT_EB;
+            if (lane < 16 && row < r1 && tb + t < a.n) {
+                float o = val;
+                if (row < a.E && a.router_bias) o = o + a.router_bias[row];
+                a.logits[(size_t)(tb + t) * (a.E + 1) + row] = o;
             }
         }
         /* the next stage goes into the other buffer, last read one stage ago */
