@@ -35,6 +35,10 @@ struct qmoe_ctx {
     qmoe_layer_slot *layers;
     size_t layer_bytes;
     int last_n; /* token count of the last qmoe_layer_forward, -1 if none */
+    /* second stream for the GEMV kernels of small segments, which run beside
+     * the MFMA kernels of large ones (fork/join with two events) */
+    hipStream_t aux;
+    hipEvent_t ev_fork, ev_join;
     /* byte offsets of each tensor inside a layer allocation */
     size_t off[24];
 };
@@ -207,6 +211,12 @@ int qmoe_create(qmoe_ctx **out, const qmoe_config *cfg, qmoe_err *err) {
     c->sc.ahi = (uint16_t *)(b + offs[14]);
     c->sc.alo = (uint16_t *)(b + offs[15]);
     c->sc.ag = (float *)(b + offs[16]);
+    if (hip_fail(err, (int)hipStreamCreateWithFlags(&c->aux, hipStreamNonBlocking), "stream") ||
+        hip_fail(err, (int)hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming), "event") ||
+        hip_fail(err, (int)hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming), "event")) {
+        qmoe_destroy(c);
+        return -1;
+    }
     *out = c;
     return 0;
 }
@@ -217,6 +227,9 @@ void qmoe_destroy(qmoe_ctx *c) {
         for (int l = 0; l < c->cfg.n_layers; l++)
             if (c->layers[l].mem) hipFree(c->layers[l].mem);
     if (c->scratch_mem) hipFree(c->scratch_mem);
+    if (c->ev_fork) hipEventDestroy(c->ev_fork);
+    if (c->ev_join) hipEventDestroy(c->ev_join);
+    if (c->aux) hipStreamDestroy(c->aux);
     if (c->host_x_dev) hipFree(c->host_x_dev);
     if (c->host_out_dev) hipFree(c->host_out_dev);
     free(c->layers);
@@ -482,6 +495,18 @@ int qmoe_router(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n, float
  * their activations as packed operand planes (qk_launch_pack_rows).  The
  * MFMA task list is built from the segment table unless the caller says it
  * is already current. */
+/* the GEMV kernels of small segments go to the context's second stream,
+ * after everything already on `stream` (fork), and `stream` waits for them
+ * before its next launch (join); both work under stream capture */
+static int fork(qmoe_ctx *c, void *stream, qmoe_err *err) {
+    if (hip_fail(err, (int)hipEventRecord(c->ev_fork, (hipStream_t)stream), "fork record")) return -1;
+    return hip_fail(err, (int)hipStreamWaitEvent(c->aux, c->ev_fork, 0), "fork wait");
+}
+static int join(qmoe_ctx *c, void *stream, qmoe_err *err) {
+    if (hip_fail(err, (int)hipEventRecord(c->ev_join, c->aux), "join record")) return -1;
+    return hip_fail(err, (int)hipStreamWaitEvent((hipStream_t)stream, c->ev_join, 0), "join wait");
+}
+
 static int mfma_usable(const qmoe_ctx *c, int n, int stage) {
     const int ok = stage == 2 ? qk_mfma_down_ok(c->shape) : qk_mfma_gateup_ok(c->shape, stage == 0);
     return ok && n * (c->shape.k + 1) >= QK_MFMA_MIN_M;
@@ -500,13 +525,15 @@ static int run_gateup(qmoe_ctx *c, const qmoe_layer_weights *W, const void *x, i
                                  stream);
         if (hip_fail(err, rc, "pack x")) return -1;
     }
+    if (mm && fork(c, stream, err)) return -1;
     rc = qk_launch_gateup(W, s, x, xbf, n, perm, segtab, mm ? QK_MFMA_MIN_M : 0,
-                          mm ? qk_mfma_small_list(s, n, c->sc.tasks) : NULL, h, stream);
+                          mm ? qk_mfma_small_list(s, n, c->sc.tasks) : NULL, h, mm ? c->aux : stream);
     if (hip_fail(err, rc, "gateup")) return -1;
     if (mm) {
         rc = qk_launch_gateup_mfma(W, s, c->sc.ahi, xbf ? NULL : c->sc.alo, c->sc.ag, n, perm,
                                    c->sc.tasks, h, stream);
         if (hip_fail(err, rc, "gateup mfma")) return -1;
+        if (join(c, stream, err)) return -1;
     }
     return 0;
 }
@@ -525,12 +552,14 @@ static int run_down(qmoe_ctx *c, const qmoe_layer_weights *W, const float *h, in
                                  stream);
         if (hip_fail(err, rc, "pack h")) return -1;
     }
+    if (mm && fork(c, stream, err)) return -1;
     rc = qk_launch_down(W, s, h, n, segtab, mm ? QK_MFMA_MIN_M : 0,
-                        mm ? qk_mfma_small_list(s, n, c->sc.tasks) : NULL, y, stream);
+                        mm ? qk_mfma_small_list(s, n, c->sc.tasks) : NULL, y, mm ? c->aux : stream);
     if (hip_fail(err, rc, "down")) return -1;
     if (mm) {
         rc = qk_launch_down_mfma(W, s, c->sc.ahi, c->sc.alo, c->sc.ag, n, c->sc.tasks, y, stream);
         if (hip_fail(err, rc, "down mfma")) return -1;
+        if (join(c, stream, err)) return -1;
     }
     return 0;
 }

@@ -573,6 +573,21 @@ __global__ __launch_bounds__(1024) void k_topk_dispatch_small(SmallDispArgs a) {
     dispatch_block<1024>(s_idx, a.tk.n, a.tk.k, a.tk.E, a.offsets, a.perm, a.pos, a.segtab);
 }
 
+/* the same dispatch with the expert ids read from global memory (after a
+ * separate k_topk launch, one wave per token over many workgroups) */
+__global__ __launch_bounds__(1024) void k_dispatch_small(const int32_t *idx, int n, int k, int E,
+                                                         int32_t *offsets, int32_t *perm,
+                                                         int32_t *pos, int32_t *segtab) {
+    __shared__ int32_t s_idx[QK_SMALL_NK];
+    for (int f = threadIdx.x; f < n * k; f += 1024) s_idx[f] = qk_ld(idx + f);
+    __syncthreads();
+    dispatch_block<1024>(s_idx, n, k, E, offsets, perm, pos, segtab);
+}
+
+/* tokens above which the top-k runs as its own launch (one wave per token)
+ * rather than 16 waves of one workgroup taking turns */
+#define QK_TOPK_SPLIT_N 16
+
 extern "C" int qk_launch_topk_dispatch_small(qk_shape s, int n, const float *logits,
                                              float *logits_out, int32_t *idx, float *w, float *sg,
                                              int32_t *offsets, int32_t *perm, int32_t *pos,
@@ -583,9 +598,14 @@ extern "C" int qk_launch_topk_dispatch_small(qk_shape s, int n, const float *log
     hipStream_t st = (hipStream_t)stream;
     if (n == 1) {
         TK_DISPATCH(k_topk_dispatch_one, topk_pl(s.E), dim3(1), dim3(64), a);
-    } else {
+    } else if (n <= QK_TOPK_SPLIT_N) {
         if (!offsets) return (int)hipErrorInvalidValue;
         TK_DISPATCH(k_topk_dispatch_small, topk_pl(s.E), dim3(1), dim3(1024), a);
+    } else {
+        if (!offsets) return (int)hipErrorInvalidValue;
+        TK_DISPATCH(k_topk, topk_pl(s.E), dim3((n + 3) / 4), dim3(256), a.tk);
+        hipLaunchKernelGGL(k_dispatch_small, dim3(1), dim3(1024), 0, st, (const int32_t *)idx, n, s.k,
+                           s.E, offsets, perm, pos, segtab);
     }
     return QK_CHECK_LAUNCH();
 }
