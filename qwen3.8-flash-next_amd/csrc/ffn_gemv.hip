@@ -199,12 +199,17 @@ __global__ __launch_bounds__(256) void k_q4gemv(GemvArgs a) {
         const int rbase = rb * RB + wave * RPWAVE;
         /* input row of the segment's first token: its (possible) perm load
          * goes first, so waiting for it does not wait for the weights */
+        /* the first 64 slots of the segment, one per lane, read at once so
+         * that each token's activation load does not wait for its slot */
+        const bool gathered = !a.in_by_pos && !shared && a.n != 1;
+        int pv = 0;
+        if (gathered && lane < m) pv = qk_ld(a.perm + p0 + lane);
         auto in_row_of = [&](int j) -> long {
             const int p = p0 + j;
             if (a.in_by_pos) return p;
             if (shared) return j;
             if (a.n == 1) return 0;
-            const int f = qk_ld(a.perm + p);
+            const int f = j < 64 ? __builtin_amdgcn_readlane(pv, j) : qk_ld(a.perm + p);
             return (f < 0 || f >= a.n * a.k) ? -1 : f / a.k;
         };
         XRaw<P, XBF16> xr;
