@@ -65,10 +65,16 @@ struct MmSmem {
     int row[MM_BM];
 };
 
+/* one code word -> the B operand: bf16 128+q in (q_i, q_{i+4}) pair order,
+ * as qk_codes_to_pairs, built with byte permutes: the low nibbles of the
+ * four bytes (q0, q2, q4, q6) and the high ones (q1, q3, q5, q7) each give
+ * two pairs by interleaving with the byte 0x43 */
 __device__ __forceinline__ qm_bf16x8 qm_codes(uint32_t w) {
-    uint32_t p[4];
-    qk_codes_to_pairs(w, p);
-    return __builtin_bit_cast(qm_bf16x8, make_uint4(p[0], p[1], p[2], p[3]));
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    const uint32_t k = 0x43434343u;
+    return __builtin_bit_cast(qm_bf16x8,
+                              make_uint4(__builtin_amdgcn_perm(k, lo, 0x04020400u), __builtin_amdgcn_perm(k, hi, 0x04020400u),
+                                         __builtin_amdgcn_perm(k, lo, 0x04030401u), __builtin_amdgcn_perm(k, hi, 0x04030401u)));
 }
 
 /* column of tile ct for this lane: gate/up tiles 0,1 = gate, 2,3 = up */
@@ -128,13 +134,21 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS> &sm, int 
         }
     }
 
+    /* element offsets of this thread's staged chunks in group 0 (rows are
+     * fixed for the task; planes hold fewer than 2^31 elements) */
+    uint32_t aoff[ACH];
+#pragma unroll
+    for (int i = 0; i < ACH; i++) {
+        const int ci = tid + 256 * i;
+        aoff[i] = ci < MM_BM * 8 ? (uint32_t)sm.row[ci >> 3] * (uint32_t)a.K + (uint32_t)(ci & 7) * 8u : 0u;
+    }
     uint4 ar[TERMS][ACH];
     auto load_a = [&](int g) {
 #pragma unroll
         for (int i = 0; i < ACH; i++) {
             const int ci = tid + 256 * i;
             if (ci < MM_BM * 8) {
-                const size_t off = (size_t)sm.row[ci >> 3] * a.K + g * 64 + (ci & 7) * 8;
+                const uint32_t off = aoff[i] + (uint32_t)g * 64u;
 #pragma unroll
                 for (int tm = 0; tm < TERMS; tm++) ar[tm][i] = qk_ld((const uint4 *)(a.ap[tm] + off));
             }

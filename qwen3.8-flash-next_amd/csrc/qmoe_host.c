@@ -509,7 +509,9 @@ static int join(qmoe_ctx *c, void *stream, qmoe_err *err) {
 
 static int mfma_usable(const qmoe_ctx *c, int n, int stage) {
     const int ok = stage == 2 ? qk_mfma_down_ok(c->shape) : qk_mfma_gateup_ok(c->shape, stage == 0);
-    return ok && n * (c->shape.k + 1) >= QK_MFMA_MIN_M;
+    /* the kernels address the operand planes with 32-bit element offsets */
+    const size_t elems = stage == 2 ? (size_t)n * (c->shape.k + 1) * c->shape.I : (size_t)n * c->shape.H;
+    return ok && elems < ((size_t)1 << 31) && n * (c->shape.k + 1) >= QK_MFMA_MIN_M;
 }
 
 static int run_gateup(qmoe_ctx *c, const qmoe_layer_weights *W, const void *x, int xbf, int n,
