@@ -124,7 +124,7 @@ __device__ __forceinline__ void router_rows(const RouterArgs &a, int row, int t0
 
 template <bool XBF16, bool NORM, int NCH>
 __global__ __launch_bounds__(256) void k_router(RouterArgs a) {
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (row > a.E) return;
     const int t0 = blockIdx.y * RT_TB;
     router_rows<XBF16, NORM, NCH>(a, row, t0, min(a.n, t0 + RT_TB));
@@ -265,13 +265,17 @@ static int router_nch(int H) {
     return p;
 }
 
+#ifndef RT_WPB
+#define RT_WPB 2
+#endif
 #define RT_DISPATCH(KERNEL, XB, NORM, NCH, GRID, ARGS)                                         \
     do {                                                                                       \
-        if (NCH == 1) hipLaunchKernelGGL((KERNEL<XB, NORM, 1>), GRID, dim3(256), 0, st, ARGS);  \
-        else if (NCH == 2) hipLaunchKernelGGL((KERNEL<XB, NORM, 2>), GRID, dim3(256), 0, st, ARGS); \
-        else if (NCH == 4) hipLaunchKernelGGL((KERNEL<XB, NORM, 4>), GRID, dim3(256), 0, st, ARGS); \
-        else if (NCH == 8) hipLaunchKernelGGL((KERNEL<XB, NORM, 8>), GRID, dim3(256), 0, st, ARGS); \
-        else hipLaunchKernelGGL((KERNEL<XB, NORM, 16>), GRID, dim3(256), 0, st, ARGS);          \
+        const dim3 blk(64 * RT_WPB);                                                           \
+        if (NCH == 1) hipLaunchKernelGGL((KERNEL<XB, NORM, 1>), GRID, blk, 0, st, ARGS);        \
+        else if (NCH == 2) hipLaunchKernelGGL((KERNEL<XB, NORM, 2>), GRID, blk, 0, st, ARGS);   \
+        else if (NCH == 4) hipLaunchKernelGGL((KERNEL<XB, NORM, 4>), GRID, blk, 0, st, ARGS);   \
+        else if (NCH == 8) hipLaunchKernelGGL((KERNEL<XB, NORM, 8>), GRID, blk, 0, st, ARGS);   \
+        else hipLaunchKernelGGL((KERNEL<XB, NORM, 16>), GRID, blk, 0, st, ARGS);                \
     } while (0)
 
 #define RT_DISPATCH4(KERNEL, XBF, NRM, NCH, GRID, ARGS)                                         \
@@ -326,7 +330,9 @@ extern "C" int qk_launch_router(const qmoe_layer_weights *W, qk_shape s, const v
 #undef RTT_L
         return QK_CHECK_LAUNCH();
     }
-    dim3 grid((s.E + 1 + 3) / 4, (n + RT_TB - 1) / RT_TB);
+    /* one wave per (row, block of RT_TB tokens); RT_WPB waves per workgroup
+     * (few, so that a one-token router spreads over every CU) */
+    dim3 grid((s.E + 1 + RT_WPB - 1) / RT_WPB, (n + RT_TB - 1) / RT_TB);
     const int nch = router_nch(s.H);
     RT_DISPATCH4(k_router, x_bf16, W->norm_w != nullptr, nch, grid, a);
     return QK_CHECK_LAUNCH();
