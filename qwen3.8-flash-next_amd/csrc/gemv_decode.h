@@ -67,12 +67,16 @@ struct DecRouteOut {
  * TK = 0: segment j >= 1 is entry j-1 of `segtab` (any table made by the
  *         dispatch for one token).
  * TK = PL > 0: the workgroups of routed segments select the top k of the
- *         router logits themselves (wave 0, wave_topk<PL>, broadcast through
- *         LDS) instead of waiting for a separate top-k launch; segment j is
- *         the j-th smallest selected expert id, at dispatch position j-1.
- *         Workgroup (segment 1, block 0) writes the routing (idx, w,
- *         sigmoid gate, perm, pos, segment table) for the down projection
- *         and the combine, in the form the dispatch produces.
+ *         router logits themselves (wave 0, WaveTopk<PL>, broadcast through
+ *         LDS) instead of waiting for a separate top-k launch.  Segment j
+ *         computes the expert of slot j-1: wave 0 runs the selection rounds
+ *         up to that slot, every wave starts its weight loads, and wave 0
+ *         runs the remaining rounds under the loads to find the expert's
+ *         dispatch position (its rank among the selected ids), which only
+ *         the stores need.  Workgroup (segment 1, block 0) writes the
+ *         routing (idx, w, sigmoid gate, perm, pos, segment table) for the
+ *         down projection and the combine, in the form the dispatch
+ *         produces.
  */
 template <int LPR, int CPL, int RIT, bool XBF16, int TK = 0>
 __global__ __launch_bounds__(256) void k_gateup_dec(DecArgs a, const int32_t *__restrict__ segtab,
@@ -106,41 +110,35 @@ __global__ __launch_bounds__(256) void k_gateup_dec(DecArgs a, const int32_t *__
     }
 
     const bool shared = seg == 0;
+    const int slot = seg - 1;
     bool valid;
     int e, p0;
+    __shared__ int s_ep[2]; /* the slot's expert, then its dispatch position */
+    WaveTopk<(TK > 0 ? TK : 1)> tks;
+    uint32_t my_key = 0u; /* lane r < k: slot r's key and expert, once known */
+    int my_id = 0x7FFFFFFF;
     if (TK > 0) {
-        /* fused top-k: the expert of this segment */
-        __shared__ int s_e[QK_MAX_TOPK];
         if (!shared) {
             if (wave == 0) {
-                int id;
-                float wt;
-                wave_topk<(TK > 0 ? TK : 1)>(ro.logits, a.E, a.k, lane, id, wt);
-                const int my_id = lane < a.k ? id : 0x7FFFFFFF;
-                int rank = 0;
-                for (int s2 = 0; s2 < a.k; s2++) rank += __builtin_amdgcn_readlane(my_id, s2) < my_id ? 1 : 0;
-                if (lane < a.k) s_e[rank] = id;
-                if (seg == 1 && rb == 0) {
-                    if (lane < a.k) {
-                        ro.idx[lane] = id;
-                        ro.w[lane] = wt;
-                        ro.perm[rank] = lane;
-                        ro.pos[lane] = rank;
-                        ro.segtab[1 + 3 * rank] = id;
-                        ro.segtab[2 + 3 * rank] = rank;
-                        ro.segtab[3 + 3 * rank] = 1;
+                tks.init(ro.logits, a.E, lane);
+                int es = 0;
+                for (int r = 0; r <= slot; r++) {
+                    uint32_t m;
+                    int ei;
+                    tks.next(lane, m, ei);
+                    if (lane == r) {
+                        my_key = m;
+                        my_id = ei;
                     }
-                    if (lane == 0) {
-                        ro.segtab[0] = a.k;
-                        ro.sg[0] = qk_sigmoid(qk_ld(ro.logits + a.E));
-                    }
+                    es = ei;
                 }
+                if (lane == 0) s_ep[0] = es;
             }
             __syncthreads();
         }
         valid = true;
-        e = shared ? 0 : s_e[seg - 1];
-        p0 = shared ? a.k : seg - 1;
+        e = shared ? 0 : s_ep[0];
+        p0 = a.k;
     } else {
         /* segment entry and count, read together; bitwise tests (no branches) */
         const int s1 = shared ? 1 : seg;
@@ -177,6 +175,43 @@ __global__ __launch_bounds__(256) void k_gateup_dec(DecArgs a, const int32_t *__
         }
     }
     __builtin_amdgcn_sched_barrier(0);
+
+    if (TK > 0 && !shared) {
+        /* under the loads: the remaining rounds, then this slot's rank */
+        if (wave == 0) {
+            for (int r = slot + 1; r < a.k; r++) {
+                uint32_t m;
+                int ei;
+                tks.next(lane, m, ei);
+                if (lane == r) {
+                    my_key = m;
+                    my_id = ei;
+                }
+            }
+            const int rank = (int)__popcll(__ballot(my_id < e));
+            if (lane == 0) s_ep[1] = rank;
+            if (seg == 1 && rb == 0) {
+                const float wt = topk_weight(my_key, a.k, lane);
+                int rk = 0;
+                for (int s2 = 0; s2 < a.k; s2++) rk += __builtin_amdgcn_readlane(my_id, s2) < my_id ? 1 : 0;
+                if (lane < a.k) {
+                    ro.idx[lane] = my_id;
+                    ro.w[lane] = wt;
+                    ro.perm[rk] = lane;
+                    ro.pos[lane] = rk;
+                    ro.segtab[1 + 3 * rk] = my_id;
+                    ro.segtab[2 + 3 * rk] = rk;
+                    ro.segtab[3 + 3 * rk] = 1;
+                }
+                if (lane == 0) {
+                    ro.segtab[0] = a.k;
+                    ro.sg[0] = qk_sigmoid(qk_ld(ro.logits + a.E));
+                }
+            }
+        }
+        __syncthreads();
+        p0 = s_ep[1];
+    }
 
     /* activation pairs (x_i, x_{i+4}) per 8 columns, and chunk sums */
     uint32_t hp[CPL][16];
