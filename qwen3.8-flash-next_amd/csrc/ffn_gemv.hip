@@ -109,6 +109,74 @@ __device__ __forceinline__ void convert_xraw(const XRaw<P, XBF16> &xr, int K, in
     }
 }
 
+/*
+ * f32 activations shared by the RPW = 64/LPR lanes that use one chunk (one
+ * chunk per lane, RPW = 2 or 4): lane (sub, rsub) loads and converts NG =
+ * 4/RPW of the chunk's four 8-column groups, the wave exchanges pairs and
+ * group sums through LDS (36 words per chunk: 16 hi, 16 lo, 4 sums), and
+ * every lane ends with exactly what convert_xraw gives for its chunk.
+ */
+template <int NG>
+struct XShare {
+    float4 f[2 * NG];
+};
+
+template <int NG>
+__device__ __forceinline__ void load_xshare(const float *x, size_t row, int K, int sub, int rsub,
+                                            XShare<NG> &xq) {
+    const int CH = K >> 5;
+    const int c = sub < CH ? sub : 0;
+    const float4 *src = (const float4 *)(x + row * K) + 8 * c + 2 * NG * rsub;
+#pragma unroll
+    for (int i = 0; i < 2 * NG; i++) xq.f[i] = qk_ld(src + i);
+}
+
+/* LDS written by other lanes of this wave: order the accesses (a wave's LDS
+ * operations complete in issue order, so no hardware wait is needed) */
+__device__ __forceinline__ void qk_wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int LPR, int NG>
+__device__ __forceinline__ void convert_xshare(const XShare<NG> &xq, int K, int sub, int rsub,
+                                               uint32_t *wbuf, XPairs<LPR, 1, false> &xp) {
+    const int CH = K >> 5;
+    const bool ok = sub < CH;
+    uint32_t *cb = wbuf + 36 * sub;
+#pragma unroll
+    for (int gi = 0; gi < NG; gi++) {
+        const int g = NG * rsub + gi;
+        const float4 a0 = xq.f[2 * gi], a1 = xq.f[2 * gi + 1];
+        float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        if (!ok)
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = 0.0f;
+        uint32_t hi[4], lo[4];
+        const float gs = qk_f32x8_pairs(v, hi, lo);
+        *(uint4 *)(cb + 4 * g) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        *(uint4 *)(cb + 16 + 4 * g) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+        ((float *)cb)[32 + g] = gs;
+    }
+    qk_wave_lds_sync();
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const uint4 h = *(const uint4 *)(cb + 4 * w), l = *(const uint4 *)(cb + 16 + 4 * w);
+        xp.hi[0][4 * w] = h.x;
+        xp.hi[0][4 * w + 1] = h.y;
+        xp.hi[0][4 * w + 2] = h.z;
+        xp.hi[0][4 * w + 3] = h.w;
+        xp.lo[0][4 * w] = l.x;
+        xp.lo[0][4 * w + 1] = l.y;
+        xp.lo[0][4 * w + 2] = l.z;
+        xp.lo[0][4 * w + 3] = l.w;
+    }
+    const float4 gsv = *(const float4 *)(cb + 32);
+    xp.xs[0] = (((0.0f + gsv.x) + gsv.y) + gsv.z) + gsv.w;
+    qk_wave_lds_sync();
+}
+
 /* sum over one 32-code chunk of x * (128 + q) */
 template <int LPR, int P, bool XBF16>
 __device__ __forceinline__ float chunk_dot(uint4 q4, const XPairs<LPR, P, XBF16> &xp, int ps) {
@@ -310,11 +378,15 @@ __global__ __launch_bounds__(64 * DC_WAVES) void k_down_combine(DcArgs a,
                                                                 const int32_t *__restrict__ segtab) {
     constexpr int RPW = 64 / LPR;
     constexpr int RB = RPW * GV_RITER;
+    constexpr bool SHARE = P == 1 && (RPW == 2 || RPW == 4); /* convert_xshare */
+    constexpr int NG = 4 / (RPW < 4 ? RPW : 4);
     extern __shared__ float dc_lds[];
     const int nk = a.n * a.k;
     float *s_y = dc_lds;                              /* [(nk + n) * RB] */
     float *s_w = s_y + (nk + a.n) * RB;               /* [nk] slot weights, position order */
     int *s_p = (int *)(s_w + nk);                     /* [nk] slot positions, ascending */
+    /* per wave, when SHARE: [LPR][36] activation exchange (16-byte aligned) */
+    uint32_t *s_x = (uint32_t *)dc_lds + ((((nk + a.n) * RB + 2 * nk) + 3) & ~3);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int sub = lane % LPR, rsub = lane / LPR;
     const int CH = a.K >> 5, G = a.K >> 6;
@@ -373,7 +445,11 @@ __global__ __launch_bounds__(64 * DC_WAVES) void k_down_combine(DcArgs a,
             bi = a.sb;
         }
         XRaw<P, false> xr;
-        if (m > 0) load_xraw<LPR, P, false>(a.h, (size_t)p0, a.K, sub, xr);
+        XShare<NG> xq;
+        if (m > 0) {
+            if (SHARE) load_xshare<NG>(a.h, (size_t)p0, a.K, sub, rsub, xq);
+            else load_xraw<LPR, P, false>(a.h, (size_t)p0, a.K, sub, xr);
+        }
         uint4 wq[GV_RITER][P];
         uint16_t rs[GV_RITER][P], rbi[GV_RITER][P];
         float ws[GV_RITER][P], wb[GV_RITER][P];
@@ -405,8 +481,14 @@ __global__ __launch_bounds__(64 * DC_WAVES) void k_down_combine(DcArgs a,
         for (int j = 0; j < m; j++) {
             const int p = p0 + j;
             XPairs<LPR, P, false> xp;
-            convert_xraw<LPR, P, false>(xr, a.K, sub, xp);
-            if (j + 1 < m) load_xraw<LPR, P, false>(a.h, (size_t)(p + 1), a.K, sub, xr);
+            if (SHARE) {
+                convert_xshare<LPR, NG>(xq, a.K, sub, rsub, s_x + wave * LPR * 36,
+                                        (XPairs<LPR, 1, false> &)xp);
+                if (j + 1 < m) load_xshare<NG>(a.h, (size_t)(p + 1), a.K, sub, rsub, xq);
+            } else {
+                convert_xraw<LPR, P, false>(xr, a.K, sub, xp);
+                if (j + 1 < m) load_xraw<LPR, P, false>(a.h, (size_t)(p + 1), a.K, sub, xr);
+            }
 #pragma unroll
             for (int it = 0; it < GV_RITER; it++) {
                 const float v = qk_group_sum<LPR>(row_part<LPR, P, false>(wq[it], ws[it], wb[it], xp));
@@ -493,9 +575,13 @@ extern "C" int qk_launch_gateup_topk(const qmoe_layer_weights *W, qk_shape s, co
  * not apply (too many tokens for one workgroup's LDS) */
 extern "C" size_t qk_down_combine_lds(qk_shape s, int n) {
     if (n <= 0 || n > QK_DC_MAX_N) return 0;
-    const int rb = (64 / pick_lpr(s.I)) * GV_RITER;
+    const int lpr = pick_lpr(s.I);
+    const int rb = (64 / lpr) * GV_RITER;
+    const int P = (s.I / 32 + lpr - 1) / lpr;
+    const bool share = P == 1 && (lpr == 32 || lpr == 16); /* the kernel's SHARE */
     const size_t nk = (size_t)n * s.k;
-    const size_t bytes = ((nk + n) * rb + 2 * nk) * 4;
+    const size_t words = (((nk + n) * rb + 2 * nk + 3) & ~(size_t)3) + (share ? DC_WAVES * lpr * 36 : 0);
+    const size_t bytes = words * 4;
     return bytes <= QK_DC_MAX_LDS ? bytes : 0;
 }
 

@@ -113,20 +113,27 @@ __device__ __forceinline__ uint32_t qk_cvt_pk_bf16(float a, float b) {
 
 /* eight f32 activations -> hi and lo bf16 pair sets in (x_i, x_{i+4})
  * order with x ~= hi + lo (hi = RNE(x), lo = RNE(x - hi); x - hi is exact;
- * relative residual <= 2^-17); xsum accumulates sum (hi + lo) with
- * v_dot2 against (1, 1), hi pairs then lo pairs, i = 0..3 */
-__device__ __forceinline__ void qk_f32x8_to_pairs(const float x[8], uint32_t hi[4], uint32_t lo[4],
-                                                  float &xsum) {
+ * relative residual <= 2^-17); returns the group sum of (hi + lo): v_dot2
+ * against (1, 1) from 0, hi pair then lo pair, i = 0..3.  A chunk sum is
+ * 0 + g0 + g1 + g2 + g3 over its four groups, left to right, wherever the
+ * groups were converted. */
+__device__ __forceinline__ float qk_f32x8_pairs(const float x[8], uint32_t hi[4], uint32_t lo[4]) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         hi[i] = qk_cvt_pk_bf16(x[i], x[i + 4]);
         lo[i] = qk_cvt_pk_bf16(x[i] - qk_bf16_lo(hi[i]), x[i + 4] - qk_bf16_hi(hi[i]));
     }
+    float g = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        xsum = qk_dot2(hi[i], QK_BF16_ONES, xsum);
-        xsum = qk_dot2(lo[i], QK_BF16_ONES, xsum);
+        g = qk_dot2(hi[i], QK_BF16_ONES, g);
+        g = qk_dot2(lo[i], QK_BF16_ONES, g);
     }
+    return g;
+}
+__device__ __forceinline__ void qk_f32x8_to_pairs(const float x[8], uint32_t hi[4], uint32_t lo[4],
+                                                  float &xsum) {
+    xsum = xsum + qk_f32x8_pairs(x, hi, lo);
 }
 
 __device__ __forceinline__ float qk_silu(float v) { return v / (1.0f + expf(-v)); }

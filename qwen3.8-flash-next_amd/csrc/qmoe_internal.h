@@ -120,7 +120,7 @@ int qk_launch_gateup_topk(const qmoe_layer_weights *W, qk_shape s, const void *x
  * bit-identical to qk_launch_down + qk_launch_combine.  qk_down_combine_lds
  * returns its LDS bytes, 0 when it does not apply. */
 #define QK_DC_MAX_N 8
-#define QK_DC_MAX_LDS 32768
+#define QK_DC_MAX_LDS 65536
 size_t qk_down_combine_lds(qk_shape s, int n);
 int qk_launch_down_combine(const qmoe_layer_weights *W, qk_shape s, const float *h, int n,
                            const int32_t *segtab, const int32_t *pos, const float *w,
