@@ -102,6 +102,58 @@ void qmoe_destroy(qmoe_ctx *ctx);
  * Replaces mw_load + experts_load (model.c:213-272, 536-674). */
 int qmoe_upload_layer(qmoe_ctx *ctx, int layer, const qmoe_layer_weights *host, qmoe_err *err);
 
+/* ------------------------------------------------------------ checkpoint
+ * An index over the *.safetensors files of a checkpoint directory, as the
+ * reference's st_index_open / st_find / st_read_tensor
+ * (c/src/safetensors.h:51-63, safetensors.c:57-324): every header is parsed
+ * and validated (dtype, shape, data range inside the file, no overlapping
+ * ranges, no duplicate names); a leading "language_model." is dropped from
+ * stored names, and a lookup of "model.X" also tries "language_model.model.X".
+ * Host only: no HIP call is made by the index functions. */
+typedef struct qmoe_st qmoe_st;
+
+/* element types, in the order of the reference's st_dtype (safetensors.h:10-25) */
+enum {
+    QMOE_ST_BOOL, QMOE_ST_U8, QMOE_ST_I8, QMOE_ST_U16, QMOE_ST_I16, QMOE_ST_U32, QMOE_ST_I32,
+    QMOE_ST_U64, QMOE_ST_I64, QMOE_ST_F16, QMOE_ST_BF16, QMOE_ST_F32, QMOE_ST_F64, QMOE_ST_COUNT
+};
+
+/* one indexed tensor (st_tensor, safetensors.h:27-35) */
+typedef struct {
+    int dtype;        /* QMOE_ST_* */
+    int ndim;
+    int64_t shape[8];
+    int file;         /* index of the file, in sorted file-name order */
+    uint64_t offset;  /* absolute byte offset of the data in that file */
+    uint64_t nbytes;
+} qmoe_st_tensor;
+
+int qmoe_st_open(qmoe_st **ix, const char *dir, qmoe_err *err);
+void qmoe_st_close(qmoe_st *ix);
+size_t qmoe_st_count(const qmoe_st *ix);
+/* the i-th indexed name in sorted order, or NULL past the end */
+const char *qmoe_st_name(const qmoe_st *ix, size_t i);
+/* 1 and *out filled when the tensor exists, else 0 */
+int qmoe_st_find(const qmoe_st *ix, const char *name, qmoe_st_tensor *out);
+/* reads a whole tensor into host memory dst of cap bytes */
+int qmoe_st_read(const qmoe_st *ix, const char *name, void *dst, size_t cap, qmoe_err *err);
+int qmoe_st_dtype_size(int dtype);
+const char *qmoe_st_dtype_name(int dtype);
+
+/* Uploads the MoE tensors of checkpoint layer `model_layer` into context
+ * layer `layer`, replacing mw_load (model.c:213-272) for mlp.gate,
+ * shared_expert.*, shared_expert_gate (model.c:1902-1912) and
+ * experts_load (model.c:539-674) for switch_mlp.{gate,up,down}_proj.
+ * Every tensor is found and checked against the context's config before
+ * any is copied: expert and shared-expert projections must be q4 (U32
+ * codes with BF16 .scales; a missing .biases reads as zero, as model.c:250-256),
+ * group size = the config's; the router and the shared-expert gate must be
+ * dense BF16.  Scales and biases stay bf16 in HBM (exact; the reference
+ * widens them to f32 at load).  The layer has no logit bias and no
+ * pre-router norm.  Copies go through a 64 MiB pinned staging buffer. */
+int qmoe_upload_layer_st(qmoe_ctx *ctx, int layer, const qmoe_st *ix, int model_layer,
+                         qmoe_err *err);
+
 /* Fills one layer in HBM with the seeded synthetic distribution used by the
  * benchmarks: codes U{0..15}, scales N(0,0.02), biases N(0,0.01) (bf16),
  * router and shared-expert gate N(0,0.02) (bf16), norm weight ones when

@@ -43,13 +43,6 @@ struct qmoe_ctx {
     size_t off[24];
 };
 
-/* tensor order inside a layer allocation */
-enum {
-    T_ROUTER_W, T_ROUTER_BIAS, T_GATE_Q, T_GATE_S, T_GATE_B, T_UP_Q, T_UP_S, T_UP_B,
-    T_DOWN_Q, T_DOWN_S, T_DOWN_B, T_SH_GATE_Q, T_SH_GATE_S, T_SH_GATE_B, T_SH_UP_Q, T_SH_UP_S,
-    T_SH_UP_B, T_SH_DOWN_Q, T_SH_DOWN_S, T_SH_DOWN_B, T_SHGATE_W, T_NORM_W, T_COUNT
-};
-
 static void set_err(qmoe_err *err, const char *fmt, ...) {
     if (!err) return;
     va_list ap;
@@ -76,18 +69,18 @@ static void tensor_shape(const qmoe_config *c, int t, size_t *count, size_t *esi
     const size_t g = (size_t)c->group_size;
     size_t n = 0, es = 2;
     switch (t) {
-    case T_ROUTER_W: n = E * H; break;
-    case T_ROUTER_BIAS: n = E; es = 4; break;
-    case T_GATE_Q: case T_UP_Q: n = E * I * H / 8; es = 4; break;
-    case T_GATE_S: case T_GATE_B: case T_UP_S: case T_UP_B: n = E * I * H / g; break;
-    case T_DOWN_Q: n = E * H * I / 8; es = 4; break;
-    case T_DOWN_S: case T_DOWN_B: n = E * H * I / g; break;
-    case T_SH_GATE_Q: case T_SH_UP_Q: n = I * H / 8; es = 4; break;
-    case T_SH_GATE_S: case T_SH_GATE_B: case T_SH_UP_S: case T_SH_UP_B: n = I * H / g; break;
-    case T_SH_DOWN_Q: n = H * I / 8; es = 4; break;
-    case T_SH_DOWN_S: case T_SH_DOWN_B: n = H * I / g; break;
-    case T_SHGATE_W: n = H; break;
-    case T_NORM_W: n = H; es = 4; break;
+    case QH_T_ROUTER_W: n = E * H; break;
+    case QH_T_ROUTER_BIAS: n = E; es = 4; break;
+    case QH_T_GATE_Q: case QH_T_UP_Q: n = E * I * H / 8; es = 4; break;
+    case QH_T_GATE_S: case QH_T_GATE_B: case QH_T_UP_S: case QH_T_UP_B: n = E * I * H / g; break;
+    case QH_T_DOWN_Q: n = E * H * I / 8; es = 4; break;
+    case QH_T_DOWN_S: case QH_T_DOWN_B: n = E * H * I / g; break;
+    case QH_T_SH_GATE_Q: case QH_T_SH_UP_Q: n = I * H / 8; es = 4; break;
+    case QH_T_SH_GATE_S: case QH_T_SH_GATE_B: case QH_T_SH_UP_S: case QH_T_SH_UP_B: n = I * H / g; break;
+    case QH_T_SH_DOWN_Q: n = H * I / 8; es = 4; break;
+    case QH_T_SH_DOWN_S: case QH_T_SH_DOWN_B: n = H * I / g; break;
+    case QH_T_SHGATE_W: n = H; break;
+    case QH_T_NORM_W: n = H; es = 4; break;
     }
     *count = n;
     *esize = es;
@@ -159,7 +152,7 @@ int qmoe_create(qmoe_ctx **out, const qmoe_config *cfg, qmoe_err *err) {
     }
     /* layer layout */
     size_t o = 0;
-    for (int t = 0; t < T_COUNT; t++) {
+    for (int t = 0; t < QH_T_COUNT; t++) {
         size_t n, es;
         tensor_shape(cfg, t, &n, &es);
         c->off[t] = o;
@@ -258,61 +251,61 @@ static int ensure_layer_mem(qmoe_ctx *c, int layer, qmoe_err *err) {
     if (hip_fail(err, (int)hipMalloc(&L->mem, c->layer_bytes), "hipMalloc(layer)")) return -1;
     char *b = (char *)L->mem;
     qmoe_layer_weights *d = &L->dev;
-    d->router_w = (const uint16_t *)(b + c->off[T_ROUTER_W]);
+    d->router_w = (const uint16_t *)(b + c->off[QH_T_ROUTER_W]);
     d->router_bias = NULL;
-    d->gate_q = (const uint32_t *)(b + c->off[T_GATE_Q]);
-    d->gate_s = (const uint16_t *)(b + c->off[T_GATE_S]);
-    d->gate_b = (const uint16_t *)(b + c->off[T_GATE_B]);
-    d->up_q = (const uint32_t *)(b + c->off[T_UP_Q]);
-    d->up_s = (const uint16_t *)(b + c->off[T_UP_S]);
-    d->up_b = (const uint16_t *)(b + c->off[T_UP_B]);
-    d->down_q = (const uint32_t *)(b + c->off[T_DOWN_Q]);
-    d->down_s = (const uint16_t *)(b + c->off[T_DOWN_S]);
-    d->down_b = (const uint16_t *)(b + c->off[T_DOWN_B]);
-    d->sh_gate_q = (const uint32_t *)(b + c->off[T_SH_GATE_Q]);
-    d->sh_gate_s = (const uint16_t *)(b + c->off[T_SH_GATE_S]);
-    d->sh_gate_b = (const uint16_t *)(b + c->off[T_SH_GATE_B]);
-    d->sh_up_q = (const uint32_t *)(b + c->off[T_SH_UP_Q]);
-    d->sh_up_s = (const uint16_t *)(b + c->off[T_SH_UP_S]);
-    d->sh_up_b = (const uint16_t *)(b + c->off[T_SH_UP_B]);
-    d->sh_down_q = (const uint32_t *)(b + c->off[T_SH_DOWN_Q]);
-    d->sh_down_s = (const uint16_t *)(b + c->off[T_SH_DOWN_S]);
-    d->sh_down_b = (const uint16_t *)(b + c->off[T_SH_DOWN_B]);
-    d->sh_gate_w = (const uint16_t *)(b + c->off[T_SHGATE_W]);
+    d->gate_q = (const uint32_t *)(b + c->off[QH_T_GATE_Q]);
+    d->gate_s = (const uint16_t *)(b + c->off[QH_T_GATE_S]);
+    d->gate_b = (const uint16_t *)(b + c->off[QH_T_GATE_B]);
+    d->up_q = (const uint32_t *)(b + c->off[QH_T_UP_Q]);
+    d->up_s = (const uint16_t *)(b + c->off[QH_T_UP_S]);
+    d->up_b = (const uint16_t *)(b + c->off[QH_T_UP_B]);
+    d->down_q = (const uint32_t *)(b + c->off[QH_T_DOWN_Q]);
+    d->down_s = (const uint16_t *)(b + c->off[QH_T_DOWN_S]);
+    d->down_b = (const uint16_t *)(b + c->off[QH_T_DOWN_B]);
+    d->sh_gate_q = (const uint32_t *)(b + c->off[QH_T_SH_GATE_Q]);
+    d->sh_gate_s = (const uint16_t *)(b + c->off[QH_T_SH_GATE_S]);
+    d->sh_gate_b = (const uint16_t *)(b + c->off[QH_T_SH_GATE_B]);
+    d->sh_up_q = (const uint32_t *)(b + c->off[QH_T_SH_UP_Q]);
+    d->sh_up_s = (const uint16_t *)(b + c->off[QH_T_SH_UP_S]);
+    d->sh_up_b = (const uint16_t *)(b + c->off[QH_T_SH_UP_B]);
+    d->sh_down_q = (const uint32_t *)(b + c->off[QH_T_SH_DOWN_Q]);
+    d->sh_down_s = (const uint16_t *)(b + c->off[QH_T_SH_DOWN_S]);
+    d->sh_down_b = (const uint16_t *)(b + c->off[QH_T_SH_DOWN_B]);
+    d->sh_gate_w = (const uint16_t *)(b + c->off[QH_T_SHGATE_W]);
     d->norm_w = NULL;
     return 0;
 }
 
 static const void *host_tensor(const qmoe_layer_weights *h, int t) {
     switch (t) {
-    case T_ROUTER_W: return h->router_w;
-    case T_ROUTER_BIAS: return h->router_bias;
-    case T_GATE_Q: return h->gate_q;
-    case T_GATE_S: return h->gate_s;
-    case T_GATE_B: return h->gate_b;
-    case T_UP_Q: return h->up_q;
-    case T_UP_S: return h->up_s;
-    case T_UP_B: return h->up_b;
-    case T_DOWN_Q: return h->down_q;
-    case T_DOWN_S: return h->down_s;
-    case T_DOWN_B: return h->down_b;
-    case T_SH_GATE_Q: return h->sh_gate_q;
-    case T_SH_GATE_S: return h->sh_gate_s;
-    case T_SH_GATE_B: return h->sh_gate_b;
-    case T_SH_UP_Q: return h->sh_up_q;
-    case T_SH_UP_S: return h->sh_up_s;
-    case T_SH_UP_B: return h->sh_up_b;
-    case T_SH_DOWN_Q: return h->sh_down_q;
-    case T_SH_DOWN_S: return h->sh_down_s;
-    case T_SH_DOWN_B: return h->sh_down_b;
-    case T_SHGATE_W: return h->sh_gate_w;
-    case T_NORM_W: return h->norm_w;
+    case QH_T_ROUTER_W: return h->router_w;
+    case QH_T_ROUTER_BIAS: return h->router_bias;
+    case QH_T_GATE_Q: return h->gate_q;
+    case QH_T_GATE_S: return h->gate_s;
+    case QH_T_GATE_B: return h->gate_b;
+    case QH_T_UP_Q: return h->up_q;
+    case QH_T_UP_S: return h->up_s;
+    case QH_T_UP_B: return h->up_b;
+    case QH_T_DOWN_Q: return h->down_q;
+    case QH_T_DOWN_S: return h->down_s;
+    case QH_T_DOWN_B: return h->down_b;
+    case QH_T_SH_GATE_Q: return h->sh_gate_q;
+    case QH_T_SH_GATE_S: return h->sh_gate_s;
+    case QH_T_SH_GATE_B: return h->sh_gate_b;
+    case QH_T_SH_UP_Q: return h->sh_up_q;
+    case QH_T_SH_UP_S: return h->sh_up_s;
+    case QH_T_SH_UP_B: return h->sh_up_b;
+    case QH_T_SH_DOWN_Q: return h->sh_down_q;
+    case QH_T_SH_DOWN_S: return h->sh_down_s;
+    case QH_T_SH_DOWN_B: return h->sh_down_b;
+    case QH_T_SHGATE_W: return h->sh_gate_w;
+    case QH_T_NORM_W: return h->norm_w;
     }
     return NULL;
 }
 
 static const char *tensor_name(int t) {
-    static const char *names[T_COUNT] = {
+    static const char *names[QH_T_COUNT] = {
         "router_w", "router_bias", "gate_q", "gate_s", "gate_b", "up_q", "up_s", "up_b",
         "down_q", "down_s", "down_b", "sh_gate_q", "sh_gate_s", "sh_gate_b", "sh_up_q",
         "sh_up_s", "sh_up_b", "sh_down_q", "sh_down_s", "sh_down_b", "sh_gate_w", "norm_w"};
@@ -326,8 +319,8 @@ int qmoe_upload_layer(qmoe_ctx *c, int layer, const qmoe_layer_weights *h, qmoe_
         set_err(err, "weights pointer is NULL");
         return -1;
     }
-    for (int t = 0; t < T_COUNT; t++) {
-        if (t == T_ROUTER_BIAS || t == T_NORM_W) continue;
+    for (int t = 0; t < QH_T_COUNT; t++) {
+        if (t == QH_T_ROUTER_BIAS || t == QH_T_NORM_W) continue;
         if (!host_tensor(h, t)) {
             set_err(err, "missing tensor %s for layer %d", tensor_name(t), layer);
             return -1;
@@ -337,7 +330,7 @@ int qmoe_upload_layer(qmoe_ctx *c, int layer, const qmoe_layer_weights *h, qmoe_
     qmoe_layer_slot *L = &c->layers[layer];
     L->ready = 0;
     char *b = (char *)L->mem;
-    for (int t = 0; t < T_COUNT; t++) {
+    for (int t = 0; t < QH_T_COUNT; t++) {
         const void *src = host_tensor(h, t);
         if (!src) continue;
         size_t n, es;
@@ -346,10 +339,61 @@ int qmoe_upload_layer(qmoe_ctx *c, int layer, const qmoe_layer_weights *h, qmoe_
                      "hipMemcpy(upload)"))
             return -1;
     }
-    L->dev.router_bias = h->router_bias ? (const float *)(b + c->off[T_ROUTER_BIAS]) : NULL;
-    L->dev.norm_w = h->norm_w ? (const float *)(b + c->off[T_NORM_W]) : NULL;
+    L->dev.router_bias = h->router_bias ? (const float *)(b + c->off[QH_T_ROUTER_BIAS]) : NULL;
+    L->dev.norm_w = h->norm_w ? (const float *)(b + c->off[QH_T_NORM_W]) : NULL;
     L->ready = 1;
     return 0;
+}
+
+/* ---------------------------------------------- slots for qmoe_st.c */
+
+int qh_ctx_config(qmoe_ctx *c, int layer, qmoe_config *out, qmoe_err *err) {
+    if (check_layer_index(c, layer, err)) return -1;
+    *out = c->cfg;
+    return 0;
+}
+
+int qh_host_alloc(void **p, size_t bytes, qmoe_err *err) {
+    *p = NULL;
+    return hip_fail(err, (int)hipHostMalloc(p, bytes, hipHostMallocDefault), "hipHostMalloc(staging)");
+}
+
+void qh_host_free(void *p) {
+    if (p) (void)hipHostFree(p);
+}
+
+void qh_layer_begin(qmoe_ctx *c, int layer) {
+    if (c->layers[layer].mem) c->layers[layer].ready = 0;
+}
+
+int qh_layer_slot(qmoe_ctx *c, int layer, int t, void **dst, size_t *bytes, qmoe_err *err) {
+    if (t < 0 || t >= QH_T_COUNT) {
+        set_err(err, "tensor slot %d out of range", t);
+        return -1;
+    }
+    if (ensure_layer_mem(c, layer, err)) return -1;
+    c->layers[layer].ready = 0;
+    size_t n, es;
+    tensor_shape(&c->cfg, t, &n, &es);
+    *dst = (char *)c->layers[layer].mem + c->off[t];
+    *bytes = n * es;
+    return 0;
+}
+
+int qh_fill_zero(void *dst, size_t bytes, qmoe_err *err) {
+    return hip_fail(err, (int)hipMemset(dst, 0, bytes), "hipMemset(zero biases)");
+}
+
+int qh_copy_to_device(void *dst, const void *src, size_t bytes, qmoe_err *err) {
+    return hip_fail(err, (int)hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "hipMemcpy(checkpoint)");
+}
+
+void qh_layer_end(qmoe_ctx *c, int layer, int has_bias, int has_norm) {
+    qmoe_layer_slot *L = &c->layers[layer];
+    char *b = (char *)L->mem;
+    L->dev.router_bias = has_bias ? (const float *)(b + c->off[QH_T_ROUTER_BIAS]) : NULL;
+    L->dev.norm_w = has_norm ? (const float *)(b + c->off[QH_T_NORM_W]) : NULL;
+    L->ready = 1;
 }
 
 int qmoe_synth_layer(qmoe_ctx *c, int layer, uint64_t seed, int with_norm, const float *router_bias,
@@ -364,16 +408,16 @@ int qmoe_synth_layer(qmoe_ctx *c, int layer, uint64_t seed, int with_norm, const
         int t, tag, kind;
         float sd;
     } spec[] = {
-        {T_ROUTER_W, QMOE_TAG_ROUTER_W, 0, 0.02f},   {T_GATE_Q, QMOE_TAG_GATE_Q, 2, 0.0f},
-        {T_GATE_S, QMOE_TAG_GATE_S, 0, 0.02f},       {T_GATE_B, QMOE_TAG_GATE_B, 0, 0.01f},
-        {T_UP_Q, QMOE_TAG_UP_Q, 2, 0.0f},            {T_UP_S, QMOE_TAG_UP_S, 0, 0.02f},
-        {T_UP_B, QMOE_TAG_UP_B, 0, 0.01f},           {T_DOWN_Q, QMOE_TAG_DOWN_Q, 2, 0.0f},
-        {T_DOWN_S, QMOE_TAG_DOWN_S, 0, 0.02f},       {T_DOWN_B, QMOE_TAG_DOWN_B, 0, 0.01f},
-        {T_SH_GATE_Q, QMOE_TAG_SH_GATE_Q, 2, 0.0f},  {T_SH_GATE_S, QMOE_TAG_SH_GATE_S, 0, 0.02f},
-        {T_SH_GATE_B, QMOE_TAG_SH_GATE_B, 0, 0.01f}, {T_SH_UP_Q, QMOE_TAG_SH_UP_Q, 2, 0.0f},
-        {T_SH_UP_S, QMOE_TAG_SH_UP_S, 0, 0.02f},     {T_SH_UP_B, QMOE_TAG_SH_UP_B, 0, 0.01f},
-        {T_SH_DOWN_Q, QMOE_TAG_SH_DOWN_Q, 2, 0.0f},  {T_SH_DOWN_S, QMOE_TAG_SH_DOWN_S, 0, 0.02f},
-        {T_SH_DOWN_B, QMOE_TAG_SH_DOWN_B, 0, 0.01f}, {T_SHGATE_W, QMOE_TAG_SHGATE_W, 0, 0.02f},
+        {QH_T_ROUTER_W, QMOE_TAG_ROUTER_W, 0, 0.02f},   {QH_T_GATE_Q, QMOE_TAG_GATE_Q, 2, 0.0f},
+        {QH_T_GATE_S, QMOE_TAG_GATE_S, 0, 0.02f},       {QH_T_GATE_B, QMOE_TAG_GATE_B, 0, 0.01f},
+        {QH_T_UP_Q, QMOE_TAG_UP_Q, 2, 0.0f},            {QH_T_UP_S, QMOE_TAG_UP_S, 0, 0.02f},
+        {QH_T_UP_B, QMOE_TAG_UP_B, 0, 0.01f},           {QH_T_DOWN_Q, QMOE_TAG_DOWN_Q, 2, 0.0f},
+        {QH_T_DOWN_S, QMOE_TAG_DOWN_S, 0, 0.02f},       {QH_T_DOWN_B, QMOE_TAG_DOWN_B, 0, 0.01f},
+        {QH_T_SH_GATE_Q, QMOE_TAG_SH_GATE_Q, 2, 0.0f},  {QH_T_SH_GATE_S, QMOE_TAG_SH_GATE_S, 0, 0.02f},
+        {QH_T_SH_GATE_B, QMOE_TAG_SH_GATE_B, 0, 0.01f}, {QH_T_SH_UP_Q, QMOE_TAG_SH_UP_Q, 2, 0.0f},
+        {QH_T_SH_UP_S, QMOE_TAG_SH_UP_S, 0, 0.02f},     {QH_T_SH_UP_B, QMOE_TAG_SH_UP_B, 0, 0.01f},
+        {QH_T_SH_DOWN_Q, QMOE_TAG_SH_DOWN_Q, 2, 0.0f},  {QH_T_SH_DOWN_S, QMOE_TAG_SH_DOWN_S, 0, 0.02f},
+        {QH_T_SH_DOWN_B, QMOE_TAG_SH_DOWN_B, 0, 0.01f}, {QH_T_SHGATE_W, QMOE_TAG_SHGATE_W, 0, 0.02f},
     };
     for (size_t i = 0; i < sizeof(spec) / sizeof(spec[0]); i++) {
         size_t n, es;
@@ -385,20 +429,20 @@ int qmoe_synth_layer(qmoe_ctx *c, int layer, uint64_t seed, int with_norm, const
             return -1;
     }
     if (with_norm) {
-        if (hip_fail(err, qk_launch_synth(b + c->off[T_NORM_W], (size_t)c->cfg.hidden, 3, 0, 0,
+        if (hip_fail(err, qk_launch_synth(b + c->off[QH_T_NORM_W], (size_t)c->cfg.hidden, 3, 0, 0,
                                           1.0f, NULL),
                      "synth(norm)"))
             return -1;
     }
     if (router_bias) {
-        if (hip_fail(err, (int)hipMemcpy(b + c->off[T_ROUTER_BIAS], router_bias,
+        if (hip_fail(err, (int)hipMemcpy(b + c->off[QH_T_ROUTER_BIAS], router_bias,
                                          (size_t)c->cfg.n_experts * 4, hipMemcpyHostToDevice),
                      "hipMemcpy(router_bias)"))
             return -1;
     }
     if (hip_fail(err, (int)hipDeviceSynchronize(), "synth sync")) return -1;
-    L->dev.router_bias = router_bias ? (const float *)(b + c->off[T_ROUTER_BIAS]) : NULL;
-    L->dev.norm_w = with_norm ? (const float *)(b + c->off[T_NORM_W]) : NULL;
+    L->dev.router_bias = router_bias ? (const float *)(b + c->off[QH_T_ROUTER_BIAS]) : NULL;
+    L->dev.norm_w = with_norm ? (const float *)(b + c->off[QH_T_NORM_W]) : NULL;
     L->ready = 1;
     return 0;
 }

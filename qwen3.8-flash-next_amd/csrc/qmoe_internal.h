@@ -50,6 +50,26 @@ typedef struct {
     float *y;          /* [n*k+n, H] */
 } qk_scratch;
 
+/* tensor slots inside a layer allocation, in allocation order */
+enum {
+    QH_T_ROUTER_W, QH_T_ROUTER_BIAS, QH_T_GATE_Q, QH_T_GATE_S, QH_T_GATE_B, QH_T_UP_Q, QH_T_UP_S,
+    QH_T_UP_B, QH_T_DOWN_Q, QH_T_DOWN_S, QH_T_DOWN_B, QH_T_SH_GATE_Q, QH_T_SH_GATE_S,
+    QH_T_SH_GATE_B, QH_T_SH_UP_Q, QH_T_SH_UP_S, QH_T_SH_UP_B, QH_T_SH_DOWN_Q, QH_T_SH_DOWN_S,
+    QH_T_SH_DOWN_B, QH_T_SHGATE_W, QH_T_NORM_W, QH_T_COUNT
+};
+
+/* host-side access to a context's layer slots (qmoe_host.c), for the
+ * checkpoint reader (qmoe_st.c).  A layer being written is not ready until
+ * qh_layer_end. */
+int qh_ctx_config(qmoe_ctx *c, int layer, qmoe_config *out, qmoe_err *err);
+int qh_host_alloc(void **p, size_t bytes, qmoe_err *err);
+void qh_host_free(void *p);
+void qh_layer_begin(qmoe_ctx *c, int layer);
+int qh_layer_slot(qmoe_ctx *c, int layer, int t, void **dst, size_t *bytes, qmoe_err *err);
+int qh_fill_zero(void *dst, size_t bytes, qmoe_err *err);
+int qh_copy_to_device(void *dst, const void *src, size_t bytes, qmoe_err *err);
+void qh_layer_end(qmoe_ctx *c, int layer, int has_bias, int has_norm);
+
 /* All launchers return a hipError_t value (0 = hipSuccess). */
 
 /* logits[t, 0..E) = x_t . Wr^T (+bias), logits[t, E] = x_t . w_sg; with

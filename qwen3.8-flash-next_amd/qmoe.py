@@ -55,6 +55,15 @@ class QmoeError(RuntimeError):
     pass
 
 
+class QmoeStTensor(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_int), ("ndim", ctypes.c_int), ("shape", ctypes.c_int64 * 8),
+                ("file", ctypes.c_int), ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64)]
+
+
+# safetensors element types (include/qmoe.h QMOE_ST_*)
+ST_DTYPES = ["BOOL", "U8", "I8", "U16", "I16", "U32", "I32", "U64", "I64", "F16", "BF16", "F32", "F64"]
+
+
 # exported symbols and their signatures (must match include/qmoe.h)
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -81,6 +90,15 @@ SIGNATURES = {
     "qmoe_scratch_bytes": (ctypes.c_size_t, [_P]),
     "qmoe_layer_bytes": (ctypes.c_size_t, [_P]),
     "qmoe_version": (ctypes.c_char_p, []),
+    "qmoe_st_open": (_I, [ctypes.POINTER(_P), ctypes.c_char_p, ctypes.POINTER(QmoeErr)]),
+    "qmoe_st_close": (None, [_P]),
+    "qmoe_st_count": (ctypes.c_size_t, [_P]),
+    "qmoe_st_name": (ctypes.c_char_p, [_P, ctypes.c_size_t]),
+    "qmoe_st_find": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(QmoeStTensor)]),
+    "qmoe_st_read": (_I, [_P, ctypes.c_char_p, _P, ctypes.c_size_t, ctypes.POINTER(QmoeErr)]),
+    "qmoe_st_dtype_size": (_I, [_I]),
+    "qmoe_st_dtype_name": (ctypes.c_char_p, [_I]),
+    "qmoe_upload_layer_st": (_I, [_P, _I, _P, _I, ctypes.POINTER(QmoeErr)]),
 }
 
 
@@ -234,6 +252,12 @@ class MoeContext:
         err = QmoeErr()
         _check(lib().qmoe_upload_layer(self._h, layer, ctypes.byref(w), ctypes.byref(err)), err,
                "qmoe_upload_layer")
+
+    def upload_layer_st(self, layer: int, index: "Checkpoint", model_layer: int):
+        """MoE tensors of checkpoint layer `model_layer` -> context layer `layer`"""
+        err = QmoeErr()
+        _check(lib().qmoe_upload_layer_st(self._h, layer, index.handle, model_layer,
+                                          ctypes.byref(err)), err, "qmoe_upload_layer_st")
 
     def synth_layer(self, layer: int, seed: int, with_norm=False, router_bias=None):
         import numpy as np
@@ -404,6 +428,59 @@ class MoeContext:
         _check(lib().qmoe_moe_forward_host(self._h, layer, x.ctypes.data, n, out.ctypes.data,
                                            ctypes.byref(err)), err, "qmoe_moe_forward_host")
         return out
+
+
+class Checkpoint:
+    """index over the *.safetensors files of a directory (qmoe_st_*); host only"""
+
+    def __init__(self, path: str):
+        h = ctypes.c_void_p()
+        err = QmoeErr()
+        _check(lib().qmoe_st_open(ctypes.byref(h), os.fsencode(path), ctypes.byref(err)), err,
+               "qmoe_st_open")
+        self._h = h.value
+
+    @property
+    def handle(self):
+        return self._h
+
+    def close(self):
+        if self._h:
+            lib().qmoe_st_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def names(self) -> list:
+        n = lib().qmoe_st_count(self._h)
+        return [lib().qmoe_st_name(self._h, i).decode() for i in range(n)]
+
+    def info(self, name: str) -> Optional[dict]:
+        t = QmoeStTensor()
+        if not lib().qmoe_st_find(self._h, name.encode(), ctypes.byref(t)):
+            return None
+        return dict(dtype=ST_DTYPES[t.dtype], shape=tuple(t.shape[:t.ndim]), file=t.file,
+                    offset=t.offset, nbytes=t.nbytes)
+
+    def read(self, name: str) -> bytes:
+        t = QmoeStTensor()
+        if not lib().qmoe_st_find(self._h, name.encode(), ctypes.byref(t)):
+            raise QmoeError(f"missing tensor {name}")
+        buf = ctypes.create_string_buffer(max(int(t.nbytes), 1))
+        err = QmoeErr()
+        _check(lib().qmoe_st_read(self._h, name.encode(), buf, len(buf), ctypes.byref(err)), err,
+               "qmoe_st_read")
+        return buf.raw[:t.nbytes]
 
 
 def synth_fill(t, kind: int, seed: int, layer: int, tag: int, start=0, stddev=1.0, stream=None):
