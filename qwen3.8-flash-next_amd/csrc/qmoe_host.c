@@ -534,8 +534,9 @@ int qmoe_router(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n, float
                     "topk");
 }
 
-/* Grouped expert stages.  Segments with at least QK_MFMA_MIN_M rows run on
- * the MFMA kernels, the others on the GEMV kernels.  The MFMA kernels read
+/* Grouped expert stages.  Segments with at least QK_MFMA_MIN_M rows (every
+ * segment from QK_MFMA_ALL_N tokens on) run on the MFMA kernels, the others
+ * on the GEMV kernels.  The MFMA kernels read
  * their activations as packed operand planes (qk_launch_pack_rows).  The
  * MFMA task list is built from the segment table unless the caller says it
  * is already current. */
@@ -558,28 +559,36 @@ static int mfma_usable(const qmoe_ctx *c, int n, int stage) {
     return ok && elems < ((size_t)1 << 31) && n * (c->shape.k + 1) >= QK_MFMA_MIN_M;
 }
 
+/* segments with fewer rows than this go to the GEMV kernels (1 = none) */
+static int mfma_min_m(int n) { return n >= QK_MFMA_ALL_N ? 1 : QK_MFMA_MIN_M; }
+
 static int run_gateup(qmoe_ctx *c, const qmoe_layer_weights *W, const void *x, int xbf, int n,
                       const int32_t *perm, const int32_t *segtab, float *h, void *stream,
                       qmoe_err *err) {
     const int mm = mfma_usable(c, n, xbf ? 0 : 1);
+    const int min_m = mfma_min_m(n);
+    const int gemv = !mm || min_m > 1; /* small segments left to the GEMV */
     const qk_shape s = c->shape;
     int rc;
     if (mm) {
-        rc = qk_launch_mfma_tasks(s, n, segtab, QK_MFMA_MIN_M, c->sc.tasks, stream);
+        rc = qk_launch_mfma_tasks(s, n, segtab, min_m, c->sc.tasks, stream);
         if (hip_fail(err, rc, "mfma tasks")) return -1;
         rc = qk_launch_pack_rows(x, xbf, (size_t)n, s.H, c->sc.ahi, xbf ? NULL : c->sc.alo, c->sc.ag,
                                  stream);
         if (hip_fail(err, rc, "pack x")) return -1;
     }
-    if (mm && fork(c, stream, err)) return -1;
-    rc = qk_launch_gateup(W, s, x, xbf, n, perm, segtab, mm ? QK_MFMA_MIN_M : 0,
-                          mm ? qk_mfma_small_list(s, n, c->sc.tasks) : NULL, h, mm ? c->aux : stream);
-    if (hip_fail(err, rc, "gateup")) return -1;
+    if (mm && gemv && fork(c, stream, err)) return -1;
+    if (gemv) {
+        rc = qk_launch_gateup(W, s, x, xbf, n, perm, segtab, mm ? min_m : 0,
+                              mm ? qk_mfma_small_list(s, n, c->sc.tasks) : NULL, h,
+                              mm ? c->aux : stream);
+        if (hip_fail(err, rc, "gateup")) return -1;
+    }
     if (mm) {
         rc = qk_launch_gateup_mfma(W, s, c->sc.ahi, xbf ? NULL : c->sc.alo, c->sc.ag, n, perm,
                                    c->sc.tasks, h, stream);
         if (hip_fail(err, rc, "gateup mfma")) return -1;
-        if (join(c, stream, err)) return -1;
+        if (gemv && join(c, stream, err)) return -1;
     }
     return 0;
 }
@@ -587,25 +596,30 @@ static int run_gateup(qmoe_ctx *c, const qmoe_layer_weights *W, const void *x, i
 static int run_down(qmoe_ctx *c, const qmoe_layer_weights *W, const float *h, int n,
                     const int32_t *segtab, int tasks_ready, float *y, void *stream, qmoe_err *err) {
     const int mm = mfma_usable(c, n, 2);
+    const int min_m = mfma_min_m(n);
+    const int gemv = !mm || min_m > 1;
     const qk_shape s = c->shape;
     int rc;
     if (mm) {
         if (!tasks_ready) {
-            rc = qk_launch_mfma_tasks(s, n, segtab, QK_MFMA_MIN_M, c->sc.tasks, stream);
+            rc = qk_launch_mfma_tasks(s, n, segtab, min_m, c->sc.tasks, stream);
             if (hip_fail(err, rc, "mfma tasks")) return -1;
         }
         rc = qk_launch_pack_rows(h, 0, (size_t)n * (s.k + 1), s.I, c->sc.ahi, c->sc.alo, c->sc.ag,
                                  stream);
         if (hip_fail(err, rc, "pack h")) return -1;
     }
-    if (mm && fork(c, stream, err)) return -1;
-    rc = qk_launch_down(W, s, h, n, segtab, mm ? QK_MFMA_MIN_M : 0,
-                        mm ? qk_mfma_small_list(s, n, c->sc.tasks) : NULL, y, mm ? c->aux : stream);
-    if (hip_fail(err, rc, "down")) return -1;
+    if (mm && gemv && fork(c, stream, err)) return -1;
+    if (gemv) {
+        rc = qk_launch_down(W, s, h, n, segtab, mm ? min_m : 0,
+                            mm ? qk_mfma_small_list(s, n, c->sc.tasks) : NULL, y,
+                            mm ? c->aux : stream);
+        if (hip_fail(err, rc, "down")) return -1;
+    }
     if (mm) {
         rc = qk_launch_down_mfma(W, s, c->sc.ahi, c->sc.alo, c->sc.ag, n, c->sc.tasks, y, stream);
         if (hip_fail(err, rc, "down mfma")) return -1;
-        if (join(c, stream, err)) return -1;
+        if (gemv && join(c, stream, err)) return -1;
     }
     return 0;
 }

@@ -103,6 +103,10 @@ int qk_launch_invert_perm(int count, const int32_t *perm, int32_t *pos, void *st
  * the MFMA kernels take the (segment, row chunk) tasks built by
  * qk_launch_mfma_tasks for segments with at least min_m rows. */
 #define QK_MFMA_MIN_M 16
+/* from this many tokens on every segment runs on the MFMA kernels: with
+ * many small segments the GEMV kernels, which convert the codes again for
+ * each row, cost more than MFMA tiles that are mostly padding */
+#define QK_MFMA_ALL_N 64
 int qk_launch_gateup(const qmoe_layer_weights *W, qk_shape s, const void *x, int x_bf16, int n,
                      const int32_t *perm, const int32_t *segtab, int max_m,
                      const int32_t *seglist, float *h, void *stream);
