@@ -18,10 +18,11 @@
  * X_g = P_g / -128 is split into bf16 hi + lo.  Weights are never rounded.
  *
  * Tiles.  A task is (segment, chunk of up to MM_BM rows); the grid is tasks
- * x column tiles.  The workgroup's 4 waves each own 4 column tiles of 16
- * (gate/up: 32 columns of Wg and the same 32 of Wu, so h = silu(g)*u is
+ * x column tiles.  The workgroup's 4 waves each own CT = 4 column tiles of
+ * 16 (gate/up: 32 columns of Wg and the same 32 of Wu, so h = silu(g)*u is
  * formed in registers; down: 64 columns of Wd) and every 16-row tile of
- * the chunk.  Per group the chunk's activation rows are staged in LDS
+ * the chunk.  Batches of at most 64 tokens use CT = 2 and 64-row chunks:
+ * twice the workgroups, each with less LDS and fewer registers.  Per group the chunk's activation rows are staged in LDS
  * (double buffered, XOR-swizzled 16-byte chunks), the code words come from
  * a register ring MM_WD groups ahead, and the scales of the whole tile sit
  * in LDS.  The kernel body is specialised on the number of 16-row tiles.
@@ -57,12 +58,13 @@ struct MmArgs {
 
 #define MM_MAXG 32 /* K/64 groups held in LDS (scales, group sums) */
 
-template <int TERMS>
+/* BMT = 16-row tiles a chunk can hold, CT = 16-column tiles per wave */
+template <int TERMS, int BMT, int CT>
 struct MmSmem {
-    uint4 a[2][TERMS][MM_BM * 8];   /* activation chunks, double buffered */
-    float p[MM_MAXG][MM_BM];        /* P of the chunk's rows, [group][row] */
-    uint16_t s[MM_MAXG][4][16][4];  /* scales, [group][wave][column][tile] */
-    int row[MM_BM];
+    uint4 a[2][TERMS][BMT * 16 * 8]; /* activation chunks, double buffered */
+    float p[MM_MAXG][BMT * 16];      /* P of the chunk's rows, [group][row] */
+    uint16_t s[MM_MAXG][4][16][CT];  /* scales, [group][wave][column][tile] */
+    int row[BMT * 16];
 };
 
 /* one code word -> the B operand: bf16 128+q in (q_i, q_{i+4}) pair order,
@@ -77,45 +79,53 @@ __device__ __forceinline__ qm_bf16x8 qm_codes(uint32_t w) {
                                          __builtin_amdgcn_perm(k, lo, 0x04030401u), __builtin_amdgcn_perm(k, hi, 0x04030401u)));
 }
 
-/* column of tile ct for this lane: gate/up tiles 0,1 = gate, 2,3 = up */
-template <bool DOWN>
+/* column of tile ct for this lane.  Down: a workgroup covers 64*CT
+ * columns, 16*CT per wave.  Gate/up: tiles 0..CT/2-1 are gate and the rest
+ * the same columns of up, so a workgroup covers 32*CT columns of h. */
+template <bool DOWN, int CT>
 __device__ __forceinline__ int mm_col(int nt, int wave, int ct, int c) {
-    return DOWN ? nt * 256 + 64 * wave + 16 * ct + c : nt * 128 + 32 * wave + 16 * (ct & 1) + c;
+    return DOWN ? nt * (64 * CT) + 16 * CT * wave + 16 * ct + c
+                : nt * (32 * CT) + 8 * CT * wave + 16 * (ct % (CT / 2)) + c;
 }
+template <bool DOWN, int CT>
+__device__ __forceinline__ int mm_mat(int ct) { return DOWN ? 0 : ct / (CT / 2); }
 
-template <bool DOWN, int TERMS, int MS>
-__device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS> &sm, int e, int p0,
+template <bool DOWN, int TERMS, int MS, int BMT, int CT>
+__device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, BMT, CT> &sm, int e, int p0,
                                         int mstart, int mrows, int nt) {
-    constexpr int ACH = (MM_BM * 8 + 255) / 256; /* staged 16-byte chunks per thread */
+    constexpr int BM = BMT * 16;
+    constexpr int ACH = (MS * 16 * 8 + 255) / 256; /* staged 16-byte chunks per thread */
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c = lane & 15, kq = lane >> 4;
     const int G = a.K >> 6;
     const size_t wrow = (size_t)a.K >> 3;
     const bool shared = e < 0;
 
-    const uint32_t *wq[4];
+    const uint32_t *wq[CT];
 #pragma unroll
-    for (int ct = 0; ct < 4; ct++) {
-        const int mat = DOWN ? 0 : ct >> 1;
+    for (int ct = 0; ct < CT; ct++) {
+        const int mat = mm_mat<DOWN, CT>(ct);
         const uint32_t *base = shared ? a.sq[mat] : a.q[mat] + (size_t)e * a.N * wrow;
-        wq[ct] = base + (size_t)mm_col<DOWN>(nt, wave, ct, c) * wrow + 2 * kq;
+        wq[ct] = base + (size_t)mm_col<DOWN, CT>(nt, wave, ct, c) * wrow + 2 * kq;
     }
-    uint2 wr[MM_WD][4];
+    uint2 wr[MM_WD][CT];
     auto load_w = [&](int slot, int g) {
 #pragma unroll
-        for (int ct = 0; ct < 4; ct++) wr[slot][ct] = qk_ld((const uint2 *)(wq[ct] + 8 * g));
+        for (int ct = 0; ct < CT; ct++) wr[slot][ct] = qk_ld((const uint2 *)(wq[ct] + 8 * g));
     };
 #pragma unroll
     for (int u = 0; u < MM_WD; u++)
         if (u < G) load_w(u, u);
 
-    /* scales of the tile: thread -> (wave', tile', column'), G/8 loads of 8 */
-    const int w2 = tid >> 6, ct2 = (tid >> 4) & 3, c2 = tid & 15;
+    /* scales of the tile: thread -> (wave', tile', column') for the first
+     * 64*CT threads, G/8 loads of 8 */
+    const int w2 = tid / (16 * CT), ct2 = (tid >> 4) % CT, c2 = tid & 15;
+    const bool sthr = tid < 64 * CT;
     uint4 sv[MM_MAXG / 8];
-    {
-        const int mat = DOWN ? 0 : ct2 >> 1;
+    if (sthr) {
+        const int mat = mm_mat<DOWN, CT>(ct2);
         const uint16_t *sp = (shared ? a.ss[mat] : a.s[mat] + (size_t)e * a.N * G) +
-                             (size_t)mm_col<DOWN>(nt, w2, ct2, c2) * G;
+                             (size_t)mm_col<DOWN, CT>(nt, w2, ct2, c2) * G;
 #pragma unroll
         for (int i = 0; i < MM_MAXG / 8; i++)
             if (8 * i < G) sv[i] = qk_ld((const uint4 *)(sp + 8 * i));
@@ -123,12 +133,12 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS> &sm, int 
     __syncthreads(); /* sm.row, written by the caller */
 
     /* P of the chunk's rows: 16-byte chunk ci -> row ci / (G/4), groups 4*(ci % (G/4)).. */
-    constexpr int PCH = (MM_BM * MM_MAXG / 4 + 255) / 256;
+    constexpr int PCH = (BM * MM_MAXG / 4 + 255) / 256;
     float4 pv[PCH];
 #pragma unroll
     for (int i = 0; i < PCH; i++) {
         const int ci = tid + 256 * i;
-        if (ci < MM_BM * (G >> 2)) {
+        if (ci < BM * (G >> 2)) {
             const int row = ci / (G >> 2), g4 = ci - row * (G >> 2);
             pv[i] = qk_ld((const float4 *)(a.ag + (size_t)sm.row[row] * G) + g4);
         }
@@ -140,14 +150,14 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS> &sm, int 
 #pragma unroll
     for (int i = 0; i < ACH; i++) {
         const int ci = tid + 256 * i;
-        aoff[i] = ci < MM_BM * 8 ? (uint32_t)sm.row[ci >> 3] * (uint32_t)a.K + (uint32_t)(ci & 7) * 8u : 0u;
+        aoff[i] = ci < MS * 16 * 8 ? (uint32_t)sm.row[ci >> 3] * (uint32_t)a.K + (uint32_t)(ci & 7) * 8u : 0u;
     }
     uint4 ar[TERMS][ACH];
     auto load_a = [&](int g) {
 #pragma unroll
         for (int i = 0; i < ACH; i++) {
             const int ci = tid + 256 * i;
-            if (ci < MM_BM * 8) {
+            if (ci < MS * 16 * 8) {
                 const uint32_t off = aoff[i] + (uint32_t)g * 64u;
 #pragma unroll
                 for (int tm = 0; tm < TERMS; tm++) ar[tm][i] = qk_ld((const uint4 *)(a.ap[tm] + off));
@@ -158,7 +168,7 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS> &sm, int 
 #pragma unroll
         for (int i = 0; i < ACH; i++) {
             const int ci = tid + 256 * i;
-            if (ci < MM_BM * 8) {
+            if (ci < MS * 16 * 8) {
                 const int row = ci >> 3, kc = ci & 7;
 #pragma unroll
                 for (int tm = 0; tm < TERMS; tm++) sm.a[buf][tm][row * 8 + (kc ^ (row & 7))] = ar[tm][i];
@@ -169,7 +179,7 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS> &sm, int 
 
 #pragma unroll
     for (int i = 0; i < MM_MAXG / 8; i++) {
-        if (8 * i < G) {
+        if (sthr && 8 * i < G) {
             const uint32_t wv[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
@@ -181,7 +191,7 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS> &sm, int 
 #pragma unroll
     for (int i = 0; i < PCH; i++) {
         const int ci = tid + 256 * i;
-        if (ci < MM_BM * (G >> 2)) {
+        if (ci < BM * (G >> 2)) {
             const int row = ci / (G >> 2), g4 = ci - row * (G >> 2);
             sm.p[4 * g4][row] = pv[i].x;
             sm.p[4 * g4 + 1][row] = pv[i].y;
@@ -190,11 +200,11 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS> &sm, int 
         }
     }
 
-    qm_f32x4 acc[MS][4];
+    qm_f32x4 acc[MS][CT];
 #pragma unroll
     for (int rt = 0; rt < MS; rt++)
 #pragma unroll
-        for (int ct = 0; ct < 4; ct++) acc[rt][ct] = qm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int ct = 0; ct < CT; ct++) acc[rt][ct] = qm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     store_a(0);
     if (G > 1) load_a(1);
@@ -209,15 +219,25 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS> &sm, int 
                 /* buffer buf^1 was last read in group g-1, before the barrier ending it */
                 if (g + 1 < G) store_a(buf ^ 1);
                 if (g + 2 < G) load_a(g + 2);
-                qm_bf16x8 bop[4][2];
+                qm_bf16x8 bop[CT][2];
 #pragma unroll
-                for (int ct = 0; ct < 4; ct++) {
+                for (int ct = 0; ct < CT; ct++) {
                     bop[ct][0] = qm_codes(wr[u][ct].x);
                     bop[ct][1] = qm_codes(wr[u][ct].y);
                 }
                 if (g + MM_WD < G) load_w(u, g + MM_WD);
-                const uint2 sv = *(const uint2 *)&sm.s[g][wave][c][0];
-                const float sc[4] = {qk_bf16_lo(sv.x), qk_bf16_hi(sv.x), qk_bf16_lo(sv.y), qk_bf16_hi(sv.y)};
+                float sc[CT];
+                if (CT == 4) {
+                    const uint2 sv = *(const uint2 *)&sm.s[g][wave][c][0];
+                    sc[0] = qk_bf16_lo(sv.x);
+                    sc[1 % CT] = qk_bf16_hi(sv.x);
+                    sc[2 % CT] = qk_bf16_lo(sv.y);
+                    sc[3 % CT] = qk_bf16_hi(sv.y);
+                } else {
+                    const uint32_t sv = *(const uint32_t *)&sm.s[g][wave][c][0];
+                    sc[0] = qk_bf16_lo(sv);
+                    sc[1 % CT] = qk_bf16_hi(sv);
+                }
                 /* LDS reads run one row tile ahead with one activation plane;
                  * with two the registers are not there */
                 constexpr int PF = TERMS == 1 ? 2 : 1;
@@ -238,9 +258,9 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS> &sm, int 
                     const int sl = PF == 2 ? rt & 1 : 0;
                     if (PF == 1) lds_a(rt, 0);
                     else if (rt + 1 < MS) lds_a(rt + 1, (rt + 1) & (PF - 1));
-                    qm_f32x4 t[4];
+                    qm_f32x4 t[CT];
 #pragma unroll
-                    for (int ct = 0; ct < 4; ct++)
+                    for (int ct = 0; ct < CT; ct++)
                         t[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[sl][0][0], bop[ct][0], xi[sl], 0, 0, 0);
 #pragma unroll
                     for (int tm = 0; tm < TERMS; tm++)
@@ -248,11 +268,11 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS> &sm, int 
                         for (int j = 0; j < 2; j++) {
                             if (tm == 0 && j == 0) continue;
 #pragma unroll
-                            for (int ct = 0; ct < 4; ct++)
+                            for (int ct = 0; ct < CT; ct++)
                                 t[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[sl][tm][j], bop[ct][j], t[ct], 0, 0, 0);
                         }
 #pragma unroll
-                    for (int ct = 0; ct < 4; ct++)
+                    for (int ct = 0; ct < CT; ct++)
 #pragma unroll
                         for (int i = 0; i < 4; i++) acc[rt][ct][i] = fmaf(sc[ct], t[ct][i], acc[rt][ct][i]);
                 }
@@ -264,12 +284,12 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS> &sm, int 
     /* bias term: acc += sum_g b[col][g] * X[row][g], X = P / -128 as bf16 hi + lo */
     for (int k0 = 0; k0 < G; k0 += 32) {
         const int gk = k0 + 8 * kq;
-        qm_bf16x8 bb[4];
+        qm_bf16x8 bb[CT];
 #pragma unroll
-        for (int ct = 0; ct < 4; ct++) {
-            const int mat = DOWN ? 0 : ct >> 1;
+        for (int ct = 0; ct < CT; ct++) {
+            const int mat = mm_mat<DOWN, CT>(ct);
             const uint16_t *bp = (shared ? a.sb[mat] : a.b[mat] + (size_t)e * a.N * G) +
-                                 (size_t)mm_col<DOWN>(nt, wave, ct, c) * G;
+                                 (size_t)mm_col<DOWN, CT>(nt, wave, ct, c) * G;
             const uint4 v = gk < G ? qk_ld((const uint4 *)(bp + gk)) : make_uint4(0, 0, 0, 0);
             bb[ct] = __builtin_bit_cast(qm_bf16x8, v);
         }
@@ -288,7 +308,7 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS> &sm, int 
             const qm_bf16x8 AH = __builtin_bit_cast(qm_bf16x8, make_uint4(hi[0], hi[1], hi[2], hi[3]));
             const qm_bf16x8 AL = __builtin_bit_cast(qm_bf16x8, make_uint4(lo[0], lo[1], lo[2], lo[3]));
 #pragma unroll
-            for (int ct = 0; ct < 4; ct++) {
+            for (int ct = 0; ct < CT; ct++) {
                 acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(AH, bb[ct], acc[rt][ct], 0, 0, 0);
                 acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(AL, bb[ct], acc[rt][ct], 0, 0, 0);
             }
@@ -305,20 +325,23 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS> &sm, int 
                 float *o = a.out + (size_t)(p0 + mstart + row) * a.N;
                 if (DOWN) {
 #pragma unroll
-                    for (int ct = 0; ct < 4; ct++) qk_st(o + mm_col<true>(nt, wave, ct, c), acc[rt][ct][i]);
+                    for (int ct = 0; ct < CT; ct++) qk_st(o + mm_col<true, CT>(nt, wave, ct, c), acc[rt][ct][i]);
                 } else {
 #pragma unroll
-                    for (int h2 = 0; h2 < 2; h2++)
-                        qk_st(o + mm_col<false>(nt, wave, h2, c), qk_silu(acc[rt][h2][i]) * acc[rt][2 + h2][i]);
+                    for (int h2 = 0; h2 < CT / 2; h2++)
+                        qk_st(o + mm_col<false, CT>(nt, wave, h2, c),
+                              qk_silu(acc[rt][h2][i]) * acc[rt][CT / 2 + h2][i]);
                 }
             }
         }
     }
 }
 
-template <bool DOWN, int TERMS>
+/* BMT * 16 must hold every chunk: BMT = MM_MT, or any BMT when the host
+ * knows that no segment has more rows (a segment has at most n rows) */
+template <bool DOWN, int TERMS, int BMT, int CT>
 __global__ __launch_bounds__(256, 2) void k_mm(MmArgs a) {
-    __shared__ __attribute__((aligned(16))) MmSmem<TERMS> sm;
+    __shared__ __attribute__((aligned(16))) MmSmem<TERMS, BMT, CT> sm;
     /* workgroups are dealt round-robin over the 8 XCDs: workgroup L runs on
      * XCD L%8.  Tasks are interleaved over the XCDs (task 8j+x on XCD x) so
      * the real tasks, fewer than the grid allows for, spread over all of
@@ -330,10 +353,10 @@ __global__ __launch_bounds__(256, 2) void k_mm(MmArgs a) {
     if (mt >= qk_ld(a.tasks)) return;
     const int4 tk = qk_ld((const int4 *)(a.tasks + MM_TASK_HDR) + mt);
     const int e = tk.x, p0 = tk.y, m = tk.z, mstart = tk.w * MM_BM;
-    const int mrows = min(MM_BM, m - mstart);
+    const int mrows = min(BMT * 16, m - mstart);
     if (mrows <= 0) return;
     const int tid = threadIdx.x;
-    if (tid < MM_BM) {
+    if (tid < BMT * 16) {
         /* activation row of chunk row tid (rows past the end repeat the last) */
         const int i = min(tid, mrows - 1);
         int r;
@@ -342,14 +365,16 @@ __global__ __launch_bounds__(256, 2) void k_mm(MmArgs a) {
         else r = qk_ld(a.perm + p0 + mstart + i) / a.k;
         sm.row[tid] = r;
     }
+#define MM_CASE(T) mm_body<DOWN, TERMS, ((T) < BMT ? (T) : BMT), BMT, CT>(a, sm, e, p0, mstart, mrows, nt)
     switch ((mrows + 15) >> 4) {
-    case 1: mm_body<DOWN, TERMS, 1>(a, sm, e, p0, mstart, mrows, nt); break;
-    case 2: mm_body<DOWN, TERMS, 2>(a, sm, e, p0, mstart, mrows, nt); break;
-    case 3: mm_body<DOWN, TERMS, 3>(a, sm, e, p0, mstart, mrows, nt); break;
-    case 4: mm_body<DOWN, TERMS, 4>(a, sm, e, p0, mstart, mrows, nt); break;
-    case 5: mm_body<DOWN, TERMS, 5>(a, sm, e, p0, mstart, mrows, nt); break;
-    default: mm_body<DOWN, TERMS, MM_MT>(a, sm, e, p0, mstart, mrows, nt); break;
+    case 1: MM_CASE(1); break;
+    case 2: MM_CASE(2); break;
+    case 3: MM_CASE(3); break;
+    case 4: MM_CASE(4); break;
+    case 5: MM_CASE(5); break;
+    default: MM_CASE(BMT); break;
     }
+#undef MM_CASE
 }
 
 /*
@@ -443,17 +468,30 @@ __global__ __launch_bounds__(1024) void k_mm_tasks(const int32_t *segtab, int n,
     }
 }
 
-static int mm_launch(const MmArgs &a, bool down, int terms, int max_tasks, hipStream_t st) {
+/* Up to MM_NARROW_N tokens no segment exceeds 64 rows: the kernels then
+ * hold 64-row chunks and give each wave 2 column tiles instead of 4, so a
+ * batch of mostly small segments spreads over twice the workgroups (with
+ * few rows per task the per-group latency, not the MFMA rate, bounds a
+ * workgroup). */
+#define MM_NARROW_N 64
+
+static int mm_launch(MmArgs &a, bool down, int terms, int max_tasks, hipStream_t st) {
+    const bool narrow = a.n <= MM_NARROW_N;
+    const int ct = narrow ? 2 : 4;
+    a.ntile = a.N / (down ? 64 * ct : 32 * ct);
     /* every (task, column tile) once: 8 * ceil(max_tasks / 8) tasks */
     const long long wgs = (long long)(max_tasks + 7) / 8 * 8 * a.ntile;
     if (wgs <= 0) return 0;
-    if (down) {
-        if (terms == 2) hipLaunchKernelGGL((k_mm<true, 2>), dim3((unsigned)wgs), dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((k_mm<true, 1>), dim3((unsigned)wgs), dim3(256), 0, st, a);
+    const dim3 grid((unsigned)wgs), blk(256);
+#define MM_L(D, T, B, C) hipLaunchKernelGGL((k_mm<D, T, B, C>), grid, blk, 0, st, a)
+    if (narrow) {
+        if (down) { if (terms == 2) MM_L(true, 2, 4, 2); else MM_L(true, 1, 4, 2); }
+        else { if (terms == 2) MM_L(false, 2, 4, 2); else MM_L(false, 1, 4, 2); }
     } else {
-        if (terms == 2) hipLaunchKernelGGL((k_mm<false, 2>), dim3((unsigned)wgs), dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((k_mm<false, 1>), dim3((unsigned)wgs), dim3(256), 0, st, a);
+        if (down) { if (terms == 2) MM_L(true, 2, MM_MT, 4); else MM_L(true, 1, MM_MT, 4); }
+        else { if (terms == 2) MM_L(false, 2, MM_MT, 4); else MM_L(false, 1, MM_MT, 4); }
     }
+#undef MM_L
     return QK_CHECK_LAUNCH();
 }
 
@@ -524,7 +562,6 @@ extern "C" int qk_launch_gateup_mfma(const qmoe_layer_weights *W, qk_shape s, co
     a.N = s.I;
     a.n = n;
     a.k = s.k;
-    a.ntile = s.I / 128;
     return mm_launch(a, false, xlo ? 2 : 1, qk_mfma_max_tasks(s, n), (hipStream_t)stream);
 }
 
@@ -550,6 +587,5 @@ extern "C" int qk_launch_down_mfma(const qmoe_layer_weights *W, qk_shape s, cons
     a.N = s.H;
     a.n = n;
     a.k = s.k;
-    a.ntile = s.H / 256;
     return mm_launch(a, true, 2, qk_mfma_max_tasks(s, n), (hipStream_t)stream);
 }
