@@ -5,6 +5,14 @@
  */
 #include "qk_device.h"
 
+/* y is read once: a streaming (nontemporal) load keeps it from displacing
+ * other lines in the caches */
+typedef float cb_f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 qk_ld_stream(const float4 *p) {
+    const cb_f32x4 v = __builtin_nontemporal_load((const cb_f32x4 *)p);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 struct CombineArgs {
     const float *y;     /* [n*k+n, H] */
     const int32_t *pos; /* [n*k] dispatch position of slot t*k+s */
@@ -48,7 +56,7 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
     const int c = (blockIdx.y * 256 + threadIdx.x) * 4;
     if (c >= a.H) return;
     const float g = qk_ld(a.sg + t);
-    const float4 vs = qk_ld((const float4 *)(a.y + ((size_t)a.n * a.k + t) * a.H + c));
+    const float4 vs = qk_ld_stream((const float4 *)(a.y + ((size_t)a.n * a.k + t) * a.H + c));
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     /* issue eight independent row loads (clamped rows, no branches) before
      * the dependent fma chain */
@@ -58,7 +66,7 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
         for (int jj = 0; jj < 8; jj++) {
             const int j = min(j0 + jj, a.k - 1);
             const int p = s_pos[j] < a.n * a.k ? s_pos[j] : 0;
-            v[jj] = qk_ld((const float4 *)(a.y + (size_t)p * a.H + c));
+            v[jj] = qk_ld_stream((const float4 *)(a.y + (size_t)p * a.H + c));
         }
 #pragma unroll
         for (int jj = 0; jj < 8; jj++) {

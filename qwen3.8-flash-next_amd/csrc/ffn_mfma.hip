@@ -58,10 +58,11 @@ struct MmArgs {
 
 #define MM_MAXG 32 /* K/64 groups held in LDS (scales, group sums) */
 
-/* BMT = 16-row tiles a chunk can hold, CT = 16-column tiles per wave */
-template <int TERMS, int BMT, int CT>
+/* BMT = 16-row tiles a chunk can hold, CT = 16-column tiles per wave,
+ * KS = 64-column groups staged per barrier */
+template <int TERMS, int BMT, int CT, int KS>
 struct MmSmem {
-    uint4 a[2][TERMS][BMT * 16 * 8]; /* activation chunks, double buffered */
+    uint4 a[2][TERMS][KS * BMT * 16 * 8]; /* activation chunks, double buffered */
     float p[MM_MAXG][BMT * 16];      /* P of the chunk's rows, [group][row] */
     uint16_t s[MM_MAXG][4][16][CT];  /* scales, [group][wave][column][tile] */
     int row[BMT * 16];
@@ -90,9 +91,10 @@ __device__ __forceinline__ int mm_col(int nt, int wave, int ct, int c) {
 template <bool DOWN, int CT>
 __device__ __forceinline__ int mm_mat(int ct) { return DOWN ? 0 : ct / (CT / 2); }
 
-template <bool DOWN, int TERMS, int MS, int BMT, int CT>
-__device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, BMT, CT> &sm, int e, int p0,
+template <bool DOWN, int TERMS, int MS, int BMT, int CT, int KS>
+__device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, BMT, CT, KS> &sm, int e, int p0,
                                         int mstart, int mrows, int nt) {
+    static_assert(MM_WD % KS == 0, "a stage of KS groups lies within one code-word ring pass");
     constexpr int BM = BMT * 16;
     constexpr int ACH = (MS * 16 * 8 + 255) / 256; /* staged 16-byte chunks per thread */
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -152,28 +154,35 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, BMT, CT> 
         const int ci = tid + 256 * i;
         aoff[i] = ci < MS * 16 * 8 ? (uint32_t)sm.row[ci >> 3] * (uint32_t)a.K + (uint32_t)(ci & 7) * 8u : 0u;
     }
-    uint4 ar[TERMS][ACH];
-    auto load_a = [&](int g) {
+    /* stage st = groups st*KS .. st*KS+KS-1 (G is a multiple of 8, so of KS) */
+    const int NST = G / KS;
+    uint4 ar[KS][TERMS][ACH];
+    auto load_a = [&](int st) {
 #pragma unroll
-        for (int i = 0; i < ACH; i++) {
-            const int ci = tid + 256 * i;
-            if (ci < MS * 16 * 8) {
-                const uint32_t off = aoff[i] + (uint32_t)g * 64u;
+        for (int kk = 0; kk < KS; kk++)
 #pragma unroll
-                for (int tm = 0; tm < TERMS; tm++) ar[tm][i] = qk_ld((const uint4 *)(a.ap[tm] + off));
+            for (int i = 0; i < ACH; i++) {
+                const int ci = tid + 256 * i;
+                if (ci < MS * 16 * 8) {
+                    const uint32_t off = aoff[i] + (uint32_t)(st * KS + kk) * 64u;
+#pragma unroll
+                    for (int tm = 0; tm < TERMS; tm++) ar[kk][tm][i] = qk_ld((const uint4 *)(a.ap[tm] + off));
+                }
             }
-        }
     };
     auto store_a = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < ACH; i++) {
-            const int ci = tid + 256 * i;
-            if (ci < MS * 16 * 8) {
-                const int row = ci >> 3, kc = ci & 7;
+        for (int kk = 0; kk < KS; kk++)
 #pragma unroll
-                for (int tm = 0; tm < TERMS; tm++) sm.a[buf][tm][row * 8 + (kc ^ (row & 7))] = ar[tm][i];
+            for (int i = 0; i < ACH; i++) {
+                const int ci = tid + 256 * i;
+                if (ci < MS * 16 * 8) {
+                    const int row = ci >> 3, kc = ci & 7;
+#pragma unroll
+                    for (int tm = 0; tm < TERMS; tm++)
+                        sm.a[buf][tm][(kk * BM + row) * 8 + (kc ^ (row & 7))] = ar[kk][tm][i];
+                }
             }
-        }
     };
     load_a(0);
 
@@ -207,7 +216,7 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, BMT, CT> 
         for (int ct = 0; ct < CT; ct++) acc[rt][ct] = qm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     store_a(0);
-    if (G > 1) load_a(1);
+    if (NST > 1) load_a(1);
     __syncthreads();
 
     for (int g0 = 0; g0 < G; g0 += MM_WD) {
@@ -215,10 +224,11 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, BMT, CT> 
         for (int u = 0; u < MM_WD; u++) {
             const int g = g0 + u;
             if (g < G) {
-                const int buf = g & 1;
-                /* buffer buf^1 was last read in group g-1, before the barrier ending it */
-                if (g + 1 < G) store_a(buf ^ 1);
-                if (g + 2 < G) load_a(g + 2);
+                const int kk = u % KS; /* g0 is a multiple of MM_WD, so of KS */
+                const int st = g / KS, buf = st & 1;
+                /* buffer buf^1 was last read in stage st-1, before the barrier ending it */
+                if (kk == 0 && st + 1 < NST) store_a(buf ^ 1);
+                if (kk == 0 && st + 2 < NST) load_a(st + 2);
                 qm_bf16x8 bop[CT][2];
 #pragma unroll
                 for (int ct = 0; ct < CT; ct++) {
@@ -250,7 +260,8 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, BMT, CT> 
                     for (int tm = 0; tm < TERMS; tm++)
 #pragma unroll
                         for (int j = 0; j < 2; j++)
-                            A[sl][tm][j] = __builtin_bit_cast(qm_bf16x8, sm.a[buf][tm][row * 8 + ((2 * kq + j) ^ (c & 7))]);
+                            A[sl][tm][j] = __builtin_bit_cast(
+                                qm_bf16x8, sm.a[buf][tm][(kk * BM + row) * 8 + ((2 * kq + j) ^ (c & 7))]);
                 };
                 if (PF == 2) lds_a(0, 0);
 #pragma unroll
@@ -276,7 +287,7 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, BMT, CT> 
 #pragma unroll
                         for (int i = 0; i < 4; i++) acc[rt][ct][i] = fmaf(sc[ct], t[ct][i], acc[rt][ct][i]);
                 }
-                __syncthreads();
+                if (kk == KS - 1) __syncthreads();
             }
         }
     }
@@ -339,9 +350,17 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, BMT, CT> 
 
 /* BMT * 16 must hold every chunk: BMT = MM_MT, or any BMT when the host
  * knows that no segment has more rows (a segment has at most n rows) */
+/* bf16 gate/up at full tiles stages two groups per barrier (the LDS of two
+ * workgroups per CU still fits) */
+template <int TERMS, int BMT>
+struct MmKs {
+    static constexpr int value = (TERMS == 1 && BMT == MM_MT) ? 2 : 1;
+};
+
 template <bool DOWN, int TERMS, int BMT, int CT>
 __global__ __launch_bounds__(256, 2) void k_mm(MmArgs a) {
-    __shared__ __attribute__((aligned(16))) MmSmem<TERMS, BMT, CT> sm;
+    constexpr int KS = MmKs<TERMS, BMT>::value;
+    __shared__ __attribute__((aligned(16))) MmSmem<TERMS, BMT, CT, KS> sm;
     /* workgroups are dealt round-robin over the 8 XCDs: workgroup L runs on
      * XCD L%8.  Tasks are interleaved over the XCDs (task 8j+x on XCD x) so
      * the real tasks, fewer than the grid allows for, spread over all of
@@ -365,7 +384,7 @@ __global__ __launch_bounds__(256, 2) void k_mm(MmArgs a) {
         else r = qk_ld(a.perm + p0 + mstart + i) / a.k;
         sm.row[tid] = r;
     }
-#define MM_CASE(T) mm_body<DOWN, TERMS, ((T) < BMT ? (T) : BMT), BMT, CT>(a, sm, e, p0, mstart, mrows, nt)
+#define MM_CASE(T) mm_body<DOWN, TERMS, ((T) < BMT ? (T) : BMT), BMT, CT, KS>(a, sm, e, p0, mstart, mrows, nt)
     switch ((mrows + 15) >> 4) {
     case 1: MM_CASE(1); break;
     case 2: MM_CASE(2); break;
