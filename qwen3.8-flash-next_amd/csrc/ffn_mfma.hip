@@ -34,14 +34,12 @@
  * columns, so one 8-byte load per lane fetches both K-steps' codes.
  */
 #include "qk_device.h"
+#include "mm_tasks.h"
 
 typedef __bf16 qm_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float qm_f32x4 __attribute__((ext_vector_type(4)));
 
-#define MM_MT 6              /* 16-row tiles per chunk */
-#define MM_BM (16 * MM_MT)   /* rows per chunk */
 #define MM_WD 2              /* code-word prefetch depth, groups */
-#define MM_TASK_HDR 4        /* int32 header before the int4 task entries */
 
 struct MmArgs {
     const uint32_t *q[2]; /* routed [E, N, K/8]: gate, up (down: both Wd) */
@@ -219,23 +217,33 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, BMT, CT, 
     if (NST > 1) load_a(1);
     __syncthreads();
 
+    /* G is a multiple of 8 (the host checks), so of MM_WD and KS.  For the
+     * full-tile one-plane kernel the prefetches are unconditional, from
+     * clamped groups past the end (their data is never used): a conditional
+     * load makes the ring registers a merge of old and new values, and the
+     * copies the compiler then places at the loop edge wait for every load
+     * in flight (2 % at the prefill shape).  With two planes that costs
+     * registers the kernel does not have (it spills); the narrow tiles
+     * gained nothing. */
+    constexpr bool UNCOND = TERMS == 1 && BMT == MM_MT;
     for (int g0 = 0; g0 < G; g0 += MM_WD) {
 #pragma unroll
         for (int u = 0; u < MM_WD; u++) {
             const int g = g0 + u;
-            if (g < G) {
+            if (UNCOND || g < G) {
                 const int kk = u % KS; /* g0 is a multiple of MM_WD, so of KS */
                 const int st = g / KS, buf = st & 1;
-                /* buffer buf^1 was last read in stage st-1, before the barrier ending it */
-                if (kk == 0 && st + 1 < NST) store_a(buf ^ 1);
-                if (kk == 0 && st + 2 < NST) load_a(st + 2);
+                /* buffer buf^1 was last read in stage st-1, before the barrier
+                 * ending it (past the last stage it is not read again) */
+                if (kk == 0 && (UNCOND || st + 1 < NST)) store_a(buf ^ 1);
+                if (kk == 0 && (UNCOND || st + 2 < NST)) load_a(min(st + 2, NST - 1));
                 qm_bf16x8 bop[CT][2];
 #pragma unroll
                 for (int ct = 0; ct < CT; ct++) {
                     bop[ct][0] = qm_codes(wr[u][ct].x);
                     bop[ct][1] = qm_codes(wr[u][ct].y);
                 }
-                if (g + MM_WD < G) load_w(u, g + MM_WD);
+                if (UNCOND || g + MM_WD < G) load_w(u, min(g + MM_WD, G - 1));
                 float sc[CT];
                 if (CT == 4) {
                     const uint2 sv = *(const uint2 *)&sm.s[g][wave][c][0];
@@ -427,64 +435,10 @@ __global__ __launch_bounds__(256) void k_pack_rows(const void *x, size_t nchunks
     if ((i & 7) == 0) gsum[i >> 3] = -128.0f * s;
 }
 
-/* ---- task list: {expert (-1 = shared), first position, rows, chunk} for
- * every segment with at least min_m rows; the shared expert covers all n
- * tokens at positions n*k.. .  tasks[0] = count; entries from
- * tasks + MM_TASK_HDR.  The segments with 1..min_m-1 rows (0 = shared) are
- * listed for the GEMV kernels at `small`: small[0] = count, then ids. */
+/* the task list as its own launch (mm_tasks.h) */
 __global__ __launch_bounds__(1024) void k_mm_tasks(const int32_t *segtab, int n, int k, int E,
                                                    int min_m, int32_t *tasks, int32_t *small) {
-    __shared__ int s_scan[16];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int U = min(max(qk_ld(segtab), 0), E);
-    int4 *out = (int4 *)(tasks + MM_TASK_HDR);
-    int base = 0, sbase = 0;
-    /* segments 0..U in blocks of 1024; segment 0 is the shared expert */
-    for (int s0 = 0; s0 <= U; s0 += 1024) {
-        const int sg = s0 + tid;
-        int e = -1, p0 = n * k, m = 0;
-        if (sg == 0) {
-            m = n;
-        } else if (sg <= U) {
-            e = qk_ld(segtab + 3 * sg - 2);
-            p0 = qk_ld(segtab + 3 * sg - 1);
-            m = qk_ld(segtab + 3 * sg);
-        }
-        const int cnt = m >= min_m && m > 0 ? (m + MM_BM - 1) / MM_BM : 0;
-        const int sm = m > 0 && m < min_m ? 1 : 0;
-        /* both counts in one scan: chunks in bits 0..19, small segments above */
-        const int own = cnt + (sm << 20);
-        int inc = own;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int u = __shfl_up(inc, o, QK_WAVE);
-            if (lane >= o) inc += u;
-        }
-        if (lane == 63) s_scan[wave] = inc;
-        __syncthreads();
-        int wbase = 0, tot = 0;
-        for (int i = 0; i < 16; i++) {
-            if (i < wave) wbase += s_scan[i];
-            tot += s_scan[i];
-        }
-        __syncthreads();
-        const int ex = wbase + inc - own;
-        const int off = base + (ex & 0xFFFFF), soff = sbase + (ex >> 20);
-        for (int ch = 0; ch < cnt; ch++) {
-            int *o = (int *)(out + off + ch);
-            o[0] = e;
-            o[1] = p0;
-            o[2] = m;
-            o[3] = ch;
-        }
-        if (sm) small[1 + soff] = sg;
-        base += tot & 0xFFFFF;
-        sbase += tot >> 20;
-    }
-    if (tid == 0) {
-        tasks[0] = base;
-        small[0] = sbase;
-    }
+    mm_tasks_block(segtab, n, k, E, min_m, tasks, small);
 }
 
 /* Up to MM_NARROW_N tokens no segment exceeds 64 rows: the kernels then

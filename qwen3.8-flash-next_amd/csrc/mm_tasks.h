@@ -1,0 +1,76 @@
+/*
+ * mm_tasks.h -- the task list of the grouped MFMA kernels, built by one
+ * 1024-thread workgroup from a segment table: by its own launch
+ * (ffn_mfma.hip) or at the end of the dispatch that wrote the table
+ * (router.hip), which saves a launch per layer.
+ */
+#ifndef MM_TASKS_H
+#define MM_TASKS_H
+
+#include "qk_device.h"
+
+#define MM_MT 6              /* 16-row tiles per chunk */
+#define MM_BM (16 * MM_MT)   /* rows per chunk */
+#define MM_TASK_HDR 4        /* int32 header before the int4 task entries */
+
+/* Task list: {expert (-1 = shared), first position, rows, chunk} for
+ * every segment with at least min_m rows; the shared expert covers all n
+ * tokens at positions n*k.. .  tasks[0] = count; entries from
+ * tasks + MM_TASK_HDR.  The segments with 1..min_m-1 rows (0 = shared) are
+ * listed for the GEMV kernels at `small`: small[0] = count, then ids. */
+static __device__ void mm_tasks_block(const int32_t *segtab, int n, int k, int E, int min_m, int32_t *tasks,
+                               int32_t *small) {
+    __shared__ int s_scan[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int U = min(max(qk_ld(segtab), 0), E);
+    int4 *out = (int4 *)(tasks + MM_TASK_HDR);
+    int base = 0, sbase = 0;
+    /* segments 0..U in blocks of 1024; segment 0 is the shared expert */
+    for (int s0 = 0; s0 <= U; s0 += 1024) {
+        const int sg = s0 + tid;
+        int e = -1, p0 = n * k, m = 0;
+        if (sg == 0) {
+            m = n;
+        } else if (sg <= U) {
+            e = qk_ld(segtab + 3 * sg - 2);
+            p0 = qk_ld(segtab + 3 * sg - 1);
+            m = qk_ld(segtab + 3 * sg);
+        }
+        const int cnt = m >= min_m && m > 0 ? (m + MM_BM - 1) / MM_BM : 0;
+        const int sm = m > 0 && m < min_m ? 1 : 0;
+        /* both counts in one scan: chunks in bits 0..19, small segments above */
+        const int own = cnt + (sm << 20);
+        int inc = own;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int u = __shfl_up(inc, o, QK_WAVE);
+            if (lane >= o) inc += u;
+        }
+        if (lane == 63) s_scan[wave] = inc;
+        __syncthreads();
+        int wbase = 0, tot = 0;
+        for (int i = 0; i < 16; i++) {
+            if (i < wave) wbase += s_scan[i];
+            tot += s_scan[i];
+        }
+        __syncthreads();
+        const int ex = wbase + inc - own;
+        const int off = base + (ex & 0xFFFFF), soff = sbase + (ex >> 20);
+        for (int ch = 0; ch < cnt; ch++) {
+            int *o = (int *)(out + off + ch);
+            o[0] = e;
+            o[1] = p0;
+            o[2] = m;
+            o[3] = ch;
+        }
+        if (sm) small[1 + soff] = sg;
+        base += tot & 0xFFFFF;
+        sbase += tot >> 20;
+    }
+    if (tid == 0) {
+        tasks[0] = base;
+        small[0] = sbase;
+    }
+}
+
+#endif

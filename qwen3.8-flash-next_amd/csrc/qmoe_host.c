@@ -563,16 +563,18 @@ static int mfma_usable(const qmoe_ctx *c, int n, int stage) {
 static int mfma_min_m(int n) { return n >= QK_MFMA_ALL_N ? 1 : QK_MFMA_MIN_M; }
 
 static int run_gateup(qmoe_ctx *c, const qmoe_layer_weights *W, const void *x, int xbf, int n,
-                      const int32_t *perm, const int32_t *segtab, float *h, void *stream,
-                      qmoe_err *err) {
+                      const int32_t *perm, const int32_t *segtab, int tasks_ready, float *h,
+                      void *stream, qmoe_err *err) {
     const int mm = mfma_usable(c, n, xbf ? 0 : 1);
     const int min_m = mfma_min_m(n);
     const int gemv = !mm || min_m > 1; /* small segments left to the GEMV */
     const qk_shape s = c->shape;
     int rc;
     if (mm) {
-        rc = qk_launch_mfma_tasks(s, n, segtab, min_m, c->sc.tasks, stream);
-        if (hip_fail(err, rc, "mfma tasks")) return -1;
+        if (!tasks_ready) {
+            rc = qk_launch_mfma_tasks(s, n, segtab, min_m, c->sc.tasks, stream);
+            if (hip_fail(err, rc, "mfma tasks")) return -1;
+        }
         rc = qk_launch_pack_rows(x, xbf, (size_t)n, s.H, c->sc.ahi, xbf ? NULL : c->sc.alo, c->sc.ag,
                                  stream);
         if (hip_fail(err, rc, "pack x")) return -1;
@@ -655,8 +657,8 @@ int qmoe_dispatch(qmoe_ctx *c, const int32_t *idx, int n, int32_t *offsets_out, 
     NEED(idx, "idx");
     NEED(perm_out, "perm_out");
     return hip_fail(err, qk_launch_dispatch(c->shape, n, idx, offsets_out, perm_out, c->sc.pos,
-                                            segments_out, c->sc.bits, c->sc.wprefix,
-                                            stream),
+                                            segments_out, c->sc.bits, c->sc.wprefix, 0,
+                                            NULL, stream),
                     "dispatch");
 }
 
@@ -670,7 +672,7 @@ int qmoe_expert_gateup(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n
     NEED(perm, "perm");
     NEED(segments, "segments");
     NEED(h_out, "h_out");
-    return run_gateup(c, &c->layers[layer].dev, x, x_dtype == QMOE_BF16, n, perm, segments, h_out,
+    return run_gateup(c, &c->layers[layer].dev, x, x_dtype == QMOE_BF16, n, perm, segments, 0, h_out,
                       stream, err);
 }
 
@@ -775,20 +777,24 @@ int qmoe_layer_forward(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n
                                     (flags & QMOE_RESIDUAL) ? x : NULL, xbf, out, stream);
         return hip_fail(err, rc, "down+combine");
     }
+    /* the dispatch also builds the MFMA task list when the gate/up runs on
+     * MFMA (one launch fewer) */
+    const int gu_mm = n >= 2 && mfma_usable(c, n, xf_bf ? 0 : 1);
+    int32_t *tasks = gu_mm ? sc->tasks : NULL;
     if (n <= QK_SMALL_N && n * s.k <= QK_SMALL_NK) {
         /* offsets are not used by the layer; qmoe_last_routing derives them */
         rc = qk_launch_topk_dispatch_small(s, n, sc->logits, NULL, sc->idx, sc->w, sc->sg,
                                            n == 1 ? NULL : sc->offsets, sc->perm, sc->pos,
-                                           sc->segtab, stream);
+                                           sc->segtab, mfma_min_m(n), tasks, stream);
         if (hip_fail(err, rc, "topk+dispatch")) return -1;
     } else {
         rc = qk_launch_topk(s, n, sc->logits, NULL, sc->idx, sc->w, sc->sg, stream);
         if (hip_fail(err, rc, "topk")) return -1;
         rc = qk_launch_dispatch(s, n, sc->idx, sc->offsets, sc->perm, sc->pos, sc->segtab,
-                                sc->bits, sc->wprefix, stream);
+                                sc->bits, sc->wprefix, mfma_min_m(n), tasks, stream);
         if (hip_fail(err, rc, "dispatch")) return -1;
     }
-    if (run_gateup(c, W, xf, xf_bf, n, sc->perm, sc->segtab, sc->h, stream, err)) return -1;
+    if (run_gateup(c, W, xf, xf_bf, n, sc->perm, sc->segtab, gu_mm, sc->h, stream, err)) return -1;
     if (!mfma_usable(c, n, 2) && qk_down_combine_lds(s, n) > 0) {
         rc = qk_launch_down_combine(W, s, sc->h, n, sc->segtab, sc->pos, sc->w, sc->sg,
                                     (flags & QMOE_RESIDUAL) ? x : NULL, xbf, out, stream);

@@ -83,14 +83,16 @@ int qk_launch_topk(qk_shape s, int n, const float *logits, float *logits_out, in
                    float *w, float *sg, void *stream);
 /* top-k and the whole dispatch in one single-workgroup launch, for
  * n <= QK_SMALL_N and n*k <= QK_SMALL_NK; offsets may be NULL only for
- * n == 1 */
+ * n == 1.  With tasks set (n >= 2) the launch also builds the MFMA task
+ * list for segments of at least min_m rows (as qk_launch_mfma_tasks). */
 int qk_launch_topk_dispatch_small(qk_shape s, int n, const float *logits, float *logits_out,
                                   int32_t *idx, float *w, float *sg, int32_t *offsets,
-                                  int32_t *perm, int32_t *pos, int32_t *segtab, void *stream);
-/* dispatch from idx alone (any n) */
+                                  int32_t *perm, int32_t *pos, int32_t *segtab, int min_m,
+                                  int32_t *tasks, void *stream);
+/* dispatch from idx alone (any n); tasks as for qk_launch_topk_dispatch_small */
 int qk_launch_dispatch(qk_shape s, int n, const int32_t *idx, int32_t *offsets, int32_t *perm,
                        int32_t *pos, int32_t *segtab, uint32_t *bits, int32_t *wprefix,
-                       void *stream);
+                       int min_m, int32_t *tasks, void *stream);
 /* offsets [E+1] from a segment table */
 int qk_launch_offsets_from_segtab(qk_shape s, const int32_t *segtab, int32_t *offsets,
                                   void *stream);

@@ -10,6 +10,7 @@
  * lanes with the pairwise tree of qk_group_sum<64> (partners l^1 ... l^32).
  */
 #include "qk_device.h"
+#include "mm_tasks.h"
 
 /* ------------------------------------------------------------ logits */
 
@@ -527,6 +528,8 @@ __device__ void dispatch_block(const int32_t *s_idx, int n, int k, int E, int32_
 struct SmallDispArgs {
     TopkArgs tk;
     int32_t *offsets, *perm, *pos, *segtab;
+    int min_m;            /* MFMA task list from the table, when tasks is set */
+    int32_t *tasks, *small;
 };
 
 /*
@@ -577,17 +580,26 @@ __global__ __launch_bounds__(1024) void k_topk_dispatch_small(SmallDispArgs a) {
     for (int t = wave; t < a.tk.n; t += 16) topk_token<PL>(a.tk, t, lane, s_idx);
     __syncthreads();
     dispatch_block<1024>(s_idx, a.tk.n, a.tk.k, a.tk.E, a.offsets, a.perm, a.pos, a.segtab);
+    if (a.tasks) {
+        __syncthreads(); /* the segment table, written by this workgroup */
+        mm_tasks_block(a.segtab, a.tk.n, a.tk.k, a.tk.E, a.min_m, a.tasks, a.small);
+    }
 }
 
 /* the same dispatch with the expert ids read from global memory (after a
  * separate k_topk launch, one wave per token over many workgroups) */
 __global__ __launch_bounds__(1024) void k_dispatch_small(const int32_t *idx, int n, int k, int E,
                                                          int32_t *offsets, int32_t *perm,
-                                                         int32_t *pos, int32_t *segtab) {
+                                                         int32_t *pos, int32_t *segtab, int min_m,
+                                                         int32_t *tasks, int32_t *small) {
     __shared__ int32_t s_idx[QK_SMALL_NK];
     for (int f = threadIdx.x; f < n * k; f += 1024) s_idx[f] = qk_ld(idx + f);
     __syncthreads();
     dispatch_block<1024>(s_idx, n, k, E, offsets, perm, pos, segtab);
+    if (tasks) {
+        __syncthreads();
+        mm_tasks_block(segtab, n, k, E, min_m, tasks, small);
+    }
 }
 
 /* tokens above which the top-k runs as its own launch (one wave per token)
@@ -597,10 +609,13 @@ __global__ __launch_bounds__(1024) void k_dispatch_small(const int32_t *idx, int
 extern "C" int qk_launch_topk_dispatch_small(qk_shape s, int n, const float *logits,
                                              float *logits_out, int32_t *idx, float *w, float *sg,
                                              int32_t *offsets, int32_t *perm, int32_t *pos,
-                                             int32_t *segtab, void *stream) {
+                                             int32_t *segtab, int min_m, int32_t *tasks,
+                                             void *stream) {
     if (n <= 0) return 0;
     if (n > QK_SMALL_N || n * s.k > QK_SMALL_NK) return (int)hipErrorInvalidValue;
-    SmallDispArgs a{{logits, logits_out, idx, w, sg, s.E, s.k, n}, offsets, perm, pos, segtab};
+    if (n == 1 && tasks) return (int)hipErrorInvalidValue;
+    SmallDispArgs a{{logits, logits_out, idx, w, sg, s.E, s.k, n}, offsets, perm, pos, segtab,
+                    min_m, tasks, tasks ? qk_mfma_small_list(s, n, tasks) : nullptr};
     hipStream_t st = (hipStream_t)stream;
     if (n == 1) {
         TK_DISPATCH(k_topk_dispatch_one, topk_pl(s.E), dim3(1), dim3(64), a);
@@ -611,7 +626,8 @@ extern "C" int qk_launch_topk_dispatch_small(qk_shape s, int n, const float *log
         if (!offsets) return (int)hipErrorInvalidValue;
         TK_DISPATCH(k_topk, topk_pl(s.E), dim3((n + 3) / 4), dim3(256), a.tk);
         hipLaunchKernelGGL(k_dispatch_small, dim3(1), dim3(1024), 0, st, (const int32_t *)idx, n, s.k,
-                           s.E, offsets, perm, pos, segtab);
+                           s.E, offsets, perm, pos, segtab, min_m, tasks,
+                           tasks ? qk_mfma_small_list(s, n, tasks) : nullptr);
     }
     return QK_CHECK_LAUNCH();
 }
@@ -659,13 +675,18 @@ __global__ __launch_bounds__(1024) void k_word_prefix(const uint32_t *bits, int3
  * segment table; perm entries past the dispatched total (slots with invalid
  * expert ids) are set to -1 */
 __global__ __launch_bounds__(1024) void k_count_offsets(int E, int32_t *offsets, int32_t *segtab,
-                                                        int32_t *perm, int nk) {
+                                                        int32_t *perm, int nk, int n, int k,
+                                                        int min_m, int32_t *tasks, int32_t *small) {
     __shared__ int s_scan[16];
     const int tid = threadIdx.x;
     int cnt[1] = {tid < E ? offsets[tid] : 0};
     __syncthreads();
     const int total = counts_to_offsets<1024>(cnt, E, s_scan, offsets, segtab, nullptr);
     for (int i = total + tid; i < nk; i += 1024) perm[i] = -1;
+    if (tasks) {
+        __syncthreads(); /* the segment table, written by this workgroup */
+        mm_tasks_block(segtab, n, k, E, min_m, tasks, small);
+    }
 }
 
 __global__ void k_scatter(const int32_t *idx, int n, int k, int E, int NW, const uint32_t *bits,
@@ -686,7 +707,8 @@ __global__ void k_scatter(const int32_t *idx, int n, int k, int E, int NW, const
 
 extern "C" int qk_launch_dispatch(qk_shape s, int n, const int32_t *idx, int32_t *offsets,
                                   int32_t *perm, int32_t *pos, int32_t *segtab,
-                                  uint32_t *bits, int32_t *wprefix, void *stream) {
+                                  uint32_t *bits, int32_t *wprefix, int min_m, int32_t *tasks,
+                                  void *stream) {
     hipStream_t st = (hipStream_t)stream;
     if (n <= 0) return 0;
     const int NW = (n + 31) / 32;
@@ -697,7 +719,8 @@ extern "C" int qk_launch_dispatch(qk_shape s, int n, const int32_t *idx, int32_t
                        bits);
     hipLaunchKernelGGL(k_word_prefix, dim3((s.E + 15) / 16), dim3(1024), 0, st, (const uint32_t *)bits,
                        wprefix, s.E, NW, offsets);
-    hipLaunchKernelGGL(k_count_offsets, dim3(1), dim3(1024), 0, st, s.E, offsets, segtab, perm, nk);
+    hipLaunchKernelGGL(k_count_offsets, dim3(1), dim3(1024), 0, st, s.E, offsets, segtab, perm, nk, n,
+                       s.k, min_m, tasks, tasks ? qk_mfma_small_list(s, n, tasks) : nullptr);
     hipLaunchKernelGGL(k_scatter, dim3((nk + 255) / 256), dim3(256), 0, st, idx, n, s.k, s.E, NW,
                        (const uint32_t *)bits, (const int32_t *)wprefix, (const int32_t *)offsets,
                        perm, pos);
