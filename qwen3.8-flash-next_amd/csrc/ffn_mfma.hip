@@ -48,6 +48,7 @@ struct MmArgs {
     const uint16_t *ss[2], *sb[2];
     const uint16_t *ap[2]; /* activation planes [rows, K] (hi, lo) */
     const float *ag;       /* [rows, G]: -128 * group sums */
+    const float *af;       /* down: f32 activations [rows, K], split while staged */
     float *out;            /* gate/up: h [n*k+n, N]; down: y [n*k+n, N] */
     const int32_t *perm;   /* gate/up: dispatch permutation */
     const int32_t *tasks;
@@ -132,13 +133,19 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, BMT, CT, 
     }
     __syncthreads(); /* sm.row, written by the caller */
 
+    /* The down projection reads h in f32 and forms the hi/lo planes and the
+     * group sums P while staging each group (as k_pack_rows would, in the
+     * same order); the gate/up reads packed planes and their P. */
+    constexpr bool F32IN = DOWN;
+    static_assert(!F32IN || TERMS == 2, "f32 activations give two planes");
+
     /* P of the chunk's rows: 16-byte chunk ci -> row ci / (G/4), groups 4*(ci % (G/4)).. */
     constexpr int PCH = (BM * MM_MAXG / 4 + 255) / 256;
     float4 pv[PCH];
 #pragma unroll
     for (int i = 0; i < PCH; i++) {
         const int ci = tid + 256 * i;
-        if (ci < BM * (G >> 2)) {
+        if (!F32IN && ci < BM * (G >> 2)) {
             const int row = ci / (G >> 2), g4 = ci - row * (G >> 2);
             pv[i] = qk_ld((const float4 *)(a.ag + (size_t)sm.row[row] * G) + g4);
         }
@@ -154,7 +161,8 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, BMT, CT, 
     }
     /* stage st = groups st*KS .. st*KS+KS-1 (G is a multiple of 8, so of KS) */
     const int NST = G / KS;
-    uint4 ar[KS][TERMS][ACH];
+    uint4 ar[F32IN ? 1 : KS][F32IN ? 1 : TERMS][F32IN ? 1 : ACH];
+    float4 af[F32IN ? KS : 1][F32IN ? ACH : 1][2];
     auto load_a = [&](int st) {
 #pragma unroll
         for (int kk = 0; kk < KS; kk++)
@@ -163,22 +171,51 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, BMT, CT, 
                 const int ci = tid + 256 * i;
                 if (ci < MS * 16 * 8) {
                     const uint32_t off = aoff[i] + (uint32_t)(st * KS + kk) * 64u;
+                    if (F32IN) {
+                        const float4 *src = (const float4 *)(a.af + off);
+                        af[F32IN ? kk : 0][F32IN ? i : 0][0] = qk_ld(src);
+                        af[F32IN ? kk : 0][F32IN ? i : 0][1] = qk_ld(src + 1);
+                    } else {
 #pragma unroll
-                    for (int tm = 0; tm < TERMS; tm++) ar[kk][tm][i] = qk_ld((const uint4 *)(a.ap[tm] + off));
+                        for (int tm = 0; tm < TERMS; tm++)
+                            ar[F32IN ? 0 : kk][F32IN ? 0 : tm][F32IN ? 0 : i] =
+                                qk_ld((const uint4 *)(a.ap[tm] + off));
+                    }
                 }
             }
     };
-    auto store_a = [&](int buf) {
+    auto store_a = [&](int buf, int st) {
 #pragma unroll
         for (int kk = 0; kk < KS; kk++)
 #pragma unroll
             for (int i = 0; i < ACH; i++) {
                 const int ci = tid + 256 * i;
-                if (ci < MS * 16 * 8) {
-                    const int row = ci >> 3, kc = ci & 7;
+                const bool ok = ci < MS * 16 * 8; /* uniform over each 8-lane row group */
+                const int row = ci >> 3, kc = ci & 7;
+                const int li = (kk * BM + row) * 8 + (kc ^ (row & 7));
+                if (F32IN) {
+                    /* k_pack_rows' arithmetic: pairs, then the group sum over
+                     * the 8 chunk-lanes of the row (xor 1, 2, 4) */
+                    const float4 a0 = af[F32IN ? kk : 0][F32IN ? i : 0][0], a1 = af[F32IN ? kk : 0][F32IN ? i : 0][1];
+                    float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+                    if (!ok)
+#pragma unroll
+                        for (int j = 0; j < 8; j++) v[j] = 0.0f;
+                    uint32_t hi[4], lo[4];
+                    float sg = 0.0f;
+                    sg = sg + qk_f32x8_pairs(v, hi, lo);
+                    sg += qk_dpp<QK_DPP_XOR1>(sg);
+                    sg += qk_dpp<QK_DPP_XOR2>(sg);
+                    sg += __shfl_xor(sg, 4, QK_WAVE);
+                    if (ok) {
+                        sm.a[buf][0][li] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+                        sm.a[buf][TERMS - 1][li] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+                        if (kc == 0) sm.p[st * KS + kk][row] = -128.0f * sg;
+                    }
+                } else if (ok) {
 #pragma unroll
                     for (int tm = 0; tm < TERMS; tm++)
-                        sm.a[buf][tm][(kk * BM + row) * 8 + (kc ^ (row & 7))] = ar[kk][tm][i];
+                        sm.a[buf][tm][li] = ar[F32IN ? 0 : kk][F32IN ? 0 : tm][F32IN ? 0 : i];
                 }
             }
     };
@@ -198,7 +235,7 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, BMT, CT, 
 #pragma unroll
     for (int i = 0; i < PCH; i++) {
         const int ci = tid + 256 * i;
-        if (ci < BM * (G >> 2)) {
+        if (!F32IN && ci < BM * (G >> 2)) {
             const int row = ci / (G >> 2), g4 = ci - row * (G >> 2);
             sm.p[4 * g4][row] = pv[i].x;
             sm.p[4 * g4 + 1][row] = pv[i].y;
@@ -213,7 +250,7 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, BMT, CT, 
 #pragma unroll
         for (int ct = 0; ct < CT; ct++) acc[rt][ct] = qm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    store_a(0);
+    store_a(0, 0);
     if (NST > 1) load_a(1);
     __syncthreads();
 
@@ -235,7 +272,7 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, BMT, CT, 
                 const int st = g / KS, buf = st & 1;
                 /* buffer buf^1 was last read in stage st-1, before the barrier
                  * ending it (past the last stage it is not read again) */
-                if (kk == 0 && (UNCOND || st + 1 < NST)) store_a(buf ^ 1);
+                if (kk == 0 && (UNCOND || st + 1 < NST)) store_a(buf ^ 1, st + 1);
                 if (kk == 0 && (UNCOND || st + 2 < NST)) load_a(min(st + 2, NST - 1));
                 qm_bf16x8 bop[CT][2];
 #pragma unroll
@@ -457,11 +494,12 @@ static int mm_launch(MmArgs &a, bool down, int terms, int max_tasks, hipStream_t
     if (wgs <= 0) return 0;
     const dim3 grid((unsigned)wgs), blk(256);
 #define MM_L(D, T, B, C) hipLaunchKernelGGL((k_mm<D, T, B, C>), grid, blk, 0, st, a)
+    /* down: always the two planes formed from f32 h */
     if (narrow) {
-        if (down) { if (terms == 2) MM_L(true, 2, 4, 2); else MM_L(true, 1, 4, 2); }
+        if (down) MM_L(true, 2, 4, 2);
         else { if (terms == 2) MM_L(false, 2, 4, 2); else MM_L(false, 1, 4, 2); }
     } else {
-        if (down) { if (terms == 2) MM_L(true, 2, MM_MT, 4); else MM_L(true, 1, MM_MT, 4); }
+        if (down) MM_L(true, 2, MM_MT, 4);
         else { if (terms == 2) MM_L(false, 2, MM_MT, 4); else MM_L(false, 1, MM_MT, 4); }
     }
 #undef MM_L
@@ -528,6 +566,7 @@ extern "C" int qk_launch_gateup_mfma(const qmoe_layer_weights *W, qk_shape s, co
     a.ap[0] = xhi;
     a.ap[1] = xlo ? xlo : xhi;
     a.ag = xg;
+    a.af = nullptr;
     a.out = h;
     a.perm = perm;
     a.tasks = tasks;
@@ -538,8 +577,7 @@ extern "C" int qk_launch_gateup_mfma(const qmoe_layer_weights *W, qk_shape s, co
     return mm_launch(a, false, xlo ? 2 : 1, qk_mfma_max_tasks(s, n), (hipStream_t)stream);
 }
 
-extern "C" int qk_launch_down_mfma(const qmoe_layer_weights *W, qk_shape s, const uint16_t *hhi,
-                                   const uint16_t *hlo, const float *hg, int n,
+extern "C" int qk_launch_down_mfma(const qmoe_layer_weights *W, qk_shape s, const float *h, int n,
                                    const int32_t *tasks, float *y, void *stream) {
     if (n <= 0) return 0;
     if (!qk_mfma_down_ok(s)) return (int)hipErrorInvalidValue;
@@ -550,9 +588,9 @@ extern "C" int qk_launch_down_mfma(const qmoe_layer_weights *W, qk_shape s, cons
     a.sq[0] = a.sq[1] = W->sh_down_q;
     a.ss[0] = a.ss[1] = W->sh_down_s;
     a.sb[0] = a.sb[1] = W->sh_down_b;
-    a.ap[0] = hhi;
-    a.ap[1] = hlo;
-    a.ag = hg;
+    a.ap[0] = a.ap[1] = nullptr;
+    a.ag = nullptr;
+    a.af = h;
     a.out = y;
     a.perm = nullptr;
     a.tasks = tasks;

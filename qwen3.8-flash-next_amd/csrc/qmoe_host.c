@@ -607,9 +607,6 @@ static int run_down(qmoe_ctx *c, const qmoe_layer_weights *W, const float *h, in
             rc = qk_launch_mfma_tasks(s, n, segtab, min_m, c->sc.tasks, stream);
             if (hip_fail(err, rc, "mfma tasks")) return -1;
         }
-        rc = qk_launch_pack_rows(h, 0, (size_t)n * (s.k + 1), s.I, c->sc.ahi, c->sc.alo, c->sc.ag,
-                                 stream);
-        if (hip_fail(err, rc, "pack h")) return -1;
     }
     if (mm && gemv && fork(c, stream, err)) return -1;
     if (gemv) {
@@ -619,7 +616,7 @@ static int run_down(qmoe_ctx *c, const qmoe_layer_weights *W, const float *h, in
         if (hip_fail(err, rc, "down")) return -1;
     }
     if (mm) {
-        rc = qk_launch_down_mfma(W, s, c->sc.ahi, c->sc.alo, c->sc.ag, n, c->sc.tasks, y, stream);
+        rc = qk_launch_down_mfma(W, s, h, n, c->sc.tasks, y, stream);
         if (hip_fail(err, rc, "down mfma")) return -1;
         if (gemv && join(c, stream, err)) return -1;
     }

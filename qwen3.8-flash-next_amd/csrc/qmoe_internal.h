@@ -132,9 +132,9 @@ int qk_launch_pack_rows(const void *x, int x_bf16, size_t rows, int K, uint16_t 
 int qk_launch_gateup_mfma(const qmoe_layer_weights *W, qk_shape s, const uint16_t *xhi,
                           const uint16_t *xlo, const float *xg, int n, const int32_t *perm,
                           const int32_t *tasks, float *h, void *stream);
-int qk_launch_down_mfma(const qmoe_layer_weights *W, qk_shape s, const uint16_t *hhi,
-                        const uint16_t *hlo, const float *hg, int n, const int32_t *tasks,
-                        float *y, void *stream);
+/* the down projection reads h [n*k+n, I] f32 itself (no packed planes) */
+int qk_launch_down_mfma(const qmoe_layer_weights *W, qk_shape s, const float *h, int n,
+                        const int32_t *tasks, float *y, void *stream);
 /* one token, layer path: gate/up with the top-k of `logits` selected inside
  * the kernel, which also writes idx, w, sg, perm, pos and the segment
  * table (the form the dispatch produces for one token) */
