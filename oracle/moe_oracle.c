@@ -280,6 +280,75 @@ void orc_gemm_q4(int M, int N, int K, const float *A, const uint32_t *W,
     free(b);
 }
 
+/* ------------------------------------------------------- hyper connection */
+
+/* kernel.c:22-36 (groups of `group` with weight w[(g % per_row) * group..]);
+ * the sum of squares contracts to an fma chain as kernel_rmsnorm's does */
+static void rmsnorm_grouped(const float *x, const float *w, size_t total, size_t group, size_t rows,
+                            float eps, float *y) {
+    const size_t groups = total / group, per_row = rows ? groups / rows : groups;
+    for (size_t g = 0; g < groups; g++) {
+        const float *xg = x + g * group;
+        float ss = 0.0f;
+        for (size_t i = 0; i < group; i++) ss = fmaf(xg[i], xg[i], ss);
+        const float r = 1.0f / sqrtf(ss / (float)group + eps);
+        const float *wg = w ? w + (g % per_row) * group : NULL;
+        for (size_t i = 0; i < group; i++) y[g * group + i] = xg[i] * r * (wg ? wg[i] : 1.0f);
+    }
+}
+
+int orc_hc_mix(const orc_hc *H, const float *hyper, int n, float *mixed, float *inject,
+               float *normed_out) {
+    const int hc = H->hc, d = H->d, R = H->lowrank, hd = hc * d;
+    if (n <= 0) return 0;
+    float *normed = (float *)malloc((size_t)n * hd * sizeof(float));
+    float *w = (float *)malloc((size_t)n * R * sizeof(float));
+    float *tmp = (float *)malloc((size_t)n * hd * sizeof(float));
+    if (!normed || !w || !tmp) {
+        free(normed);
+        free(w);
+        free(tmp);
+        return -1;
+    }
+    rmsnorm_grouped(hyper, H->hc_norm, (size_t)n * hd, (size_t)d, (size_t)n, 1e-6f, normed);
+    /* w = silu(down(normed) / hc) (model.c:755-758) */
+    orc_gemm_q4(n, R, hd, normed, H->down_q, H->down_s, H->down_b, H->group_size, w);
+    for (size_t i = 0; i < (size_t)n * R; i++) w[i] = orc_silu(w[i] * (1.0f / hc));
+    /* tmp = sigmoid(up(w)) (model.c:760-761) */
+    orc_gemm_q4(n, hd, R, w, H->up_q, H->up_s, H->up_b, H->group_size, tmp);
+    for (size_t i = 0; i < (size_t)n * hd; i++) tmp[i] = orc_sigmoid(tmp[i]);
+    /* mixed = mean over hc of tmp * normed (model.c:776-785) */
+    for (int t = 0; t < n; t++)
+        for (int i = 0; i < d; i++) {
+            float acc = 0.0f;
+            for (int h = 0; h < hc; h++)
+                acc = fmaf(tmp[(size_t)t * hd + (size_t)h * d + i], normed[(size_t)t * hd + (size_t)h * d + i],
+                           acc);
+            mixed[(size_t)t * d + i] = acc / (float)hc;
+        }
+    /* inject = 2 * sigmoid(block_inject(normed) / hc) (model.c:787-793) */
+    if (inject) {
+        orc_gemm_bf16(n, hc, hd, normed, H->inject_w, inject);
+        for (size_t i = 0; i < (size_t)n * hc; i++)
+            inject[i] = 2.0f * orc_sigmoid(inject[i] * (1.0f / hc));
+    }
+    if (normed_out) memcpy(normed_out, normed, (size_t)n * hd * sizeof(float));
+    free(normed);
+    free(w);
+    free(tmp);
+    return 0;
+}
+
+void orc_hc_inject(int hc, int d, int n, const float *inject, const float *out, float *hyper) {
+    for (int t = 0; t < n; t++)
+        for (int hh = 0; hh < hc; hh++) {
+            const float inj = inject[(size_t)t * hc + hh];
+            for (int j = 0; j < d; j++)
+                hyper[((size_t)t * hc + hh) * d + j] =
+                    fmaf(inj, out[(size_t)t * d + j], hyper[((size_t)t * hc + hh) * d + j]);
+        }
+}
+
 /* -------------------------------------------------------------- dispatch */
 
 /* Stable counting sort of flat slots f = t*k + s by expert id.  Because the

@@ -18,6 +18,8 @@
  *   c/src/kernel.c:230-309    gemm_q4 (per-group s*sum(xq) + b*sum(x) identity)
  *   c/src/util.h:56-71        bf16 <-> f32 (shift widen, RNE narrow)
  *   c/src/model.c:424-472,539-674  expert tensor layout [E,I,H/8] / [E,H,I/8]
+ *   c/src/model.c:728-796,1703-1731  the MLP hyper connection around the layer
+ *   c/src/kernel.c:22-36,45-55  kernel_rmsnorm_grouped, sigmoid, scale
  *
  * Deliberate departures (each is also a contract the GPU path keeps):
  *   1. Router dot products use the fixed "R64" order (orc_dot_r64): 64
@@ -144,6 +146,28 @@ int orc_moe_forward(const orc_layer *L, const void *x, int n, float *out,
 int orc_route(const orc_layer *L, const void *x, int x_is_bf16, int n, float *logits_out,
               float *gate_logit_out, int *idx_out, float *w_out, float *shared_gate_out,
               float *xn_out, int n_threads, char *err);
+
+/* ---- the hyper connection around the MoE layer (c/src/model.c:728-796,
+ * 1703-1731): the MLP's gated_residual produces the MoE input from the
+ * hyper state, and the MoE output is injected back into every copy ---- */
+typedef struct {
+    int hc, d, lowrank, group_size;
+    const float *hc_norm;          /* [hc*d] */
+    const uint32_t *down_q;        /* [lowrank, hc*d/8] q4 (input_mix_weight_down) */
+    const uint16_t *down_s, *down_b; /* [lowrank, hc*d/g] bf16 */
+    const uint32_t *up_q;          /* [hc*d, lowrank/8] q4 (input_mix_weight_up) */
+    const uint16_t *up_s, *up_b;   /* [hc*d, lowrank/g] bf16 */
+    const uint16_t *inject_w;      /* [hc, hc*d] bf16 (block_inject_weight) */
+} orc_hc;
+
+/* gated_residual with inject (model.c:728-796): hyper [n, hc*d] ->
+ * mixed [n, d] (the MoE input), inject [n, hc]; normed [n, hc*d] may be
+ * NULL.  Grouped RMSNorm as kernel.c:22-36 (eps 1e-6), linear layers as
+ * linear_forward (gemm_q4) and gemm_bf16 (naive order). */
+int orc_hc_mix(const orc_hc *H, const float *hyper, int n, float *mixed, float *inject,
+               float *normed_out);
+/* model.c:1724-1731: hyper[t, hh, j] += inject[t, hh] * out[t, j] */
+void orc_hc_inject(int hc, int d, int n, const float *inject, const float *out, float *hyper);
 
 /* ---- seeded synthetic tensors (counter-based; the GPU generator in the
  * product library produces the same values) ---- */

@@ -21,6 +21,8 @@ TAG = dict(
     ROUTER_W=1, GATE_Q=2, GATE_S=3, GATE_B=4, UP_Q=5, UP_S=6, UP_B=7, DOWN_Q=8, DOWN_S=9,
     DOWN_B=10, SH_GATE_Q=11, SH_GATE_S=12, SH_GATE_B=13, SH_UP_Q=14, SH_UP_S=15, SH_UP_B=16,
     SH_DOWN_Q=17, SH_DOWN_S=18, SH_DOWN_B=19, SHGATE_W=20, X=22,
+    HC_DOWN_Q=24, HC_DOWN_S=25, HC_DOWN_B=26, HC_UP_Q=27, HC_UP_S=28, HC_UP_B=29,
+    HC_INJECT_W=30, HYPER=31,
 )
 
 ROUTED_FAITHFUL, ROUTED_Q4 = 0, 1
@@ -44,6 +46,14 @@ class OrcLayer(ctypes.Structure):
         ("sh_up_q", _P), ("sh_up_s", _P), ("sh_up_b", _P),
         ("sh_down_q", _P), ("sh_down_s", _P), ("sh_down_b", _P),
         ("sh_gate_w", _P), ("norm_w", _P),
+    ]
+
+
+class OrcHc(ctypes.Structure):
+    _fields_ = [
+        ("hc", _I), ("d", _I), ("lowrank", _I), ("group_size", _I), ("hc_norm", _P),
+        ("down_q", _P), ("down_s", _P), ("down_b", _P),
+        ("up_q", _P), ("up_s", _P), ("up_b", _P), ("inject_w", _P),
     ]
 
 
@@ -72,6 +82,8 @@ _SIG = {
     "orc_moe_forward": (_I, [ctypes.POINTER(OrcLayer), _P, _I, _P, ctypes.POINTER(OrcOpts), _P, _I,
                              _P, _P, _P, _P, _P, _P, _P]),
     "orc_route": (_I, [ctypes.POINTER(OrcLayer), _P, _I, _I, _P, _P, _P, _P, _P, _P, _I, _P]),
+    "orc_hc_mix": (_I, [ctypes.POINTER(OrcHc), _P, _I, _P, _P, _P]),
+    "orc_hc_inject": (None, [_I, _I, _I, _P, _P, _P]),
     "orc_mix64": (_U64, [_U64]),
     "orc_tensor_key": (_U64, [_U64, ctypes.c_uint32, ctypes.c_uint32]),
     "orc_gen_normal_bf16": (None, [_P, _SZ, _U64, _U64, _F]),
@@ -281,6 +293,85 @@ class Layer:
         opts = OrcOpts(int(x_is_bf16), int(residual), routed_mode, n_threads)
         return lib().orc_time_forward(ctypes.byref(self.st), _p(x), x.shape[0], _p(out),
                                       ctypes.byref(opts), warmup, iters)
+
+
+class Hyper:
+    """The MLP hyper connection of one layer (c/src/model.c:728-796,
+    1703-1731) in host memory: hc_norm [hc*d] f32, input_mix_weight_down
+    [R, hc*d] and input_mix_weight_up [hc*d, R] as q4 (codes U{0..15},
+    scales N(0,0.02), biases N(0,0.01)), block_inject_weight [hc, hc*d] bf16
+    N(0,0.02), from the same seeded streams as qmoe_hc_synth_layer;
+    hc_norm is all ones there (norm_std = 0) or 1 + N(0, norm_std)."""
+
+    KEYS = ("hc_norm", "down_q", "down_s", "down_b", "up_q", "up_s", "up_b", "inject_w")
+
+    def __init__(self, hc, d, lowrank, seed=0, layer=0, group_size=64, norm_std=0.0):
+        self.hc, self.d, self.R, self.g = hc, d, lowrank, group_size
+        D, R, g, s, L = hc * d, lowrank, group_size, seed, layer
+        self.t = {}
+        if norm_std:
+            self.t["hc_norm"] = (1.0 + np.random.default_rng(seed * 7919 + layer)
+                                 .normal(0.0, norm_std, D)).astype(np.float32)
+        else:
+            self.t["hc_norm"] = np.ones(D, np.float32)
+        self.t["down_q"] = gen_codes(R * D // 8, s, L, "HC_DOWN_Q")
+        self.t["down_s"] = gen_bf16(R * D // g, s, L, "HC_DOWN_S", 0.02)
+        self.t["down_b"] = gen_bf16(R * D // g, s, L, "HC_DOWN_B", 0.01)
+        self.t["up_q"] = gen_codes(D * R // 8, s, L, "HC_UP_Q")
+        self.t["up_s"] = gen_bf16(D * R // g, s, L, "HC_UP_S", 0.02)
+        self.t["up_b"] = gen_bf16(D * R // g, s, L, "HC_UP_B", 0.01)
+        self.t["inject_w"] = gen_bf16(hc * D, s, L, "HC_INJECT_W", 0.02)
+        self._build()
+
+    @classmethod
+    def from_arrays(cls, hc, d, lowrank, arrays, group_size=64):
+        self = cls.__new__(cls)
+        self.hc, self.d, self.R, self.g = hc, d, lowrank, group_size
+        self.t = {k: np.ascontiguousarray(arrays[k]) for k in cls.KEYS}
+        self._build()
+        return self
+
+    def _build(self):
+        st = OrcHc()
+        st.hc, st.d, st.lowrank, st.group_size = self.hc, self.d, self.R, self.g
+        for f, a in self.t.items():
+            setattr(st, f, _p(a))
+        self.st = st
+
+    def arrays(self):
+        return dict(self.t)
+
+    def mix(self, hyper):
+        """gated_residual: hyper [n, hc*d] f32 -> mixed [n, d], inject [n, hc], normed"""
+        hyper = np.ascontiguousarray(hyper, dtype=np.float32)
+        n = hyper.shape[0]
+        mixed = np.empty((n, self.d), np.float32)
+        inject = np.empty((n, self.hc), np.float32)
+        normed = np.empty((n, self.hc * self.d), np.float32)
+        if lib().orc_hc_mix(ctypes.byref(self.st), _p(hyper), n, _p(mixed), _p(inject), _p(normed)):
+            raise MemoryError("orc_hc_mix")
+        return dict(mixed=mixed, inject=inject, normed=normed)
+
+    def inject_update(self, hyper, inject, out):
+        """hyper[t, hh, :] += inject[t, hh] * out[t, :] on a copy"""
+        h = np.array(hyper, dtype=np.float32, order="C", copy=True)
+        inject = np.ascontiguousarray(inject, dtype=np.float32)
+        out = np.ascontiguousarray(out, dtype=np.float32)
+        lib().orc_hc_inject(self.hc, self.d, h.shape[0], _p(inject), _p(out), _p(h))
+        return h
+
+    def layer_forward(self, layer, hyper):
+        """model.c:1710-1731: mix, the MoE layer on mixed (f32), inject update;
+        returns the new hyper state and the intermediates"""
+        m = self.mix(hyper)
+        r = layer.forward(m["mixed"], False)
+        return dict(hyper=self.inject_update(hyper, m["inject"], r["out"]), moe_out=r["out"],
+                    **m)
+
+
+def gen_hyper(n, hc, d, seed, layer=0, std=1.0):
+    """hyper states [n, hc*d] f32 from the HYPER stream"""
+    return gen_f32(n * hc * d, seed, layer, "HYPER", std).reshape(n, hc * d)
 
 
 def gen_x(n, H, seed, bf16, layer=0, std=1.0):
