@@ -183,7 +183,11 @@ enum {
     QMOE_TAG_SH_UP_Q = 14, QMOE_TAG_SH_UP_S = 15, QMOE_TAG_SH_UP_B = 16,
     QMOE_TAG_SH_DOWN_Q = 17, QMOE_TAG_SH_DOWN_S = 18, QMOE_TAG_SH_DOWN_B = 19,
     QMOE_TAG_SHGATE_W = 20,
-    QMOE_TAG_X = 22
+    QMOE_TAG_X = 22,
+    /* hyper connection (qmoe_hc_synth_layer) and hyper states */
+    QMOE_TAG_HC_DOWN_Q = 24, QMOE_TAG_HC_DOWN_S = 25, QMOE_TAG_HC_DOWN_B = 26,
+    QMOE_TAG_HC_UP_Q = 27, QMOE_TAG_HC_UP_S = 28, QMOE_TAG_HC_UP_B = 29,
+    QMOE_TAG_HC_INJECT_W = 30, QMOE_TAG_HYPER = 31
 };
 
 /* ------------------------------------------------------------ stages */
@@ -272,6 +276,68 @@ int qmoe_last_routing(qmoe_ctx *ctx, int n, int32_t *idx_out, float *w_out, floa
  * scratch is not needed (the context owns device scratch). */
 int qmoe_moe_forward_host(qmoe_ctx *ctx, int layer, const float *x, int n, float *out,
                           qmoe_err *err);
+
+/* ------------------------------------------------------ hyper connection
+ * The MoE layer's input producer and output consumer in the reference
+ * model: the MLP hyper connection of each decoder layer.  The residual
+ * stream is a hyper state of hc copies of the hidden vector, [n, hc*H] f32
+ * (c/src/model.c:1590-1606).  Before the MoE, gated_residual
+ * (model.c:728-796, called at model.c:1710-1711) mixes it down to the MoE
+ * input:
+ *   normed = per-copy RMSNorm (eps 1e-6) * hc_norm            [n, hc*H]
+ *   w      = silu(input_mix_weight_down(normed) / hc)         [n, R]
+ *   mixed  = mean over copies of sigmoid(input_mix_weight_up(w)) * normed   [n, H]
+ *   inject = 2 * sigmoid(block_inject_weight(normed) / hc)    [n, hc]
+ * and after it every copy takes the MoE output (model.c:1724-1731):
+ *   hyper[t, j, :] += inject[t, j] * out[t, :].
+ * R = hc_lowrank.  The two mix weights are MLX q4 (group 64) as in the
+ * checkpoint; block_inject_weight is dense bf16 (gemm_bf16, model.c:789). */
+typedef struct {
+    const float *hc_norm;     /* [hc*H]      f32   mlp_hyper_connection.hc_norm.weight */
+    const uint32_t *down_q;   /* [R, hc*H/8] u32   .input_mix_weight_down.weight */
+    const uint16_t *down_s;   /* [R, hc*H/g] bf16  .scales */
+    const uint16_t *down_b;   /* [R, hc*H/g] bf16  .biases */
+    const uint32_t *up_q;     /* [hc*H, R/8] u32   .input_mix_weight_up.weight */
+    const uint16_t *up_s;     /* [hc*H, R/g] bf16  .scales */
+    const uint16_t *up_b;     /* [hc*H, R/g] bf16  .biases */
+    const uint16_t *inject_w; /* [hc, hc*H]  bf16  .block_inject_weight.weight */
+} qmoe_hc_weights;
+
+/* Gives the context hyper-connection slots for every layer and the mix
+ * scratch (sized by max_tokens): hc_count (<= 8) copies, low rank
+ * hc_lowrank (a multiple of 64, <= 2048), hc_count*hidden <= 8192.  The
+ * text_config's hc_count / hc_lowrank (model.c:86-87).  Calling it again
+ * with the same values is a no-op. */
+int qmoe_hc_enable(qmoe_ctx *ctx, int hc_count, int hc_lowrank, qmoe_err *err);
+/* one layer's hyper-connection tensors from host memory (mw_load and
+ * mw_load_f32 of model.c:1945-1952) */
+int qmoe_hc_upload_layer(qmoe_ctx *ctx, int layer, const qmoe_hc_weights *host, qmoe_err *err);
+/* the same from a checkpoint: model.layers.<model_layer>.mlp_hyper_connection.*
+ * (model.c:1945-1952, 1959-1964).  hc_norm is BF16 in the file and widened
+ * to f32 (mw_load_f32, model.c:275-294); the mix weights must be q4 (a
+ * missing .biases reads as zero), block_inject_weight dense BF16. */
+int qmoe_hc_upload_layer_st(qmoe_ctx *ctx, int layer, const qmoe_st *ix, int model_layer,
+                            qmoe_err *err);
+/* seeded synthetic hyper-connection weights: hc_norm ones, codes U{0..15},
+ * scales N(0,0.02), biases N(0,0.01), block_inject_weight N(0,0.02).  No
+ * counterpart in the reference (bench/test helper). */
+int qmoe_hc_synth_layer(qmoe_ctx *ctx, int layer, uint64_t seed, qmoe_err *err);
+int qmoe_hc_device_weights(qmoe_ctx *ctx, int layer, qmoe_hc_weights *out, qmoe_err *err);
+
+/* gated_residual with inject (model.c:728-796): hyper [n, hc*H] f32 ->
+ * mixed_out [n, H] f32, inject_out [n, hc] f32 (may be NULL), normed_out
+ * [n, hc*H] f32 (may be NULL). */
+int qmoe_hc_mix(qmoe_ctx *ctx, int layer, const float *hyper, int n, float *mixed_out,
+                float *inject_out, float *normed_out, void *stream, qmoe_err *err);
+/* the inject update alone (model.c:1724-1731), hyper updated in place */
+int qmoe_hc_inject(qmoe_ctx *ctx, const float *inject, const float *moe_out, int n, float *hyper,
+                   void *stream, qmoe_err *err);
+/* model.c:1710-1731 on device buffers: gated_residual, the MoE layer on
+ * the mixed input, and the inject update fused into the layer's combine;
+ * hyper [n, hc*H] f32 is updated in place.  moe_out [n, H] f32 receives the
+ * MoE output when non-NULL. */
+int qmoe_hc_layer_forward(qmoe_ctx *ctx, int layer, float *hyper, int n, float *moe_out,
+                          void *stream, qmoe_err *err);
 
 /* Size in bytes of the context's device scratch and of one resident layer. */
 size_t qmoe_scratch_bytes(const qmoe_ctx *ctx);

@@ -19,8 +19,10 @@ struct CombineArgs {
     const float *w;     /* [n, k] */
     const float *sg;    /* [n] */
     const void *xres;   /* [n, H] or null */
-    float *out;         /* [n, H] */
-    int H, k, n, xbf16;
+    float *out;         /* [n, H] or null (with hyper) */
+    float *hyper;       /* [n, hc, H] or null: hyper[t, j] += inject[t, j] * out[t] */
+    const float *inject; /* [n, hc] */
+    int H, k, n, xbf16, hc;
 };
 
 /*
@@ -28,6 +30,8 @@ struct CombineArgs {
  * slots are taken in ascending dispatch position, i.e. ascending expert id
  * (the expert loop order of model.c:1338), each as out = fma(w, y, out)
  * from out = 0, then out = fma(g, y_shared, out), then the optional residual.
+ * With a hyper state, every copy j of token t becomes
+ * fma(inject[t, j], out, hyper[t, j]) (model.c:1724-1731).
  */
 __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
     __shared__ int s_pos[QK_MAX_TOPK];
@@ -97,14 +101,27 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
         acc.z = xv.z + acc.z;
         acc.w = xv.w + acc.w;
     }
-    *(float4 *)(a.out + (size_t)t * a.H + c) = acc;
+    if (a.out) *(float4 *)(a.out + (size_t)t * a.H + c) = acc;
+    if (a.hyper) {
+        for (int j = 0; j < a.hc; j++) {
+            const float inj = qk_ld(a.inject + (size_t)t * a.hc + j);
+            float4 *hp = (float4 *)(a.hyper + ((size_t)t * a.hc + j) * a.H + c);
+            float4 hv = *hp;
+            hv.x = fmaf(inj, acc.x, hv.x);
+            hv.y = fmaf(inj, acc.y, hv.y);
+            hv.z = fmaf(inj, acc.z, hv.z);
+            hv.w = fmaf(inj, acc.w, hv.w);
+            *hp = hv;
+        }
+    }
 }
 
 extern "C" int qk_launch_combine(qk_shape s, int n, const float *y, const int32_t *pos,
                                  const float *w, const float *sg, const void *x_res, int x_bf16,
-                                 float *out, void *stream) {
+                                 float *out, float *hyper, const float *inject, int hc,
+                                 void *stream) {
     if (n <= 0) return 0;
-    CombineArgs a{y, pos, w, sg, x_res, out, s.H, s.k, n, x_bf16};
+    CombineArgs a{y, pos, w, sg, x_res, out, hyper, inject, s.H, s.k, n, x_bf16, hc};
     dim3 grid(n, (s.H + 1023) / 1024);
     hipLaunchKernelGGL(k_combine, grid, dim3(256), 0, (hipStream_t)stream, a);
     return QK_CHECK_LAUNCH();

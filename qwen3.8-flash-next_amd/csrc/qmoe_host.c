@@ -41,6 +41,14 @@ struct qmoe_ctx {
     hipEvent_t ev_fork, ev_join;
     /* byte offsets of each tensor inside a layer allocation */
     size_t off[24];
+    /* MLP hyper connection (qmoe_hc_enable): hc copies, low rank R, per-layer
+     * weights in one allocation each, and the scratch of the mix */
+    int hc, hc_R;
+    size_t hc_off[QH_HC_COUNT], hc_layer_bytes;
+    void **hc_mem;
+    int *hc_ready;
+    void *hc_scratch;
+    float *hc_normed, *hc_down, *hc_inject, *hc_mixed;
 };
 
 static void set_err(qmoe_err *err, const char *fmt, ...) {
@@ -225,6 +233,12 @@ void qmoe_destroy(qmoe_ctx *c) {
     if (c->aux) hipStreamDestroy(c->aux);
     if (c->host_x_dev) hipFree(c->host_x_dev);
     if (c->host_out_dev) hipFree(c->host_out_dev);
+    if (c->hc_mem)
+        for (int l = 0; l < c->cfg.n_layers; l++)
+            if (c->hc_mem[l]) hipFree(c->hc_mem[l]);
+    if (c->hc_scratch) hipFree(c->hc_scratch);
+    free(c->hc_mem);
+    free(c->hc_ready);
     free(c->layers);
     free(c);
 }
@@ -739,26 +753,20 @@ int qmoe_combine(qmoe_ctx *c, const float *y, const int32_t *perm, const float *
     if (hip_fail(err, qk_launch_invert_perm(n * c->cfg.top_k, perm, c->sc.pos, stream), "invert"))
         return -1;
     return hip_fail(err, qk_launch_combine(c->shape, n, y, c->sc.pos, w, shared_gate, x_residual,
-                                           x_dtype == QMOE_BF16, out, stream),
+                                           x_dtype == QMOE_BF16, out, NULL, NULL, 0, stream),
                     "combine");
 }
 
-int qmoe_layer_forward(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n, float *out,
-                       int flags, void *stream, qmoe_err *err) {
-    clear_err(err);
-    if (check_call(c, layer, n, err) || check_dtype(x_dtype, err)) return -1;
-    if (flags & ~QMOE_RESIDUAL) {
-        set_err(err, "unknown flags 0x%x", flags);
-        return -1;
-    }
-    if (n == 0) return 0;
-    NEED(x, "x");
-    NEED(out, "out");
+/* the layer on checked arguments; with hyper set the combine also applies
+ * the hyper connection's inject update (out may then be NULL) */
+static int layer_forward(qmoe_ctx *c, int layer, const void *x, int xbf, int n, float *out,
+                         int residual, float *hyper, const float *inject, void *stream,
+                         qmoe_err *err) {
     c->last_n = n;
     const qmoe_layer_weights *W = &c->layers[layer].dev;
     const qk_shape s = c->shape;
     qk_scratch *sc = &c->sc;
-    const int xbf = x_dtype == QMOE_BF16;
+    const int hc = hyper ? c->hc : 0;
     int rc;
     float *xn = W->norm_w ? sc->xn : NULL;
     rc = qk_launch_router(W, s, x, xbf, n, sc->logits, xn, stream);
@@ -771,7 +779,7 @@ int qmoe_layer_forward(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n
                                    sc->pos, sc->segtab, sc->h, stream);
         if (hip_fail(err, rc, "gate/up + top-k")) return -1;
         rc = qk_launch_down_combine(W, s, sc->h, n, sc->segtab, sc->pos, sc->w, sc->sg,
-                                    (flags & QMOE_RESIDUAL) ? x : NULL, xbf, out, stream);
+                                    residual ? x : NULL, xbf, out, hyper, inject, hc, stream);
         return hip_fail(err, rc, "down+combine");
     }
     /* the dispatch also builds the MFMA task list when the gate/up runs on
@@ -794,14 +802,304 @@ int qmoe_layer_forward(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n
     if (run_gateup(c, W, xf, xf_bf, n, sc->perm, sc->segtab, gu_mm, sc->h, stream, err)) return -1;
     if (!mfma_usable(c, n, 2) && qk_down_combine_lds(s, n) > 0) {
         rc = qk_launch_down_combine(W, s, sc->h, n, sc->segtab, sc->pos, sc->w, sc->sg,
-                                    (flags & QMOE_RESIDUAL) ? x : NULL, xbf, out, stream);
+                                    residual ? x : NULL, xbf, out, hyper, inject, hc, stream);
         return hip_fail(err, rc, "down+combine");
     }
     if (run_down(c, W, sc->h, n, sc->segtab, mfma_usable(c, n, xf_bf ? 0 : 1), sc->y, stream, err))
         return -1;
-    rc = qk_launch_combine(s, n, sc->y, sc->pos, sc->w, sc->sg,
-                           (flags & QMOE_RESIDUAL) ? x : NULL, xbf, out, stream);
+    rc = qk_launch_combine(s, n, sc->y, sc->pos, sc->w, sc->sg, residual ? x : NULL, xbf, out,
+                           hyper, inject, hc, stream);
     return hip_fail(err, rc, "combine");
+}
+
+int qmoe_layer_forward(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n, float *out,
+                       int flags, void *stream, qmoe_err *err) {
+    clear_err(err);
+    if (check_call(c, layer, n, err) || check_dtype(x_dtype, err)) return -1;
+    if (flags & ~QMOE_RESIDUAL) {
+        set_err(err, "unknown flags 0x%x", flags);
+        return -1;
+    }
+    if (n == 0) return 0;
+    NEED(x, "x");
+    NEED(out, "out");
+    return layer_forward(c, layer, x, x_dtype == QMOE_BF16, n, out, (flags & QMOE_RESIDUAL) != 0,
+                         NULL, NULL, stream, err);
+}
+
+/* ------------------------------------------------------ hyper connection */
+
+static void hc_shape(const qmoe_ctx *c, int t, size_t *count, size_t *esize) {
+    const size_t D = (size_t)c->hc * c->cfg.hidden, R = (size_t)c->hc_R, g = QK_GROUP;
+    size_t n = 0, es = 2;
+    switch (t) {
+    case QH_HC_NORM: n = D; es = 4; break;
+    case QH_HC_DOWN_Q: n = R * D / 8; es = 4; break;
+    case QH_HC_DOWN_S: case QH_HC_DOWN_B: n = R * D / g; break;
+    case QH_HC_UP_Q: n = D * R / 8; es = 4; break;
+    case QH_HC_UP_S: case QH_HC_UP_B: n = D * R / g; break;
+    case QH_HC_INJECT_W: n = (size_t)c->hc * D; break;
+    }
+    *count = n;
+    *esize = es;
+}
+
+int qmoe_hc_enable(qmoe_ctx *c, int hc_count, int hc_lowrank, qmoe_err *err) {
+    clear_err(err);
+    if (!c) {
+        set_err(err, "ctx is NULL");
+        return -1;
+    }
+    if (c->hc) {
+        if (c->hc == hc_count && c->hc_R == hc_lowrank) return 0;
+        set_err(err, "hyper connection already enabled with hc_count %d, hc_lowrank %d", c->hc,
+                c->hc_R);
+        return -1;
+    }
+    if (!qk_hc_shape_ok(hc_count, c->cfg.hidden, hc_lowrank)) {
+        set_err(err, "hc_count %d, hc_lowrank %d unsupported with hidden %d (needs 1 <= hc_count <= 8, "
+                     "hc_lowrank a multiple of 64 in [64, 2048], hc_count*hidden <= 8192)",
+                hc_count, hc_lowrank, c->cfg.hidden);
+        return -1;
+    }
+    c->hc = hc_count;
+    c->hc_R = hc_lowrank;
+    size_t o = 0;
+    for (int t = 0; t < QH_HC_COUNT; t++) {
+        size_t n, es;
+        hc_shape(c, t, &n, &es);
+        c->hc_off[t] = o;
+        o = align_up(o + n * es);
+    }
+    c->hc_layer_bytes = o;
+    c->hc_mem = (void **)calloc((size_t)c->cfg.n_layers, sizeof(void *));
+    c->hc_ready = (int *)calloc((size_t)c->cfg.n_layers, sizeof(int));
+    const size_t n = (size_t)c->cfg.max_tokens, H = (size_t)c->cfg.hidden;
+    const size_t D = (size_t)hc_count * H, R = (size_t)hc_lowrank;
+    const size_t sz[4] = {n * D * 4, n * R * 4, n * (size_t)hc_count * 4, n * H * 4};
+    size_t total = 0, offs[4];
+    for (int i = 0; i < 4; i++) {
+        offs[i] = total;
+        total = align_up(total + sz[i]);
+    }
+    if (!c->hc_mem || !c->hc_ready ||
+        hip_fail(err, (int)hipMalloc(&c->hc_scratch, total), "hipMalloc(hc scratch)")) {
+        if (!c->hc_mem || !c->hc_ready) set_err(err, "out of host memory");
+        free(c->hc_mem);
+        free(c->hc_ready);
+        c->hc_mem = NULL;
+        c->hc_ready = NULL;
+        c->hc_scratch = NULL;
+        c->hc = c->hc_R = 0;
+        return -1;
+    }
+    char *b = (char *)c->hc_scratch;
+    c->hc_normed = (float *)(b + offs[0]);
+    c->hc_down = (float *)(b + offs[1]);
+    c->hc_inject = (float *)(b + offs[2]);
+    c->hc_mixed = (float *)(b + offs[3]);
+    return 0;
+}
+
+static int hc_check_layer(qmoe_ctx *c, int layer, qmoe_err *err) {
+    if (check_layer_index(c, layer, err)) return -1;
+    if (!c->hc) {
+        set_err(err, "hyper connection not enabled (qmoe_hc_enable)");
+        return -1;
+    }
+    return 0;
+}
+
+static int hc_ensure_mem(qmoe_ctx *c, int layer, qmoe_err *err) {
+    if (c->hc_mem[layer]) return 0;
+    return hip_fail(err, (int)hipMalloc(&c->hc_mem[layer], c->hc_layer_bytes), "hipMalloc(hc layer)");
+}
+
+static void hc_dev(const qmoe_ctx *c, int layer, qmoe_hc_weights *d) {
+    char *b = (char *)c->hc_mem[layer];
+    d->hc_norm = (const float *)(b + c->hc_off[QH_HC_NORM]);
+    d->down_q = (const uint32_t *)(b + c->hc_off[QH_HC_DOWN_Q]);
+    d->down_s = (const uint16_t *)(b + c->hc_off[QH_HC_DOWN_S]);
+    d->down_b = (const uint16_t *)(b + c->hc_off[QH_HC_DOWN_B]);
+    d->up_q = (const uint32_t *)(b + c->hc_off[QH_HC_UP_Q]);
+    d->up_s = (const uint16_t *)(b + c->hc_off[QH_HC_UP_S]);
+    d->up_b = (const uint16_t *)(b + c->hc_off[QH_HC_UP_B]);
+    d->inject_w = (const uint16_t *)(b + c->hc_off[QH_HC_INJECT_W]);
+}
+
+int qh_hc_config(qmoe_ctx *c, int layer, int *hc, int *lowrank, int *d, qmoe_err *err) {
+    if (hc_check_layer(c, layer, err)) return -1;
+    *hc = c->hc;
+    *lowrank = c->hc_R;
+    *d = c->cfg.hidden;
+    return 0;
+}
+
+int qh_hc_slot(qmoe_ctx *c, int layer, int t, void **dst, size_t *bytes, qmoe_err *err) {
+    if (t < 0 || t >= QH_HC_COUNT) {
+        set_err(err, "hc tensor slot %d out of range", t);
+        return -1;
+    }
+    if (hc_ensure_mem(c, layer, err)) return -1;
+    c->hc_ready[layer] = 0;
+    size_t n, es;
+    hc_shape(c, t, &n, &es);
+    *dst = (char *)c->hc_mem[layer] + c->hc_off[t];
+    *bytes = n * es;
+    return 0;
+}
+
+void qh_hc_begin(qmoe_ctx *c, int layer) { c->hc_ready[layer] = 0; }
+void qh_hc_end(qmoe_ctx *c, int layer) { c->hc_ready[layer] = 1; }
+
+int qmoe_hc_upload_layer(qmoe_ctx *c, int layer, const qmoe_hc_weights *h, qmoe_err *err) {
+    clear_err(err);
+    if (hc_check_layer(c, layer, err)) return -1;
+    NEED(h, "weights");
+    const void *src[QH_HC_COUNT] = {h->hc_norm, h->down_q, h->down_s, h->down_b,
+                                    h->up_q,    h->up_s,   h->up_b,   h->inject_w};
+    static const char *names[QH_HC_COUNT] = {"hc_norm", "down_q", "down_s", "down_b",
+                                             "up_q",    "up_s",   "up_b",   "inject_w"};
+    for (int t = 0; t < QH_HC_COUNT; t++)
+        if (!src[t]) {
+            set_err(err, "missing hyper-connection tensor %s for layer %d", names[t], layer);
+            return -1;
+        }
+    if (hc_ensure_mem(c, layer, err)) return -1;
+    c->hc_ready[layer] = 0;
+    for (int t = 0; t < QH_HC_COUNT; t++) {
+        size_t n, es;
+        hc_shape(c, t, &n, &es);
+        if (hip_fail(err, (int)hipMemcpy((char *)c->hc_mem[layer] + c->hc_off[t], src[t], n * es,
+                                         hipMemcpyHostToDevice),
+                     "hipMemcpy(hc upload)"))
+            return -1;
+    }
+    c->hc_ready[layer] = 1;
+    return 0;
+}
+
+int qmoe_hc_synth_layer(qmoe_ctx *c, int layer, uint64_t seed, qmoe_err *err) {
+    clear_err(err);
+    if (hc_check_layer(c, layer, err)) return -1;
+    if (hc_ensure_mem(c, layer, err)) return -1;
+    c->hc_ready[layer] = 0;
+    static const struct {
+        int t, tag, kind;
+        float sd;
+    } spec[] = {
+        {QH_HC_NORM, 0, 3, 1.0f},
+        {QH_HC_DOWN_Q, QMOE_TAG_HC_DOWN_Q, 2, 0.0f}, {QH_HC_DOWN_S, QMOE_TAG_HC_DOWN_S, 0, 0.02f},
+        {QH_HC_DOWN_B, QMOE_TAG_HC_DOWN_B, 0, 0.01f}, {QH_HC_UP_Q, QMOE_TAG_HC_UP_Q, 2, 0.0f},
+        {QH_HC_UP_S, QMOE_TAG_HC_UP_S, 0, 0.02f},     {QH_HC_UP_B, QMOE_TAG_HC_UP_B, 0, 0.01f},
+        {QH_HC_INJECT_W, QMOE_TAG_HC_INJECT_W, 0, 0.02f},
+    };
+    for (size_t i = 0; i < sizeof(spec) / sizeof(spec[0]); i++) {
+        size_t n, es;
+        hc_shape(c, spec[i].t, &n, &es);
+        const uint64_t key = qk_tensor_key(seed, (uint32_t)layer, (uint32_t)spec[i].tag);
+        if (hip_fail(err, qk_launch_synth((char *)c->hc_mem[layer] + c->hc_off[spec[i].t], n,
+                                          spec[i].kind, key, 0, spec[i].sd, NULL),
+                     "synth(hc)"))
+            return -1;
+    }
+    if (hip_fail(err, (int)hipDeviceSynchronize(), "synth sync")) return -1;
+    c->hc_ready[layer] = 1;
+    return 0;
+}
+
+int qmoe_hc_device_weights(qmoe_ctx *c, int layer, qmoe_hc_weights *out, qmoe_err *err) {
+    clear_err(err);
+    if (hc_check_layer(c, layer, err)) return -1;
+    if (!c->hc_ready[layer]) {
+        set_err(err, "layer %d has no hyper-connection weights", layer);
+        return -1;
+    }
+    NEED(out, "out");
+    hc_dev(c, layer, out);
+    return 0;
+}
+
+static int hc_check_call(qmoe_ctx *c, int layer, int n, qmoe_err *err) {
+    if (hc_check_layer(c, layer, err)) return -1;
+    if (!c->hc_ready[layer]) {
+        set_err(err, "layer %d has no hyper-connection weights", layer);
+        return -1;
+    }
+    if (n < 0 || n > c->cfg.max_tokens) {
+        set_err(err, "n = %d out of range [0, max_tokens = %d]", n, c->cfg.max_tokens);
+        return -1;
+    }
+    return 0;
+}
+
+/* gated_residual (model.c:728-796): three launches */
+static int run_hc_mix(qmoe_ctx *c, int layer, const float *hyper, int n, float *mixed,
+                      float *inject, void *stream, qmoe_err *err) {
+    qmoe_hc_weights W;
+    hc_dev(c, layer, &W);
+    const int d = c->cfg.hidden, D = c->hc * d;
+    int rc = qk_launch_hc_norm_inject(hyper, W.hc_norm, W.inject_w, c->hc, d, n, 1e-6f,
+                                      c->hc_normed, inject, stream);
+    if (hip_fail(err, rc, "hc norm+inject")) return -1;
+    rc = qk_launch_hc_linear(W.down_q, W.down_s, W.down_b, c->hc_normed, n, D, c->hc_R, c->hc_down,
+                             stream);
+    if (hip_fail(err, rc, "hc down")) return -1;
+    rc = qk_launch_hc_upmix(W.up_q, W.up_s, W.up_b, c->hc_down, c->hc_normed, c->hc, d, c->hc_R, n,
+                            mixed, stream);
+    return hip_fail(err, rc, "hc up+mix");
+}
+
+int qmoe_hc_mix(qmoe_ctx *c, int layer, const float *hyper, int n, float *mixed_out,
+                float *inject_out, float *normed_out, void *stream, qmoe_err *err) {
+    clear_err(err);
+    if (hc_check_call(c, layer, n, err)) return -1;
+    if (n == 0) return 0;
+    NEED(hyper, "hyper");
+    NEED(mixed_out, "mixed_out");
+    if (run_hc_mix(c, layer, hyper, n, mixed_out, inject_out ? inject_out : c->hc_inject, stream,
+                   err))
+        return -1;
+    if (normed_out &&
+        hip_fail(err, (int)hipMemcpyAsync(normed_out, c->hc_normed,
+                                          (size_t)n * c->hc * c->cfg.hidden * sizeof(float),
+                                          hipMemcpyDeviceToDevice, (hipStream_t)stream),
+                 "copy normed"))
+        return -1;
+    return 0;
+}
+
+int qmoe_hc_inject(qmoe_ctx *c, const float *inject, const float *moe_out, int n, float *hyper,
+                   void *stream, qmoe_err *err) {
+    clear_err(err);
+    if (!c) {
+        set_err(err, "ctx is NULL");
+        return -1;
+    }
+    if (!c->hc) {
+        set_err(err, "hyper connection not enabled (qmoe_hc_enable)");
+        return -1;
+    }
+    if (n < 0 || n > c->cfg.max_tokens) {
+        set_err(err, "n = %d out of range [0, max_tokens = %d]", n, c->cfg.max_tokens);
+        return -1;
+    }
+    if (n == 0) return 0;
+    NEED(inject, "inject");
+    NEED(moe_out, "moe_out");
+    NEED(hyper, "hyper");
+    return hip_fail(err, qk_launch_hc_inject(inject, moe_out, c->hc, c->cfg.hidden, n, hyper, stream),
+                    "hc inject");
+}
+
+int qmoe_hc_layer_forward(qmoe_ctx *c, int layer, float *hyper, int n, float *moe_out,
+                          void *stream, qmoe_err *err) {
+    clear_err(err);
+    if (hc_check_call(c, layer, n, err) || check_call(c, layer, n, err)) return -1;
+    if (n == 0) return 0;
+    NEED(hyper, "hyper");
+    if (run_hc_mix(c, layer, hyper, n, c->hc_mixed, c->hc_inject, stream, err)) return -1;
+    return layer_forward(c, layer, c->hc_mixed, 0, n, moe_out, 0, hyper, c->hc_inject, stream, err);
 }
 
 int qmoe_moe_forward_host(qmoe_ctx *c, int layer, const float *x, int n, float *out,

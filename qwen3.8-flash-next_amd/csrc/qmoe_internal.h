@@ -58,6 +58,12 @@ enum {
     QH_T_SH_DOWN_B, QH_T_SHGATE_W, QH_T_NORM_W, QH_T_COUNT
 };
 
+/* hyper-connection tensor slots inside a layer's hc allocation */
+enum {
+    QH_HC_NORM, QH_HC_DOWN_Q, QH_HC_DOWN_S, QH_HC_DOWN_B, QH_HC_UP_Q, QH_HC_UP_S, QH_HC_UP_B,
+    QH_HC_INJECT_W, QH_HC_COUNT
+};
+
 /* host-side access to a context's layer slots (qmoe_host.c), for the
  * checkpoint reader (qmoe_st.c).  A layer being written is not ready until
  * qh_layer_end. */
@@ -69,6 +75,11 @@ int qh_layer_slot(qmoe_ctx *c, int layer, int t, void **dst, size_t *bytes, qmoe
 int qh_fill_zero(void *dst, size_t bytes, qmoe_err *err);
 int qh_copy_to_device(void *dst, const void *src, size_t bytes, qmoe_err *err);
 void qh_layer_end(qmoe_ctx *c, int layer, int has_bias, int has_norm);
+/* the same for the hyper-connection slots (after qmoe_hc_enable) */
+int qh_hc_config(qmoe_ctx *c, int layer, int *hc, int *lowrank, int *d, qmoe_err *err);
+int qh_hc_slot(qmoe_ctx *c, int layer, int t, void **dst, size_t *bytes, qmoe_err *err);
+void qh_hc_begin(qmoe_ctx *c, int layer);
+void qh_hc_end(qmoe_ctx *c, int layer);
 
 /* All launchers return a hipError_t value (0 = hipSuccess). */
 
@@ -148,12 +159,33 @@ int qk_launch_gateup_topk(const qmoe_layer_weights *W, qk_shape s, const void *x
 #define QK_DC_MAX_N 8
 #define QK_DC_MAX_LDS 65536
 size_t qk_down_combine_lds(qk_shape s, int n);
+/* out may be NULL when hyper is set; with hyper [n, hc, H] every copy j
+ * of token t becomes fma(inject[t, j], out[t], hyper[t, j]) */
 int qk_launch_down_combine(const qmoe_layer_weights *W, qk_shape s, const float *h, int n,
                            const int32_t *segtab, const int32_t *pos, const float *w,
                            const float *sg, const void *x_res, int x_bf16, float *out,
-                           void *stream);
+                           float *hyper, const float *inject, int hc, void *stream);
 int qk_launch_combine(qk_shape s, int n, const float *y, const int32_t *pos, const float *w,
-                      const float *sg, const void *x_res, int x_bf16, float *out, void *stream);
+                      const float *sg, const void *x_res, int x_bf16, float *out, float *hyper,
+                      const float *inject, int hc, void *stream);
+
+/* the MLP hyper connection (hyper.hip): shapes it takes (hc <= 8, d and R
+ * multiples of 64, R <= 2048, hc*d <= 8192) */
+int qk_hc_shape_ok(int hc, int d, int R);
+/* normed [n, hc*d] and inject [n, hc] from the hyper state [n, hc*d] */
+int qk_launch_hc_norm_inject(const float *hyper, const float *norm_w, const uint16_t *inject_w,
+                             int hc, int d, int n, float eps, float *normed, float *inject,
+                             void *stream);
+/* out [n, N] = x [n, K] . W^T, W q4 [N, K/8] with bf16 scales/biases per 64 */
+int qk_launch_hc_linear(const uint32_t *q, const uint16_t *s, const uint16_t *b, const float *x,
+                        int n, int K, int N, float *out, void *stream);
+/* mixed [n, d] = mean_h sigmoid(silu(down/hc) . Wup^T)[h*d + i] * normed[h*d + i] */
+int qk_launch_hc_upmix(const uint32_t *q, const uint16_t *s, const uint16_t *b, const float *down,
+                       const float *normed, int hc, int d, int R, int n, float *mixed,
+                       void *stream);
+/* hyper [n, hc, d]: every copy j of token t becomes fma(inject[t, j], out[t], hyper[t, j]) */
+int qk_launch_hc_inject(const float *inject, const float *out, int hc, int d, int n, float *hyper,
+                        void *stream);
 
 /* synthetic streams: kind 0 bf16 normal, 1 f32 normal, 2 u32 codes, 3 f32 constant (stddev) */
 int qk_launch_synth(void *dst, size_t count, int kind, uint64_t key, uint64_t start, float stddev,

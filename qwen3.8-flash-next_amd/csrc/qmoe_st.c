@@ -752,14 +752,16 @@ int qmoe_st_read(const qmoe_st *ix, const char *name, void *dst, size_t cap, qmo
 
 /* ------------------------------------------------------------ layer upload */
 
-/* one MoE tensor of a layer: checkpoint name suffix, slot, expected dtype and shape */
+/* one tensor of a layer: checkpoint name suffix, slot, expected dtype and shape */
 typedef struct {
-    const char *suffix; /* after "model.layers.<L>.mlp." */
-    int slot;           /* QH_T_* */
+    const char *suffix; /* after the layer prefix */
+    int slot;           /* QH_T_* or QH_HC_* */
     int dtype;
     int ndim;
     int64_t shape[3];
     int optional_zero;  /* biases: absent means zero (model.c:250-256) */
+    int dense;          /* must not have .scales (used unquantized by the reference) */
+    int widen;          /* BF16 in the file, f32 in the slot (mw_load_f32, model.c:275-294) */
 } st_want;
 
 static int check_tensor(const st_entry *e, const st_want *w, qmoe_err *err) {
@@ -782,6 +784,104 @@ static int check_tensor(const st_entry *e, const st_want *w, qmoe_err *err) {
     return 0;
 }
 
+/* where a table's tensors go: the MoE layer slots or the hyper-connection slots */
+typedef struct {
+    int (*slot)(qmoe_ctx *c, int layer, int t, void **dst, size_t *bytes, qmoe_err *err);
+    void (*begin)(qmoe_ctx *c, int layer);
+    void (*end)(qmoe_ctx *c, int layer);
+    const char *dense_what; /* message for q4 weights found without scales */
+    const char *quant_what; /* message for a dense tensor found quantized */
+} st_target;
+
+/* Locates and checks every tensor of `want` under `prefix` before anything
+ * is copied, then copies through a pinned staging buffer, a chunk at a time. */
+static int upload_table(qmoe_ctx *ctx, int layer, const qmoe_st *ix, const char *prefix,
+                        const st_want *want, int nw, const st_target *tg, qmoe_err *err) {
+    const st_entry *found[32];
+    if (nw > 32) {
+        st_err(err, "tensor table too long");
+        return -1;
+    }
+    for (int i = 0; i < nw; i++) {
+        char nm[256];
+        snprintf(nm, sizeof(nm), "%s%s", prefix, want[i].suffix);
+        found[i] = find_entry(ix, nm);
+        if (!found[i]) {
+            if (want[i].optional_zero) continue;
+            /* name the departures from the reference's loader precisely */
+            const size_t sl = strlen(nm);
+            if (sl > 7 && !strcmp(nm + sl - 7, ".scales")) {
+                char wn[256];
+                snprintf(wn, sizeof(wn), "%.*s.weight", (int)(sl - 7), nm);
+                if (find_entry(ix, wn)) {
+                    st_err(err, "%s has no scales: %s", wn, tg->dense_what);
+                    return -1;
+                }
+            }
+            st_err(err, "missing tensor %s", nm);
+            return -1;
+        }
+        if (want[i].dense) {
+            char sn[256];
+            snprintf(sn, sizeof(sn), "%s%.*s.scales", prefix, (int)(strlen(want[i].suffix) - 7),
+                     want[i].suffix);
+            if (find_entry(ix, sn)) {
+                st_err(err, "%s is quantized: %s", found[i]->name, tg->quant_what);
+                return -1;
+            }
+        }
+        if (check_tensor(found[i], &want[i], err)) return -1;
+    }
+
+    const size_t chunk = (size_t)64 << 20;
+    void *stage = NULL;
+    if (qh_host_alloc(&stage, chunk, err)) return -1;
+    int rc = 0;
+    tg->begin(ctx, layer);
+    for (int i = 0; i < nw && rc == 0; i++) {
+        void *dst;
+        size_t bytes;
+        if (tg->slot(ctx, layer, want[i].slot, &dst, &bytes, err)) {
+            rc = -1;
+            break;
+        }
+        if (!found[i]) {
+            rc = qh_fill_zero(dst, bytes, err);
+            continue;
+        }
+        const size_t fbytes = want[i].widen ? bytes / 2 : bytes;
+        if (found[i]->t.nbytes != fbytes) {
+            st_err(err, "%s holds %llu bytes, the slot %zu", found[i]->name,
+                   (unsigned long long)found[i]->t.nbytes, fbytes);
+            rc = -1;
+            break;
+        }
+        /* widened tensors: half a chunk of bf16 becomes a chunk of f32 */
+        const size_t step = want[i].widen ? chunk / 2 : chunk;
+        for (size_t at = 0; at < fbytes && rc == 0; at += step) {
+            const size_t len = fbytes - at < step ? fbytes - at : step;
+            if (want[i].widen) {
+                uint16_t *src = (uint16_t *)((char *)stage + chunk / 2);
+                rc = read_range(ix, found[i], at, src, len, err);
+                float *f = (float *)stage;
+                for (size_t e = 0; rc == 0 && e < len / 2; e++) {
+                    const uint32_t u = (uint32_t)src[e] << 16;
+                    memcpy(&f[e], &u, 4);
+                }
+                if (rc == 0) rc = qh_copy_to_device((char *)dst + 2 * at, stage, 2 * len, err);
+            } else {
+                rc = read_range(ix, found[i], at, stage, len, err);
+                if (rc == 0) rc = qh_copy_to_device((char *)dst + at, stage, len, err);
+            }
+        }
+    }
+    qh_host_free(stage);
+    if (rc == 0) tg->end(ctx, layer);
+    return rc;
+}
+
+static void moe_end(qmoe_ctx *c, int layer) { qh_layer_end(c, layer, 0, 0); }
+
 int qmoe_upload_layer_st(qmoe_ctx *ctx, int layer, const qmoe_st *ix, int model_layer, qmoe_err *err) {
     if (err) err->msg[0] = 0;
     if (!ix) {
@@ -796,94 +896,66 @@ int qmoe_upload_layer_st(qmoe_ctx *ctx, int layer, const qmoe_st *ix, int model_
     }
     const int64_t H = cfg.hidden, E = cfg.n_experts, I = cfg.moe_inter, g = cfg.group_size;
     const st_want want[] = {
-        {"gate.weight", QH_T_ROUTER_W, QMOE_ST_BF16, 2, {E, H}, 0},
-        {"switch_mlp.gate_proj.weight", QH_T_GATE_Q, QMOE_ST_U32, 3, {E, I, H / 8}, 0},
-        {"switch_mlp.gate_proj.scales", QH_T_GATE_S, QMOE_ST_BF16, 3, {E, I, H / g}, 0},
-        {"switch_mlp.gate_proj.biases", QH_T_GATE_B, QMOE_ST_BF16, 3, {E, I, H / g}, 1},
-        {"switch_mlp.up_proj.weight", QH_T_UP_Q, QMOE_ST_U32, 3, {E, I, H / 8}, 0},
-        {"switch_mlp.up_proj.scales", QH_T_UP_S, QMOE_ST_BF16, 3, {E, I, H / g}, 0},
-        {"switch_mlp.up_proj.biases", QH_T_UP_B, QMOE_ST_BF16, 3, {E, I, H / g}, 1},
-        {"switch_mlp.down_proj.weight", QH_T_DOWN_Q, QMOE_ST_U32, 3, {E, H, I / 8}, 0},
-        {"switch_mlp.down_proj.scales", QH_T_DOWN_S, QMOE_ST_BF16, 3, {E, H, I / g}, 0},
-        {"switch_mlp.down_proj.biases", QH_T_DOWN_B, QMOE_ST_BF16, 3, {E, H, I / g}, 1},
-        {"shared_expert.gate_proj.weight", QH_T_SH_GATE_Q, QMOE_ST_U32, 2, {I, H / 8}, 0},
-        {"shared_expert.gate_proj.scales", QH_T_SH_GATE_S, QMOE_ST_BF16, 2, {I, H / g}, 0},
-        {"shared_expert.gate_proj.biases", QH_T_SH_GATE_B, QMOE_ST_BF16, 2, {I, H / g}, 1},
-        {"shared_expert.up_proj.weight", QH_T_SH_UP_Q, QMOE_ST_U32, 2, {I, H / 8}, 0},
-        {"shared_expert.up_proj.scales", QH_T_SH_UP_S, QMOE_ST_BF16, 2, {I, H / g}, 0},
-        {"shared_expert.up_proj.biases", QH_T_SH_UP_B, QMOE_ST_BF16, 2, {I, H / g}, 1},
-        {"shared_expert.down_proj.weight", QH_T_SH_DOWN_Q, QMOE_ST_U32, 2, {H, I / 8}, 0},
-        {"shared_expert.down_proj.scales", QH_T_SH_DOWN_S, QMOE_ST_BF16, 2, {H, I / g}, 0},
-        {"shared_expert.down_proj.biases", QH_T_SH_DOWN_B, QMOE_ST_BF16, 2, {H, I / g}, 1},
-        {"shared_expert_gate.weight", QH_T_SHGATE_W, QMOE_ST_BF16, 2, {1, H}, 0},
+        {"gate.weight", QH_T_ROUTER_W, QMOE_ST_BF16, 2, {E, H}, 0, 1, 0},
+        {"switch_mlp.gate_proj.weight", QH_T_GATE_Q, QMOE_ST_U32, 3, {E, I, H / 8}, 0, 0, 0},
+        {"switch_mlp.gate_proj.scales", QH_T_GATE_S, QMOE_ST_BF16, 3, {E, I, H / g}, 0, 0, 0},
+        {"switch_mlp.gate_proj.biases", QH_T_GATE_B, QMOE_ST_BF16, 3, {E, I, H / g}, 1, 0, 0},
+        {"switch_mlp.up_proj.weight", QH_T_UP_Q, QMOE_ST_U32, 3, {E, I, H / 8}, 0, 0, 0},
+        {"switch_mlp.up_proj.scales", QH_T_UP_S, QMOE_ST_BF16, 3, {E, I, H / g}, 0, 0, 0},
+        {"switch_mlp.up_proj.biases", QH_T_UP_B, QMOE_ST_BF16, 3, {E, I, H / g}, 1, 0, 0},
+        {"switch_mlp.down_proj.weight", QH_T_DOWN_Q, QMOE_ST_U32, 3, {E, H, I / 8}, 0, 0, 0},
+        {"switch_mlp.down_proj.scales", QH_T_DOWN_S, QMOE_ST_BF16, 3, {E, H, I / g}, 0, 0, 0},
+        {"switch_mlp.down_proj.biases", QH_T_DOWN_B, QMOE_ST_BF16, 3, {E, H, I / g}, 1, 0, 0},
+        {"shared_expert.gate_proj.weight", QH_T_SH_GATE_Q, QMOE_ST_U32, 2, {I, H / 8}, 0, 0, 0},
+        {"shared_expert.gate_proj.scales", QH_T_SH_GATE_S, QMOE_ST_BF16, 2, {I, H / g}, 0, 0, 0},
+        {"shared_expert.gate_proj.biases", QH_T_SH_GATE_B, QMOE_ST_BF16, 2, {I, H / g}, 1, 0, 0},
+        {"shared_expert.up_proj.weight", QH_T_SH_UP_Q, QMOE_ST_U32, 2, {I, H / 8}, 0, 0, 0},
+        {"shared_expert.up_proj.scales", QH_T_SH_UP_S, QMOE_ST_BF16, 2, {I, H / g}, 0, 0, 0},
+        {"shared_expert.up_proj.biases", QH_T_SH_UP_B, QMOE_ST_BF16, 2, {I, H / g}, 1, 0, 0},
+        {"shared_expert.down_proj.weight", QH_T_SH_DOWN_Q, QMOE_ST_U32, 2, {H, I / 8}, 0, 0, 0},
+        {"shared_expert.down_proj.scales", QH_T_SH_DOWN_S, QMOE_ST_BF16, 2, {H, I / g}, 0, 0, 0},
+        {"shared_expert.down_proj.biases", QH_T_SH_DOWN_B, QMOE_ST_BF16, 2, {H, I / g}, 1, 0, 0},
+        {"shared_expert_gate.weight", QH_T_SHGATE_W, QMOE_ST_BF16, 2, {1, H}, 0, 1, 0},
     };
-    const int nw = (int)(sizeof(want) / sizeof(want[0]));
-    const st_entry *found[sizeof(want) / sizeof(want[0])];
+    const st_target tg = {qh_layer_slot, qh_layer_begin, moe_end,
+                          "dense expert weights are not supported (this build runs q4 experts only)",
+                          "the router and the shared-expert gate must be dense BF16 "
+                          "(model.c:1301, 1396)"};
+    char prefix[64];
+    snprintf(prefix, sizeof(prefix), "model.layers.%d.mlp.", model_layer);
+    return upload_table(ctx, layer, ix, prefix, want, (int)(sizeof(want) / sizeof(want[0])), &tg,
+                        err);
+}
 
-    /* every tensor is located and checked before anything is copied */
-    for (int i = 0; i < nw; i++) {
-        char nm[256];
-        snprintf(nm, sizeof(nm), "model.layers.%d.mlp.%s", model_layer, want[i].suffix);
-        found[i] = find_entry(ix, nm);
-        if (!found[i]) {
-            if (want[i].optional_zero) continue;
-            /* name the departures from the reference's loader precisely */
-            const size_t sl = strlen(nm);
-            if (sl > 7 && !strcmp(nm + sl - 7, ".scales")) {
-                char wn[256];
-                snprintf(wn, sizeof(wn), "%.*s.weight", (int)(sl - 7), nm);
-                if (find_entry(ix, wn)) {
-                    st_err(err, "%s has no scales: dense expert weights are not supported "
-                                "(this build runs q4 experts only)", wn);
-                    return -1;
-                }
-            }
-            st_err(err, "missing tensor %s", nm);
-            return -1;
-        }
-        if (want[i].slot == QH_T_ROUTER_W || want[i].slot == QH_T_SHGATE_W) {
-            char sn[256];
-            snprintf(sn, sizeof(sn), "model.layers.%d.mlp.%.*s.scales", model_layer,
-                     (int)(strlen(want[i].suffix) - 7), want[i].suffix);
-            if (find_entry(ix, sn)) {
-                st_err(err, "%s is quantized: the router and the shared-expert gate must be dense "
-                            "BF16 (model.c:1301, 1396)", found[i]->name);
-                return -1;
-            }
-        }
-        if (check_tensor(found[i], &want[i], err)) return -1;
+int qmoe_hc_upload_layer_st(qmoe_ctx *ctx, int layer, const qmoe_st *ix, int model_layer,
+                            qmoe_err *err) {
+    if (err) err->msg[0] = 0;
+    if (!ix) {
+        st_err(err, "index is NULL");
+        return -1;
     }
-
-    /* copy through a pinned staging buffer, a chunk at a time */
-    const size_t chunk = (size_t)64 << 20;
-    void *stage = NULL;
-    if (qh_host_alloc(&stage, chunk, err)) return -1;
-    int rc = 0;
-    qh_layer_begin(ctx, layer);
-    for (int i = 0; i < nw && rc == 0; i++) {
-        void *dst;
-        size_t bytes;
-        if (qh_layer_slot(ctx, layer, want[i].slot, &dst, &bytes, err)) {
-            rc = -1;
-            break;
-        }
-        if (!found[i]) {
-            rc = qh_fill_zero(dst, bytes, err);
-            continue;
-        }
-        if (found[i]->t.nbytes != bytes) {
-            st_err(err, "%s holds %llu bytes, the slot %zu", found[i]->name,
-                   (unsigned long long)found[i]->t.nbytes, bytes);
-            rc = -1;
-            break;
-        }
-        for (size_t at = 0; at < bytes && rc == 0; at += chunk) {
-            const size_t len = bytes - at < chunk ? bytes - at : chunk;
-            rc = read_range(ix, found[i], at, stage, len, err);
-            if (rc == 0) rc = qh_copy_to_device((char *)dst + at, stage, len, err);
-        }
+    int hc, R, d;
+    if (qh_hc_config(ctx, layer, &hc, &R, &d, err)) return -1;
+    if (model_layer < 0) {
+        st_err(err, "model layer %d is negative", model_layer);
+        return -1;
     }
-    qh_host_free(stage);
-    if (rc == 0) qh_layer_end(ctx, layer, 0, 0);
-    return rc;
+    const int64_t D = (int64_t)hc * d, g = QK_GROUP;
+    const st_want want[] = {
+        {"hc_norm.weight", QH_HC_NORM, QMOE_ST_BF16, 1, {D}, 0, 1, 1},
+        {"input_mix_weight_down.weight", QH_HC_DOWN_Q, QMOE_ST_U32, 2, {R, D / 8}, 0, 0, 0},
+        {"input_mix_weight_down.scales", QH_HC_DOWN_S, QMOE_ST_BF16, 2, {R, D / g}, 0, 0, 0},
+        {"input_mix_weight_down.biases", QH_HC_DOWN_B, QMOE_ST_BF16, 2, {R, D / g}, 1, 0, 0},
+        {"input_mix_weight_up.weight", QH_HC_UP_Q, QMOE_ST_U32, 2, {D, R / 8}, 0, 0, 0},
+        {"input_mix_weight_up.scales", QH_HC_UP_S, QMOE_ST_BF16, 2, {D, R / g}, 0, 0, 0},
+        {"input_mix_weight_up.biases", QH_HC_UP_B, QMOE_ST_BF16, 2, {D, R / g}, 1, 0, 0},
+        {"block_inject_weight.weight", QH_HC_INJECT_W, QMOE_ST_BF16, 2, {hc, D}, 0, 1, 0},
+    };
+    const st_target tg = {qh_hc_slot, qh_hc_begin, qh_hc_end,
+                          "dense mix weights are not supported (this build runs q4 mix weights)",
+                          "block_inject_weight must be dense BF16 (model.c:789)"};
+    char prefix[96];
+    snprintf(prefix, sizeof(prefix), "model.layers.%d.mlp_hyper_connection.", model_layer);
+    return upload_table(ctx, layer, ix, prefix, want, (int)(sizeof(want) / sizeof(want[0])), &tg,
+                        err);
 }

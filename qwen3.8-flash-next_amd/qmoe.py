@@ -51,6 +51,13 @@ class QmoeLayerWeights(ctypes.Structure):
     _fields_ = [(f, ctypes.c_void_p) for f in WEIGHT_FIELDS]
 
 
+HC_FIELDS = ["hc_norm", "down_q", "down_s", "down_b", "up_q", "up_s", "up_b", "inject_w"]
+
+
+class QmoeHcWeights(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_void_p) for f in HC_FIELDS]
+
+
 class QmoeError(RuntimeError):
     pass
 
@@ -99,6 +106,14 @@ SIGNATURES = {
     "qmoe_st_dtype_size": (_I, [_I]),
     "qmoe_st_dtype_name": (ctypes.c_char_p, [_I]),
     "qmoe_upload_layer_st": (_I, [_P, _I, _P, _I, ctypes.POINTER(QmoeErr)]),
+    "qmoe_hc_enable": (_I, [_P, _I, _I, ctypes.POINTER(QmoeErr)]),
+    "qmoe_hc_upload_layer": (_I, [_P, _I, ctypes.POINTER(QmoeHcWeights), ctypes.POINTER(QmoeErr)]),
+    "qmoe_hc_upload_layer_st": (_I, [_P, _I, _P, _I, ctypes.POINTER(QmoeErr)]),
+    "qmoe_hc_synth_layer": (_I, [_P, _I, ctypes.c_uint64, ctypes.POINTER(QmoeErr)]),
+    "qmoe_hc_device_weights": (_I, [_P, _I, ctypes.POINTER(QmoeHcWeights), ctypes.POINTER(QmoeErr)]),
+    "qmoe_hc_mix": (_I, [_P, _I, _P, _I, _P, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_hc_inject": (_I, [_P, _P, _P, _I, _P, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_hc_layer_forward": (_I, [_P, _I, _P, _I, _P, _P, ctypes.POINTER(QmoeErr)]),
 }
 
 
@@ -417,6 +432,86 @@ class MoeContext:
                                        _ptr(r["segments"]), _stream(stream), ctypes.byref(err)),
                err, "qmoe_last_routing")
         return r
+
+    # -- MLP hyper connection around the layer
+    def hc_enable(self, hc_count: int, hc_lowrank: int):
+        err = QmoeErr()
+        _check(lib().qmoe_hc_enable(self._h, hc_count, hc_lowrank, ctypes.byref(err)), err,
+               "qmoe_hc_enable")
+        self.hc, self.hc_R = hc_count, hc_lowrank
+
+    def hc_upload_layer(self, layer: int, host: dict):
+        """host: numpy arrays keyed by HC_FIELDS (hc_norm f32, codes u32, bf16 bits u16)"""
+        import numpy as np
+        w = QmoeHcWeights()
+        keep = []
+        for f in HC_FIELDS:
+            a = host.get(f)
+            if a is not None:
+                a = np.ascontiguousarray(a)
+                keep.append(a)
+            setattr(w, f, None if a is None else a.ctypes.data)
+        err = QmoeErr()
+        _check(lib().qmoe_hc_upload_layer(self._h, layer, ctypes.byref(w), ctypes.byref(err)), err,
+               "qmoe_hc_upload_layer")
+
+    def hc_upload_layer_st(self, layer: int, index: "Checkpoint", model_layer: int):
+        err = QmoeErr()
+        _check(lib().qmoe_hc_upload_layer_st(self._h, layer, index.handle, model_layer,
+                                             ctypes.byref(err)), err, "qmoe_hc_upload_layer_st")
+
+    def hc_synth_layer(self, layer: int, seed: int):
+        err = QmoeErr()
+        _check(lib().qmoe_hc_synth_layer(self._h, layer, seed, ctypes.byref(err)), err,
+               "qmoe_hc_synth_layer")
+
+    def hc_device_weights(self, layer: int) -> dict:
+        w = QmoeHcWeights()
+        err = QmoeErr()
+        _check(lib().qmoe_hc_device_weights(self._h, layer, ctypes.byref(w), ctypes.byref(err)),
+               err, "qmoe_hc_device_weights")
+        return {f: getattr(w, f) for f in HC_FIELDS}
+
+    def hc_mix(self, layer, hyper, stream=None):
+        """gated_residual: hyper [n, hc*H] f32 -> dict(mixed, inject, normed)"""
+        import torch
+        n = hyper.shape[0]
+        dev = hyper.device
+        r = dict(mixed=torch.empty((n, self.H), dtype=torch.float32, device=dev),
+                 inject=torch.empty((n, self.hc), dtype=torch.float32, device=dev),
+                 normed=torch.empty((n, self.hc * self.H), dtype=torch.float32, device=dev))
+        err = QmoeErr()
+        _check(lib().qmoe_hc_mix(self._h, layer, _ptr(hyper), n, _ptr(r["mixed"]), _ptr(r["inject"]),
+                                 _ptr(r["normed"]), _stream(stream), ctypes.byref(err)), err,
+               "qmoe_hc_mix")
+        return r
+
+    def hc_inject(self, inject, moe_out, hyper, stream=None):
+        """hyper[t, j] += inject[t, j] * moe_out[t], in place"""
+        err = QmoeErr()
+        _check(lib().qmoe_hc_inject(self._h, _ptr(inject), _ptr(moe_out), hyper.shape[0],
+                                    _ptr(hyper), _stream(stream), ctypes.byref(err)), err,
+               "qmoe_hc_inject")
+        return hyper
+
+    def hc_layer_forward(self, layer, hyper, want_out=True, stream=None):
+        """mix, the MoE layer and the inject update; hyper is updated in place.
+        Returns the MoE output [n, H] (or None)."""
+        import torch
+        n = hyper.shape[0]
+        out = torch.empty((n, self.H), dtype=torch.float32, device=hyper.device) if want_out else None
+        err = QmoeErr()
+        _check(lib().qmoe_hc_layer_forward(self._h, layer, _ptr(hyper), n, _ptr(out),
+                                           _stream(stream), ctypes.byref(err)), err,
+               "qmoe_hc_layer_forward")
+        return out
+
+    def hc_layer_forward_raw(self, layer, hyper_ptr, n, out_ptr, stream_handle):
+        """no-allocation variant for timing loops; returns the rc and message"""
+        err = QmoeErr()
+        rc = lib().qmoe_hc_layer_forward(self._h, layer, hyper_ptr, n, out_ptr, stream_handle,
+                                         ctypes.byref(err))
+        return rc, err.msg.decode(errors="replace")
 
     def forward_host(self, layer, x):
         """moe_forward's host contract: numpy f32 [n,H] in, numpy f32 [n,H] out"""

@@ -32,8 +32,41 @@ MOE_TENSORS = {
 }
 
 
+# hyper connection: array key -> (suffix after "model.layers.<L>.mlp_hyper_connection.",
+# shape from (hc, D=hc*H, R, g)); hc_norm is stored BF16 (mw_load_f32, model.c:275-294)
+HC_TENSORS = {
+    "hc_norm": ("hc_norm.weight", lambda hc, D, R, g: (D,)),
+    "down_q": ("input_mix_weight_down.weight", lambda hc, D, R, g: (R, D // 8)),
+    "down_s": ("input_mix_weight_down.scales", lambda hc, D, R, g: (R, D // g)),
+    "down_b": ("input_mix_weight_down.biases", lambda hc, D, R, g: (R, D // g)),
+    "up_q": ("input_mix_weight_up.weight", lambda hc, D, R, g: (D, R // 8)),
+    "up_s": ("input_mix_weight_up.scales", lambda hc, D, R, g: (D, R // g)),
+    "up_b": ("input_mix_weight_up.biases", lambda hc, D, R, g: (D, R // g)),
+    "inject_w": ("block_inject_weight.weight", lambda hc, D, R, g: (hc, D)),
+}
+
+
 def moe_name(layer, key):
     return f"model.layers.{layer}.mlp.{MOE_TENSORS[key][0]}"
+
+
+def hc_name(layer, key):
+    return f"model.layers.{layer}.mlp_hyper_connection.{HC_TENSORS[key][0]}"
+
+
+def hc_tensors(arrays, hc, H, R, layer, g=64, drop=()):
+    """name -> torch tensor for one layer's hyper connection (hc_norm f32 -> bf16
+    bits, exact when the values are bf16-representable)"""
+    D = hc * H
+    out = {}
+    for key, (suffix, shp) in HC_TENSORS.items():
+        if key in drop:
+            continue
+        a = arrays[key]
+        if key == "hc_norm":
+            a = (np.ascontiguousarray(a, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+        out[hc_name(layer, key)] = _torch_tensor(a, shp(hc, D, R, g))
+    return out
 
 
 def _torch_tensor(a, shape):
