@@ -147,6 +147,36 @@ def bench_layer(pkg, torch, w, n_layers, steps, warmup):
     return sec / (reps * S), reps * S, reps_w * S, st
 
 
+HC_COUNT, HC_LOWRANK = 4, 320  # the model's hyper connection (text_config hc_count, hc_lowrank)
+
+
+def bench_hyper(pkg, torch, w, n_layers, steps, warmup):
+    """whole hyper-connection layers: gated_residual, the MoE layer on the
+    mixed rows and the inject update fused into the combine, on a resident
+    hyper state [n, hc*hidden] updated in place; returns seconds per step"""
+    ctx = pkg.MoeContext.for_workload(w, n_layers=n_layers, max_tokens=w.n_tokens)
+    ctx.hc_enable(HC_COUNT, HC_LOWRANK)
+    for layer in range(n_layers):
+        rb = None
+        if w.zipf_s > 0:
+            rb = zipf_bias_host(w.n_experts, w.zipf_s, w.zipf_scale, w.seed * 1000003 + layer)
+        ctx.synth_layer(layer, w.seed, router_bias=rb)
+        ctx.hc_synth_layer(layer, w.seed)
+    hyper = torch.empty((w.n_tokens, HC_COUNT * w.hidden), dtype=torch.float32, device="cuda")
+    pkg.synth_fill(hyper, 1, 77, 0, pkg.TAGS["HYPER"], stddev=1.0)
+    torch.cuda.synchronize()
+
+    def run():
+        for i in range(n_layers):
+            ctx.hc_layer_forward(i, hyper, want_out=False)
+    g = capture(torch, run)
+    time_graph(torch, g, max(1, math.ceil(warmup / n_layers)))
+    reps = max(1, math.ceil(steps / n_layers))
+    sec = time_graph(torch, g, reps)
+    ctx.close()
+    return sec / (reps * n_layers), reps * n_layers
+
+
 def bench_gateup(pkg, torch, st, reps_target=200):
     """dominant kernel of the one-token layer step: the launch that selects
     the top-k from the router logits and runs the grouped gate/up GEMV
@@ -253,6 +283,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--extra", default="batched,prefill",
                     help="comma list of other workloads to time (secondary results)")
+    ap.add_argument("--hyper", default="decode,batched,prefill",
+                    help="comma list of workloads also timed as hyper-connection layers "
+                         f"(hc {HC_COUNT}, rank {HC_LOWRANK}; secondary results)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 8 plain copies of MIB MiB (counter calibration) and exit")
     args = ap.parse_args()
@@ -304,6 +337,17 @@ def main():
                            tokens_per_step=we.n_tokens, layers_rotated=nl, steps=k_e)
         log(f"{name}: {s_e * 1e3:.3f} ms/step -> {we.n_tokens / s_e:.0f} tokens/s")
     st.ctx.close()
+    del st
+    torch.cuda.empty_cache()
+    for name in [e for e in args.hyper.split(",") if e]:
+        we = pkg.WORKLOADS[name]
+        nl = 16 if we.n_tokens == 1 else (8 if we.n_tokens <= 64 else 2)
+        s_h, k_h = bench_hyper(pkg, torch, we, nl, max(48, nl * 4), nl)
+        extra[name + "+hyper"] = dict(tokens_per_s=we.n_tokens / s_h, ms_per_step=s_h * 1e3,
+                                      tokens_per_step=we.n_tokens, layers_rotated=nl, steps=k_h,
+                                      hc_count=HC_COUNT, hc_lowrank=HC_LOWRANK)
+        log(f"{name}+hyper: {s_h * 1e3:.3f} ms/step -> {we.n_tokens / s_h:.0f} tokens/s")
+        torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu:

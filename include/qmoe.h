@@ -305,7 +305,7 @@ typedef struct {
 
 /* Gives the context hyper-connection slots for every layer and the mix
  * scratch (sized by max_tokens): hc_count (<= 8) copies, low rank
- * hc_lowrank (a multiple of 64, <= 2048), hc_count*hidden <= 8192.  The
+ * hc_lowrank (a multiple of 64, <= 2048), hidden <= 2048.  The
  * text_config's hc_count / hc_lowrank (model.c:86-87).  Calling it again
  * with the same values is a no-op. */
 int qmoe_hc_enable(qmoe_ctx *ctx, int hc_count, int hc_lowrank, qmoe_err *err);

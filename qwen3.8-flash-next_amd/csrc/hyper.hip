@@ -8,11 +8,11 @@
  *     gate   = sigmoid(input_mix_weight_up(w))                    [n, hc*d]
  *     mixed  = mean over the copies of gate * normed              [n, d]
  *     inject = 2 * sigmoid(block_inject_weight(normed) / hc)      [n, hc]
- * in three launches:
- *   k_hc_norm_inject  one token per workgroup: the copy norms, normed, and
- *                     the hc inject dots (bf16 weights, 64 KiB per token);
- *   k_hc_linear       q4 GEMV normed -> down outputs (before silu);
- *   k_hc_upmix        q4 GEMV silu(down/hc) -> gates, with the mean over the
+ * in two launches:
+ *   k_hc_down         the copy norms, normed, the q4 GEMV normed -> w with
+ *                     silu(./hc) and the hc inject dots (bf16 weights), each
+ *                     wave on one copy so the norms need no second pass;
+ *   k_hc_upmix        q4 GEMV w -> gates, with the mean over the
  *                     copies in its epilogue: a workgroup holds the rows
  *                     h*d + i of every copy h for its block of columns i,
  *                     so the [n, hc*d] gates never reach memory.
@@ -28,158 +28,177 @@
 
 #define HC_MAX 8
 
-__device__ __forceinline__ float hc_wave_sum(float v) { return qk_group_sum<64>(v); }
+/* --------------------------------------------- norm + down + inject */
 
-struct HcNormArgs {
+struct HcDownArgs {
     const float *hyper;        /* [n, hc*d] */
-    const float *norm_w;       /* [hc*d] */
-    const uint16_t *inject_w;  /* [hc, hc*d] bf16 */
-    float *normed;             /* [n, hc*d] */
+    const float *norm_w;       /* [hc*d] hc_norm */
+    const uint32_t *q;         /* input_mix_weight_down [R, hc*d/8] */
+    const uint16_t *s, *b;     /* [R, hc*d/64] */
+    const uint16_t *inject_w;  /* block_inject_weight [hc, hc*d] bf16 */
+    float *normed;             /* [n, hc*d], written by the first row block */
+    float *w;                  /* [n, R]: silu(down(normed) / hc) */
     float *inject;             /* [n, hc] */
-    int hc, d;
+    int hc, d, R, n, tb;
     float eps;
 };
 
+#define HD_RW 2 /* weight rows per workgroup */
+
 /*
- * grid = n, 1024 threads, 4 columns per thread per step.  Copy h's norm is
- * kernel_rmsnorm_grouped's (kernel.c:22-36): r = 1/sqrt(ss/d + eps),
- * normed = (x * r) * w; the inject dots sum in a fixed order (per thread,
- * then the wave butterfly, then the 16 waves in order).
+ * Workgroup = hc waves; wave h owns copy h (columns h*d .. h*d+d) of the
+ * hyper state, P chunks of 32 columns per lane, so the copy's RMSNorm is a
+ * wave sum and needs no other wave: normed = (x * r) * w with
+ * r = 1/sqrt(ss/d + eps) (kernel_rmsnorm_grouped, kernel.c:22-36).  A task
+ * is (block of tb tokens, block of HD_RW rows) of either the down matrix
+ * (q4) or the inject matrix (bf16); per token each wave leaves its copy's
+ * partial row sums in LDS (double-buffered by token parity) and the first
+ * threads add the copies in order and apply the activation: silu(v / hc)
+ * for down rows (kernel_scale + kernel_silu, model.c:757-758), 2 *
+ * sigmoid(v / hc) for inject rows (model.c:790-792).
  */
-__global__ __launch_bounds__(1024) void k_hc_norm_inject(HcNormArgs a) {
-    __shared__ float s_ss[HC_MAX][16];
-    __shared__ float s_ip[HC_MAX][16];
-    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int D = a.hc * a.d;
-    const float *x = a.hyper + (size_t)t * D;
-    for (int h = 0; h < a.hc; h++) {
-        float ss = 0.0f;
-        for (int i = tid * 4; i < a.d; i += 4096) {
-            const float4 v = qk_ld((const float4 *)(x + (size_t)h * a.d + i));
-            ss = fmaf(v.x, v.x, ss);
-            ss = fmaf(v.y, v.y, ss);
-            ss = fmaf(v.z, v.z, ss);
-            ss = fmaf(v.w, v.w, ss);
-        }
-        ss = hc_wave_sum(ss);
-        if (lane == 0) s_ss[h][wave] = ss;
+template <int P>
+__global__ __launch_bounds__(64 * HC_MAX) void k_hc_down(HcDownArgs a) {
+    __shared__ float s_part[2][HC_MAX][HD_RW];
+    const int lane = threadIdx.x & 63, h = threadIdx.x >> 6;
+    const int D = a.hc * a.d, CPC = a.d >> 5, G = D >> 6;
+    const size_t wrow = (size_t)D >> 3;
+    const int nrb = (a.R + HD_RW - 1) / HD_RW;
+    const int nblk = nrb + (a.hc + HD_RW - 1) / HD_RW;
+    const int tblk = blockIdx.x / nblk, rb = blockIdx.x - tblk * nblk;
+    const bool inj = rb >= nrb;
+    const int r0 = inj ? (rb - nrb) * HD_RW : rb * HD_RW;
+    const int nrows = inj ? a.hc : a.R;
+    const int t0 = tblk * a.tb, m = min(a.tb, a.n - t0);
+    if (m <= 0) return;
+    const float inv_hc = 1.0f / (float)a.hc;
+
+    /* this lane's chunks: copy-local chunk ps*64 + lane, global chunk gc[ps] */
+    int gc[P];
+    bool cok[P];
+#pragma unroll
+    for (int ps = 0; ps < P; ps++) {
+        const int cc = ps * 64 + lane;
+        cok[ps] = cc < CPC;
+        gc[ps] = h * CPC + (cok[ps] ? cc : 0);
     }
-    __syncthreads();
-    float ip[HC_MAX];
+    /* weights: q4 rows (codes, scale, bias) or bf16 rows (32 weights a chunk) */
+    uint4 wq[HD_RW][P];
+    float ws[HD_RW][P], wb[HD_RW][P];
+    uint4 wi[HD_RW][P][4];
 #pragma unroll
-    for (int j = 0; j < HC_MAX; j++) ip[j] = 0.0f;
-    for (int h = 0; h < a.hc; h++) {
-        float ss = 0.0f;
+    for (int it = 0; it < HD_RW; it++) {
+        const int r = min(r0 + it, nrows - 1);
 #pragma unroll
-        for (int w = 0; w < 16; w++) ss += s_ss[h][w];
-        const float r = 1.0f / sqrtf(ss / (float)a.d + a.eps);
-        for (int i = tid * 4; i < a.d; i += 4096) {
-            const size_t c = (size_t)h * a.d + i;
-            const float4 v = qk_ld((const float4 *)(x + c));
-            const float4 w = qk_ld((const float4 *)(a.norm_w + c));
-            const float4 y = make_float4(v.x * r * w.x, v.y * r * w.y, v.z * r * w.z, v.w * r * w.w);
-            qk_st((float4 *)(a.normed + (size_t)t * D + c), y);
+        for (int ps = 0; ps < P; ps++) {
+            const bool ok = cok[ps] && r0 + it < nrows;
+            if (inj) {
+                const uint4 *src = (const uint4 *)(a.inject_w + (size_t)r * D) + 4 * gc[ps];
 #pragma unroll
-            for (int j = 0; j < HC_MAX; j++) {
-                if (j < a.hc) {
-                    const uint2 wb = qk_ld((const uint2 *)(a.inject_w + (size_t)j * D + c));
-                    ip[j] = fmaf(y.x, qk_bf16_lo(wb.x), ip[j]);
-                    ip[j] = fmaf(y.y, qk_bf16_hi(wb.x), ip[j]);
-                    ip[j] = fmaf(y.z, qk_bf16_lo(wb.y), ip[j]);
-                    ip[j] = fmaf(y.w, qk_bf16_hi(wb.y), ip[j]);
-                }
+                for (int v = 0; v < 4; v++) wi[it][ps][v] = ok ? qk_ld(src + v) : make_uint4(0u, 0u, 0u, 0u);
+                wq[it][ps] = make_uint4(0u, 0u, 0u, 0u);
+                ws[it][ps] = wb[it][ps] = 0.0f;
+            } else {
+                wq[it][ps] = ok ? qk_ld((const uint4 *)(a.q + (size_t)r * wrow) + gc[ps])
+                                : make_uint4(0u, 0u, 0u, 0u);
+                ws[it][ps] = ok ? qk_bf16(qk_ld(a.s + (size_t)r * G + (gc[ps] >> 1))) : 0.0f;
+                wb[it][ps] = ok ? qk_bf16(qk_ld(a.b + (size_t)r * G + (gc[ps] >> 1))) : 0.0f;
+#pragma unroll
+                for (int v = 0; v < 4; v++) wi[it][ps][v] = make_uint4(0u, 0u, 0u, 0u);
             }
         }
     }
+    float4 wn[P][8];
 #pragma unroll
-    for (int j = 0; j < HC_MAX; j++) {
-        if (j < a.hc) {
-            const float v = hc_wave_sum(ip[j]);
-            if (lane == 0) s_ip[j][wave] = v;
-        }
-    }
-    __syncthreads();
-    if (tid < a.hc) {
-        float v = 0.0f;
+    for (int ps = 0; ps < P; ps++)
 #pragma unroll
-        for (int w = 0; w < 16; w++) v += s_ip[tid][w];
-        a.inject[(size_t)t * a.hc + tid] = 2.0f * qk_sigmoid(v * (1.0f / (float)a.hc));
-    }
-}
+        for (int v = 0; v < 8; v++)
+            wn[ps][v] = qk_ld((const float4 *)(a.norm_w + (size_t)gc[ps] * 32) + v);
+    const bool store_normed = rb == 0;
 
-/* ---------------------------------------------------------------- q4 GEMV */
-
-struct HcLinArgs {
-    const uint32_t *q;  /* [N, K/8] */
-    const uint16_t *s;  /* [N, K/64] bf16 */
-    const uint16_t *b;
-    const float *x;     /* [n, K] */
-    float *out;         /* [n, N] */
-    int K, N, n, tb;    /* tb: tokens per task */
-};
-
-#define HC_RITER 2
-
-/*
- * out = x . W^T for a q4 W.  Task = (block of tb tokens, block of RB rows);
- * the workgroup keeps its rows' codes in registers and walks its tokens,
- * prefetching the next token's activations under the current token's math
- * (the lane mapping of the expert GEMV: LPR lanes per row, P chunks of 32
- * columns per lane).
- */
-template <int LPR, int P>
-__global__ __launch_bounds__(256) void k_hc_linear(HcLinArgs a) {
-    constexpr int RPW = 64 / LPR;
-    constexpr int RB = 4 * RPW * HC_RITER;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int sub = lane % LPR, rsub = lane / LPR;
-    const int CH = a.K >> 5, G = a.K >> 6;
-    const size_t wrow = (size_t)a.K >> 3;
-    const int tps = (a.N + RB - 1) / RB;
-    const int tblk = blockIdx.x / tps, rb = blockIdx.x - tblk * tps;
-    const int t0 = tblk * a.tb;
-    const int m = min(a.tb, a.n - t0);
-    if (m <= 0) return;
-    const int rbase = rb * RB + wave * RPW * HC_RITER;
-    uint4 wq[HC_RITER][P];
-    uint16_t rs[HC_RITER][P], rbi[HC_RITER][P];
-    float ws[HC_RITER][P], wb[HC_RITER][P];
-    XRaw<P, false> xr;
-    load_xraw<LPR, P, false>(a.x, (size_t)t0, a.K, sub, xr);
+    float4 xr[P][8];
+    auto load_x = [&](int t) {
 #pragma unroll
-    for (int it = 0; it < HC_RITER; it++) {
-        const int r0 = rbase + it * RPW + rsub;
-        const int r = r0 < a.N ? r0 : 0;
+        for (int ps = 0; ps < P; ps++)
 #pragma unroll
-        for (int ps = 0; ps < P; ps++) {
-            const int c0 = ps * LPR + sub;
-            const int c = c0 < CH ? c0 : 0;
-            wq[it][ps] = qk_ld((const uint4 *)(a.q + (size_t)r * wrow) + c);
-            rs[it][ps] = qk_ld(a.s + (size_t)r * G + (c >> 1));
-            rbi[it][ps] = qk_ld(a.b + (size_t)r * G + (c >> 1));
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int it = 0; it < HC_RITER; it++) {
-        const bool rok = rbase + it * RPW + rsub < a.N;
-#pragma unroll
-        for (int ps = 0; ps < P; ps++) {
-            const bool ok = rok && ps * LPR + sub < CH;
-            ws[it][ps] = ok ? qk_bf16(rs[it][ps]) : 0.0f;
-            wb[it][ps] = ok ? qk_bf16(rbi[it][ps]) : 0.0f;
-            if (!ok) wq[it][ps] = make_uint4(0u, 0u, 0u, 0u);
-        }
-    }
+            for (int v = 0; v < 8; v++)
+                xr[ps][v] = qk_ld((const float4 *)(a.hyper + (size_t)t * D + (size_t)gc[ps] * 32) + v);
+    };
+    load_x(t0);
     for (int j = 0; j < m; j++) {
-        XPairs<LPR, P, false> xp;
-        convert_xraw<LPR, P, false>(xr, a.K, sub, xp);
-        if (j + 1 < m) load_xraw<LPR, P, false>(a.x, (size_t)(t0 + j + 1), a.K, sub, xr);
+        const int t = t0 + j;
+        float xv[P][32];
+        float ss = 0.0f;
 #pragma unroll
-        for (int it = 0; it < HC_RITER; it++) {
-            const float v = qk_group_sum<LPR>(row_part<LPR, P, false>(wq[it], ws[it], wb[it], xp));
-            const int r = rbase + it * RPW + rsub;
-            if (sub == 0 && r < a.N) qk_st(a.out + (size_t)(t0 + j) * a.N + r, v);
+        for (int ps = 0; ps < P; ps++)
+#pragma unroll
+            for (int v = 0; v < 8; v++) {
+                const float4 f = xr[ps][v];
+                xv[ps][4 * v] = cok[ps] ? f.x : 0.0f;
+                xv[ps][4 * v + 1] = cok[ps] ? f.y : 0.0f;
+                xv[ps][4 * v + 2] = cok[ps] ? f.z : 0.0f;
+                xv[ps][4 * v + 3] = cok[ps] ? f.w : 0.0f;
+            }
+        if (j + 1 < m) load_x(t + 1);
+#pragma unroll
+        for (int ps = 0; ps < P; ps++)
+#pragma unroll
+            for (int i = 0; i < 32; i++) ss = fmaf(xv[ps][i], xv[ps][i], ss);
+        ss = qk_group_sum<64>(ss);
+        const float r = 1.0f / sqrtf(ss / (float)a.d + a.eps);
+        XPairs<64, P, false> xp;
+#pragma unroll
+        for (int ps = 0; ps < P; ps++) {
+            xp.xs[ps] = 0.0f;
+#pragma unroll
+            for (int v = 0; v < 8; v++) {
+                const float4 wv = wn[ps][v];
+                xv[ps][4 * v] = xv[ps][4 * v] * r * wv.x;
+                xv[ps][4 * v + 1] = xv[ps][4 * v + 1] * r * wv.y;
+                xv[ps][4 * v + 2] = xv[ps][4 * v + 2] * r * wv.z;
+                xv[ps][4 * v + 3] = xv[ps][4 * v + 3] * r * wv.w;
+            }
+            if (store_normed && cok[ps]) {
+                float4 *dst = (float4 *)(a.normed + (size_t)t * D + (size_t)gc[ps] * 32);
+#pragma unroll
+                for (int v = 0; v < 8; v++)
+                    qk_st(dst + v, make_float4(xv[ps][4 * v], xv[ps][4 * v + 1], xv[ps][4 * v + 2],
+                                               xv[ps][4 * v + 3]));
+            }
+#pragma unroll
+            for (int w = 0; w < 4; w++)
+                qk_f32x8_to_pairs(&xv[ps][8 * w], &xp.hi[ps][4 * w], &xp.lo[ps][4 * w], xp.xs[ps]);
+        }
+#pragma unroll
+        for (int it = 0; it < HD_RW; it++) {
+            float part;
+            if (inj) {
+                part = 0.0f;
+#pragma unroll
+                for (int ps = 0; ps < P; ps++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        uint32_t pr[4];
+                        qk_bf16x8_to_pairs(wi[it][ps][v], pr);
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            part = qk_dot2(xp.hi[ps][4 * v + i], pr[i], part);
+                            part = qk_dot2(xp.lo[ps][4 * v + i], pr[i], part);
+                        }
+                    }
+            } else {
+                part = row_part<64, P, false>(wq[it], ws[it], wb[it], xp);
+            }
+            const float v = qk_group_sum<64>(part);
+            if (lane == 0) s_part[j & 1][h][it] = v;
+        }
+        __syncthreads();
+        if ((int)threadIdx.x < HD_RW && r0 + (int)threadIdx.x < nrows) {
+            const int it = threadIdx.x;
+            float acc = 0.0f;
+            for (int hh = 0; hh < a.hc; hh++) acc += s_part[j & 1][hh][it];
+            if (inj) a.inject[(size_t)t * a.hc + r0 + it] = 2.0f * qk_sigmoid(acc * inv_hc);
+            else a.w[(size_t)t * a.R + r0 + it] = qk_silu(acc * inv_hc);
         }
     }
 }
@@ -190,34 +209,13 @@ struct HcUpArgs {
     const uint32_t *q;    /* input_mix_weight_up [hc*d, R/8] */
     const uint16_t *s;    /* [hc*d, R/64] */
     const uint16_t *b;
-    const float *down;    /* [n, R] down outputs before silu */
+    const float *w;       /* [n, R] silu(down / hc) */
     const float *normed;  /* [n, hc*d] */
     float *mixed;         /* [n, d] */
     int hc, d, R, n, tb;
 };
 
 #define HU_RIT 4
-
-/* this lane's chunks of w = silu(down / hc) as bf16 pairs (kernel_scale
- * then kernel_silu, model.c:757-758) */
-template <int LPR, int P>
-__device__ __forceinline__ void hc_convert_silu(const XRaw<P, false> &xr, int K, int sub, float inv_hc,
-                                                XPairs<LPR, P, false> &xp) {
-    const int CH = K >> 5;
-#pragma unroll
-    for (int ps = 0; ps < P; ps++) {
-        const bool ok = ps * LPR + sub < CH;
-        xp.xs[ps] = 0.0f;
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-            const float4 a0 = xr.f[ps][2 * w], a1 = xr.f[ps][2 * w + 1];
-            float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-#pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = ok ? qk_silu(v[j] * inv_hc) : 0.0f;
-            qk_f32x8_to_pairs(v, &xp.hi[ps][4 * w], &xp.lo[ps][4 * w], xp.xs[ps]);
-        }
-    }
-}
 
 /*
  * Workgroup = hc waves (wave h computes rows h*d + i of the up projection)
@@ -242,12 +240,11 @@ __global__ __launch_bounds__(64 * HC_MAX) void k_hc_upmix(HcUpArgs a) {
     const int c0 = cb * CB, t0 = tblk * a.tb;
     const int m = min(a.tb, a.n - t0);
     if (m <= 0) return;
-    const float inv_hc = 1.0f / (float)a.hc;
     uint4 wq[HU_RIT][P];
     uint16_t rs[HU_RIT][P], rbi[HU_RIT][P];
     float ws[HU_RIT][P], wb[HU_RIT][P];
     XRaw<P, false> xr;
-    load_xraw<LPR, P, false>(a.down, (size_t)t0, K, sub, xr);
+    load_xraw<LPR, P, false>(a.w, (size_t)t0, K, sub, xr);
 #pragma unroll
     for (int it = 0; it < HU_RIT; it++) {
         const int i0 = c0 + it * RPW + rsub;
@@ -284,8 +281,8 @@ __global__ __launch_bounds__(64 * HC_MAX) void k_hc_upmix(HcUpArgs a) {
             nv[hh] = (mixer && hh < a.hc) ? qk_ld(a.normed + (size_t)t * D + (size_t)hh * a.d + mix_i)
                                           : 0.0f;
         XPairs<LPR, P, false> xp;
-        hc_convert_silu<LPR, P>(xr, K, sub, inv_hc, xp);
-        if (j + 1 < m) load_xraw<LPR, P, false>(a.down, (size_t)(t + 1), K, sub, xr);
+        convert_xraw<LPR, P, false>(xr, K, sub, xp);
+        if (j + 1 < m) load_xraw<LPR, P, false>(a.w, (size_t)(t + 1), K, sub, xr);
 #pragma unroll
         for (int it = 0; it < HU_RIT; it++) {
             const float v = qk_group_sum<LPR>(row_part<LPR, P, false>(wq[it], ws[it], wb[it], xp));
@@ -341,42 +338,24 @@ static int hc_tokens_per_task(int n, int blocks) {
 }
 
 extern "C" int qk_hc_shape_ok(int hc, int d, int R) {
-    return hc >= 1 && hc <= HC_MAX && d > 0 && d % 64 == 0 && R >= 64 && R % 64 == 0 &&
-           R <= 2048 && (long long)hc * d <= 8192;
+    /* k_hc_down: one wave per copy, one 32-column chunk per lane (d <= 2048);
+     * k_hc_upmix: one chunk of the low-rank vector per lane (R <= 2048) */
+    return hc >= 1 && hc <= HC_MAX && d > 0 && d % 64 == 0 && d <= 2048 && R >= 64 &&
+           R % 64 == 0 && R <= 2048;
 }
 
-extern "C" int qk_launch_hc_norm_inject(const float *hyper, const float *norm_w,
-                                        const uint16_t *inject_w, int hc, int d, int n, float eps,
-                                        float *normed, float *inject, void *stream) {
+extern "C" int qk_launch_hc_down(const float *hyper, const float *norm_w, const uint32_t *q,
+                                 const uint16_t *s, const uint16_t *b, const uint16_t *inject_w,
+                                 int hc, int d, int R, int n, float eps, float *normed, float *w,
+                                 float *inject, void *stream) {
     if (n <= 0) return 0;
-    HcNormArgs a{hyper, norm_w, inject_w, normed, inject, hc, d, eps};
-    hipLaunchKernelGGL(k_hc_norm_inject, dim3(n), dim3(1024), 0, (hipStream_t)stream, a);
-    return QK_CHECK_LAUNCH();
-}
-
-extern "C" int qk_launch_hc_linear(const uint32_t *q, const uint16_t *s, const uint16_t *b,
-                                   const float *x, int n, int K, int N, float *out, void *stream) {
-    if (n <= 0) return 0;
-    const int lpr = hc_pick_lpr(K), ch = K / 32;
-    const int P = (ch + lpr - 1) / lpr;
-    const int rb = 4 * (64 / lpr) * HC_RITER;
-    const int tps = (N + rb - 1) / rb;
-    const int tb = hc_tokens_per_task(n, tps);
-    HcLinArgs a{q, s, b, x, out, K, N, n, tb};
-    const dim3 grid((unsigned)(((n + tb - 1) / tb) * tps));
+    if (!qk_hc_shape_ok(hc, d, R)) return (int)hipErrorInvalidValue;
+    const int nblk = (R + HD_RW - 1) / HD_RW + (hc + HD_RW - 1) / HD_RW;
+    const int tb = hc_tokens_per_task(n, nblk);
+    HcDownArgs a{hyper, norm_w, q, s, b, inject_w, normed, w, inject, hc, d, R, n, tb, eps};
+    const dim3 grid((unsigned)(((n + tb - 1) / tb) * nblk)), blk(64 * hc);
     hipStream_t st = (hipStream_t)stream;
-#define HL(L, PP) hipLaunchKernelGGL((k_hc_linear<L, PP>), grid, dim3(256), 0, st, a)
-    if (lpr == 64) {
-        if (P == 1) HL(64, 1);
-        else if (P == 2) HL(64, 2);
-        else if (P <= 4) HL(64, 4);
-        else return (int)hipErrorInvalidValue;
-    } else if (lpr == 32) HL(32, 1);
-    else if (lpr == 16) HL(16, 1);
-    else if (lpr == 8) HL(8, 1);
-    else if (lpr == 4) HL(4, 1);
-    else HL(2, 1);
-#undef HL
+    hipLaunchKernelGGL(k_hc_down<1>, grid, blk, 0, st, a);
     return QK_CHECK_LAUNCH();
 }
 

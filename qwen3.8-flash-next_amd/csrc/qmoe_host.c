@@ -858,7 +858,7 @@ int qmoe_hc_enable(qmoe_ctx *c, int hc_count, int hc_lowrank, qmoe_err *err) {
     }
     if (!qk_hc_shape_ok(hc_count, c->cfg.hidden, hc_lowrank)) {
         set_err(err, "hc_count %d, hc_lowrank %d unsupported with hidden %d (needs 1 <= hc_count <= 8, "
-                     "hc_lowrank a multiple of 64 in [64, 2048], hc_count*hidden <= 8192)",
+                     "hc_lowrank a multiple of 64 in [64, 2048], hidden <= 2048)",
                 hc_count, hc_lowrank, c->cfg.hidden);
         return -1;
     }
@@ -1033,18 +1033,15 @@ static int hc_check_call(qmoe_ctx *c, int layer, int n, qmoe_err *err) {
     return 0;
 }
 
-/* gated_residual (model.c:728-796): three launches */
+/* gated_residual (model.c:728-796): two launches */
 static int run_hc_mix(qmoe_ctx *c, int layer, const float *hyper, int n, float *mixed,
                       float *inject, void *stream, qmoe_err *err) {
     qmoe_hc_weights W;
     hc_dev(c, layer, &W);
-    const int d = c->cfg.hidden, D = c->hc * d;
-    int rc = qk_launch_hc_norm_inject(hyper, W.hc_norm, W.inject_w, c->hc, d, n, 1e-6f,
-                                      c->hc_normed, inject, stream);
-    if (hip_fail(err, rc, "hc norm+inject")) return -1;
-    rc = qk_launch_hc_linear(W.down_q, W.down_s, W.down_b, c->hc_normed, n, D, c->hc_R, c->hc_down,
-                             stream);
-    if (hip_fail(err, rc, "hc down")) return -1;
+    const int d = c->cfg.hidden;
+    int rc = qk_launch_hc_down(hyper, W.hc_norm, W.down_q, W.down_s, W.down_b, W.inject_w, c->hc, d,
+                               c->hc_R, n, 1e-6f, c->hc_normed, c->hc_down, inject, stream);
+    if (hip_fail(err, rc, "hc norm+down+inject")) return -1;
     rc = qk_launch_hc_upmix(W.up_q, W.up_s, W.up_b, c->hc_down, c->hc_normed, c->hc, d, c->hc_R, n,
                             mixed, stream);
     return hip_fail(err, rc, "hc up+mix");

@@ -170,17 +170,16 @@ int qk_launch_combine(qk_shape s, int n, const float *y, const int32_t *pos, con
                       const float *inject, int hc, void *stream);
 
 /* the MLP hyper connection (hyper.hip): shapes it takes (hc <= 8, d and R
- * multiples of 64, R <= 2048, hc*d <= 8192) */
+ * multiples of 64, d <= 2048, R <= 2048) */
 int qk_hc_shape_ok(int hc, int d, int R);
-/* normed [n, hc*d] and inject [n, hc] from the hyper state [n, hc*d] */
-int qk_launch_hc_norm_inject(const float *hyper, const float *norm_w, const uint16_t *inject_w,
-                             int hc, int d, int n, float eps, float *normed, float *inject,
-                             void *stream);
-/* out [n, N] = x [n, K] . W^T, W q4 [N, K/8] with bf16 scales/biases per 64 */
-int qk_launch_hc_linear(const uint32_t *q, const uint16_t *s, const uint16_t *b, const float *x,
-                        int n, int K, int N, float *out, void *stream);
-/* mixed [n, d] = mean_h sigmoid(silu(down/hc) . Wup^T)[h*d + i] * normed[h*d + i] */
-int qk_launch_hc_upmix(const uint32_t *q, const uint16_t *s, const uint16_t *b, const float *down,
+/* from the hyper state [n, hc*d]: normed [n, hc*d], w [n, R] =
+ * silu(normed . Wdown^T / hc) (Wdown q4 [R, hc*d/8]) and inject [n, hc] =
+ * 2 sigmoid(normed . Winject^T / hc) (Winject bf16 [hc, hc*d]) */
+int qk_launch_hc_down(const float *hyper, const float *norm_w, const uint32_t *q, const uint16_t *s,
+                      const uint16_t *b, const uint16_t *inject_w, int hc, int d, int R, int n,
+                      float eps, float *normed, float *w, float *inject, void *stream);
+/* mixed [n, d] = mean_h sigmoid(w . Wup^T)[h*d + i] * normed[h*d + i] */
+int qk_launch_hc_upmix(const uint32_t *q, const uint16_t *s, const uint16_t *b, const float *w,
                        const float *normed, int hc, int d, int R, int n, float *mixed,
                        void *stream);
 /* hyper [n, hc, d]: every copy j of token t becomes fma(inject[t, j], out[t], hyper[t, j]) */

@@ -26,6 +26,8 @@ TAGS = dict(
     ROUTER_W=1, GATE_Q=2, GATE_S=3, GATE_B=4, UP_Q=5, UP_S=6, UP_B=7, DOWN_Q=8, DOWN_S=9,
     DOWN_B=10, SH_GATE_Q=11, SH_GATE_S=12, SH_GATE_B=13, SH_UP_Q=14, SH_UP_S=15, SH_UP_B=16,
     SH_DOWN_Q=17, SH_DOWN_S=18, SH_DOWN_B=19, SHGATE_W=20, X=22,
+    HC_DOWN_Q=24, HC_DOWN_S=25, HC_DOWN_B=26, HC_UP_Q=27, HC_UP_S=28, HC_UP_B=29,
+    HC_INJECT_W=30, HYPER=31,
 )
 
 WEIGHT_FIELDS = [
