@@ -35,9 +35,7 @@
  */
 #include "qk_device.h"
 #include "mm_tasks.h"
-
-typedef __bf16 qm_bf16x8 __attribute__((ext_vector_type(8)));
-typedef float qm_f32x4 __attribute__((ext_vector_type(4)));
+#include "mfma_parts.h"
 
 #define MM_WD 2              /* code-word prefetch depth, groups */
 
@@ -66,18 +64,6 @@ struct MmSmem {
     uint16_t s[MM_MAXG][4][16][CT];  /* scales, [group][wave][column][tile] */
     int row[BMT * 16];
 };
-
-/* one code word -> the B operand: bf16 128+q in (q_i, q_{i+4}) pair order,
- * as qk_codes_to_pairs, built with byte permutes: the low nibbles of the
- * four bytes (q0, q2, q4, q6) and the high ones (q1, q3, q5, q7) each give
- * two pairs by interleaving with the byte 0x43 */
-__device__ __forceinline__ qm_bf16x8 qm_codes(uint32_t w) {
-    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-    const uint32_t k = 0x43434343u;
-    return __builtin_bit_cast(qm_bf16x8,
-                              make_uint4(__builtin_amdgcn_perm(k, lo, 0x04020400u), __builtin_amdgcn_perm(k, hi, 0x04020400u),
-                                         __builtin_amdgcn_perm(k, lo, 0x04030401u), __builtin_amdgcn_perm(k, hi, 0x04030401u)));
-}
 
 /* column of tile ct for this lane.  Down: a workgroup covers 64*CT
  * columns, 16*CT per wave.  Gate/up: tiles 0..CT/2-1 are gate and the rest

@@ -49,6 +49,7 @@ struct qmoe_ctx {
     int *hc_ready;
     void *hc_scratch;
     float *hc_normed, *hc_down, *hc_inject, *hc_mixed;
+    void *hc_ws; /* MFMA path workspace (max_tokens >= QK_HC_MM_MIN) */
 };
 
 static void set_err(qmoe_err *err, const char *fmt, ...) {
@@ -237,6 +238,7 @@ void qmoe_destroy(qmoe_ctx *c) {
         for (int l = 0; l < c->cfg.n_layers; l++)
             if (c->hc_mem[l]) hipFree(c->hc_mem[l]);
     if (c->hc_scratch) hipFree(c->hc_scratch);
+    if (c->hc_ws) hipFree(c->hc_ws);
     free(c->hc_mem);
     free(c->hc_ready);
     free(c->layers);
@@ -893,6 +895,19 @@ int qmoe_hc_enable(qmoe_ctx *c, int hc_count, int hc_lowrank, qmoe_err *err) {
         c->hc = c->hc_R = 0;
         return -1;
     }
+    if (c->cfg.max_tokens >= QK_HC_MM_MIN &&
+        hip_fail(err, (int)hipMalloc(&c->hc_ws, qk_hc_mm_ws_bytes(hc_count, c->cfg.hidden, hc_lowrank,
+                                                                 c->cfg.max_tokens)),
+                 "hipMalloc(hc workspace)")) {
+        hipFree(c->hc_scratch);
+        free(c->hc_mem);
+        free(c->hc_ready);
+        c->hc_mem = NULL;
+        c->hc_ready = NULL;
+        c->hc_scratch = c->hc_ws = NULL;
+        c->hc = c->hc_R = 0;
+        return -1;
+    }
     char *b = (char *)c->hc_scratch;
     c->hc_normed = (float *)(b + offs[0]);
     c->hc_down = (float *)(b + offs[1]);
@@ -1033,18 +1048,33 @@ static int hc_check_call(qmoe_ctx *c, int layer, int n, qmoe_err *err) {
     return 0;
 }
 
-/* gated_residual (model.c:728-796): two launches */
+/* gated_residual (model.c:728-796): two GEMV launches for few tokens, the
+ * MFMA path for many; normed_out (may be NULL) receives normed */
 static int run_hc_mix(qmoe_ctx *c, int layer, const float *hyper, int n, float *mixed,
-                      float *inject, void *stream, qmoe_err *err) {
+                      float *inject, float *normed_out, void *stream, qmoe_err *err) {
     qmoe_hc_weights W;
     hc_dev(c, layer, &W);
     const int d = c->cfg.hidden;
-    int rc = qk_launch_hc_down(hyper, W.hc_norm, W.down_q, W.down_s, W.down_b, W.inject_w, c->hc, d,
+    int rc;
+    if (n >= QK_HC_MM_MIN && c->hc_ws) {
+        rc = qk_launch_hc_mm(hyper, W.hc_norm, W.down_q, W.down_s, W.down_b, W.up_q, W.up_s, W.up_b,
+                             W.inject_w, c->hc, d, c->hc_R, n, 1e-6f, c->hc_ws, mixed, inject,
+                             normed_out, stream);
+        return hip_fail(err, rc, "hc mix (MFMA)");
+    }
+    rc = qk_launch_hc_down(hyper, W.hc_norm, W.down_q, W.down_s, W.down_b, W.inject_w, c->hc, d,
                                c->hc_R, n, 1e-6f, c->hc_normed, c->hc_down, inject, stream);
     if (hip_fail(err, rc, "hc norm+down+inject")) return -1;
     rc = qk_launch_hc_upmix(W.up_q, W.up_s, W.up_b, c->hc_down, c->hc_normed, c->hc, d, c->hc_R, n,
                             mixed, stream);
-    return hip_fail(err, rc, "hc up+mix");
+    if (hip_fail(err, rc, "hc up+mix")) return -1;
+    if (normed_out &&
+        hip_fail(err, (int)hipMemcpyAsync(normed_out, c->hc_normed,
+                                          (size_t)n * c->hc * d * sizeof(float),
+                                          hipMemcpyDeviceToDevice, (hipStream_t)stream),
+                 "copy normed"))
+        return -1;
+    return 0;
 }
 
 int qmoe_hc_mix(qmoe_ctx *c, int layer, const float *hyper, int n, float *mixed_out,
@@ -1054,16 +1084,8 @@ int qmoe_hc_mix(qmoe_ctx *c, int layer, const float *hyper, int n, float *mixed_
     if (n == 0) return 0;
     NEED(hyper, "hyper");
     NEED(mixed_out, "mixed_out");
-    if (run_hc_mix(c, layer, hyper, n, mixed_out, inject_out ? inject_out : c->hc_inject, stream,
-                   err))
-        return -1;
-    if (normed_out &&
-        hip_fail(err, (int)hipMemcpyAsync(normed_out, c->hc_normed,
-                                          (size_t)n * c->hc * c->cfg.hidden * sizeof(float),
-                                          hipMemcpyDeviceToDevice, (hipStream_t)stream),
-                 "copy normed"))
-        return -1;
-    return 0;
+    return run_hc_mix(c, layer, hyper, n, mixed_out, inject_out ? inject_out : c->hc_inject,
+                      normed_out, stream, err);
 }
 
 int qmoe_hc_inject(qmoe_ctx *c, const float *inject, const float *moe_out, int n, float *hyper,
@@ -1095,7 +1117,7 @@ int qmoe_hc_layer_forward(qmoe_ctx *c, int layer, float *hyper, int n, float *mo
     if (hc_check_call(c, layer, n, err) || check_call(c, layer, n, err)) return -1;
     if (n == 0) return 0;
     NEED(hyper, "hyper");
-    if (run_hc_mix(c, layer, hyper, n, c->hc_mixed, c->hc_inject, stream, err)) return -1;
+    if (run_hc_mix(c, layer, hyper, n, c->hc_mixed, c->hc_inject, NULL, stream, err)) return -1;
     return layer_forward(c, layer, c->hc_mixed, 0, n, moe_out, 0, hyper, c->hc_inject, stream, err);
 }
 

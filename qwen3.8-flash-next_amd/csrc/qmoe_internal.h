@@ -182,6 +182,16 @@ int qk_launch_hc_down(const float *hyper, const float *norm_w, const uint32_t *q
 int qk_launch_hc_upmix(const uint32_t *q, const uint16_t *s, const uint16_t *b, const float *w,
                        const float *normed, int hc, int d, int R, int n, float *mixed,
                        void *stream);
+/* the same on MFMA for many tokens (hyper_mm.hip), from this many on */
+#define QK_HC_MM_MIN 16
+size_t qk_hc_mm_ws_bytes(int hc, int d, int R, int max_n);
+int qk_hc_mm_kspl(int hc, int d, int R, int n);
+/* mixed [n, d], inject [n, hc] and (if non-NULL) normed [n, hc*d]; ws of
+ * qk_hc_mm_ws_bytes(hc, d, R, >= n) bytes */
+int qk_launch_hc_mm(const float *hyper, const float *norm_w, const uint32_t *dq, const uint16_t *ds,
+                    const uint16_t *db, const uint32_t *uq, const uint16_t *us, const uint16_t *ub,
+                    const uint16_t *inject_w, int hc, int d, int R, int n, float eps, void *ws,
+                    float *mixed, float *inject, float *normed, void *stream);
 /* hyper [n, hc, d]: every copy j of token t becomes fma(inject[t, j], out[t], hyper[t, j]) */
 int qk_launch_hc_inject(const float *inject, const float *out, int hc, int d, int n, float *hyper,
                         void *stream);
