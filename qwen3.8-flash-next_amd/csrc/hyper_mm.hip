@@ -265,12 +265,13 @@ struct HcFinishArgs {
 };
 
 /* sum_h r[h] * (sum of copy h's kspl parts) over the parts at p (copy-major,
- * kspl = 1 << lk), every load issued before the sums */
+ * kspl = 1 << lk, parts <= PM), every load issued before the sums */
+template <int PM>
 __device__ __forceinline__ float hm_parts_dot(const float *p, int parts, int lk, const float *r) {
-    float pv[64];
+    float pv[PM];
     if ((parts & 3) == 0) {
 #pragma unroll
-        for (int q4 = 0; q4 < 16; q4++) {
+        for (int q4 = 0; q4 < PM / 4; q4++) {
             const float4 v = 4 * q4 < parts ? qk_ld((const float4 *)p + q4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             pv[4 * q4] = v.x;
             pv[4 * q4 + 1] = v.y;
@@ -279,12 +280,12 @@ __device__ __forceinline__ float hm_parts_dot(const float *p, int parts, int lk,
         }
     } else {
 #pragma unroll
-        for (int q = 0; q < 64; q++) pv[q] = q < parts ? qk_ld(p + q) : 0.0f;
+        for (int q = 0; q < PM; q++) pv[q] = q < parts ? qk_ld(p + q) : 0.0f;
     }
     const int km = (1 << lk) - 1;
     float v = 0.0f, ph = 0.0f;
 #pragma unroll
-    for (int q = 0; q < 64; q++) {
+    for (int q = 0; q < PM; q++) {
         if (q < parts) {
             ph += pv[q];
             if (((q + 1) & km) == 0) {
@@ -297,7 +298,8 @@ __device__ __forceinline__ float hm_parts_dot(const float *p, int parts, int lk,
 }
 
 /* grid = n, 512 threads: r_h, w = silu(sum_h r_h * partial_h / hc),
- * inject, and the MFMA planes of w */
+ * inject, and the MFMA planes of w; PM bounds the parts */
+template <int PM>
 __global__ __launch_bounds__(512) void k_hc_finish(HcFinishArgs a) {
     __shared__ float s_w[2048];
     __shared__ float s_r[HC_MAX];
@@ -318,7 +320,7 @@ __global__ __launch_bounds__(512) void k_hc_finish(HcFinishArgs a) {
         if (!isw && r - a.R >= a.hc) continue;
         const float *p = isw ? a.pd + ((size_t)t * a.R + r) * parts
                              : a.pi + ((size_t)t * 16 + (r - a.R)) * parts;
-        const float v = hm_parts_dot(p, parts, lk, s_r);
+        const float v = hm_parts_dot<PM>(p, parts, lk, s_r);
         if (isw) s_w[r] = qk_silu(v * inv_hc);
         else a.inject[(size_t)t * a.hc + (r - a.R)] = 2.0f * qk_sigmoid(v * inv_hc);
     }
@@ -519,7 +521,11 @@ extern "C" int qk_launch_hc_mm(const float *hyper, const float *norm_w, const ui
     else if (nt == 8) hipLaunchKernelGGL(k_hc_mm_down<8>, gd, dim3(256), 0, st, da);
     else hipLaunchKernelGGL(k_hc_mm_down<4>, gd, dim3(256), 0, st, da);
     HcFinishArgs fa{pd, pi, pss, rs, whi, wlo, wp, inject, hc, d, R, n, kspl, eps};
-    hipLaunchKernelGGL(k_hc_finish, dim3(n), dim3(512), 0, st, fa);
+    if (parts <= 4) hipLaunchKernelGGL(k_hc_finish<4>, dim3(n), dim3(512), 0, st, fa);
+    else if (parts <= 8) hipLaunchKernelGGL(k_hc_finish<8>, dim3(n), dim3(512), 0, st, fa);
+    else if (parts <= 16) hipLaunchKernelGGL(k_hc_finish<16>, dim3(n), dim3(512), 0, st, fa);
+    else if (parts <= 32) hipLaunchKernelGGL(k_hc_finish<32>, dim3(n), dim3(512), 0, st, fa);
+    else hipLaunchKernelGGL(k_hc_finish<64>, dim3(n), dim3(512), 0, st, fa);
     HcMmUpArgs ua{whi, wlo, wp, uq, us, ub, hyper, norm_w, rs, mixed, d, R, n};
     /* few tokens: one block of 16 columns per workgroup (4x the workgroups) */
     if (n <= 256) hc_launch_up<1>(hc, dim3(nrb, d / 16), st, ua);
