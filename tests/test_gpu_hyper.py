@@ -138,6 +138,28 @@ def test_prefill_hyper_layer(torch_dev):
     _case(torch, dev, DECODE, 4096, seed=9, n_check=16)
 
 
+def test_golden_hyper_tiny(torch_dev):
+    """tests/golden/hyper_tiny.npz: the tiny layer inside its hyper connection"""
+    import os
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    say("case: golden hyper_tiny (4 tokens, hc 4, rank 128, non-unit hc_norm)")
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "hyper_tiny.npz"))
+    L = orc.Layer(256, 8, 2, 128, seed=0)
+    a = orc.Hyper(4, 256, 128, seed=0, norm_std=0.2).arrays()
+    a["hc_norm"] = np.array(g["hc_norm"])
+    with pkg.MoeContext(256, 8, 2, 128, max_tokens=4) as ctx:
+        ctx.upload_layer(0, L.arrays())
+        ctx.hc_enable(4, 128)
+        ctx.hc_upload_layer(0, a)
+        h = torch.from_numpy(np.array(g["hyper_in"])).to(dev)
+        out = ctx.hc_layer_forward(0, h)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(ctx.last_routing(4)["idx"].cpu().numpy(), g["idx"])
+        assert_close(out.cpu().numpy(), g["moe_out"], "golden moe out")
+        assert_close(h.cpu().numpy(), g["hyper_out"], "golden hyper")
+
+
 def test_hc_synth_matches_host_generator(torch_dev):
     torch, dev = torch_dev
     pkg = load_pkg()

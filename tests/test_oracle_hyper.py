@@ -135,3 +135,25 @@ def test_hyper_generator_is_seeded_and_shaped():
     assert not np.array_equal(a.t["down_q"], c.t["down_q"])
     assert a.t["down_q"].size == 64 * 512 // 8 and a.t["up_s"].size == 512 * 64 // 64
     assert a.t["inject_w"].size == 4 * 512 and np.all(a.t["hc_norm"] == 1.0)
+
+
+def _golden_case():
+    """the case of tests/golden/hyper_tiny.npz (make_golden.py:hyper_tiny_case)"""
+    L = orc.Layer(256, 8, 2, 128, seed=0)
+    a = orc.Hyper(4, 256, 128, seed=0, norm_std=0.2).arrays()
+    a["hc_norm"] = orc.bf16_to_f32(orc.f32_to_bf16(a["hc_norm"]))
+    return L, orc.Hyper.from_arrays(4, 256, 128, a), orc.gen_hyper(4, 4, 256, seed=0)
+
+
+def test_golden_hyper_tiny_reproduces():
+    import hashlib
+    import os
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "hyper_tiny.npz"))
+    L, hp, hyper = _golden_case()
+    for name, digest in zip(g["weight_names"], g["weight_sha256"]):
+        assert hashlib.sha256(np.ascontiguousarray(hp.t[str(name)]).tobytes()).hexdigest() == digest
+    assert np.array_equal(hyper, g["hyper_in"])
+    r = hp.layer_forward(L, hyper)
+    for k in ("mixed", "inject", "moe_out"):
+        assert np.array_equal(r[k], g[k]), k
+    assert np.array_equal(r["hyper"], g["hyper_out"])
