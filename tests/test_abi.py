@@ -52,6 +52,13 @@ def test_null_and_bad_arguments_return_errors():
                             ctypes.byref(err)) == -1
     assert lib.qmoe_last_routing(None, 1, None, None, None, None, None, None, None,
                                  ctypes.byref(err)) == -1
+    # the hyper-connection entry points too
+    for rc in (lib.qmoe_hc_enable(None, 4, 320, ctypes.byref(err)),
+               lib.qmoe_hc_mix(None, 0, None, 1, None, None, None, None, ctypes.byref(err)),
+               lib.qmoe_hc_inject(None, None, None, 1, None, None, ctypes.byref(err)),
+               lib.qmoe_hc_layer_forward(None, 0, None, 1, None, None, ctypes.byref(err)),
+               lib.qmoe_hc_synth_layer(None, 0, 1, ctypes.byref(err))):
+        assert rc == -1 and b"ctx is NULL" in err.msg
     # config validation happens before any device call
     h = ctypes.c_void_p()
     for bad, msg in (((256, 8, 2, 128, 32, 1, 4, 1e-6), b"group_size"),
