@@ -339,6 +339,56 @@ int qmoe_hc_inject(qmoe_ctx *ctx, const float *inject, const float *moe_out, int
 int qmoe_hc_layer_forward(qmoe_ctx *ctx, int layer, float *hyper, int n, float *moe_out,
                           void *stream, qmoe_err *err);
 
+/* ------------------------------------------------------ expert streaming
+ * For family sizes whose experts do not fit in HBM: the routed experts of
+ * every layer live in pinned host memory and each layer owns a pool of
+ * HBM expert slots; qmoe_layer_forward then routes on the GPU, brings the
+ * layer's missing experts into slots (evicting by the reference's policy,
+ * c/src/cache.c:99-259), remaps the segment table from expert ids to slots
+ * and runs the same expert kernels on the slot pool.  Replaces the SSD
+ * stream + expert cache of experts_load (model.c:536-674) and the
+ * route-transition prefetch of the MLX runtime (streaming.py:400-435).  The
+ * router, shared expert and gates stay resident. */
+
+/* cache policies, as CACHE_POLICY_* (c/src/cache.h:8-10) */
+enum { QMOE_CACHE_LRU = 0, QMOE_CACHE_LFU = 1, QMOE_CACHE_ADAPTIVE = 2 };
+
+/* Switches the context to streamed experts: slots_per_layer HBM expert
+ * slots per layer (>= the distinct experts one call can route, i.e.
+ * min(n_experts, max_tokens * top_k), and <= n_experts), the eviction
+ * policy, and up to `prefetch` experts requested ahead per layer call (0 =
+ * none).  Must precede every upload or synthesis.  In this mode the expert
+ * stage functions (qmoe_expert_*) are refused: the layer call runs them. */
+int qmoe_stream_enable(qmoe_ctx *ctx, int slots_per_layer, int policy, int prefetch,
+                       qmoe_err *err);
+
+typedef struct {
+    uint64_t hits, misses, evictions, rejected; /* cache_snapshot's counters (cache.h:45-48) */
+    uint64_t bytes_in;        /* host -> HBM expert bytes, demand and prefetch */
+    uint64_t prefetched;      /* experts brought in ahead of use */
+    uint64_t prefetch_hits;   /* ... of which a later call used */
+} qmoe_stream_stats;
+
+int qmoe_stream_get_stats(qmoe_ctx *ctx, qmoe_stream_stats *out, qmoe_err *err);
+
+/* The slot cache itself, host only (the policy's test surface; mirrors
+ * cache_init / cache_peek / cache_get / cache_put / cache_pin / cache_unpin /
+ * cache_mark_hot / cache_snapshot of c/src/cache.h:36-58 for `parts`
+ * partitions of `slots` entries of entry_bytes each over items 0..items-1).
+ * qmoe_xcache_get and _put return the slot or -1; counts = hits, misses,
+ * evictions, rejected. */
+typedef struct qmoe_xcache qmoe_xcache;
+int qmoe_xcache_create(qmoe_xcache **out, int parts, int items, int slots, int policy,
+                       uint64_t entry_bytes, qmoe_err *err);
+void qmoe_xcache_destroy(qmoe_xcache *c);
+int qmoe_xcache_peek(qmoe_xcache *c, int part, int item);
+int qmoe_xcache_get(qmoe_xcache *c, int part, int item);
+int qmoe_xcache_put(qmoe_xcache *c, int part, int item, int pin, int hot, int *evicted);
+int qmoe_xcache_pin(qmoe_xcache *c, int part, int item, int pinned);
+int qmoe_xcache_mark_hot(qmoe_xcache *c, int part, int item, int hot);
+void qmoe_xcache_clear(qmoe_xcache *c, int part);
+void qmoe_xcache_counts(const qmoe_xcache *c, uint64_t out[4]);
+
 /* Size in bytes of the context's device scratch and of one resident layer. */
 size_t qmoe_scratch_bytes(const qmoe_ctx *ctx);
 size_t qmoe_layer_bytes(const qmoe_ctx *ctx);

@@ -50,7 +50,30 @@ struct qmoe_ctx {
     void *hc_scratch;
     float *hc_normed, *hc_down, *hc_inject, *hc_mixed;
     void *hc_ws; /* MFMA path workspace (max_tokens >= QK_HC_MM_MIN) */
+    /* expert streaming (qmoe_stream_enable): routed experts in pinned host
+     * memory, s_slots HBM slots per layer */
+    int streamed, s_slots, s_prefetch;
+    qmoe_xcache *xc;
+    void **s_host;               /* per layer: the routed tensors, checkpoint layout */
+    void *s_pool;                /* per layer, per routed tensor: s_slots experts */
+    size_t s_tb[QH_T_COUNT];     /* per-expert bytes of a routed tensor (0: not routed) */
+    size_t s_hoff[QH_T_COUNT];   /* offset of a routed tensor in a layer's host copy */
+    size_t s_poff[QH_T_COUNT];   /* ... and in a layer's slot pool */
+    size_t s_host_layer, s_pool_layer, s_expert_bytes;
+    int32_t *s_seg;              /* pinned [1+3E]: the segment table, then its remap */
+    int32_t *s_ids;              /* [E] the call's experts */
+    int32_t *s_segtab;           /* device [1+3E]: segment table over slots */
+    hipStream_t s_copy;          /* prefetch copies */
+    hipEvent_t *s_ev_used, *s_ev_pf;
+    int *s_pf_pending;
+    uint32_t *s_freq;            /* [L, E] routed slots per expert */
+    uint32_t *s_trans;           /* [L, E, E] experts of one call -> experts of the next */
+    int32_t *s_prev;             /* [L, E+1]: count, then the previous call's experts */
+    uint8_t *s_pf_flag;          /* [L, E] brought in by prefetch, not used yet */
+    uint64_t s_bytes_in, s_prefetched, s_prefetch_hits;
 };
+
+static int is_routed(int t) { return t >= QH_T_GATE_Q && t <= QH_T_DOWN_B; }
 
 static void set_err(qmoe_err *err, const char *fmt, ...) {
     if (!err) return;
@@ -223,6 +246,42 @@ int qmoe_create(qmoe_ctx **out, const qmoe_config *cfg, qmoe_err *err) {
     return 0;
 }
 
+static void stream_free(qmoe_ctx *c) {
+    if (c->s_host) {
+        for (int l = 0; l < c->cfg.n_layers; l++)
+            if (c->s_host[l]) hipHostFree(c->s_host[l]);
+        free(c->s_host);
+    }
+    if (c->s_pool) hipFree(c->s_pool);
+    if (c->s_seg) hipHostFree(c->s_seg);
+    if (c->s_segtab) hipFree(c->s_segtab);
+    if (c->s_copy) hipStreamDestroy(c->s_copy);
+    for (int l = 0; l < c->cfg.n_layers; l++) {
+        if (c->s_ev_used && c->s_ev_used[l]) hipEventDestroy(c->s_ev_used[l]);
+        if (c->s_ev_pf && c->s_ev_pf[l]) hipEventDestroy(c->s_ev_pf[l]);
+    }
+    free(c->s_ev_used);
+    free(c->s_ev_pf);
+    free(c->s_pf_pending);
+    free(c->s_freq);
+    free(c->s_trans);
+    free(c->s_prev);
+    free(c->s_pf_flag);
+    free(c->s_ids);
+    qmoe_xcache_destroy(c->xc);
+    c->s_host = NULL;
+    c->s_pool = c->s_seg = NULL;
+    c->s_segtab = NULL;
+    c->s_copy = NULL;
+    c->s_ev_used = c->s_ev_pf = NULL;
+    c->s_pf_pending = NULL;
+    c->s_freq = c->s_trans = NULL;
+    c->s_prev = c->s_ids = NULL;
+    c->s_pf_flag = NULL;
+    c->xc = NULL;
+    c->streamed = 0;
+}
+
 void qmoe_destroy(qmoe_ctx *c) {
     if (!c) return;
     if (c->layers)
@@ -239,6 +298,7 @@ void qmoe_destroy(qmoe_ctx *c) {
             if (c->hc_mem[l]) hipFree(c->hc_mem[l]);
     if (c->hc_scratch) hipFree(c->hc_scratch);
     if (c->hc_ws) hipFree(c->hc_ws);
+    stream_free(c);
     free(c->hc_mem);
     free(c->hc_ready);
     free(c->layers);
@@ -261,33 +321,40 @@ static int check_layer_index(qmoe_ctx *c, int layer, qmoe_err *err) {
     return 0;
 }
 
+/* device address of tensor t of a layer: its slot in the layer allocation,
+ * or for a routed tensor of a streamed context the layer's slot pool */
+static char *dev_tensor(qmoe_ctx *c, int layer, int t) {
+    if (c->streamed && is_routed(t))
+        return (char *)c->s_pool + (size_t)layer * c->s_pool_layer + c->s_poff[t];
+    return (char *)c->layers[layer].mem + c->off[t];
+}
+
 static int ensure_layer_mem(qmoe_ctx *c, int layer, qmoe_err *err) {
     qmoe_layer_slot *L = &c->layers[layer];
     if (L->mem) return 0;
     if (hip_fail(err, (int)hipMalloc(&L->mem, c->layer_bytes), "hipMalloc(layer)")) return -1;
-    char *b = (char *)L->mem;
     qmoe_layer_weights *d = &L->dev;
-    d->router_w = (const uint16_t *)(b + c->off[QH_T_ROUTER_W]);
+    d->router_w = (const uint16_t *)dev_tensor(c, layer, QH_T_ROUTER_W);
     d->router_bias = NULL;
-    d->gate_q = (const uint32_t *)(b + c->off[QH_T_GATE_Q]);
-    d->gate_s = (const uint16_t *)(b + c->off[QH_T_GATE_S]);
-    d->gate_b = (const uint16_t *)(b + c->off[QH_T_GATE_B]);
-    d->up_q = (const uint32_t *)(b + c->off[QH_T_UP_Q]);
-    d->up_s = (const uint16_t *)(b + c->off[QH_T_UP_S]);
-    d->up_b = (const uint16_t *)(b + c->off[QH_T_UP_B]);
-    d->down_q = (const uint32_t *)(b + c->off[QH_T_DOWN_Q]);
-    d->down_s = (const uint16_t *)(b + c->off[QH_T_DOWN_S]);
-    d->down_b = (const uint16_t *)(b + c->off[QH_T_DOWN_B]);
-    d->sh_gate_q = (const uint32_t *)(b + c->off[QH_T_SH_GATE_Q]);
-    d->sh_gate_s = (const uint16_t *)(b + c->off[QH_T_SH_GATE_S]);
-    d->sh_gate_b = (const uint16_t *)(b + c->off[QH_T_SH_GATE_B]);
-    d->sh_up_q = (const uint32_t *)(b + c->off[QH_T_SH_UP_Q]);
-    d->sh_up_s = (const uint16_t *)(b + c->off[QH_T_SH_UP_S]);
-    d->sh_up_b = (const uint16_t *)(b + c->off[QH_T_SH_UP_B]);
-    d->sh_down_q = (const uint32_t *)(b + c->off[QH_T_SH_DOWN_Q]);
-    d->sh_down_s = (const uint16_t *)(b + c->off[QH_T_SH_DOWN_S]);
-    d->sh_down_b = (const uint16_t *)(b + c->off[QH_T_SH_DOWN_B]);
-    d->sh_gate_w = (const uint16_t *)(b + c->off[QH_T_SHGATE_W]);
+    d->gate_q = (const uint32_t *)dev_tensor(c, layer, QH_T_GATE_Q);
+    d->gate_s = (const uint16_t *)dev_tensor(c, layer, QH_T_GATE_S);
+    d->gate_b = (const uint16_t *)dev_tensor(c, layer, QH_T_GATE_B);
+    d->up_q = (const uint32_t *)dev_tensor(c, layer, QH_T_UP_Q);
+    d->up_s = (const uint16_t *)dev_tensor(c, layer, QH_T_UP_S);
+    d->up_b = (const uint16_t *)dev_tensor(c, layer, QH_T_UP_B);
+    d->down_q = (const uint32_t *)dev_tensor(c, layer, QH_T_DOWN_Q);
+    d->down_s = (const uint16_t *)dev_tensor(c, layer, QH_T_DOWN_S);
+    d->down_b = (const uint16_t *)dev_tensor(c, layer, QH_T_DOWN_B);
+    d->sh_gate_q = (const uint32_t *)dev_tensor(c, layer, QH_T_SH_GATE_Q);
+    d->sh_gate_s = (const uint16_t *)dev_tensor(c, layer, QH_T_SH_GATE_S);
+    d->sh_gate_b = (const uint16_t *)dev_tensor(c, layer, QH_T_SH_GATE_B);
+    d->sh_up_q = (const uint32_t *)dev_tensor(c, layer, QH_T_SH_UP_Q);
+    d->sh_up_s = (const uint16_t *)dev_tensor(c, layer, QH_T_SH_UP_S);
+    d->sh_up_b = (const uint16_t *)dev_tensor(c, layer, QH_T_SH_UP_B);
+    d->sh_down_q = (const uint32_t *)dev_tensor(c, layer, QH_T_SH_DOWN_Q);
+    d->sh_down_s = (const uint16_t *)dev_tensor(c, layer, QH_T_SH_DOWN_S);
+    d->sh_down_b = (const uint16_t *)dev_tensor(c, layer, QH_T_SH_DOWN_B);
+    d->sh_gate_w = (const uint16_t *)dev_tensor(c, layer, QH_T_SHGATE_W);
     d->norm_w = NULL;
     return 0;
 }
@@ -328,6 +395,23 @@ static const char *tensor_name(int t) {
     return names[t];
 }
 
+/* host copy of routed tensor t of a streamed layer (allocated on first use) */
+static char *host_tensor_store(qmoe_ctx *c, int layer, int t, qmoe_err *err) {
+    if (!c->s_host[layer] &&
+        hip_fail(err, (int)hipHostMalloc(&c->s_host[layer], c->s_host_layer, hipHostMallocDefault),
+                 "hipHostMalloc(expert store)"))
+        return NULL;
+    return (char *)c->s_host[layer] + c->s_hoff[t];
+}
+
+/* a layer's weights were replaced: forget its resident experts */
+static void stream_layer_written(qmoe_ctx *c, int layer) {
+    if (!c->streamed) return;
+    qmoe_xcache_clear(c->xc, layer);
+    memset(c->s_pf_flag + (size_t)layer * c->cfg.n_experts, 0, (size_t)c->cfg.n_experts);
+    c->s_pf_pending[layer] = 0;
+}
+
 int qmoe_upload_layer(qmoe_ctx *c, int layer, const qmoe_layer_weights *h, qmoe_err *err) {
     clear_err(err);
     if (check_layer_index(c, layer, err)) return -1;
@@ -351,10 +435,17 @@ int qmoe_upload_layer(qmoe_ctx *c, int layer, const qmoe_layer_weights *h, qmoe_
         if (!src) continue;
         size_t n, es;
         tensor_shape(&c->cfg, t, &n, &es);
+        if (c->streamed && is_routed(t)) {
+            char *dst = host_tensor_store(c, layer, t, err);
+            if (!dst) return -1;
+            memcpy(dst, src, n * es);
+            continue;
+        }
         if (hip_fail(err, (int)hipMemcpy(b + c->off[t], src, n * es, hipMemcpyHostToDevice),
                      "hipMemcpy(upload)"))
             return -1;
     }
+    stream_layer_written(c, layer);
     L->dev.router_bias = h->router_bias ? (const float *)(b + c->off[QH_T_ROUTER_BIAS]) : NULL;
     L->dev.norm_w = h->norm_w ? (const float *)(b + c->off[QH_T_NORM_W]) : NULL;
     L->ready = 1;
@@ -382,7 +473,8 @@ void qh_layer_begin(qmoe_ctx *c, int layer) {
     if (c->layers[layer].mem) c->layers[layer].ready = 0;
 }
 
-int qh_layer_slot(qmoe_ctx *c, int layer, int t, void **dst, size_t *bytes, qmoe_err *err) {
+int qh_layer_slot(qmoe_ctx *c, int layer, int t, void **dst, size_t *bytes, int *on_host,
+                  qmoe_err *err) {
     if (t < 0 || t >= QH_T_COUNT) {
         set_err(err, "tensor slot %d out of range", t);
         return -1;
@@ -391,22 +483,36 @@ int qh_layer_slot(qmoe_ctx *c, int layer, int t, void **dst, size_t *bytes, qmoe
     c->layers[layer].ready = 0;
     size_t n, es;
     tensor_shape(&c->cfg, t, &n, &es);
-    *dst = (char *)c->layers[layer].mem + c->off[t];
     *bytes = n * es;
+    *on_host = c->streamed && is_routed(t);
+    if (*on_host) {
+        *dst = host_tensor_store(c, layer, t, err);
+        return *dst ? 0 : -1;
+    }
+    *dst = (char *)c->layers[layer].mem + c->off[t];
     return 0;
 }
 
-int qh_fill_zero(void *dst, size_t bytes, qmoe_err *err) {
+int qh_fill_zero(void *dst, size_t bytes, int on_host, qmoe_err *err) {
+    if (on_host) {
+        memset(dst, 0, bytes);
+        return 0;
+    }
     return hip_fail(err, (int)hipMemset(dst, 0, bytes), "hipMemset(zero biases)");
 }
 
-int qh_copy_to_device(void *dst, const void *src, size_t bytes, qmoe_err *err) {
+int qh_copy_to_slot(void *dst, const void *src, size_t bytes, int on_host, qmoe_err *err) {
+    if (on_host) {
+        memcpy(dst, src, bytes);
+        return 0;
+    }
     return hip_fail(err, (int)hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "hipMemcpy(checkpoint)");
 }
 
 void qh_layer_end(qmoe_ctx *c, int layer, int has_bias, int has_norm) {
     qmoe_layer_slot *L = &c->layers[layer];
     char *b = (char *)L->mem;
+    stream_layer_written(c, layer);
     L->dev.router_bias = has_bias ? (const float *)(b + c->off[QH_T_ROUTER_BIAS]) : NULL;
     L->dev.norm_w = has_norm ? (const float *)(b + c->off[QH_T_NORM_W]) : NULL;
     L->ready = 1;
@@ -435,15 +541,40 @@ int qmoe_synth_layer(qmoe_ctx *c, int layer, uint64_t seed, int with_norm, const
         {QH_T_SH_DOWN_Q, QMOE_TAG_SH_DOWN_Q, 2, 0.0f},  {QH_T_SH_DOWN_S, QMOE_TAG_SH_DOWN_S, 0, 0.02f},
         {QH_T_SH_DOWN_B, QMOE_TAG_SH_DOWN_B, 0, 0.01f}, {QH_T_SHGATE_W, QMOE_TAG_SHGATE_W, 0, 0.02f},
     };
+    /* streamed: routed tensors are generated in a temporary buffer and
+     * copied to the host store */
+    void *tmp = NULL;
+    if (c->streamed) {
+        size_t big = 0;
+        for (int t = 0; t < QH_T_COUNT; t++) {
+            size_t n, es;
+            tensor_shape(&c->cfg, t, &n, &es);
+            if (is_routed(t) && n * es > big) big = n * es;
+        }
+        if (hip_fail(err, (int)hipMalloc(&tmp, big), "hipMalloc(synth staging)")) return -1;
+    }
     for (size_t i = 0; i < sizeof(spec) / sizeof(spec[0]); i++) {
         size_t n, es;
         tensor_shape(&c->cfg, spec[i].t, &n, &es);
         uint64_t key = qk_tensor_key(seed, (uint32_t)layer, (uint32_t)spec[i].tag);
-        if (hip_fail(err, qk_launch_synth(b + c->off[spec[i].t], n, spec[i].kind, key, 0,
-                                          spec[i].sd, NULL),
-                     "synth"))
+        const int host = c->streamed && is_routed(spec[i].t);
+        char *dst = host ? (char *)tmp : b + c->off[spec[i].t];
+        int rc = qk_launch_synth(dst, n, spec[i].kind, key, 0, spec[i].sd, NULL);
+        if (!rc && host) {
+            char *hd = host_tensor_store(c, layer, spec[i].t, err);
+            rc = hd ? (int)hipMemcpy(hd, tmp, n * es, hipMemcpyDeviceToHost) : -1;
+            if (!hd) {
+                hipFree(tmp);
+                return -1;
+            }
+        }
+        if (hip_fail(err, rc, "synth")) {
+            if (tmp) hipFree(tmp);
             return -1;
+        }
     }
+    if (tmp) hipFree(tmp);
+    stream_layer_written(c, layer);
     if (with_norm) {
         if (hip_fail(err, qk_launch_synth(b + c->off[QH_T_NORM_W], (size_t)c->cfg.hidden, 3, 0, 0,
                                           1.0f, NULL),
@@ -680,6 +811,11 @@ int qmoe_expert_gateup(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n
                        qmoe_err *err) {
     clear_err(err);
     if (check_call(c, layer, n, err) || check_dtype(x_dtype, err)) return -1;
+    if (c->streamed) {
+        set_err(err, "expert stage calls are not available with streamed experts "
+                     "(qmoe_layer_forward routes and stages them)");
+        return -1;
+    }
     if (n == 0) return 0;
     NEED(x, "x");
     NEED(perm, "perm");
@@ -695,6 +831,11 @@ int qmoe_expert_gateup_topk(qmoe_ctx *c, int layer, const void *x, int x_dtype,
                             float *h_out, void *stream, qmoe_err *err) {
     clear_err(err);
     if (check_call(c, layer, 1, err) || check_dtype(x_dtype, err)) return -1;
+    if (c->streamed) {
+        set_err(err, "expert stage calls are not available with streamed experts "
+                     "(qmoe_layer_forward routes and stages them)");
+        return -1;
+    }
     if (!qk_gateup_topk_supported(c->shape)) {
         set_err(err, "one-token gate/up with top-k needs hidden/32 a power of two >= 64 (hidden = %d)",
                 c->cfg.hidden);
@@ -719,6 +860,11 @@ int qmoe_expert_down(qmoe_ctx *c, int layer, const float *h, int n, const int32_
                      float *y_out, void *stream, qmoe_err *err) {
     clear_err(err);
     if (check_call(c, layer, n, err)) return -1;
+    if (c->streamed) {
+        set_err(err, "expert stage calls are not available with streamed experts "
+                     "(qmoe_layer_forward routes and stages them)");
+        return -1;
+    }
     if (n == 0) return 0;
     NEED(h, "h");
     NEED(segments, "segments");
@@ -761,9 +907,15 @@ int qmoe_combine(qmoe_ctx *c, const float *y, const int32_t *perm, const float *
 
 /* the layer on checked arguments; with hyper set the combine also applies
  * the hyper connection's inject update (out may then be NULL) */
+static int layer_forward_streamed(qmoe_ctx *c, int layer, const void *x, int xbf, int n,
+                                  float *out, int residual, float *hyper, const float *inject,
+                                  void *stream, qmoe_err *err);
+
 static int layer_forward(qmoe_ctx *c, int layer, const void *x, int xbf, int n, float *out,
                          int residual, float *hyper, const float *inject, void *stream,
                          qmoe_err *err) {
+    if (c->streamed)
+        return layer_forward_streamed(c, layer, x, xbf, n, out, residual, hyper, inject, stream, err);
     c->last_n = n;
     const qmoe_layer_weights *W = &c->layers[layer].dev;
     const qk_shape s = c->shape;
@@ -950,7 +1102,9 @@ int qh_hc_config(qmoe_ctx *c, int layer, int *hc, int *lowrank, int *d, qmoe_err
     return 0;
 }
 
-int qh_hc_slot(qmoe_ctx *c, int layer, int t, void **dst, size_t *bytes, qmoe_err *err) {
+int qh_hc_slot(qmoe_ctx *c, int layer, int t, void **dst, size_t *bytes, int *on_host,
+               qmoe_err *err) {
+    *on_host = 0;
     if (t < 0 || t >= QH_HC_COUNT) {
         set_err(err, "hc tensor slot %d out of range", t);
         return -1;
@@ -1119,6 +1273,349 @@ int qmoe_hc_layer_forward(qmoe_ctx *c, int layer, float *hyper, int n, float *mo
     NEED(hyper, "hyper");
     if (run_hc_mix(c, layer, hyper, n, c->hc_mixed, c->hc_inject, NULL, stream, err)) return -1;
     return layer_forward(c, layer, c->hc_mixed, 0, n, moe_out, 0, hyper, c->hc_inject, stream, err);
+}
+
+/* ------------------------------------------------------ expert streaming */
+
+int qmoe_stream_enable(qmoe_ctx *c, int slots, int policy, int prefetch, qmoe_err *err) {
+    clear_err(err);
+    if (!c) {
+        set_err(err, "ctx is NULL");
+        return -1;
+    }
+    const int E = c->cfg.n_experts, L = c->cfg.n_layers;
+    if (c->streamed) {
+        if (slots == c->s_slots && prefetch == c->s_prefetch) return 0;
+        set_err(err, "expert streaming already enabled with %d slots per layer", c->s_slots);
+        return -1;
+    }
+    for (int l = 0; l < L; l++)
+        if (c->layers[l].mem) {
+            set_err(err, "qmoe_stream_enable must precede every layer upload (layer %d is allocated)", l);
+            return -1;
+        }
+    const long long need = (long long)c->cfg.max_tokens * c->cfg.top_k < E
+                               ? (long long)c->cfg.max_tokens * c->cfg.top_k : E;
+    if (slots < need || slots > E) {
+        set_err(err, "slots_per_layer %d must be in [%lld, %d] (one call routes up to "
+                     "min(n_experts, max_tokens * top_k) experts)", slots, need, E);
+        return -1;
+    }
+    if (policy < QMOE_CACHE_LRU || policy > QMOE_CACHE_ADAPTIVE || prefetch < 0 || prefetch > E) {
+        set_err(err, "policy %d or prefetch %d out of range", policy, prefetch);
+        return -1;
+    }
+    /* layouts: resident tensors in the layer allocation, routed ones in the
+     * host copy (E experts) and the slot pool (slots experts) */
+    size_t o = 0, ho = 0, po = 0, eb = 0;
+    for (int t = 0; t < QH_T_COUNT; t++) {
+        size_t n, es;
+        tensor_shape(&c->cfg, t, &n, &es);
+        if (is_routed(t)) {
+            c->s_tb[t] = n * es / (size_t)E;
+            eb += c->s_tb[t];
+            c->s_hoff[t] = ho;
+            ho = align_up(ho + n * es);
+            c->s_poff[t] = po;
+            po = align_up(po + c->s_tb[t] * (size_t)slots);
+            c->off[t] = 0;
+        } else {
+            c->s_tb[t] = 0;
+            c->off[t] = o;
+            o = align_up(o + n * es);
+        }
+    }
+    c->s_host_layer = ho;
+    c->s_pool_layer = po;
+    c->s_expert_bytes = eb;
+    c->s_slots = slots;
+    c->s_prefetch = prefetch;
+    c->streamed = 1; /* stream_free resets it on failure */
+    int ok = hip_fail(err, (int)hipMalloc(&c->s_pool, po * (size_t)L), "hipMalloc(expert slots)") == 0 &&
+             hip_fail(err, (int)hipHostMalloc((void **)&c->s_seg, (size_t)(3 * E + 1) * 4,
+                                              hipHostMallocDefault), "hipHostMalloc(segments)") == 0 &&
+             hip_fail(err, (int)hipMalloc((void **)&c->s_segtab, (size_t)(3 * E + 1) * 4),
+                      "hipMalloc(segments)") == 0 &&
+             hip_fail(err, (int)hipStreamCreateWithFlags(&c->s_copy, hipStreamNonBlocking),
+                      "stream") == 0;
+    if (ok) {
+        c->s_host = (void **)calloc((size_t)L, sizeof(void *));
+        c->s_ev_used = (hipEvent_t *)calloc((size_t)L, sizeof(hipEvent_t));
+        c->s_ev_pf = (hipEvent_t *)calloc((size_t)L, sizeof(hipEvent_t));
+        c->s_pf_pending = (int *)calloc((size_t)L, sizeof(int));
+        c->s_freq = (uint32_t *)calloc((size_t)L * E, sizeof(uint32_t));
+        c->s_trans = (uint32_t *)calloc((size_t)L * E * E, sizeof(uint32_t));
+        c->s_prev = (int32_t *)calloc((size_t)L * (E + 1), sizeof(int32_t));
+        c->s_pf_flag = (uint8_t *)calloc((size_t)L * E, 1);
+        c->s_ids = (int32_t *)calloc((size_t)E, sizeof(int32_t));
+        ok = c->s_host && c->s_ev_used && c->s_ev_pf && c->s_pf_pending && c->s_freq && c->s_trans &&
+             c->s_prev && c->s_pf_flag && c->s_ids;
+        if (!ok) set_err(err, "out of host memory");
+    }
+    for (int l = 0; ok && l < L; l++)
+        ok = hip_fail(err, (int)hipEventCreateWithFlags(&c->s_ev_used[l], hipEventDisableTiming), "event") == 0 &&
+             hip_fail(err, (int)hipEventCreateWithFlags(&c->s_ev_pf[l], hipEventDisableTiming), "event") == 0;
+    if (ok && qmoe_xcache_create(&c->xc, L, E, slots, policy, eb, err)) ok = 0;
+    if (!ok) {
+        stream_free(c);
+        /* back to the resident layout */
+        size_t r = 0;
+        for (int t = 0; t < QH_T_COUNT; t++) {
+            size_t n, es;
+            tensor_shape(&c->cfg, t, &n, &es);
+            c->off[t] = r;
+            r = align_up(r + n * es);
+        }
+        c->layer_bytes = r;
+        return -1;
+    }
+    c->layer_bytes = o;
+    return 0;
+}
+
+int qmoe_stream_get_stats(qmoe_ctx *c, qmoe_stream_stats *out, qmoe_err *err) {
+    clear_err(err);
+    if (!c || !out) {
+        set_err(err, "%s is NULL", c ? "out" : "ctx");
+        return -1;
+    }
+    if (!c->streamed) {
+        set_err(err, "expert streaming not enabled");
+        return -1;
+    }
+    uint64_t k[4];
+    qmoe_xcache_counts(c->xc, k);
+    out->hits = k[0];
+    out->misses = k[1];
+    out->evictions = k[2];
+    out->rejected = k[3];
+    out->bytes_in = c->s_bytes_in;
+    out->prefetched = c->s_prefetched;
+    out->prefetch_hits = c->s_prefetch_hits;
+    return 0;
+}
+
+/* expert e of a layer from the host copy into slot `slot` of its pool */
+static int stream_copy_expert(qmoe_ctx *c, int layer, int e, int slot, hipStream_t st, qmoe_err *err) {
+    const char *h = (const char *)c->s_host[layer];
+    char *p = (char *)c->s_pool + (size_t)layer * c->s_pool_layer;
+    for (int t = QH_T_GATE_Q; t <= QH_T_DOWN_B; t++) {
+        const size_t tb = c->s_tb[t];
+        if (hip_fail(err, (int)hipMemcpyAsync(p + c->s_poff[t] + (size_t)slot * tb,
+                                              h + c->s_hoff[t] + (size_t)e * tb, tb,
+                                              hipMemcpyHostToDevice, st),
+                     "copy expert"))
+            return -1;
+    }
+    c->s_bytes_in += c->s_expert_bytes;
+    return 0;
+}
+
+/* prefetch requests of one layer (request(prefetch=True), streaming.py:360-398):
+ * experts not resident go into slots on the copy stream, after the
+ * compute stream's last use of that layer's slots */
+static int stream_prefetch(qmoe_ctx *c, int layer, const int32_t *ids, int cnt, qmoe_err *err) {
+    const int E = c->cfg.n_experts;
+    int issued = 0;
+    for (int i = 0; i < cnt; i++) {
+        const int e = ids[i];
+        if (qmoe_xcache_peek(c->xc, layer, e) >= 0) continue;
+        if (!issued &&
+            hip_fail(err, (int)hipStreamWaitEvent(c->s_copy, c->s_ev_used[layer], 0), "prefetch wait"))
+            return -1;
+        int ev;
+        const int slot = qmoe_xcache_put(c->xc, layer, e, 0, c->s_freq[(size_t)layer * E + e] >= 4, &ev);
+        if (slot < 0) continue;
+        if (ev >= 0) c->s_pf_flag[(size_t)layer * E + ev] = 0;
+        if (stream_copy_expert(c, layer, e, slot, c->s_copy, err)) return -1;
+        c->s_pf_flag[(size_t)layer * E + e] = 1;
+        c->s_prefetched++;
+        issued = 1;
+    }
+    if (issued) {
+        if (hip_fail(err, (int)hipEventRecord(c->s_ev_pf[layer], c->s_copy), "prefetch record")) return -1;
+        c->s_pf_pending[layer] = 1;
+    }
+    return 0;
+}
+
+/* the `cnt` largest of score[0..E) that are > 0, ties to the lower id */
+static int top_scores(const uint64_t *score, int E, int cnt, int32_t *out) {
+    int m = 0;
+    for (int e = 0; e < E; e++) {
+        if (!score[e]) continue;
+        int pos = m < cnt ? m : cnt;
+        while (pos > 0 && score[out[pos - 1]] < score[e]) pos--;
+        if (pos >= cnt) continue;
+        const int last = m < cnt ? m : cnt - 1;
+        for (int j = last; j > pos; j--) out[j] = out[j - 1];
+        out[pos] = e;
+        if (m < cnt) m++;
+    }
+    return m;
+}
+
+/* record_route and prefetch_predictions (streaming.py:400-435): count the
+ * experts after the previous call's experts of this layer and each
+ * expert's routed slots, mark the frequent ones hot (>= 4), then request
+ * the most likely experts of this layer (transitions from this call's
+ * experts, else frequency, plus twice the next layer's frequency) and the
+ * most frequent of the next layer.  Ties go to the lower expert id (the
+ * MLX runtime keeps first-seen order). */
+static int stream_after_route(qmoe_ctx *c, int layer, const int32_t *ids, const int32_t *counts,
+                              int U, qmoe_err *err) {
+    const int E = c->cfg.n_experts, L = c->cfg.n_layers;
+    uint32_t *freq = c->s_freq + (size_t)layer * E;
+    uint32_t *trans = c->s_trans + (size_t)layer * E * E;
+    int32_t *prev = c->s_prev + (size_t)layer * (E + 1);
+    for (int j = 0; j < prev[0]; j++)
+        for (int i = 0; i < U; i++) trans[(size_t)prev[1 + j] * E + ids[i]]++;
+    for (int i = 0; i < U; i++) freq[ids[i]] += (uint32_t)counts[i];
+    prev[0] = U;
+    for (int i = 0; i < U; i++) prev[1 + i] = ids[i];
+    for (int i = 0; i < U; i++) qmoe_xcache_mark_hot(c->xc, layer, ids[i], freq[ids[i]] >= 4);
+    if (!c->s_prefetch) return 0;
+    uint64_t *cand = (uint64_t *)calloc((size_t)E, sizeof(uint64_t));
+    int32_t *pick = (int32_t *)malloc((size_t)c->s_prefetch * sizeof(int32_t));
+    if (!cand || !pick) {
+        free(cand);
+        free(pick);
+        set_err(err, "out of host memory");
+        return -1;
+    }
+    int any = 0;
+    for (int i = 0; i < U; i++)
+        for (int e = 0; e < E; e++) {
+            cand[e] += trans[(size_t)ids[i] * E + e];
+            any |= trans[(size_t)ids[i] * E + e] != 0;
+        }
+    if (!any)
+        for (int e = 0; e < E; e++) cand[e] = freq[e];
+    const uint32_t *nfreq = layer + 1 < L ? c->s_freq + (size_t)(layer + 1) * E : NULL;
+    if (nfreq)
+        for (int e = 0; e < E; e++) cand[e] += 2ull * nfreq[e];
+    int m = top_scores(cand, E, c->s_prefetch, pick);
+    int rc = stream_prefetch(c, layer, pick, m, err);
+    if (!rc && nfreq) {
+        for (int e = 0; e < E; e++) cand[e] = nfreq[e];
+        m = top_scores(cand, E, c->s_prefetch, pick);
+        rc = stream_prefetch(c, layer + 1, pick, m, err);
+    }
+    free(cand);
+    free(pick);
+    return rc;
+}
+
+/* the layer with streamed experts: route and dispatch on the GPU, bring
+ * the routed experts into the layer's slots (one host round trip for the
+ * segment table), remap the segment table to slots, then the same expert
+ * kernels on the slot pool */
+static int layer_forward_streamed(qmoe_ctx *c, int layer, const void *x, int xbf, int n,
+                                  float *out, int residual, float *hyper, const float *inject,
+                                  void *stream, qmoe_err *err) {
+    c->last_n = n;
+    const qmoe_layer_weights *W = &c->layers[layer].dev;
+    const qk_shape s = c->shape;
+    qk_scratch *sc = &c->sc;
+    const int hc = hyper ? c->hc : 0, E = s.E;
+    hipStream_t st = (hipStream_t)stream;
+    int rc;
+    float *xn = W->norm_w ? sc->xn : NULL;
+    rc = qk_launch_router(W, s, x, xbf, n, sc->logits, xn, stream);
+    if (hip_fail(err, rc, "router")) return -1;
+    const void *xf = W->norm_w ? (const void *)sc->xn : x;
+    const int xf_bf = W->norm_w ? 0 : xbf;
+    if (n <= QK_SMALL_N && n * s.k <= QK_SMALL_NK) {
+        rc = qk_launch_topk_dispatch_small(s, n, sc->logits, NULL, sc->idx, sc->w, sc->sg,
+                                           n == 1 ? NULL : sc->offsets, sc->perm, sc->pos,
+                                           sc->segtab, 1, NULL, stream);
+        if (hip_fail(err, rc, "topk+dispatch")) return -1;
+    } else {
+        rc = qk_launch_topk(s, n, sc->logits, NULL, sc->idx, sc->w, sc->sg, stream);
+        if (hip_fail(err, rc, "topk")) return -1;
+        rc = qk_launch_dispatch(s, n, sc->idx, sc->offsets, sc->perm, sc->pos, sc->segtab, sc->bits,
+                                sc->wprefix, 1, NULL, stream);
+        if (hip_fail(err, rc, "dispatch")) return -1;
+    }
+    if (hip_fail(err, (int)hipMemcpyAsync(c->s_seg, sc->segtab, (size_t)(3 * E + 1) * 4,
+                                          hipMemcpyDeviceToHost, st), "segments to host") ||
+        hip_fail(err, (int)hipStreamSynchronize(st), "segments sync"))
+        return -1;
+    const int U = c->s_seg[0];
+    if (U < 0 || U > c->s_slots || U > E) {
+        set_err(err, "layer %d routed %d experts, more than its %d slots", layer, U, c->s_slots);
+        return -1;
+    }
+    if (c->s_pf_pending[layer]) {
+        if (hip_fail(err, (int)hipStreamWaitEvent(st, c->s_ev_pf[layer], 0), "prefetch join")) return -1;
+        c->s_pf_pending[layer] = 0;
+    }
+    int32_t *cnt = (int32_t *)malloc((size_t)(U > 0 ? U : 1) * sizeof(int32_t));
+    if (!cnt) {
+        set_err(err, "out of host memory");
+        return -1;
+    }
+    for (int i = 0; i < U; i++) {
+        const int e = c->s_seg[1 + 3 * i];
+        c->s_ids[i] = e;
+        cnt[i] = c->s_seg[3 + 3 * i];
+        if (e < 0 || e >= E) {
+            free(cnt);
+            set_err(err, "segment %d names expert %d", i, e);
+            return -1;
+        }
+        int slot = qmoe_xcache_get(c->xc, layer, e);
+        if (slot >= 0) {
+            uint8_t *f = &c->s_pf_flag[(size_t)layer * E + e];
+            if (*f) {
+                c->s_prefetch_hits++;
+                *f = 0;
+            }
+            qmoe_xcache_pin(c->xc, layer, e, 1);
+        } else {
+            int ev;
+            slot = qmoe_xcache_put(c->xc, layer, e, 1, c->s_freq[(size_t)layer * E + e] >= 4, &ev);
+            if (slot < 0) {
+                free(cnt);
+                set_err(err, "no slot for expert %d of layer %d", e, layer);
+                return -1;
+            }
+            if (ev >= 0) c->s_pf_flag[(size_t)layer * E + ev] = 0;
+            if (stream_copy_expert(c, layer, e, slot, st, err)) {
+                free(cnt);
+                return -1;
+            }
+        }
+        c->s_seg[1 + 3 * i] = slot;
+    }
+    for (int i = 0; i < U; i++) qmoe_xcache_pin(c->xc, layer, c->s_ids[i], 0);
+    if (hip_fail(err, (int)hipMemcpyAsync(c->s_segtab, c->s_seg, (size_t)(3 * U + 1) * 4,
+                                          hipMemcpyHostToDevice, st), "segments to device")) {
+        free(cnt);
+        return -1;
+    }
+    /* the expert kernels on the slot pool, segments over slots */
+    const int gu_mm = n >= 2 && mfma_usable(c, n, xf_bf ? 0 : 1);
+    rc = run_gateup(c, W, xf, xf_bf, n, sc->perm, c->s_segtab, 0, sc->h, stream, err);
+    if (!rc) {
+        if (!mfma_usable(c, n, 2) && qk_down_combine_lds(s, n) > 0) {
+            rc = hip_fail(err, qk_launch_down_combine(W, s, sc->h, n, c->s_segtab, sc->pos, sc->w,
+                                                      sc->sg, residual ? x : NULL, xbf, out, hyper,
+                                                      inject, hc, stream),
+                          "down+combine");
+        } else {
+            rc = run_down(c, W, sc->h, n, c->s_segtab, gu_mm, sc->y, stream, err);
+            if (!rc)
+                rc = hip_fail(err, qk_launch_combine(s, n, sc->y, sc->pos, sc->w, sc->sg,
+                                                     residual ? x : NULL, xbf, out, hyper, inject,
+                                                     hc, stream),
+                              "combine");
+        }
+    }
+    if (!rc) rc = hip_fail(err, (int)hipEventRecord(c->s_ev_used[layer], st), "layer record");
+    if (!rc) rc = stream_after_route(c, layer, c->s_ids, cnt, U, err);
+    free(cnt);
+    return rc;
 }
 
 int qmoe_moe_forward_host(qmoe_ctx *c, int layer, const float *x, int n, float *out,

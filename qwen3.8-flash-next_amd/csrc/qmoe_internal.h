@@ -71,13 +71,17 @@ int qh_ctx_config(qmoe_ctx *c, int layer, qmoe_config *out, qmoe_err *err);
 int qh_host_alloc(void **p, size_t bytes, qmoe_err *err);
 void qh_host_free(void *p);
 void qh_layer_begin(qmoe_ctx *c, int layer);
-int qh_layer_slot(qmoe_ctx *c, int layer, int t, void **dst, size_t *bytes, qmoe_err *err);
-int qh_fill_zero(void *dst, size_t bytes, qmoe_err *err);
-int qh_copy_to_device(void *dst, const void *src, size_t bytes, qmoe_err *err);
+/* *on_host: the slot is host memory (a routed expert tensor of a context
+ * with streamed experts) */
+int qh_layer_slot(qmoe_ctx *c, int layer, int t, void **dst, size_t *bytes, int *on_host,
+                  qmoe_err *err);
+int qh_fill_zero(void *dst, size_t bytes, int on_host, qmoe_err *err);
+int qh_copy_to_slot(void *dst, const void *src, size_t bytes, int on_host, qmoe_err *err);
 void qh_layer_end(qmoe_ctx *c, int layer, int has_bias, int has_norm);
 /* the same for the hyper-connection slots (after qmoe_hc_enable) */
 int qh_hc_config(qmoe_ctx *c, int layer, int *hc, int *lowrank, int *d, qmoe_err *err);
-int qh_hc_slot(qmoe_ctx *c, int layer, int t, void **dst, size_t *bytes, qmoe_err *err);
+int qh_hc_slot(qmoe_ctx *c, int layer, int t, void **dst, size_t *bytes, int *on_host,
+               qmoe_err *err);
 void qh_hc_begin(qmoe_ctx *c, int layer);
 void qh_hc_end(qmoe_ctx *c, int layer);
 

@@ -786,7 +786,8 @@ static int check_tensor(const st_entry *e, const st_want *w, qmoe_err *err) {
 
 /* where a table's tensors go: the MoE layer slots or the hyper-connection slots */
 typedef struct {
-    int (*slot)(qmoe_ctx *c, int layer, int t, void **dst, size_t *bytes, qmoe_err *err);
+    int (*slot)(qmoe_ctx *c, int layer, int t, void **dst, size_t *bytes, int *on_host,
+                qmoe_err *err);
     void (*begin)(qmoe_ctx *c, int layer);
     void (*end)(qmoe_ctx *c, int layer);
     const char *dense_what; /* message for q4 weights found without scales */
@@ -841,12 +842,13 @@ static int upload_table(qmoe_ctx *ctx, int layer, const qmoe_st *ix, const char 
     for (int i = 0; i < nw && rc == 0; i++) {
         void *dst;
         size_t bytes;
-        if (tg->slot(ctx, layer, want[i].slot, &dst, &bytes, err)) {
+        int on_host = 0;
+        if (tg->slot(ctx, layer, want[i].slot, &dst, &bytes, &on_host, err)) {
             rc = -1;
             break;
         }
         if (!found[i]) {
-            rc = qh_fill_zero(dst, bytes, err);
+            rc = qh_fill_zero(dst, bytes, on_host, err);
             continue;
         }
         const size_t fbytes = want[i].widen ? bytes / 2 : bytes;
@@ -868,10 +870,10 @@ static int upload_table(qmoe_ctx *ctx, int layer, const qmoe_st *ix, const char 
                     const uint32_t u = (uint32_t)src[e] << 16;
                     memcpy(&f[e], &u, 4);
                 }
-                if (rc == 0) rc = qh_copy_to_device((char *)dst + 2 * at, stage, 2 * len, err);
+                if (rc == 0) rc = qh_copy_to_slot((char *)dst + 2 * at, stage, 2 * len, on_host, err);
             } else {
                 rc = read_range(ix, found[i], at, stage, len, err);
-                if (rc == 0) rc = qh_copy_to_device((char *)dst + at, stage, len, err);
+                if (rc == 0) rc = qh_copy_to_slot((char *)dst + at, stage, len, on_host, err);
             }
         }
     }

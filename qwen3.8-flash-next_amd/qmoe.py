@@ -60,6 +60,14 @@ class QmoeHcWeights(ctypes.Structure):
     _fields_ = [(f, ctypes.c_void_p) for f in HC_FIELDS]
 
 
+class QmoeStreamStats(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_uint64) for f in ("hits", "misses", "evictions", "rejected",
+                                               "bytes_in", "prefetched", "prefetch_hits")]
+
+
+CACHE_LRU, CACHE_LFU, CACHE_ADAPTIVE = 0, 1, 2
+
+
 class QmoeError(RuntimeError):
     pass
 
@@ -116,6 +124,18 @@ SIGNATURES = {
     "qmoe_hc_mix": (_I, [_P, _I, _P, _I, _P, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_hc_inject": (_I, [_P, _P, _P, _I, _P, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_hc_layer_forward": (_I, [_P, _I, _P, _I, _P, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_stream_enable": (_I, [_P, _I, _I, _I, ctypes.POINTER(QmoeErr)]),
+    "qmoe_stream_get_stats": (_I, [_P, ctypes.POINTER(QmoeStreamStats), ctypes.POINTER(QmoeErr)]),
+    "qmoe_xcache_create": (_I, [ctypes.POINTER(_P), _I, _I, _I, _I, ctypes.c_uint64,
+                                ctypes.POINTER(QmoeErr)]),
+    "qmoe_xcache_destroy": (None, [_P]),
+    "qmoe_xcache_peek": (_I, [_P, _I, _I]),
+    "qmoe_xcache_get": (_I, [_P, _I, _I]),
+    "qmoe_xcache_put": (_I, [_P, _I, _I, _I, _I, ctypes.POINTER(_I)]),
+    "qmoe_xcache_pin": (_I, [_P, _I, _I, _I]),
+    "qmoe_xcache_mark_hot": (_I, [_P, _I, _I, _I]),
+    "qmoe_xcache_clear": (None, [_P, _I]),
+    "qmoe_xcache_counts": (None, [_P, ctypes.POINTER(ctypes.c_uint64 * 4)]),
 }
 
 
@@ -435,6 +455,19 @@ class MoeContext:
                err, "qmoe_last_routing")
         return r
 
+    # -- expert streaming
+    def stream_enable(self, slots_per_layer: int, policy: int = CACHE_ADAPTIVE, prefetch: int = 0):
+        err = QmoeErr()
+        _check(lib().qmoe_stream_enable(self._h, slots_per_layer, policy, prefetch,
+                                        ctypes.byref(err)), err, "qmoe_stream_enable")
+
+    def stream_stats(self) -> dict:
+        st = QmoeStreamStats()
+        err = QmoeErr()
+        _check(lib().qmoe_stream_get_stats(self._h, ctypes.byref(st), ctypes.byref(err)), err,
+               "qmoe_stream_get_stats")
+        return {f: getattr(st, f) for f, _ in QmoeStreamStats._fields_}
+
     # -- MLP hyper connection around the layer
     def hc_enable(self, hc_count: int, hc_lowrank: int):
         err = QmoeErr()
@@ -578,6 +611,53 @@ class Checkpoint:
         _check(lib().qmoe_st_read(self._h, name.encode(), buf, len(buf), ctypes.byref(err)), err,
                "qmoe_st_read")
         return buf.raw[:t.nbytes]
+
+
+class ExpertCache:
+    """the library's expert slot cache on its own (host only): partitions of
+    `slots` entries over items 0..items-1"""
+
+    def __init__(self, parts, items, slots, policy, entry_bytes):
+        self._h = ctypes.c_void_p()
+        err = QmoeErr()
+        _check(lib().qmoe_xcache_create(ctypes.byref(self._h), parts, items, slots, policy,
+                                        entry_bytes, ctypes.byref(err)), err, "qmoe_xcache_create")
+
+    def close(self):
+        if self._h:
+            lib().qmoe_xcache_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def peek(self, part, item):
+        return lib().qmoe_xcache_peek(self._h, part, item)
+
+    def get(self, part, item):
+        return lib().qmoe_xcache_get(self._h, part, item)
+
+    def put(self, part, item, pin=False, hot=False):
+        ev = ctypes.c_int(-1)
+        slot = lib().qmoe_xcache_put(self._h, part, item, int(pin), int(hot), ctypes.byref(ev))
+        return slot, ev.value
+
+    def pin(self, part, item, pinned):
+        return lib().qmoe_xcache_pin(self._h, part, item, int(pinned))
+
+    def mark_hot(self, part, item, hot):
+        return lib().qmoe_xcache_mark_hot(self._h, part, item, int(hot))
+
+    def clear(self, part):
+        lib().qmoe_xcache_clear(self._h, part)
+
+    def counts(self):
+        out = (ctypes.c_uint64 * 4)()
+        lib().qmoe_xcache_counts(self._h, ctypes.byref(out))
+        return dict(hits=out[0], misses=out[1], evictions=out[2], rejected=out[3])
 
 
 def synth_fill(t, kind: int, seed: int, layer: int, tag: int, start=0, stddev=1.0, stream=None):

@@ -1,0 +1,153 @@
+"""Expert streaming on the GPU (qmoe_stream_enable): routed experts in pinned
+host memory, a few HBM slots per layer, the reference's cache policy
+(c/src/cache.c) and route-transition prefetch (streaming.py:400-435).
+
+Bar: the streamed layer runs the same kernels on the same weights, so its
+outputs are bit-identical to the resident layer's on every call, whatever
+the cache did (misses, evictions, prefetches); routing is unchanged; the
+counters add up (every routed expert is a hit or a miss)."""
+import numpy as np
+import pytest
+
+from ckpt_util import write_moe_layer
+from conftest import load_oracle, load_pkg
+
+orc = load_oracle()
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def torch_dev(gpu):
+    import torch
+    return torch, gpu
+
+
+def _pair(pkg, H, E, k, I, L, max_tokens, slots, policy, prefetch, seed, zipf=0.0):
+    """a resident and a streamed context holding the same synthetic layers"""
+    res = pkg.MoeContext(H, E, k, I, n_layers=L, max_tokens=max_tokens)
+    stm = pkg.MoeContext(H, E, k, I, n_layers=L, max_tokens=max_tokens)
+    stm.stream_enable(slots, policy, prefetch)
+    for layer in range(L):
+        rb = orc.zipf_bias(E, zipf, 1.0, seed * 1000003 + layer) if zipf else None
+        res.synth_layer(layer, seed, router_bias=rb)
+        stm.synth_layer(layer, seed, router_bias=rb)
+    return res, stm
+
+
+def _run_sequence(torch, dev, res, stm, L, steps, n, H, bf16, seed):
+    routed = 0
+    for step in range(steps):
+        x = orc.gen_x(n, H, seed + step, bf16=bf16)
+        xt = (torch.from_numpy(x.view(np.int16)).to(dev).view(torch.bfloat16) if bf16
+              else torch.from_numpy(x).to(dev))
+        for layer in range(L):
+            a = res.layer_forward(layer, xt)
+            b = stm.layer_forward(layer, xt)
+            torch.cuda.synchronize()
+            ra, rb = res.last_routing(n), stm.last_routing(n)
+            assert np.array_equal(ra["idx"].cpu().numpy(), rb["idx"].cpu().numpy())
+            sa, sb = ra["segments"].cpu().numpy(), rb["segments"].cpu().numpy()
+            u = int(sa[0])  # entries past the count are not written by the call
+            assert np.array_equal(sa[:1 + 3 * u], sb[:1 + 3 * u])
+            routed += u
+            assert np.array_equal(a.cpu().numpy(), b.cpu().numpy()), (step, layer)
+    return routed
+
+
+@pytest.mark.parametrize("policy", [0, 1, 2])
+def test_tiny_streamed_bit_identical(torch_dev, policy):
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    say(f"case: tiny layers streamed, 4 slots of 8 experts, policy {policy}, prefetch 2")
+    res, stm = _pair(pkg, 256, 8, 2, 128, 3, 2, 4, policy, 2, seed=5)
+    routed = _run_sequence(torch, dev, res, stm, 3, 12, 2, 256, False, seed=40)
+    st = stm.stream_stats()
+    say(f"stats {st}")
+    assert st["hits"] + st["misses"] == routed
+    assert st["misses"] > 0 and st["evictions"] > 0 and st["rejected"] == 0
+    expert_bytes = 3 * (128 * 256 // 2 + 128 * (256 // 64) * 4)
+    assert st["bytes_in"] == (st["misses"] + st["prefetched"]) * expert_bytes
+    res.close()
+    stm.close()
+
+
+def test_decode_shape_streamed_with_prefetch(torch_dev):
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    say("case: decode-shape layers (E 512, top-10) streamed, 32 slots per layer, prefetch 16, Zipf routing")
+    res, stm = _pair(pkg, 2048, 512, 10, 512, 3, 1, 32, 2, 16, seed=3, zipf=1.1)
+    routed = _run_sequence(torch, dev, res, stm, 3, 10, 1, 2048, True, seed=90)
+    st = stm.stream_stats()
+    say(f"stats {st}")
+    assert st["hits"] + st["misses"] == routed
+    assert st["prefetched"] > 0 and st["hits"] > 0
+    assert st["bytes_in"] == (st["misses"] + st["prefetched"]) * 1769472
+    res.close()
+    stm.close()
+
+
+def test_batched_streamed_mfma_path(torch_dev):
+    """64 tokens route to up to 512 experts: every slot in use, segments
+    remapped to slots on the MFMA path"""
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    say("case: decode-shape layer, 64 tokens, 512 slots (MFMA path over remapped segments)")
+    res, stm = _pair(pkg, 2048, 512, 10, 512, 1, 64, 512, 0, 0, seed=8, zipf=1.1)
+    _run_sequence(torch, dev, res, stm, 1, 3, 64, 2048, True, seed=7)
+    res.close()
+    stm.close()
+
+
+def test_streamed_checkpoint_and_hyper(torch_dev, tmp_path):
+    """a streamed context loaded from a checkpoint, run inside the hyper
+    connection, equals the resident one"""
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    say("case: streamed tiny layer from a checkpoint, inside its hyper connection")
+    H, E, k, I = 256, 8, 2, 128
+    L = orc.Layer(H, E, k, I, seed=2)
+    write_moe_layer(str(tmp_path), L.arrays(), H, E, I, layer=0)
+    hp = orc.Hyper(4, H, 128, seed=2)
+    hyper = orc.gen_hyper(3, 4, H, seed=3)
+    outs = []
+    with pkg.Checkpoint(str(tmp_path)) as ck:
+        for streamed in (False, True):
+            with pkg.MoeContext(H, E, k, I, max_tokens=3) as ctx:
+                if streamed:
+                    ctx.stream_enable(6, 2, 0)
+                ctx.upload_layer_st(0, ck, 0)
+                ctx.hc_enable(4, 128)
+                ctx.hc_upload_layer(0, hp.arrays())
+                h = torch.from_numpy(hyper).to(dev)
+                for _ in range(3):
+                    ctx.hc_layer_forward(0, h, want_out=False)
+                torch.cuda.synchronize()
+                outs.append(h.cpu().numpy())
+    assert np.array_equal(outs[0], outs[1])
+
+
+def test_stream_errors(torch_dev):
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    say("case: expert streaming argument errors")
+    with pkg.MoeContext(256, 8, 2, 128, max_tokens=2) as ctx:
+        for slots, needle in ((3, "must be in [4, 8]"), (9, "must be in [4, 8]")):
+            with pytest.raises(pkg.QmoeError, match=needle.replace("[", r"\[").replace("]", r"\]")):
+                ctx.stream_enable(slots)
+        with pytest.raises(pkg.QmoeError, match="not enabled"):
+            ctx.stream_stats()
+        ctx.stream_enable(4)
+        ctx.stream_enable(4)  # same values: no-op
+        ctx.synth_layer(0, 1)
+        x = torch.zeros((1, 256), dtype=torch.float32, device=dev)
+        with pytest.raises(pkg.QmoeError, match="not available with streamed experts"):
+            ctx.expert_ffn(0, x, ctx.dispatch(ctx.router(0, x)["idx"]))
+    with pkg.MoeContext(256, 8, 2, 128, max_tokens=2) as ctx:
+        ctx.synth_layer(0, 1)
+        with pytest.raises(pkg.QmoeError, match="must precede every layer upload"):
+            ctx.stream_enable(4)
