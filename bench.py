@@ -177,6 +177,43 @@ def bench_hyper(pkg, torch, w, n_layers, steps, warmup):
     return sec / (reps * n_layers), reps * n_layers
 
 
+def bench_stream(pkg, torch, w, n_layers, slots, prefetch, steps, warmup):
+    """decode with streamed experts: every layer's routed experts in pinned
+    host memory, `slots` HBM expert slots per layer (ADAPTIVE policy,
+    route-transition prefetch); one token through all layers per step, run
+    eagerly (each layer call reads its segment table on the host).  Returns
+    seconds per layer call and the cache counters of the timed steps."""
+    ctx = pkg.MoeContext.for_workload(w, n_layers=n_layers, max_tokens=w.n_tokens)
+    ctx.stream_enable(slots, pkg.CACHE_ADAPTIVE, prefetch)
+    for layer in range(n_layers):
+        rb = None
+        if w.zipf_s > 0:
+            rb = zipf_bias_host(w.n_experts, w.zipf_s, w.zipf_scale, w.seed * 1000003 + layer)
+        ctx.synth_layer(layer, w.seed, router_bias=rb)
+    dt = torch.bfloat16 if w.x_bf16 else torch.float32
+    xs = []
+    for i in range(steps + warmup):
+        t = torch.empty((w.n_tokens, w.hidden), dtype=dt, device="cuda")
+        pkg.synth_fill(t, 0 if w.x_bf16 else 1, 5000 + i, 0, pkg.TAGS["X"], stddev=1.0)
+        xs.append(t)
+    out = torch.empty((w.n_tokens, w.hidden), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    for i in range(warmup):
+        for layer in range(n_layers):
+            ctx.layer_forward(layer, xs[i], out=out)
+    torch.cuda.synchronize()
+    s0 = ctx.stream_stats()
+    t0 = time.perf_counter()
+    for i in range(warmup, warmup + steps):
+        for layer in range(n_layers):
+            ctx.layer_forward(layer, xs[i], out=out)
+    torch.cuda.synchronize()
+    sec = time.perf_counter() - t0
+    s1 = ctx.stream_stats()
+    ctx.close()
+    return sec / (steps * n_layers), {k: s1[k] - s0[k] for k in s1}
+
+
 def bench_gateup(pkg, torch, st, reps_target=200):
     """dominant kernel of the one-token layer step: the launch that selects
     the top-k from the router logits and runs the grouped gate/up GEMV
@@ -286,6 +323,9 @@ def main():
     ap.add_argument("--hyper", default="decode,batched,prefill",
                     help="comma list of workloads also timed as hyper-connection layers "
                          f"(hc {HC_COUNT}, rank {HC_LOWRANK}; secondary results)")
+    ap.add_argument("--stream", default="16,64,16", metavar="LAYERS,SLOTS,PREFETCH",
+                    help="also time Zipf decode with streamed experts (pinned host store, SLOTS "
+                         "of 512 HBM expert slots per layer); empty: skip")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 8 plain copies of MIB MiB (counter calibration) and exit")
     args = ap.parse_args()
@@ -347,6 +387,21 @@ def main():
                                       tokens_per_step=we.n_tokens, layers_rotated=nl, steps=k_h,
                                       hc_count=HC_COUNT, hc_lowrank=HC_LOWRANK)
         log(f"{name}+hyper: {s_h * 1e3:.3f} ms/step -> {we.n_tokens / s_h:.0f} tokens/s")
+        torch.cuda.empty_cache()
+    if args.stream:
+        nl, slots, pf = (int(v) for v in args.stream.split(","))
+        we = pkg.Workload("decode-zipf", 2048, 512, 10, 512, 1, x_bf16=True, zipf_s=1.1)
+        s_s, cs = bench_stream(pkg, torch, we, nl, slots, pf, steps=24, warmup=4)
+        calls = cs["hits"] + cs["misses"]
+        extra["decode+streamed"] = dict(
+            tokens_per_s=1.0 / s_s, ms_per_layer_call=s_s * 1e3, layers=nl,
+            slots_per_layer=slots, prefetch=pf, hit_rate=cs["hits"] / max(1, calls),
+            host_to_hbm_bytes_per_layer_call=cs["bytes_in"] / (24 * nl),
+            prefetched=cs["prefetched"], prefetch_hits=cs["prefetch_hits"],
+            note="one token through one layer per call (tokens/s = layer calls/s), experts "
+                 "streamed from pinned host memory over PCIe, eager (host reads each segment table)")
+        log(f"decode+streamed: {s_s * 1e6:.1f} us per layer call, hit rate "
+            f"{cs['hits'] / max(1, calls):.3f}, {cs['bytes_in'] / (24 * nl) / 1e6:.2f} MB in per call")
         torch.cuda.empty_cache()
 
     cpu = None

@@ -1395,20 +1395,34 @@ int qmoe_stream_get_stats(qmoe_ctx *c, qmoe_stream_stats *out, qmoe_err *err) {
     return 0;
 }
 
-/* expert e of a layer from the host copy into slot `slot` of its pool */
-static int stream_copy_expert(qmoe_ctx *c, int layer, int e, int slot, hipStream_t st, qmoe_err *err) {
-    const char *h = (const char *)c->s_host[layer];
+/* batches of whole-expert copies from a layer's host copy into its slots
+ * (one k_expert_copy launch per batch) */
+static int xc_begin(qmoe_ctx *c, int layer, QkExpertCopy *a, qmoe_err *err) {
+    void *hd = NULL;
+    if (hip_fail(err, (int)hipHostGetDevicePointer(&hd, c->s_host[layer], 0), "host mapping"))
+        return -1;
     char *p = (char *)c->s_pool + (size_t)layer * c->s_pool_layer;
-    for (int t = QH_T_GATE_Q; t <= QH_T_DOWN_B; t++) {
-        const size_t tb = c->s_tb[t];
-        if (hip_fail(err, (int)hipMemcpyAsync(p + c->s_poff[t] + (size_t)slot * tb,
-                                              h + c->s_hoff[t] + (size_t)e * tb, tb,
-                                              hipMemcpyHostToDevice, st),
-                     "copy expert"))
-            return -1;
+    for (int t = QH_T_GATE_Q, i = 0; t <= QH_T_DOWN_B; t++, i++) {
+        a->src[i] = (const char *)hd + c->s_hoff[t];
+        a->dst[i] = p + c->s_poff[t];
+        a->tb[i] = c->s_tb[t];
     }
-    c->s_bytes_in += c->s_expert_bytes;
+    a->n = 0;
     return 0;
+}
+
+static int xc_flush(QkExpertCopy *a, hipStream_t st, qmoe_err *err) {
+    const int rc = qk_launch_expert_copy(a, st);
+    a->n = 0;
+    return hip_fail(err, rc, "expert copy");
+}
+
+static int xc_add(qmoe_ctx *c, QkExpertCopy *a, int e, int slot, hipStream_t st, qmoe_err *err) {
+    a->pair[a->n][0] = e;
+    a->pair[a->n][1] = slot;
+    a->n++;
+    c->s_bytes_in += c->s_expert_bytes;
+    return a->n == QK_XC_MAX ? xc_flush(a, st, err) : 0;
 }
 
 /* prefetch requests of one layer (request(prefetch=True), streaming.py:360-398):
@@ -1417,6 +1431,8 @@ static int stream_copy_expert(qmoe_ctx *c, int layer, int e, int slot, hipStream
 static int stream_prefetch(qmoe_ctx *c, int layer, const int32_t *ids, int cnt, qmoe_err *err) {
     const int E = c->cfg.n_experts;
     int issued = 0;
+    QkExpertCopy xc;
+    if (xc_begin(c, layer, &xc, err)) return -1;
     for (int i = 0; i < cnt; i++) {
         const int e = ids[i];
         if (qmoe_xcache_peek(c->xc, layer, e) >= 0) continue;
@@ -1427,11 +1443,12 @@ static int stream_prefetch(qmoe_ctx *c, int layer, const int32_t *ids, int cnt, 
         const int slot = qmoe_xcache_put(c->xc, layer, e, 0, c->s_freq[(size_t)layer * E + e] >= 4, &ev);
         if (slot < 0) continue;
         if (ev >= 0) c->s_pf_flag[(size_t)layer * E + ev] = 0;
-        if (stream_copy_expert(c, layer, e, slot, c->s_copy, err)) return -1;
+        if (xc_add(c, &xc, e, slot, c->s_copy, err)) return -1;
         c->s_pf_flag[(size_t)layer * E + e] = 1;
         c->s_prefetched++;
         issued = 1;
     }
+    if (issued && xc_flush(&xc, c->s_copy, err)) return -1;
     if (issued) {
         if (hip_fail(err, (int)hipEventRecord(c->s_ev_pf[layer], c->s_copy), "prefetch record")) return -1;
         c->s_pf_pending[layer] = 1;
@@ -1555,6 +1572,11 @@ static int layer_forward_streamed(qmoe_ctx *c, int layer, const void *x, int xbf
         set_err(err, "out of host memory");
         return -1;
     }
+    QkExpertCopy xc;
+    if (xc_begin(c, layer, &xc, err)) {
+        free(cnt);
+        return -1;
+    }
     for (int i = 0; i < U; i++) {
         const int e = c->s_seg[1 + 3 * i];
         c->s_ids[i] = e;
@@ -1581,12 +1603,16 @@ static int layer_forward_streamed(qmoe_ctx *c, int layer, const void *x, int xbf
                 return -1;
             }
             if (ev >= 0) c->s_pf_flag[(size_t)layer * E + ev] = 0;
-            if (stream_copy_expert(c, layer, e, slot, st, err)) {
+            if (xc_add(c, &xc, e, slot, st, err)) {
                 free(cnt);
                 return -1;
             }
         }
         c->s_seg[1 + 3 * i] = slot;
+    }
+    if (xc.n && xc_flush(&xc, st, err)) {
+        free(cnt);
+        return -1;
     }
     for (int i = 0; i < U; i++) qmoe_xcache_pin(c->xc, layer, c->s_ids[i], 0);
     if (hip_fail(err, (int)hipMemcpyAsync(c->s_segtab, c->s_seg, (size_t)(3 * U + 1) * 4,

@@ -200,6 +200,23 @@ int qk_launch_hc_mm(const float *hyper, const float *norm_w, const uint32_t *dq,
 int qk_launch_hc_inject(const float *inject, const float *out, int hc, int d, int n, float *hyper,
                         void *stream);
 
+/* copies of whole experts (the nine routed tensor pieces) from the
+ * pinned host store into HBM slots: pair[i] = (expert, slot), src/dst =
+ * each piece's base (host-mapped / device), tb = its bytes per expert (a
+ * multiple of 16) */
+#define QK_XC_PIECES 9
+#define QK_XC_MAX 64
+typedef struct {
+    const char *src[QK_XC_PIECES];
+    char *dst[QK_XC_PIECES];
+    size_t tb[QK_XC_PIECES];
+    int chunks[QK_XC_PIECES]; /* filled by the launcher */
+    int chunks_per_expert;
+    int n;
+    int32_t pair[QK_XC_MAX][2];
+} QkExpertCopy;
+int qk_launch_expert_copy(const QkExpertCopy *a, void *stream);
+
 /* synthetic streams: kind 0 bf16 normal, 1 f32 normal, 2 u32 codes, 3 f32 constant (stddev) */
 int qk_launch_synth(void *dst, size_t count, int kind, uint64_t key, uint64_t start, float stddev,
                     void *stream);
