@@ -180,9 +180,11 @@ def bench_hyper(pkg, torch, w, n_layers, steps, warmup):
 def bench_stream(pkg, torch, w, n_layers, slots, prefetch, steps, warmup):
     """decode with streamed experts: every layer's routed experts in pinned
     host memory, `slots` HBM expert slots per layer (ADAPTIVE policy,
-    route-transition prefetch); one token through all layers per step, run
-    eagerly (each layer call reads its segment table on the host).  Returns
-    seconds per layer call and the cache counters of the timed steps."""
+    route-transition prefetch); one token through all layers per step.
+    prefetch >= 0: run eagerly (each layer call reads its segment table on
+    the host); prefetch -1: residency resolved on the GPU, the timed steps
+    captured in one HIP graph and replayed once.  Returns seconds per layer
+    call and the cache counters of the timed steps."""
     ctx = pkg.MoeContext.for_workload(w, n_layers=n_layers, max_tokens=w.n_tokens)
     ctx.stream_enable(slots, pkg.CACHE_ADAPTIVE, prefetch)
     for layer in range(n_layers):
@@ -202,11 +204,26 @@ def bench_stream(pkg, torch, w, n_layers, slots, prefetch, steps, warmup):
         for layer in range(n_layers):
             ctx.layer_forward(layer, xs[i], out=out)
     torch.cuda.synchronize()
+
+    def timed_steps():
+        for i in range(warmup, warmup + steps):
+            for layer in range(n_layers):
+                ctx.layer_forward(layer, xs[i], out=out)
+
+    g = None
+    if prefetch < 0:
+        # captured without a run first (the warmup steps warmed the launch
+        # path), so the replay meets the cache the warmup left
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            timed_steps()
+        torch.cuda.synchronize()
     s0 = ctx.stream_stats()
     t0 = time.perf_counter()
-    for i in range(warmup, warmup + steps):
-        for layer in range(n_layers):
-            ctx.layer_forward(layer, xs[i], out=out)
+    if g is not None:
+        g.replay()
+    else:
+        timed_steps()
     torch.cuda.synchronize()
     sec = time.perf_counter() - t0
     s1 = ctx.stream_stats()
@@ -323,6 +340,9 @@ def main():
     ap.add_argument("--hyper", default="decode,batched,prefill",
                     help="comma list of workloads also timed as hyper-connection layers "
                          f"(hc {HC_COUNT}, rank {HC_LOWRANK}; secondary results)")
+    ap.add_argument("--stream-device", default="16,64", metavar="LAYERS,SLOTS",
+                    help="decode with streamed experts, residency resolved on the GPU, graph "
+                         "replay ('' to skip)")
     ap.add_argument("--stream", default="16,64,16", metavar="LAYERS,SLOTS,PREFETCH",
                     help="also time Zipf decode with streamed experts (pinned host store, SLOTS "
                          "of 512 HBM expert slots per layer); empty: skip")
@@ -401,6 +421,21 @@ def main():
             note="one token through one layer per call (tokens/s = layer calls/s), experts "
                  "streamed from pinned host memory over PCIe, eager (host reads each segment table)")
         log(f"decode+streamed: {s_s * 1e6:.1f} us per layer call, hit rate "
+            f"{cs['hits'] / max(1, calls):.3f}, {cs['bytes_in'] / (24 * nl) / 1e6:.2f} MB in per call")
+        torch.cuda.empty_cache()
+    if args.stream_device:
+        nl, slots = (int(v) for v in args.stream_device.split(","))
+        we = pkg.Workload("decode-zipf", 2048, 512, 10, 512, 1, x_bf16=True, zipf_s=1.1)
+        s_s, cs = bench_stream(pkg, torch, we, nl, slots, -1, steps=24, warmup=4)
+        calls = cs["hits"] + cs["misses"]
+        extra["decode+streamed-device"] = dict(
+            tokens_per_s=1.0 / s_s, ms_per_layer_call=s_s * 1e3, layers=nl,
+            slots_per_layer=slots, hit_rate=cs["hits"] / max(1, calls),
+            host_to_hbm_bytes_per_layer_call=cs["bytes_in"] / (24 * nl),
+            note="one token through one layer per call (tokens/s = layer calls/s), experts "
+                 "streamed from pinned host memory over PCIe, residency resolved on the GPU, "
+                 "no prefetch, timed steps replayed from one HIP graph")
+        log(f"decode+streamed-device: {s_s * 1e6:.1f} us per layer call, hit rate "
             f"{cs['hits'] / max(1, calls):.3f}, {cs['bytes_in'] / (24 * nl) / 1e6:.2f} MB in per call")
         torch.cuda.empty_cache()
 

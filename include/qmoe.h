@@ -358,7 +358,14 @@ enum { QMOE_CACHE_LRU = 0, QMOE_CACHE_LFU = 1, QMOE_CACHE_ADAPTIVE = 2 };
  * min(n_experts, max_tokens * top_k), and <= n_experts), the eviction
  * policy, and up to `prefetch` experts requested ahead per layer call (0 =
  * none).  Must precede every upload or synthesis.  In this mode the expert
- * stage functions (qmoe_expert_*) are refused: the layer call runs them. */
+ * stage functions (qmoe_expert_*) are refused: the layer call runs them.
+ * prefetch = -1 selects the device-resolved mode: the same residency
+ * decisions (hits, misses, victims) made by one GPU workgroup inside the
+ * layer call, which then copies the misses and runs the experts with no
+ * host round trip and no host synchronisation, so the call can be
+ * captured in a graph; it requests nothing ahead.  Calls of one context
+ * must then share one stream (the state of a layer is updated in stream
+ * order). */
 int qmoe_stream_enable(qmoe_ctx *ctx, int slots_per_layer, int policy, int prefetch,
                        qmoe_err *err);
 

@@ -180,44 +180,3 @@ extern "C" int qk_launch_synth(void *dst, size_t count, int kind, uint64_t key, 
                        count, kind, key, start, stddev);
     return QK_CHECK_LAUNCH();
 }
-
-/* ------------------------------------------------------ expert copies
- * Routed experts of a streamed context move from the pinned host store
- * into HBM slots with one launch per batch of experts: every workgroup
- * reads a 16 KiB chunk of one tensor piece of one expert over PCIe
- * (16-byte loads from the host mapping) and writes it to the slot.  One
- * launch replaces nine DMA copies per expert, whose fixed cost dominated
- * the 32 KiB scale and bias pieces. */
-
-#define XC_CHUNK 16384
-
-__global__ __launch_bounds__(256) void k_expert_copy(QkExpertCopy a) {
-    /* workgroup -> (pair, piece, chunk) */
-    int rest = blockIdx.x;
-    const int pair = rest / a.chunks_per_expert;
-    rest -= pair * a.chunks_per_expert;
-    int piece = 0;
-    while (piece < QK_XC_PIECES - 1 && rest >= a.chunks[piece]) {
-        rest -= a.chunks[piece];
-        piece++;
-    }
-    const size_t tb = a.tb[piece];
-    const uint4 *src = (const uint4 *)(a.src[piece] + (size_t)a.pair[pair][0] * tb);
-    uint4 *dst = (uint4 *)(a.dst[piece] + (size_t)a.pair[pair][1] * tb);
-    const size_t beg = (size_t)rest * (XC_CHUNK / 16), end = min(beg + XC_CHUNK / 16, tb / 16);
-    for (size_t i = beg + threadIdx.x; i < end; i += 256) dst[i] = src[i];
-}
-
-extern "C" int qk_launch_expert_copy(const QkExpertCopy *a, void *stream) {
-    if (a->n <= 0) return 0;
-    QkExpertCopy k = *a;
-    int per = 0;
-    for (int p = 0; p < QK_XC_PIECES; p++) {
-        if (k.tb[p] % 16) return (int)hipErrorInvalidValue;
-        k.chunks[p] = (int)((k.tb[p] + XC_CHUNK - 1) / XC_CHUNK);
-        per += k.chunks[p];
-    }
-    k.chunks_per_expert = per;
-    hipLaunchKernelGGL(k_expert_copy, dim3((unsigned)(per * k.n)), dim3(256), 0, (hipStream_t)stream, k);
-    return QK_CHECK_LAUNCH();
-}

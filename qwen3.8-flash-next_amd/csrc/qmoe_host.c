@@ -52,9 +52,10 @@ struct qmoe_ctx {
     void *hc_ws; /* MFMA path workspace (max_tokens >= QK_HC_MM_MIN) */
     /* expert streaming (qmoe_stream_enable): routed experts in pinned host
      * memory, s_slots HBM slots per layer */
-    int streamed, s_slots, s_prefetch;
+    int streamed, s_slots, s_prefetch, s_policy;
     qmoe_xcache *xc;
     void **s_host;               /* per layer: the routed tensors, checkpoint layout */
+    void **s_hdev;               /* ... and its device mapping, looked up on first use */
     void *s_pool;                /* per layer, per routed tensor: s_slots experts */
     size_t s_tb[QH_T_COUNT];     /* per-expert bytes of a routed tensor (0: not routed) */
     size_t s_hoff[QH_T_COUNT];   /* offset of a routed tensor in a layer's host copy */
@@ -71,6 +72,13 @@ struct qmoe_ctx {
     int32_t *s_prev;             /* [L, E+1]: count, then the previous call's experts */
     uint8_t *s_pf_flag;          /* [L, E] brought in by prefetch, not used yet */
     uint64_t s_bytes_in, s_prefetched, s_prefetch_hits;
+    /* device-resolved mode (prefetch -1): the slot cache of every layer in
+     * device memory, decided by k_stream_resolve inside the layer call */
+    int s_dev;
+    void *s_dstate;              /* per layer: where[E] item[S] | freq[S] touched[S] efreq[E] clock nused hot[S] */
+    size_t s_dlayer;             /* bytes of one layer's state */
+    int32_t *s_miss;             /* [1+2E] the call's misses */
+    unsigned long long *s_dstats; /* [5] hits, misses, evictions, rejected, copies */
 };
 
 static int is_routed(int t) { return t >= QH_T_GATE_Q && t <= QH_T_DOWN_B; }
@@ -255,11 +263,13 @@ static void stream_free(qmoe_ctx *c) {
     if (c->s_pool) hipFree(c->s_pool);
     if (c->s_seg) hipHostFree(c->s_seg);
     if (c->s_segtab) hipFree(c->s_segtab);
+    if (c->s_dstate) hipFree(c->s_dstate);
     if (c->s_copy) hipStreamDestroy(c->s_copy);
     for (int l = 0; l < c->cfg.n_layers; l++) {
         if (c->s_ev_used && c->s_ev_used[l]) hipEventDestroy(c->s_ev_used[l]);
         if (c->s_ev_pf && c->s_ev_pf[l]) hipEventDestroy(c->s_ev_pf[l]);
     }
+    free(c->s_hdev);
     free(c->s_ev_used);
     free(c->s_ev_pf);
     free(c->s_pf_pending);
@@ -269,9 +279,13 @@ static void stream_free(qmoe_ctx *c) {
     free(c->s_pf_flag);
     free(c->s_ids);
     qmoe_xcache_destroy(c->xc);
-    c->s_host = NULL;
+    c->s_host = c->s_hdev = NULL;
     c->s_pool = c->s_seg = NULL;
     c->s_segtab = NULL;
+    c->s_dstate = NULL;
+    c->s_miss = NULL;
+    c->s_dstats = NULL;
+    c->s_dev = 0;
     c->s_copy = NULL;
     c->s_ev_used = c->s_ev_pf = NULL;
     c->s_pf_pending = NULL;
@@ -405,8 +419,36 @@ static char *host_tensor_store(qmoe_ctx *c, int layer, int t, qmoe_err *err) {
 }
 
 /* a layer's weights were replaced: forget its resident experts */
+/* the device state of a layer back to empty: no resident expert, zero counts */
+static int dstate_reset(qmoe_ctx *c, int layer) {
+    const int E = c->cfg.n_experts, S = c->s_slots;
+    char *p = (char *)c->s_dstate + (size_t)layer * c->s_dlayer;
+    const size_t neg = (size_t)(E + S) * 4; /* where, item = -1 */
+    if (hipMemset(p, 0xFF, neg) != hipSuccess) return -1;
+    return hipMemset(p + neg, 0, c->s_dlayer - neg) == hipSuccess ? 0 : -1;
+}
+
+static void dstate_args(qmoe_ctx *c, int layer, QkStreamResolve *a) {
+    const int E = c->cfg.n_experts, S = c->s_slots;
+    char *p = (char *)c->s_dstate + (size_t)layer * c->s_dlayer;
+    a->where = (int32_t *)p;
+    a->item = a->where + E;
+    a->freq = (uint32_t *)(a->item + S);
+    a->touched = a->freq + S;
+    a->efreq = a->touched + S;
+    a->clock = a->efreq + E;
+    a->nused = (int32_t *)(a->clock + 1);
+    a->hot = (uint8_t *)(a->nused + 1);
+    a->miss = c->s_miss;
+    a->stats = c->s_dstats;
+    a->E = E;
+    a->slots = S;
+    a->policy = c->s_policy;
+}
+
 static void stream_layer_written(qmoe_ctx *c, int layer) {
     if (!c->streamed) return;
+    if (c->s_dev) (void)dstate_reset(c, layer); /* the upload's own later calls report a failed device */
     qmoe_xcache_clear(c->xc, layer);
     memset(c->s_pf_flag + (size_t)layer * c->cfg.n_experts, 0, (size_t)c->cfg.n_experts);
     c->s_pf_pending[layer] = 0;
@@ -1285,7 +1327,8 @@ int qmoe_stream_enable(qmoe_ctx *c, int slots, int policy, int prefetch, qmoe_er
     }
     const int E = c->cfg.n_experts, L = c->cfg.n_layers;
     if (c->streamed) {
-        if (slots == c->s_slots && prefetch == c->s_prefetch) return 0;
+        if (slots == c->s_slots && (prefetch < 0 ? c->s_dev : !c->s_dev && prefetch == c->s_prefetch))
+            return 0;
         set_err(err, "expert streaming already enabled with %d slots per layer", c->s_slots);
         return -1;
     }
@@ -1301,7 +1344,7 @@ int qmoe_stream_enable(qmoe_ctx *c, int slots, int policy, int prefetch, qmoe_er
                      "min(n_experts, max_tokens * top_k) experts)", slots, need, E);
         return -1;
     }
-    if (policy < QMOE_CACHE_LRU || policy > QMOE_CACHE_ADAPTIVE || prefetch < 0 || prefetch > E) {
+    if (policy < QMOE_CACHE_LRU || policy > QMOE_CACHE_ADAPTIVE || prefetch < -1 || prefetch > E) {
         set_err(err, "policy %d or prefetch %d out of range", policy, prefetch);
         return -1;
     }
@@ -1329,7 +1372,9 @@ int qmoe_stream_enable(qmoe_ctx *c, int slots, int policy, int prefetch, qmoe_er
     c->s_pool_layer = po;
     c->s_expert_bytes = eb;
     c->s_slots = slots;
-    c->s_prefetch = prefetch;
+    c->s_dev = prefetch < 0;
+    c->s_prefetch = prefetch < 0 ? 0 : prefetch;
+    c->s_policy = policy;
     c->streamed = 1; /* stream_free resets it on failure */
     int ok = hip_fail(err, (int)hipMalloc(&c->s_pool, po * (size_t)L), "hipMalloc(expert slots)") == 0 &&
              hip_fail(err, (int)hipHostMalloc((void **)&c->s_seg, (size_t)(3 * E + 1) * 4,
@@ -1340,6 +1385,7 @@ int qmoe_stream_enable(qmoe_ctx *c, int slots, int policy, int prefetch, qmoe_er
                       "stream") == 0;
     if (ok) {
         c->s_host = (void **)calloc((size_t)L, sizeof(void *));
+        c->s_hdev = (void **)calloc((size_t)L, sizeof(void *));
         c->s_ev_used = (hipEvent_t *)calloc((size_t)L, sizeof(hipEvent_t));
         c->s_ev_pf = (hipEvent_t *)calloc((size_t)L, sizeof(hipEvent_t));
         c->s_pf_pending = (int *)calloc((size_t)L, sizeof(int));
@@ -1348,7 +1394,7 @@ int qmoe_stream_enable(qmoe_ctx *c, int slots, int policy, int prefetch, qmoe_er
         c->s_prev = (int32_t *)calloc((size_t)L * (E + 1), sizeof(int32_t));
         c->s_pf_flag = (uint8_t *)calloc((size_t)L * E, 1);
         c->s_ids = (int32_t *)calloc((size_t)E, sizeof(int32_t));
-        ok = c->s_host && c->s_ev_used && c->s_ev_pf && c->s_pf_pending && c->s_freq && c->s_trans &&
+        ok = c->s_host && c->s_hdev && c->s_ev_used && c->s_ev_pf && c->s_pf_pending && c->s_freq && c->s_trans &&
              c->s_prev && c->s_pf_flag && c->s_ids;
         if (!ok) set_err(err, "out of host memory");
     }
@@ -1356,6 +1402,20 @@ int qmoe_stream_enable(qmoe_ctx *c, int slots, int policy, int prefetch, qmoe_er
         ok = hip_fail(err, (int)hipEventCreateWithFlags(&c->s_ev_used[l], hipEventDisableTiming), "event") == 0 &&
              hip_fail(err, (int)hipEventCreateWithFlags(&c->s_ev_pf[l], hipEventDisableTiming), "event") == 0;
     if (ok && qmoe_xcache_create(&c->xc, L, E, slots, policy, eb, err)) ok = 0;
+    if (ok && c->s_dev) {
+        /* where, item, freq, touched, efreq, clock, nused as 4-byte words, hot bytes */
+        c->s_dlayer = align_up((size_t)(2 * E + 3 * slots + 2) * 4 + (size_t)slots);
+        const size_t tail = (size_t)(1 + 2 * E) * 4;
+        ok = hip_fail(err, (int)hipMalloc(&c->s_dstate, c->s_dlayer * (size_t)L + align_up(tail) + 64),
+                      "hipMalloc(device cache state)") == 0;
+        if (ok) {
+            c->s_miss = (int32_t *)((char *)c->s_dstate + c->s_dlayer * (size_t)L);
+            c->s_dstats = (unsigned long long *)((char *)c->s_miss + align_up(tail));
+            ok = hip_fail(err, (int)hipMemset(c->s_miss, 0, align_up(tail) + 64), "clear state") == 0;
+            for (int l = 0; ok && l < L; l++)
+                if (dstate_reset(c, l)) ok = hip_fail(err, (int)hipErrorInvalidValue, "clear state") == 0;
+        }
+    }
     if (!ok) {
         stream_free(c);
         /* back to the resident layout */
@@ -1383,13 +1443,22 @@ int qmoe_stream_get_stats(qmoe_ctx *c, qmoe_stream_stats *out, qmoe_err *err) {
         set_err(err, "expert streaming not enabled");
         return -1;
     }
-    uint64_t k[4];
-    qmoe_xcache_counts(c->xc, k);
+    uint64_t k[5] = {0, 0, 0, 0, 0};
+    if (c->s_dev) {
+        unsigned long long d[5];
+        if (hip_fail(err, (int)hipMemcpy(d, c->s_dstats, sizeof(d), hipMemcpyDeviceToHost), "stats to host"))
+            return -1;
+        for (int i = 0; i < 5; i++) k[i] = d[i];
+        k[4] *= c->s_expert_bytes;
+    } else {
+        qmoe_xcache_counts(c->xc, k);
+        k[4] = c->s_bytes_in;
+    }
     out->hits = k[0];
     out->misses = k[1];
     out->evictions = k[2];
     out->rejected = k[3];
-    out->bytes_in = c->s_bytes_in;
+    out->bytes_in = k[4];
     out->prefetched = c->s_prefetched;
     out->prefetch_hits = c->s_prefetch_hits;
     return 0;
@@ -1398,9 +1467,10 @@ int qmoe_stream_get_stats(qmoe_ctx *c, qmoe_stream_stats *out, qmoe_err *err) {
 /* batches of whole-expert copies from a layer's host copy into its slots
  * (one k_expert_copy launch per batch) */
 static int xc_begin(qmoe_ctx *c, int layer, QkExpertCopy *a, qmoe_err *err) {
-    void *hd = NULL;
-    if (hip_fail(err, (int)hipHostGetDevicePointer(&hd, c->s_host[layer], 0), "host mapping"))
+    if (!c->s_hdev[layer] &&
+        hip_fail(err, (int)hipHostGetDevicePointer(&c->s_hdev[layer], c->s_host[layer], 0), "host mapping"))
         return -1;
+    const void *hd = c->s_hdev[layer];
     char *p = (char *)c->s_pool + (size_t)layer * c->s_pool_layer;
     for (int t = QH_T_GATE_Q, i = 0; t <= QH_T_DOWN_B; t++, i++) {
         a->src[i] = (const char *)hd + c->s_hoff[t];
@@ -1523,6 +1593,27 @@ static int stream_after_route(qmoe_ctx *c, int layer, const int32_t *ids, const 
     return rc;
 }
 
+/* the expert kernels on the slot pool, segments over slots (c->s_segtab) */
+static int streamed_experts(qmoe_ctx *c, const qmoe_layer_weights *W, const void *x, int xbf,
+                            const void *xf, int xf_bf, int n, float *out, int residual, float *hyper,
+                            const float *inject, int hc, void *stream, qmoe_err *err) {
+    const qk_shape s = c->shape;
+    qk_scratch *sc = &c->sc;
+    const int gu_mm = n >= 2 && mfma_usable(c, n, xf_bf ? 0 : 1);
+    int rc = run_gateup(c, W, xf, xf_bf, n, sc->perm, c->s_segtab, 0, sc->h, stream, err);
+    if (rc) return rc;
+    if (!mfma_usable(c, n, 2) && qk_down_combine_lds(s, n) > 0)
+        return hip_fail(err, qk_launch_down_combine(W, s, sc->h, n, c->s_segtab, sc->pos, sc->w, sc->sg,
+                                                    residual ? x : NULL, xbf, out, hyper, inject, hc,
+                                                    stream),
+                        "down+combine");
+    rc = run_down(c, W, sc->h, n, c->s_segtab, gu_mm, sc->y, stream, err);
+    if (rc) return rc;
+    return hip_fail(err, qk_launch_combine(s, n, sc->y, sc->pos, sc->w, sc->sg, residual ? x : NULL, xbf,
+                                           out, hyper, inject, hc, stream),
+                    "combine");
+}
+
 /* the layer with streamed experts: route and dispatch on the GPU, bring
  * the routed experts into the layer's slots (one host round trip for the
  * segment table), remap the segment table to slots, then the same expert
@@ -1553,6 +1644,21 @@ static int layer_forward_streamed(qmoe_ctx *c, int layer, const void *x, int xbf
         rc = qk_launch_dispatch(s, n, sc->idx, sc->offsets, sc->perm, sc->pos, sc->segtab, sc->bits,
                                 sc->wprefix, 1, NULL, stream);
         if (hip_fail(err, rc, "dispatch")) return -1;
+    }
+    if (c->s_dev) {
+        /* residency decided on the device: remap, then copy the misses, all
+         * on the call's stream with no host round trip */
+        QkStreamResolve r;
+        dstate_args(c, layer, &r);
+        r.segtab = sc->segtab;
+        r.out = c->s_segtab;
+        QkExpertCopy xd;
+        if (xc_begin(c, layer, &xd, err)) return -1;
+        const int max_pairs = n * s.k < E ? n * s.k : E;
+        if (hip_fail(err, qk_launch_stream_resolve(&r, stream), "stream resolve") ||
+            hip_fail(err, qk_launch_expert_copy_list(&xd, c->s_miss, max_pairs, stream), "expert copy"))
+            return -1;
+        return streamed_experts(c, W, x, xbf, xf, xf_bf, n, out, residual, hyper, inject, hc, stream, err);
     }
     if (hip_fail(err, (int)hipMemcpyAsync(c->s_seg, sc->segtab, (size_t)(3 * E + 1) * 4,
                                           hipMemcpyDeviceToHost, st), "segments to host") ||
@@ -1620,24 +1726,7 @@ static int layer_forward_streamed(qmoe_ctx *c, int layer, const void *x, int xbf
         free(cnt);
         return -1;
     }
-    /* the expert kernels on the slot pool, segments over slots */
-    const int gu_mm = n >= 2 && mfma_usable(c, n, xf_bf ? 0 : 1);
-    rc = run_gateup(c, W, xf, xf_bf, n, sc->perm, c->s_segtab, 0, sc->h, stream, err);
-    if (!rc) {
-        if (!mfma_usable(c, n, 2) && qk_down_combine_lds(s, n) > 0) {
-            rc = hip_fail(err, qk_launch_down_combine(W, s, sc->h, n, c->s_segtab, sc->pos, sc->w,
-                                                      sc->sg, residual ? x : NULL, xbf, out, hyper,
-                                                      inject, hc, stream),
-                          "down+combine");
-        } else {
-            rc = run_down(c, W, sc->h, n, c->s_segtab, gu_mm, sc->y, stream, err);
-            if (!rc)
-                rc = hip_fail(err, qk_launch_combine(s, n, sc->y, sc->pos, sc->w, sc->sg,
-                                                     residual ? x : NULL, xbf, out, hyper, inject,
-                                                     hc, stream),
-                              "combine");
-        }
-    }
+    rc = streamed_experts(c, W, x, xbf, xf, xf_bf, n, out, residual, hyper, inject, hc, stream, err);
     if (!rc) rc = hip_fail(err, (int)hipEventRecord(c->s_ev_used[layer], st), "layer record");
     if (!rc) rc = stream_after_route(c, layer, c->s_ids, cnt, U, err);
     free(cnt);

@@ -217,6 +217,29 @@ typedef struct {
 } QkExpertCopy;
 int qk_launch_expert_copy(const QkExpertCopy *a, void *stream);
 
+/* device-resolved residency of one layer (stream.hip): per layer state in
+ * device memory; out = the segment table over slots, miss = [count,
+ * (expert, slot)...] for qk_launch_expert_copy_list; stats = hits, misses,
+ * evictions, rejected, copies */
+typedef struct {
+    const int32_t *segtab;  /* [1+3E] expert segments */
+    int32_t *out;           /* [1+3E] slot segments */
+    int32_t *where;         /* [E] slot or -1 */
+    int32_t *item;          /* [S] expert or -1 */
+    uint32_t *freq, *touched; /* [S] */
+    uint8_t *hot;           /* [S] */
+    uint32_t *efreq;        /* [E] routed slots per expert */
+    uint32_t *clock;        /* [1] */
+    int32_t *nused;         /* [1] */
+    int32_t *miss;          /* [1+2E] */
+    unsigned long long *stats; /* [5] */
+    int E, slots, policy;
+} QkStreamResolve;
+int qk_launch_stream_resolve(const QkStreamResolve *a, void *stream);
+size_t qk_stream_resolve_lds(int E, int slots);
+int qk_launch_expert_copy_list(const QkExpertCopy *a, const int32_t *miss, int max_pairs,
+                               void *stream);
+
 /* synthetic streams: kind 0 bf16 normal, 1 f32 normal, 2 u32 codes, 3 f32 constant (stddev) */
 int qk_launch_synth(void *dst, size_t count, int kind, uint64_t key, uint64_t start, float stddev,
                     void *stream);

@@ -151,3 +151,77 @@ def test_stream_errors(torch_dev):
         ctx.synth_layer(0, 1)
         with pytest.raises(pkg.QmoeError, match="must precede every layer upload"):
             ctx.stream_enable(4)
+
+
+@pytest.mark.parametrize("policy", [0, 1, 2])
+def test_device_resolved_matches_host_policy(torch_dev, policy):
+    """prefetch -1: residency decided on the GPU.  Outputs bit-identical to
+    the resident layer, and the hit/miss/eviction counts equal the host
+    cache's (prefetch 0) on the same call sequence, which holds only if
+    every victim is the one the host policy picks"""
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    say(f"case: tiny layers, device-resolved vs host-resolved residency, policy {policy}")
+    res, dvc = _pair(pkg, 256, 8, 2, 128, 3, 2, 4, policy, -1, seed=5)
+    routed = _run_sequence(torch, dev, res, dvc, 3, 12, 2, 256, False, seed=40)
+    res.close()
+    res, hst = _pair(pkg, 256, 8, 2, 128, 3, 2, 4, policy, 0, seed=5)
+    _run_sequence(torch, dev, res, hst, 3, 12, 2, 256, False, seed=40)
+    a, b = dvc.stream_stats(), hst.stream_stats()
+    say(f"device {a} host {b}")
+    assert a["hits"] + a["misses"] == routed
+    for f in ("hits", "misses", "evictions", "rejected", "bytes_in"):
+        assert a[f] == b[f], f
+    assert a["evictions"] > 0 and a["prefetched"] == 0
+    for c in (res, dvc, hst):
+        c.close()
+
+
+def test_device_resolved_decode_zipf(torch_dev):
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    say("case: decode-shape layers (E 512, top-10), 16 slots, device-resolved, Zipf routing")
+    stats = []
+    for prefetch in (-1, 0):
+        res, stm = _pair(pkg, 2048, 512, 10, 512, 2, 1, 16, 2, prefetch, seed=3, zipf=1.1)
+        _run_sequence(torch, dev, res, stm, 2, 12, 1, 2048, True, seed=90)
+        stats.append(stm.stream_stats())
+        res.close()
+        stm.close()
+    say(f"device {stats[0]} host {stats[1]}")
+    for f in ("hits", "misses", "evictions", "rejected", "bytes_in"):
+        assert stats[0][f] == stats[1][f], f
+
+
+def test_device_resolved_graph_replay(torch_dev):
+    """the device-resolved layer call captured once and replayed: each
+    replay equals an eager resident call on the same input, while the
+    residency state keeps changing inside the graph"""
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    say("case: device-resolved streamed layer captured in a graph, 6 replays")
+    H, E, k, I, L = 256, 8, 2, 128, 2
+    res, stm = _pair(pkg, H, E, k, I, L, 2, 4, 2, -1, seed=6)
+    xs = [torch.from_numpy(orc.gen_x(2, H, 70 + i, bf16=False)).to(dev) for i in range(6)]
+    x = xs[0].clone()
+    outs = [torch.zeros((2, H), dtype=torch.float32, device=dev) for _ in range(L)]
+    for layer in range(L):  # warm the slots eagerly once
+        stm.layer_forward(layer, x, out=outs[layer])
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for layer in range(L):
+            stm.layer_forward(layer, x, out=outs[layer])
+    for i, xi in enumerate(xs):
+        x.copy_(xi)
+        g.replay()
+        torch.cuda.synchronize()
+        for layer in range(L):
+            want = res.layer_forward(layer, xi)
+            torch.cuda.synchronize()
+            assert np.array_equal(outs[layer].cpu().numpy(), want.cpu().numpy()), (i, layer)
+    st = stm.stream_stats()
+    say(f"stats {st}")
+    assert st["misses"] > 0 and st["rejected"] == 0
+    res.close()
+    stm.close()
