@@ -60,7 +60,7 @@ extern "C" int qk_launch_expert_copy(const QkExpertCopy *a, void *stream) {
  * (after a cold entry replaces a hot best the best score is 0, which no
  * later entry beats), with score 0 for LRU, freq for LFU and freq + 4*hot
  * for ADAPTIVE (the same order as (freq + 4*hot) / nbytes for one entry
- * size).  Two block-wide minima per eviction.  Slots are pinned for the
+ * size).  Two or three block-wide minima per eviction.  Slots are pinned for the
  * call, and after it each routed expert's frequency (routed slots so far)
  * marks it hot from 4 on, as the host path does. */
 
@@ -78,39 +78,50 @@ __device__ __forceinline__ uint64_t xr_block_min(uint64_t v, uint64_t *s_red) {
     return r;
 }
 
-__global__ __launch_bounds__(256) void k_stream_resolve(QkStreamResolve a) {
-    __shared__ uint64_t s_red[4];
+/* threads of the resolve workgroup (one wave measured slower: the slot
+ * scans grow and the serial walk stays) */
+#define SR_T 256
+
+__global__ __launch_bounds__(SR_T) void k_stream_resolve(QkStreamResolve a) {
+    __shared__ uint64_t s_red[SR_T / 64];
     __shared__ int s_slot, s_nused;
     __shared__ uint32_t s_clock;
     /* the layer's cache state lives in LDS for the call (one writer, thread
      * 0, and block-wide readers between barriers) */
     extern __shared__ uint32_t s_dyn[];
-    const int S = a.slots, E = a.E;
+    const int S = a.slots, E = a.E, UM = min(E, S);
     int32_t *where = (int32_t *)s_dyn;          /* [E] */
-    int32_t *item = where + E;                  /* [S] */
+    uint32_t *efreq = (uint32_t *)(where + E);  /* [E] */
+    int32_t *item = (int32_t *)(efreq + E);     /* [S] */
     uint32_t *freq = (uint32_t *)(item + S);    /* [S] */
     uint32_t *touched = freq + S;               /* [S] */
     uint32_t *hot = touched + S;                /* [S] */
-    uint32_t *pin = hot + S;                    /* [ceil(S/32)] */
+    int32_t *seg = (int32_t *)(hot + S);        /* [3 * min(E, S)] the call's segments */
+    uint32_t *pin = (uint32_t *)(seg + 3 * UM); /* [ceil(S/32)] */
     const int tid = threadIdx.x;
-    for (int i = tid; i < E; i += 256) where[i] = a.where[i];
-    for (int i = tid; i < S; i += 256) {
+    /* everything the walk reads comes into LDS in one round of loads */
+    const int U = min(max(a.segtab[0], 0), UM);
+    for (int i = tid; i < 3 * U; i += SR_T) seg[i] = a.segtab[1 + i];
+    for (int i = tid; i < E; i += SR_T) {
+        where[i] = a.where[i];
+        efreq[i] = a.efreq[i];
+    }
+    for (int i = tid; i < S; i += SR_T) {
         item[i] = a.item[i];
         freq[i] = a.freq[i];
         touched[i] = a.touched[i];
         hot[i] = a.hot[i];
     }
-    for (int i = tid; i < (S + 31) / 32; i += 256) pin[i] = 0u;
+    for (int i = tid; i < (S + 31) / 32; i += SR_T) pin[i] = 0u;
     if (tid == 0) {
         s_nused = a.nused[0];
         s_clock = a.clock[0];
     }
     __syncthreads();
-    const int U = min(max(a.segtab[0], 0), min(E, S));
     int nmiss = 0;
     unsigned long long st[5] = {0, 0, 0, 0, 0};
     for (int i = 0; i < U; i++) {
-        const int e = a.segtab[1 + 3 * i];
+        const int e = seg[3 * i];
         const int ok = e >= 0 && e < E; /* the dispatch writes ids in [0, E) */
         const int nu = s_nused;
         int slot = ok ? where[e] : -1;
@@ -130,7 +141,7 @@ __global__ __launch_bounds__(256) void k_stream_resolve(QkStreamResolve a) {
             } else {
                 /* the oldest unpinned entry and the oldest unpinned cold one */
                 uint64_t oldest = ~0ull, oldest_cold = ~0ull;
-                for (int s2 = tid; s2 < S; s2 += 256) {
+                for (int s2 = tid; s2 < S; s2 += SR_T) {
                     if (pin[s2 >> 5] & (1u << (s2 & 31))) continue;
                     const uint64_t k = ((uint64_t)touched[s2] << 32) | (uint32_t)s2;
                     oldest = k < oldest ? k : oldest;
@@ -147,7 +158,7 @@ __global__ __launch_bounds__(256) void k_stream_resolve(QkStreamResolve a) {
                         /* min (score, touched) over the unpinned entries of the oldest's temperature */
                         const uint32_t want_hot = oldest_cold == ~0ull ? 1u : 0u;
                         uint64_t best = ~0ull;
-                        for (int s2 = tid; s2 < S; s2 += 256) {
+                        for (int s2 = tid; s2 < S; s2 += SR_T) {
                             if (pin[s2 >> 5] & (1u << (s2 & 31))) continue;
                             if ((hot[s2] != 0u) != (want_hot != 0u)) continue;
                             uint64_t score = 0;
@@ -160,7 +171,7 @@ __global__ __launch_bounds__(256) void k_stream_resolve(QkStreamResolve a) {
                         best = xr_block_min(best, s_red);
                         if (tid == 0) s_slot = -1;
                         __syncthreads();
-                        for (int s2 = tid; s2 < S; s2 += 256)
+                        for (int s2 = tid; s2 < S; s2 += SR_T)
                             if (!(pin[s2 >> 5] & (1u << (s2 & 31))) &&
                                 touched[s2] == (uint32_t)(best & 0xFFFFFFFFu))
                                 s_slot = s2;
@@ -185,7 +196,7 @@ __global__ __launch_bounds__(256) void k_stream_resolve(QkStreamResolve a) {
                     where[e] = slot;
                     freq[slot] = 1u;
                     touched[slot] = ++s_clock;
-                    hot[slot] = a.efreq[e] >= 4u ? 1u : 0u;
+                    hot[slot] = efreq[e] >= 4u ? 1u : 0u;
                     pin[slot >> 5] |= 1u << (slot & 31);
                     a.miss[1 + 2 * nmiss] = e;
                     a.miss[2 + 2 * nmiss] = slot;
@@ -199,8 +210,8 @@ __global__ __launch_bounds__(256) void k_stream_resolve(QkStreamResolve a) {
         if (tid == 0) {
             /* an unresolved entry (not reached) still names a slot in the pool */
             a.out[1 + 3 * i] = slot >= 0 ? slot : 0;
-            a.out[2 + 3 * i] = a.segtab[2 + 3 * i];
-            a.out[3 + 3 * i] = a.segtab[3 + 3 * i];
+            a.out[2 + 3 * i] = seg[3 * i + 1];
+            a.out[3 + 3 * i] = seg[3 * i + 2];
         }
         __syncthreads();
     }
@@ -209,19 +220,22 @@ __global__ __launch_bounds__(256) void k_stream_resolve(QkStreamResolve a) {
         a.miss[0] = nmiss;
         /* routed slots per expert, then hot marks (record_route's bookkeeping) */
         for (int i = 0; i < U; i++) {
-            const int e = a.segtab[1 + 3 * i];
+            const int e = seg[3 * i];
             if (e < 0 || e >= E) continue;
-            a.efreq[e] += (uint32_t)max(a.segtab[3 + 3 * i], 0);
+            efreq[e] += (uint32_t)max(seg[3 * i + 2], 0);
             const int s2 = where[e];
-            if (s2 >= 0) hot[s2] = a.efreq[e] >= 4u ? 1u : 0u;
+            if (s2 >= 0) hot[s2] = efreq[e] >= 4u ? 1u : 0u;
         }
         a.nused[0] = s_nused;
         a.clock[0] = s_clock;
         for (int k = 0; k < 5; k++) a.stats[k] += st[k];
     }
     __syncthreads();
-    for (int i = tid; i < E; i += 256) a.where[i] = where[i];
-    for (int i = tid; i < S; i += 256) {
+    for (int i = tid; i < E; i += SR_T) {
+        a.where[i] = where[i];
+        a.efreq[i] = efreq[i];
+    }
+    for (int i = tid; i < S; i += SR_T) {
         a.item[i] = item[i];
         a.freq[i] = freq[i];
         a.touched[i] = touched[i];
@@ -230,12 +244,13 @@ __global__ __launch_bounds__(256) void k_stream_resolve(QkStreamResolve a) {
 }
 
 extern "C" size_t qk_stream_resolve_lds(int E, int slots) {
-    return (size_t)E * 4 + (size_t)slots * 16 + (size_t)((slots + 31) / 32) * 4;
+    return (size_t)E * 8 + (size_t)slots * 16 + (size_t)(E < slots ? E : slots) * 12 +
+           (size_t)((slots + 31) / 32) * 4;
 }
 
 extern "C" int qk_launch_stream_resolve(const QkStreamResolve *a, void *stream) {
     const size_t lds = qk_stream_resolve_lds(a->E, a->slots);
-    hipLaunchKernelGGL(k_stream_resolve, dim3(1), dim3(256), lds, (hipStream_t)stream, *a);
+    hipLaunchKernelGGL(k_stream_resolve, dim3(1), dim3(SR_T), lds, (hipStream_t)stream, *a);
     return QK_CHECK_LAUNCH();
 }
 
