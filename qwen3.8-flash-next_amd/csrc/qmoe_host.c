@@ -79,6 +79,7 @@ struct qmoe_ctx {
     size_t s_dlayer;             /* bytes of one layer's state */
     int32_t *s_miss;             /* [1+2E] the call's misses */
     unsigned long long *s_dstats; /* [5] hits, misses, evictions, rejected, copies */
+    int s_dstale;                /* 1 + a layer whose state could not be cleared, 0: none */
 };
 
 static int is_routed(int t) { return t >= QH_T_GATE_Q && t <= QH_T_DOWN_B; }
@@ -448,7 +449,7 @@ static void dstate_args(qmoe_ctx *c, int layer, QkStreamResolve *a) {
 
 static void stream_layer_written(qmoe_ctx *c, int layer) {
     if (!c->streamed) return;
-    if (c->s_dev) (void)dstate_reset(c, layer); /* the upload's own later calls report a failed device */
+    if (c->s_dev && dstate_reset(c, layer)) c->s_dstale = 1 + layer; /* refused by the layer call */
     qmoe_xcache_clear(c->xc, layer);
     memset(c->s_pf_flag + (size_t)layer * c->cfg.n_experts, 0, (size_t)c->cfg.n_experts);
     c->s_pf_pending[layer] = 0;
@@ -1648,6 +1649,10 @@ static int layer_forward_streamed(qmoe_ctx *c, int layer, const void *x, int xbf
     if (c->s_dev) {
         /* residency decided on the device: remap, then copy the misses, all
          * on the call's stream with no host round trip */
+        if (c->s_dstale) {
+            set_err(err, "the slot cache of layer %d could not be cleared after its upload", c->s_dstale - 1);
+            return -1;
+        }
         QkStreamResolve r;
         dstate_args(c, layer, &r);
         r.segtab = sc->segtab;
