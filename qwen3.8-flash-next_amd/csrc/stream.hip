@@ -120,7 +120,37 @@ __global__ __launch_bounds__(SR_T) void k_stream_resolve(QkStreamResolve a) {
     __syncthreads();
     int nmiss = 0;
     unsigned long long st[5] = {0, 0, 0, 0, 0};
-    for (int i = 0; i < U; i++) {
+    for (int start = 0;;) {
+        /* the run of hits before the next miss, in parallel: distinct
+         * experts hold distinct slots, and the run takes the next clock
+         * ticks in segment order */
+        uint64_t m = ~0ull;
+        for (int j = start + tid; j < U; j += SR_T) {
+            const int ej = seg[3 * j];
+            if (ej < 0 || ej >= E || where[ej] < 0) {
+                m = (uint64_t)j;
+                break;
+            }
+        }
+        m = xr_block_min(m, s_red);
+        const int first = m == ~0ull ? U : (int)m;
+        const uint32_t clk = s_clock;
+        for (int j = start + tid; j < first; j += SR_T) {
+            const int sj = where[seg[3 * j]];
+            freq[sj] += 1u;
+            touched[sj] = clk + 1u + (uint32_t)(j - start);
+            atomicOr(&pin[sj >> 5], 1u << (sj & 31));
+            a.out[1 + 3 * j] = sj;
+            a.out[2 + 3 * j] = seg[3 * j + 1];
+            a.out[3 + 3 * j] = seg[3 * j + 2];
+        }
+        if (tid == 0) st[0] += (unsigned long long)(first - start);
+        __syncthreads();
+        if (tid == 0) s_clock = clk + (uint32_t)(first - start);
+        if (first >= U) break;
+        /* entry `first` misses (or names no expert): decided alone */
+        const int i = first;
+        start = first + 1;
         const int e = seg[3 * i];
         const int ok = e >= 0 && e < E; /* the dispatch writes ids in [0, E) */
         const int nu = s_nused;
