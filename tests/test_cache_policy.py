@@ -111,3 +111,46 @@ def test_slots_stay_within_the_partition_and_are_reused():
     assert all(c.peek(0, i) == -1 for i in range(10)) and c.peek(1, 0) == 0
     with pytest.raises(pkg.QmoeError):
         pkg.ExpertCache(1, 4, 5, cr.LRU, 64)  # more slots than items
+
+
+def _closed_form_victim(entries, policy):
+    """the victim rule the device-resolved residency kernel evaluates with
+    block-wide minima instead of a recency walk: no unpinned cold entry ->
+    min (score, touched) over the hot; the oldest unpinned entry cold ->
+    min (score, touched) over the cold; else the oldest cold entry.  Score
+    0 (LRU), freq (LFU), freq + 4*hot (ADAPTIVE, one entry size)."""
+    un = [e for e in entries if not e.pinned]
+    if not un:
+        return None
+    oldest = min(un, key=lambda e: e.touched)
+    cold = [e for e in un if not e.hot]
+    if cold and oldest.hot:
+        return min(cold, key=lambda e: e.touched)
+    cand = cold if cold else un
+
+    def score(e):
+        return 0 if policy == cr.LRU else e.freq + (4 if policy == cr.ADAPTIVE and e.hot else 0)
+    return min(cand, key=lambda e: (score(e), e.touched))
+
+
+@pytest.mark.parametrize("policy", [cr.LRU, cr.LFU, cr.ADAPTIVE])
+def test_closed_form_victim_equals_recency_walk(policy):
+    """the closed form against pick_victim's walk (cache.c:99-163, restated
+    in the oracle) on random states: frequencies with many ties, hot and
+    pinned marks at random, distinct touch times"""
+    rng = random.Random(1234 + policy)
+    for trial in range(3000):
+        slots = rng.randint(1, 12)
+        c = cr.PartitionCache(slots, policy, 1769472)
+        touched = rng.sample(range(1, 10 * slots + 1), slots)
+        entries = []
+        for s, t in enumerate(touched):
+            e = cr.Entry(s, rng.random() < 0.3, rng.random() < 0.5, t)
+            e.freq = rng.randint(1, 6)
+            entries.append(e)
+        c.recency = sorted(entries, key=lambda e: -e.touched)  # most recent first
+        want = c.pick_victim()
+        got = _closed_form_victim(entries, policy)
+        assert (want is None) == (got is None), trial
+        if want is not None:
+            assert got.item == want.item, (trial, slots)
