@@ -26,13 +26,16 @@ struct CombineArgs {
 };
 
 /*
- * grid = (n, ceil(H/1024)); 256 threads x 4 columns.  For token t the k
+ * grid = (n, ceil(H/(1024*CB_HALVES))); 256 threads x 4 columns in each of
+ * CB_HALVES blocks of 1024 (two from 256 tokens on, one for small batches
+ * so that they still spread over the CUs).  For token t the k
  * slots are taken in ascending dispatch position, i.e. ascending expert id
  * (the expert loop order of model.c:1338), each as out = fma(w, y, out)
  * from out = 0, then out = fma(g, y_shared, out), then the optional residual.
  * With a hyper state, every copy j of token t becomes
  * fma(inject[t, j], out, hyper[t, j]) (model.c:1724-1731).
  */
+template <int CB_HALVES>
 __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
     __shared__ int s_pos[QK_MAX_TOPK];
     __shared__ float s_w[QK_MAX_TOPK];
@@ -57,61 +60,84 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs a) {
         }
     }
     __syncthreads();
-    const int c = (blockIdx.y * 256 + threadIdx.x) * 4;
-    if (c >= a.H) return;
+    /* a thread owns 4 columns in each of CB_HALVES blocks of 1024, so one
+     * workgroup's prologue (positions, ranks, barrier) serves 2048 columns
+     * and every thread has twice the row loads in flight */
+    const int cb = blockIdx.y * (1024 * CB_HALVES) + threadIdx.x * 4;
+    if (cb >= a.H) return;
+    bool live[CB_HALVES];
+#pragma unroll
+    for (int hh = 0; hh < CB_HALVES; hh++) live[hh] = cb + 1024 * hh < a.H;
     const float g = qk_ld(a.sg + t);
-    const float4 vs = qk_ld_stream((const float4 *)(a.y + ((size_t)a.n * a.k + t) * a.H + c));
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    /* issue eight independent row loads (clamped rows, no branches) before
-     * the dependent fma chain */
+    float4 acc[CB_HALVES], vs[CB_HALVES];
+#pragma unroll
+    for (int hh = 0; hh < CB_HALVES; hh++) {
+        acc[hh] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        vs[hh] = live[hh] ? qk_ld_stream((const float4 *)(a.y + ((size_t)a.n * a.k + t) * a.H + cb + 1024 * hh))
+                          : acc[hh];
+    }
+    /* issue the independent row loads (clamped rows, no branches on the
+     * row) before the dependent fma chains */
     for (int j0 = 0; j0 < a.k; j0 += 8) {
-        float4 v[8];
+        float4 v[CB_HALVES][8];
 #pragma unroll
         for (int jj = 0; jj < 8; jj++) {
             const int j = min(j0 + jj, a.k - 1);
             const int p = s_pos[j] < a.n * a.k ? s_pos[j] : 0;
-            v[jj] = qk_ld_stream((const float4 *)(a.y + (size_t)p * a.H + c));
+#pragma unroll
+            for (int hh = 0; hh < CB_HALVES; hh++)
+                if (live[hh]) v[hh][jj] = qk_ld_stream((const float4 *)(a.y + (size_t)p * a.H + cb + 1024 * hh));
         }
 #pragma unroll
         for (int jj = 0; jj < 8; jj++) {
             const int j = j0 + jj;
             if (j < a.k && s_pos[j] < a.n * a.k) {
                 const float wt = s_w[j];
-                acc.x = fmaf(wt, v[jj].x, acc.x);
-                acc.y = fmaf(wt, v[jj].y, acc.y);
-                acc.z = fmaf(wt, v[jj].z, acc.z);
-                acc.w = fmaf(wt, v[jj].w, acc.w);
+#pragma unroll
+                for (int hh = 0; hh < CB_HALVES; hh++) {
+                    if (!live[hh]) continue;
+                    acc[hh].x = fmaf(wt, v[hh][jj].x, acc[hh].x);
+                    acc[hh].y = fmaf(wt, v[hh][jj].y, acc[hh].y);
+                    acc[hh].z = fmaf(wt, v[hh][jj].z, acc[hh].z);
+                    acc[hh].w = fmaf(wt, v[hh][jj].w, acc[hh].w);
+                }
             }
         }
     }
-    acc.x = fmaf(g, vs.x, acc.x);
-    acc.y = fmaf(g, vs.y, acc.y);
-    acc.z = fmaf(g, vs.z, acc.z);
-    acc.w = fmaf(g, vs.w, acc.w);
-    if (a.xres) {
-        float4 xv;
-        if (a.xbf16) {
-            const uint2 d = *(const uint2 *)((const uint16_t *)a.xres + (size_t)t * a.H + c);
-            xv = make_float4(qk_bf16_lo(d.x), qk_bf16_hi(d.x), qk_bf16_lo(d.y), qk_bf16_hi(d.y));
-        } else {
-            xv = *(const float4 *)((const float *)a.xres + (size_t)t * a.H + c);
+#pragma unroll
+    for (int hh = 0; hh < CB_HALVES; hh++) {
+        if (!live[hh]) continue;
+        const int c = cb + 1024 * hh;
+        float4 r = acc[hh];
+        r.x = fmaf(g, vs[hh].x, r.x);
+        r.y = fmaf(g, vs[hh].y, r.y);
+        r.z = fmaf(g, vs[hh].z, r.z);
+        r.w = fmaf(g, vs[hh].w, r.w);
+        if (a.xres) {
+            float4 xv;
+            if (a.xbf16) {
+                const uint2 d = *(const uint2 *)((const uint16_t *)a.xres + (size_t)t * a.H + c);
+                xv = make_float4(qk_bf16_lo(d.x), qk_bf16_hi(d.x), qk_bf16_lo(d.y), qk_bf16_hi(d.y));
+            } else {
+                xv = *(const float4 *)((const float *)a.xres + (size_t)t * a.H + c);
+            }
+            r.x = xv.x + r.x;
+            r.y = xv.y + r.y;
+            r.z = xv.z + r.z;
+            r.w = xv.w + r.w;
         }
-        acc.x = xv.x + acc.x;
-        acc.y = xv.y + acc.y;
-        acc.z = xv.z + acc.z;
-        acc.w = xv.w + acc.w;
-    }
-    if (a.out) *(float4 *)(a.out + (size_t)t * a.H + c) = acc;
-    if (a.hyper) {
-        for (int j = 0; j < a.hc; j++) {
-            const float inj = qk_ld(a.inject + (size_t)t * a.hc + j);
-            float4 *hp = (float4 *)(a.hyper + ((size_t)t * a.hc + j) * a.H + c);
-            float4 hv = *hp;
-            hv.x = fmaf(inj, acc.x, hv.x);
-            hv.y = fmaf(inj, acc.y, hv.y);
-            hv.z = fmaf(inj, acc.z, hv.z);
-            hv.w = fmaf(inj, acc.w, hv.w);
-            *hp = hv;
+        if (a.out) *(float4 *)(a.out + (size_t)t * a.H + c) = r;
+        if (a.hyper) {
+            for (int j = 0; j < a.hc; j++) {
+                const float inj = qk_ld(a.inject + (size_t)t * a.hc + j);
+                float4 *hp = (float4 *)(a.hyper + ((size_t)t * a.hc + j) * a.H + c);
+                float4 hv = *hp;
+                hv.x = fmaf(inj, r.x, hv.x);
+                hv.y = fmaf(inj, r.y, hv.y);
+                hv.z = fmaf(inj, r.z, hv.z);
+                hv.w = fmaf(inj, r.w, hv.w);
+                *hp = hv;
+            }
         }
     }
 }
@@ -122,8 +148,13 @@ extern "C" int qk_launch_combine(qk_shape s, int n, const float *y, const int32_
                                  void *stream) {
     if (n <= 0) return 0;
     CombineArgs a{y, pos, w, sg, x_res, out, hyper, inject, s.H, s.k, n, x_bf16, hc};
-    dim3 grid(n, (s.H + 1023) / 1024);
-    hipLaunchKernelGGL(k_combine, grid, dim3(256), 0, (hipStream_t)stream, a);
+    if (n >= 256) {
+        dim3 grid(n, (s.H + 2047) / 2048);
+        hipLaunchKernelGGL(k_combine<2>, grid, dim3(256), 0, (hipStream_t)stream, a);
+    } else {
+        dim3 grid(n, (s.H + 1023) / 1024);
+        hipLaunchKernelGGL(k_combine<1>, grid, dim3(256), 0, (hipStream_t)stream, a);
+    }
     return QK_CHECK_LAUNCH();
 }
 
