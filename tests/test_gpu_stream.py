@@ -91,24 +91,26 @@ def test_decode_shape_streamed_with_prefetch(torch_dev):
     stm.close()
 
 
-def test_batched_streamed_mfma_path(torch_dev):
+@pytest.mark.parametrize("prefetch", [0, -1])
+def test_batched_streamed_mfma_path(torch_dev, prefetch):
     """64 tokens route to up to 512 experts: every slot in use, segments
-    remapped to slots on the MFMA path"""
+    remapped to slots on the MFMA path (host- and device-resolved)"""
     torch, dev = torch_dev
     pkg = load_pkg()
-    say("case: decode-shape layer, 64 tokens, 512 slots (MFMA path over remapped segments)")
-    res, stm = _pair(pkg, 2048, 512, 10, 512, 1, 64, 512, 0, 0, seed=8, zipf=1.1)
+    say(f"case: decode-shape layer, 64 tokens, 512 slots (MFMA path over remapped segments), prefetch {prefetch}")
+    res, stm = _pair(pkg, 2048, 512, 10, 512, 1, 64, 512, 0, prefetch, seed=8, zipf=1.1)
     _run_sequence(torch, dev, res, stm, 1, 3, 64, 2048, True, seed=7)
     res.close()
     stm.close()
 
 
-def test_streamed_checkpoint_and_hyper(torch_dev, tmp_path):
+@pytest.mark.parametrize("prefetch", [0, -1])
+def test_streamed_checkpoint_and_hyper(torch_dev, tmp_path, prefetch):
     """a streamed context loaded from a checkpoint, run inside the hyper
-    connection, equals the resident one"""
+    connection, equals the resident one (host- and device-resolved)"""
     torch, dev = torch_dev
     pkg = load_pkg()
-    say("case: streamed tiny layer from a checkpoint, inside its hyper connection")
+    say(f"case: streamed tiny layer from a checkpoint, inside its hyper connection, prefetch {prefetch}")
     H, E, k, I = 256, 8, 2, 128
     L = orc.Layer(H, E, k, I, seed=2)
     write_moe_layer(str(tmp_path), L.arrays(), H, E, I, layer=0)
@@ -119,7 +121,7 @@ def test_streamed_checkpoint_and_hyper(torch_dev, tmp_path):
         for streamed in (False, True):
             with pkg.MoeContext(H, E, k, I, max_tokens=3) as ctx:
                 if streamed:
-                    ctx.stream_enable(6, 2, 0)
+                    ctx.stream_enable(6, 2, prefetch)
                 ctx.upload_layer_st(0, ck, 0)
                 ctx.hc_enable(4, 128)
                 ctx.hc_upload_layer(0, hp.arrays())
