@@ -1349,6 +1349,11 @@ int qmoe_stream_enable(qmoe_ctx *c, int slots, int policy, int prefetch, qmoe_er
         set_err(err, "policy %d or prefetch %d out of range", policy, prefetch);
         return -1;
     }
+    if (prefetch < 0 && qk_stream_resolve_lds(E, slots) > 65536) {
+        set_err(err, "device-resolved streaming keeps a layer's slot cache in 64 KB of LDS: "
+                     "%d experts and %d slots need %zu bytes", E, slots, qk_stream_resolve_lds(E, slots));
+        return -1;
+    }
     /* layouts: resident tensors in the layer allocation, routed ones in the
      * host copy (E experts) and the slot pool (slots experts) */
     size_t o = 0, ho = 0, po = 0, eb = 0;

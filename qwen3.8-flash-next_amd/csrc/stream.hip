@@ -280,6 +280,7 @@ extern "C" size_t qk_stream_resolve_lds(int E, int slots) {
 
 extern "C" int qk_launch_stream_resolve(const QkStreamResolve *a, void *stream) {
     const size_t lds = qk_stream_resolve_lds(a->E, a->slots);
+    if (a->E <= 0 || a->slots <= 0 || lds > 65536) return (int)hipErrorInvalidValue; /* E = S = 512: 18.5 KB */
     hipLaunchKernelGGL(k_stream_resolve, dim3(1), dim3(SR_T), lds, (hipStream_t)stream, *a);
     return QK_CHECK_LAUNCH();
 }
