@@ -5,15 +5,20 @@ Default workload ("decode"): one bf16 token per step through one MoE layer
 (hidden 2048, 512 experts top-10 + a sigmoid-gated shared expert, SwiGLU
 intermediate 512, MLX affine 4-bit weights with group 64).  Consecutive
 steps use different tokens and rotate over --layers resident layers so the
-expert weights come from HBM, not from the 256 MB Infinity Cache.  Steps are
-captured in a HIP graph (one node per kernel) and replayed.
+expert weights come from HBM, not from the 256 MB Infinity Cache.  The
+--warmup steps run eagerly; the --steps timed steps are captured in one HIP
+graph (one node per kernel), uploaded, and replayed once between two
+synchronisations.
 
 Prints ONE JSON line: whole-job tokens/s, the roofline of the dominant
-kernel (measured with HIP events on the stream it runs on), and the CPU
-baseline (the oracle's C restatement of the reference C port, timed on this
-host's cores on a bounded sample).
+kernel (measured with HIP events on the stream it runs on), the other
+workloads (the tiny block, batched decode, prefill with its MFMA fraction,
+48-layer decode) and the CPU baseline (the oracle's C restatement of the
+reference C port, timed on this host's cores on bounded samples, in both
+weight modes: warm fp32 experts and q4-resident experts).
 """
 import argparse
+import ctypes
 import importlib.util
 import json
 import math
@@ -56,15 +61,40 @@ def expert_bytes(w):
         q4_matrix_bytes(w.hidden, w.moe_inter, w.group_size)
 
 
+def layer_token_bytes(w):
+    """algorithmic bytes of one token through one layer: top-k routed experts
+    + the shared expert, router [E,H] bf16, shared gate [H] bf16, the
+    token's row in and out (2 x H x 2 B), and the RMSNorm weight (H x 2 B)
+    when the layer has one: 21,573,632 B at hidden 2048 / 512 experts /
+    top-10 / intermediate 512, 21,577,728 B with the norm"""
+    return ((w.top_k + 1) * expert_bytes(w) + w.n_experts * w.hidden * 2 + w.hidden * 2 +
+            4 * w.hidden + (2 * w.hidden if w.rms_norm else 0))
+
+
+def step_bytes_batched(w, U):
+    """algorithmic bytes of one batched step with U distinct routed experts:
+    U x 1,769,472 + 4,395,008 B at 64 tokens of the decode shape (experts,
+    shared expert, router and gate weights, 2 x H x 2 B per token)"""
+    return (U + 1) * expert_bytes(w) + w.n_experts * w.hidden * 2 + w.hidden * 2 + \
+        w.n_tokens * 4 * w.hidden
+
+
+def prefill_flops(w):
+    """(grouped GEMM: routed + shared experts, router) flops of one prefill step"""
+    per_pair = 3 * 2 * w.hidden * w.moe_inter
+    gemm = w.n_tokens * (w.top_k + 1) * per_pair
+    router = w.n_tokens * 2 * w.hidden * w.n_experts
+    return gemm, router
+
+
 class Setup:
     """resident layers + per-step token batches for one workload"""
 
-    def __init__(self, pkg, torch, w, n_layers, n_steps, seed_base=1000):
+    def __init__(self, pkg, torch, w, n_layers, n_inputs, seed_base=1000, max_tokens=None):
         self.pkg, self.torch, self.w = pkg, torch, w
         self.L = n_layers
-        self.ctx = pkg.MoeContext.for_workload(w, n_layers=n_layers, max_tokens=w.n_tokens)
-        self.bias = []
-        sys.path.insert(0, ROOT)
+        self.ctx = pkg.MoeContext.for_workload(w, n_layers=n_layers,
+                                               max_tokens=max_tokens or w.n_tokens)
         for layer in range(n_layers):
             rb = None
             if w.zipf_s > 0:
@@ -73,12 +103,12 @@ class Setup:
         dt = torch.bfloat16 if w.x_bf16 else torch.float32
         kind = 0 if w.x_bf16 else 1
         self.x = []
-        for i in range(n_steps):
+        for i in range(n_inputs):
             t = torch.empty((w.n_tokens, w.hidden), dtype=dt, device="cuda")
             pkg.synth_fill(t, kind, seed_base + i, 0, pkg.TAGS["X"], stddev=1.0)
             self.x.append(t)
         self.out = [torch.empty((w.n_tokens, w.hidden), dtype=torch.float32, device="cuda")
-                    for _ in range(n_steps)]
+                    for _ in range(n_inputs)]
         torch.cuda.synchronize()
 
 
@@ -105,17 +135,37 @@ def zipf_bias_host(E, s, scale, seed):
     return (scale * np.log(p)).astype(np.float32)
 
 
-def capture(torch, fn):
+_HIP = None
+
+
+def hip():
+    global _HIP
+    if _HIP is None:
+        _HIP = ctypes.CDLL("libamdhip64.so")
+    return _HIP
+
+
+def capture(torch, fn, warm=True):
+    """fn's launches captured in one graph on a side stream; the graph is
+    uploaded to the device so its first replay carries no set-up cost"""
     g = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        fn()  # warm the launch path outside capture
-    torch.cuda.current_stream().wait_stream(s)
+    if warm:
+        with torch.cuda.stream(s):
+            fn()  # warm the launch path outside capture
+        torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):
         fn()
     torch.cuda.synchronize()
+    try:
+        rc = hip().hipGraphUpload(ctypes.c_void_p(g.raw_cuda_graph_exec()),
+                                  ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        if rc == 0:
+            torch.cuda.synchronize()
+    except (AttributeError, RuntimeError):
+        pass
     return g
 
 
@@ -130,21 +180,33 @@ def time_graph(torch, g, reps):
     return start.elapsed_time(end) / 1000.0  # seconds
 
 
-def bench_layer(pkg, torch, w, n_layers, steps, warmup):
-    """whole-layer steps: returns (seconds per step, setup)"""
-    S = n_layers
-    st = Setup(pkg, torch, w, n_layers, S)
+def bench_layer(pkg, torch, w, n_layers, steps, warmup, n_inputs=None):
+    """exactly `steps` timed whole-layer steps after `warmup` untimed eager
+    ones; step i runs layer i % n_layers on input batch i % n_inputs.
+    Returns (seconds per step, setup)."""
+    X = n_inputs or max(1, min(max(steps, warmup), 64))
+    st = Setup(pkg, torch, w, n_layers, X)
 
-    def run():
-        for i in range(S):
-            st.ctx.layer_forward(i % n_layers, st.x[i], out=st.out[i],
-                                 residual=w.rms_norm)
-    g = capture(torch, run)
-    reps_w = max(1, math.ceil(warmup / S))
-    time_graph(torch, g, reps_w)
-    reps = max(1, math.ceil(steps / S))
-    sec = time_graph(torch, g, reps)
-    return sec / (reps * S), reps * S, reps_w * S, st
+    def run(first, count):
+        for i in range(first, first + count):
+            st.ctx.layer_forward(i % n_layers, st.x[i % X], out=st.out[i % X], residual=w.rms_norm)
+
+    run(0, warmup)
+    torch.cuda.synchronize()
+    g = capture(torch, lambda: run(warmup, steps), warm=warmup == 0)
+    sec = time_graph(torch, g, 1)
+    return sec / steps, st
+
+
+def distinct_experts(st, steps):
+    """U (distinct routed experts) of each step, from an eager pass"""
+    us = []
+    torch = st.torch
+    for i in range(min(steps, len(st.x))):
+        st.ctx.layer_forward(i % st.L, st.x[i], out=st.out[i], residual=st.w.rms_norm)
+        torch.cuda.synchronize()
+        us.append(int(st.ctx.last_routing(st.w.n_tokens)["segments"][0].item()))
+    return us
 
 
 HC_COUNT, HC_LOWRANK = 4, 320  # the model's hyper connection (text_config hc_count, hc_lowrank)
@@ -240,13 +302,14 @@ def bench_gateup(pkg, torch, st, reps_target=200):
     over the launches)"""
     w, ctx = st.w, st.ctx
     S = st.L
+    X = len(st.x)
     logits, outs = [], []
     for i in range(S):
-        r = ctx.router(i % st.L, st.x[i], want_logits=True)
+        r = ctx.router(i, st.x[i % X], want_logits=True)
         # [E+1]: the router logits, then a shared-gate logit (its value does
         # not change the work)
         logits.append(torch.cat([r["logits"][0], torch.zeros(1, device="cuda")]).contiguous())
-        outs.append(ctx.expert_gateup_topk(i % st.L, st.x[i], logits[-1]))
+        outs.append(ctx.expert_gateup_topk(i, st.x[i % X], logits[-1]))
     torch.cuda.synchronize()
     mb = q4_matrix_bytes(w.moe_inter, w.hidden, w.group_size)
     xbytes = w.hidden * (2 if w.x_bf16 else 4)
@@ -259,7 +322,7 @@ def bench_gateup(pkg, torch, st, reps_target=200):
     def run_raw():
         stream = torch.cuda.current_stream().cuda_stream
         for i in range(S):
-            ctx.expert_gateup_topk_raw(i % st.L, st.x[i], logits[i], outs[i], stream)
+            ctx.expert_gateup_topk_raw(i, st.x[i % X], logits[i], outs[i], stream)
     g = capture(torch, run_raw)
     time_graph(torch, g, 2)
     reps = max(1, math.ceil(reps_target / S))
@@ -267,31 +330,190 @@ def bench_gateup(pkg, torch, st, reps_target=200):
     return sec / (reps * S), sum(algo) / len(algo)
 
 
-def cpu_baseline(w, budget_s=12.0):
-    """the oracle (C restatement of the reference C port's CPU path, q4
-    weights resident, gemm_q4 for every expert) timed on this host"""
+def bench_prefill_stages(pkg, torch, st, reps=6):
+    """the grouped expert GEMMs of the prefill layer, timed alone: the
+    gate/up stage (activation packing + MFMA gate/up) and the down stage
+    (MFMA down) of qmoe_expert_gateup / qmoe_expert_down on each resident
+    layer's own routing; returns seconds per launch of each stage"""
+    w, ctx = st.w, st.ctx
+    n = w.n_tokens
+    ds, hs, ys = [], [], []
+    for layer in range(st.L):
+        ctx.layer_forward(layer, st.x[layer], out=st.out[layer])
+        torch.cuda.synchronize()
+        r = ctx.last_routing(n)
+        ds.append(dict(perm=r["perm"].clone(), segments=r["segments"].clone()))
+        hs.append(torch.empty((n * w.top_k + n, w.moe_inter), dtype=torch.float32, device="cuda"))
+    ys = torch.empty((n * w.top_k + n, w.hidden), dtype=torch.float32, device="cuda")
+    for layer in range(st.L):
+        ctx.expert_gateup(layer, st.x[layer], ds[layer], out=hs[layer])
+    torch.cuda.synchronize()
+
+    def gu():
+        for layer in range(st.L):
+            ctx.expert_gateup(layer, st.x[layer], ds[layer], out=hs[layer])
+
+    def dn():
+        for layer in range(st.L):
+            ctx.expert_down(layer, hs[layer], n, ds[layer], out=ys)
+    res = []
+    for fn in (gu, dn):
+        g = capture(torch, fn)
+        time_graph(torch, g, 1)
+        res.append(time_graph(torch, g, reps) / (reps * st.L))
+    return res
+
+
+def bench_depth(pkg, torch, w, tokens, warmup):
+    """48 stacked layers, one token: h <- h + MoE(RMSNorm(h)) layer after
+    layer (f32 residual stream), captured as one graph per token; returns
+    seconds per token"""
+    L = w.n_layers
+    ctx = pkg.MoeContext.for_workload(w, n_layers=L, max_tokens=1)
+    for layer in range(L):
+        rb = zipf_bias_host(w.n_experts, w.zipf_s, w.zipf_scale, w.seed * 1000003 + layer)
+        ctx.synth_layer(layer, w.seed, with_norm=True, router_bias=rb)
+    xs = []
+    for i in range(tokens + warmup):
+        t = torch.empty((1, w.hidden), dtype=torch.float32, device="cuda")
+        pkg.synth_fill(t, 1, 7000 + i, 0, pkg.TAGS["X"], stddev=1.0)
+        xs.append(t)
+    h = [torch.empty((1, w.hidden), dtype=torch.float32, device="cuda") for _ in range(2)]
+    torch.cuda.synchronize()
+
+    def token(x):
+        src = x
+        for layer in range(L):
+            dst = h[layer & 1]
+            ctx.layer_forward(layer, src, out=dst, residual=True)
+            src = dst
+
+    for i in range(warmup):
+        token(xs[i])
+    torch.cuda.synchronize()
+    g = capture(torch, lambda: [token(xs[i]) for i in range(warmup, warmup + tokens)],
+                warm=warmup == 0)
+    sec = time_graph(torch, g, 1)
+    ctx.close()
+    return sec / tokens
+
+
+# ------------------------------------------------------------ CPU baseline
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _timed(fn, budget_s, max_iters=10, warm=3):
+    """median of up to max_iters runs after up to `warm` warm-ups, fitted to
+    a time budget (at least 1 run)"""
+    one = fn(0, 1)
+    iters = max(1, min(max_iters, int(budget_s / max(one, 1e-6))))
+    wu = min(warm, max(0, iters - 1))
+    return fn(wu, iters), iters, wu
+
+
+def cpu_baselines(pkg, names, threads, budget_s):
+    """The oracle (the C restatement of the reference C port's path) on
+    this host's cores, per workload, in both weight modes: (i) warm fp32
+    experts (the steady state of the C port's expert cache, gemm_fp32 on
+    dequantised weights) and (ii) q4-resident experts (gemm_q4 for every
+    expert); all threads and one thread.  Layers are the workloads' seeded
+    layers with only the routed experts generated (no other expert is
+    touched).  Prefill runs on a token sample (stated); the 48-layer stack
+    is q4 only (a warm fp32 cache of 48 layers does not fit host memory)."""
     sys.path.insert(0, ROOT)
     from oracle import oracle as orc
+    res = {}
+    for name in names:
+        w = pkg.WORKLOADS[name]
+        t0 = time.time()
+        if name == "depth48":
+            res[name] = cpu_depth(orc, w, threads, budget_s)
+            log(f"cpu {name}: {res[name]['q4']['tokens_per_s_all']:.1f} tokens/s (q4, "
+                f"{threads} threads) in {time.time() - t0:.1f}s")
+            continue
+        n_all = min(w.n_tokens, 256)
+        n_one = min(w.n_tokens, 32)
+        x = orc.gen_x(n_all, w.hidden, 4242, bf16=w.x_bf16)
+        rb = (orc.zipf_bias(w.n_experts, w.zipf_s, w.zipf_scale, w.seed * 1000003)
+              if w.zipf_s > 0 else None)
+        Lr = orc.Layer(w.hidden, w.n_experts, w.top_k, w.moe_inter, seed=w.seed, router_bias=rb,
+                       only_experts=[], group_size=w.group_size)
+        ids = Lr.route(x, w.x_bf16)["idx"].reshape(-1)
+        L = orc.Layer(w.hidden, w.n_experts, w.top_k, w.moe_inter, seed=w.seed, router_bias=rb,
+                      only_experts=ids, group_size=w.group_size)
+        warm = orc.Warm(L, ids, n_threads=threads)
+        entry = dict(sample_tokens_all_threads=n_all, sample_tokens_one_thread=n_one,
+                     warm_fp32_bytes=warm.nbytes)
+        for mode in ("warm_fp32", "q4"):
+            row = {}
+            for th, n in ((threads, n_all), (1, n_one)):
+                xs = x[:n]
+                if mode == "warm_fp32":
+                    fn = lambda wu, it, xs=xs, th=th: warm.time_forward(xs, w.x_bf16, th, wu, it)  # noqa: E731
+                else:
+                    fn = lambda wu, it, xs=xs, th=th: L.time_forward(xs, w.x_bf16, th, wu, it)  # noqa: E731
+                med, iters, wu = _timed(fn, budget_s if th > 1 else budget_s / 2)
+                key = "all" if th > 1 else "1"
+                row[f"tokens_per_s_{key}"] = n / med
+                row[f"runs_{key}"] = iters
+                row[f"warmups_{key}"] = wu
+                if name == "prefill":
+                    gemm, router = prefill_flops(w)
+                    row[f"gflops_{key}"] = (gemm + router) / w.n_tokens * n / med / 1e9
+                elif w.n_tokens <= 64:
+                    row[f"gbs_{key}"] = layer_token_bytes(w) * n / med / 1e9 if n == 1 else None
+            entry[mode] = row
+        warm.close()
+        res[name] = entry
+        log(f"cpu {name}: warm fp32 {entry['warm_fp32']['tokens_per_s_all']:.1f} / q4 "
+            f"{entry['q4']['tokens_per_s_all']:.1f} tokens/s ({threads} threads), "
+            f"{entry['warm_fp32']['tokens_per_s_1']:.1f} / {entry['q4']['tokens_per_s_1']:.1f} "
+            f"(1 thread) in {time.time() - t0:.1f}s")
+    return res
+
+
+def cpu_depth(orc, w, threads, budget_s, sample_layers=8):
+    """one token through the stacked layers (RMSNorm + residual), q4
+    experts: the first `sample_layers` layers of the stack run as a chain,
+    their per-layer medians summed and scaled to the stack's depth (every
+    layer has the same shape and routes the same number of experts)"""
     import numpy as np
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
-    t0 = time.time()
-    rb = orc.zipf_bias(w.n_experts, w.zipf_s, w.zipf_scale, w.seed * 1000003) if w.zipf_s > 0 else None
-    L = orc.Layer(w.hidden, w.n_experts, w.top_k, w.moe_inter, seed=w.seed, router_bias=rb,
-                  with_norm=w.rms_norm, group_size=w.group_size)
-    log(f"cpu baseline: host layer generated in {time.time() - t0:.1f}s")
-    ntok_batch = w.n_tokens
-    # sample: as many batches as fit the budget (at least 2)
-    x = orc.gen_x(ntok_batch, w.hidden, 4242, bf16=w.x_bf16)
-    one = L.time_forward(x, w.x_bf16, threads, warmup=1, iters=1)
-    iters = max(2, min(50, int(budget_s / max(one, 1e-6))))
-    med = L.time_forward(x, w.x_bf16, threads, warmup=1, iters=iters, residual=w.rms_norm)
-    med1 = L.time_forward(x, w.x_bf16, 1, warmup=0, iters=max(1, min(3, int(4.0 / max(med * threads, 1e-6)))))
-    return dict(value=ntok_batch / med, unit="tokens/s", cores=threads, kind="port",
-                value_1thread=ntok_batch / med1,
-                sample=f"{iters} runs of the {w.name} batch ({ntok_batch} token(s), one layer, "
-                       f"H={w.hidden} E={w.n_experts} k={w.top_k} I={w.moe_inter}) through "
-                       f"oracle/moe_oracle.c with q4-resident gemm_q4 experts; median; "
-                       f"{threads} OpenMP threads (value_1thread: 1 thread)")
+    h = orc.gen_x(1, w.hidden, 4242, bf16=False)
+    layers = []
+    for layer in range(min(sample_layers, w.n_layers)):
+        rb = orc.zipf_bias(w.n_experts, w.zipf_s, w.zipf_scale, w.seed * 1000003 + layer)
+        Lr = orc.Layer(w.hidden, w.n_experts, w.top_k, w.moe_inter, seed=w.seed, layer=layer,
+                       with_norm=True, router_bias=rb, only_experts=[])
+        ids = Lr.route(h, False)["idx"].reshape(-1)
+        L = orc.Layer(w.hidden, w.n_experts, w.top_k, w.moe_inter, seed=w.seed, layer=layer,
+                      with_norm=True, router_bias=rb, only_experts=ids)
+        layers.append((L, h))
+        h = L.forward(h, False, residual=True, routed_mode=orc.ROUTED_Q4)["out"]
+    out = {}
+    per_layer = budget_s / len(layers)
+    for th, key in ((threads, "all"), (1, "1")):
+        tot = 0.0
+        for L, hin in layers:
+            med, _, _ = _timed(lambda wu, it: L.time_forward(np.ascontiguousarray(hin), False, th,
+                                                             wu, it, residual=True),
+                               per_layer if th > 1 else per_layer / 2, max_iters=10, warm=3)
+            tot += med
+        tot *= w.n_layers / len(layers)
+        out[f"tokens_per_s_{key}"] = 1.0 / tot
+        out[f"gbs_{key}"] = layer_token_bytes(w) * w.n_layers / tot / 1e9
+    return dict(q4=out, sample_tokens=1, sample_layers=len(layers),
+                note=f"one token through the first {len(layers)} of the {w.n_layers} layers as a "
+                     f"chain, per-layer medians summed and scaled to {w.n_layers} layers; only the "
+                     f"routed experts of each layer generated")
 
 
 def copy_calibration(torch, mib):
@@ -326,6 +548,14 @@ def measured_traffic(kernel_symbol, workload):
     return None
 
 
+def free(torch, *objs):
+    for o in objs:
+        if o is not None and hasattr(o, "ctx"):
+            o.ctx.close()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -335,7 +565,11 @@ def main():
     ap.add_argument("--layers", type=int, default=48,
                     help="resident layers rotated over (defeats the Infinity Cache)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--extra", default="batched,prefill",
+    ap.add_argument("--cpu-budget", type=float, default=2.0,
+                    help="seconds of CPU timing per (workload, mode, thread count)")
+    ap.add_argument("--cpu", default="tiny,decode,batched,prefill,depth48",
+                    help="workloads timed on the CPU (the oracle)")
+    ap.add_argument("--extra", default="tiny,batched,prefill,depth48",
                     help="comma list of other workloads to time (secondary results)")
     ap.add_argument("--hyper", default="decode,batched,prefill",
                     help="comma list of workloads also timed as hyper-connection layers "
@@ -353,6 +587,9 @@ def main():
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               f"(the MoE layer runs on a single MI355X here)", file=sys.stderr)
         sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        sys.exit(2)
 
     import torch
     if args.copy_calibration > 0:
@@ -364,10 +601,11 @@ def main():
     w = pkg.WORKLOADS[args.workload]
     n_layers = max(1, min(args.layers, 48 if w.n_tokens <= 64 else 8))
 
-    sec_step, steps, warm, st = bench_layer(pkg, torch, w, n_layers, args.steps, args.warmup)
-    log(f"{w.name}: {sec_step * 1e6:.2f} us/step over {steps} steps, {n_layers} layers")
+    sec_step, st = bench_layer(pkg, torch, w, n_layers, args.steps, args.warmup)
+    log(f"{w.name}: {sec_step * 1e6:.2f} us/step over {args.steps} steps "
+        f"(+{args.warmup} warm-up), {n_layers} layers")
     roof = None
-    if w.n_tokens == 1:
+    if w.n_tokens == 1 and w.x_bf16 and not w.rms_norm:
         k_sec, k_bytes = bench_gateup(pkg, torch, st)
         achieved = k_bytes / k_sec / 1e9
         log(f"gate/up kernel: {k_sec * 1e6:.2f} us/launch, {k_bytes / 1e6:.2f} MB -> {achieved:.0f} GB/s")
@@ -383,22 +621,48 @@ def main():
             "algorithmic_bytes_per_launch": int(k_bytes),
         }
     value = w.n_tokens / sec_step
-    layer_bytes = (10 + 1) * expert_bytes(w) + w.n_experts * w.hidden * 2 + w.hidden * 2
+    layer_bytes = layer_token_bytes(w)
+    free(torch, st)
+    del st
 
     extra = {}
     for name in [e for e in args.extra.split(",") if e and e != w.name]:
         we = pkg.WORKLOADS[name]
-        st.ctx.close()
+        if name == "depth48":
+            s_t = bench_depth(pkg, torch, we, tokens=20, warmup=3)
+            b = layer_token_bytes(we) * we.n_layers
+            extra[name] = dict(us_per_token=s_t * 1e6, tokens_per_s=1.0 / s_t, layers=we.n_layers,
+                               tokens=20, algorithmic_bytes_per_token=b,
+                               hbm_fraction=round(b / s_t / 1e9 / HBM_PEAK_GBS, 4),
+                               note="one f32 token through 48 stacked layers (RMSNorm, Zipf "
+                                    "routing, residual), one HIP graph per 20 tokens")
+            log(f"{name}: {s_t * 1e6:.1f} us/token -> {b / s_t / 1e9:.0f} GB/s")
+            torch.cuda.empty_cache()
+            continue
+        nl = 1 if we.n_tokens <= 4 else (8 if we.n_tokens <= 64 else 2)
+        steps_e = 64 if we.n_tokens <= 64 else 16
+        s_e, st = bench_layer(pkg, torch, we, nl, steps_e, nl * 2, n_inputs=nl * 4)
+        ent = dict(tokens_per_s=we.n_tokens / s_e, ms_per_step=s_e * 1e3,
+                   tokens_per_step=we.n_tokens, layers_rotated=nl, steps=steps_e)
+        if name == "batched":
+            us = distinct_experts(st, nl * 4)
+            b = sum(step_bytes_batched(we, u) for u in us) / len(us)
+            ent.update(mean_distinct_experts=sum(us) / len(us), algorithmic_bytes_per_step=int(b),
+                       hbm_fraction=round(b / s_e / 1e9 / HBM_PEAK_GBS, 4))
+        if name == "prefill":
+            t_gu, t_dn = bench_prefill_stages(pkg, torch, st)
+            gemm, router = prefill_flops(we)
+            ent.update(gateup_stage_us=t_gu * 1e6, down_stage_us=t_dn * 1e6,
+                       grouped_gemm_flops=gemm,
+                       grouped_gemm_mfma_fraction=round(gemm / (t_gu + t_dn) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                       layer_flops=gemm + router,
+                       layer_mfma_fraction=round((gemm + router) / s_e / 1e12 / BF16_PEAK_TFLOPS, 4))
+            log(f"prefill stages: gate/up {t_gu * 1e6:.1f} us, down {t_dn * 1e6:.1f} us -> "
+                f"{gemm / (t_gu + t_dn) / 1e12:.0f} TFLOP/s")
+        extra[name] = ent
+        log(f"{name}: {s_e * 1e3:.4f} ms/step -> {we.n_tokens / s_e:.0f} tokens/s")
+        free(torch, st)
         del st
-        torch.cuda.empty_cache()
-        nl = 8 if we.n_tokens <= 64 else 2
-        s_e, k_e, _, st = bench_layer(pkg, torch, we, nl, max(16, nl * 4), nl)
-        extra[name] = dict(tokens_per_s=we.n_tokens / s_e, ms_per_step=s_e * 1e3,
-                           tokens_per_step=we.n_tokens, layers_rotated=nl, steps=k_e)
-        log(f"{name}: {s_e * 1e3:.3f} ms/step -> {we.n_tokens / s_e:.0f} tokens/s")
-    st.ctx.close()
-    del st
-    torch.cuda.empty_cache()
     for name in [e for e in args.hyper.split(",") if e]:
         we = pkg.WORKLOADS[name]
         nl = 16 if we.n_tokens == 1 else (8 if we.n_tokens <= 64 else 2)
@@ -441,17 +705,33 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(w)
-        log(f"cpu baseline: {cpu['value']:.1f} tokens/s with {cpu['cores']} threads, "
-            f"{cpu['value_1thread']:.1f} with 1")
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+        names = [c for c in args.cpu.split(",") if c]
+        if w.name not in names:
+            names.insert(0, w.name)
+        per = cpu_baselines(pkg, names, threads, args.cpu_budget)
+        head = per[w.name]
+        mode = "warm_fp32" if "warm_fp32" in head else "q4"
+        cpu = dict(value=round(head[mode]["tokens_per_s_all"], 2), unit="tokens/s", cores=threads,
+                   kind="port", value_1thread=round(head[mode]["tokens_per_s_1"], 2),
+                   cpu_model=cpu_model(),
+                   sample=f"the {w.name} workload through oracle/moe_oracle.c (the C restatement of "
+                          f"the reference C port's moe_forward) with warm fp32-dequantised routed "
+                          f"experts (weight mode i, gemm_fp32), median of the runs that fit "
+                          f"{args.cpu_budget:.0f} s after up to 3 warm-ups; {threads} OpenMP threads "
+                          f"(value_1thread: 1 thread); per_config holds every workload in both weight "
+                          f"modes (q4: gemm_q4 for every expert)",
+                   per_config=per)
+        log(f"cpu baseline: {cpu['value']:.1f} tokens/s with {threads} threads "
+            f"({cpu['cpu_model']}), {cpu['value_1thread']:.1f} with 1")
 
     line = {
         "metric": METRIC,
         "value": round(value, 2),
         "unit": "tokens/s",
         "n_gpus": 1,
-        "steps": steps,
-        "warmup": warm,
+        "steps": args.steps,
+        "warmup": args.warmup,
         "ms_per_step": round(sec_step * 1e3, 6),
         "higher_is_better": True,
         "scaling": "weak",

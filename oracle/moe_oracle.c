@@ -748,3 +748,235 @@ double orc_time_forward(const orc_layer *L, const void *x, int n, float *out, co
     free(t);
     return med;
 }
+
+/* ------------------------------------------------ warm fp32 experts (mode i) */
+
+struct orc_warm {
+    int E, H, I;
+    int *slot;    /* [E]: index into w, or -1 */
+    float *w;     /* [count][gate I*H | up I*H | down H*I] */
+    size_t count;
+};
+
+orc_warm *orc_warm_create(const orc_layer *L, const int *experts, int count, int n_threads) {
+    const int E = L->n_experts, H = L->hidden, I = L->moe_inter, gs = L->group_size;
+    orc_warm *w = (orc_warm *)calloc(1, sizeof(orc_warm));
+    if (!w) return NULL;
+    w->E = E;
+    w->H = H;
+    w->I = I;
+    w->slot = (int *)malloc((size_t)E * sizeof(int));
+    int *list = (int *)malloc((size_t)(count > 0 ? count : 1) * sizeof(int));
+    if (!w->slot || !list) {
+        free(list);
+        orc_warm_destroy(w);
+        return NULL;
+    }
+    for (int e = 0; e < E; e++) w->slot[e] = -1;
+    size_t m = 0;
+    for (int i = 0; i < count; i++) {
+        const int e = experts[i];
+        if (e < 0 || e >= E || w->slot[e] >= 0) continue;
+        w->slot[e] = (int)m;
+        list[m++] = e;
+    }
+    const size_t per = (size_t)3 * I * H;
+    w->w = (float *)malloc((m ? m : 1) * per * sizeof(float));
+    if (!w->w) {
+        free(list);
+        orc_warm_destroy(w);
+        return NULL;
+    }
+    w->count = m;
+#ifdef _OPENMP
+    if (n_threads > 0) omp_set_num_threads(n_threads);
+#else
+    (void)n_threads;
+#endif
+#pragma omp parallel for schedule(dynamic, 1)
+    for (long long q = 0; q < (long long)(m * 3); q++) {
+        const int e = list[q / 3], part = (int)(q % 3);
+        const expert_ptrs P = expert_of(L, e);
+        float *dst = w->w + (size_t)(q / 3) * per + (size_t)part * I * H;
+        if (part == 0) orc_dequant_q4(P.gq, P.gs, P.gb, (size_t)I, (size_t)H, (size_t)gs, dst);
+        else if (part == 1) orc_dequant_q4(P.uq, P.us, P.ub, (size_t)I, (size_t)H, (size_t)gs, dst);
+        else orc_dequant_q4(P.dq, P.ds, P.db, (size_t)H, (size_t)I, (size_t)gs, dst);
+    }
+    free(list);
+    return w;
+}
+
+void orc_warm_destroy(orc_warm *w) {
+    if (!w) return;
+    free(w->slot);
+    free(w->w);
+    free(w);
+}
+
+size_t orc_warm_bytes(const orc_warm *w) { return w ? w->count * (size_t)3 * w->I * w->H * sizeof(float) : 0; }
+
+/* fp32 dot with 16 independent partial sums (vectorisable), tail in order */
+static float dot16(const float *a, const float *b, int K) {
+    float acc[16];
+    for (int j = 0; j < 16; j++) acc[j] = 0.0f;
+    int c = 0;
+    for (; c + 16 <= K; c += 16)
+        for (int j = 0; j < 16; j++) acc[j] = fmaf(a[c + j], b[c + j], acc[j]);
+    for (int j = 8; j > 0; j >>= 1)
+        for (int i = 0; i < j; i++) acc[i] = acc[i] + acc[i + j];
+    float r = acc[0];
+    for (; c < K; c++) r = fmaf(a[c], b[c], r);
+    return r;
+}
+
+int orc_moe_forward_warm(const orc_layer *L, const orc_warm *W, const void *x, int n, float *out,
+                         const orc_opts *opt, char *err) {
+    if (check_layer(L, n, err)) return -1;
+    if (!W || W->E != L->n_experts || W->H != L->hidden || W->I != L->moe_inter) {
+        if (err) snprintf(err, 512, "warm expert set does not match the layer");
+        return -1;
+    }
+    if (L->top_k > 64) {
+        if (err) snprintf(err, 512, "top_k %d > 64", L->top_k);
+        return -1;
+    }
+    orc_opts o = {0, 0, ORC_ROUTED_FAITHFUL, 0};
+    if (opt) o = *opt;
+    const int H = L->hidden, E = L->n_experts, k = L->top_k, I = L->moe_inter, gs = L->group_size;
+    const int G = H / gs, GI = I / gs;
+    if (n == 0) return 0;
+    const size_t nk = (size_t)n * k, rows = nk + (size_t)n, per = (size_t)3 * I * H;
+    float *xn = (float *)malloc((size_t)n * H * sizeof(float));
+    int *idx = (int *)malloc(nk * sizeof(int));
+    float *wts = (float *)malloc(nk * sizeof(float));
+    float *sg = (float *)malloc((size_t)n * sizeof(float));
+    int *offsets = (int *)malloc(((size_t)E + 1) * sizeof(int));
+    int *perm = (int *)malloc(nk * sizeof(int));
+    int *pos = (int *)malloc(nk * sizeof(int));
+    int *active = (int *)malloc((size_t)E * sizeof(int));
+    float *h = (float *)malloc(rows * I * sizeof(float));
+    float *y = (float *)malloc(rows * H * sizeof(float));
+    float *xs_h = (float *)malloc((size_t)n * G * sizeof(float));
+    float *xs_i = (float *)malloc((size_t)n * GI * sizeof(float));
+    int rc = -1;
+    if (orc_route(L, x, o.x_is_bf16, n, NULL, NULL, idx, wts, sg, xn, o.n_threads, err)) goto done;
+    const int na = orc_dispatch(idx, n, k, E, offsets, perm, pos, active);
+    for (int a = 0; a < na; a++)
+        if (W->slot[active[a]] < 0) {
+            if (err) snprintf(err, 512, "expert %d is not in the warm set", active[a]);
+            goto done;
+        }
+#ifdef _OPENMP
+    if (o.n_threads > 0) omp_set_num_threads(o.n_threads);
+#endif
+    /* routed gate/up: one task per (active expert, row); the row's weights
+     * stay in cache across the expert's tokens */
+#pragma omp parallel for schedule(dynamic, 8)
+    for (long long q = 0; q < (long long)na * I; q++) {
+        const int e = active[q / I], r = (int)(q % I);
+        const float *we = W->w + (size_t)W->slot[e] * per;
+        const float *wg = we + (size_t)r * H, *wu = we + (size_t)I * H + (size_t)r * H;
+        for (int p = offsets[e]; p < offsets[e + 1]; p++) {
+            const float *xr = xn + (size_t)(perm[p] / k) * H;
+            const float g = dot16(xr, wg, H), u = dot16(xr, wu, H);
+            h[(size_t)p * I + r] = orc_silu(g) * u;
+        }
+    }
+    /* shared expert gate/up: gemm_q4 */
+    for (int t = 0; t < n; t++) group_sums(xn + (size_t)t * H, H, gs, xs_h + (size_t)t * G);
+    {
+        const expert_ptrs P = expert_of(L, -1);
+#pragma omp parallel for schedule(static)
+        for (long long q = 0; q < (long long)n * I; q++) {
+            const int t = (int)(q / I), r = (int)(q % I);
+            const float *xr = xn + (size_t)t * H;
+            const size_t wq = (size_t)r * (H / 8), ws = (size_t)r * G;
+            const float g = q4_row_dot_bf16sb(xr, xs_h + (size_t)t * G, P.gq + wq, P.gs + ws, P.gb + ws, H, gs);
+            const float u = q4_row_dot_bf16sb(xr, xs_h + (size_t)t * G, P.uq + wq, P.us + ws, P.ub + ws, H, gs);
+            h[(nk + (size_t)t) * I + r] = orc_silu(g) * u;
+        }
+    }
+    /* routed down: one task per (active expert, output column) */
+#pragma omp parallel for schedule(dynamic, 32)
+    for (long long q = 0; q < (long long)na * H; q++) {
+        const int e = active[q / H], c = (int)(q % H);
+        const float *wd = W->w + (size_t)W->slot[e] * per + (size_t)2 * I * H + (size_t)c * I;
+        for (int p = offsets[e]; p < offsets[e + 1]; p++) y[(size_t)p * H + c] = dot16(h + (size_t)p * I, wd, I);
+    }
+    for (int t = 0; t < n; t++) group_sums(h + (nk + (size_t)t) * I, I, gs, xs_i + (size_t)t * GI);
+    {
+        const expert_ptrs P = expert_of(L, -1);
+#pragma omp parallel for schedule(static)
+        for (long long q = 0; q < (long long)n * H; q++) {
+            const int t = (int)(q / H), c = (int)(q % H);
+            const size_t wq = (size_t)c * (I / 8), ws = (size_t)c * GI;
+            y[(nk + (size_t)t) * H + c] = q4_row_dot_bf16sb(h + (nk + (size_t)t) * I, xs_i + (size_t)t * GI,
+                                                           P.dq + wq, P.ds + ws, P.db + ws, I, gs);
+        }
+    }
+    /* combine in ascending expert order, then the shared expert */
+#pragma omp parallel for schedule(static)
+    for (int t = 0; t < n; t++) {
+        int ps[64], m = 0;
+        for (int s2 = 0; s2 < k; s2++) ps[m++] = pos[(size_t)t * k + s2];
+        for (int a2 = 1; a2 < m; a2++)
+            for (int b2 = a2; b2 > 0 && ps[b2 - 1] > ps[b2]; b2--) {
+                const int tmp = ps[b2];
+                ps[b2] = ps[b2 - 1];
+                ps[b2 - 1] = tmp;
+            }
+        float *orow = out + (size_t)t * H;
+        for (int c = 0; c < H; c++) orow[c] = 0.0f;
+        for (int a2 = 0; a2 < m; a2++) {
+            const int p = ps[a2];
+            const float wt = wts[perm[p]];
+            for (int c = 0; c < H; c++) orow[c] = fmaf(wt, y[(size_t)p * H + c], orow[c]);
+        }
+        for (int c = 0; c < H; c++) orow[c] = fmaf(sg[t], y[(nk + (size_t)t) * H + c], orow[c]);
+        if (o.residual) {
+            if (o.x_is_bf16) {
+                const uint16_t *xb = (const uint16_t *)x + (size_t)t * H;
+                for (int c = 0; c < H; c++) orow[c] = orc_bf16_to_f32(xb[c]) + orow[c];
+            } else {
+                const float *xf = (const float *)x + (size_t)t * H;
+                for (int c = 0; c < H; c++) orow[c] = xf[c] + orow[c];
+            }
+        }
+    }
+    rc = 0;
+done:
+    free(xn);
+    free(idx);
+    free(wts);
+    free(sg);
+    free(offsets);
+    free(perm);
+    free(pos);
+    free(active);
+    free(h);
+    free(y);
+    free(xs_h);
+    free(xs_i);
+    return rc;
+}
+
+double orc_time_forward_warm(const orc_layer *L, const orc_warm *W, const void *x, int n,
+                             float *out, const orc_opts *opt, int warmup, int iters) {
+    char err[512];
+    for (int i = 0; i < warmup; i++)
+        if (orc_moe_forward_warm(L, W, x, n, out, opt, err)) return -1.0;
+    if (iters < 1) iters = 1;
+    double *t = (double *)malloc((size_t)iters * sizeof(double));
+    for (int i = 0; i < iters; i++) {
+        double t0 = now_s();
+        if (orc_moe_forward_warm(L, W, x, n, out, opt, err)) {
+            free(t);
+            return -1.0;
+        }
+        t[i] = now_s() - t0;
+    }
+    qsort(t, (size_t)iters, sizeof(double), cmp_dbl);
+    double med = t[iters / 2];
+    free(t);
+    return med;
+}

@@ -185,6 +185,28 @@ void orc_zipf_bias(float *bias, int E, double s, double scale, uint64_t seed);
 double orc_time_forward(const orc_layer *L, const void *x, int n, float *out,
                         const orc_opts *opt, int warmup, int iters);
 
+/* ---- CPU baseline, weight mode (i): warm fp32 experts ----
+ * The steady state of the C port's expert cache: each listed routed expert
+ * dequantised once to fp32 in the cache's gate | up | down layout
+ * (model.c:603-662, dequant_raw + kernel_dequant_q4), then every layer call
+ * runs gemm_fp32 on them (model.c:1368-1375, kernel.c:181-186).  The fp32
+ * products here are blocked like a BLAS sgemm: each weight row is read once
+ * per call and dotted with every token routed to its expert, 16 independent
+ * partial sums per dot (the summation order is a BLAS's, not the oracle's
+ * single fma chain).  The shared expert stays q4 (linear_forward ->
+ * gemm_q4, model.c:193-202).  Timing only; the result is checked against
+ * orc_moe_forward within fp32 tolerance. */
+typedef struct orc_warm orc_warm;
+orc_warm *orc_warm_create(const orc_layer *L, const int *experts, int count, int n_threads);
+void orc_warm_destroy(orc_warm *w);
+size_t orc_warm_bytes(const orc_warm *w);
+/* -1 with a message when a routed expert is not in the warm set */
+int orc_moe_forward_warm(const orc_layer *L, const orc_warm *W, const void *x, int n, float *out,
+                         const orc_opts *opt, char *err);
+/* median seconds of `iters` calls after `warmup`; < 0 on error */
+double orc_time_forward_warm(const orc_layer *L, const orc_warm *W, const void *x, int n,
+                             float *out, const orc_opts *opt, int warmup, int iters);
+
 #ifdef __cplusplus
 }
 #endif

@@ -78,6 +78,11 @@ _SIG = {
     "orc_gemm_bf16": (None, [_I, _I, _I, _P, _P, _P]),
     "orc_gemm_q4_f32sb": (None, [_I, _I, _I, _P, _P, _P, _P, _I, _P]),
     "orc_gemm_q4": (None, [_I, _I, _I, _P, _P, _P, _P, _I, _P]),
+    "orc_warm_create": (_P, [_P, _P, _I, _I]),
+    "orc_warm_destroy": (None, [_P]),
+    "orc_warm_bytes": (_SZ, [_P]),
+    "orc_moe_forward_warm": (_I, [_P, _P, _P, _I, _P, _P, _P]),
+    "orc_time_forward_warm": (ctypes.c_double, [_P, _P, _P, _I, _P, _P, _I, _I]),
     "orc_dispatch": (_I, [_P, _I, _I, _I, _P, _P, _P, _P]),
     "orc_moe_forward": (_I, [ctypes.POINTER(OrcLayer), _P, _I, _P, ctypes.POINTER(OrcOpts), _P, _I,
                              _P, _P, _P, _P, _P, _P, _P]),
@@ -293,6 +298,52 @@ class Layer:
         opts = OrcOpts(int(x_is_bf16), int(residual), routed_mode, n_threads)
         return lib().orc_time_forward(ctypes.byref(self.st), _p(x), x.shape[0], _p(out),
                                       ctypes.byref(opts), warmup, iters)
+
+
+class Warm:
+    """Weight mode (i) of the CPU baseline: the listed routed experts of a
+    Layer dequantised once to fp32 (the C port's warm expert cache); calls
+    run fp32 GEMMs on them.  Timing only."""
+
+    def __init__(self, layer: Layer, experts, n_threads=0):
+        ids = np.ascontiguousarray(sorted(set(int(e) for e in experts)), dtype=np.int32)
+        self.layer = layer
+        self.h = lib().orc_warm_create(ctypes.byref(layer.st), _p(ids), len(ids), n_threads)
+        if not self.h:
+            raise MemoryError("orc_warm_create failed")
+
+    @property
+    def nbytes(self):
+        return int(lib().orc_warm_bytes(self.h))
+
+    def close(self):
+        if self.h:
+            lib().orc_warm_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def forward(self, x, x_is_bf16, residual=False, n_threads=0):
+        x = np.ascontiguousarray(x)
+        out = np.empty((x.shape[0], self.layer.H), np.float32)
+        opts = OrcOpts(int(x_is_bf16), int(residual), ROUTED_FAITHFUL, n_threads)
+        err = ctypes.create_string_buffer(512)
+        rc = lib().orc_moe_forward_warm(ctypes.byref(self.layer.st), self.h, _p(x), x.shape[0],
+                                        _p(out), ctypes.byref(opts), err)
+        if rc:
+            raise RuntimeError(err.value.decode())
+        return out
+
+    def time_forward(self, x, x_is_bf16, n_threads, warmup=1, iters=3, residual=False):
+        x = np.ascontiguousarray(x)
+        out = np.empty((x.shape[0], self.layer.H), np.float32)
+        opts = OrcOpts(int(x_is_bf16), int(residual), ROUTED_FAITHFUL, n_threads)
+        t = lib().orc_time_forward_warm(ctypes.byref(self.layer.st), self.h, _p(x), x.shape[0],
+                                        _p(out), ctypes.byref(opts), warmup, iters)
+        if t < 0:
+            raise RuntimeError("warm forward failed (expert not warm?)")
+        return t
 
 
 class Hyper:

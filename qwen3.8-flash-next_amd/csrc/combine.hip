@@ -30,7 +30,9 @@ struct CombineArgs {
  * CB_HALVES blocks of 1024 (two from 256 tokens on, one for small batches
  * so that they still spread over the CUs).  For token t the k
  * slots are taken in ascending dispatch position, i.e. ascending expert id
- * (the expert loop order of model.c:1338), each as out = fma(w, y, out)
+ * (the MLX dispatch order, model.py:433-441; the C port's loop at
+ * model.c:1338 takes the experts in first-seen order, which only reorders
+ * these fp32 sums), each as out = fma(w, y, out)
  * from out = 0, then out = fma(g, y_shared, out), then the optional residual.
  * With a hyper state, every copy j of token t becomes
  * fma(inject[t, j], out, hyper[t, j]) (model.c:1724-1731).

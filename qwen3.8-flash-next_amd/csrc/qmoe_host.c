@@ -79,7 +79,7 @@ struct qmoe_ctx {
     size_t s_dlayer;             /* bytes of one layer's state */
     int32_t *s_miss;             /* [1+2E] the call's misses */
     unsigned long long *s_dstats; /* [5] hits, misses, evictions, rejected, copies */
-    int s_dstale;                /* 1 + a layer whose state could not be cleared, 0: none */
+    uint8_t *s_dstale;           /* [L] 1: the layer's state could not be cleared at its last upload */
 };
 
 static int is_routed(int t) { return t >= QH_T_GATE_Q && t <= QH_T_DOWN_B; }
@@ -279,6 +279,7 @@ static void stream_free(qmoe_ctx *c) {
     free(c->s_prev);
     free(c->s_pf_flag);
     free(c->s_ids);
+    free(c->s_dstale);
     qmoe_xcache_destroy(c->xc);
     c->s_host = c->s_hdev = NULL;
     c->s_pool = c->s_seg = NULL;
@@ -293,6 +294,7 @@ static void stream_free(qmoe_ctx *c) {
     c->s_freq = c->s_trans = NULL;
     c->s_prev = c->s_ids = NULL;
     c->s_pf_flag = NULL;
+    c->s_dstale = NULL;
     c->xc = NULL;
     c->streamed = 0;
 }
@@ -419,7 +421,16 @@ static char *host_tensor_store(qmoe_ctx *c, int layer, int t, qmoe_err *err) {
     return (char *)c->s_host[layer] + c->s_hoff[t];
 }
 
-/* a layer's weights were replaced: forget its resident experts */
+/* Before a streamed layer's pinned host store or its slots are rewritten:
+ * copies of expert pieces out of the store run asynchronously (prefetch on
+ * the copy stream, demand misses on the caller's stream) and may still be
+ * reading it or filling a slot, so every queued device operation is
+ * finished first.  Uploads are not on the per-token path. */
+static int stream_quiesce(qmoe_ctx *c, qmoe_err *err) {
+    if (!c->streamed) return 0;
+    return hip_fail(err, (int)hipDeviceSynchronize(), "wait for expert copies before an upload");
+}
+
 /* the device state of a layer back to empty: no resident expert, zero counts */
 static int dstate_reset(qmoe_ctx *c, int layer) {
     const int E = c->cfg.n_experts, S = c->s_slots;
@@ -447,9 +458,11 @@ static void dstate_args(qmoe_ctx *c, int layer, QkStreamResolve *a) {
     a->policy = c->s_policy;
 }
 
+/* a layer's weights were replaced: forget its resident experts (after
+ * stream_quiesce, so no copy of the old weights is in flight) */
 static void stream_layer_written(qmoe_ctx *c, int layer) {
     if (!c->streamed) return;
-    if (c->s_dev && dstate_reset(c, layer)) c->s_dstale = 1 + layer; /* refused by the layer call */
+    if (c->s_dev) c->s_dstale[layer] = dstate_reset(c, layer) != 0; /* refused by the layer call */
     qmoe_xcache_clear(c->xc, layer);
     memset(c->s_pf_flag + (size_t)layer * c->cfg.n_experts, 0, (size_t)c->cfg.n_experts);
     c->s_pf_pending[layer] = 0;
@@ -469,7 +482,7 @@ int qmoe_upload_layer(qmoe_ctx *c, int layer, const qmoe_layer_weights *h, qmoe_
             return -1;
         }
     }
-    if (ensure_layer_mem(c, layer, err)) return -1;
+    if (ensure_layer_mem(c, layer, err) || stream_quiesce(c, err)) return -1;
     qmoe_layer_slot *L = &c->layers[layer];
     L->ready = 0;
     char *b = (char *)L->mem;
@@ -512,8 +525,9 @@ void qh_host_free(void *p) {
     if (p) (void)hipHostFree(p);
 }
 
-void qh_layer_begin(qmoe_ctx *c, int layer) {
+int qh_layer_begin(qmoe_ctx *c, int layer, qmoe_err *err) {
     if (c->layers[layer].mem) c->layers[layer].ready = 0;
+    return stream_quiesce(c, err);
 }
 
 int qh_layer_slot(qmoe_ctx *c, int layer, int t, void **dst, size_t *bytes, int *on_host,
@@ -565,7 +579,7 @@ int qmoe_synth_layer(qmoe_ctx *c, int layer, uint64_t seed, int with_norm, const
                      qmoe_err *err) {
     clear_err(err);
     if (check_layer_index(c, layer, err)) return -1;
-    if (ensure_layer_mem(c, layer, err)) return -1;
+    if (ensure_layer_mem(c, layer, err) || stream_quiesce(c, err)) return -1;
     qmoe_layer_slot *L = &c->layers[layer];
     L->ready = 0;
     char *b = (char *)L->mem;
@@ -1161,7 +1175,11 @@ int qh_hc_slot(qmoe_ctx *c, int layer, int t, void **dst, size_t *bytes, int *on
     return 0;
 }
 
-void qh_hc_begin(qmoe_ctx *c, int layer) { c->hc_ready[layer] = 0; }
+int qh_hc_begin(qmoe_ctx *c, int layer, qmoe_err *err) {
+    (void)err;
+    c->hc_ready[layer] = 0;
+    return 0;
+}
 void qh_hc_end(qmoe_ctx *c, int layer) { c->hc_ready[layer] = 1; }
 
 int qmoe_hc_upload_layer(qmoe_ctx *c, int layer, const qmoe_hc_weights *h, qmoe_err *err) {
@@ -1328,9 +1346,11 @@ int qmoe_stream_enable(qmoe_ctx *c, int slots, int policy, int prefetch, qmoe_er
     }
     const int E = c->cfg.n_experts, L = c->cfg.n_layers;
     if (c->streamed) {
-        if (slots == c->s_slots && (prefetch < 0 ? c->s_dev : !c->s_dev && prefetch == c->s_prefetch))
+        if (slots == c->s_slots && policy == c->s_policy &&
+            (prefetch < 0 ? c->s_dev : !c->s_dev && prefetch == c->s_prefetch))
             return 0;
-        set_err(err, "expert streaming already enabled with %d slots per layer", c->s_slots);
+        set_err(err, "expert streaming already enabled with %d slots per layer, policy %d, prefetch %d",
+                c->s_slots, c->s_policy, c->s_dev ? -1 : c->s_prefetch);
         return -1;
     }
     for (int l = 0; l < L; l++)
@@ -1400,8 +1420,9 @@ int qmoe_stream_enable(qmoe_ctx *c, int slots, int policy, int prefetch, qmoe_er
         c->s_prev = (int32_t *)calloc((size_t)L * (E + 1), sizeof(int32_t));
         c->s_pf_flag = (uint8_t *)calloc((size_t)L * E, 1);
         c->s_ids = (int32_t *)calloc((size_t)E, sizeof(int32_t));
+        c->s_dstale = (uint8_t *)calloc((size_t)L, 1);
         ok = c->s_host && c->s_hdev && c->s_ev_used && c->s_ev_pf && c->s_pf_pending && c->s_freq && c->s_trans &&
-             c->s_prev && c->s_pf_flag && c->s_ids;
+             c->s_prev && c->s_pf_flag && c->s_ids && c->s_dstale;
         if (!ok) set_err(err, "out of host memory");
     }
     for (int l = 0; ok && l < L; l++)
@@ -1654,8 +1675,8 @@ static int layer_forward_streamed(qmoe_ctx *c, int layer, const void *x, int xbf
     if (c->s_dev) {
         /* residency decided on the device: remap, then copy the misses, all
          * on the call's stream with no host round trip */
-        if (c->s_dstale) {
-            set_err(err, "the slot cache of layer %d could not be cleared after its upload", c->s_dstale - 1);
+        if (c->s_dstale[layer]) {
+            set_err(err, "the slot cache of layer %d could not be cleared after its upload", layer);
             return -1;
         }
         QkStreamResolve r;

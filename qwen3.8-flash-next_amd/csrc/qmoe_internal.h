@@ -70,7 +70,7 @@ enum {
 int qh_ctx_config(qmoe_ctx *c, int layer, qmoe_config *out, qmoe_err *err);
 int qh_host_alloc(void **p, size_t bytes, qmoe_err *err);
 void qh_host_free(void *p);
-void qh_layer_begin(qmoe_ctx *c, int layer);
+int qh_layer_begin(qmoe_ctx *c, int layer, qmoe_err *err);
 /* *on_host: the slot is host memory (a routed expert tensor of a context
  * with streamed experts) */
 int qh_layer_slot(qmoe_ctx *c, int layer, int t, void **dst, size_t *bytes, int *on_host,
@@ -82,7 +82,7 @@ void qh_layer_end(qmoe_ctx *c, int layer, int has_bias, int has_norm);
 int qh_hc_config(qmoe_ctx *c, int layer, int *hc, int *lowrank, int *d, qmoe_err *err);
 int qh_hc_slot(qmoe_ctx *c, int layer, int t, void **dst, size_t *bytes, int *on_host,
                qmoe_err *err);
-void qh_hc_begin(qmoe_ctx *c, int layer);
+int qh_hc_begin(qmoe_ctx *c, int layer, qmoe_err *err);
 void qh_hc_end(qmoe_ctx *c, int layer);
 
 /* All launchers return a hipError_t value (0 = hipSuccess). */

@@ -788,7 +788,7 @@ static int check_tensor(const st_entry *e, const st_want *w, qmoe_err *err) {
 typedef struct {
     int (*slot)(qmoe_ctx *c, int layer, int t, void **dst, size_t *bytes, int *on_host,
                 qmoe_err *err);
-    void (*begin)(qmoe_ctx *c, int layer);
+    int (*begin)(qmoe_ctx *c, int layer, qmoe_err *err);
     void (*end)(qmoe_ctx *c, int layer);
     const char *dense_what; /* message for q4 weights found without scales */
     const char *quant_what; /* message for a dense tensor found quantized */
@@ -837,8 +837,7 @@ static int upload_table(qmoe_ctx *ctx, int layer, const qmoe_st *ix, const char 
     const size_t chunk = (size_t)64 << 20;
     void *stage = NULL;
     if (qh_host_alloc(&stage, chunk, err)) return -1;
-    int rc = 0;
-    tg->begin(ctx, layer);
+    int rc = tg->begin(ctx, layer, err);
     for (int i = 0; i < nw && rc == 0; i++) {
         void *dst;
         size_t bytes;

@@ -357,10 +357,11 @@ class MoeContext:
                "qmoe_dispatch")
         return dict(offsets=offsets, perm=perm[: n * self.k], segments=segments)
 
-    def expert_gateup(self, layer, x, d, stream=None):
+    def expert_gateup(self, layer, x, d, stream=None, out=None):
         import torch
         n = x.shape[0]
-        h = torch.empty((n * self.k + n, self.I), dtype=torch.float32, device=x.device)
+        h = out if out is not None else torch.empty((n * self.k + n, self.I), dtype=torch.float32,
+                                                    device=x.device)
         err = QmoeErr()
         _check(lib().qmoe_expert_gateup(self._h, layer, _ptr(x), _dtype_code(x), n, _ptr(d["perm"]),
                                         _ptr(d["segments"]), _ptr(h), _stream(stream),
@@ -392,9 +393,10 @@ class MoeContext:
                                              _stream(stream), ctypes.byref(err)), err,
                "qmoe_expert_gateup_topk")
 
-    def expert_down(self, layer, h, n, d, stream=None):
+    def expert_down(self, layer, h, n, d, stream=None, out=None):
         import torch
-        y = torch.empty((n * self.k + n, self.H), dtype=torch.float32, device=h.device)
+        y = out if out is not None else torch.empty((n * self.k + n, self.H), dtype=torch.float32,
+                                                    device=h.device)
         err = QmoeErr()
         _check(lib().qmoe_expert_down(self._h, layer, _ptr(h), n, _ptr(d["segments"]), _ptr(y),
                                       _stream(stream), ctypes.byref(err)), err, "qmoe_expert_down")

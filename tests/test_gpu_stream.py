@@ -39,7 +39,7 @@ def _pair(pkg, H, E, k, I, L, max_tokens, slots, policy, prefetch, seed, zipf=0.
     return res, stm
 
 
-def _run_sequence(torch, dev, res, stm, L, steps, n, H, bf16, seed):
+def _run_sequence(torch, dev, res, stm, L, steps, n, H, bf16, seed, us=None):
     routed = 0
     for step in range(steps):
         x = orc.gen_x(n, H, seed + step, bf16=bf16)
@@ -55,6 +55,8 @@ def _run_sequence(torch, dev, res, stm, L, steps, n, H, bf16, seed):
             u = int(sa[0])  # entries past the count are not written by the call
             assert np.array_equal(sa[:1 + 3 * u], sb[:1 + 3 * u])
             routed += u
+            if us is not None:
+                us.append(u)
             assert np.array_equal(a.cpu().numpy(), b.cpu().numpy()), (step, layer)
     return routed
 
@@ -225,5 +227,57 @@ def test_device_resolved_graph_replay(torch_dev):
     st = stm.stream_stats()
     say(f"stats {st}")
     assert st["misses"] > 0 and st["rejected"] == 0
+    res.close()
+    stm.close()
+
+
+def test_device_resolved_many_experts_evicting(torch_dev):
+    """more than 256 routed experts in one call (the resolve kernel takes the
+    hits before each miss in passes of 256 threads) while the slots still
+    evict: device-resolved and host-resolved residency give the same counts,
+    and both give the resident layer's bits"""
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    H, E, k, I, n, slots = 128, 1024, 10, 64, 32, 320
+    say(f"case: E={E} top-{k}, {n} tokens per call, {slots} slots, device vs host residency")
+    stats, routed, us = [], [], []
+    for prefetch in (-1, 0):
+        res, stm = _pair(pkg, H, E, k, I, 1, n, slots, 2, prefetch, seed=12)
+        routed.append(_run_sequence(torch, dev, res, stm, 1, 6, n, H, False, seed=300, us=us))
+        stats.append(stm.stream_stats())
+        res.close()
+        stm.close()
+    say(f"device {stats[0]} host {stats[1]} routed {routed}")
+    assert routed[0] == routed[1] and max(us) > 256
+    for f in ("hits", "misses", "evictions", "rejected", "bytes_in"):
+        assert stats[0][f] == stats[1][f], f
+    assert stats[0]["evictions"] > 0 and stats[0]["hits"] > 0
+
+
+def test_reupload_after_prefetch(torch_dev):
+    """a layer re-uploaded right after a call that queued prefetch copies:
+    the upload waits for the copies, the layer forgets its slots, and the
+    next call gives the new weights' bits"""
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    H, E, k, I, L = 256, 8, 2, 128, 2
+    say("case: re-upload of a streamed layer with prefetch copies in flight")
+    res, stm = _pair(pkg, H, E, k, I, L, 2, 4, 2, 4, seed=21)
+    xs = [torch.from_numpy(orc.gen_x(2, H, 500 + i, bf16=False)).to(dev) for i in range(4)]
+    for x in xs:
+        for layer in range(L):
+            stm.layer_forward(layer, x)
+    # no synchronisation: the last calls' prefetches may still be queued
+    stm.synth_layer(0, 99)
+    res.synth_layer(0, 99)
+    for i, x in enumerate(xs):
+        for layer in range(L):
+            a = res.layer_forward(layer, x)
+            b = stm.layer_forward(layer, x)
+            torch.cuda.synchronize()
+            assert np.array_equal(a.cpu().numpy(), b.cpu().numpy()), (i, layer)
+    st = stm.stream_stats()
+    say(f"stats {st}")
+    assert st["prefetched"] > 0
     res.close()
     stm.close()

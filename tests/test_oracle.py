@@ -490,3 +490,31 @@ def test_zipf_bias():
     ranks = np.sort(p)[::-1]
     r = np.arange(1, 513, dtype=np.float64)
     np.testing.assert_allclose(ranks, r ** -1.1 / (r ** -1.1).sum(), rtol=1e-5)
+
+
+def test_warm_fp32_mode_matches_faithful():
+    """the CPU baseline's weight mode (i) -- warm fp32-dequantised experts,
+    sgemm-blocked fp32 products -- computes the same layer as the faithful
+    oracle (fp32 dequant + one fma chain per dot) up to fp32 summation
+    order, and refuses a routed expert it does not hold"""
+    import pytest
+    for (H, E, k, I, n, bf, zipf) in ((256, 8, 2, 128, 4, False, 0.0), (512, 64, 6, 128, 40, True, 1.1)):
+        rb = orc.zipf_bias(E, zipf, 1.0, 3) if zipf else None
+        x = orc.gen_x(n, H, 3, bf16=bf)
+        r = orc.Layer(H, E, k, I, seed=1, router_bias=rb, only_experts=[]).route(x, bf)
+        L = orc.Layer(H, E, k, I, seed=1, router_bias=rb, only_experts=r["idx"].reshape(-1))
+        ref = L.forward(x, bf)["out"]
+        W = orc.Warm(L, r["idx"].reshape(-1))
+        got = W.forward(x, bf)
+        assert W.nbytes == len(set(r["idx"].reshape(-1).tolist())) * 3 * I * H * 4
+        rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+        assert np.abs(got - ref).max() < 1e-3 * np.abs(ref).max() and rel < 1e-5, rel
+        # residual form
+        got_r = W.forward(x, bf, residual=True)
+        xf = orc.bf16_to_f32(x) if bf else x
+        np.testing.assert_allclose(got_r, xf + got, rtol=1e-6, atol=1e-4)
+        W.close()
+        partial = orc.Warm(L, r["idx"].reshape(-1)[:1])
+        with pytest.raises(RuntimeError, match="not in the warm set"):
+            partial.forward(x, bf)
+        partial.close()
