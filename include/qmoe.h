@@ -262,6 +262,27 @@ int qmoe_combine(qmoe_ctx *ctx, const float *y, const int32_t *perm, const float
 int qmoe_layer_forward(qmoe_ctx *ctx, int layer, const void *x, int x_dtype, int n, float *out,
                        int flags, void *stream, qmoe_err *err);
 
+/* enable = 1 runs one-token calls (n = 1) of qmoe_layer_forward and
+ * qmoe_hc_layer_forward in two launches (hidden 2048 or 4096, moe_inter 512
+ * or 1024, n_experts <= 1024, top_k <= 16): the router with the shared
+ * expert's gate/up, then top-k, routed gate/up, down and the combine
+ * together, the down projection taking h from the gate/up workgroups of the
+ * same launch through a bounded in-kernel wait.  The default (enable = 0)
+ * is the staged kernels (router; gate/up with top-k; down + combine), which
+ * measure faster at the decode shape (17.0 against 28.9 us per layer); both
+ * give bit-identical outputs.  No counterpart in the reference (its layer is
+ * one CPU call).  enable = 1 on a shape the two-launch path does not take
+ * is an error. */
+int qmoe_set_fused_decode(qmoe_ctx *ctx, int enable, qmoe_err *err);
+
+/* Synchronises the device and reports whether a two-launch one-token call
+ * gave up a wait (20 ms bound; only possible when other work keeps its
+ * gate/up workgroups off the GPU): returns 0 with *flags = 0 when none did;
+ * otherwise -1 with *flags != 0, after resetting the hand-off state.  The
+ * outputs of the calls since the previous check may then be NaN.  No
+ * counterpart in the reference. */
+int qmoe_decode_status(qmoe_ctx *ctx, uint32_t *flags, qmoe_err *err);
+
 /* Copies the routing of the last qmoe_layer_forward call on this context
  * (n must be that call's token count) into caller device buffers, any of
  * which may be NULL: idx [n,k], w [n,k], shared_gate [n], offsets [E+1],

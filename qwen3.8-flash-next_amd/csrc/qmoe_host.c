@@ -35,6 +35,7 @@ struct qmoe_ctx {
     qmoe_layer_slot *layers;
     size_t layer_bytes;
     int last_n; /* token count of the last qmoe_layer_forward, -1 if none */
+    int dec_fused; /* one-token calls in two launches (qk_launch_dec_layer) when supported */
     /* second stream for the GEMV kernels of small segments, which run beside
      * the MFMA kernels of large ones (fork/join with two events) */
     hipStream_t aux;
@@ -201,6 +202,7 @@ int qmoe_create(qmoe_ctx **out, const qmoe_config *cfg, qmoe_err *err) {
     }
     c->layer_bytes = o;
     c->last_n = -1;
+    c->dec_fused = 0;
     c->layers = (qmoe_layer_slot *)calloc((size_t)cfg->n_layers, sizeof(qmoe_layer_slot));
     if (!c->layers) {
         free(c);
@@ -212,12 +214,13 @@ int qmoe_create(qmoe_ctx **out, const qmoe_config *cfg, qmoe_err *err) {
     const size_t H = (size_t)cfg->hidden, I = (size_t)cfg->moe_inter;
     const size_t nw = (n + 31) / 32, rows = n * k + n;
     const size_t plane = n * H > rows * I ? n * H : rows * I;
-    size_t sz[17] = {n * (E + 1) * 4, n * k * 4, n * k * 4, n * 4, (E + 1) * 4, n * k * 4,
+    const size_t rep = qk_dec_supported(c->shape) ? qk_dec_replica_bytes(c->shape) : 0;
+    size_t sz[19] = {n * (E + 1) * 4, n * k * 4, n * k * 4, n * 4, (E + 1) * 4, n * k * 4,
                      n * k * 4, E * nw * 4, E * nw * 4, n * H * 4, rows * I * 4,
                      rows * H * 4, (3 * E + 1) * 4, qk_mfma_task_bytes(c->shape, (int)n),
-                     plane * 2, plane * 2, plane / 64 * 4};
-    size_t total = 0, offs[17];
-    for (int i = 0; i < 17; i++) {
+                     plane * 2, plane * 2, plane / 64 * 4, rep, 4};
+    size_t total = 0, offs[19];
+    for (int i = 0; i < 19; i++) {
         offs[i] = total;
         total = align_up(total + sz[i]);
     }
@@ -245,6 +248,15 @@ int qmoe_create(qmoe_ctx **out, const qmoe_config *cfg, qmoe_err *err) {
     c->sc.ahi = (uint16_t *)(b + offs[14]);
     c->sc.alo = (uint16_t *)(b + offs[15]);
     c->sc.ag = (float *)(b + offs[16]);
+    c->sc.rep = rep ? (uint32_t *)(b + offs[17]) : NULL;
+    c->sc.status = (uint32_t *)(b + offs[18]);
+    if (hip_fail(err, (int)hipMemset(c->sc.status, 0, 4), "clear status") ||
+        (rep && hip_fail(err, (int)hipMemset(c->sc.rep, 0xFF, rep), "clear replicas"))) {
+        hipFree(c->scratch_mem);
+        free(c->layers);
+        free(c);
+        return -1;
+    }
     if (hip_fail(err, (int)hipStreamCreateWithFlags(&c->aux, hipStreamNonBlocking), "stream") ||
         hip_fail(err, (int)hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming), "event") ||
         hip_fail(err, (int)hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming), "event")) {
@@ -980,6 +992,13 @@ static int layer_forward(qmoe_ctx *c, int layer, const void *x, int xbf, int n, 
     const int hc = hyper ? c->hc : 0;
     int rc;
     float *xn = W->norm_w ? sc->xn : NULL;
+    if (n == 1 && sc->rep && c->dec_fused) {
+        /* one token: router + shared gate/up, then everything else in one launch */
+        rc = qk_launch_dec_layer(W, s, x, xbf, sc->logits, sc->xn, sc->h, sc->rep, sc->status,
+                                 sc->idx, sc->w, sc->sg, sc->perm, sc->pos, sc->segtab,
+                                 residual ? x : NULL, out, hyper, inject, hc, stream);
+        return hip_fail(err, rc, "one-token layer");
+    }
     rc = qk_launch_router(W, s, x, xbf, n, sc->logits, xn, stream);
     if (hip_fail(err, rc, "router")) return -1;
     const void *xf = W->norm_w ? (const void *)sc->xn : x;
@@ -1021,6 +1040,44 @@ static int layer_forward(qmoe_ctx *c, int layer, const void *x, int xbf, int n, 
     rc = qk_launch_combine(s, n, sc->y, sc->pos, sc->w, sc->sg, residual ? x : NULL, xbf, out,
                            hyper, inject, hc, stream);
     return hip_fail(err, rc, "combine");
+}
+
+int qmoe_set_fused_decode(qmoe_ctx *c, int enable, qmoe_err *err) {
+    clear_err(err);
+    if (!c) {
+        set_err(err, "ctx is NULL");
+        return -1;
+    }
+    if (enable && !c->sc.rep) {
+        set_err(err, "the two-launch one-token layer does not take this shape (hidden %d, "
+                     "n_experts %d, top_k %d, moe_inter %d)", c->cfg.hidden, c->cfg.n_experts,
+                c->cfg.top_k, c->cfg.moe_inter);
+        return -1;
+    }
+    c->dec_fused = enable != 0;
+    return 0;
+}
+
+int qmoe_decode_status(qmoe_ctx *c, uint32_t *flags, qmoe_err *err) {
+    clear_err(err);
+    if (!c || !flags) {
+        set_err(err, "%s is NULL", c ? "flags" : "ctx");
+        return -1;
+    }
+    *flags = 0;
+    if (hip_fail(err, (int)hipDeviceSynchronize(), "synchronise") ||
+        hip_fail(err, (int)hipMemcpy(flags, c->sc.status, 4, hipMemcpyDeviceToHost), "read status"))
+        return -1;
+    if (*flags == 0) return 0;
+    /* a wait expired: put every replica word back to the sentinel and clear
+     * the status, so later one-token calls start from a clean hand-off */
+    if ((c->sc.rep && hip_fail(err, (int)hipMemset(c->sc.rep, 0xFF, qk_dec_replica_bytes(c->shape)),
+                               "reset replicas")) ||
+        hip_fail(err, (int)hipMemset(c->sc.status, 0, 4), "clear status"))
+        return -1;
+    set_err(err, "a one-token layer call waited past its bound for h (flags 0x%x); its output "
+                 "was NaN; the hand-off state is reset", *flags);
+    return -1;
 }
 
 int qmoe_layer_forward(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n, float *out,
