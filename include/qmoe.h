@@ -424,6 +424,75 @@ size_t qmoe_layer_bytes(const qmoe_ctx *ctx);
 /* Library version string. */
 const char *qmoe_version(void);
 
+/* ------------------------------------------------------ gated DeltaNet
+ * The linear-attention mixer of the decoder's DeltaNet layers, the step
+ * before each MoE layer in the reference model: deltanet_forward
+ * (c/src/model.c:1146-1278), per layer and per call of n tokens:
+ *   mixed = in_proj_qkv(x), z = in_proj_z(x)        (q4, model.c:1168-1170)
+ *   a = x.Wa^T, b = x.Wb^T                          (bf16, model.c:1172-1175)
+ *   causal depthwise conv over [conv_state; mixed], the state keeps the last
+ *   conv_kernel-1 rows, then silu                    (model.c:1177-1187)
+ *   q, k, v = split; q = l2norm(q) / sqrt(dk), k = l2norm(k)  (model.c:1202-1222)
+ *   per value head h (key head h / (hv/hk)), per token:
+ *     g = exp(-exp(A_log[h]) * log1p(exp(a[h] + dt_bias[h]))), beta = sigmoid(b[h])
+ *     S <- g S;  S += (beta (v - S k)) k^T;  o = S q  (S [dv, dk], model.c:1225-1248)
+ *   o_h = rmsnorm(o_h) * norm_w * sigmoid(z_h)       (model.c:1263-1274)
+ *   out = out_proj(o)                                (q4, model.c:1276)
+ * The conv and recurrent states live in HBM with the layer and carry over
+ * from call to call (tokens in order), as the reference's per-layer
+ * conv_state / rec_state.  Sums run in parallel orders: results agree with
+ * the reference to rounding, not bit for bit.  Weights, like the MoE
+ * layer's, use the checkpoint layout (names model.c:1866-1883):
+ * linear_attn.{in_proj_qkv,in_proj_z,out_proj} q4 (u32 codes, bf16
+ * scales/biases per 64 columns), in_proj_{a,b} and conv1d bf16, norm,
+ * A_log and dt_bias widened to f32 (the reference's mw_load_f32). */
+typedef struct qmoe_dn_ctx qmoe_dn_ctx;
+
+typedef struct {
+    int hidden;      /* d: multiple of 64, <= 8192 */
+    int n_k_heads;   /* hk: linear_num_key_heads */
+    int n_v_heads;   /* hv: linear_num_value_heads, a multiple of hk */
+    int k_head_dim;  /* dk: 32, 64, 128 or 256 */
+    int v_head_dim;  /* dv: multiple of 16; hv*dv a multiple of 256, <= 8192 */
+    int conv_kernel; /* linear_conv_kernel_dim, 1..16 */
+    int group_size;  /* must be 64 */
+    int n_layers;
+    int max_tokens;
+} qmoe_dn_config;
+
+/* conv_dim = 2*hk*dk + hv*dv, value_dim = hv*dv */
+typedef struct {
+    const uint32_t *qkv_q;   /* [conv_dim, d/8]   in_proj_qkv.weight */
+    const uint16_t *qkv_s;   /* [conv_dim, d/64]  .scales */
+    const uint16_t *qkv_b;   /* [conv_dim, d/64]  .biases */
+    const uint32_t *z_q;     /* [value_dim, d/8]  in_proj_z.* */
+    const uint16_t *z_s, *z_b;
+    const uint16_t *a_w;     /* [hv, d] bf16      in_proj_a.weight */
+    const uint16_t *b_w;     /* [hv, d] bf16      in_proj_b.weight */
+    const uint32_t *out_q;   /* [d, value_dim/8]  out_proj.* */
+    const uint16_t *out_s, *out_b;
+    const uint16_t *conv_w;  /* [conv_dim, conv_kernel] bf16  conv1d.weight */
+    const float *norm_w;     /* [dv]  norm.weight */
+    const float *a_log;      /* [hv]  A_log */
+    const float *dt_bias;    /* [hv]  dt_bias */
+} qmoe_dn_weights;
+
+int qmoe_dn_create(qmoe_dn_ctx **ctx, const qmoe_dn_config *cfg, qmoe_err *err);
+void qmoe_dn_destroy(qmoe_dn_ctx *ctx);
+/* copies one layer from HOST memory and clears its states */
+int qmoe_dn_upload_layer(qmoe_dn_ctx *ctx, int layer, const qmoe_dn_weights *host, qmoe_err *err);
+/* zeroes the conv and recurrent states of one layer (-1: every layer), as
+ * the reference's model reset (model.c:402-403), on `stream` */
+int qmoe_dn_reset_state(qmoe_dn_ctx *ctx, int layer, void *stream, qmoe_err *err);
+/* x [n, d] f32 device -> out [n, d] f32 device, n <= max_tokens; updates
+ * the layer's states.  Asynchronous on `stream`. */
+int qmoe_dn_forward(qmoe_dn_ctx *ctx, int layer, const float *x, int n, float *out, void *stream,
+                    qmoe_err *err);
+/* device addresses of a layer's states: conv [conv_kernel-1, conv_dim] and
+ * recurrent [hv, dv, dk] f32 (for inspection and for seeding a state) */
+int qmoe_dn_state(qmoe_dn_ctx *ctx, int layer, float **conv_state, float **rec_state,
+                  qmoe_err *err);
+
 #ifdef __cplusplus
 }
 #endif

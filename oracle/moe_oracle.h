@@ -207,6 +207,31 @@ int orc_moe_forward_warm(const orc_layer *L, const orc_warm *W, const void *x, i
 double orc_time_forward_warm(const orc_layer *L, const orc_warm *W, const void *x, int n,
                              float *out, const orc_opts *opt, int warmup, int iters);
 
+/* ---- gated DeltaNet mixer (dn_oracle.c; model.c:1146-1278) ---- */
+typedef struct {
+    int hidden;       /* d */
+    int n_k_heads;    /* linear_num_key_heads */
+    int n_v_heads;    /* linear_num_value_heads, a multiple of n_k_heads */
+    int k_head_dim;   /* dk */
+    int v_head_dim;   /* dv */
+    int conv_kernel;  /* linear_conv_kernel_dim */
+    int group_size;
+    const uint32_t *qkv_q; const uint16_t *qkv_s, *qkv_b;  /* in_proj_qkv [2*hk*dk + hv*dv, d] q4 */
+    const uint32_t *z_q; const uint16_t *z_s, *z_b;        /* in_proj_z [hv*dv, d] q4 */
+    const uint16_t *a_w, *b_w;                              /* in_proj_a, in_proj_b [hv, d] bf16 */
+    const uint32_t *out_q; const uint16_t *out_s, *out_b;  /* out_proj [d, hv*dv] q4 */
+    const uint16_t *conv_w;                                 /* conv1d [conv_dim, conv_kernel] bf16 */
+    const float *norm_w;                                    /* [dv] */
+    const float *a_log, *dt_bias;                           /* [hv] */
+} orc_dn;
+/* the decay factor exp(-exp(a_log) * log1p(exp(a + dt_bias))) of model.c:1229 */
+float orc_dn_decay(float a_log, float a, float dt_bias);
+/* x [n, d] f32 -> out [n, d]; conv_state [conv_kernel-1, conv_dim] and
+ * rec_state [hv, dv, dk] are read and updated in place; core_out (or NULL)
+ * receives the recurrence output [n, hv*dv] before the gated norm */
+int orc_dn_forward(const orc_dn *D, const float *x, int n, float *out, float *conv_state,
+                   float *rec_state, float *core_out);
+
 #ifdef __cplusplus
 }
 #endif

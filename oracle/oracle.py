@@ -23,6 +23,9 @@ TAG = dict(
     SH_DOWN_Q=17, SH_DOWN_S=18, SH_DOWN_B=19, SHGATE_W=20, X=22,
     HC_DOWN_Q=24, HC_DOWN_S=25, HC_DOWN_B=26, HC_UP_Q=27, HC_UP_S=28, HC_UP_B=29,
     HC_INJECT_W=30, HYPER=31,
+    DN_QKV_Q=40, DN_QKV_S=41, DN_QKV_B=42, DN_Z_Q=43, DN_Z_S=44, DN_Z_B=45, DN_A_W=46,
+    DN_B_W=47, DN_OUT_Q=48, DN_OUT_S=49, DN_OUT_B=50, DN_CONV_W=51, DN_NORM_W=52, DN_A_LOG=53,
+    DN_DT_BIAS=54, DN_X=55,
 )
 
 ROUTED_FAITHFUL, ROUTED_Q4 = 0, 1
@@ -54,6 +57,16 @@ class OrcHc(ctypes.Structure):
         ("hc", _I), ("d", _I), ("lowrank", _I), ("group_size", _I), ("hc_norm", _P),
         ("down_q", _P), ("down_s", _P), ("down_b", _P),
         ("up_q", _P), ("up_s", _P), ("up_b", _P), ("inject_w", _P),
+    ]
+
+
+class OrcDn(ctypes.Structure):
+    _fields_ = [
+        ("hidden", _I), ("n_k_heads", _I), ("n_v_heads", _I), ("k_head_dim", _I),
+        ("v_head_dim", _I), ("conv_kernel", _I), ("group_size", _I),
+        ("qkv_q", _P), ("qkv_s", _P), ("qkv_b", _P), ("z_q", _P), ("z_s", _P), ("z_b", _P),
+        ("a_w", _P), ("b_w", _P), ("out_q", _P), ("out_s", _P), ("out_b", _P), ("conv_w", _P),
+        ("norm_w", _P), ("a_log", _P), ("dt_bias", _P),
     ]
 
 
@@ -95,6 +108,8 @@ _SIG = {
     "orc_gen_normal_f32": (None, [_P, _SZ, _U64, _U64, _F]),
     "orc_gen_codes": (None, [_P, _SZ, _U64, _U64]),
     "orc_zipf_bias": (None, [_P, _I, ctypes.c_double, ctypes.c_double, _U64]),
+    "orc_dn_decay": (_F, [_F, _F, _F]),
+    "orc_dn_forward": (_I, [ctypes.POINTER(OrcDn), _P, _I, _P, _P, _P, _P]),
     "orc_time_forward": (ctypes.c_double, [ctypes.POINTER(OrcLayer), _P, _I, _P,
                                            ctypes.POINTER(OrcOpts), _I, _I]),
 }
@@ -418,6 +433,92 @@ class Hyper:
         r = layer.forward(m["mixed"], False)
         return dict(hyper=self.inject_update(hyper, m["inject"], r["out"]), moe_out=r["out"],
                     **m)
+
+
+class DeltaNet:
+    """One gated DeltaNet mixer (c/src/model.c:1146-1278) in host memory,
+    checkpoint layout (names model.c:1866-1883): in_proj_qkv [conv_dim, d],
+    in_proj_z [value_dim, d] and out_proj [d, value_dim] q4 (codes
+    U{0..15}, scales N(0,0.02), biases N(0,0.01)); in_proj_a, in_proj_b
+    [hv, d] bf16 N(0,0.02); conv1d [conv_dim, kc] bf16 N(0, conv_std);
+    norm.weight [dv] = 1 + N(0,0.1), A_log and dt_bias [hv] N(0,1), all
+    three rounded to bf16 and widened, as the reference loads them
+    (mw_load_f32, model.c:275-293)."""
+
+    KEYS = ("qkv_q", "qkv_s", "qkv_b", "z_q", "z_s", "z_b", "a_w", "b_w", "out_q", "out_s",
+            "out_b", "conv_w", "norm_w", "a_log", "dt_bias")
+
+    def __init__(self, d, hk, hv, dk, dv, kc=4, seed=0, layer=0, group_size=64, conv_std=0.5):
+        self.d, self.hk, self.hv, self.dk, self.dv, self.kc, self.g = d, hk, hv, dk, dv, kc, group_size
+        self.key_dim, self.value_dim = hk * dk, hv * dv
+        self.conv_dim = 2 * self.key_dim + self.value_dim
+        cd, vd, g, s, L = self.conv_dim, self.value_dim, group_size, seed, layer
+        t = {}
+        t["qkv_q"] = gen_codes(cd * d // 8, s, L, "DN_QKV_Q")
+        t["qkv_s"] = gen_bf16(cd * d // g, s, L, "DN_QKV_S", 0.02)
+        t["qkv_b"] = gen_bf16(cd * d // g, s, L, "DN_QKV_B", 0.01)
+        t["z_q"] = gen_codes(vd * d // 8, s, L, "DN_Z_Q")
+        t["z_s"] = gen_bf16(vd * d // g, s, L, "DN_Z_S", 0.02)
+        t["z_b"] = gen_bf16(vd * d // g, s, L, "DN_Z_B", 0.01)
+        t["a_w"] = gen_bf16(hv * d, s, L, "DN_A_W", 0.02)
+        t["b_w"] = gen_bf16(hv * d, s, L, "DN_B_W", 0.02)
+        t["out_q"] = gen_codes(d * vd // 8, s, L, "DN_OUT_Q")
+        t["out_s"] = gen_bf16(d * vd // g, s, L, "DN_OUT_S", 0.02)
+        t["out_b"] = gen_bf16(d * vd // g, s, L, "DN_OUT_B", 0.01)
+        t["conv_w"] = gen_bf16(cd * kc, s, L, "DN_CONV_W", conv_std)
+        t["norm_w"] = bf16_to_f32(f32_to_bf16(1.0 + gen_f32(dv, s, L, "DN_NORM_W", 0.1)))
+        t["a_log"] = bf16_to_f32(gen_bf16(hv, s, L, "DN_A_LOG", 1.0))
+        t["dt_bias"] = bf16_to_f32(gen_bf16(hv, s, L, "DN_DT_BIAS", 1.0))
+        self.t = t
+        self._build()
+
+    @classmethod
+    def from_arrays(cls, d, hk, hv, dk, dv, kc, arrays, group_size=64):
+        self = cls.__new__(cls)
+        self.d, self.hk, self.hv, self.dk, self.dv, self.kc, self.g = d, hk, hv, dk, dv, kc, group_size
+        self.key_dim, self.value_dim = hk * dk, hv * dv
+        self.conv_dim = 2 * self.key_dim + self.value_dim
+        self.t = {k: np.ascontiguousarray(arrays[k]) for k in cls.KEYS}
+        self._build()
+        return self
+
+    def _build(self):
+        st = OrcDn()
+        st.hidden, st.n_k_heads, st.n_v_heads = self.d, self.hk, self.hv
+        st.k_head_dim, st.v_head_dim, st.conv_kernel, st.group_size = self.dk, self.dv, self.kc, self.g
+        for f, a in self.t.items():
+            setattr(st, f, _p(a))
+        self.st = st
+
+    def arrays(self):
+        return dict(self.t)
+
+    def new_state(self):
+        return (np.zeros((self.kc - 1, self.conv_dim), np.float32),
+                np.zeros((self.hv, self.dv, self.dk), np.float32))
+
+    def forward(self, x, conv_state, rec_state, want_core=False):
+        """x [n, d] f32; conv_state, rec_state updated IN PLACE (float32,
+        C-contiguous); returns out [n, d] (and the recurrence output)"""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        assert conv_state.dtype == np.float32 and conv_state.flags.c_contiguous
+        assert rec_state.dtype == np.float32 and rec_state.flags.c_contiguous
+        n = x.shape[0]
+        out = np.empty((n, self.d), np.float32)
+        core = np.empty((n, self.value_dim), np.float32) if want_core else None
+        if lib().orc_dn_forward(ctypes.byref(self.st), _p(x), n, _p(out), _p(conv_state),
+                                _p(rec_state), _p(core)):
+            raise MemoryError("orc_dn_forward")
+        return (out, core) if want_core else out
+
+
+def dn_decay(a_log, a, dt_bias):
+    return lib().orc_dn_decay(a_log, a, dt_bias)
+
+
+def gen_dn_x(n, d, seed, layer=0, std=1.0):
+    """DeltaNet inputs [n, d] f32 from their own stream"""
+    return gen_f32(n * d, seed, layer, "DN_X", std).reshape(n, d)
 
 
 def gen_hyper(n, hc, d, seed, layer=0, std=1.0):

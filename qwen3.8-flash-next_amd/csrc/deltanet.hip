@@ -1,0 +1,437 @@
+/*
+ * deltanet.hip -- the gated DeltaNet mixer (linear attention) on gfx950,
+ * replacing deltanet_forward of the reference C port (c/src/model.c:
+ * 1146-1278) for n tokens in three launches:
+ *
+ *   k_dn_in   one wave per four rows of [in_proj_qkv | in_proj_z | in_proj_a
+ *             | in_proj_b]: the q4 rows with the per-group identity of
+ *             gemm_q4 (kernel.c:279-282, gemv_parts.h), the bf16 rows as
+ *             dot products of bf16 pairs; x (f32) enters as bf16 hi + lo
+ *             pairs.  Writes mixed [n, conv_dim], z [n, value_dim], a, b
+ *             [n, hv].
+ *   k_dn_rec  one workgroup per (value head, block of 16 state rows), the
+ *             state rows in registers across the tokens: per token the
+ *             causal depthwise conv over [conv_state; mixed] (kernel.c:
+ *             311-324) + silu for the head's q and k channels and its v
+ *             rows, l2norm(q)*dk^-1/2 and l2norm(k) (kernel.c:73-78), the
+ *             decay exp(-exp(A_log) softplus(a + dt_bias)) and beta =
+ *             sigmoid(b), then per row S <- g S; kv = S.k; S += k (beta
+ *             (v - kv)); o = S.q (model.c:1225-1248).  Writes o [n, value_dim]
+ *             and the new recurrent state.
+ *   k_dn_out  per token the gated norm rmsnorm(o_h) * norm_w * sigmoid(z_h)
+ *             (model.c:1263-1274) into LDS, then one wave per four rows of
+ *             out_proj (q4); also moves the conv state on by n tokens (its
+ *             old rows are read by k_dn_rec, so it changes only here).
+ *
+ * Sums run in parallel orders (lane trees), so results match the reference
+ * to rounding, not bit for bit.
+ */
+#include "qk_device.h"
+#include "gemv_parts.h"
+
+#define DN_RPW 4   /* rows per wave in the two GEMV kernels */
+#define DN_RB 16   /* state rows per recurrence workgroup */
+
+struct DnInArgs {
+    const uint32_t *qkv_q, *z_q;
+    const uint16_t *qkv_s, *qkv_b, *z_s, *z_b;
+    const uint16_t *a_w, *b_w;
+    const float *x;  /* [n, d] */
+    float *mixed;    /* [n, conv_dim] */
+    float *z;        /* [n, value_dim] */
+    float *a, *b;    /* [n, hv] */
+    int d, n, conv_dim, value_dim, hv;
+};
+
+/* x chunks of token t as bf16 pairs: lane owns chunks ps*64 + lane */
+template <int P>
+__device__ __forceinline__ void dn_x_pairs(const float *x, int t, int K, int lane, XPairs<64, P, false> &xp) {
+    XRaw<P, false> xr;
+    load_xraw<64, P, false>(x, (size_t)t, K, lane, xr);
+    convert_xraw<64, P, false>(xr, K, lane, xp);
+}
+
+template <int P>
+__global__ __launch_bounds__(256) void k_dn_in(DnInArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * DN_RPW;
+    const int R1 = a.conv_dim, R2 = R1 + a.value_dim, R3 = R2 + a.hv, R = R3 + a.hv;
+    if (r0 >= R) return;
+    const int CH = a.d >> 5, G = a.d >> 6;
+    const size_t wrow = (size_t)a.d >> 3;
+    if (r0 < R2) {
+        /* q4 rows: codes, scales and biases of the wave's rows stay in registers */
+        uint4 wq[DN_RPW][P];
+        float ws[DN_RPW][P], wb[DN_RPW][P];
+#pragma unroll
+        for (int j = 0; j < DN_RPW; j++) {
+            const int r = min(r0 + j, R2 - 1);
+            const bool z = r >= R1;
+            const int rr = z ? r - R1 : r;
+            const uint32_t *q = (z ? a.z_q : a.qkv_q) + (size_t)rr * wrow;
+            const uint16_t *s = (z ? a.z_s : a.qkv_s) + (size_t)rr * G;
+            const uint16_t *bb = (z ? a.z_b : a.qkv_b) + (size_t)rr * G;
+#pragma unroll
+            for (int ps = 0; ps < P; ps++) {
+                const int c0 = ps * 64 + lane;
+                const bool ok = c0 < CH;
+                const int c = ok ? c0 : 0;
+                wq[j][ps] = qk_ld((const uint4 *)(q + 4 * (size_t)c));
+                ws[j][ps] = ok ? qk_bf16(qk_ld(s + (c >> 1))) : 0.0f;
+                wb[j][ps] = ok ? qk_bf16(qk_ld(bb + (c >> 1))) : 0.0f;
+                if (!ok) wq[j][ps] = make_uint4(0u, 0u, 0u, 0u);
+            }
+        }
+        for (int t = 0; t < a.n; t++) {
+            XPairs<64, P, false> xp;
+            dn_x_pairs<P>(a.x, t, a.d, lane, xp);
+#pragma unroll
+            for (int j = 0; j < DN_RPW; j++) {
+                const float v = qk_group_sum<64>(row_part<64, P, false>(wq[j], ws[j], wb[j], xp));
+                const int r = r0 + j;
+                if (lane == 0 && r < R2) {
+                    if (r < R1) qk_st(a.mixed + (size_t)t * a.conv_dim + r, v);
+                    else qk_st(a.z + (size_t)t * a.value_dim + (r - R1), v);
+                }
+            }
+        }
+        return;
+    }
+    /* bf16 rows (in_proj_a, in_proj_b): w pairs against the x pairs */
+    for (int t = 0; t < a.n; t++) {
+        XPairs<64, P, false> xp;
+        dn_x_pairs<P>(a.x, t, a.d, lane, xp);
+#pragma unroll
+        for (int j = 0; j < DN_RPW; j++) {
+            const int r = r0 + j;
+            const int rc = min(r, R - 1);
+            const bool isb = rc >= R3;
+            const uint16_t *w = (isb ? a.b_w : a.a_w) + (size_t)(isb ? rc - R3 : rc - R2) * a.d;
+            float part = 0.0f;
+#pragma unroll
+            for (int ps = 0; ps < P; ps++) {
+                const int c0 = ps * 64 + lane;
+                const bool ok = c0 < CH;
+                const uint4 *src = (const uint4 *)(w + 32 * (size_t)(ok ? c0 : 0));
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    uint32_t wp[4];
+                    qk_bf16x8_to_pairs(qk_ld(src + g), wp);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const uint32_t w2 = ok ? wp[i] : 0u;
+                        part = qk_dot2(xp.hi[ps][4 * g + i], w2, part);
+                        part = qk_dot2(xp.lo[ps][4 * g + i], w2, part);
+                    }
+                }
+            }
+            const float v = qk_group_sum<64>(part);
+            if (lane == 0 && r < R) {
+                if (r < R3) qk_st(a.a + (size_t)t * a.hv + (r - R2), v);
+                else qk_st(a.b + (size_t)t * a.hv + (r - R3), v);
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------ recurrence */
+
+struct DnRecArgs {
+    const float *mixed, *a, *b;  /* [n, conv_dim], [n, hv], [n, hv] */
+    const float *conv_state;     /* [kc-1, conv_dim], the state before these tokens */
+    const uint16_t *conv_w;      /* [conv_dim, kc] */
+    const float *a_log, *dt_bias;
+    float *rec_state;            /* [hv, dv, dk] */
+    float *core;                 /* [n, value_dim] */
+    int n, hk, hv, dk, dv, kc, conv_dim;
+};
+
+/* silu(conv) of channel c at token t: sum over taps i of w[c, i] * seq[t+i, c]
+ * with seq = [conv_state rows; mixed rows] */
+__device__ __forceinline__ float dn_conv_silu(const DnRecArgs &a, int t, int c) {
+    float acc = 0.0f;
+    for (int i = 0; i < a.kc; i++) {
+        const int j = t + i;
+        const float s = j < a.kc - 1 ? qk_ld(a.conv_state + (size_t)j * a.conv_dim + c)
+                                     : qk_ld(a.mixed + (size_t)(j - (a.kc - 1)) * a.conv_dim + c);
+        acc = fmaf(s, qk_bf16(qk_ld(a.conv_w + (size_t)c * a.kc + i)), acc);
+    }
+    return qk_silu(acc);
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void k_dn_rec(DnRecArgs a) {
+    constexpr int DK = 16 * EPL;
+    __shared__ float s_ch[2 * DK + DN_RB]; /* q, k, v of the block's rows */
+    __shared__ float s_sc[4];              /* q and k norms, decay, beta */
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = blockIdx.y, rb = blockIdx.x * DN_RB;
+    const int kh = h / (a.hv / a.hk);
+    const int key_dim = a.hk * DK, value_dim = a.hv * a.dv;
+    const int row = rb + (tid >> 4), i0 = (tid & 15) * EPL;
+    float *srow = a.rec_state + ((size_t)h * a.dv + row) * DK + i0;
+    float s[EPL];
+    if (EPL % 4 == 0) {
+#pragma unroll
+        for (int e = 0; e < EPL; e += 4) {
+            const float4 v = qk_ld((const float4 *)(srow + e));
+            s[e] = v.x; s[e + 1] = v.y; s[e + 2] = v.z; s[e + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < EPL; e++) s[e] = qk_ld(srow + e);
+    }
+    const float al = expf(qk_ld(a.a_log + h)), dtb = qk_ld(a.dt_bias + h);
+    const float scale_q = 1.0f / sqrtf((float)DK);
+    for (int t = 0; t < a.n; t++) {
+        for (int c = tid; c < 2 * DK + DN_RB; c += 256) {
+            const int ch = c < DK ? kh * DK + c
+                         : c < 2 * DK ? key_dim + kh * DK + (c - DK)
+                                      : 2 * key_dim + h * a.dv + rb + (c - 2 * DK);
+            s_ch[c] = dn_conv_silu(a, t, ch);
+        }
+        __syncthreads();
+        if (wave < 2) {
+            /* wave 0: |q|^2, wave 1: |k|^2 */
+            float ss = 0.0f;
+            for (int i = lane; i < DK; i += 64) {
+                const float v = s_ch[wave * DK + i];
+                ss = fmaf(v, v, ss);
+            }
+            ss = qk_group_sum<64>(ss);
+            if (lane == 0) s_sc[wave] = 1.0f / sqrtf(ss + 1e-6f);
+        } else if (tid == 128) {
+            const float av = qk_ld(a.a + (size_t)t * a.hv + h), bv = qk_ld(a.b + (size_t)t * a.hv + h);
+            s_sc[2] = expf(-al * log1pf(expf(av + dtb)));
+            s_sc[3] = 1.0f / (1.0f + expf(-bv));
+        }
+        __syncthreads();
+        const float rq = s_sc[0], rk = s_sc[1], g = s_sc[2], beta = s_sc[3];
+        float kk[EPL], qq[EPL];
+#pragma unroll
+        for (int e = 0; e < EPL; e++) {
+            kk[e] = s_ch[DK + i0 + e] * rk;
+            qq[e] = (s_ch[i0 + e] * rq) * scale_q;
+        }
+        float kv = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) {
+            s[e] = s[e] * g;
+            kv = fmaf(s[e], kk[e], kv);
+        }
+        kv = qk_group_sum<16>(kv);
+        const float delta = (s_ch[2 * DK + (tid >> 4)] - kv) * beta;
+        float o = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) {
+            s[e] = fmaf(kk[e], delta, s[e]);
+            o = fmaf(s[e], qq[e], o);
+        }
+        o = qk_group_sum<16>(o);
+        if ((tid & 15) == 0) qk_st(a.core + (size_t)t * value_dim + (size_t)h * a.dv + row, o);
+        __syncthreads(); /* s_ch, s_sc are rewritten for the next token */
+    }
+    if (EPL % 4 == 0) {
+#pragma unroll
+        for (int e = 0; e < EPL; e += 4)
+            qk_st((float4 *)(srow + e), make_float4(s[e], s[e + 1], s[e + 2], s[e + 3]));
+    } else {
+#pragma unroll
+        for (int e = 0; e < EPL; e++) qk_st(srow + e, s[e]);
+    }
+}
+
+/* ------------------------------------------------------------ out_proj */
+
+struct DnOutArgs {
+    const uint32_t *out_q;
+    const uint16_t *out_s, *out_b;
+    const float *core, *z;     /* [n, value_dim] */
+    const float *norm_w;       /* [dv] */
+    const float *mixed;        /* [n, conv_dim] */
+    float *conv_state;         /* [kc-1, conv_dim], moved on by n tokens */
+    float *out;                /* [n, d] */
+    int n, d, value_dim, dv, kc, conv_dim, ch_per_wg;
+};
+
+template <int P>
+__global__ __launch_bounds__(256) void k_dn_out(DnOutArgs a) {
+    extern __shared__ float dn_lds[];
+    float *s_act = dn_lds;                 /* [value_dim] */
+    float *s_ss = dn_lds + a.value_dim;    /* [256] */
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int K = a.value_dim, CH = K >> 5, G = K >> 6;
+    const size_t wrow = (size_t)K >> 3;
+
+    /* the conv state: channels [c0, c0 + ch_per_wg) move on by n tokens */
+    {
+        const int c = blockIdx.x * a.ch_per_wg + tid;
+        if (tid < a.ch_per_wg && c < a.conv_dim) {
+            for (int j = 0; j < a.kc - 1; j++) {
+                const int m = a.n + j;
+                const float v = m < a.kc - 1 ? a.conv_state[(size_t)m * a.conv_dim + c]
+                                             : qk_ld(a.mixed + (size_t)(m - (a.kc - 1)) * a.conv_dim + c);
+                a.conv_state[(size_t)j * a.conv_dim + c] = v;
+            }
+        }
+    }
+
+    const int r0 = (blockIdx.x * 4 + (tid >> 6)) * DN_RPW;
+    uint4 wq[DN_RPW][P];
+    float ws[DN_RPW][P], wb[DN_RPW][P];
+#pragma unroll
+    for (int j = 0; j < DN_RPW; j++) {
+        const int r = min(r0 + j, a.d - 1);
+#pragma unroll
+        for (int ps = 0; ps < P; ps++) {
+            const int c0 = ps * 64 + lane;
+            const bool ok = c0 < CH;
+            const int c = ok ? c0 : 0;
+            wq[j][ps] = qk_ld((const uint4 *)(a.out_q + (size_t)r * wrow + 4 * (size_t)c));
+            ws[j][ps] = ok ? qk_bf16(qk_ld(a.out_s + (size_t)r * G + (c >> 1))) : 0.0f;
+            wb[j][ps] = ok ? qk_bf16(qk_ld(a.out_b + (size_t)r * G + (c >> 1))) : 0.0f;
+            if (!ok) wq[j][ps] = make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+    const int EPT = K / 256;          /* elements per thread in the norm */
+    const int TPH = a.dv / EPT;       /* threads per head */
+    for (int t = 0; t < a.n; t++) {
+        const float *o = a.core + (size_t)t * K + (size_t)tid * EPT;
+        float ss = 0.0f;
+        for (int e = 0; e < EPT; e++) {
+            const float v = qk_ld(o + e);
+            ss = fmaf(v, v, ss);
+        }
+        s_ss[tid] = ss;
+        __syncthreads();
+        /* the head's sum of squares: its TPH threads' partials in order */
+        const int hb = (tid / TPH) * TPH;
+        float hs = 0.0f;
+        for (int j = 0; j < TPH; j++) hs = hs + s_ss[hb + j];
+        const float r = 1.0f / sqrtf(hs / (float)a.dv + 1e-6f);
+        for (int e = 0; e < EPT; e++) {
+            const int i = tid * EPT + e;
+            const float zv = qk_ld(a.z + (size_t)t * K + i);
+            s_act[i] = ((qk_ld(o + e) * r) * qk_ld(a.norm_w + i % a.dv)) * (1.0f / (1.0f + expf(-zv)));
+        }
+        __syncthreads();
+        if (r0 < a.d) {
+            XRaw<P, false> xr;
+#pragma unroll
+            for (int ps = 0; ps < P; ps++) {
+                const int c0 = ps * 64 + lane;
+                const int c = c0 < CH ? c0 : 0;
+                const float4 *src = (const float4 *)(s_act + 32 * c);
+#pragma unroll
+                for (int w = 0; w < 8; w++) xr.f[ps][w] = src[w];
+            }
+            XPairs<64, P, false> xp;
+            convert_xraw<64, P, false>(xr, K, lane, xp);
+#pragma unroll
+            for (int j = 0; j < DN_RPW; j++) {
+                const float v = qk_group_sum<64>(row_part<64, P, false>(wq[j], ws[j], wb[j], xp));
+                const int rr = r0 + j;
+                if (lane == 0 && rr < a.d) qk_st(a.out + (size_t)t * a.d + rr, v);
+            }
+        }
+        __syncthreads(); /* s_act, s_ss are rewritten for the next token */
+    }
+}
+
+/* ------------------------------------------------------------ host side */
+
+extern "C" int qk_dn_shape_ok(const qk_dn_shape *s) {
+    const int key_dim = s->hk * s->dk, value_dim = s->hv * s->dv;
+    const int conv_dim = 2 * key_dim + value_dim;
+    if (s->d <= 0 || s->d % 64 || s->d > 8192) return 0;
+    if (s->hk <= 0 || s->hv <= 0 || s->hv % s->hk) return 0;
+    if (!(s->dk == 32 || s->dk == 64 || s->dk == 128 || s->dk == 256)) return 0;
+    if (s->dv <= 0 || s->dv % DN_RB) return 0;
+    if (value_dim % 256 || value_dim > 8192 || s->dv % (value_dim / 256)) return 0;
+    if ((s->dv / (value_dim / 256)) > 256) return 0;
+    if (s->kc < 1 || s->kc > 16) return 0;
+    if (conv_dim <= 0) return 0;
+    return 1;
+}
+
+extern "C" size_t qk_dn_out_lds(const qk_dn_shape *s) {
+    return ((size_t)s->hv * s->dv + 256) * sizeof(float);
+}
+
+extern "C" int qk_launch_dn(const qk_dn_shape *s, const qk_dn_dev *W, const float *x, int n, float *out,
+                            float *conv_state, float *rec_state, float *mixed, float *z, float *av,
+                            float *bv, float *core, void *stream) {
+    if (n <= 0) return 0;
+    if (!qk_dn_shape_ok(s)) return (int)hipErrorInvalidValue;
+    hipStream_t st = (hipStream_t)stream;
+    const int key_dim = s->hk * s->dk, value_dim = s->hv * s->dv;
+    const int conv_dim = 2 * key_dim + value_dim;
+
+    DnInArgs ia;
+    ia.qkv_q = W->qkv_q; ia.qkv_s = W->qkv_s; ia.qkv_b = W->qkv_b;
+    ia.z_q = W->z_q; ia.z_s = W->z_s; ia.z_b = W->z_b;
+    ia.a_w = W->a_w; ia.b_w = W->b_w;
+    ia.x = x; ia.mixed = mixed; ia.z = z; ia.a = av; ia.b = bv;
+    ia.d = s->d; ia.n = n; ia.conv_dim = conv_dim; ia.value_dim = value_dim; ia.hv = s->hv;
+    const int rows = conv_dim + value_dim + 2 * s->hv;
+    const int waves = (rows + DN_RPW - 1) / DN_RPW;
+    const dim3 igrid((waves + 3) / 4);
+    const int p_in = (s->d / 32 + 63) / 64;
+    switch (p_in) {
+    case 1: hipLaunchKernelGGL(k_dn_in<1>, igrid, dim3(256), 0, st, ia); break;
+    case 2: hipLaunchKernelGGL(k_dn_in<2>, igrid, dim3(256), 0, st, ia); break;
+    case 3: hipLaunchKernelGGL(k_dn_in<3>, igrid, dim3(256), 0, st, ia); break;
+    default: hipLaunchKernelGGL(k_dn_in<4>, igrid, dim3(256), 0, st, ia); break;
+    }
+    int rc = QK_CHECK_LAUNCH();
+    if (rc) return rc;
+
+    DnRecArgs ra;
+    ra.mixed = mixed; ra.a = av; ra.b = bv;
+    ra.conv_state = conv_state; ra.conv_w = W->conv_w;
+    ra.a_log = W->a_log; ra.dt_bias = W->dt_bias;
+    ra.rec_state = rec_state; ra.core = core;
+    ra.n = n; ra.hk = s->hk; ra.hv = s->hv; ra.dk = s->dk; ra.dv = s->dv; ra.kc = s->kc;
+    ra.conv_dim = conv_dim;
+    const dim3 rgrid(s->dv / DN_RB, s->hv);
+    switch (s->dk) {
+    case 32: hipLaunchKernelGGL(k_dn_rec<2>, rgrid, dim3(256), 0, st, ra); break;
+    case 64: hipLaunchKernelGGL(k_dn_rec<4>, rgrid, dim3(256), 0, st, ra); break;
+    case 128: hipLaunchKernelGGL(k_dn_rec<8>, rgrid, dim3(256), 0, st, ra); break;
+    default: hipLaunchKernelGGL(k_dn_rec<16>, rgrid, dim3(256), 0, st, ra); break;
+    }
+    rc = QK_CHECK_LAUNCH();
+    if (rc) return rc;
+
+    DnOutArgs oa;
+    oa.out_q = W->out_q; oa.out_s = W->out_s; oa.out_b = W->out_b;
+    oa.core = core; oa.z = z; oa.norm_w = W->norm_w; oa.mixed = mixed;
+    oa.conv_state = conv_state; oa.out = out;
+    oa.n = n; oa.d = s->d; oa.value_dim = value_dim; oa.dv = s->dv; oa.kc = s->kc;
+    oa.conv_dim = conv_dim;
+    const int owgs = (s->d + 4 * DN_RPW - 1) / (4 * DN_RPW);
+    oa.ch_per_wg = (conv_dim + owgs - 1) / owgs;
+    if (oa.ch_per_wg > 256) return (int)hipErrorInvalidValue;
+    const size_t lds = qk_dn_out_lds(s);
+    const int p_out = (value_dim / 32 + 63) / 64;
+    switch (p_out) {
+    case 1: hipLaunchKernelGGL(k_dn_out<1>, dim3(owgs), dim3(256), lds, st, oa); break;
+    case 2: hipLaunchKernelGGL(k_dn_out<2>, dim3(owgs), dim3(256), lds, st, oa); break;
+    case 3: hipLaunchKernelGGL(k_dn_out<3>, dim3(owgs), dim3(256), lds, st, oa); break;
+    default: hipLaunchKernelGGL(k_dn_out<4>, dim3(owgs), dim3(256), lds, st, oa); break;
+    }
+    return QK_CHECK_LAUNCH();
+}
+
+/* a fill kernel for the state (graph capture records no memset node) */
+__global__ __launch_bounds__(256) void k_dn_zero(float *p, size_t count) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < count) p[i] = 0.0f;
+}
+
+extern "C" int qk_launch_dn_zero(float *p, size_t count, void *stream) {
+    if (count == 0) return 0;
+    hipLaunchKernelGGL(k_dn_zero, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       p, count);
+    return QK_CHECK_LAUNCH();
+}

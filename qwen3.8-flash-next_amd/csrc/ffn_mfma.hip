@@ -372,7 +372,7 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, MmSmem<TERMS, BMT, CT, 
 #pragma unroll
                     for (int h2 = 0; h2 < CT / 2; h2++)
                         qk_st(o + mm_col<false, CT>(nt, wave, h2, c),
-                              qk_silu(acc[rt][h2][i]) * acc[rt][CT / 2 + h2][i]);
+                              qk_silu_fast(acc[rt][h2][i]) * acc[rt][CT / 2 + h2][i]);
                 }
             }
         }

@@ -138,6 +138,11 @@ __device__ __forceinline__ void qk_f32x8_to_pairs(const float x[8], uint32_t hi[
 
 __device__ __forceinline__ float qk_silu(float v) { return v / (1.0f + expf(-v)); }
 __device__ __forceinline__ float qk_sigmoid(float v) { return 1.0f / (1.0f + expf(-v)); }
+/* silu with the hardware exp2 and reciprocal (a few ulp): for epilogues
+ * where the correctly rounded division costs more than the output is worth */
+__device__ __forceinline__ float qk_silu_fast(float v) {
+    return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v));
+}
 
 /* ------------------------------------------------ cross-lane reductions
  * DPP moves within a 16-lane row (no LDS round trip), ds_bpermute for the

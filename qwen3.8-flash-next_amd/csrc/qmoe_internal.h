@@ -192,6 +192,26 @@ int qk_launch_dec_layer(const qmoe_layer_weights *W, qk_shape s, const void *x, 
                         int32_t *segtab, const void *x_res, float *out, float *hyper,
                         const float *inject, int hc, void *stream);
 
+/* the gated DeltaNet mixer (deltanet.hip) */
+typedef struct {
+    int d, hk, hv, dk, dv, kc; /* hidden, key/value heads, head dims, conv taps */
+} qk_dn_shape;
+typedef struct {
+    const uint32_t *qkv_q, *z_q, *out_q;
+    const uint16_t *qkv_s, *qkv_b, *z_s, *z_b, *out_s, *out_b;
+    const uint16_t *a_w, *b_w, *conv_w;
+    const float *norm_w, *a_log, *dt_bias;
+} qk_dn_dev;
+int qk_dn_shape_ok(const qk_dn_shape *s);
+size_t qk_dn_out_lds(const qk_dn_shape *s);
+/* x [n, d] f32 -> out [n, d]; conv_state and rec_state are updated;
+ * mixed [n, conv_dim], z [n, value_dim], a, b [n, hv], core [n, value_dim]
+ * are scratch */
+int qk_launch_dn(const qk_dn_shape *s, const qk_dn_dev *W, const float *x, int n, float *out,
+                 float *conv_state, float *rec_state, float *mixed, float *z, float *a, float *b,
+                 float *core, void *stream);
+int qk_launch_dn_zero(float *p, size_t count, void *stream);
+
 /* the MLP hyper connection (hyper.hip): shapes it takes (hc <= 8, d and R
  * multiples of 64, d <= 2048, R <= 2048) */
 int qk_hc_shape_ok(int hc, int d, int R);

@@ -72,6 +72,20 @@ class QmoeError(RuntimeError):
     pass
 
 
+class QmoeDnConfig(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_int) for f in ("hidden", "n_k_heads", "n_v_heads", "k_head_dim",
+                                            "v_head_dim", "conv_kernel", "group_size", "n_layers",
+                                            "max_tokens")]
+
+
+DN_FIELDS = ["qkv_q", "qkv_s", "qkv_b", "z_q", "z_s", "z_b", "a_w", "b_w", "out_q", "out_s", "out_b",
+             "conv_w", "norm_w", "a_log", "dt_bias"]
+
+
+class QmoeDnWeights(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_void_p) for f in DN_FIELDS]
+
+
 class QmoeStTensor(ctypes.Structure):
     _fields_ = [("dtype", ctypes.c_int), ("ndim", ctypes.c_int), ("shape", ctypes.c_int64 * 8),
                 ("file", ctypes.c_int), ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64)]
@@ -104,6 +118,12 @@ SIGNATURES = {
     "qmoe_layer_forward": (_I, [_P, _I, _P, _I, _I, _P, _I, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_moe_forward_host": (_I, [_P, _I, _P, _I, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_set_fused_decode": (_I, [_P, _I, ctypes.POINTER(QmoeErr)]),
+    "qmoe_dn_create": (_I, [ctypes.POINTER(_P), ctypes.POINTER(QmoeDnConfig), ctypes.POINTER(QmoeErr)]),
+    "qmoe_dn_destroy": (None, [_P]),
+    "qmoe_dn_upload_layer": (_I, [_P, _I, ctypes.POINTER(QmoeDnWeights), ctypes.POINTER(QmoeErr)]),
+    "qmoe_dn_reset_state": (_I, [_P, _I, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_dn_forward": (_I, [_P, _I, _P, _I, _P, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_dn_state": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(_P), ctypes.POINTER(QmoeErr)]),
     "qmoe_decode_status": (_I, [_P, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(QmoeErr)]),
     "qmoe_last_routing": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_scratch_bytes": (ctypes.c_size_t, [_P]),
@@ -678,6 +698,87 @@ class ExpertCache:
         out = (ctypes.c_uint64 * 4)()
         lib().qmoe_xcache_counts(self._h, ctypes.byref(out))
         return dict(hits=out[0], misses=out[1], evictions=out[2], rejected=out[3])
+
+
+class DeltaNetContext:
+    """Owns a qmoe_dn_ctx: the gated DeltaNet mixer's resident layers (weights
+    and conv/recurrent states) plus device scratch."""
+
+    def __init__(self, hidden, n_k_heads, n_v_heads, k_head_dim, v_head_dim, conv_kernel=4,
+                 n_layers=1, max_tokens=1, group_size=64):
+        self.cfg = QmoeDnConfig(hidden, n_k_heads, n_v_heads, k_head_dim, v_head_dim, conv_kernel,
+                                group_size, n_layers, max_tokens)
+        self.d, self.hk, self.hv, self.dk, self.dv, self.kc = (hidden, n_k_heads, n_v_heads,
+                                                              k_head_dim, v_head_dim, conv_kernel)
+        self.conv_dim = 2 * n_k_heads * k_head_dim + n_v_heads * v_head_dim
+        self._h = ctypes.c_void_p()
+        err = QmoeErr()
+        _check(lib().qmoe_dn_create(ctypes.byref(self._h), ctypes.byref(self.cfg), ctypes.byref(err)),
+               err, "qmoe_dn_create")
+
+    def close(self):
+        if self._h:
+            lib().qmoe_dn_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def upload_layer(self, layer: int, host: dict):
+        """host: numpy arrays keyed by DN_FIELDS (codes u32, bf16 bits u16, f32)"""
+        import numpy as np
+        w = QmoeDnWeights()
+        keep = []
+        for f in DN_FIELDS:
+            a = host.get(f)
+            if a is not None:
+                a = np.ascontiguousarray(a)
+                keep.append(a)
+            setattr(w, f, None if a is None else a.ctypes.data)
+        err = QmoeErr()
+        _check(lib().qmoe_dn_upload_layer(self._h, layer, ctypes.byref(w), ctypes.byref(err)), err,
+               "qmoe_dn_upload_layer")
+
+    def reset_state(self, layer=-1, stream=None):
+        err = QmoeErr()
+        _check(lib().qmoe_dn_reset_state(self._h, layer, _stream(stream), ctypes.byref(err)), err,
+               "qmoe_dn_reset_state")
+
+    def forward(self, layer, x, out=None, stream=None):
+        """x [n, d] f32 CUDA tensor -> out [n, d] f32; the layer's states advance by n tokens"""
+        import torch
+        n = x.shape[0]
+        if out is None:
+            out = torch.empty((n, self.d), dtype=torch.float32, device=x.device)
+        err = QmoeErr()
+        _check(lib().qmoe_dn_forward(self._h, layer, _ptr(x), n, _ptr(out), _stream(stream),
+                                     ctypes.byref(err)), err, "qmoe_dn_forward")
+        return out
+
+    def forward_raw(self, layer, x_ptr, n, out_ptr, stream_handle):
+        """no-allocation variant for timing loops; returns the rc and message"""
+        err = QmoeErr()
+        rc = lib().qmoe_dn_forward(self._h, layer, x_ptr, n, out_ptr, stream_handle, ctypes.byref(err))
+        return rc, err.msg.decode(errors="replace")
+
+    def state_ptrs(self, layer):
+        conv, rec = ctypes.c_void_p(), ctypes.c_void_p()
+        err = QmoeErr()
+        _check(lib().qmoe_dn_state(self._h, layer, ctypes.byref(conv), ctypes.byref(rec),
+                                   ctypes.byref(err)), err, "qmoe_dn_state")
+        return conv.value, rec.value
+
+    def state_shapes(self):
+        return (self.kc - 1, self.conv_dim), (self.hv, self.dv, self.dk)
 
 
 def synth_fill(t, kind: int, seed: int, layer: int, tag: int, start=0, stddev=1.0, stream=None):
