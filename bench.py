@@ -364,6 +364,63 @@ def bench_prefill_stages(pkg, torch, st, reps=6):
     return res
 
 
+DN_SHAPE = (2048, 16, 32, 128, 128, 4)  # hidden, key heads, value heads, dk, dv, conv taps
+
+
+def dn_token_bytes(shape):
+    """algorithmic HBM bytes of one token through one DeltaNet mixer: q4
+    in_proj_qkv, in_proj_z, out_proj (codes + bf16 scale/bias per 64),
+    bf16 in_proj_a/b and conv1d, the f32 vectors, the recurrent state read
+    and written, the conv state read and written, x in and out"""
+    d, hk, hv, dk, dv, kc = shape
+    kd, vd = hk * dk, hv * dv
+    cd = 2 * kd + vd
+    q4 = lambda rows, cols: rows * cols // 2 + rows * (cols // 64) * 4
+    w = q4(cd, d) + q4(vd, d) + q4(d, vd) + 2 * hv * d * 2 + cd * kc * 2 + (dv + 2 * hv) * 4
+    state = 2 * (hv * dv * dk * 4) + 2 * ((kc - 1) * cd * 4)
+    return w + state + 2 * d * 4
+
+
+def bench_deltanet(pkg, torch, layers, steps, warmup):
+    """one f32 token per step through one gated DeltaNet mixer of DN_SHAPE,
+    layer i % layers on input i % 16 (states carried from step to step);
+    random q4/bf16 weights (numpy), the same host arrays in every layer
+    slot.  Returns seconds per token-layer."""
+    import numpy as np
+    d, hk, hv, dk, dv, kc = DN_SHAPE
+    kd, vd = hk * dk, hv * dv
+    cd = 2 * kd + vd
+    rng = np.random.default_rng(0)
+    bf = lambda n, std: ((rng.normal(0, std, n).astype(np.float32).view(np.uint32) + 0x8000) >> 16).astype(np.uint16)
+    codes = lambda n: rng.integers(0, 2**32, n, dtype=np.uint32)
+    host = dict(qkv_q=codes(cd * d // 8), qkv_s=bf(cd * d // 64, 0.02), qkv_b=bf(cd * d // 64, 0.01),
+                z_q=codes(vd * d // 8), z_s=bf(vd * d // 64, 0.02), z_b=bf(vd * d // 64, 0.01),
+                a_w=bf(hv * d, 0.02), b_w=bf(hv * d, 0.02),
+                out_q=codes(d * vd // 8), out_s=bf(d * vd // 64, 0.02), out_b=bf(d * vd // 64, 0.01),
+                conv_w=bf(cd * kc, 0.5), norm_w=(1 + rng.normal(0, 0.1, dv)).astype(np.float32),
+                a_log=rng.normal(0, 1, hv).astype(np.float32), dt_bias=rng.normal(0, 1, hv).astype(np.float32))
+    ctx = pkg.DeltaNetContext(d, hk, hv, dk, dv, kc, n_layers=layers, max_tokens=1)
+    for layer in range(layers):
+        ctx.upload_layer(layer, host)
+    X = 16
+    xs = [torch.randn((1, d), device="cuda") for _ in range(X)]
+    outs = [torch.empty((1, d), device="cuda") for _ in range(X)]
+
+    def run(first, count):
+        for i in range(first, first + count):
+            rc, msg = ctx.forward_raw(i % layers, xs[i % X].data_ptr(), 1, outs[i % X].data_ptr(),
+                                      torch.cuda.current_stream().cuda_stream)
+            if rc:
+                raise RuntimeError(msg)
+
+    run(0, warmup)
+    torch.cuda.synchronize()
+    g = capture(torch, lambda: run(warmup, steps), warm=False)
+    sec = time_graph(torch, g, 1) / steps
+    ctx.close()
+    return sec
+
+
 def bench_depth(pkg, torch, w, tokens, warmup):
     """48 stacked layers, one token: h <- h + MoE(RMSNorm(h)) layer after
     layer (f32 residual stream), captured as one graph per token; returns
@@ -571,6 +628,8 @@ def main():
                     help="workloads timed on the CPU (the oracle)")
     ap.add_argument("--extra", default="tiny,batched,prefill,depth48",
                     help="comma list of other workloads to time (secondary results)")
+    ap.add_argument("--deltanet", type=int, default=1,
+                    help="also time the gated DeltaNet mixer at one token (0: skip)")
     ap.add_argument("--hyper", default="decode,batched,prefill",
                     help="comma list of workloads also timed as hyper-connection layers "
                          f"(hc {HC_COUNT}, rank {HC_LOWRANK}; secondary results)")
@@ -663,6 +722,20 @@ def main():
         log(f"{name}: {s_e * 1e3:.4f} ms/step -> {we.n_tokens / s_e:.0f} tokens/s")
         free(torch, st)
         del st
+    if args.deltanet:
+        nl = 16
+        s_d = bench_deltanet(pkg, torch, nl, 256, 32)
+        b = dn_token_bytes(DN_SHAPE)
+        extra["deltanet"] = dict(
+            us_per_token=s_d * 1e6, tokens_per_s=1.0 / s_d, layers_rotated=nl, steps=256,
+            algorithmic_bytes_per_token=b, hbm_fraction=round(b / s_d / 1e9 / HBM_PEAK_GBS, 4),
+            shape=dict(zip(("hidden", "key_heads", "value_heads", "k_head_dim", "v_head_dim",
+                            "conv_kernel"), DN_SHAPE)),
+            note="one f32 token through one gated DeltaNet mixer (projections, conv + delta-rule "
+                 "recurrence with HBM-resident states, gated norm + out_proj), layers rotated, "
+                 "one HIP graph")
+        log(f"deltanet: {s_d * 1e6:.2f} us/token-layer -> {b / s_d / 1e9:.0f} GB/s")
+        torch.cuda.empty_cache()
     for name in [e for e in args.hyper.split(",") if e]:
         we = pkg.WORKLOADS[name]
         nl = 16 if we.n_tokens == 1 else (8 if we.n_tokens <= 64 else 2)

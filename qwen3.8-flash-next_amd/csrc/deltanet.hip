@@ -18,10 +18,13 @@
  *             sigmoid(b), then per row S <- g S; kv = S.k; S += k (beta
  *             (v - kv)); o = S.q (model.c:1225-1248).  Writes o [n, value_dim]
  *             and the new recurrent state.
- *   k_dn_out  per token the gated norm rmsnorm(o_h) * norm_w * sigmoid(z_h)
- *             (model.c:1263-1274) into LDS, then one wave per four rows of
- *             out_proj (q4); also moves the conv state on by n tokens (its
- *             old rows are read by k_dn_rec, so it changes only here).
+ *             The gated norm rmsnorm(o_h) * norm_w * sigmoid(z_h) (model.c:
+ *             1263-1274) is split: k_dn_rec writes o * norm_w * sigmoid(z)
+ *             per row and the sum of o^2 over its rows.
+ *   k_dn_out  one wave per two rows of out_proj (q4); each lane scales its
+ *             own columns by the head's 1/sqrt(sum(o^2)/dv + eps); also
+ *             moves the conv state on by n tokens (its old rows are read by
+ *             k_dn_rec, so it changes only here).
  *
  * Sums run in parallel orders (lane trees), so results match the reference
  * to rounding, not bit for bit.
@@ -141,8 +144,11 @@ struct DnRecArgs {
     const float *conv_state;     /* [kc-1, conv_dim], the state before these tokens */
     const uint16_t *conv_w;      /* [conv_dim, kc] */
     const float *a_log, *dt_bias;
+    const float *z;              /* [n, value_dim] */
+    const float *norm_w;         /* [dv] */
     float *rec_state;            /* [hv, dv, dk] */
-    float *core;                 /* [n, value_dim] */
+    float *core;                 /* [n, value_dim]: o * norm_w * sigmoid(z) */
+    float *ssp;                  /* [n, hv, dv/16]: sums of o^2 over each block's rows */
     int n, hk, hv, dk, dv, kc, conv_dim;
 };
 
@@ -164,6 +170,7 @@ __global__ __launch_bounds__(256) void k_dn_rec(DnRecArgs a) {
     constexpr int DK = 16 * EPL;
     __shared__ float s_ch[2 * DK + DN_RB]; /* q, k, v of the block's rows */
     __shared__ float s_sc[4];              /* q and k norms, decay, beta */
+    __shared__ float s_o[DN_RB];           /* the block's outputs of this token */
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = blockIdx.y, rb = blockIdx.x * DN_RB;
     const int kh = h / (a.hv / a.hk);
@@ -228,8 +235,21 @@ __global__ __launch_bounds__(256) void k_dn_rec(DnRecArgs a) {
             o = fmaf(s[e], qq[e], o);
         }
         o = qk_group_sum<16>(o);
-        if ((tid & 15) == 0) qk_st(a.core + (size_t)t * value_dim + (size_t)h * a.dv + row, o);
-        __syncthreads(); /* s_ch, s_sc are rewritten for the next token */
+        if ((tid & 15) == 0) {
+            /* the gated norm's row factors here, its head factor (from the
+             * sums of squares) in k_dn_out */
+            const size_t i = (size_t)t * value_dim + (size_t)h * a.dv + row;
+            const float zv = qk_ld(a.z + i);
+            qk_st(a.core + i, (o * qk_ld(a.norm_w + row)) * (1.0f / (1.0f + expf(-zv))));
+            s_o[tid >> 4] = o;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float ss = 0.0f;
+            for (int j = 0; j < DN_RB; j++) ss = fmaf(s_o[j], s_o[j], ss);
+            qk_st(a.ssp + ((size_t)t * a.hv + h) * (a.dv / DN_RB) + blockIdx.x, ss);
+        }
+        __syncthreads(); /* s_ch, s_sc, s_o are rewritten for the next token */
     }
     if (EPL % 4 == 0) {
 #pragma unroll
@@ -246,19 +266,25 @@ __global__ __launch_bounds__(256) void k_dn_rec(DnRecArgs a) {
 struct DnOutArgs {
     const uint32_t *out_q;
     const uint16_t *out_s, *out_b;
-    const float *core, *z;     /* [n, value_dim] */
-    const float *norm_w;       /* [dv] */
+    const float *core;         /* [n, value_dim]: o * norm_w * sigmoid(z) */
+    const float *ssp;          /* [n, hv, dv/16] */
     const float *mixed;        /* [n, conv_dim] */
     float *conv_state;         /* [kc-1, conv_dim], moved on by n tokens */
     float *out;                /* [n, d] */
     int n, d, value_dim, dv, kc, conv_dim, ch_per_wg;
 };
 
+#define DN_ORW 2 /* out_proj rows per wave */
+
+/*
+ * One wave per DN_ORW rows of out_proj.  The gated norm's head factor
+ * r = 1/sqrt(sum(o^2)/dv + eps) comes from the per-block sums of squares
+ * of k_dn_rec (dv/16 of them per head); each lane scales its own chunks
+ * (32 columns of one head) and splits them into bf16 hi + lo pairs.  No
+ * LDS and no barrier.
+ */
 template <int P>
 __global__ __launch_bounds__(256) void k_dn_out(DnOutArgs a) {
-    extern __shared__ float dn_lds[];
-    float *s_act = dn_lds;                 /* [value_dim] */
-    float *s_ss = dn_lds + a.value_dim;    /* [256] */
     const int tid = threadIdx.x, lane = tid & 63;
     const int K = a.value_dim, CH = K >> 5, G = K >> 6;
     const size_t wrow = (size_t)K >> 3;
@@ -276,11 +302,12 @@ __global__ __launch_bounds__(256) void k_dn_out(DnOutArgs a) {
         }
     }
 
-    const int r0 = (blockIdx.x * 4 + (tid >> 6)) * DN_RPW;
-    uint4 wq[DN_RPW][P];
-    float ws[DN_RPW][P], wb[DN_RPW][P];
+    const int r0 = (blockIdx.x * 4 + (tid >> 6)) * DN_ORW;
+    if (r0 >= a.d) return;
+    uint4 wq[DN_ORW][P];
+    float ws[DN_ORW][P], wb[DN_ORW][P];
 #pragma unroll
-    for (int j = 0; j < DN_RPW; j++) {
+    for (int j = 0; j < DN_ORW; j++) {
         const int r = min(r0 + j, a.d - 1);
 #pragma unroll
         for (int ps = 0; ps < P; ps++) {
@@ -293,48 +320,33 @@ __global__ __launch_bounds__(256) void k_dn_out(DnOutArgs a) {
             if (!ok) wq[j][ps] = make_uint4(0u, 0u, 0u, 0u);
         }
     }
-    const int EPT = K / 256;          /* elements per thread in the norm */
-    const int TPH = a.dv / EPT;       /* threads per head */
     for (int t = 0; t < a.n; t++) {
-        const float *o = a.core + (size_t)t * K + (size_t)tid * EPT;
-        float ss = 0.0f;
-        for (int e = 0; e < EPT; e++) {
-            const float v = qk_ld(o + e);
-            ss = fmaf(v, v, ss);
-        }
-        s_ss[tid] = ss;
-        __syncthreads();
-        /* the head's sum of squares: its TPH threads' partials in order */
-        const int hb = (tid / TPH) * TPH;
-        float hs = 0.0f;
-        for (int j = 0; j < TPH; j++) hs = hs + s_ss[hb + j];
-        const float r = 1.0f / sqrtf(hs / (float)a.dv + 1e-6f);
-        for (int e = 0; e < EPT; e++) {
-            const int i = tid * EPT + e;
-            const float zv = qk_ld(a.z + (size_t)t * K + i);
-            s_act[i] = ((qk_ld(o + e) * r) * qk_ld(a.norm_w + i % a.dv)) * (1.0f / (1.0f + expf(-zv)));
-        }
-        __syncthreads();
-        if (r0 < a.d) {
-            XRaw<P, false> xr;
+        XRaw<P, false> xr;
 #pragma unroll
-            for (int ps = 0; ps < P; ps++) {
-                const int c0 = ps * 64 + lane;
-                const int c = c0 < CH ? c0 : 0;
-                const float4 *src = (const float4 *)(s_act + 32 * c);
+        for (int ps = 0; ps < P; ps++) {
+            const int c0 = ps * 64 + lane;
+            const bool ok = c0 < CH;
+            const int c = ok ? c0 : 0;
+            const float4 *o = (const float4 *)(a.core + (size_t)t * K + 32 * c);
+            const int head = (32 * c) / a.dv, nb = a.dv / DN_RB;
+            const float *sp = a.ssp + ((size_t)t * (K / a.dv) + head) * nb;
+            float ss = 0.0f;
+            for (int j = 0; j < nb; j++) ss = ss + qk_ld(sp + j);
+            const float r = 1.0f / sqrtf(ss / (float)a.dv + 1e-6f);
 #pragma unroll
-                for (int w = 0; w < 8; w++) xr.f[ps][w] = src[w];
-            }
-            XPairs<64, P, false> xp;
-            convert_xraw<64, P, false>(xr, K, lane, xp);
-#pragma unroll
-            for (int j = 0; j < DN_RPW; j++) {
-                const float v = qk_group_sum<64>(row_part<64, P, false>(wq[j], ws[j], wb[j], xp));
-                const int rr = r0 + j;
-                if (lane == 0 && rr < a.d) qk_st(a.out + (size_t)t * a.d + rr, v);
+            for (int w = 0; w < 8; w++) {
+                const float4 v = qk_ld(o + w);
+                xr.f[ps][w] = make_float4(v.x * r, v.y * r, v.z * r, v.w * r);
             }
         }
-        __syncthreads(); /* s_act, s_ss are rewritten for the next token */
+        XPairs<64, P, false> xp;
+        convert_xraw<64, P, false>(xr, K, lane, xp);
+#pragma unroll
+        for (int j = 0; j < DN_ORW; j++) {
+            const float v = qk_group_sum<64>(row_part<64, P, false>(wq[j], ws[j], wb[j], xp));
+            const int rr = r0 + j;
+            if (lane == 0 && rr < a.d) qk_st(a.out + (size_t)t * a.d + rr, v);
+        }
     }
 }
 
@@ -346,21 +358,19 @@ extern "C" int qk_dn_shape_ok(const qk_dn_shape *s) {
     if (s->d <= 0 || s->d % 64 || s->d > 8192) return 0;
     if (s->hk <= 0 || s->hv <= 0 || s->hv % s->hk) return 0;
     if (!(s->dk == 32 || s->dk == 64 || s->dk == 128 || s->dk == 256)) return 0;
-    if (s->dv <= 0 || s->dv % DN_RB) return 0;
-    if (value_dim % 256 || value_dim > 8192 || s->dv % (value_dim / 256)) return 0;
-    if ((s->dv / (value_dim / 256)) > 256) return 0;
+    /* dv: a power-of-two count (<= 64) of 32-column chunks */
+    if (!(s->dv == 32 || s->dv == 64 || s->dv == 128 || s->dv == 256 || s->dv == 512 ||
+          s->dv == 1024 || s->dv == 2048))
+        return 0;
+    if (value_dim > 8192) return 0;
     if (s->kc < 1 || s->kc > 16) return 0;
     if (conv_dim <= 0) return 0;
     return 1;
 }
 
-extern "C" size_t qk_dn_out_lds(const qk_dn_shape *s) {
-    return ((size_t)s->hv * s->dv + 256) * sizeof(float);
-}
-
 extern "C" int qk_launch_dn(const qk_dn_shape *s, const qk_dn_dev *W, const float *x, int n, float *out,
                             float *conv_state, float *rec_state, float *mixed, float *z, float *av,
-                            float *bv, float *core, void *stream) {
+                            float *bv, float *core, float *ssp, void *stream) {
     if (n <= 0) return 0;
     if (!qk_dn_shape_ok(s)) return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)stream;
@@ -390,7 +400,8 @@ extern "C" int qk_launch_dn(const qk_dn_shape *s, const qk_dn_dev *W, const floa
     ra.mixed = mixed; ra.a = av; ra.b = bv;
     ra.conv_state = conv_state; ra.conv_w = W->conv_w;
     ra.a_log = W->a_log; ra.dt_bias = W->dt_bias;
-    ra.rec_state = rec_state; ra.core = core;
+    ra.z = z; ra.norm_w = W->norm_w;
+    ra.rec_state = rec_state; ra.core = core; ra.ssp = ssp;
     ra.n = n; ra.hk = s->hk; ra.hv = s->hv; ra.dk = s->dk; ra.dv = s->dv; ra.kc = s->kc;
     ra.conv_dim = conv_dim;
     const dim3 rgrid(s->dv / DN_RB, s->hv);
@@ -405,20 +416,19 @@ extern "C" int qk_launch_dn(const qk_dn_shape *s, const qk_dn_dev *W, const floa
 
     DnOutArgs oa;
     oa.out_q = W->out_q; oa.out_s = W->out_s; oa.out_b = W->out_b;
-    oa.core = core; oa.z = z; oa.norm_w = W->norm_w; oa.mixed = mixed;
+    oa.core = core; oa.ssp = ssp; oa.mixed = mixed;
     oa.conv_state = conv_state; oa.out = out;
     oa.n = n; oa.d = s->d; oa.value_dim = value_dim; oa.dv = s->dv; oa.kc = s->kc;
     oa.conv_dim = conv_dim;
-    const int owgs = (s->d + 4 * DN_RPW - 1) / (4 * DN_RPW);
+    const int owgs = (s->d + 4 * DN_ORW - 1) / (4 * DN_ORW);
     oa.ch_per_wg = (conv_dim + owgs - 1) / owgs;
     if (oa.ch_per_wg > 256) return (int)hipErrorInvalidValue;
-    const size_t lds = qk_dn_out_lds(s);
     const int p_out = (value_dim / 32 + 63) / 64;
     switch (p_out) {
-    case 1: hipLaunchKernelGGL(k_dn_out<1>, dim3(owgs), dim3(256), lds, st, oa); break;
-    case 2: hipLaunchKernelGGL(k_dn_out<2>, dim3(owgs), dim3(256), lds, st, oa); break;
-    case 3: hipLaunchKernelGGL(k_dn_out<3>, dim3(owgs), dim3(256), lds, st, oa); break;
-    default: hipLaunchKernelGGL(k_dn_out<4>, dim3(owgs), dim3(256), lds, st, oa); break;
+    case 1: hipLaunchKernelGGL(k_dn_out<1>, dim3(owgs), dim3(256), 0, st, oa); break;
+    case 2: hipLaunchKernelGGL(k_dn_out<2>, dim3(owgs), dim3(256), 0, st, oa); break;
+    case 3: hipLaunchKernelGGL(k_dn_out<3>, dim3(owgs), dim3(256), 0, st, oa); break;
+    default: hipLaunchKernelGGL(k_dn_out<4>, dim3(owgs), dim3(256), 0, st, oa); break;
     }
     return QK_CHECK_LAUNCH();
 }

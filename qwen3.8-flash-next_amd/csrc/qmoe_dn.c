@@ -32,7 +32,7 @@ struct qmoe_dn_ctx {
     size_t off[DT_COUNT + 1], bytes[DT_COUNT];
     dn_layer *layers;
     void *scratch;
-    float *mixed, *z, *a, *b, *core;
+    float *mixed, *z, *a, *b, *core, *ssp;
 };
 
 static void dn_set_err(qmoe_err *err, const char *fmt, ...) {
@@ -69,7 +69,7 @@ int qmoe_dn_create(qmoe_dn_ctx **out, const qmoe_dn_config *cfg, qmoe_err *err) 
     if (cfg->group_size != 64 || !qk_dn_shape_ok(&s)) {
         dn_set_err(err, "DeltaNet shape unsupported: hidden %d (multiple of 64, <= 8192), heads %d/%d "
                         "(value heads a multiple of key heads), k_head_dim %d (32, 64, 128, 256), "
-                        "v_head_dim %d (multiple of 16; heads*dim a multiple of 256, <= 8192), "
+                        "v_head_dim %d (a power of two, 32..2048; heads*dim <= 8192), "
                         "conv_kernel %d (1..16), group_size %d (64)",
                    cfg->hidden, cfg->n_k_heads, cfg->n_v_heads, cfg->k_head_dim, cfg->v_head_dim,
                    cfg->conv_kernel, cfg->group_size);
@@ -109,9 +109,10 @@ int qmoe_dn_create(qmoe_dn_ctx **out, const qmoe_dn_config *cfg, qmoe_err *err) 
     c->off[DT_COUNT] = total;
     c->layers = (dn_layer *)calloc((size_t)cfg->n_layers, sizeof(dn_layer));
     const size_t n = (size_t)cfg->max_tokens;
-    const size_t ssz[5] = {n * conv_dim * 4, n * value_dim * 4, n * hv * 4, n * hv * 4, n * value_dim * 4};
-    size_t stot = 0, soff[5];
-    for (int i = 0; i < 5; i++) {
+    const size_t ssz[6] = {n * conv_dim * 4, n * value_dim * 4, n * hv * 4, n * hv * 4, n * value_dim * 4,
+                           n * (value_dim / 16) * 4};
+    size_t stot = 0, soff[6];
+    for (int i = 0; i < 6; i++) {
         soff[i] = stot;
         stot = dn_align(stot + ssz[i]);
     }
@@ -126,6 +127,7 @@ int qmoe_dn_create(qmoe_dn_ctx **out, const qmoe_dn_config *cfg, qmoe_err *err) 
     c->a = (float *)(b + soff[2]);
     c->b = (float *)(b + soff[3]);
     c->core = (float *)(b + soff[4]);
+    c->ssp = (float *)(b + soff[5]);
     for (int l = 0; l < cfg->n_layers; l++) {
         if (dn_hip_fail(err, (int)hipMalloc(&c->layers[l].mem, total), "layer weights")) {
             qmoe_dn_destroy(c);
@@ -247,7 +249,7 @@ int qmoe_dn_forward(qmoe_dn_ctx *c, int layer, const float *x, int n, float *out
     W.dt_bias = (const float *)dn_ptr(c, layer, DT_DT_BIAS);
     const int rc = qk_launch_dn(&c->shape, &W, x, n, out, (float *)dn_ptr(c, layer, DT_CONV_STATE),
                                 (float *)dn_ptr(c, layer, DT_REC_STATE), c->mixed, c->z, c->a, c->b,
-                                c->core, stream);
+                                c->core, c->ssp, stream);
     return dn_hip_fail(err, rc, "DeltaNet launch");
 }
 

@@ -203,13 +203,12 @@ typedef struct {
     const float *norm_w, *a_log, *dt_bias;
 } qk_dn_dev;
 int qk_dn_shape_ok(const qk_dn_shape *s);
-size_t qk_dn_out_lds(const qk_dn_shape *s);
 /* x [n, d] f32 -> out [n, d]; conv_state and rec_state are updated;
  * mixed [n, conv_dim], z [n, value_dim], a, b [n, hv], core [n, value_dim]
- * are scratch */
+ * and ssp [n, hv, dv/16] are scratch */
 int qk_launch_dn(const qk_dn_shape *s, const qk_dn_dev *W, const float *x, int n, float *out,
                  float *conv_state, float *rec_state, float *mixed, float *z, float *a, float *b,
-                 float *core, void *stream);
+                 float *core, float *ssp, void *stream);
 int qk_launch_dn_zero(float *p, size_t count, void *stream);
 
 /* the MLP hyper connection (hyper.hip): shapes it takes (hc <= 8, d and R
