@@ -232,6 +232,37 @@ float orc_dn_decay(float a_log, float a, float dt_bias);
 int orc_dn_forward(const orc_dn *D, const float *x, int n, float *out, float *conv_state,
                    float *rec_state, float *core_out);
 
+/* ---- full attention with the QSA indexer (attn_oracle.c; model.c:798-1144) ---- */
+typedef struct {
+    int hidden;         /* d */
+    int n_heads;        /* h */
+    int n_kv_heads;     /* kvh; head hh reads kv head hh % kvh */
+    int head_dim;       /* hd */
+    int idx_heads;      /* indexer_n_heads */
+    int idx_head_dim;   /* indexer_head_dim */
+    int idx_budget;     /* indexer_budget */
+    int idx_compress;   /* indexer_compress_ratio */
+    int kv_cap;         /* cache rows (QMODEL_KV_CAP) */
+    int group_size;
+    float rotary_factor, rope_theta;
+    const uint32_t *q_q; const uint16_t *q_s, *q_b;   /* q_proj [2*h*hd, d] q4: q | gate per head */
+    const uint32_t *k_q; const uint16_t *k_s, *k_b;   /* k_proj [kvh*hd, d] q4 */
+    const uint32_t *v_q; const uint16_t *v_s, *v_b;   /* v_proj [kvh*hd, d] q4 */
+    const uint32_t *o_q; const uint16_t *o_s, *o_b;   /* o_proj [d, h*hd] q4 */
+    const uint16_t *idx_w;                              /* index_qk_proj [idx_heads*idx_hd + idx_hd, d] bf16 */
+    const float *q_norm, *k_norm;                       /* [hd] */
+    const float *idx_q_norm, *idx_k_norm;               /* [idx_hd] */
+} orc_attn;
+typedef struct {
+    float *k_cache, *v_cache; /* [kv_cap, kvh*hd] */
+    float *idx_keys;          /* [kv_cap, idx_hd] */
+    int kv_len, idx_len;
+} orc_attn_state;
+/* x [n, d] f32 at positions offset.. -> out [n, d]; appends to the caches;
+ * -2 when the call would pass the cache capacity */
+int orc_attn_forward(const orc_attn *A, orc_attn_state *S, const float *x, int n, int offset,
+                     float *out);
+
 #ifdef __cplusplus
 }
 #endif

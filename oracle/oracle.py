@@ -26,6 +26,9 @@ TAG = dict(
     DN_QKV_Q=40, DN_QKV_S=41, DN_QKV_B=42, DN_Z_Q=43, DN_Z_S=44, DN_Z_B=45, DN_A_W=46,
     DN_B_W=47, DN_OUT_Q=48, DN_OUT_S=49, DN_OUT_B=50, DN_CONV_W=51, DN_NORM_W=52, DN_A_LOG=53,
     DN_DT_BIAS=54, DN_X=55,
+    AT_Q_Q=60, AT_Q_S=61, AT_Q_B=62, AT_K_Q=63, AT_K_S=64, AT_K_B=65, AT_V_Q=66, AT_V_S=67,
+    AT_V_B=68, AT_O_Q=69, AT_O_S=70, AT_O_B=71, AT_IDX_W=72, AT_Q_NORM=73, AT_K_NORM=74,
+    AT_IDX_Q_NORM=75, AT_IDX_K_NORM=76, AT_X=77,
 )
 
 ROUTED_FAITHFUL, ROUTED_Q4 = 0, 1
@@ -70,6 +73,21 @@ class OrcDn(ctypes.Structure):
     ]
 
 
+class OrcAttn(ctypes.Structure):
+    _fields_ = [
+        ("hidden", _I), ("n_heads", _I), ("n_kv_heads", _I), ("head_dim", _I), ("idx_heads", _I),
+        ("idx_head_dim", _I), ("idx_budget", _I), ("idx_compress", _I), ("kv_cap", _I),
+        ("group_size", _I), ("rotary_factor", _F), ("rope_theta", _F),
+        ("q_q", _P), ("q_s", _P), ("q_b", _P), ("k_q", _P), ("k_s", _P), ("k_b", _P),
+        ("v_q", _P), ("v_s", _P), ("v_b", _P), ("o_q", _P), ("o_s", _P), ("o_b", _P),
+        ("idx_w", _P), ("q_norm", _P), ("k_norm", _P), ("idx_q_norm", _P), ("idx_k_norm", _P),
+    ]
+
+
+class OrcAttnState(ctypes.Structure):
+    _fields_ = [("k_cache", _P), ("v_cache", _P), ("idx_keys", _P), ("kv_len", _I), ("idx_len", _I)]
+
+
 class OrcOpts(ctypes.Structure):
     _fields_ = [("x_is_bf16", _I), ("residual", _I), ("routed_mode", _I), ("n_threads", _I)]
 
@@ -108,6 +126,7 @@ _SIG = {
     "orc_gen_normal_f32": (None, [_P, _SZ, _U64, _U64, _F]),
     "orc_gen_codes": (None, [_P, _SZ, _U64, _U64]),
     "orc_zipf_bias": (None, [_P, _I, ctypes.c_double, ctypes.c_double, _U64]),
+    "orc_attn_forward": (_I, [ctypes.POINTER(OrcAttn), ctypes.POINTER(OrcAttnState), _P, _I, _I, _P]),
     "orc_dn_decay": (_F, [_F, _F, _F]),
     "orc_dn_forward": (_I, [ctypes.POINTER(OrcDn), _P, _I, _P, _P, _P, _P]),
     "orc_time_forward": (ctypes.c_double, [ctypes.POINTER(OrcLayer), _P, _I, _P,
@@ -510,6 +529,87 @@ class DeltaNet:
                                 _p(rec_state), _p(core)):
             raise MemoryError("orc_dn_forward")
         return (out, core) if want_core else out
+
+
+class Attention:
+    """One full-attention mixer with the QSA indexer (c/src/model.c:798-1144)
+    in host memory, checkpoint layout (names model.c:1833-1850): q_proj
+    [2*h*hd, d] (q and gate interleaved per head), k_proj, v_proj
+    [kvh*hd, d], o_proj [d, h*hd] q4 (codes U{0..15}, scales N(0,0.02),
+    biases N(0,0.01)); index_qk_proj [idx_heads*idx_hd + idx_hd, d] bf16
+    N(0,0.02); the four norm weights 1 + N(0,0.1), rounded to bf16 and
+    widened (mw_load_f32).  A State holds the caches."""
+
+    KEYS = ("q_q", "q_s", "q_b", "k_q", "k_s", "k_b", "v_q", "v_s", "v_b", "o_q", "o_s", "o_b",
+            "idx_w", "q_norm", "k_norm", "idx_q_norm", "idx_k_norm")
+
+    def __init__(self, d, h, kvh, hd, idx_heads, idx_hd, budget, compress, kv_cap=2048,
+                 rotary_factor=0.25, rope_theta=1e7, seed=0, layer=0, group_size=64):
+        self.d, self.h, self.kvh, self.hd = d, h, kvh, hd
+        self.ih, self.ihd, self.budget, self.compress = idx_heads, idx_hd, budget, compress
+        self.cap, self.rf, self.theta, self.g = kv_cap, rotary_factor, rope_theta, group_size
+        g, s, L = group_size, seed, layer
+        t = {}
+        for nm, rows, cols in (("q", 2 * h * hd, d), ("k", kvh * hd, d), ("v", kvh * hd, d),
+                               ("o", d, h * hd)):
+            T = nm.upper()
+            t[nm + "_q"] = gen_codes(rows * cols // 8, s, L, f"AT_{T}_Q")
+            t[nm + "_s"] = gen_bf16(rows * cols // g, s, L, f"AT_{T}_S", 0.02)
+            t[nm + "_b"] = gen_bf16(rows * cols // g, s, L, f"AT_{T}_B", 0.01)
+        t["idx_w"] = gen_bf16((idx_heads * idx_hd + idx_hd) * d, s, L, "AT_IDX_W", 0.02)
+        for nm, n in (("q_norm", hd), ("k_norm", hd), ("idx_q_norm", idx_hd), ("idx_k_norm", idx_hd)):
+            t[nm] = bf16_to_f32(f32_to_bf16(1.0 + gen_f32(n, s, L, "AT_" + nm.upper(), 0.1)))
+        self.t = t
+        self._build()
+
+    @classmethod
+    def from_arrays(cls, proto, arrays):
+        self = cls.__new__(cls)
+        self.__dict__.update({k: v for k, v in proto.__dict__.items() if k not in ("t", "st")})
+        self.t = {k: np.ascontiguousarray(arrays[k]) for k in cls.KEYS}
+        self._build()
+        return self
+
+    def _build(self):
+        st = OrcAttn()
+        st.hidden, st.n_heads, st.n_kv_heads, st.head_dim = self.d, self.h, self.kvh, self.hd
+        st.idx_heads, st.idx_head_dim, st.idx_budget, st.idx_compress = self.ih, self.ihd, self.budget, self.compress
+        st.kv_cap, st.group_size, st.rotary_factor, st.rope_theta = self.cap, self.g, self.rf, self.theta
+        for f, a in self.t.items():
+            setattr(st, f, _p(a))
+        self.st = st
+
+    def arrays(self):
+        return dict(self.t)
+
+    class State:
+        def __init__(self, A):
+            self.k = np.zeros((A.cap, A.kvh * A.hd), np.float32)
+            self.v = np.zeros((A.cap, A.kvh * A.hd), np.float32)
+            self.idx = np.zeros((A.cap, A.ihd), np.float32)
+            self.len = 0
+
+    def new_state(self):
+        return Attention.State(self)
+
+    def forward(self, x, state, offset):
+        """x [n, d] f32 at positions offset..offset+n-1 -> out [n, d]; appends to state"""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        n = x.shape[0]
+        out = np.empty((n, self.d), np.float32)
+        S = OrcAttnState(_p(state.k), _p(state.v), _p(state.idx), state.len, state.len)
+        rc = lib().orc_attn_forward(ctypes.byref(self.st), ctypes.byref(S), _p(x), n, offset, _p(out))
+        if rc == -2:
+            raise ValueError("the call passes the cache capacity")
+        if rc:
+            raise MemoryError("orc_attn_forward")
+        state.len = S.kv_len
+        return out
+
+
+def gen_attn_x(n, d, seed, layer=0, std=1.0):
+    """attention inputs [n, d] f32 from their own stream"""
+    return gen_f32(n * d, seed, layer, "AT_X", std).reshape(n, d)
 
 
 def dn_decay(a_log, a, dt_bias):
