@@ -493,6 +493,81 @@ int qmoe_dn_forward(qmoe_dn_ctx *ctx, int layer, const float *x, int n, float *o
 int qmoe_dn_state(qmoe_dn_ctx *ctx, int layer, float **conv_state, float **rec_state,
                   qmoe_err *err);
 
+/* ------------------------------------------------------ full attention
+ * The full-attention mixer of the decoder's attention layers with its QSA
+ * indexer: attention_forward (c/src/model.c:798-1144), per layer and per
+ * call of n tokens at positions offset..offset+n-1:
+ *   qk = x.Wi^T (index_qk_proj, bf16): indexer query heads and a raw key,
+ *   appended to the indexer key cache                    (model.c:807-843)
+ *   q|gate (interleaved per head), k, v = q4 projections (model.c:847-862)
+ *   q, k: per-head rmsnorm (q_norm, k_norm), then RoPE of the first
+ *   rot = head_dim * rotary_factor dims at the token's position; k and v
+ *   appended to the caches                                (model.c:871-937)
+ *   scores q.k / sqrt(head_dim), head hh reading kv head hh % kv_heads,
+ *   keys at cache rows > offset + t masked (causal)      (model.c:951-967)
+ *   past idx_budget cached keys: the QSA block mask -- mean-pooled indexer
+ *   keys per block of idx_compress rows, rmsnorm + RoPE at the block start,
+ *   block score sum over indexer heads of sum relu(q_i p_i) / sqrt(idx_hd),
+ *   blocks ending past the token invisible, the top idx_budget/idx_compress
+ *   blocks and the token's own block tail kept            (model.c:969-1104)
+ *   softmax, weighted sum of v, * sigmoid(gate), o_proj   (model.c:1107-1143)
+ * The caches live in HBM with the layer, kv_cap rows; a call that would pass
+ * kv_cap is refused (the reference drops the oldest rows of its v and
+ * indexer caches there but not of its k cache, model.c:815-821, 863-867,
+ * 935-936; that is not reproduced).  Block selection ties go to the lower
+ * block (the reference's quickselect leaves their order open).  Sums run
+ * in parallel orders: outputs agree with the reference to rounding.
+ * Weights use the checkpoint layout (names model.c:1833-1850). */
+typedef struct qmoe_attn_ctx qmoe_attn_ctx;
+
+typedef struct {
+    int hidden;        /* d: multiple of 64, <= 8192 */
+    int n_heads;       /* h: num_attention_heads */
+    int n_kv_heads;    /* kvh: num_key_value_heads, divides h */
+    int head_dim;      /* hd: multiple of 64, <= 256; h*hd <= 8192 */
+    int idx_heads;     /* indexer_n_heads */
+    int idx_head_dim;  /* indexer_head_dim: multiple of 4, <= 256, >= rot */
+    int idx_budget;    /* indexer_budget */
+    int idx_compress;  /* indexer_compress_ratio */
+    int kv_cap;        /* cache rows, <= 8192 */
+    int group_size;    /* must be 64 */
+    float rotary_factor; /* partial_rotary_factor: rot = (int)(hd * factor), even */
+    float rope_theta;
+    int n_layers;
+    int max_tokens;
+} qmoe_attn_config;
+
+typedef struct {
+    const uint32_t *q_q;  /* [2*h*hd, d/8]   q_proj.weight (q | gate per head) */
+    const uint16_t *q_s, *q_b;
+    const uint32_t *k_q;  /* [kvh*hd, d/8]   k_proj.* */
+    const uint16_t *k_s, *k_b;
+    const uint32_t *v_q;  /* [kvh*hd, d/8]   v_proj.* */
+    const uint16_t *v_s, *v_b;
+    const uint32_t *o_q;  /* [d, h*hd/8]     o_proj.* */
+    const uint16_t *o_s, *o_b;
+    const uint16_t *idx_w;     /* [(idx_heads+1)*idx_hd, d] bf16  indexer.index_qk_proj.weight */
+    const float *q_norm, *k_norm;          /* [hd] */
+    const float *idx_q_norm, *idx_k_norm;  /* [idx_hd] */
+} qmoe_attn_weights;
+
+int qmoe_attn_create(qmoe_attn_ctx **ctx, const qmoe_attn_config *cfg, qmoe_err *err);
+void qmoe_attn_destroy(qmoe_attn_ctx *ctx);
+/* copies one layer from HOST memory and empties its caches */
+int qmoe_attn_upload_layer(qmoe_attn_ctx *ctx, int layer, const qmoe_attn_weights *host,
+                           qmoe_err *err);
+/* empties the caches of one layer (-1: every layer) */
+int qmoe_attn_reset(qmoe_attn_ctx *ctx, int layer, qmoe_err *err);
+/* x [n, d] f32 device at positions offset.. -> out [n, d] f32 device;
+ * appends n rows to the layer's caches.  Asynchronous on `stream`; the
+ * cache length is host state, so calls on one layer run in call order. */
+int qmoe_attn_forward(qmoe_attn_ctx *ctx, int layer, const float *x, int n, int offset, float *out,
+                      void *stream, qmoe_err *err);
+/* device addresses of a layer's caches (k and v [kv_cap, kvh*hd], indexer
+ * keys [kv_cap, idx_hd]) and their current length */
+int qmoe_attn_cache(qmoe_attn_ctx *ctx, int layer, float **k_cache, float **v_cache, float **idx_keys,
+                    int *len, qmoe_err *err);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,552 @@
+/*
+ * attention.hip -- the full-attention mixer with the QSA indexer on gfx950,
+ * replacing attention_forward of the reference C port (c/src/model.c:
+ * 798-1144) for n tokens at positions offset.. in five or six launches:
+ *
+ *   k_rows    one wave per four rows of [q_proj | k_proj | v_proj] (q4) and
+ *             index_qk_proj (bf16); x (f32) as bf16 hi + lo pairs, the q4
+ *             rows with gemm_q4's per-group identity (gemv_parts.h).  Also
+ *             o_proj at the end.
+ *   k_at_qk   one wave per (token, head): rmsnorm with q_norm / k_norm /
+ *             the indexer's q norm, then partial RoPE at position offset+t
+ *             (kernel.c:80-93); k, v and the indexer's raw key go into their
+ *             caches at rows len0 + t.
+ *   k_at_sel  (past the indexer budget) one workgroup per token: every
+ *             key block's mean-pooled indexer key, rmsnorm + RoPE at the
+ *             block start, score sum_heads sum_i relu(q_i p_i) / sqrt(ihd),
+ *             invisible blocks -inf; the top budget/compress blocks (value
+ *             descending, ties to the lower block) by an 8-bit radix select
+ *             -> a bitmap of kept blocks.
+ *   k_at_attn one workgroup per (token, head, 256 keys): scores q.k/sqrt(hd)
+ *             (kv head = head % kv_heads), the causal mask kk > offset + t and
+ *             the block mask, chunk max, sum of exp and exp-weighted v.
+ *   k_at_comb one wave per (token, head): the chunks merged (max, rescaled
+ *             sums), times sigmoid(gate).
+ * Sums run in parallel orders: outputs match the reference to rounding.
+ */
+#include "qk_device.h"
+#include "gemv_parts.h"
+#include "topk_wave.h"
+
+/* ------------------------------------------------------------ rows GEMV */
+
+#define AT_SEGS 4
+#define AT_RPW 4 /* rows per wave; every segment's row count is a multiple */
+
+struct RowSeg {
+    const uint32_t *q;          /* q4 codes [rows, K/8], or NULL for bf16 */
+    const uint16_t *s, *b;      /* q4 scales, biases [rows, K/64] */
+    const uint16_t *w;          /* bf16 weights [rows, K] */
+    float *out;                 /* out[t * ostride + r] */
+    int rows, ostride;
+};
+
+struct RowsArgs {
+    RowSeg seg[AT_SEGS];
+    int start[AT_SEGS + 1];     /* first global row of each segment, then the total */
+    int nseg;
+    const float *x;             /* [n, K] */
+    int K, n;
+};
+
+template <int P>
+__global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * AT_RPW;
+    if (r0 >= a.start[a.nseg]) return;
+    /* the wave's segment (a segment's row count is a multiple of AT_RPW) */
+    RowSeg S = a.seg[0];
+    int rr = r0;
+    if (a.nseg > 1 && r0 >= a.start[1]) { S = a.seg[1]; rr = r0 - a.start[1]; }
+    if (a.nseg > 2 && r0 >= a.start[2]) { S = a.seg[2]; rr = r0 - a.start[2]; }
+    if (a.nseg > 3 && r0 >= a.start[3]) { S = a.seg[3]; rr = r0 - a.start[3]; }
+    const int CH = a.K >> 5, G = a.K >> 6;
+    const size_t wrow = (size_t)a.K >> 3;
+    if (S.q) {
+        uint4 wq[AT_RPW][P];
+        float ws[AT_RPW][P], wb[AT_RPW][P];
+#pragma unroll
+        for (int j = 0; j < AT_RPW; j++) {
+            const int r = rr + j;
+#pragma unroll
+            for (int ps = 0; ps < P; ps++) {
+                const int c0 = ps * 64 + lane;
+                const bool ok = c0 < CH;
+                const int c = ok ? c0 : 0;
+                wq[j][ps] = qk_ld((const uint4 *)(S.q + (size_t)r * wrow + 4 * (size_t)c));
+                ws[j][ps] = ok ? qk_bf16(qk_ld(S.s + (size_t)r * G + (c >> 1))) : 0.0f;
+                wb[j][ps] = ok ? qk_bf16(qk_ld(S.b + (size_t)r * G + (c >> 1))) : 0.0f;
+                if (!ok) wq[j][ps] = make_uint4(0u, 0u, 0u, 0u);
+            }
+        }
+        for (int t = 0; t < a.n; t++) {
+            XRaw<P, false> xr;
+            load_xraw<64, P, false>(a.x, (size_t)t, a.K, lane, xr);
+            XPairs<64, P, false> xp;
+            convert_xraw<64, P, false>(xr, a.K, lane, xp);
+#pragma unroll
+            for (int j = 0; j < AT_RPW; j++) {
+                const float v = qk_group_sum<64>(row_part<64, P, false>(wq[j], ws[j], wb[j], xp));
+                if (lane == 0) qk_st(S.out + (size_t)t * S.ostride + rr + j, v);
+            }
+        }
+        return;
+    }
+    for (int t = 0; t < a.n; t++) {
+        XRaw<P, false> xr;
+        load_xraw<64, P, false>(a.x, (size_t)t, a.K, lane, xr);
+        XPairs<64, P, false> xp;
+        convert_xraw<64, P, false>(xr, a.K, lane, xp);
+#pragma unroll
+        for (int j = 0; j < AT_RPW; j++) {
+            const uint16_t *w = S.w + (size_t)(rr + j) * a.K;
+            float part = 0.0f;
+#pragma unroll
+            for (int ps = 0; ps < P; ps++) {
+                const int c0 = ps * 64 + lane;
+                const bool ok = c0 < CH;
+                const uint4 *src = (const uint4 *)(w + 32 * (size_t)(ok ? c0 : 0));
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    uint32_t wp[4];
+                    qk_bf16x8_to_pairs(qk_ld(src + g), wp);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const uint32_t w2 = ok ? wp[i] : 0u;
+                        part = qk_dot2(xp.hi[ps][4 * g + i], w2, part);
+                        part = qk_dot2(xp.lo[ps][4 * g + i], w2, part);
+                    }
+                }
+            }
+            const float v = qk_group_sum<64>(part);
+            if (lane == 0) qk_st(S.out + (size_t)t * S.ostride + rr + j, v);
+        }
+    }
+}
+
+/* ------------------------------------------------------------ norms, RoPE, caches */
+
+struct AtQkArgs {
+    const float *qg;        /* [n, 2h*hd]: q | gate per head */
+    const float *kraw;      /* [n, kvh*hd] */
+    const float *vraw;      /* [n, kvh*hd] */
+    const float *qk;        /* [n, ih*ihd + ihd]: indexer q heads, raw key */
+    const float *q_norm, *k_norm, *iq_norm;
+    float *qn;              /* [n, h, hd] */
+    float *k_cache, *v_cache; /* [cap, kvh*hd] */
+    float *idx_keys;        /* [cap, ihd] */
+    float *qi;              /* [n, ih, ihd], or NULL when the indexer is off */
+    int n, h, kvh, hd, ih, ihd, len0, offset, rot;
+    float theta;
+};
+
+/* rmsnorm (kernel.c:10-20: (x*r)*w) of the L values in s, then partial
+ * RoPE of the first rot (kernel.c:80-93) at position pos; one wave */
+__device__ __forceinline__ void at_norm_rope(float *s, const float *w, int L, int rot, float theta,
+                                             int pos, float *dst, int lane) {
+    float ss = 0.0f;
+    for (int i = lane; i < L; i += 64) ss = fmaf(s[i], s[i], ss);
+    ss = qk_group_sum<64>(ss);
+    const float r = 1.0f / sqrtf(ss / (float)L + 1e-6f);
+    for (int i = lane; i < L; i += 64) s[i] = (s[i] * r) * qk_ld(w + i);
+    qk_wave_lds_sync();
+    const int half = rot / 2;
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int i = lane + 64 * e;
+        if (i >= L) break;
+        if (i < half) {
+            const float ang = (float)pos * powf(theta, -(2.0f * (float)i) / (float)rot);
+            v[e] = s[i] * cosf(ang) - s[i + half] * sinf(ang);
+        } else if (i < rot) {
+            const float ang = (float)pos * powf(theta, -(2.0f * (float)(i - half)) / (float)rot);
+            v[e] = s[i - half] * sinf(ang) + s[i] * cosf(ang);
+        } else {
+            v[e] = s[i];
+        }
+    }
+    qk_wave_lds_sync(); /* dst may be s itself */
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int i = lane + 64 * e;
+        if (i >= L) break;
+        dst[i] = v[e];
+    }
+}
+
+__global__ __launch_bounds__(64) void k_at_qk(AtQkArgs a) {
+    __shared__ float s[256];
+    const int lane = threadIdx.x, t = blockIdx.x, role = blockIdx.y;
+    const int pos = a.offset + t, row = a.len0 + t;
+    if (role < a.h) {
+        const float *src = a.qg + (size_t)t * 2 * a.h * a.hd + (size_t)role * 2 * a.hd;
+        for (int i = lane; i < a.hd; i += 64) s[i] = qk_ld(src + i);
+        qk_wave_lds_sync();
+        at_norm_rope(s, a.q_norm, a.hd, a.rot, a.theta, pos, a.qn + ((size_t)t * a.h + role) * a.hd, lane);
+    } else if (role < a.h + a.kvh) {
+        const int kh = role - a.h;
+        const size_t off = (size_t)t * a.kvh * a.hd + (size_t)kh * a.hd;
+        for (int i = lane; i < a.hd; i += 64) {
+            s[i] = qk_ld(a.kraw + off + i);
+            a.v_cache[(size_t)row * a.kvh * a.hd + (size_t)kh * a.hd + i] = qk_ld(a.vraw + off + i);
+        }
+        if (kh == 0) {
+            const float *rk = a.qk + (size_t)t * (a.ih + 1) * a.ihd + (size_t)a.ih * a.ihd;
+            for (int i = lane; i < a.ihd; i += 64) a.idx_keys[(size_t)row * a.ihd + i] = qk_ld(rk + i);
+        }
+        qk_wave_lds_sync();
+        at_norm_rope(s, a.k_norm, a.hd, a.rot, a.theta, pos,
+                     a.k_cache + (size_t)row * a.kvh * a.hd + (size_t)kh * a.hd, lane);
+    } else {
+        const int ihh = role - a.h - a.kvh;
+        const float *src = a.qk + (size_t)t * (a.ih + 1) * a.ihd + (size_t)ihh * a.ihd;
+        for (int i = lane; i < a.ihd; i += 64) s[i] = qk_ld(src + i);
+        qk_wave_lds_sync();
+        at_norm_rope(s, a.iq_norm, a.ihd, a.rot, a.theta, pos, a.qi + ((size_t)t * a.ih + ihh) * a.ihd, lane);
+    }
+}
+
+/* ------------------------------------------------------------ QSA block selection */
+
+#define AT_SEL_T 256
+
+struct AtSelArgs {
+    const float *idx_keys;  /* [cap, ihd] */
+    const float *ik_norm;   /* [ihd] */
+    const float *qi;        /* [n, ih, ihd] */
+    uint32_t *keep;         /* [n, kw] */
+    int ih, ihd, comp, nb, btop, offset, rot, kw;
+    float theta;
+};
+
+__global__ __launch_bounds__(AT_SEL_T) void k_at_sel(AtSelArgs a) {
+    extern __shared__ float at_lds[];
+    float *s_q = at_lds;                               /* [ih * ihd] */
+    float *s_p = s_q + a.ih * a.ihd;                   /* [4][ihd] per-wave pooled key */
+    uint32_t *s_key = (uint32_t *)(s_p + 4 * a.ihd);   /* [nb] order keys of the scores */
+    uint32_t *s_bits = s_key + a.nb;                   /* [kw] */
+    int *s_hist = (int *)(s_bits + a.kw);              /* [256] */
+    int *s_misc = s_hist + 256;                        /* [8] */
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, t = blockIdx.x;
+    const int qpos = a.offset + t;
+    for (int i = tid; i < a.ih * a.ihd; i += AT_SEL_T) s_q[i] = qk_ld(a.qi + (size_t)t * a.ih * a.ihd + i);
+    for (int i = tid; i < a.kw; i += AT_SEL_T) s_bits[i] = 0u;
+    __syncthreads();
+    float *pw = s_p + wave * a.ihd;
+    const float inv_sqrt = 1.0f / sqrtf((float)a.ihd);
+    for (int b = wave; b < a.nb; b += 4) {
+        for (int i = lane; i < a.ihd; i += 64) {
+            float acc = 0.0f;
+            for (int j = 0; j < a.comp; j++) acc = acc + qk_ld(a.idx_keys + ((size_t)b * a.comp + j) * a.ihd + i);
+            pw[i] = acc / (float)a.comp;
+        }
+        qk_wave_lds_sync();
+        at_norm_rope(pw, a.ik_norm, a.ihd, a.rot, a.theta, b * a.comp, pw, lane);
+        qk_wave_lds_sync();
+        float sc = 0.0f;
+        for (int hh = 0; hh < a.ih; hh++) {
+            float dot = 0.0f;
+            for (int i = lane; i < a.ihd; i += 64) {
+                const float v = s_q[hh * a.ihd + i] * pw[i];
+                dot = dot + (v > 0.0f ? v : 0.0f);
+            }
+            sc = sc + qk_group_sum<64>(dot);
+        }
+        float score = sc * inv_sqrt;
+        if ((long long)b * a.comp + a.comp - 1 > (long long)qpos) score = -INFINITY;
+        if (lane == 0) s_key[b] = qk_ordkey(score);
+        qk_wave_lds_sync();
+    }
+    __syncthreads();
+    if (a.btop >= a.nb) {
+        for (int b = tid; b < a.nb; b += AT_SEL_T) atomicOr(&s_bits[b >> 5], 1u << (b & 31));
+    } else {
+        /* radix select of the btop-th largest key, 8 bits a pass */
+        uint32_t prefix = 0u, pmask = 0u;
+        int need = a.btop;
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            s_hist[tid] = 0;
+            __syncthreads();
+            for (int b = tid; b < a.nb; b += AT_SEL_T) {
+                const uint32_t k = s_key[b];
+                if ((k & pmask) == prefix) atomicAdd(&s_hist[(k >> shift) & 255], 1);
+            }
+            __syncthreads();
+            if (tid == 0) {
+                int cum = 0, dg = 0;
+                for (dg = 255; dg > 0; dg--) {
+                    if (cum + s_hist[dg] >= need) break;
+                    cum += s_hist[dg];
+                }
+                s_misc[0] = dg;
+                s_misc[1] = need - cum;
+            }
+            __syncthreads();
+            prefix |= (uint32_t)s_misc[0] << shift;
+            pmask |= 255u << shift;
+            need = s_misc[1];
+            __syncthreads();
+        }
+        /* keys above the threshold all, equal ones in block order up to need */
+        const int per = (a.nb + AT_SEL_T - 1) / AT_SEL_T;
+        const int b0 = tid * per;
+        int eq = 0;
+        for (int j = 0; j < per; j++) eq += (b0 + j < a.nb && s_key[b0 + j] == prefix) ? 1 : 0;
+        /* exclusive scan of eq over the threads */
+        int inc = eq;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int u = __shfl_up(inc, o, QK_WAVE);
+            if (lane >= o) inc += u;
+        }
+        if (lane == 63) s_hist[wave] = inc;
+        __syncthreads();
+        int base = 0;
+        for (int w = 0; w < wave; w++) base += s_hist[w];
+        int rank = base + inc - eq;
+        for (int j = 0; j < per; j++) {
+            const int b = b0 + j;
+            if (b >= a.nb) break;
+            const uint32_t k = s_key[b];
+            bool kp = k > prefix;
+            if (k == prefix) {
+                kp = rank < need;
+                rank++;
+            }
+            if (kp) atomicOr(&s_bits[b >> 5], 1u << (b & 31));
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < a.kw; i += AT_SEL_T) a.keep[(size_t)t * a.kw + i] = s_bits[i];
+}
+
+/* ------------------------------------------------------------ attention */
+
+#define AT_CHUNK 256
+
+struct AtAttnArgs {
+    const float *qn;        /* [n, h, hd] */
+    const float *k_cache, *v_cache;
+    const uint32_t *keep;   /* [n, kw] or NULL */
+    float *part;            /* [n, h, nchunks, hd + 2] */
+    int h, kvh, hd, kv_total, offset, comp, nb, kw, nchunks;
+};
+
+__global__ __launch_bounds__(AT_CHUNK) void k_at_attn(AtAttnArgs a) {
+    __shared__ float s_q[256];
+    __shared__ float s_p[AT_CHUNK];
+    __shared__ float s_red[4 * 256];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int t = blockIdx.x / a.h, hh = blockIdx.x - t * a.h, c = blockIdx.y;
+    const int kh = hh % a.kvh, qpos = a.offset + t;
+    const size_t kvw = (size_t)a.kvh * a.hd;
+    for (int i = tid; i < a.hd; i += AT_CHUNK) s_q[i] = qk_ld(a.qn + ((size_t)t * a.h + hh) * a.hd + i);
+    __syncthreads();
+    const int kk = c * AT_CHUNK + tid;
+    float sc = -INFINITY;
+    if (kk < a.kv_total) {
+        const float4 *kr = (const float4 *)(a.k_cache + (size_t)kk * kvw + (size_t)kh * a.hd);
+        float acc = 0.0f;
+        for (int i = 0; i < a.hd / 4; i++) {
+            const float4 k4 = qk_ld(kr + i);
+            acc = fmaf(s_q[4 * i], k4.x, acc);
+            acc = fmaf(s_q[4 * i + 1], k4.y, acc);
+            acc = fmaf(s_q[4 * i + 2], k4.z, acc);
+            acc = fmaf(s_q[4 * i + 3], k4.w, acc);
+        }
+        sc = acc * (1.0f / sqrtf((float)a.hd));
+        if (kk > qpos) sc = -INFINITY;
+        if (a.keep) {
+            const int blk = kk / a.comp;
+            bool kp = blk < a.nb && ((qk_ld(a.keep + (size_t)t * a.kw + (blk >> 5)) >> (blk & 31)) & 1u);
+            const long long own = ((long long)(qpos + 1) / a.comp) * a.comp;
+            if (kk >= own && kk <= qpos) kp = true;
+            if (!kp && kk <= qpos) sc = -INFINITY;
+        }
+    }
+    /* chunk max */
+    float m = sc;
+    m = fmaxf(m, qk_dpp<QK_DPP_XOR1>(m));
+    m = fmaxf(m, qk_dpp<QK_DPP_XOR2>(m));
+    m = fmaxf(m, qk_dpp<QK_DPP_HALF_MIRROR>(m));
+    m = fmaxf(m, qk_dpp<QK_DPP_MIRROR>(m));
+    m = fmaxf(m, __uint_as_float(qk_xor16_u(__float_as_uint(m))));
+    m = fmaxf(m, __uint_as_float(qk_xor32_u(__float_as_uint(m))));
+    if (lane == 0) s_red[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    const float p = m == -INFINITY ? 0.0f : expf(sc - m);
+    s_p[tid] = p;
+    float l = qk_group_sum<64>(p);
+    __syncthreads(); /* s_red reused */
+    if (lane == 0) s_red[wave] = l;
+    __syncthreads();
+    l = ((s_red[0] + s_red[1]) + s_red[2]) + s_red[3];
+    /* exp-weighted v: wave w takes the keys w, w+4, ...; lane the dims lane, lane+64, .. */
+    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int nk = min(AT_CHUNK, a.kv_total - c * AT_CHUNK);
+    for (int j = wave; j < nk; j += 4) {
+        const float pj = s_p[j];
+        const float *vr = a.v_cache + (size_t)(c * AT_CHUNK + j) * kvw + (size_t)kh * a.hd;
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            if (lane + 64 * e < a.hd) o[e] = fmaf(pj, qk_ld(vr + lane + 64 * e), o[e]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        if (lane + 64 * e < a.hd) s_red[wave * 256 + lane + 64 * e] = o[e];
+    __syncthreads();
+    float *dst = a.part + (((size_t)t * a.h + hh) * a.nchunks + c) * (a.hd + 2);
+    for (int i = tid; i < a.hd; i += AT_CHUNK)
+        dst[2 + i] = ((s_red[i] + s_red[256 + i]) + s_red[512 + i]) + s_red[768 + i];
+    if (tid == 0) {
+        dst[0] = m;
+        dst[1] = l;
+    }
+}
+
+struct AtCombArgs {
+    const float *part;      /* [n, h, nchunks, hd + 2] */
+    const float *qg;        /* [n, 2h*hd] */
+    float *ao;              /* [n, h*hd] */
+    int h, hd, nchunks;
+};
+
+__global__ __launch_bounds__(64) void k_at_comb(AtCombArgs a) {
+    const int lane = threadIdx.x, th = blockIdx.x;
+    const int t = th / a.h, hh = th - t * a.h;
+    const float *pp = a.part + (size_t)th * a.nchunks * (a.hd + 2);
+    float M = -INFINITY;
+    for (int c = 0; c < a.nchunks; c++) M = fmaxf(M, qk_ld(pp + (size_t)c * (a.hd + 2)));
+    float L = 0.0f;
+    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c = 0; c < a.nchunks; c++) {
+        const float *q = pp + (size_t)c * (a.hd + 2);
+        const float mc = qk_ld(q);
+        if (mc == -INFINITY) continue;
+        const float f = expf(mc - M);
+        L = fmaf(qk_ld(q + 1), f, L);
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            if (lane + 64 * e < a.hd) o[e] = fmaf(qk_ld(q + 2 + lane + 64 * e), f, o[e]);
+    }
+    const float inv = 1.0f / L;
+    const float *g = a.qg + (size_t)t * 2 * a.h * a.hd + (size_t)hh * 2 * a.hd + a.hd;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int i = lane + 64 * e;
+        if (i < a.hd) a.ao[(size_t)th * a.hd + i] = (o[e] * inv) * (1.0f / (1.0f + expf(-qk_ld(g + i))));
+    }
+}
+
+/* ------------------------------------------------------------ host side */
+
+static int at_rows_launch(RowsArgs &r, hipStream_t st) {
+    const int rows = r.start[r.nseg];
+    const int waves = (rows + AT_RPW - 1) / AT_RPW;
+    const dim3 grid((waves + 3) / 4);
+    switch ((r.K / 32 + 63) / 64) {
+    case 1: hipLaunchKernelGGL(k_rows<1>, grid, dim3(256), 0, st, r); break;
+    case 2: hipLaunchKernelGGL(k_rows<2>, grid, dim3(256), 0, st, r); break;
+    case 3: hipLaunchKernelGGL(k_rows<3>, grid, dim3(256), 0, st, r); break;
+    default: hipLaunchKernelGGL(k_rows<4>, grid, dim3(256), 0, st, r); break;
+    }
+    return QK_CHECK_LAUNCH();
+}
+
+static void at_seg(RowsArgs &r, const uint32_t *q, const uint16_t *s, const uint16_t *b, const uint16_t *w,
+                   int rows, float *out, int ostride) {
+    RowSeg &g = r.seg[r.nseg];
+    g.q = q; g.s = s; g.b = b; g.w = w; g.out = out; g.rows = rows; g.ostride = ostride;
+    r.start[r.nseg + 1] = r.start[r.nseg] + rows;
+    r.nseg++;
+}
+
+extern "C" int qk_at_shape_ok(const qk_at_shape *s) {
+    if (s->d <= 0 || s->d % 64 || s->d > 8192) return 0;
+    if (s->h <= 0 || s->kvh <= 0 || s->h % s->kvh) return 0;
+    if (s->hd <= 0 || s->hd % 64 || s->hd > 256 || (s->h * s->hd) % 64 || s->h * s->hd > 8192) return 0;
+    if (s->ih <= 0 || s->ihd <= 0 || s->ihd % 4 || s->ihd > 256) return 0;
+    if (s->rot < 0 || s->rot % 2 || s->rot > s->hd || s->rot > s->ihd) return 0;
+    if (s->cap <= 0 || s->cap > 8192 || s->comp <= 0 || s->budget <= 0) return 0;
+    return 1;
+}
+
+extern "C" size_t qk_at_sel_lds(const qk_at_shape *s, int nb) {
+    const int kw = (nb + 31) / 32;
+    return ((size_t)s->ih * s->ihd + 4 * (size_t)s->ihd + (size_t)nb + kw + 256 + 8) * 4;
+}
+
+extern "C" int qk_launch_at(const qk_at_shape *s, const qk_at_dev *W, const float *x, int n, int offset,
+                            int len0, float *out, float *k_cache, float *v_cache, float *idx_keys,
+                            const qk_at_scratch *sc, void *stream) {
+    if (n <= 0) return 0;
+    if (!qk_at_shape_ok(s)) return (int)hipErrorInvalidValue;
+    hipStream_t st = (hipStream_t)stream;
+    const int h = s->h, kvh = s->kvh, hd = s->hd, ih = s->ih, ihd = s->ihd;
+    const int kv_total = len0 + n;
+    const int use_idx = kv_total > s->budget;
+
+    RowsArgs r;
+    r.nseg = 0;
+    r.start[0] = 0;
+    r.x = x;
+    r.K = s->d;
+    r.n = n;
+    at_seg(r, W->q_q, W->q_s, W->q_b, nullptr, 2 * h * hd, sc->qg, 2 * h * hd);
+    at_seg(r, W->k_q, W->k_s, W->k_b, nullptr, kvh * hd, sc->kraw, kvh * hd);
+    at_seg(r, W->v_q, W->v_s, W->v_b, nullptr, kvh * hd, sc->vraw, kvh * hd);
+    at_seg(r, nullptr, nullptr, nullptr, W->idx_w, (ih + 1) * ihd, sc->qk, (ih + 1) * ihd);
+    int rc = at_rows_launch(r, st);
+    if (rc) return rc;
+
+    AtQkArgs q;
+    q.qg = sc->qg; q.kraw = sc->kraw; q.vraw = sc->vraw; q.qk = sc->qk;
+    q.q_norm = W->q_norm; q.k_norm = W->k_norm; q.iq_norm = W->idx_q_norm;
+    q.qn = sc->qn; q.k_cache = k_cache; q.v_cache = v_cache; q.idx_keys = idx_keys;
+    q.qi = use_idx ? sc->qi : nullptr;
+    q.n = n; q.h = h; q.kvh = kvh; q.hd = hd; q.ih = ih; q.ihd = ihd; q.len0 = len0;
+    q.offset = offset; q.rot = s->rot; q.theta = s->theta;
+    hipLaunchKernelGGL(k_at_qk, dim3(n, h + kvh + (use_idx ? ih : 0)), dim3(64), 0, st, q);
+    rc = QK_CHECK_LAUNCH();
+    if (rc) return rc;
+
+    const int nb = use_idx ? kv_total / s->comp : 0;
+    const int kw = (nb + 31) / 32;
+    if (use_idx && nb > 0) {
+        AtSelArgs e;
+        e.idx_keys = idx_keys; e.ik_norm = W->idx_k_norm; e.qi = sc->qi; e.keep = sc->keep;
+        e.ih = ih; e.ihd = ihd; e.comp = s->comp; e.nb = nb; e.btop = s->budget / s->comp;
+        e.offset = offset; e.rot = s->rot; e.kw = kw; e.theta = s->theta;
+        hipLaunchKernelGGL(k_at_sel, dim3(n), dim3(AT_SEL_T), qk_at_sel_lds(s, nb), st, e);
+        rc = QK_CHECK_LAUNCH();
+        if (rc) return rc;
+    }
+
+    AtAttnArgs at;
+    at.qn = sc->qn; at.k_cache = k_cache; at.v_cache = v_cache;
+    at.keep = use_idx ? sc->keep : nullptr;
+    at.part = sc->part;
+    at.h = h; at.kvh = kvh; at.hd = hd; at.kv_total = kv_total; at.offset = offset;
+    at.comp = s->comp; at.nb = nb; at.kw = kw;
+    at.nchunks = (kv_total + AT_CHUNK - 1) / AT_CHUNK;
+    hipLaunchKernelGGL(k_at_attn, dim3(n * h, at.nchunks), dim3(AT_CHUNK), 0, st, at);
+    rc = QK_CHECK_LAUNCH();
+    if (rc) return rc;
+
+    AtCombArgs cb;
+    cb.part = sc->part; cb.qg = sc->qg; cb.ao = sc->ao; cb.h = h; cb.hd = hd; cb.nchunks = at.nchunks;
+    hipLaunchKernelGGL(k_at_comb, dim3(n * h), dim3(64), 0, st, cb);
+    rc = QK_CHECK_LAUNCH();
+    if (rc) return rc;
+
+    RowsArgs o;
+    o.nseg = 0;
+    o.start[0] = 0;
+    o.x = sc->ao;
+    o.K = h * hd;
+    o.n = n;
+    at_seg(o, W->o_q, W->o_s, W->o_b, nullptr, s->d, out, s->d);
+    return at_rows_launch(o, st);
+}

@@ -1,0 +1,263 @@
+/*
+ * qmoe_attn.c -- C11 host side of the full-attention mixer with the QSA
+ * indexer: context, HBM residency of each layer's weights and caches, the
+ * cache lengths, argument checks and the launches of attention.hip.
+ * Replaces attention_forward (c/src/model.c:798-1144) and the cache state
+ * around it (model.c:341-345, 402-406).
+ */
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <hip/hip_runtime_api.h>
+
+#include "qmoe_internal.h"
+
+#define AT_ALIGN 256u
+
+enum { AT_Q_Q, AT_Q_S, AT_Q_B, AT_K_Q, AT_K_S, AT_K_B, AT_V_Q, AT_V_S, AT_V_B, AT_O_Q, AT_O_S, AT_O_B,
+       AT_IDX_W, AT_Q_NORM, AT_K_NORM, AT_IQ_NORM, AT_IK_NORM, AT_K_CACHE, AT_V_CACHE, AT_IDX_KEYS,
+       AT_COUNT };
+
+typedef struct {
+    void *mem;
+    int ready, len;
+} at_layer;
+
+struct qmoe_attn_ctx {
+    qmoe_attn_config cfg;
+    qk_at_shape shape;
+    size_t off[AT_COUNT], bytes[AT_COUNT];
+    at_layer *layers;
+    void *scratch;
+    qk_at_scratch sc;
+};
+
+static void at_set_err(qmoe_err *err, const char *fmt, ...) {
+    if (!err) return;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(err->msg, sizeof(err->msg), fmt, ap);
+    va_end(ap);
+}
+
+static int at_hip_fail(qmoe_err *err, int rc, const char *what) {
+    if (rc == 0) return 0;
+    at_set_err(err, "%s: HIP error %d (%s)", what, rc, hipGetErrorString((hipError_t)rc));
+    return -1;
+}
+
+static size_t at_align(size_t v) { return (v + AT_ALIGN - 1) / AT_ALIGN * AT_ALIGN; }
+
+int qmoe_attn_create(qmoe_attn_ctx **out, const qmoe_attn_config *cfg, qmoe_err *err) {
+    if (err) err->msg[0] = 0;
+    if (!out || !cfg) {
+        at_set_err(err, "%s is NULL", out ? "cfg" : "ctx");
+        return -1;
+    }
+    *out = NULL;
+    const qk_at_shape s = {cfg->hidden, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, cfg->idx_heads,
+                           cfg->idx_head_dim, cfg->idx_budget, cfg->idx_compress, cfg->kv_cap,
+                           (int)((float)cfg->head_dim * cfg->rotary_factor), cfg->rope_theta};
+    if (cfg->group_size != 64 || !(cfg->rotary_factor > 0.0f && cfg->rotary_factor <= 1.0f) ||
+        !qk_at_shape_ok(&s)) {
+        at_set_err(err, "attention shape unsupported: hidden %d (multiple of 64, <= 8192), heads %d/%d "
+                        "(kv heads divide heads), head_dim %d (multiple of 64, <= 256, heads*dim <= 8192), "
+                        "indexer %d heads of %d (dim a multiple of 4, <= 256, >= the rotated dims %d, "
+                        "even), budget %d, compress %d, kv_cap %d (<= 8192), group_size %d (64)",
+                   cfg->hidden, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, cfg->idx_heads,
+                   cfg->idx_head_dim, s.rot, cfg->idx_budget, cfg->idx_compress, cfg->kv_cap,
+                   cfg->group_size);
+        return -1;
+    }
+    if (cfg->n_layers < 1 || cfg->max_tokens < 1 || cfg->max_tokens > cfg->kv_cap) {
+        at_set_err(err, "n_layers %d and max_tokens %d must be >= 1 (max_tokens <= kv_cap %d)",
+                   cfg->n_layers, cfg->max_tokens, cfg->kv_cap);
+        return -1;
+    }
+    qmoe_attn_ctx *c = (qmoe_attn_ctx *)calloc(1, sizeof(*c));
+    if (!c) {
+        at_set_err(err, "out of host memory");
+        return -1;
+    }
+    c->cfg = *cfg;
+    c->shape = s;
+    const size_t d = (size_t)s.d, h = (size_t)s.h, kvh = (size_t)s.kvh, hd = (size_t)s.hd;
+    const size_t ih = (size_t)s.ih, ihd = (size_t)s.ihd, cap = (size_t)s.cap;
+    const size_t qr = 2 * h * hd, kr = kvh * hd, orow = d, ok = h * hd;
+    const size_t sz[AT_COUNT] = {
+        qr * d / 2, qr * (d / 64) * 2, qr * (d / 64) * 2,
+        kr * d / 2, kr * (d / 64) * 2, kr * (d / 64) * 2,
+        kr * d / 2, kr * (d / 64) * 2, kr * (d / 64) * 2,
+        orow * ok / 2, orow * (ok / 64) * 2, orow * (ok / 64) * 2,
+        (ih + 1) * ihd * d * 2, hd * 4, hd * 4, ihd * 4, ihd * 4,
+        cap * kr * 4, cap * kr * 4, cap * ihd * 4};
+    size_t total = 0;
+    for (int i = 0; i < AT_COUNT; i++) {
+        c->off[i] = total;
+        c->bytes[i] = sz[i];
+        total = at_align(total + sz[i]);
+    }
+    const size_t n = (size_t)cfg->max_tokens;
+    const size_t nchunks = (cap + 255) / 256, kw = (cap / (size_t)s.comp + 31) / 32 + 1;
+    const size_t ssz[9] = {n * qr * 4, n * kr * 4, n * kr * 4, n * (ih + 1) * ihd * 4, n * h * hd * 4,
+                           n * ih * ihd * 4, n * kw * 4, n * h * nchunks * (hd + 2) * 4, n * h * hd * 4};
+    size_t stot = 0, soff[9];
+    for (int i = 0; i < 9; i++) {
+        soff[i] = stot;
+        stot = at_align(stot + ssz[i]);
+    }
+    c->layers = (at_layer *)calloc((size_t)cfg->n_layers, sizeof(at_layer));
+    if (!c->layers || at_hip_fail(err, (int)hipMalloc(&c->scratch, stot), "scratch")) {
+        free(c->layers);
+        free(c);
+        return -1;
+    }
+    char *b = (char *)c->scratch;
+    c->sc.qg = (float *)(b + soff[0]);
+    c->sc.kraw = (float *)(b + soff[1]);
+    c->sc.vraw = (float *)(b + soff[2]);
+    c->sc.qk = (float *)(b + soff[3]);
+    c->sc.qn = (float *)(b + soff[4]);
+    c->sc.qi = (float *)(b + soff[5]);
+    c->sc.keep = (uint32_t *)(b + soff[6]);
+    c->sc.part = (float *)(b + soff[7]);
+    c->sc.ao = (float *)(b + soff[8]);
+    for (int l = 0; l < cfg->n_layers; l++)
+        if (at_hip_fail(err, (int)hipMalloc(&c->layers[l].mem, total), "layer weights")) {
+            qmoe_attn_destroy(c);
+            return -1;
+        }
+    *out = c;
+    return 0;
+}
+
+void qmoe_attn_destroy(qmoe_attn_ctx *c) {
+    if (!c) return;
+    if (c->layers)
+        for (int l = 0; l < c->cfg.n_layers; l++) hipFree(c->layers[l].mem);
+    hipFree(c->scratch);
+    free(c->layers);
+    free(c);
+}
+
+static int at_check_layer(qmoe_attn_ctx *c, int layer, qmoe_err *err) {
+    if (err) err->msg[0] = 0;
+    if (!c) {
+        at_set_err(err, "ctx is NULL");
+        return -1;
+    }
+    if (layer < 0 || layer >= c->cfg.n_layers) {
+        at_set_err(err, "layer %d out of range [0, %d)", layer, c->cfg.n_layers);
+        return -1;
+    }
+    return 0;
+}
+
+static void *at_ptr(const qmoe_attn_ctx *c, int layer, int t) {
+    return (char *)c->layers[layer].mem + c->off[t];
+}
+
+int qmoe_attn_upload_layer(qmoe_attn_ctx *c, int layer, const qmoe_attn_weights *w, qmoe_err *err) {
+    if (at_check_layer(c, layer, err)) return -1;
+    if (!w) {
+        at_set_err(err, "weights is NULL");
+        return -1;
+    }
+    const void *src[AT_K_CACHE] = {w->q_q, w->q_s, w->q_b, w->k_q, w->k_s, w->k_b, w->v_q, w->v_s,
+                                   w->v_b, w->o_q, w->o_s, w->o_b, w->idx_w, w->q_norm, w->k_norm,
+                                   w->idx_q_norm, w->idx_k_norm};
+    static const char *names[AT_K_CACHE] = {"q_q", "q_s", "q_b", "k_q", "k_s", "k_b", "v_q", "v_s",
+                                            "v_b", "o_q", "o_s", "o_b", "idx_w", "q_norm", "k_norm",
+                                            "idx_q_norm", "idx_k_norm"};
+    for (int i = 0; i < AT_K_CACHE; i++)
+        if (!src[i]) {
+            at_set_err(err, "layer %d: %s is NULL", layer, names[i]);
+            return -1;
+        }
+    c->layers[layer].ready = 0;
+    for (int i = 0; i < AT_K_CACHE; i++)
+        if (at_hip_fail(err, (int)hipMemcpy(at_ptr(c, layer, i), src[i], c->bytes[i], hipMemcpyHostToDevice),
+                        names[i]))
+            return -1;
+    c->layers[layer].len = 0;
+    c->layers[layer].ready = 1;
+    return 0;
+}
+
+int qmoe_attn_reset(qmoe_attn_ctx *c, int layer, qmoe_err *err) {
+    if (err) err->msg[0] = 0;
+    if (!c) {
+        at_set_err(err, "ctx is NULL");
+        return -1;
+    }
+    if (layer == -1) {
+        for (int l = 0; l < c->cfg.n_layers; l++) c->layers[l].len = 0;
+        return 0;
+    }
+    if (at_check_layer(c, layer, err)) return -1;
+    c->layers[layer].len = 0;
+    return 0;
+}
+
+int qmoe_attn_forward(qmoe_attn_ctx *c, int layer, const float *x, int n, int offset, float *out,
+                      void *stream, qmoe_err *err) {
+    if (at_check_layer(c, layer, err)) return -1;
+    if (n < 0 || n > c->cfg.max_tokens) {
+        at_set_err(err, "n = %d out of range [0, max_tokens = %d]", n, c->cfg.max_tokens);
+        return -1;
+    }
+    if (!c->layers[layer].ready) {
+        at_set_err(err, "layer %d has no weights", layer);
+        return -1;
+    }
+    if (offset < 0) {
+        at_set_err(err, "offset %d is negative", offset);
+        return -1;
+    }
+    if (n == 0) return 0;
+    if (!x || !out) {
+        at_set_err(err, "%s is NULL", x ? "out" : "x");
+        return -1;
+    }
+    const int len0 = c->layers[layer].len;
+    if (len0 + n > c->cfg.kv_cap) {
+        at_set_err(err, "layer %d: %d cached + %d new tokens pass kv_cap %d", layer, len0, n, c->cfg.kv_cap);
+        return -1;
+    }
+    qk_at_dev W;
+    W.q_q = (const uint32_t *)at_ptr(c, layer, AT_Q_Q);
+    W.q_s = (const uint16_t *)at_ptr(c, layer, AT_Q_S);
+    W.q_b = (const uint16_t *)at_ptr(c, layer, AT_Q_B);
+    W.k_q = (const uint32_t *)at_ptr(c, layer, AT_K_Q);
+    W.k_s = (const uint16_t *)at_ptr(c, layer, AT_K_S);
+    W.k_b = (const uint16_t *)at_ptr(c, layer, AT_K_B);
+    W.v_q = (const uint32_t *)at_ptr(c, layer, AT_V_Q);
+    W.v_s = (const uint16_t *)at_ptr(c, layer, AT_V_S);
+    W.v_b = (const uint16_t *)at_ptr(c, layer, AT_V_B);
+    W.o_q = (const uint32_t *)at_ptr(c, layer, AT_O_Q);
+    W.o_s = (const uint16_t *)at_ptr(c, layer, AT_O_S);
+    W.o_b = (const uint16_t *)at_ptr(c, layer, AT_O_B);
+    W.idx_w = (const uint16_t *)at_ptr(c, layer, AT_IDX_W);
+    W.q_norm = (const float *)at_ptr(c, layer, AT_Q_NORM);
+    W.k_norm = (const float *)at_ptr(c, layer, AT_K_NORM);
+    W.idx_q_norm = (const float *)at_ptr(c, layer, AT_IQ_NORM);
+    W.idx_k_norm = (const float *)at_ptr(c, layer, AT_IK_NORM);
+    const int rc = qk_launch_at(&c->shape, &W, x, n, offset, len0, out, (float *)at_ptr(c, layer, AT_K_CACHE),
+                                (float *)at_ptr(c, layer, AT_V_CACHE), (float *)at_ptr(c, layer, AT_IDX_KEYS),
+                                &c->sc, stream);
+    if (at_hip_fail(err, rc, "attention launch")) return -1;
+    c->layers[layer].len = len0 + n;
+    return 0;
+}
+
+int qmoe_attn_cache(qmoe_attn_ctx *c, int layer, float **k_cache, float **v_cache, float **idx_keys,
+                    int *len, qmoe_err *err) {
+    if (at_check_layer(c, layer, err)) return -1;
+    if (k_cache) *k_cache = (float *)at_ptr(c, layer, AT_K_CACHE);
+    if (v_cache) *v_cache = (float *)at_ptr(c, layer, AT_V_CACHE);
+    if (idx_keys) *idx_keys = (float *)at_ptr(c, layer, AT_IDX_KEYS);
+    if (len) *len = c->layers[layer].len;
+    return 0;
+}

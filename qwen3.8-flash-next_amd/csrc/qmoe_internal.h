@@ -211,6 +211,36 @@ int qk_launch_dn(const qk_dn_shape *s, const qk_dn_dev *W, const float *x, int n
                  float *core, float *ssp, void *stream);
 int qk_launch_dn_zero(float *p, size_t count, void *stream);
 
+/* the full-attention mixer with the QSA indexer (attention.hip) */
+typedef struct {
+    int d, h, kvh, hd, ih, ihd, budget, comp, cap, rot; /* rot: rotated dims per head */
+    float theta;
+} qk_at_shape;
+typedef struct {
+    const uint32_t *q_q, *k_q, *v_q, *o_q;
+    const uint16_t *q_s, *q_b, *k_s, *k_b, *v_s, *v_b, *o_s, *o_b;
+    const uint16_t *idx_w;
+    const float *q_norm, *k_norm, *idx_q_norm, *idx_k_norm;
+} qk_at_dev;
+typedef struct {
+    float *qg;    /* [n, 2h*hd] */
+    float *kraw;  /* [n, kvh*hd] */
+    float *vraw;  /* [n, kvh*hd] */
+    float *qk;    /* [n, (ih+1)*ihd] */
+    float *qn;    /* [n, h*hd] */
+    float *qi;    /* [n, ih*ihd] */
+    uint32_t *keep; /* [n, ceil(cap/comp/32)] */
+    float *part;  /* [n, h, ceil(cap/256), hd+2] */
+    float *ao;    /* [n, h*hd] */
+} qk_at_scratch;
+int qk_at_shape_ok(const qk_at_shape *s);
+size_t qk_at_sel_lds(const qk_at_shape *s, int nb);
+/* x [n, d] f32 at positions offset.. -> out [n, d]; the caches hold len0
+ * rows before the call and len0 + n after it (len0 + n <= cap) */
+int qk_launch_at(const qk_at_shape *s, const qk_at_dev *W, const float *x, int n, int offset, int len0,
+                 float *out, float *k_cache, float *v_cache, float *idx_keys, const qk_at_scratch *sc,
+                 void *stream);
+
 /* the MLP hyper connection (hyper.hip): shapes it takes (hc <= 8, d and R
  * multiples of 64, d <= 2048, R <= 2048) */
 int qk_hc_shape_ok(int hc, int d, int R);

@@ -78,6 +78,22 @@ class QmoeDnConfig(ctypes.Structure):
                                             "max_tokens")]
 
 
+class QmoeAttnConfig(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_int) for f in ("hidden", "n_heads", "n_kv_heads", "head_dim", "idx_heads",
+                                            "idx_head_dim", "idx_budget", "idx_compress", "kv_cap",
+                                            "group_size")] + \
+               [("rotary_factor", ctypes.c_float), ("rope_theta", ctypes.c_float),
+                ("n_layers", ctypes.c_int), ("max_tokens", ctypes.c_int)]
+
+
+AT_FIELDS = ["q_q", "q_s", "q_b", "k_q", "k_s", "k_b", "v_q", "v_s", "v_b", "o_q", "o_s", "o_b", "idx_w",
+             "q_norm", "k_norm", "idx_q_norm", "idx_k_norm"]
+
+
+class QmoeAttnWeights(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_void_p) for f in AT_FIELDS]
+
+
 DN_FIELDS = ["qkv_q", "qkv_s", "qkv_b", "z_q", "z_s", "z_b", "a_w", "b_w", "out_q", "out_s", "out_b",
              "conv_w", "norm_w", "a_log", "dt_bias"]
 
@@ -118,6 +134,13 @@ SIGNATURES = {
     "qmoe_layer_forward": (_I, [_P, _I, _P, _I, _I, _P, _I, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_moe_forward_host": (_I, [_P, _I, _P, _I, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_set_fused_decode": (_I, [_P, _I, ctypes.POINTER(QmoeErr)]),
+    "qmoe_attn_create": (_I, [ctypes.POINTER(_P), ctypes.POINTER(QmoeAttnConfig), ctypes.POINTER(QmoeErr)]),
+    "qmoe_attn_destroy": (None, [_P]),
+    "qmoe_attn_upload_layer": (_I, [_P, _I, ctypes.POINTER(QmoeAttnWeights), ctypes.POINTER(QmoeErr)]),
+    "qmoe_attn_reset": (_I, [_P, _I, ctypes.POINTER(QmoeErr)]),
+    "qmoe_attn_forward": (_I, [_P, _I, _P, _I, _I, _P, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_attn_cache": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(_P), ctypes.POINTER(_P),
+                             ctypes.POINTER(_I), ctypes.POINTER(QmoeErr)]),
     "qmoe_dn_create": (_I, [ctypes.POINTER(_P), ctypes.POINTER(QmoeDnConfig), ctypes.POINTER(QmoeErr)]),
     "qmoe_dn_destroy": (None, [_P]),
     "qmoe_dn_upload_layer": (_I, [_P, _I, ctypes.POINTER(QmoeDnWeights), ctypes.POINTER(QmoeErr)]),
@@ -698,6 +721,86 @@ class ExpertCache:
         out = (ctypes.c_uint64 * 4)()
         lib().qmoe_xcache_counts(self._h, ctypes.byref(out))
         return dict(hits=out[0], misses=out[1], evictions=out[2], rejected=out[3])
+
+
+class AttentionContext:
+    """Owns a qmoe_attn_ctx: the full-attention mixer's resident layers
+    (weights, k/v and indexer caches) plus device scratch."""
+
+    def __init__(self, hidden, n_heads, n_kv_heads, head_dim, idx_heads, idx_head_dim, idx_budget,
+                 idx_compress, kv_cap=2048, rotary_factor=0.25, rope_theta=1e7, n_layers=1,
+                 max_tokens=1, group_size=64):
+        self.cfg = QmoeAttnConfig(hidden, n_heads, n_kv_heads, head_dim, idx_heads, idx_head_dim,
+                                  idx_budget, idx_compress, kv_cap, group_size, rotary_factor,
+                                  rope_theta, n_layers, max_tokens)
+        self.d, self.h, self.kvh, self.hd = hidden, n_heads, n_kv_heads, head_dim
+        self.ihd, self.cap = idx_head_dim, kv_cap
+        self._h = ctypes.c_void_p()
+        err = QmoeErr()
+        _check(lib().qmoe_attn_create(ctypes.byref(self._h), ctypes.byref(self.cfg), ctypes.byref(err)),
+               err, "qmoe_attn_create")
+
+    def close(self):
+        if self._h:
+            lib().qmoe_attn_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def upload_layer(self, layer: int, host: dict):
+        """host: numpy arrays keyed by AT_FIELDS"""
+        import numpy as np
+        w = QmoeAttnWeights()
+        keep = []
+        for f in AT_FIELDS:
+            a = host.get(f)
+            if a is not None:
+                a = np.ascontiguousarray(a)
+                keep.append(a)
+            setattr(w, f, None if a is None else a.ctypes.data)
+        err = QmoeErr()
+        _check(lib().qmoe_attn_upload_layer(self._h, layer, ctypes.byref(w), ctypes.byref(err)), err,
+               "qmoe_attn_upload_layer")
+
+    def reset(self, layer=-1):
+        err = QmoeErr()
+        _check(lib().qmoe_attn_reset(self._h, layer, ctypes.byref(err)), err, "qmoe_attn_reset")
+
+    def forward(self, layer, x, offset, out=None, stream=None):
+        """x [n, d] f32 CUDA tensor at positions offset.. -> out [n, d]"""
+        import torch
+        n = x.shape[0]
+        if out is None:
+            out = torch.empty((n, self.d), dtype=torch.float32, device=x.device)
+        err = QmoeErr()
+        _check(lib().qmoe_attn_forward(self._h, layer, _ptr(x), n, offset, _ptr(out), _stream(stream),
+                                       ctypes.byref(err)), err, "qmoe_attn_forward")
+        return out
+
+    def forward_raw(self, layer, x_ptr, n, offset, out_ptr, stream_handle):
+        err = QmoeErr()
+        rc = lib().qmoe_attn_forward(self._h, layer, x_ptr, n, offset, out_ptr, stream_handle,
+                                     ctypes.byref(err))
+        return rc, err.msg.decode(errors="replace")
+
+    def cache(self, layer):
+        """device addresses (k, v, indexer keys) and the cached length"""
+        k, v, i = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+        ln = ctypes.c_int()
+        err = QmoeErr()
+        _check(lib().qmoe_attn_cache(self._h, layer, ctypes.byref(k), ctypes.byref(v), ctypes.byref(i),
+                                     ctypes.byref(ln), ctypes.byref(err)), err, "qmoe_attn_cache")
+        return k.value, v.value, i.value, ln.value
 
 
 class DeltaNetContext:

@@ -1,0 +1,134 @@
+"""The HIP full-attention mixer with the QSA indexer (qmoe_attn_*, through
+the C ABI) against the oracle (oracle/attn_oracle.c, pinned by
+tests/test_oracle_attn.py).
+
+Bar: per call, outputs within 2e-2 max-abs and 1e-3 relative L2 of the
+oracle run on the same weights and inputs from the same caches; the k, v
+and indexer-key caches within 1e-4 relative L2.  Dense (budget past the
+cache) and sparse (the QSA block mask active) cases, several shapes,
+prefill chunks and one-token steps.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import load_oracle, load_pkg
+
+orc = load_oracle()
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, REL_L2 = 2e-2, 1e-3
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def rel(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+_hip = None
+
+
+def d2h(ptr, shape):
+    global _hip
+    if _hip is None:
+        _hip = ctypes.CDLL("libamdhip64.so")
+    buf = np.empty(shape, np.float32)
+    assert _hip.hipMemcpy(ctypes.c_void_p(buf.ctypes.data), ctypes.c_void_p(ptr),
+                          ctypes.c_size_t(buf.nbytes), 2) == 0
+    return buf
+
+
+@pytest.fixture(scope="module")
+def torch_dev(gpu):
+    import torch
+    return torch, gpu
+
+
+def run_calls(torch, dev, case, calls, seed=1):
+    d, h, kvh, hd, ih, ihd, budget, comp, cap, rf = case
+    pkg = load_pkg()
+    A = orc.Attention(d, h, kvh, hd, ih, ihd, budget, comp, kv_cap=cap, rotary_factor=rf, seed=seed)
+    st = A.new_state()
+    x = orc.gen_attn_x(sum(calls), d, seed + 50)
+    with pkg.AttentionContext(d, h, kvh, hd, ih, ihd, budget, comp, kv_cap=cap, rotary_factor=rf,
+                              n_layers=2, max_tokens=max(calls)) as ctx:
+        ctx.upload_layer(1, A.arrays())
+        t0 = 0
+        for i, n in enumerate(calls):
+            ref = A.forward(x[t0:t0 + n], st, t0)
+            got = ctx.forward(1, torch.from_numpy(x[t0:t0 + n]).to(dev), t0)
+            torch.cuda.synchronize()
+            g = got.cpu().numpy()
+            err, r = float(np.abs(g - ref).max()), rel(g, ref)
+            kp, vp, ip, ln = ctx.cache(1)
+            assert ln == t0 + n
+            kc = d2h(kp, (ln, kvh * hd))
+            vc = d2h(vp, (ln, kvh * hd))
+            ic = d2h(ip, (ln, ihd))
+            rk, rv, ri = rel(kc, st.k[:ln]), rel(vc, st.v[:ln]), rel(ic, st.idx[:ln])
+            say(f"{case} call {i} (n={n}, cached {ln}, mask {'on' if ln > budget else 'off'}): "
+                f"max-abs {err:.2e} rel-L2 {r:.2e} (|ref| max {np.abs(ref).max():.2f}); "
+                f"caches rel {rk:.1e}/{rv:.1e}/{ri:.1e}")
+            assert err < MAX_ABS and r < REL_L2, (i, err, r)
+            assert rk < 1e-4 and rv < 1e-4 and ri < 1e-4, (i, rk, rv, ri)
+            t0 += n
+
+
+CASES = [
+    # d, h, kvh, hd, idx heads, idx hd, budget, compress, cap, rotary factor
+    (256, 4, 2, 64, 2, 64, 4096, 4, 64, 0.25),
+    (256, 4, 2, 64, 2, 64, 8, 2, 64, 0.25),
+    (192, 2, 1, 64, 2, 32, 6, 3, 48, 0.5),
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_small_shapes(torch_dev, case):
+    torch, dev = torch_dev
+    say(f"case: attention {case}")
+    run_calls(torch, dev, case, [1, 3, 1, 8, 1, 5, 1, 4])
+
+
+def test_model_shape_long_context(torch_dev):
+    """hidden 2048, 16 heads of 128 over 2 kv heads, indexer 4 x 128,
+    rotary 1/4, cache 2048: a 700-token prefill in chunks, then decode
+    steps; the budget of 512 turns the block mask on past 512 keys"""
+    torch, dev = torch_dev
+    case = (2048, 16, 2, 128, 4, 128, 512, 4, 2048, 0.25)
+    say(f"case: attention {case}")
+    run_calls(torch, dev, case, [256, 256, 188, 1, 1, 1], seed=2)
+
+
+def test_dense_model_shape(torch_dev):
+    torch, dev = torch_dev
+    case = (2048, 16, 2, 128, 4, 128, 2048, 4, 2048, 0.25)
+    say(f"case: attention {case}")
+    run_calls(torch, dev, case, [64, 1, 1, 1], seed=3)
+
+
+def test_errors(torch_dev):
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    for bad in [(100, 4, 2, 64, 2, 64, 8, 2, 64), (256, 4, 3, 64, 2, 64, 8, 2, 64),
+                (256, 4, 2, 96, 2, 64, 8, 2, 64), (256, 4, 2, 64, 2, 8, 8, 2, 64)]:
+        with pytest.raises(pkg.QmoeError, match="attention shape unsupported"):
+            pkg.AttentionContext(*bad)
+    with pkg.AttentionContext(256, 4, 2, 64, 2, 64, 8, 2, kv_cap=4, max_tokens=4) as ctx:
+        x = torch.zeros((1, 256), device=dev)
+        with pytest.raises(pkg.QmoeError, match="has no weights"):
+            ctx.forward(0, x, 0)
+        A = orc.Attention(256, 4, 2, 64, 2, 64, 8, 2, kv_cap=4)
+        ctx.upload_layer(0, A.arrays())
+        ctx.forward(0, torch.zeros((4, 256), device=dev), 0)
+        with pytest.raises(pkg.QmoeError, match="pass kv_cap"):
+            ctx.forward(0, x, 4)
+        ctx.reset(0)
+        ctx.forward(0, x, 0)
+        torch.cuda.synchronize()
+        assert ctx.cache(0)[3] == 1
