@@ -568,6 +568,45 @@ int qmoe_attn_forward(qmoe_attn_ctx *ctx, int layer, const float *x, int n, int 
 int qmoe_attn_cache(qmoe_attn_ctx *ctx, int layer, float **k_cache, float **v_cache, float **idx_keys,
                     int *len, qmoe_err *err);
 
+/* ------------------------------------------------- gated residual slots
+ * gated_residual (c/src/model.c:728-796) on its own, for the two hyper
+ * connections that are not the MoE layer's: each decoder layer's
+ * attention-block connection (attn_hyper_connection, model.c:1671-1672,
+ * with inject, applied after the mixer as hyper += inject (x) out,
+ * model.c:1699-1707) and the final mixer before the LM head
+ * (hyper_connection_mixer, model.c:1743-1745, no inject).  The same
+ * arithmetic and kernels as qmoe_hc_mix: normed = per-copy RMSNorm * hc_norm,
+ * w = silu(down(normed)/hc), mixed = mean_h sigmoid(up(w)) * normed,
+ * inject = 2 sigmoid(inject_w(normed)/hc).  A context holds n_slots weight
+ * sets of one shape (a slot per layer plus one for the mixer, say), each
+ * uploaded with or without its inject matrix. */
+typedef struct qmoe_gr_ctx qmoe_gr_ctx;
+
+typedef struct {
+    int hidden;     /* d: multiple of 64, <= 2048 */
+    int hc_count;   /* hc: 1..8 */
+    int hc_lowrank; /* R: multiple of 64, 64..2048 */
+    int n_slots;
+    int max_tokens;
+} qmoe_gr_config;
+
+int qmoe_gr_create(qmoe_gr_ctx **ctx, const qmoe_gr_config *cfg, qmoe_err *err);
+void qmoe_gr_destroy(qmoe_gr_ctx *ctx);
+/* one slot's weights from HOST memory, the layout of qmoe_hc_weights
+ * (model.layers.<i>.attn_hyper_connection.* or
+ * model.hyper_connection_mixer.*, names model.c:1817-1824, 1925-1958);
+ * inject_w NULL makes a slot without inject (the final mixer) */
+int qmoe_gr_upload_slot(qmoe_gr_ctx *ctx, int slot, const qmoe_hc_weights *host, qmoe_err *err);
+/* hyper [n, hc*d] f32 device -> mixed_out [n, d] f32 device and, for a
+ * slot with inject, inject_out [n, hc] (may be NULL: not computed).  A slot
+ * without inject refuses a non-NULL inject_out.  Asynchronous on `stream`;
+ * calls on one context share its scratch, so they run on one stream. */
+int qmoe_gr_mix(qmoe_gr_ctx *ctx, int slot, const float *hyper, int n, float *mixed_out,
+                float *inject_out, void *stream, qmoe_err *err);
+/* hyper[t, j, :] += inject[t, j] * out[t, :] (model.c:1699-1707) */
+int qmoe_gr_inject(qmoe_gr_ctx *ctx, const float *inject, const float *out, int n, float *hyper,
+                   void *stream, qmoe_err *err);
+
 #ifdef __cplusplus
 }
 #endif

@@ -386,11 +386,13 @@ class Hyper:
     [R, hc*d] and input_mix_weight_up [hc*d, R] as q4 (codes U{0..15},
     scales N(0,0.02), biases N(0,0.01)), block_inject_weight [hc, hc*d] bf16
     N(0,0.02), from the same seeded streams as qmoe_hc_synth_layer;
-    hc_norm is all ones there (norm_std = 0) or 1 + N(0, norm_std)."""
+    hc_norm is all ones there (norm_std = 0) or 1 + N(0, norm_std).
+    with_inject=False leaves block_inject_weight out: the final mixer
+    (model.c:1743-1745), whose mix returns no inject."""
 
     KEYS = ("hc_norm", "down_q", "down_s", "down_b", "up_q", "up_s", "up_b", "inject_w")
 
-    def __init__(self, hc, d, lowrank, seed=0, layer=0, group_size=64, norm_std=0.0):
+    def __init__(self, hc, d, lowrank, seed=0, layer=0, group_size=64, norm_std=0.0, with_inject=True):
         self.hc, self.d, self.R, self.g = hc, d, lowrank, group_size
         D, R, g, s, L = hc * d, lowrank, group_size, seed, layer
         self.t = {}
@@ -405,14 +407,15 @@ class Hyper:
         self.t["up_q"] = gen_codes(D * R // 8, s, L, "HC_UP_Q")
         self.t["up_s"] = gen_bf16(D * R // g, s, L, "HC_UP_S", 0.02)
         self.t["up_b"] = gen_bf16(D * R // g, s, L, "HC_UP_B", 0.01)
-        self.t["inject_w"] = gen_bf16(hc * D, s, L, "HC_INJECT_W", 0.02)
+        if with_inject:
+            self.t["inject_w"] = gen_bf16(hc * D, s, L, "HC_INJECT_W", 0.02)
         self._build()
 
     @classmethod
     def from_arrays(cls, hc, d, lowrank, arrays, group_size=64):
         self = cls.__new__(cls)
         self.hc, self.d, self.R, self.g = hc, d, lowrank, group_size
-        self.t = {k: np.ascontiguousarray(arrays[k]) for k in cls.KEYS}
+        self.t = {k: np.ascontiguousarray(arrays[k]) for k in cls.KEYS if arrays.get(k) is not None}
         self._build()
         return self
 
@@ -431,9 +434,10 @@ class Hyper:
         hyper = np.ascontiguousarray(hyper, dtype=np.float32)
         n = hyper.shape[0]
         mixed = np.empty((n, self.d), np.float32)
-        inject = np.empty((n, self.hc), np.float32)
+        inject = np.empty((n, self.hc), np.float32) if "inject_w" in self.t else None
         normed = np.empty((n, self.hc * self.d), np.float32)
-        if lib().orc_hc_mix(ctypes.byref(self.st), _p(hyper), n, _p(mixed), _p(inject), _p(normed)):
+        if lib().orc_hc_mix(ctypes.byref(self.st), _p(hyper), n, _p(mixed),
+                            None if inject is None else _p(inject), _p(normed)):
             raise MemoryError("orc_hc_mix")
         return dict(mixed=mixed, inject=inject, normed=normed)
 
@@ -497,7 +501,7 @@ class DeltaNet:
         self.d, self.hk, self.hv, self.dk, self.dv, self.kc, self.g = d, hk, hv, dk, dv, kc, group_size
         self.key_dim, self.value_dim = hk * dk, hv * dv
         self.conv_dim = 2 * self.key_dim + self.value_dim
-        self.t = {k: np.ascontiguousarray(arrays[k]) for k in cls.KEYS}
+        self.t = {k: np.ascontiguousarray(arrays[k]) for k in cls.KEYS if arrays.get(k) is not None}
         self._build()
         return self
 
@@ -566,7 +570,7 @@ class Attention:
     def from_arrays(cls, proto, arrays):
         self = cls.__new__(cls)
         self.__dict__.update({k: v for k, v in proto.__dict__.items() if k not in ("t", "st")})
-        self.t = {k: np.ascontiguousarray(arrays[k]) for k in cls.KEYS}
+        self.t = {k: np.ascontiguousarray(arrays[k]) for k in cls.KEYS if arrays.get(k) is not None}
         self._build()
         return self
 

@@ -51,7 +51,7 @@ struct HcDownArgs {
  * wave sum and needs no other wave: normed = (x * r) * w with
  * r = 1/sqrt(ss/d + eps) (kernel_rmsnorm_grouped, kernel.c:22-36).  A task
  * is (block of tb tokens, block of HD_RW rows) of either the down matrix
- * (q4) or the inject matrix (bf16); per token each wave leaves its copy's
+ * (q4) or the inject matrix (bf16; no inject blocks when inject_w is NULL); per token each wave leaves its copy's
  * partial row sums in LDS (double-buffered by token parity) and the first
  * threads add the copies in order and apply the activation: silu(v / hc)
  * for down rows (kernel_scale + kernel_silu, model.c:757-758), 2 *
@@ -64,7 +64,7 @@ __global__ __launch_bounds__(64 * HC_MAX) void k_hc_down(HcDownArgs a) {
     const int D = a.hc * a.d, CPC = a.d >> 5, G = D >> 6;
     const size_t wrow = (size_t)D >> 3;
     const int nrb = (a.R + HD_RW - 1) / HD_RW;
-    const int nblk = nrb + (a.hc + HD_RW - 1) / HD_RW;
+    const int nblk = nrb + (a.inject_w ? (a.hc + HD_RW - 1) / HD_RW : 0);
     const int tblk = blockIdx.x / nblk, rb = blockIdx.x - tblk * nblk;
     const bool inj = rb >= nrb;
     const int r0 = inj ? (rb - nrb) * HD_RW : rb * HD_RW;
@@ -350,7 +350,9 @@ extern "C" int qk_launch_hc_down(const float *hyper, const float *norm_w, const 
                                  float *inject, void *stream) {
     if (n <= 0) return 0;
     if (!qk_hc_shape_ok(hc, d, R)) return (int)hipErrorInvalidValue;
-    const int nblk = (R + HD_RW - 1) / HD_RW + (hc + HD_RW - 1) / HD_RW;
+    if (inject_w && !inject) return (int)hipErrorInvalidValue;
+    /* no inject matrix (the final mixer): the down row blocks alone */
+    const int nblk = (R + HD_RW - 1) / HD_RW + (inject_w ? (hc + HD_RW - 1) / HD_RW : 0);
     const int tb = hc_tokens_per_task(n, nblk);
     HcDownArgs a{hyper, norm_w, q, s, b, inject_w, normed, w, inject, hc, d, R, n, tb, eps};
     const dim3 grid((unsigned)(((n + tb - 1) / tb) * nblk)), blk(64 * hc);

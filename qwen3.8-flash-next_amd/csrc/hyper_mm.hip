@@ -9,7 +9,8 @@
  *                columns) with P_g = -128 * (sum of the group's 64 a);
  *   k_hc_mm_down partial products of the down projection over one K range
  *                of one copy h, sum_k a_k W[r, k], and of the inject
- *                projection (bf16 weights) as one more column block;
+ *                projection (bf16 weights; none for the final mixer) as
+ *                one more column block;
  *   k_hc_finish  per token: w = silu(sum_h r_h * partial_h / hc) (the norm
  *                scale is constant over a copy, so it applies after the
  *                product), inject = 2 sigmoid(sum_h r_h * partial_h / hc),
@@ -151,7 +152,8 @@ __global__ __launch_bounds__(256) void k_hc_mm_down(HcMmDownArgs a) {
     const int gpc = a.d >> 6, gper = gpc / a.kspl;
     const int g0 = h * gpc + ks * gper;
     const int t0 = (int)blockIdx.y * NT; /* first column tile of this pass */
-    const bool with_inj = blockIdx.y == 0;
+    const bool with_ss = blockIdx.y == 0;                /* pass 0: the copy's sum of squares */
+    const bool with_inj = with_ss && a.inject_w != nullptr; /* and the inject tile */
     const int r0 = blockIdx.x * HM_BM + 16 * wave;
     const size_t arow = (size_t)min(r0 + c, a.n - 1);
     const float *xr = a.hyper + arow * D;
@@ -160,7 +162,7 @@ __global__ __launch_bounds__(256) void k_hc_mm_down(HcMmDownArgs a) {
 #pragma unroll
     for (int ct = 0; ct < NT; ct++) acc[ct] = qm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const bool iok = c < a.hc;
-    const uint16_t *wi = a.inject_w + (size_t)(iok ? c : 0) * D;
+    const uint16_t *wi = with_inj ? a.inject_w + (size_t)(iok ? c : 0) * D : nullptr;
     float ssp = 0.0f;
 
     HmStage<NC> stg;
@@ -245,7 +247,7 @@ __global__ __launch_bounds__(256) void k_hc_mm_down(HcMmDownArgs a) {
             if (with_inj) qk_st(a.pi + ((size_t)row * 16 + c) * parts + part, acci[i]);
         }
     }
-    if (with_inj) {
+    if (with_ss) {
         ssp += __uint_as_float(qk_xor16_u(__float_as_uint(ssp)));
         ssp += __uint_as_float(qk_xor32_u(__float_as_uint(ssp)));
         if (kq == 0 && r0 + c < a.n) qk_st(a.pss + (size_t)(r0 + c) * parts + part, ssp);
@@ -317,7 +319,7 @@ __global__ __launch_bounds__(512) void k_hc_finish(HcFinishArgs a) {
     __syncthreads();
     for (int r = tid; r < a.R + 16; r += 512) {
         const bool isw = r < a.R;
-        if (!isw && r - a.R >= a.hc) continue;
+        if (!isw && (r - a.R >= a.hc || !a.inject)) continue;
         const float *p = isw ? a.pd + ((size_t)t * a.R + r) * parts
                              : a.pi + ((size_t)t * 16 + (r - a.R)) * parts;
         const float v = hm_parts_dot<PM>(p, parts, lk, s_r);
@@ -498,6 +500,7 @@ extern "C" int qk_launch_hc_mm(const float *hyper, const float *norm_w, const ui
                                float *inject, float *normed, void *stream) {
     if (n <= 0) return 0;
     if (hc < 1 || hc > HC_MAX || d % 64 || R % 64 || R > 2048) return (int)hipErrorInvalidValue;
+    if (inject_w && !inject) return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)stream;
     const int kspl = qk_hc_mm_kspl(hc, d, R, n), parts = hc * kspl;
     /* workspace carve-up (qk_hc_mm_ws_bytes) */
@@ -520,7 +523,7 @@ extern "C" int qk_launch_hc_mm(const float *hyper, const float *norm_w, const ui
     if (nt == 10) hipLaunchKernelGGL(k_hc_mm_down<10>, gd, dim3(256), 0, st, da);
     else if (nt == 8) hipLaunchKernelGGL(k_hc_mm_down<8>, gd, dim3(256), 0, st, da);
     else hipLaunchKernelGGL(k_hc_mm_down<4>, gd, dim3(256), 0, st, da);
-    HcFinishArgs fa{pd, pi, pss, rs, whi, wlo, wp, inject, hc, d, R, n, kspl, eps};
+    HcFinishArgs fa{pd, pi, pss, rs, whi, wlo, wp, inject_w ? inject : nullptr, hc, d, R, n, kspl, eps};
     if (parts <= 4) hipLaunchKernelGGL(k_hc_finish<4>, dim3(n), dim3(512), 0, st, fa);
     else if (parts <= 8) hipLaunchKernelGGL(k_hc_finish<8>, dim3(n), dim3(512), 0, st, fa);
     else if (parts <= 16) hipLaunchKernelGGL(k_hc_finish<16>, dim3(n), dim3(512), 0, st, fa);

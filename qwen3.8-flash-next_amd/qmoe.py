@@ -102,6 +102,10 @@ class QmoeDnWeights(ctypes.Structure):
     _fields_ = [(f, ctypes.c_void_p) for f in DN_FIELDS]
 
 
+class QmoeGrConfig(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_int) for f in ("hidden", "hc_count", "hc_lowrank", "n_slots", "max_tokens")]
+
+
 class QmoeStTensor(ctypes.Structure):
     _fields_ = [("dtype", ctypes.c_int), ("ndim", ctypes.c_int), ("shape", ctypes.c_int64 * 8),
                 ("file", ctypes.c_int), ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64)]
@@ -141,6 +145,11 @@ SIGNATURES = {
     "qmoe_attn_forward": (_I, [_P, _I, _P, _I, _I, _P, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_attn_cache": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(_P), ctypes.POINTER(_P),
                              ctypes.POINTER(_I), ctypes.POINTER(QmoeErr)]),
+    "qmoe_gr_create": (_I, [ctypes.POINTER(_P), ctypes.POINTER(QmoeGrConfig), ctypes.POINTER(QmoeErr)]),
+    "qmoe_gr_destroy": (None, [_P]),
+    "qmoe_gr_upload_slot": (_I, [_P, _I, ctypes.POINTER(QmoeHcWeights), ctypes.POINTER(QmoeErr)]),
+    "qmoe_gr_mix": (_I, [_P, _I, _P, _I, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_gr_inject": (_I, [_P, _P, _P, _I, _P, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_dn_create": (_I, [ctypes.POINTER(_P), ctypes.POINTER(QmoeDnConfig), ctypes.POINTER(QmoeErr)]),
     "qmoe_dn_destroy": (None, [_P]),
     "qmoe_dn_upload_layer": (_I, [_P, _I, ctypes.POINTER(QmoeDnWeights), ctypes.POINTER(QmoeErr)]),
@@ -882,6 +891,79 @@ class DeltaNetContext:
 
     def state_shapes(self):
         return (self.kc - 1, self.conv_dim), (self.hv, self.dv, self.dk)
+
+
+class GatedResidualContext:
+    """Owns a qmoe_gr_ctx: weight slots of gated_residual for the
+    attention-block hyper connections (with inject) and the final mixer
+    (without), plus device scratch."""
+
+    def __init__(self, hidden, hc_count, hc_lowrank, n_slots=1, max_tokens=1):
+        self.cfg = QmoeGrConfig(hidden, hc_count, hc_lowrank, n_slots, max_tokens)
+        self.d, self.hc, self.R = hidden, hc_count, hc_lowrank
+        self.has_inject = [False] * n_slots
+        self._h = ctypes.c_void_p()
+        err = QmoeErr()
+        _check(lib().qmoe_gr_create(ctypes.byref(self._h), ctypes.byref(self.cfg), ctypes.byref(err)),
+               err, "qmoe_gr_create")
+
+    def close(self):
+        if self._h:
+            lib().qmoe_gr_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def upload_slot(self, slot: int, host: dict):
+        """host: numpy arrays keyed by HC_FIELDS; no "inject_w" (or None)
+        makes a slot without inject (the final mixer)"""
+        import numpy as np
+        w = QmoeHcWeights()
+        keep = []
+        for f in HC_FIELDS:
+            a = host.get(f)
+            if a is not None:
+                a = np.ascontiguousarray(a)
+                keep.append(a)
+            setattr(w, f, None if a is None else a.ctypes.data)
+        err = QmoeErr()
+        _check(lib().qmoe_gr_upload_slot(self._h, slot, ctypes.byref(w), ctypes.byref(err)), err,
+               "qmoe_gr_upload_slot")
+        self.has_inject[slot] = host.get("inject_w") is not None
+
+    def mix(self, slot, hyper, mixed=None, inject=None, want_inject=None, stream=None):
+        """hyper [n, hc*d] f32 CUDA tensor -> (mixed [n, d], inject [n, hc] or None);
+        the inject is formed when the slot has inject weights (or want_inject)"""
+        import torch
+        n = hyper.shape[0]
+        if want_inject is None:  # a slot out of range is the library's error to report
+            want_inject = 0 <= slot < len(self.has_inject) and self.has_inject[slot]
+        if mixed is None:
+            mixed = torch.empty((n, self.d), dtype=torch.float32, device=hyper.device)
+        if want_inject and inject is None:
+            inject = torch.empty((n, self.hc), dtype=torch.float32, device=hyper.device)
+        err = QmoeErr()
+        _check(lib().qmoe_gr_mix(self._h, slot, _ptr(hyper), n, _ptr(mixed),
+                                 _ptr(inject) if want_inject else None, _stream(stream),
+                                 ctypes.byref(err)), err, "qmoe_gr_mix")
+        return mixed, inject if want_inject else None
+
+    def inject(self, inject, out, hyper, stream=None):
+        """hyper[t, j] += inject[t, j] * out[t], in place"""
+        err = QmoeErr()
+        _check(lib().qmoe_gr_inject(self._h, _ptr(inject), _ptr(out), hyper.shape[0], _ptr(hyper),
+                                    _stream(stream), ctypes.byref(err)), err, "qmoe_gr_inject")
+        return hyper
 
 
 def synth_fill(t, kind: int, seed: int, layer: int, tag: int, start=0, stddev=1.0, stream=None):

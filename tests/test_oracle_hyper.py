@@ -56,6 +56,22 @@ def test_mix_vs_float64_statement(hc, d, R, n):
     assert np.abs(got["mixed"] - mixed).max() < 1e-5 * scale
 
 
+def test_final_mixer_has_no_inject():
+    """the final mixer (model.c:1743-1745) passes no inject matrix: mixed is
+    the float64 statement's, bit for bit the mix of the same weights with an
+    inject matrix, and no inject comes back"""
+    hc, d, R, n = 4, 128, 64, 4
+    full = orc.Hyper(hc, d, R, seed=5, layer=1, norm_std=0.1)
+    mixer = orc.Hyper(hc, d, R, seed=5, layer=1, norm_std=0.1, with_inject=False)
+    assert "inject_w" not in mixer.arrays()
+    hyper = orc.gen_hyper(n, hc, d, seed=4) * 2.0
+    got = mixer.mix(hyper)
+    assert got["inject"] is None
+    np.testing.assert_array_equal(got["mixed"], full.mix(hyper)["mixed"])
+    mixed, _, _ = gated_residual_f64(full, hyper)
+    assert np.abs(got["mixed"] - mixed).max() < 1e-5 * np.abs(mixed).max()
+
+
 def test_norm_is_per_copy():
     """scaling one copy of the hyper state leaves mixed and inject unchanged
     (a norm over the whole hc*d row would not)"""
