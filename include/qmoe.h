@@ -262,6 +262,26 @@ int qmoe_combine(qmoe_ctx *ctx, const float *y, const int32_t *perm, const float
 int qmoe_layer_forward(qmoe_ctx *ctx, int layer, const void *x, int x_dtype, int n, float *out,
                        int flags, void *stream, qmoe_err *err);
 
+/* qmoe_layer_forward that allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No context: cfg gives the shape (n_layers unused; n <=
+ * max_tokens) and dev_weights the layer as DEVICE pointers in the layout
+ * of qmoe_layer_weights (qmoe_layer_device_weights of a resident layer, or
+ * the caller's own copies); x, out, flags and stream as qmoe_layer_forward,
+ * with the same kernels and the same results.  The scratch is one static
+ * block of QMOE_NOALLOC_SCRATCH_BYTES per GPU, held from the first call on
+ * that GPU until the process ends; a call whose scratch for n tokens does
+ * not fit is refused with an error (hidden 2048, 512 experts, top-10,
+ * moe_inter 512: n <= 459).  Every call on one GPU uses that one block:
+ * calls that overlap on a GPU (two streams or two threads) race.  The
+ * stages all run on `stream`; the call makes no hipMalloc, hipFree or
+ * other allocating call. */
+#define QMOE_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int qmoe_layer_forward_noalloc(const qmoe_config *cfg, const qmoe_layer_weights *dev_weights,
+                               const void *x, int x_dtype, int n, float *out, int flags,
+                               void *stream, qmoe_err *err);
+
 /* enable = 1 runs one-token calls (n = 1) of qmoe_layer_forward and
  * qmoe_hc_layer_forward in two launches (hidden 2048 or 4096, moe_inter 512
  * or 1024, n_experts <= 1024, top_k <= 16): the router with the shared

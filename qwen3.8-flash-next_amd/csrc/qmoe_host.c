@@ -169,6 +169,48 @@ static int check_config(const qmoe_config *c, qmoe_err *err) {
     return 0;
 }
 
+/* the layer scratch for n tokens, carved out of one block: region offsets
+ * (QH_SC_COUNT of them) and the total; rep = bytes of the one-token
+ * replicas (0: none) */
+enum { QH_SC_COUNT = 19 };
+static size_t scratch_plan(qk_shape s, size_t n, size_t rep, size_t offs[QH_SC_COUNT]) {
+    const size_t E = (size_t)s.E, k = (size_t)s.k, H = (size_t)s.H, I = (size_t)s.I;
+    const size_t nw = (n + 31) / 32, rows = n * k + n;
+    const size_t plane = n * H > rows * I ? n * H : rows * I;
+    const size_t sz[QH_SC_COUNT] = {n * (E + 1) * 4, n * k * 4, n * k * 4, n * 4, (E + 1) * 4, n * k * 4,
+                                    n * k * 4, E * nw * 4, E * nw * 4, n * H * 4, rows * I * 4,
+                                    rows * H * 4, (3 * E + 1) * 4, qk_mfma_task_bytes(s, (int)n),
+                                    plane * 2, plane * 2, plane / 64 * 4, rep, 4};
+    size_t total = 0;
+    for (int i = 0; i < QH_SC_COUNT; i++) {
+        offs[i] = total;
+        total = align_up(total + sz[i]);
+    }
+    return total;
+}
+
+static void scratch_bind(qk_scratch *sc, char *b, const size_t offs[QH_SC_COUNT], int with_rep) {
+    sc->logits = (float *)(b + offs[0]);
+    sc->idx = (int32_t *)(b + offs[1]);
+    sc->w = (float *)(b + offs[2]);
+    sc->sg = (float *)(b + offs[3]);
+    sc->offsets = (int32_t *)(b + offs[4]);
+    sc->perm = (int32_t *)(b + offs[5]);
+    sc->pos = (int32_t *)(b + offs[6]);
+    sc->bits = (uint32_t *)(b + offs[7]);
+    sc->wprefix = (int32_t *)(b + offs[8]);
+    sc->xn = (float *)(b + offs[9]);
+    sc->h = (float *)(b + offs[10]);
+    sc->y = (float *)(b + offs[11]);
+    sc->segtab = (int32_t *)(b + offs[12]);
+    sc->tasks = (int32_t *)(b + offs[13]);
+    sc->ahi = (uint16_t *)(b + offs[14]);
+    sc->alo = (uint16_t *)(b + offs[15]);
+    sc->ag = (float *)(b + offs[16]);
+    sc->rep = with_rep ? (uint32_t *)(b + offs[17]) : NULL;
+    sc->status = (uint32_t *)(b + offs[18]);
+}
+
 int qmoe_create(qmoe_ctx **out, const qmoe_config *cfg, qmoe_err *err) {
     clear_err(err);
     if (!out) {
@@ -210,46 +252,16 @@ int qmoe_create(qmoe_ctx **out, const qmoe_config *cfg, qmoe_err *err) {
         return -1;
     }
     /* scratch */
-    const size_t n = (size_t)cfg->max_tokens, E = (size_t)cfg->n_experts, k = (size_t)cfg->top_k;
-    const size_t H = (size_t)cfg->hidden, I = (size_t)cfg->moe_inter;
-    const size_t nw = (n + 31) / 32, rows = n * k + n;
-    const size_t plane = n * H > rows * I ? n * H : rows * I;
     const size_t rep = qk_dec_supported(c->shape) ? qk_dec_replica_bytes(c->shape) : 0;
-    size_t sz[19] = {n * (E + 1) * 4, n * k * 4, n * k * 4, n * 4, (E + 1) * 4, n * k * 4,
-                     n * k * 4, E * nw * 4, E * nw * 4, n * H * 4, rows * I * 4,
-                     rows * H * 4, (3 * E + 1) * 4, qk_mfma_task_bytes(c->shape, (int)n),
-                     plane * 2, plane * 2, plane / 64 * 4, rep, 4};
-    size_t total = 0, offs[19];
-    for (int i = 0; i < 19; i++) {
-        offs[i] = total;
-        total = align_up(total + sz[i]);
-    }
+    size_t offs[QH_SC_COUNT];
+    const size_t total = scratch_plan(c->shape, (size_t)cfg->max_tokens, rep, offs);
     c->scratch_bytes = total;
     if (hip_fail(err, (int)hipMalloc(&c->scratch_mem, total), "hipMalloc(scratch)")) {
         free(c->layers);
         free(c);
         return -1;
     }
-    char *b = (char *)c->scratch_mem;
-    c->sc.logits = (float *)(b + offs[0]);
-    c->sc.idx = (int32_t *)(b + offs[1]);
-    c->sc.w = (float *)(b + offs[2]);
-    c->sc.sg = (float *)(b + offs[3]);
-    c->sc.offsets = (int32_t *)(b + offs[4]);
-    c->sc.perm = (int32_t *)(b + offs[5]);
-    c->sc.pos = (int32_t *)(b + offs[6]);
-    c->sc.bits = (uint32_t *)(b + offs[7]);
-    c->sc.wprefix = (int32_t *)(b + offs[8]);
-    c->sc.xn = (float *)(b + offs[9]);
-    c->sc.h = (float *)(b + offs[10]);
-    c->sc.y = (float *)(b + offs[11]);
-    c->sc.segtab = (int32_t *)(b + offs[12]);
-    c->sc.tasks = (int32_t *)(b + offs[13]);
-    c->sc.ahi = (uint16_t *)(b + offs[14]);
-    c->sc.alo = (uint16_t *)(b + offs[15]);
-    c->sc.ag = (float *)(b + offs[16]);
-    c->sc.rep = rep ? (uint32_t *)(b + offs[17]) : NULL;
-    c->sc.status = (uint32_t *)(b + offs[18]);
+    scratch_bind(&c->sc, (char *)c->scratch_mem, offs, rep != 0);
     if (hip_fail(err, (int)hipMemset(c->sc.status, 0, 4), "clear status") ||
         (rep && hip_fail(err, (int)hipMemset(c->sc.rep, 0xFF, rep), "clear replicas"))) {
         hipFree(c->scratch_mem);
@@ -756,85 +768,103 @@ int qmoe_router(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n, float
  * their activations as packed operand planes (qk_launch_pack_rows).  The
  * MFMA task list is built from the segment table unless the caller says it
  * is already current. */
-/* the GEMV kernels of small segments go to the context's second stream,
- * after everything already on `stream` (fork), and `stream` waits for them
- * before its next launch (join); both work under stream capture */
-static int fork(qmoe_ctx *c, void *stream, qmoe_err *err) {
-    if (hip_fail(err, (int)hipEventRecord(c->ev_fork, (hipStream_t)stream), "fork record")) return -1;
-    return hip_fail(err, (int)hipStreamWaitEvent(c->aux, c->ev_fork, 0), "fork wait");
-}
-static int join(qmoe_ctx *c, void *stream, qmoe_err *err) {
-    if (hip_fail(err, (int)hipEventRecord(c->ev_join, c->aux), "join record")) return -1;
-    return hip_fail(err, (int)hipStreamWaitEvent((hipStream_t)stream, c->ev_join, 0), "join wait");
+/* what the layer's stages run on: the shape, a scratch carve-up, and the
+ * second stream of the mixed MFMA + GEMV stages (NULL: both on `stream`,
+ * in order) */
+typedef struct {
+    qk_shape s;
+    qk_scratch *sc;
+    hipStream_t aux;
+    hipEvent_t ev_fork, ev_join;
+} stage_env;
+
+static stage_env ctx_env(qmoe_ctx *c) {
+    stage_env e = {c->shape, &c->sc, c->aux, c->ev_fork, c->ev_join};
+    return e;
 }
 
-static int mfma_usable(const qmoe_ctx *c, int n, int stage) {
-    const int ok = stage == 2 ? qk_mfma_down_ok(c->shape) : qk_mfma_gateup_ok(c->shape, stage == 0);
+/* the GEMV kernels of small segments go to the second stream, after
+ * everything already on `stream` (fork), and `stream` waits for them before
+ * its next launch (join); both work under stream capture */
+static int fork(const stage_env *e, void *stream, qmoe_err *err) {
+    if (!e->aux) return 0;
+    if (hip_fail(err, (int)hipEventRecord(e->ev_fork, (hipStream_t)stream), "fork record")) return -1;
+    return hip_fail(err, (int)hipStreamWaitEvent(e->aux, e->ev_fork, 0), "fork wait");
+}
+static int join(const stage_env *e, void *stream, qmoe_err *err) {
+    if (!e->aux) return 0;
+    if (hip_fail(err, (int)hipEventRecord(e->ev_join, e->aux), "join record")) return -1;
+    return hip_fail(err, (int)hipStreamWaitEvent((hipStream_t)stream, e->ev_join, 0), "join wait");
+}
+
+static int mfma_usable(qk_shape s, int n, int stage) {
+    const int ok = stage == 2 ? qk_mfma_down_ok(s) : qk_mfma_gateup_ok(s, stage == 0);
     /* the kernels address the operand planes with 32-bit element offsets */
-    const size_t elems = stage == 2 ? (size_t)n * (c->shape.k + 1) * c->shape.I : (size_t)n * c->shape.H;
-    return ok && elems < ((size_t)1 << 31) && n * (c->shape.k + 1) >= QK_MFMA_MIN_M;
+    const size_t elems = stage == 2 ? (size_t)n * (s.k + 1) * s.I : (size_t)n * s.H;
+    return ok && elems < ((size_t)1 << 31) && n * (s.k + 1) >= QK_MFMA_MIN_M;
 }
 
 /* segments with fewer rows than this go to the GEMV kernels (1 = none) */
 static int mfma_min_m(int n) { return n >= QK_MFMA_ALL_N ? 1 : QK_MFMA_MIN_M; }
 
-static int run_gateup(qmoe_ctx *c, const qmoe_layer_weights *W, const void *x, int xbf, int n,
+static int run_gateup(const stage_env *e, const qmoe_layer_weights *W, const void *x, int xbf, int n,
                       const int32_t *perm, const int32_t *segtab, int tasks_ready, float *h,
                       void *stream, qmoe_err *err) {
-    const int mm = mfma_usable(c, n, xbf ? 0 : 1);
+    const qk_shape s = e->s;
+    const qk_scratch *sc = e->sc;
+    const int mm = mfma_usable(s, n, xbf ? 0 : 1);
     const int min_m = mfma_min_m(n);
     const int gemv = !mm || min_m > 1; /* small segments left to the GEMV */
-    const qk_shape s = c->shape;
+    void *gs = mm && e->aux ? (void *)e->aux : stream;
     int rc;
     if (mm) {
         if (!tasks_ready) {
-            rc = qk_launch_mfma_tasks(s, n, segtab, min_m, c->sc.tasks, stream);
+            rc = qk_launch_mfma_tasks(s, n, segtab, min_m, sc->tasks, stream);
             if (hip_fail(err, rc, "mfma tasks")) return -1;
         }
-        rc = qk_launch_pack_rows(x, xbf, (size_t)n, s.H, c->sc.ahi, xbf ? NULL : c->sc.alo, c->sc.ag,
-                                 stream);
+        rc = qk_launch_pack_rows(x, xbf, (size_t)n, s.H, sc->ahi, xbf ? NULL : sc->alo, sc->ag, stream);
         if (hip_fail(err, rc, "pack x")) return -1;
     }
-    if (mm && gemv && fork(c, stream, err)) return -1;
+    if (mm && gemv && fork(e, stream, err)) return -1;
     if (gemv) {
         rc = qk_launch_gateup(W, s, x, xbf, n, perm, segtab, mm ? min_m : 0,
-                              mm ? qk_mfma_small_list(s, n, c->sc.tasks) : NULL, h,
-                              mm ? c->aux : stream);
+                              mm ? qk_mfma_small_list(s, n, sc->tasks) : NULL, h, gs);
         if (hip_fail(err, rc, "gateup")) return -1;
     }
     if (mm) {
-        rc = qk_launch_gateup_mfma(W, s, c->sc.ahi, xbf ? NULL : c->sc.alo, c->sc.ag, n, perm,
-                                   c->sc.tasks, h, stream);
+        rc = qk_launch_gateup_mfma(W, s, sc->ahi, xbf ? NULL : sc->alo, sc->ag, n, perm, sc->tasks, h,
+                                   stream);
         if (hip_fail(err, rc, "gateup mfma")) return -1;
-        if (gemv && join(c, stream, err)) return -1;
+        if (gemv && join(e, stream, err)) return -1;
     }
     return 0;
 }
 
-static int run_down(qmoe_ctx *c, const qmoe_layer_weights *W, const float *h, int n,
+static int run_down(const stage_env *e, const qmoe_layer_weights *W, const float *h, int n,
                     const int32_t *segtab, int tasks_ready, float *y, void *stream, qmoe_err *err) {
-    const int mm = mfma_usable(c, n, 2);
+    const qk_shape s = e->s;
+    const qk_scratch *sc = e->sc;
+    const int mm = mfma_usable(s, n, 2);
     const int min_m = mfma_min_m(n);
     const int gemv = !mm || min_m > 1;
-    const qk_shape s = c->shape;
+    void *gs = mm && e->aux ? (void *)e->aux : stream;
     int rc;
     if (mm) {
         if (!tasks_ready) {
-            rc = qk_launch_mfma_tasks(s, n, segtab, min_m, c->sc.tasks, stream);
+            rc = qk_launch_mfma_tasks(s, n, segtab, min_m, sc->tasks, stream);
             if (hip_fail(err, rc, "mfma tasks")) return -1;
         }
     }
-    if (mm && gemv && fork(c, stream, err)) return -1;
+    if (mm && gemv && fork(e, stream, err)) return -1;
     if (gemv) {
         rc = qk_launch_down(W, s, h, n, segtab, mm ? min_m : 0,
-                            mm ? qk_mfma_small_list(s, n, c->sc.tasks) : NULL, y,
-                            mm ? c->aux : stream);
+                            mm ? qk_mfma_small_list(s, n, sc->tasks) : NULL, y, gs);
         if (hip_fail(err, rc, "down")) return -1;
     }
     if (mm) {
-        rc = qk_launch_down_mfma(W, s, h, n, c->sc.tasks, y, stream);
+        rc = qk_launch_down_mfma(W, s, h, n, sc->tasks, y, stream);
         if (hip_fail(err, rc, "down mfma")) return -1;
-        if (gemv && join(c, stream, err)) return -1;
+        if (gemv && join(e, stream, err)) return -1;
     }
     return 0;
 }
@@ -890,7 +920,8 @@ int qmoe_expert_gateup(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n
     NEED(perm, "perm");
     NEED(segments, "segments");
     NEED(h_out, "h_out");
-    return run_gateup(c, &c->layers[layer].dev, x, x_dtype == QMOE_BF16, n, perm, segments, 0, h_out,
+    const stage_env e = ctx_env(c);
+    return run_gateup(&e, &c->layers[layer].dev, x, x_dtype == QMOE_BF16, n, perm, segments, 0, h_out,
                       stream, err);
 }
 
@@ -938,7 +969,8 @@ int qmoe_expert_down(qmoe_ctx *c, int layer, const float *h, int n, const int32_
     NEED(h, "h");
     NEED(segments, "segments");
     NEED(y_out, "y_out");
-    return run_down(c, &c->layers[layer].dev, h, n, segments, 0, y_out, stream, err);
+    const stage_env e = ctx_env(c);
+    return run_down(&e, &c->layers[layer].dev, h, n, segments, 0, y_out, stream, err);
 }
 
 int qmoe_expert_ffn(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n, const int32_t *perm,
@@ -980,19 +1012,16 @@ static int layer_forward_streamed(qmoe_ctx *c, int layer, const void *x, int xbf
                                   float *out, int residual, float *hyper, const float *inject,
                                   void *stream, qmoe_err *err);
 
-static int layer_forward(qmoe_ctx *c, int layer, const void *x, int xbf, int n, float *out,
-                         int residual, float *hyper, const float *inject, void *stream,
-                         qmoe_err *err) {
-    if (c->streamed)
-        return layer_forward_streamed(c, layer, x, xbf, n, out, residual, hyper, inject, stream, err);
-    c->last_n = n;
-    const qmoe_layer_weights *W = &c->layers[layer].dev;
-    const qk_shape s = c->shape;
-    qk_scratch *sc = &c->sc;
-    const int hc = hyper ? c->hc : 0;
+/* the layer of resident weights W on the stages of e; dec_fused selects
+ * the two-launch one-token path (needs the replicas in e's scratch) */
+static int layer_core(const stage_env *e, const qmoe_layer_weights *W, int dec_fused, int hc,
+                      const void *x, int xbf, int n, float *out, int residual, float *hyper,
+                      const float *inject, void *stream, qmoe_err *err) {
+    const qk_shape s = e->s;
+    qk_scratch *sc = e->sc;
     int rc;
     float *xn = W->norm_w ? sc->xn : NULL;
-    if (n == 1 && sc->rep && c->dec_fused) {
+    if (n == 1 && sc->rep && dec_fused) {
         /* one token: router + shared gate/up, then everything else in one launch */
         rc = qk_launch_dec_layer(W, s, x, xbf, sc->logits, sc->xn, sc->h, sc->rep, sc->status,
                                  sc->idx, sc->w, sc->sg, sc->perm, sc->pos, sc->segtab,
@@ -1014,7 +1043,7 @@ static int layer_forward(qmoe_ctx *c, int layer, const void *x, int xbf, int n, 
     }
     /* the dispatch also builds the MFMA task list when the gate/up runs on
      * MFMA (one launch fewer) */
-    const int gu_mm = n >= 2 && mfma_usable(c, n, xf_bf ? 0 : 1);
+    const int gu_mm = n >= 2 && mfma_usable(s, n, xf_bf ? 0 : 1);
     int32_t *tasks = gu_mm ? sc->tasks : NULL;
     if (n <= QK_SMALL_N && n * s.k <= QK_SMALL_NK) {
         /* offsets are not used by the layer; qmoe_last_routing derives them */
@@ -1029,17 +1058,75 @@ static int layer_forward(qmoe_ctx *c, int layer, const void *x, int xbf, int n, 
                                 sc->bits, sc->wprefix, mfma_min_m(n), tasks, stream);
         if (hip_fail(err, rc, "dispatch")) return -1;
     }
-    if (run_gateup(c, W, xf, xf_bf, n, sc->perm, sc->segtab, gu_mm, sc->h, stream, err)) return -1;
-    if (!mfma_usable(c, n, 2) && qk_down_combine_lds(s, n) > 0) {
+    if (run_gateup(e, W, xf, xf_bf, n, sc->perm, sc->segtab, gu_mm, sc->h, stream, err)) return -1;
+    if (!mfma_usable(s, n, 2) && qk_down_combine_lds(s, n) > 0) {
         rc = qk_launch_down_combine(W, s, sc->h, n, sc->segtab, sc->pos, sc->w, sc->sg,
                                     residual ? x : NULL, xbf, out, hyper, inject, hc, stream);
         return hip_fail(err, rc, "down+combine");
     }
-    if (run_down(c, W, sc->h, n, sc->segtab, mfma_usable(c, n, xf_bf ? 0 : 1), sc->y, stream, err))
+    if (run_down(e, W, sc->h, n, sc->segtab, mfma_usable(s, n, xf_bf ? 0 : 1), sc->y, stream, err))
         return -1;
     rc = qk_launch_combine(s, n, sc->y, sc->pos, sc->w, sc->sg, residual ? x : NULL, xbf, out,
                            hyper, inject, hc, stream);
     return hip_fail(err, rc, "combine");
+}
+
+static int layer_forward(qmoe_ctx *c, int layer, const void *x, int xbf, int n, float *out,
+                         int residual, float *hyper, const float *inject, void *stream,
+                         qmoe_err *err) {
+    if (c->streamed)
+        return layer_forward_streamed(c, layer, x, xbf, n, out, residual, hyper, inject, stream, err);
+    c->last_n = n;
+    const stage_env e = ctx_env(c);
+    return layer_core(&e, &c->layers[layer].dev, c->dec_fused, hyper ? c->hc : 0, x, xbf, n, out,
+                      residual, hyper, inject, stream, err);
+}
+
+int qmoe_layer_forward_noalloc(const qmoe_config *cfg, const qmoe_layer_weights *w, const void *x,
+                               int x_dtype, int n, float *out, int flags, void *stream,
+                               qmoe_err *err) {
+    clear_err(err);
+    if (!cfg || !w) {
+        set_err(err, "%s is NULL", cfg ? "dev_weights" : "cfg");
+        return -1;
+    }
+    if (check_config(cfg, err) || check_dtype(x_dtype, err)) return -1;
+    if (flags & ~QMOE_RESIDUAL) {
+        set_err(err, "unknown flags 0x%x", flags);
+        return -1;
+    }
+    if (n < 0 || n > cfg->max_tokens) {
+        set_err(err, "n = %d out of range [0, max_tokens = %d]", n, cfg->max_tokens);
+        return -1;
+    }
+    const void *need[] = {w->router_w,  w->gate_q,    w->gate_s,    w->gate_b,    w->up_q,
+                          w->up_s,      w->up_b,      w->down_q,    w->down_s,    w->down_b,
+                          w->sh_gate_q, w->sh_gate_s, w->sh_gate_b, w->sh_up_q,   w->sh_up_s,
+                          w->sh_up_b,   w->sh_down_q, w->sh_down_s, w->sh_down_b, w->sh_gate_w};
+    for (size_t i = 0; i < sizeof(need) / sizeof(need[0]); i++)
+        if (!need[i]) {
+            set_err(err, "dev_weights: tensor %zu of the layout is NULL (only router_bias and norm_w "
+                         "may be)", i);
+            return -1;
+        }
+    if (n == 0) return 0;
+    NEED(x, "x");
+    NEED(out, "out");
+    const qk_shape s = {cfg->hidden, cfg->n_experts, cfg->top_k, cfg->moe_inter, cfg->rms_eps};
+    size_t offs[QH_SC_COUNT];
+    const size_t bytes = scratch_plan(s, (size_t)n, 0, offs);
+    if (bytes > QK_NOALLOC_SCRATCH_BYTES) {
+        set_err(err, "n = %d needs %zu bytes of scratch at this shape; the static scratch holds %zu "
+                     "(call with fewer tokens)", n, bytes, (size_t)QK_NOALLOC_SCRATCH_BYTES);
+        return -1;
+    }
+    void *base = NULL;
+    if (hip_fail(err, qk_noalloc_scratch(&base), "static scratch address")) return -1;
+    qk_scratch sc;
+    scratch_bind(&sc, (char *)base, offs, 0);
+    const stage_env e = {s, &sc, NULL, NULL, NULL}; /* every stage on `stream` */
+    return layer_core(&e, w, 0, 0, x, x_dtype == QMOE_BF16, n, out, (flags & QMOE_RESIDUAL) != 0,
+                      NULL, NULL, stream, err);
 }
 
 int qmoe_set_fused_decode(qmoe_ctx *c, int enable, qmoe_err *err) {
@@ -1683,15 +1770,16 @@ static int streamed_experts(qmoe_ctx *c, const qmoe_layer_weights *W, const void
                             const float *inject, int hc, void *stream, qmoe_err *err) {
     const qk_shape s = c->shape;
     qk_scratch *sc = &c->sc;
-    const int gu_mm = n >= 2 && mfma_usable(c, n, xf_bf ? 0 : 1);
-    int rc = run_gateup(c, W, xf, xf_bf, n, sc->perm, c->s_segtab, 0, sc->h, stream, err);
+    const stage_env e = ctx_env(c);
+    const int gu_mm = n >= 2 && mfma_usable(s, n, xf_bf ? 0 : 1);
+    int rc = run_gateup(&e, W, xf, xf_bf, n, sc->perm, c->s_segtab, 0, sc->h, stream, err);
     if (rc) return rc;
-    if (!mfma_usable(c, n, 2) && qk_down_combine_lds(s, n) > 0)
+    if (!mfma_usable(s, n, 2) && qk_down_combine_lds(s, n) > 0)
         return hip_fail(err, qk_launch_down_combine(W, s, sc->h, n, c->s_segtab, sc->pos, sc->w, sc->sg,
                                                     residual ? x : NULL, xbf, out, hyper, inject, hc,
                                                     stream),
                         "down+combine");
-    rc = run_down(c, W, sc->h, n, c->s_segtab, gu_mm, sc->y, stream, err);
+    rc = run_down(&e, W, sc->h, n, c->s_segtab, gu_mm, sc->y, stream, err);
     if (rc) return rc;
     return hip_fail(err, qk_launch_combine(s, n, sc->y, sc->pos, sc->w, sc->sg, residual ? x : NULL, xbf,
                                            out, hyper, inject, hc, stream),

@@ -313,6 +313,11 @@ int qk_launch_synth(void *dst, size_t count, int kind, uint64_t key, uint64_t st
                     void *stream);
 uint64_t qk_tensor_key(uint64_t seed, uint32_t layer, uint32_t tag);
 
+/* the static scratch of qmoe_layer_forward_noalloc (noalloc.hip): its size
+ * and its device address on the current device (looked up once per device) */
+#define QK_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int qk_noalloc_scratch(void **ptr);
+
 #ifdef __cplusplus
 }
 #endif

@@ -136,6 +136,8 @@ SIGNATURES = {
     "qmoe_expert_ffn": (_I, [_P, _I, _P, _I, _I, _P, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_combine": (_I, [_P, _P, _P, _P, _P, _I, _P, _I, _P, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_layer_forward": (_I, [_P, _I, _P, _I, _I, _P, _I, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_layer_forward_noalloc": (_I, [ctypes.POINTER(QmoeConfig), ctypes.POINTER(QmoeLayerWeights), _P,
+                                        _I, _I, _P, _I, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_moe_forward_host": (_I, [_P, _I, _P, _I, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_set_fused_decode": (_I, [_P, _I, ctypes.POINTER(QmoeErr)]),
     "qmoe_attn_create": (_I, [ctypes.POINTER(_P), ctypes.POINTER(QmoeAttnConfig), ctypes.POINTER(QmoeErr)]),
