@@ -1,53 +1,47 @@
 /*
- * decode_layer.hip -- the MoE layer for one token in two launches (gfx950),
+ * decode_layer.hip -- the MoE layer for one token in one launch (gfx950),
  * replacing model.c:1301-1403 of the reference C port for n = 1 (router,
  * top-k + renormalise, dispatch, routed and shared SwiGLU experts, weighted
  * combine).
  *
- * Launch 1, k_dec_front (256 threads per workgroup): workgroups [0, NR)
- * compute the router logits, one wave per row (the E experts, then the
- * shared-expert gate) in the R64 order of router_rows.h; workgroups
- * [NR, NR + NS) compute the shared expert's gate/up GEMV for 8 rows each
- * (h row k), RMS-normalising x themselves when the layer has a norm.
- * Nothing in this launch depends on the routing.
+ * k_dec_layer, 256 threads per workgroup, four roles by workgroup index:
+ *   [0, NR)        router logits, DEC_RT_ROWS rows each (the E experts, then
+ *                  the shared-expert gate), one wave per row in the R64
+ *                  order of router_rows.h, the workgroup's logits going out
+ *                  as one full 64-byte line;
+ *   [NR, +NS)      the shared expert's gate/up GEMV, DEC_RB_G rows each;
+ *   [.., +k*NG)    the routed slots' gate/up GEMV, DEC_RB_G rows of the
+ *                  expert of slot s each: wave 0 waits for the logits and
+ *                  runs the top-k rounds up to slot s, every wave loads its
+ *                  rows, and the remaining rounds and the expert's dispatch
+ *                  position run under the loads;
+ *   [.., +ND)      down + combine for RBD output rows each: wave 0 waits
+ *                  for the logits and ranks the k experts, every wave loads
+ *                  its down rows of every segment, then the workgroup waits
+ *                  for h.
+ * Producers come first in the grid and wait for nothing placed after them.
  *
- * Launch 2, k_dec_experts (1024 threads per workgroup):
- *   workgroups [0, ND): down + combine for RBD output rows each.  Wave 0
- *     selects the top k from the logits and ranks the experts (their
- *     dispatch positions); every wave then issues the loads of its
- *     down-projection rows of every segment, and only then waits for h:
- *     each thread takes its own 8 h values from this workgroup's replica,
- *     converts them to bf16 hi/lo pairs in LDS and puts the sentinel back.
- *   workgroups [ND, ND + k*NG): the routed slots' gate/up GEMV, 32 rows
- *     each, with k_gateup_dec's arithmetic and in-kernel top-k; each pair
- *     of h rows a wave computes is written into every down workgroup's
- *     replica.
+ * The hand-off uses no fence and no lock.  Every logit and h value goes out
+ * as one 64-bit word (tag << 32 | f32 bits) by a relaxed agent-scope atomic
+ * store, and a consumer reads the words with relaxed agent-scope atomic
+ * loads until each carries this launch's tag; only per-location coherence
+ * is relied on.  The tag is epoch + 1, with epoch = C / ND for a 64-bit
+ * counter C that every down workgroup increments once, when it has taken
+ * all of h, and that every workgroup reads as it starts.  C reaches the
+ * next multiple of ND only when the last down workgroup has taken all of h,
+ * and by then every workgroup has read C, since each has produced a word a
+ * down workgroup consumed and that word's tag came from its read.  The next
+ * launch reads C after the kernel boundary, so graph replays need nothing
+ * from the host.
  *
- * The h hand-off uses no fence and no read-modify-write atomic.  Each down
- * workgroup owns a replica [k, I] of the routed h rows (dispatch order)
- * whose words all hold QK_DEC_SENT between launches (set when the context
- * is created).  A gate/up wave writes each row pair with one 64-bit relaxed
- * agent-scope atomic store per replica; a down thread reads its words with
- * 64-bit relaxed agent-scope atomic loads until none holds the sentinel,
- * then stores the sentinel back.  Only per-location coherence is relied on:
- * a word read is either the sentinel or this launch's value, because the
- * previous launch's value was reset by its only reader and the kernel
- * boundary orders that reset before this launch's writes.  A value whose
- * bits equal the sentinel (one NaN pattern) is written as the canonical
- * quiet NaN.  The wait is bounded by time (QK_DEC_WAIT_TICKS of the 100 MHz
- * s_memrealtime clock): on expiry the thread sets QK_DEC_ERR_WAIT in the
- * status word and goes on; while the status word is non-zero the down
- * workgroups write NaN and wait for nothing, until the host clears it
- * (qmoe_decode_status).
+ * Waits are bounded (QK_DEC_WAIT_TICKS of the 100 MHz s_memrealtime
+ * clock): on expiry the thread sets QK_DEC_ERR_WAIT in the status word and
+ * goes on; down workgroups that see the status set write NaN, and
+ * qmoe_decode_status reports it, clears it and resets the hand-off state.
  *
- * Deadlock freedom: only down workgroups wait, and only for gate/up
- * workgroups, which wait for nothing.  The down workgroups come first in
- * the grid and occupy at most ND (< the number of compute units) units, so
- * every gate/up workgroup can be placed whatever the order of placement.
- *
- * Arithmetic: every value is computed as in the three-launch path
- * (k_router, k_gateup_dec<.., TK>, k_down_combine), so outputs and routing
- * are bit-identical to it.
+ * Arithmetic: every value is computed as in the staged path (k_router,
+ * k_gateup_dec, k_down_combine), so outputs and routing are bit-identical
+ * to it.
  */
 #include "qk_device.h"
 #include "gemv_decode.h"
@@ -55,11 +49,13 @@
 #include "router_rows.h"
 #include "topk_wave.h"
 
-#define DEC_WG 1024        /* threads per workgroup of the experts launch */
+#define DEC_WG 256
 #define DEC_WAVES (DEC_WG / 64)
-#define DEC_RB_G 32        /* gate/up rows per workgroup: 16 waves x 2 rows */
-#define DEC_NPASS 8        /* down items per wave, at most */
-#define DEC_FRONT_RB 8     /* shared gate/up rows per front workgroup */
+#define DEC_GRW 4                       /* gate/up rows per wave */
+#define DEC_RB_G (DEC_WAVES * DEC_GRW)  /* gate/up rows per workgroup */
+#define DEC_NPASS 6                     /* down items per wave, at most */
+#define DEC_CTL_BYTES 256               /* epoch, counter; then the tagged words */
+#define DEC_RT_ROWS 8                   /* router rows per workgroup: a 64-byte line of words */
 
 __device__ __forceinline__ uint64_t dec_ald(const uint64_t *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -70,21 +66,35 @@ __device__ __forceinline__ void dec_ast(uint64_t *p, uint64_t v) {
 __device__ __forceinline__ uint32_t dec_ald32(const uint32_t *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-/* bits of a value for the replica: never the sentinel */
-__device__ __forceinline__ uint32_t dec_bits(float v) {
-    const uint32_t b = __float_as_uint(v);
-    return b == QK_DEC_SENT ? 0x7FC00000u : b;
+__device__ __forceinline__ uint64_t dec_word(float v, uint32_t tag) {
+    return ((uint64_t)tag << 32) | __float_as_uint(v);
 }
 
-/* ------------------------------------------------------------ launch 1 */
 
-struct DecFrontArgs {
-    RouterArgs ra;             /* router rows (n = 1) */
-    const uint32_t *sq[2];     /* shared gate, up [I, H/8] */
-    const uint16_t *ss[2], *sb[2];
-    float *h;                  /* [k+1, I]: row k = shared */
-    int NR, k, I;
-};
+/* a workgroup barrier that orders LDS only: loads and stores to global
+ * memory stay in flight across it (__syncthreads would wait for them) */
+__device__ __forceinline__ void dec_lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ void dec_bump(uint64_t *c) {
+    __hip_atomic_fetch_add(c, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* a bounded wait step: false once the bound has passed (status set) */
+__device__ __forceinline__ bool dec_keep_waiting(uint64_t &t0, uint32_t *status) {
+    const uint64_t now = __builtin_amdgcn_s_memrealtime();
+    if (t0 == 0) {
+        t0 = now;
+    } else if (now - t0 > QK_DEC_WAIT_TICKS) {
+        __hip_atomic_fetch_or(status, QK_DEC_ERR_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return false;
+    }
+    __builtin_amdgcn_s_sleep(1);
+    return true;
+}
 
 /*
  * r = 1/sqrt(mean(x^2) + eps) of the token row, in the R64 order of
@@ -186,27 +196,103 @@ __device__ __forceinline__ float dec_row_part(const uint4 (&wq)[CPL], const floa
     return part;
 }
 
-template <bool XBF16, bool NORM, int NCH, int CPL>
-__global__ __launch_bounds__(256) void k_dec_front(DecFrontArgs a) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if ((int)blockIdx.x < a.NR) {
-        const int row = blockIdx.x * 4 + wave;
-        if (row <= a.ra.E) router_rows<XBF16, NORM, NCH>(a.ra, row, 0, 1);
-        return;
+/* ------------------------------------------------------------ arguments */
+
+struct DlArgs {
+    RouterArgs ra;             /* router rows (n = 1) */
+    uint64_t *lt;              /* [E+1] tagged logits */
+    const uint32_t *q[2];      /* routed gate, up [E, I, H/8] */
+    const uint16_t *s[2], *b[2];
+    const uint32_t *sq[2];     /* shared gate, up [I, H/8] */
+    const uint16_t *ss[2], *sb[2];
+    const uint32_t *dq;        /* routed down [E, H, I/8] */
+    const uint16_t *ds, *db;
+    const uint32_t *sdq;       /* shared down [H, I/8] */
+    const uint16_t *sds, *sdb;
+    const void *xres;          /* residual input (x) or NULL */
+    int xres_bf16;
+    uint64_t *ctl;             /* [0] down workgroups past their wait for h, all launches */
+    uint64_t *ht;              /* [(k+1)*I] tagged h: dispatch positions 0..k-1, then shared */
+    uint32_t *status;
+    float *h;                  /* [(k+1)*I] plain copy of h */
+    int32_t *idx;              /* routing outputs (one workgroup writes them) */
+    float *w, *sg;
+    int32_t *perm, *pos, *segtab;
+    float *out;                /* [H] or NULL */
+    float *hyper;              /* [hc, H] or NULL */
+    const float *inject;       /* [hc] */
+    int hc;
+    int H, E, k, I, NR, NS, NG, ND, RBD;
+};
+
+/*
+ * Wave 0 of a consumer: this launch's logits, lane l getting row[l*PL + i]
+ * in lv[i], and the shared-expert gate logit in lsh.  The tagged words are
+ * read lane-contiguous (coalesced) and regrouped through s_lv.  False when
+ * the wait expired (the values are then not this launch's).
+ */
+template <int PL>
+__device__ __forceinline__ bool dec_take_logits(const DlArgs &a, uint32_t tag, float *s_lv,
+                                                int lane, float (&lv)[PL], float &lsh) {
+    const int n = a.E + 1; /* <= 64 * (PL + 1) */
+    uint64_t t0 = 0;
+    /* first one word per lane, spread over the router workgroups' lines
+     * (every lane's line, and lane 0 the last line too): polling every word
+     * slows the producers' own loads */
+    {
+        const int pw = min(lane * DEC_RT_ROWS, n - 1);
+        while ((uint32_t)(dec_ald(a.lt + pw) >> 32) != tag ||
+               (lane == 0 && (uint32_t)(dec_ald(a.lt + n - 1) >> 32) != tag))
+            if (!dec_keep_waiting(t0, a.status)) break;
     }
-    /* shared expert gate/up: rows j*8 + wave*2 + it (64 lanes per row,
-     * lane `lane` owns chunks lane*CPL .. lane*CPL+CPL-1) */
+    uint64_t u[PL + 1];
+    bool all;
+    do {
+#pragma unroll
+        for (int j = 0; j <= PL; j++) u[j] = dec_ald(a.lt + min(lane + 64 * j, n - 1));
+        all = true;
+#pragma unroll
+        for (int j = 0; j <= PL; j++) all &= (uint32_t)(u[j] >> 32) == tag;
+    } while (!all && dec_keep_waiting(t0, a.status));
+#pragma unroll
+    for (int j = 0; j <= PL; j++)
+        if (lane + 64 * j < n) s_lv[lane + 64 * j] = __uint_as_float((uint32_t)u[j]);
+    const bool ok = __all(all);
+    qk_wave_lds_sync();
+#pragma unroll
+    for (int i = 0; i < PL; i++) lv[i] = s_lv[min(lane * PL + i, a.E - 1)];
+    lsh = s_lv[a.E];
+    return ok;
+}
+
+/* ------------------------------------------------------------ gate/up */
+
+/* the workgroup's DEC_RB_G values of h (s_h) out as tagged words and as
+ * plain floats, row r0 + t of segment p */
+__device__ __forceinline__ void dec_put_h(const DlArgs &a, uint32_t tag, int p, int r0,
+                                          const float *s_h) {
+    const int t = threadIdx.x;
+    if (t < DEC_RB_G && r0 + t < a.I) {
+        const size_t i = (size_t)p * a.I + r0 + t;
+        dec_ast(a.ht + i, dec_word(s_h[t], tag));
+        a.h[i] = s_h[t];
+    }
+}
+
+/* the shared expert's gate/up: rows j*DEC_RB_G + wave*DEC_GRW + it */
+template <int CPL, bool XBF16, bool NORM, int NCH>
+__device__ __forceinline__ void dec_gateup_shared(const DlArgs &a, uint32_t tag, int j, float *lds) {
     constexpr bool PB = XBF16 && !NORM;
     constexpr int GPL = CPL >= 2 ? CPL / 2 : 1;
-    const int H = a.ra.H;
-    const int G = H >> 6;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int H = a.H, G = H >> 6;
     const size_t wrow = (size_t)H >> 3;
     const int c0 = lane * CPL, g0 = c0 >> 1;
-    const int rbase = (blockIdx.x - a.NR) * DEC_FRONT_RB + wave * 2;
-    uint4 wq[2][2][CPL];
-    float ws[2][2][GPL], wb[2][2][GPL];
+    const int rbase = j * DEC_RB_G + wave * DEC_GRW;
+    uint4 wq[DEC_GRW][2][CPL];
+    float ws[DEC_GRW][2][GPL], wb[DEC_GRW][2][GPL];
 #pragma unroll
-    for (int it = 0; it < 2; it++) {
+    for (int it = 0; it < DEC_GRW; it++) {
         const int r0 = rbase + it;
         const int r = r0 < a.I ? r0 : 0;
 #pragma unroll
@@ -222,72 +308,44 @@ __global__ __launch_bounds__(256) void k_dec_front(DecFrontArgs a) {
     float xs[CPL];
     dec_act_pairs<CPL, XBF16, NORM, NCH>(a.ra.x, a.ra.norm_w, H, a.ra.eps, lane, c0, hp, lp, xs);
 #pragma unroll
-    for (int it = 0; it < 2; it++) {
+    for (int it = 0; it < DEC_GRW; it++) {
         float acc[2];
 #pragma unroll
         for (int mt = 0; mt < 2; mt++)
             acc[mt] = qk_group_sum<64>(dec_row_part<CPL, PB>(wq[it][mt], ws[it][mt], wb[it][mt], hp, lp, xs));
-        const int r = rbase + it;
-        if (lane == 0 && r < a.I) qk_st(a.h + (size_t)a.k * a.I + r, qk_silu(acc[0]) * acc[1]);
+        if (lane == 0) lds[wave * DEC_GRW + it] = qk_silu(acc[0]) * acc[1];
     }
+    dec_lds_barrier();
+    dec_put_h(a, tag, a.k, j * DEC_RB_G, lds);
 }
 
-/* ------------------------------------------------------------ launch 2 */
-
-struct DecExpertsArgs {
-    const uint32_t *q[2];      /* routed gate, up [E, I, H/8] */
-    const uint16_t *s[2], *b[2];
-    const uint32_t *dq;        /* routed down [E, H, I/8] */
-    const uint16_t *ds, *db;
-    const uint32_t *sdq;       /* shared down [H, I/8] */
-    const uint16_t *sds, *sdb;
-    const void *act;           /* gate/up input: x (bf16 or f32) or the normalised row (f32) */
-    const void *xres;          /* residual input (x) or NULL */
-    int xres_bf16;
-    const float *logits;       /* [E+1] */
-    float *h;                  /* [k+1, I] */
-    uint64_t *rep;             /* [ND, k, I/2] row pairs */
-    uint32_t *status;
-    int32_t *idx;              /* routing outputs (one workgroup writes them) */
-    float *w, *sg;
-    int32_t *perm, *pos, *segtab;
-    float *out;                /* [H] or NULL */
-    float *hyper;              /* [hc, H] or NULL */
-    const float *inject;       /* [hc] */
-    int hc;
-    int H, E, k, I, ND, RBD, NG;
-};
-
-/* routed gate/up: 32 rows (16 waves x 2) of slot `slot`'s expert */
-template <int CPL, bool PB, int PL>
-__device__ __forceinline__ void dec_gateup_routed(const DecExpertsArgs &a, int slot, int rb, int *s_ep) {
+/* routed gate/up: DEC_RB_G rows (block rb) of the expert of slot `slot` */
+template <int CPL, bool XBF16, bool NORM, int NCH, int PL>
+__device__ __forceinline__ void dec_gateup_routed(const DlArgs &a, uint32_t tag, int slot, int rb,
+                                                  float *lds) {
+    constexpr bool PB = XBF16 && !NORM;
     constexpr int GPL = CPL >= 2 ? CPL / 2 : 1;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int H = a.H, G = H >> 6;
     const size_t wrow = (size_t)H >> 3;
     const int c0 = lane * CPL, g0 = c0 >> 1;
+    float *s_h = lds;                               /* [DEC_RB_G] */
+    int *s_i = (int *)(lds + DEC_RB_G);             /* [0] expert, [1] its dispatch position */
+    float *s_lv = lds + DEC_RB_G + 4;               /* [64 * (PL + 1)] */
 
-    /* activations: no routing dependence, issued first */
-    uint4 xd[PB ? CPL : 1][4];
-    float4 xf[PB ? 1 : CPL][8];
-#pragma unroll
-    for (int c = 0; c < CPL; c++) {
-        if (PB) {
-            const uint4 *src = (const uint4 *)((const uint16_t *)a.act) + 4 * (c0 + c);
-#pragma unroll
-            for (int w = 0; w < 4; w++) xd[PB ? c : 0][w] = qk_ld(src + w);
-        } else {
-            const float4 *src = (const float4 *)((const float *)a.act) + 8 * (c0 + c);
-#pragma unroll
-            for (int w = 0; w < 8; w++) xf[PB ? 0 : c][w] = qk_ld(src + w);
-        }
-    }
+    /* the activation pairs do not depend on the routing: formed first */
+    uint32_t hp[CPL][16], lp[PB ? 1 : CPL][16];
+    float xs[CPL];
+    dec_act_pairs<CPL, XBF16, NORM, NCH>(a.ra.x, a.ra.norm_w, H, a.ra.eps, lane, c0, hp, lp, xs);
 
     WaveTopk<PL> tks;
     uint32_t my_key = 0u;
     int my_id = 0x7FFFFFFF;
+    float lsh = 0.0f;
     if (wave == 0) {
-        tks.init(a.logits, a.E, lane);
+        float lv[PL];
+        dec_take_logits<PL>(a, tag, s_lv, lane, lv, lsh);
+        tks.init_vals(lv, a.E, lane);
         int es = 0;
         for (int r = 0; r <= slot; r++) {
             uint32_t m;
@@ -299,15 +357,15 @@ __device__ __forceinline__ void dec_gateup_routed(const DecExpertsArgs &a, int s
             }
             es = ei;
         }
-        if (lane == 0) s_ep[0] = es;
+        if (lane == 0) s_i[0] = min(max(es, 0), a.E - 1);
     }
-    __syncthreads();
-    const int e = s_ep[0];
-    const int rbase = rb * DEC_RB_G + wave * 2;
-    uint4 wq[2][2][CPL];
-    float ws[2][2][GPL], wb[2][2][GPL];
+    dec_lds_barrier();
+    const int e = s_i[0];
+    const int rbase = rb * DEC_RB_G + wave * DEC_GRW;
+    uint4 wq[DEC_GRW][2][CPL];
+    float ws[DEC_GRW][2][GPL], wb[DEC_GRW][2][GPL];
 #pragma unroll
-    for (int it = 0; it < 2; it++) {
+    for (int it = 0; it < DEC_GRW; it++) {
         const int r0 = rbase + it;
         const int r = r0 < a.I ? r0 : 0;
 #pragma unroll
@@ -321,7 +379,7 @@ __device__ __forceinline__ void dec_gateup_routed(const DecExpertsArgs &a, int s
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    /* under the loads: the remaining rounds, then this slot's rank */
+    /* under the loads: the remaining rounds, then this expert's position */
     if (wave == 0) {
         for (int r = slot + 1; r < a.k; r++) {
             uint32_t m;
@@ -333,7 +391,7 @@ __device__ __forceinline__ void dec_gateup_routed(const DecExpertsArgs &a, int s
             }
         }
         const int rank = (int)__popcll(__ballot(my_id < e));
-        if (lane == 0) s_ep[1] = rank;
+        if (lane == 0) s_i[1] = rank;
         if (slot == 0 && rb == 0) {
             const float wt = topk_weight(my_key, a.k, lane);
             int rk = 0;
@@ -349,54 +407,26 @@ __device__ __forceinline__ void dec_gateup_routed(const DecExpertsArgs &a, int s
             }
             if (lane == 0) {
                 a.segtab[0] = a.k;
-                a.sg[0] = qk_sigmoid(qk_ld(a.logits + a.E));
+                a.sg[0] = qk_sigmoid(lsh);
             }
         }
     }
-
-    /* activation pairs (x_i, x_{i+4}) per 8 columns, and chunk sums */
-    uint32_t hp[CPL][16], lp[PB ? 1 : CPL][16];
-    float xs[CPL];
 #pragma unroll
-    for (int c = 0; c < CPL; c++) {
-        if (PB) {
-#pragma unroll
-            for (int w = 0; w < 4; w++) qk_bf16x8_to_pairs(xd[PB ? c : 0][w], &hp[c][4 * w]);
-            float s = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 16; i++) s = qk_dot2(hp[c][i], QK_BF16_ONES, s);
-            xs[c] = s;
-        } else {
-            xs[c] = 0.0f;
-#pragma unroll
-            for (int w = 0; w < 4; w++) {
-                const float4 a0 = xf[PB ? 0 : c][2 * w], a1 = xf[PB ? 0 : c][2 * w + 1];
-                const float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-                qk_f32x8_to_pairs(v, &hp[c][4 * w], &lp[PB ? 0 : c][4 * w], xs[c]);
-            }
-        }
-    }
-    float hv[2];
-#pragma unroll
-    for (int it = 0; it < 2; it++) {
+    for (int it = 0; it < DEC_GRW; it++) {
         float acc[2];
 #pragma unroll
         for (int mt = 0; mt < 2; mt++)
             acc[mt] = qk_group_sum<64>(dec_row_part<CPL, PB>(wq[it][mt], ws[it][mt], wb[it][mt], hp, lp, xs));
-        hv[it] = qk_silu(acc[0]) * acc[1];
+        if (lane == 0) s_h[wave * DEC_GRW + it] = qk_silu(acc[0]) * acc[1];
     }
-    __syncthreads(); /* s_ep[1] */
-    const int p0 = s_ep[1];
-    if (rbase < a.I) {
-        const uint64_t pair = (uint64_t)dec_bits(hv[0]) | ((uint64_t)dec_bits(hv[1]) << 32);
-        const size_t col = (size_t)p0 * (a.I >> 1) + (rbase >> 1);
-        for (int d = lane; d < a.ND; d += 64) dec_ast(a.rep + (size_t)d * a.k * (a.I >> 1) + col, pair);
-        if (lane == 0) {
-            qk_st(a.h + (size_t)p0 * a.I + rbase, hv[0]);
-            qk_st(a.h + (size_t)p0 * a.I + rbase + 1, hv[1]);
-        }
-    }
+    dec_lds_barrier(); /* s_h, s_i[1] */
+    dec_put_h(a, tag, s_i[1], rb * DEC_RB_G, s_h);
 }
+
+/* ------------------------------------------------------------ down */
+
+#define DEC_HW 24 /* tagged h words per thread, at most: (k+1)*I <= DEC_WG * DEC_HW */
+#define DEC_HPH 4 /* h is staged in this many parts */
 
 /*
  * down + combine for output rows r0 .. r0+RBD-1.  Items are (segment,
@@ -405,7 +435,7 @@ __device__ __forceinline__ void dec_gateup_routed(const DecExpertsArgs &a, int s
  * (segment, row) and the combine are k_down_combine's.
  */
 template <int LPRD, int PL>
-__device__ __forceinline__ void dec_down_combine(const DecExpertsArgs &a, float *lds) {
+__device__ __forceinline__ void dec_down_combine(const DlArgs &a, uint32_t tag, float *lds) {
     constexpr int RPW = 64 / LPRD;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int sub = lane % LPRD, rsub = lane / LPRD;
@@ -413,20 +443,27 @@ __device__ __forceinline__ void dec_down_combine(const DecExpertsArgs &a, float 
     const int CH = I >> 5, GI = I >> 6;
     const size_t wrow = (size_t)I >> 3;
     const int RBD = a.RBD;
-    const int r0 = blockIdx.x * RBD;
+    const int r0 = ((int)blockIdx.x - (a.NR + a.NS + a.k * a.NG)) * RBD;
     const int gps = RBD / RPW; /* row groups per segment */
     const int items = (k + 1) * gps;
+    const int nw = (k + 1) * I, half = nw / DEC_HPH; /* words of one part */
 
     float *s_x = lds;                                  /* [(k+1) * CH * 36] pairs, sums */
-    float *s_y = s_x + (size_t)(k + 1) * CH * 36;      /* [(k+1) * RBD] */
+    float *s_hv = s_x + (size_t)(k + 1) * CH * 36;     /* [half] h values of one part */
+    float *s_y = s_hv + half;                          /* [(k+1) * RBD] */
     float *s_pw = s_y + (size_t)(k + 1) * RBD;         /* [k] weight by position */
     int *s_pe = (int *)(s_pw + QK_MAX_TOPK);           /* [k] expert by position */
     int *s_misc = s_pe + QK_MAX_TOPK;                  /* [0] bad, [1] sigmoid bits */
+    float *s_lv = s_x;                                 /* logits, before s_x is used */
 
     if (wave == 0) {
-        const uint32_t st = dec_ald32(a.status);
+        float lv[PL], lsh;
+        const bool ok = dec_take_logits<PL>(a, tag, s_lv, lane, lv, lsh);
+        /* outputs are NaN while the status is set or when a wait of this
+         * workgroup expires */
+        if (lane == 0) s_misc[0] = !ok || dec_ald32(a.status) != 0u;
         WaveTopk<PL> tks;
-        tks.init(a.logits, a.E, lane);
+        tks.init_vals(lv, a.E, lane);
         uint32_t my_key = 0u;
         int my_id = 0x7FFFFFFF;
         for (int r = 0; r < k; r++) {
@@ -442,16 +479,12 @@ __device__ __forceinline__ void dec_down_combine(const DecExpertsArgs &a, float 
         int rk = 0;
         for (int s2 = 0; s2 < k; s2++) rk += __builtin_amdgcn_readlane(my_id, s2) < my_id ? 1 : 0;
         if (lane < k) {
-            s_pe[rk] = my_id;
+            s_pe[rk] = min(max(my_id, 0), a.E - 1);
             s_pw[rk] = wt;
         }
-        if (lane == 0) {
-            s_misc[0] = st != 0u;
-            s_misc[1] = __float_as_int(qk_sigmoid(qk_ld(a.logits + a.E)));
-        }
+        if (lane == 0) s_misc[1] = __float_as_int(qk_sigmoid(lsh));
     }
-    __syncthreads();
-    const bool bad = s_misc[0] != 0;
+    dec_lds_barrier();
 
     /* the down rows of this wave's items (weights do not depend on h) */
     uint4 wq[DEC_NPASS][1];
@@ -479,63 +512,81 @@ __device__ __forceinline__ void dec_down_combine(const DecExpertsArgs &a, float 
         rbv[ps] = qk_ld(bi + (size_t)r * GI + (sub >> 1));
     }
 
-    /* h: thread i takes 8 values (rows 8*q8 .. 8*q8+7 of segment sg8) */
-    const int n8 = (k + 1) * (I >> 3);
-    for (int i = threadIdx.x; i < n8; i += DEC_WG) {
-        const int sg8 = i / (I >> 3), q8 = i - sg8 * (I >> 3);
-        float v[8];
-        if (sg8 < k) {
-            uint64_t *src = a.rep + ((size_t)blockIdx.x * k + sg8) * (I >> 1) + 4 * q8;
-            uint64_t u[4] = {0, 0, 0, 0};
-            if (!bad) {
-                uint64_t t0 = 0;
-                while (true) {
-#pragma unroll
-                    for (int j = 0; j < 4; j++) u[j] = dec_ald(src + j);
-                    bool ok = true;
-#pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        ok &= (uint32_t)u[j] != QK_DEC_SENT && (uint32_t)(u[j] >> 32) != QK_DEC_SENT;
-                    if (ok) break;
-                    const uint64_t now = __builtin_amdgcn_s_memrealtime();
-                    if (t0 == 0) {
-                        t0 = now;
-                    } else if (now - t0 > QK_DEC_WAIT_TICKS) {
-                        __hip_atomic_fetch_or(a.status, QK_DEC_ERR_WAIT, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(1);
-                }
-#pragma unroll
-                for (int j = 0; j < 4; j++) dec_ast(src + j, ((uint64_t)QK_DEC_SENT << 32) | QK_DEC_SENT);
+    /* h in DEC_HPH parts: every thread reads words t + DEC_WG*j of a part
+     * (coalesced; the next part's loads in flight under this part's work)
+     * until each carries this launch's tag; the values go to s_hv and the
+     * units of 8 become bf16 hi/lo pairs with group sums */
+    const int u8 = I >> 3;
+    constexpr int PW = DEC_HW / DEC_HPH;
+    /* one word per thread first (spread over h: every producer's rows are
+     * sampled), then every thread reads all of its words at once until each
+     * carries this launch's tag */
+    bool expired = false;
+    {
+        uint64_t t0 = 0;
+        const int pw = min((int)threadIdx.x * (nw / DEC_WG), nw - 1);
+        while ((uint32_t)(dec_ald(a.ht + pw) >> 32) != tag)
+            if (!dec_keep_waiting(t0, a.status)) {
+                expired = true;
+                break;
             }
+    }
+    dec_lds_barrier();
+    uint64_t u[DEC_HW];
+    {
+        uint64_t t0 = 0;
+        while (true) {
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                v[2 * j] = __uint_as_float((uint32_t)u[j]);
-                v[2 * j + 1] = __uint_as_float((uint32_t)(u[j] >> 32));
+            for (int hh = 0; hh < DEC_HPH; hh++)
+#pragma unroll
+                for (int j = 0; j < PW; j++)
+                    u[hh * PW + j] = dec_ald(a.ht + (size_t)hh * half + min((int)threadIdx.x + DEC_WG * j, half - 1));
+            bool all = true;
+#pragma unroll
+            for (int j = 0; j < DEC_HW; j++) all &= (uint32_t)(u[j] >> 32) == tag;
+            if (all) break;
+            if (!dec_keep_waiting(t0, a.status)) {
+                expired = true;
+                break;
             }
-        } else {
-            const float4 *src = (const float4 *)(a.h + (size_t)k * I + 8 * q8);
-            const float4 f0 = qk_ld(src), f1 = qk_ld(src + 1);
+        }
+    }
+    if (threadIdx.x == 0) dec_bump(a.ctl); /* this workgroup has read all of h */
+#pragma unroll
+    for (int hh = 0; hh < DEC_HPH; hh++) {
+#pragma unroll
+        for (int j = 0; j < PW; j++) {
+            const int i = (int)threadIdx.x + DEC_WG * j;
+            if (i < half) s_hv[i] = __uint_as_float((uint32_t)u[hh * PW + j]);
+        }
+        dec_lds_barrier();
+        {
+            const int i = threadIdx.x; /* a part has at most DEC_WG units of 8 values */
+            const int ui = hh * (half / 8) + min(i, half / 8 - 1);
+            const int sg8 = ui / u8, q8 = ui - sg8 * u8;
+            float v[8];
+            const int li = 8 * min(i, half / 8 - 1);
+            const float4 f0 = *(const float4 *)(s_hv + li), f1 = *(const float4 *)(s_hv + li + 4);
             v[0] = f0.x; v[1] = f0.y; v[2] = f0.z; v[3] = f0.w;
             v[4] = f1.x; v[5] = f1.y; v[6] = f1.z; v[7] = f1.w;
+            uint32_t hi[4], lo[4];
+            const float gs = qk_f32x8_pairs(v, hi, lo);
+            uint32_t *cb = (uint32_t *)s_x + ((size_t)sg8 * CH + (q8 >> 2)) * 36;
+            const int gi = q8 & 3;
+            if (i < half / 8) {
+                *(uint4 *)(cb + 4 * gi) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+                *(uint4 *)(cb + 16 + 4 * gi) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+                ((float *)cb)[32 + gi] = gs;
+            }
         }
-        uint32_t hi[4], lo[4];
-        const float gs = qk_f32x8_pairs(v, hi, lo);
-        uint32_t *cb = (uint32_t *)s_x + ((size_t)sg8 * CH + (q8 >> 2)) * 36;
-        const int gi = q8 & 3;
-        *(uint4 *)(cb + 4 * gi) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-        *(uint4 *)(cb + 16 + 4 * gi) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-        ((float *)cb)[32 + gi] = gs;
+        dec_lds_barrier();
     }
-    __syncthreads();
 
     /* y for every item */
 #pragma unroll
     for (int ps = 0; ps < DEC_NPASS; ps++) {
         const int item = ps * DEC_WAVES + wave;
-        if (item >= items) break;
+        if (item >= items) continue;
         const int sgm = item / gps, g = item - sgm * gps;
         const uint32_t *cb = (const uint32_t *)s_x + ((size_t)sgm * CH + sub) * 36;
         XPairs<LPRD, 1, false> xp;
@@ -557,7 +608,9 @@ __device__ __forceinline__ void dec_down_combine(const DecExpertsArgs &a, float 
         const float v = qk_group_sum<LPRD>(row_part<LPRD, 1, false>(wq[ps], wsv, wbv, xp));
         if (sub == 0) s_y[sgm * RBD + g * RPW + rsub] = v;
     }
-    __syncthreads();
+    if (expired) s_misc[0] = 1;
+    dec_lds_barrier();
+    const bool bad = s_misc[0] != 0;
 
     /* combine: out = sum over positions of w*y, then sigmoid * y_shared, + x */
     for (int t = threadIdx.x; t < RBD; t += DEC_WG) {
@@ -580,16 +633,41 @@ __device__ __forceinline__ void dec_down_combine(const DecExpertsArgs &a, float 
     }
 }
 
-template <int CPL, int LPRD, bool PB, int PL>
-__global__ __launch_bounds__(DEC_WG) void k_dec_experts(DecExpertsArgs a) {
+/* ------------------------------------------------------------ the launch */
+
+template <int CPL, int LPRD, bool XBF16, bool NORM, int NCH, int PL>
+__global__ __launch_bounds__(DEC_WG) void k_dec_layer(DlArgs a) {
     extern __shared__ float dec_lds[];
-    if ((int)blockIdx.x < a.ND) {
-        dec_down_combine<LPRD, PL>(a, dec_lds);
+    const uint32_t tag = (uint32_t)(dec_ald(a.ctl) / (uint64_t)a.ND) + 1u;
+    const int b = blockIdx.x;
+    if (b < a.NR) {
+        /* whole-line stores: partial-line stores under polling reach the
+         * readers several times slower */
+        const int wave = threadIdx.x >> 6;
+#pragma unroll
+        for (int i = 0; i < DEC_RT_ROWS / DEC_WAVES; i++) {
+            const int row = b * DEC_RT_ROWS + i * DEC_WAVES + wave;
+            if (row <= a.E) {
+                const float v = router_rows<XBF16, NORM, NCH>(a.ra, row, 0, 1);
+                if ((threadIdx.x & 63) == 0) dec_lds[i * DEC_WAVES + wave] = v;
+            }
+        }
+        dec_lds_barrier();
+        const int row = b * DEC_RT_ROWS + (int)threadIdx.x;
+        if ((int)threadIdx.x < DEC_RT_ROWS && row <= a.E) dec_ast(a.lt + row, dec_word(dec_lds[threadIdx.x], tag));
         return;
     }
-    const int gi = blockIdx.x - a.ND;
-    const int slot = gi / a.NG, rb = gi - slot * a.NG;
-    dec_gateup_routed<CPL, PB, PL>(a, slot, rb, (int *)dec_lds);
+    if (b < a.NR + a.NS) {
+        dec_gateup_shared<CPL, XBF16, NORM, NCH>(a, tag, b - a.NR, dec_lds);
+        return;
+    }
+    const int g = b - a.NR - a.NS;
+    if (g < a.k * a.NG) {
+        const int slot = g / a.NG;
+        dec_gateup_routed<CPL, XBF16, NORM, NCH, PL>(a, tag, slot, g - slot * a.NG, dec_lds);
+        return;
+    }
+    dec_down_combine<LPRD, PL>(a, tag, dec_lds);
 }
 
 /* ------------------------------------------------------------ host side */
@@ -602,126 +680,104 @@ static int dec_pl(int E) {
 
 /* rows per down workgroup: the largest power of two <= 32 dividing H with
  * every (segment, row group) item of a workgroup within DEC_NPASS passes;
- * 0 when none fits */
+ * 0 when none fits (16 lanes per down row, so 4 rows per wave item) */
 static int dec_rbd(qk_shape s) {
-    const int rpw = 64 / (s.I / 32);
-    for (int rbd = 32; rbd >= rpw; rbd >>= 1)
-        if (s.H % rbd == 0 && (s.k + 1) * (rbd / rpw) <= DEC_NPASS * DEC_WAVES) return rbd;
+    for (int rbd = 32; rbd >= 4; rbd >>= 1)
+        if (s.H % rbd == 0 && (s.k + 1) * (rbd / 4) <= DEC_NPASS * DEC_WAVES) return rbd;
     return 0;
+}
+
+static size_t dec_up256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+extern "C" size_t qk_dec_lds(qk_shape s) {
+    const int rbd = dec_rbd(s);
+    const size_t down = ((size_t)(s.k + 1) * (s.I / 32) * 36 + (size_t)(s.k + 1) * s.I / DEC_HPH +
+                         (size_t)(s.k + 1) * rbd + 2 * QK_MAX_TOPK + 4) * 4;
+    const size_t gateup = (size_t)(DEC_RB_G + 4 + 64 * (dec_pl(s.E) + 1)) * 4;
+    return down > gateup ? down : gateup;
 }
 
 extern "C" int qk_dec_supported(qk_shape s) {
     const int ch = s.H / 32;
-    const int lprd = s.I / 32;
-    if (!(ch == 64 || ch == 128)) return 0; /* gate/up: 64 lanes x 1 or 2 chunks */
-    if (!(lprd == 16 || lprd == 32) || s.I % DEC_RB_G) return 0;
-    if (s.E < s.k || s.E > 64 * 16 || s.k > 16) return 0;
-    if ((size_t)(s.k + 1) * s.I / 8 > DEC_WG) return 0; /* one 8-group of h per thread */
-    const int rbd = dec_rbd(s);
-    if (!rbd || s.H / rbd > 256) return 0;
+    if (!(ch == 64 || ch == 128)) return 0;          /* gate/up: 64 lanes x 1 or 2 chunks */
+    if (s.I != 512) return 0;                        /* down: 16 lanes per row of h */
+    if (s.E < s.k || s.E > 64 * 16 || s.k > QK_MAX_TOPK) return 0;
+    if ((s.k + 1) * s.I > DEC_WG * DEC_HW || (s.k + 1) * s.I % (8 * DEC_HPH)) return 0; /* h parts */
+    if (!dec_rbd(s)) return 0;
+    if ((size_t)(s.k + 1) * (s.I / 32) * 36 < (size_t)64 * (dec_pl(s.E) + 1)) return 0; /* logits in s_x */
     return qk_dec_lds(s) <= 65536;
 }
 
-extern "C" size_t qk_dec_lds(qk_shape s) {
-    const int rbd = dec_rbd(s);
-    return ((size_t)(s.k + 1) * (s.I / 32) * 36 + (size_t)(s.k + 1) * rbd + 2 * QK_MAX_TOPK + 2) * 4;
+extern "C" size_t qk_dec_handoff_bytes(qk_shape s) {
+    return DEC_CTL_BYTES + dec_up256((size_t)(s.E + 1) * 8) + dec_up256((size_t)(s.k + 1) * s.I * 8);
 }
 
-extern "C" size_t qk_dec_replica_bytes(qk_shape s) {
-    const int rbd = dec_rbd(s);
-    return rbd ? (size_t)(s.H / rbd) * s.k * s.I * 4 : 0;
-}
-
-template <bool XBF16, bool NORM>
-static void dec_front_launch(int cpl, dim3 grid, const DecFrontArgs &f, hipStream_t st) {
-    if (cpl == 1) hipLaunchKernelGGL((k_dec_front<XBF16, NORM, 4, 1>), grid, dim3(256), 0, st, f);
-    else hipLaunchKernelGGL((k_dec_front<XBF16, NORM, 8, 2>), grid, dim3(256), 0, st, f);
-}
-
-template <int CPL, int LPRD, bool PB>
-static void dec_experts_launch(int pl, dim3 grid, size_t lds, const DecExpertsArgs &e, hipStream_t st) {
+template <int CPL, bool XBF16, bool NORM>
+static void dec_launch(int pl, dim3 grid, size_t lds, const DlArgs &a, hipStream_t st) {
+    constexpr int NCH = 4 * CPL; /* router: chunks of 8 per lane */
     switch (pl) {
-    case 2: hipLaunchKernelGGL((k_dec_experts<CPL, LPRD, PB, 2>), grid, dim3(DEC_WG), lds, st, e); break;
-    case 4: hipLaunchKernelGGL((k_dec_experts<CPL, LPRD, PB, 4>), grid, dim3(DEC_WG), lds, st, e); break;
-    case 8: hipLaunchKernelGGL((k_dec_experts<CPL, LPRD, PB, 8>), grid, dim3(DEC_WG), lds, st, e); break;
-    default: hipLaunchKernelGGL((k_dec_experts<CPL, LPRD, PB, 16>), grid, dim3(DEC_WG), lds, st, e); break;
+    case 2: hipLaunchKernelGGL((k_dec_layer<CPL, 16, XBF16, NORM, NCH, 2>), grid, dim3(DEC_WG), lds, st, a); break;
+    case 4: hipLaunchKernelGGL((k_dec_layer<CPL, 16, XBF16, NORM, NCH, 4>), grid, dim3(DEC_WG), lds, st, a); break;
+    case 8: hipLaunchKernelGGL((k_dec_layer<CPL, 16, XBF16, NORM, NCH, 8>), grid, dim3(DEC_WG), lds, st, a); break;
+    default: hipLaunchKernelGGL((k_dec_layer<CPL, 16, XBF16, NORM, NCH, 16>), grid, dim3(DEC_WG), lds, st, a); break;
     }
 }
 
 extern "C" int qk_launch_dec_layer(const qmoe_layer_weights *W, qk_shape s, const void *x, int x_bf16,
-                                   float *logits, float *xn, float *h, uint32_t *rep, uint32_t *status,
+                                   float *logits, float *xn, float *h, void *handoff, uint32_t *status,
                                    int32_t *idx, float *w, float *sg, int32_t *perm, int32_t *pos,
                                    int32_t *segtab, const void *x_res, float *out, float *hyper,
                                    const float *inject, int hc, void *stream) {
-    if (!qk_dec_supported(s)) return (int)hipErrorInvalidValue;
+    if (!qk_dec_supported(s) || !handoff) return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)stream;
     const int cpl = s.H / 2048;
     const bool norm = W->norm_w != nullptr;
-
-    DecFrontArgs f;
-    f.ra.router_w = W->router_w;
-    f.ra.router_bias = W->router_bias;
-    f.ra.sh_gate_w = W->sh_gate_w;
-    f.ra.norm_w = W->norm_w;
-    f.ra.x = x;
-    f.ra.logits = logits;
-    f.ra.xn = norm ? xn : nullptr;
-    f.ra.H = s.H;
-    f.ra.E = s.E;
-    f.ra.n = 1;
-    f.ra.eps = s.eps;
-    f.sq[0] = W->sh_gate_q; f.ss[0] = W->sh_gate_s; f.sb[0] = W->sh_gate_b;
-    f.sq[1] = W->sh_up_q;   f.ss[1] = W->sh_up_s;   f.sb[1] = W->sh_up_b;
-    f.h = h;
-    f.NR = (s.E + 1 + 3) / 4;
-    f.k = s.k;
-    f.I = s.I;
-    const dim3 fgrid(f.NR + s.I / DEC_FRONT_RB);
-    if (x_bf16) {
-        if (norm) dec_front_launch<true, true>(cpl, fgrid, f, st);
-        else dec_front_launch<true, false>(cpl, fgrid, f, st);
-    } else {
-        if (norm) dec_front_launch<false, true>(cpl, fgrid, f, st);
-        else dec_front_launch<false, false>(cpl, fgrid, f, st);
-    }
-    int rc = QK_CHECK_LAUNCH();
-    if (rc) return rc;
-
-    DecExpertsArgs e;
-    e.q[0] = W->gate_q; e.s[0] = W->gate_s; e.b[0] = W->gate_b;
-    e.q[1] = W->up_q;   e.s[1] = W->up_s;   e.b[1] = W->up_b;
-    e.dq = W->down_q; e.ds = W->down_s; e.db = W->down_b;
-    e.sdq = W->sh_down_q; e.sds = W->sh_down_s; e.sdb = W->sh_down_b;
-    const bool pb = x_bf16 && !norm;
-    e.act = norm ? (const void *)xn : x;
-    e.xres = x_res;
-    e.xres_bf16 = x_bf16;
-    e.logits = logits;
-    e.h = h;
-    e.rep = (uint64_t *)rep;
-    e.status = status;
-    e.idx = idx; e.w = w; e.sg = sg; e.perm = perm; e.pos = pos; e.segtab = segtab;
-    e.out = out;
-    e.hyper = hyper;
-    e.inject = inject;
-    e.hc = hc;
-    e.H = s.H; e.E = s.E; e.k = s.k; e.I = s.I;
-    e.RBD = dec_rbd(s);
-    e.ND = s.H / e.RBD;
-    e.NG = s.I / DEC_RB_G;
-    const dim3 egrid(e.ND + s.k * e.NG);
+    char *hb = (char *)handoff;
+    DlArgs a;
+    a.ra.router_w = W->router_w;
+    a.ra.router_bias = W->router_bias;
+    a.ra.sh_gate_w = W->sh_gate_w;
+    a.ra.norm_w = W->norm_w;
+    a.ra.x = x;
+    a.ra.logits = logits;
+    a.ra.xn = norm ? xn : nullptr;
+    a.ra.H = s.H;
+    a.ra.E = s.E;
+    a.ra.n = 1;
+    a.ra.eps = s.eps;
+    a.lt = (uint64_t *)(hb + DEC_CTL_BYTES);
+    a.q[0] = W->gate_q; a.s[0] = W->gate_s; a.b[0] = W->gate_b;
+    a.q[1] = W->up_q;   a.s[1] = W->up_s;   a.b[1] = W->up_b;
+    a.sq[0] = W->sh_gate_q; a.ss[0] = W->sh_gate_s; a.sb[0] = W->sh_gate_b;
+    a.sq[1] = W->sh_up_q;   a.ss[1] = W->sh_up_s;   a.sb[1] = W->sh_up_b;
+    a.dq = W->down_q; a.ds = W->down_s; a.db = W->down_b;
+    a.sdq = W->sh_down_q; a.sds = W->sh_down_s; a.sdb = W->sh_down_b;
+    a.xres = x_res;
+    a.xres_bf16 = x_bf16;
+    a.ctl = (uint64_t *)hb;
+    a.ht = (uint64_t *)(hb + DEC_CTL_BYTES + dec_up256((size_t)(s.E + 1) * 8));
+    a.status = status;
+    a.h = h;
+    a.idx = idx; a.w = w; a.sg = sg; a.perm = perm; a.pos = pos; a.segtab = segtab;
+    a.out = out;
+    a.hyper = hyper;
+    a.inject = inject;
+    a.hc = hc;
+    a.H = s.H; a.E = s.E; a.k = s.k; a.I = s.I;
+    a.NR = (s.E + 1 + DEC_RT_ROWS - 1) / DEC_RT_ROWS;
+    a.NS = s.I / DEC_RB_G;
+    a.NG = s.I / DEC_RB_G;
+    a.RBD = dec_rbd(s);
+    a.ND = s.H / a.RBD;
+    const dim3 grid(a.NR + a.NS + s.k * a.NG + a.ND);
     const size_t lds = qk_dec_lds(s);
     const int pl = dec_pl(s.E);
-    const int lprd = s.I / 32;
-#define DEC_EX(C, L) \
-    (pb ? dec_experts_launch<C, L, true>(pl, egrid, lds, e, st) : dec_experts_launch<C, L, false>(pl, egrid, lds, e, st))
     if (cpl == 1) {
-        if (lprd == 16) DEC_EX(1, 16);
-        else DEC_EX(1, 32);
+        if (x_bf16) norm ? dec_launch<1, true, true>(pl, grid, lds, a, st) : dec_launch<1, true, false>(pl, grid, lds, a, st);
+        else norm ? dec_launch<1, false, true>(pl, grid, lds, a, st) : dec_launch<1, false, false>(pl, grid, lds, a, st);
     } else {
-        if (lprd == 16) DEC_EX(2, 16);
-        else DEC_EX(2, 32);
+        if (x_bf16) norm ? dec_launch<2, true, true>(pl, grid, lds, a, st) : dec_launch<2, true, false>(pl, grid, lds, a, st);
+        else norm ? dec_launch<2, false, true>(pl, grid, lds, a, st) : dec_launch<2, false, false>(pl, grid, lds, a, st);
     }
-#undef DEC_EX
     return QK_CHECK_LAUNCH();
 }

@@ -35,7 +35,7 @@ struct qmoe_ctx {
     qmoe_layer_slot *layers;
     size_t layer_bytes;
     int last_n; /* token count of the last qmoe_layer_forward, -1 if none */
-    int dec_fused; /* one-token calls in two launches (qk_launch_dec_layer) when supported */
+    int dec_fused; /* one-token calls in one launch (qk_launch_dec_layer) when supported */
     /* second stream for the GEMV kernels of small segments, which run beside
      * the MFMA kernels of large ones (fork/join with two events) */
     hipStream_t aux;
@@ -171,7 +171,7 @@ static int check_config(const qmoe_config *c, qmoe_err *err) {
 
 /* the layer scratch for n tokens, carved out of one block: region offsets
  * (QH_SC_COUNT of them) and the total; rep = bytes of the one-token
- * replicas (0: none) */
+ * hand-off block (0: none) */
 enum { QH_SC_COUNT = 19 };
 static size_t scratch_plan(qk_shape s, size_t n, size_t rep, size_t offs[QH_SC_COUNT]) {
     const size_t E = (size_t)s.E, k = (size_t)s.k, H = (size_t)s.H, I = (size_t)s.I;
@@ -207,7 +207,7 @@ static void scratch_bind(qk_scratch *sc, char *b, const size_t offs[QH_SC_COUNT]
     sc->ahi = (uint16_t *)(b + offs[14]);
     sc->alo = (uint16_t *)(b + offs[15]);
     sc->ag = (float *)(b + offs[16]);
-    sc->rep = with_rep ? (uint32_t *)(b + offs[17]) : NULL;
+    sc->rep = with_rep ? (void *)(b + offs[17]) : NULL;
     sc->status = (uint32_t *)(b + offs[18]);
 }
 
@@ -252,7 +252,7 @@ int qmoe_create(qmoe_ctx **out, const qmoe_config *cfg, qmoe_err *err) {
         return -1;
     }
     /* scratch */
-    const size_t rep = qk_dec_supported(c->shape) ? qk_dec_replica_bytes(c->shape) : 0;
+    const size_t rep = qk_dec_supported(c->shape) ? qk_dec_handoff_bytes(c->shape) : 0;
     size_t offs[QH_SC_COUNT];
     const size_t total = scratch_plan(c->shape, (size_t)cfg->max_tokens, rep, offs);
     c->scratch_bytes = total;
@@ -263,7 +263,7 @@ int qmoe_create(qmoe_ctx **out, const qmoe_config *cfg, qmoe_err *err) {
     }
     scratch_bind(&c->sc, (char *)c->scratch_mem, offs, rep != 0);
     if (hip_fail(err, (int)hipMemset(c->sc.status, 0, 4), "clear status") ||
-        (rep && hip_fail(err, (int)hipMemset(c->sc.rep, 0xFF, rep), "clear replicas"))) {
+        (rep && hip_fail(err, (int)hipMemset(c->sc.rep, 0, rep), "clear hand-off"))) {
         hipFree(c->scratch_mem);
         free(c->layers);
         free(c);
@@ -1013,7 +1013,7 @@ static int layer_forward_streamed(qmoe_ctx *c, int layer, const void *x, int xbf
                                   void *stream, qmoe_err *err);
 
 /* the layer of resident weights W on the stages of e; dec_fused selects
- * the two-launch one-token path (needs the replicas in e's scratch) */
+ * the one-launch one-token path (needs the hand-off block in e's scratch) */
 static int layer_core(const stage_env *e, const qmoe_layer_weights *W, int dec_fused, int hc,
                       const void *x, int xbf, int n, float *out, int residual, float *hyper,
                       const float *inject, void *stream, qmoe_err *err) {
@@ -1022,7 +1022,7 @@ static int layer_core(const stage_env *e, const qmoe_layer_weights *W, int dec_f
     int rc;
     float *xn = W->norm_w ? sc->xn : NULL;
     if (n == 1 && sc->rep && dec_fused) {
-        /* one token: router + shared gate/up, then everything else in one launch */
+        /* one token: the whole layer in one launch */
         rc = qk_launch_dec_layer(W, s, x, xbf, sc->logits, sc->xn, sc->h, sc->rep, sc->status,
                                  sc->idx, sc->w, sc->sg, sc->perm, sc->pos, sc->segtab,
                                  residual ? x : NULL, out, hyper, inject, hc, stream);
@@ -1136,7 +1136,7 @@ int qmoe_set_fused_decode(qmoe_ctx *c, int enable, qmoe_err *err) {
         return -1;
     }
     if (enable && !c->sc.rep) {
-        set_err(err, "the two-launch one-token layer does not take this shape (hidden %d, "
+        set_err(err, "the one-launch one-token layer does not take this shape (hidden %d, "
                      "n_experts %d, top_k %d, moe_inter %d)", c->cfg.hidden, c->cfg.n_experts,
                 c->cfg.top_k, c->cfg.moe_inter);
         return -1;
@@ -1156,10 +1156,10 @@ int qmoe_decode_status(qmoe_ctx *c, uint32_t *flags, qmoe_err *err) {
         hip_fail(err, (int)hipMemcpy(flags, c->sc.status, 4, hipMemcpyDeviceToHost), "read status"))
         return -1;
     if (*flags == 0) return 0;
-    /* a wait expired: put every replica word back to the sentinel and clear
+    /* a wait expired: zero the hand-off block (epoch, counter, tagged words) and clear
      * the status, so later one-token calls start from a clean hand-off */
-    if ((c->sc.rep && hip_fail(err, (int)hipMemset(c->sc.rep, 0xFF, qk_dec_replica_bytes(c->shape)),
-                               "reset replicas")) ||
+    if ((c->sc.rep && hip_fail(err, (int)hipMemset(c->sc.rep, 0, qk_dec_handoff_bytes(c->shape)),
+                               "reset hand-off")) ||
         hip_fail(err, (int)hipMemset(c->sc.status, 0, 4), "clear status"))
         return -1;
     set_err(err, "a one-token layer call waited past its bound for h (flags 0x%x); its output "

@@ -46,7 +46,7 @@ typedef struct {
     uint32_t *bits;    /* [E, ceil(n/32)] token membership bitmask (large dispatch) */
     int32_t *wprefix;  /* [E, ceil(n/32)] per-word exclusive popcount prefix */
     float *xn;         /* [n, H] normalised router input */
-    uint32_t *rep;     /* one-token h replicas (qk_dec_replica_bytes) or NULL */
+    void *rep;         /* one-token hand-off block (qk_dec_handoff_bytes) or NULL */
     uint32_t *status;  /* [1] expired waits of the one-token launch */
     float *h;          /* [n*k+n, I] */
     float *y;          /* [n*k+n, H] */
@@ -175,19 +175,18 @@ int qk_launch_combine(qk_shape s, int n, const float *y, const int32_t *pos, con
                       const float *sg, const void *x_res, int x_bf16, float *out, float *hyper,
                       const float *inject, int hc, void *stream);
 
-/* one token in two launches (decode_layer.hip): router + shared gate/up,
- * then top-k + routed gate/up and down + combine in one launch whose down
- * workgroups take h through per-workgroup replicas (rep, qk_dec_replica_bytes
- * bytes, every word QK_DEC_SENT between launches) and record an expired
- * wait in *status.  Bit-identical to the staged kernels. */
-#define QK_DEC_SENT 0xFFFFFFFFu
+/* one token in one launch (decode_layer.hip): router, shared and routed
+ * gate/up, down + combine, handing the logits and h over inside the launch
+ * through tagged words in `handoff` (qk_dec_handoff_bytes, zero before the
+ * first call) and recording an expired wait in *status.  Bit-identical to
+ * the staged kernels. */
 #define QK_DEC_WAIT_TICKS 2000000ull /* 20 ms of the 100 MHz s_memrealtime clock */
 #define QK_DEC_ERR_WAIT 1u
 int qk_dec_supported(qk_shape s);
 size_t qk_dec_lds(qk_shape s);
-size_t qk_dec_replica_bytes(qk_shape s);
+size_t qk_dec_handoff_bytes(qk_shape s);
 int qk_launch_dec_layer(const qmoe_layer_weights *W, qk_shape s, const void *x, int x_bf16,
-                        float *logits, float *xn, float *h, uint32_t *rep, uint32_t *status,
+                        float *logits, float *xn, float *h, void *handoff, uint32_t *status,
                         int32_t *idx, float *w, float *sg, int32_t *perm, int32_t *pos,
                         int32_t *segtab, const void *x_res, float *out, float *hyper,
                         const float *inject, int hc, void *stream);

@@ -55,9 +55,10 @@ __device__ __forceinline__ void load_x8(const void *x, size_t row_off, int c, fl
  * all loads issue back to back.  With NORM, every wave RMS-normalises its
  * tokens itself (R64 sum of squares, r = 1/sqrt(ss/H + eps), (x*r)*w as
  * kernel.c:10-20) and the wave of row 0 writes the normalised rows.
+ * Returns the last token's logit (complete in lane 0).
  */
 template <bool XBF16, bool NORM, int NCH>
-__device__ __forceinline__ void router_rows(const RouterArgs &a, int row, int t0, int t1) {
+__device__ __forceinline__ float router_rows(const RouterArgs &a, int row, int t0, int t1) {
     const int lane = threadIdx.x & 63;
     const int chunks = a.H >> 3;
     const uint16_t *wrow = row < a.E ? a.router_w + (size_t)row * a.H : a.sh_gate_w;
@@ -72,6 +73,7 @@ __device__ __forceinline__ void router_rows(const RouterArgs &a, int row, int t0
         wv[i] = qk_ld((const uint4 *)wrow + cc[i]);
     }
     const float bias = (row < a.E && a.router_bias) ? a.router_bias[row] : 0.0f;
+    float last = 0.0f;
     for (int t = t0; t < t1; t++) {
         const size_t roff = (size_t)t * a.H;
         float v[NCH][8];
@@ -122,7 +124,9 @@ __device__ __forceinline__ void router_rows(const RouterArgs &a, int row, int t0
             if (row < a.E && a.router_bias) acc = acc + bias;
             a.logits[(size_t)t * (a.E + 1) + row] = acc;
         }
+        last = acc;
     }
+    return last; /* the logit of token t1-1 (lane 0 adds the bias) */
 }
 
 #endif

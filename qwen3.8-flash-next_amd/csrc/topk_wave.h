@@ -37,7 +37,6 @@ struct WaveTopk {
     uint32_t pk0, pk1;   /* their local indices, 4 bits each (entries past 8 in pk1) */
 
     __device__ __forceinline__ void init(const float *row, int E, int lane) {
-        int ii[PL]; /* local index i of each sorted entry */
         float lv[PL];
         if (PL % 4 == 0 && E % PL == 0) {
             /* whole float4s; lanes past the row read its last PL values (unused) */
@@ -57,6 +56,13 @@ struct WaveTopk {
                 lv[i] = qk_ld(row + (e < E ? e : E - 1));
             }
         }
+        init_vals(lv, E, lane);
+    }
+
+    /* the same from values already loaded: lv[i] = row[lane*PL + i] (any
+     * value where that index is past E) */
+    __device__ __forceinline__ void init_vals(const float (&lv)[PL], int E, int lane) {
+        int ii[PL]; /* local index i of each sorted entry */
 #pragma unroll
         for (int i = 0; i < PL; i++) {
             const int e = lane * PL + i;

@@ -497,14 +497,14 @@ class MoeContext:
         return rc, err.msg.decode(errors="replace")
 
     def set_fused_decode(self, enable: bool):
-        """one-token calls in two launches (True) or through the staged
+        """one-token calls in one launch (True) or through the staged
         kernels (False, the default); the outputs are bit-identical"""
         err = QmoeErr()
         _check(lib().qmoe_set_fused_decode(self._h, 1 if enable else 0, ctypes.byref(err)), err,
                "qmoe_set_fused_decode")
 
     def decode_status(self):
-        """synchronises; raises QmoeError if a two-launch one-token call gave
+        """synchronises; raises QmoeError if a one-launch one-token call gave
         up its wait for h since the last check (its outputs were NaN)"""
         flags = ctypes.c_uint32(0)
         err = QmoeErr()
