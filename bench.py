@@ -421,6 +421,71 @@ def bench_deltanet(pkg, torch, layers, steps, warmup):
     return sec
 
 
+AT_SHAPE = (2048, 16, 2, 128, 4, 128, 2048, 4)  # hidden, heads, kv heads, head dim, indexer heads,
+#                                                 indexer head dim, indexer budget, compress ratio
+AT_CONTEXT = 4096  # cached tokens before the timed steps: past the budget, so the block mask runs
+
+
+def at_token_bytes(shape, context):
+    """algorithmic HBM bytes of one token through one attention mixer at
+    `context` cached tokens with the block mask active: q4 q/k/v/o
+    projections (codes + bf16 scale/bias per 64), the bf16 indexer matrix,
+    every cached indexer key (pooled each step), the k and v rows of the
+    kept blocks (budget) and of the token's own tail, the cache rows
+    appended, x in and out"""
+    d, h, kvh, hd, ih, ihd, budget, comp = shape
+    q4 = lambda rows, cols: rows * cols // 2 + rows * (cols // 64) * 4
+    w = q4(2 * h * hd, d) + 2 * q4(kvh * hd, d) + q4(d, h * hd) + (ih + 1) * ihd * d * 2
+    kept = min(budget, context) + comp
+    return w + context * ihd * 4 + 2 * kept * kvh * hd * 4 + (2 * kvh * hd + ihd) * 4 + 2 * d * 4
+
+
+def bench_attention(pkg, torch, layers, steps, warmup, context=AT_CONTEXT):
+    """one f32 token per step through one full-attention mixer of AT_SHAPE
+    with its QSA indexer, layer i % layers, each layer's caches first filled
+    with `context` tokens; random q4/bf16 weights (numpy), the same host
+    arrays in every layer slot.  Returns seconds per token-layer."""
+    import numpy as np
+    d, h, kvh, hd, ih, ihd, budget, comp = AT_SHAPE
+    rng = np.random.default_rng(1)
+    bf = lambda n, std: ((rng.normal(0, std, n).astype(np.float32).view(np.uint32) + 0x8000) >> 16).astype(np.uint16)
+    codes = lambda n: rng.integers(0, 2**32, n, dtype=np.uint32)
+    q4 = lambda rows, cols: (codes(rows * cols // 8), bf(rows * cols // 64, 0.02), bf(rows * cols // 64, 0.01))
+    host = {}
+    for nm, (rows, cols) in (("q", (2 * h * hd, d)), ("k", (kvh * hd, d)), ("v", (kvh * hd, d)), ("o", (d, h * hd))):
+        host[nm + "_q"], host[nm + "_s"], host[nm + "_b"] = q4(rows, cols)
+    host["idx_w"] = bf((ih + 1) * ihd * d, 0.02)
+    for nm, n in (("q_norm", hd), ("k_norm", hd), ("idx_q_norm", ihd), ("idx_k_norm", ihd)):
+        host[nm] = (1 + rng.normal(0, 0.1, n)).astype(np.float32)
+    chunk = 256
+    cap = context + (warmup + steps) // layers + 2 * layers + chunk
+    ctx = pkg.AttentionContext(d, h, kvh, hd, ih, ihd, budget, comp, kv_cap=cap, n_layers=layers,
+                               max_tokens=chunk)
+    xs = torch.randn((chunk, d), device="cuda") * 0.5
+    for layer in range(layers):
+        ctx.upload_layer(layer, host)
+        for t0 in range(0, context, chunk):
+            ctx.forward(layer, xs, t0)
+    torch.cuda.synchronize()
+    pos = [context] * layers
+    X = 16
+    xt = [torch.randn((1, d), device="cuda") for _ in range(X)]
+    outs = [torch.empty((1, d), device="cuda") for _ in range(X)]
+
+    def run(first, count):
+        for i in range(first, first + count):
+            layer = i % layers
+            ctx.forward(layer, xt[i % X], pos[layer], out=outs[i % X])
+            pos[layer] += 1
+
+    run(0, warmup)
+    torch.cuda.synchronize()
+    g = capture(torch, lambda: run(warmup, steps), warm=False)
+    sec = time_graph(torch, g, 1) / steps
+    ctx.close()
+    return sec
+
+
 def bench_depth(pkg, torch, w, tokens, warmup):
     """48 stacked layers, one token: h <- h + MoE(RMSNorm(h)) layer after
     layer (f32 residual stream), captured as one graph per token; returns
@@ -630,6 +695,8 @@ def main():
                     help="comma list of other workloads to time (secondary results)")
     ap.add_argument("--deltanet", type=int, default=1,
                     help="also time the gated DeltaNet mixer at one token (0: skip)")
+    ap.add_argument("--attention", type=int, default=1,
+                    help=f"also time the full-attention mixer at one token, {AT_CONTEXT} cached (0: skip)")
     ap.add_argument("--hyper", default="decode,batched,prefill",
                     help="comma list of workloads also timed as hyper-connection layers "
                          f"(hc {HC_COUNT}, rank {HC_LOWRANK}; secondary results)")
@@ -735,6 +802,22 @@ def main():
                  "recurrence with HBM-resident states, gated norm + out_proj), layers rotated, "
                  "one HIP graph")
         log(f"deltanet: {s_d * 1e6:.2f} us/token-layer -> {b / s_d / 1e9:.0f} GB/s")
+        torch.cuda.empty_cache()
+    if args.attention:
+        nl = 16
+        s_a = bench_attention(pkg, torch, nl, 256, 32)
+        b = at_token_bytes(AT_SHAPE, AT_CONTEXT)
+        extra["attention"] = dict(
+            us_per_token=s_a * 1e6, tokens_per_s=1.0 / s_a, layers_rotated=nl, steps=256,
+            context=AT_CONTEXT, algorithmic_bytes_per_token=b,
+            hbm_fraction=round(b / s_a / 1e9 / HBM_PEAK_GBS, 4),
+            shape=dict(zip(("hidden", "heads", "kv_heads", "head_dim", "idx_heads", "idx_head_dim",
+                            "idx_budget", "idx_compress"), AT_SHAPE)),
+            note="one f32 token through one full-attention mixer (q4 projections, per-head norm + "
+                 "partial RoPE, indexer block selection, masked softmax over the cache, gate, "
+                 "o_proj) at 4096 cached tokens, layers rotated, one HIP graph")
+        log(f"attention: {s_a * 1e6:.2f} us/token-layer at {AT_CONTEXT} cached -> "
+            f"{b / s_a / 1e9:.0f} GB/s")
         torch.cuda.empty_cache()
     for name in [e for e in args.hyper.split(",") if e]:
         we = pkg.WORKLOADS[name]

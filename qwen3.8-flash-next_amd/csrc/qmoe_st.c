@@ -410,26 +410,26 @@ static int cmp_range(const void *a, const void *b) {
 static int parse_file(qmoe_st *ix, const char *path, int file, qmoe_err *err) {
     const int fd = open(path, O_RDONLY);
     if (fd < 0) {
-        st_err(err, "cannot open %s: %s", path, strerror(errno));
+        st_err(err, "%s: open failed (%s)", path, strerror(errno));
         return -1;
     }
     struct stat sb;
     if (fstat(fd, &sb) != 0) {
-        st_err(err, "cannot stat %s: %s", path, strerror(errno));
+        st_err(err, "%s: size query failed (%s)", path, strerror(errno));
         close(fd);
         return -1;
     }
     const uint64_t fsize = (uint64_t)sb.st_size;
     unsigned char lb[8];
     if (fsize < 8 || pread(fd, lb, 8, 0) != 8) {
-        st_err(err, "truncated safetensors header: %s", path);
+        st_err(err, "%s: shorter than the 8-byte header length field", path);
         close(fd);
         return -1;
     }
     uint64_t hlen = 0;
     for (int i = 7; i >= 0; i--) hlen = (hlen << 8) | lb[i];
     if (hlen > fsize - 8 || hlen > ST_MAX_HEADER) {
-        st_err(err, "truncated safetensors json: %s", path);
+        st_err(err, "%s: header length runs past the end of the file", path);
         close(fd);
         return -1;
     }
@@ -444,7 +444,7 @@ static int parse_file(qmoe_st *ix, const char *path, int file, qmoe_err *err) {
         const ssize_t r = pread(fd, hdr + got, (size_t)hlen - got, (off_t)(8 + got));
         if (r < 0 && errno == EINTR) continue;
         if (r <= 0) {
-            st_err(err, "truncated safetensors json: %s", path);
+            st_err(err, "%s: header length runs past the end of the file", path);
             free(hdr);
             close(fd);
             return -1;
@@ -464,8 +464,8 @@ static int parse_file(qmoe_st *ix, const char *path, int file, qmoe_err *err) {
     }
     free(hdr);
     if (!root || root->type != J_OBJ) {
-        st_err(err, "invalid safetensors json %s: %s", path,
-               root ? "header must be an object" : ps.msg);
+        st_err(err, "%s: header is not a JSON object (%s)", path,
+               root ? "top level is not an object" : ps.msg);
         jfree(root);
         close(fd);
         return -1;
@@ -483,7 +483,7 @@ static int parse_file(qmoe_st *ix, const char *path, int file, qmoe_err *err) {
         const jv *jd = jget(m, "dtype"), *jo = jget(m, "data_offsets"), *js = jget(m, "shape");
         if (!m || m->type != J_OBJ || !jd || jd->type != J_STR || !jo || jo->type != J_ARR ||
             jo->n != 2 || !js || js->type != J_ARR) {
-            st_err(err, "invalid safetensors metadata for %s", stored);
+            st_err(err, "%s: entry lacks dtype, shape or data_offsets", stored);
             failed = 1;
             break;
         }
@@ -491,19 +491,19 @@ static int parse_file(qmoe_st *ix, const char *path, int file, qmoe_err *err) {
         memset(&t, 0, sizeof(t));
         t.dtype = dtype_of(jd->str);
         if (t.dtype < 0) {
-            st_err(err, "unsupported safetensors dtype %s for %s", jd->str, stored);
+            st_err(err, "%s: element type %s is not supported", stored, jd->str);
             failed = 1;
             break;
         }
         const jv *lo = jo->items[0], *hi = jo->items[1];
         if (lo->type != J_NUM || !lo->is_int || hi->type != J_NUM || !hi->is_int || lo->inum < 0 ||
             hi->inum < 0) {
-            st_err(err, "invalid data offsets for %s", stored);
+            st_err(err, "%s: data_offsets must be two ordered non-negative integers", stored);
             failed = 1;
             break;
         }
         if (js->n > 8) {
-            st_err(err, "tensor %s has too many dims", stored);
+            st_err(err, "%s: more dimensions than the index keeps (8)", stored);
             failed = 1;
             break;
         }
@@ -521,13 +521,13 @@ static int parse_file(qmoe_st *ix, const char *path, int file, qmoe_err *err) {
             elems *= (uint64_t)sv->inum;
         }
         if (bad || elems > UINT64_MAX / 8) {
-            st_err(err, "invalid shape for %s", stored);
+            st_err(err, "%s: shape entries must be non-negative integers", stored);
             failed = 1;
             break;
         }
         const uint64_t l = (uint64_t)lo->inum, h = (uint64_t)hi->inum;
         if (h < l || h - l != elems * (uint64_t)DTYPES[t.dtype].size || h > fsize - base) {
-            st_err(err, "invalid safetensors range for %s", stored);
+            st_err(err, "%s: byte range disagrees with the shape or leaves the file", stored);
             failed = 1;
             break;
         }
@@ -555,7 +555,7 @@ static int parse_file(qmoe_st *ix, const char *path, int file, qmoe_err *err) {
         for (size_t i = 0; i < nr; i++) {
             if (rg[i].hi == rg[i].lo) continue;
             if (who && rg[i].lo < reach) {
-                st_err(err, "overlapping safetensors ranges for %s", rg[i].name);
+                st_err(err, "%s: data overlaps another tensor of the file", rg[i].name);
                 failed = 1;
                 break;
             }
@@ -615,7 +615,7 @@ int qmoe_st_open(qmoe_st **out, const char *dir, qmoe_err *err) {
     *out = NULL;
     DIR *d = opendir(dir);
     if (!d) {
-        st_err(err, "cannot open model dir %s: %s", dir, strerror(errno));
+        st_err(err, "%s: checkpoint directory cannot be listed (%s)", dir, strerror(errno));
         return -1;
     }
     /* file names, sorted so the index does not depend on directory order */
@@ -647,7 +647,7 @@ int qmoe_st_open(qmoe_st **out, const char *dir, qmoe_err *err) {
         goto done;
     }
     if (nf == 0) {
-        st_err(err, "no safetensors in %s", dir);
+        st_err(err, "%s: no .safetensors file in the directory", dir);
         goto done;
     }
     qsort(names, (size_t)nf, sizeof(char *), cmp_str);
@@ -670,7 +670,7 @@ int qmoe_st_open(qmoe_st **out, const char *dir, qmoe_err *err) {
     if (ix->n) qsort(ix->ent, ix->n, sizeof(st_entry), cmp_entry);
     for (size_t i = 1; i < ix->n; i++)
         if (!strcmp(ix->ent[i - 1].name, ix->ent[i].name)) {
-            st_err(err, "duplicate tensor %s", ix->ent[i].name);
+            st_err(err, "%s: tensor name given twice in the checkpoint", ix->ent[i].name);
             goto done;
         }
     *out = ix;
@@ -723,11 +723,11 @@ static int read_range(const qmoe_st *ix, const st_entry *e, uint64_t at, void *d
         const ssize_t r = pread(ix->fds[e->t.file], p + got, len - got, (off_t)(e->t.offset + at + got));
         if (r < 0 && errno == EINTR) continue;
         if (r < 0) {
-            st_err(err, "read failed for %s: %s", e->name, strerror(errno));
+            st_err(err, "%s: data read failed (%s)", e->name, strerror(errno));
             return -1;
         }
         if (r == 0) {
-            st_err(err, "short read for %s", e->name);
+            st_err(err, "%s: file ended inside the tensor data", e->name);
             return -1;
         }
         got += (size_t)r;

@@ -105,19 +105,19 @@ def _open_error(path):
 
 
 @pytest.mark.parametrize("case,needle", [
-    ("short", "truncated safetensors header"),
-    ("hlen_past_end", "truncated safetensors json"),
-    ("bad_json", "invalid safetensors json"),
-    ("trailing", "invalid safetensors json"),
-    ("not_object", "header must be an object"),
-    ("bad_dtype", "unsupported safetensors dtype F8_E4M3"),
-    ("no_offsets", "invalid safetensors metadata"),
-    ("float_offset", "invalid data offsets"),
-    ("range_vs_shape", "invalid safetensors range"),
-    ("past_end", "invalid safetensors range"),
-    ("neg_dim", "invalid shape"),
-    ("overlap", "overlapping safetensors ranges"),
-    ("dup_prefix", "duplicate tensor a"),
+    ("short", "shorter than the 8-byte header length field"),
+    ("hlen_past_end", "header length runs past the end of the file"),
+    ("bad_json", "header is not a JSON object"),
+    ("trailing", "trailing bytes after the header object"),
+    ("not_object", "top level is not an object"),
+    ("bad_dtype", "element type F8_E4M3 is not supported"),
+    ("no_offsets", "entry lacks dtype, shape or data_offsets"),
+    ("float_offset", "data_offsets must be two ordered non-negative integers"),
+    ("range_vs_shape", "byte range disagrees with the shape"),
+    ("past_end", "byte range disagrees with the shape or leaves the file"),
+    ("neg_dim", "shape entries must be non-negative integers"),
+    ("overlap", "data overlaps another tensor of the file"),
+    ("dup_prefix", "a: tensor name given twice"),
 ])
 def test_malformed_files_are_refused(tmp_path, case, needle):
     p = os.path.join(str(tmp_path), "m.safetensors")
@@ -157,11 +157,11 @@ def test_malformed_files_are_refused(tmp_path, case, needle):
 def test_duplicate_across_files_and_empty_dir(tmp_path):
     d16 = bytes(16)
     ok = {"dtype": "F32", "shape": [4], "data_offsets": [0, 16]}
-    assert "no safetensors in" in _open_error(str(tmp_path))
-    assert "cannot open model dir" in _open_error(os.path.join(str(tmp_path), "missing"))
+    assert "no .safetensors file in the directory" in _open_error(str(tmp_path))
+    assert "checkpoint directory cannot be listed" in _open_error(os.path.join(str(tmp_path), "missing"))
     write_raw(os.path.join(str(tmp_path), "a.safetensors"), {"model.x": ok}, d16)
     write_raw(os.path.join(str(tmp_path), "b.safetensors"), {"language_model.model.x": ok}, d16)
-    assert "duplicate tensor model.x" in _open_error(str(tmp_path))
+    assert "model.x: tensor name given twice" in _open_error(str(tmp_path))
 
 
 def test_read_errors(tmp_path):
