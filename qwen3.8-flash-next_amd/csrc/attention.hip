@@ -11,15 +11,22 @@
  *             the indexer's q norm, then partial RoPE at position offset+t
  *             (kernel.c:80-93); k, v and the indexer's raw key go into their
  *             caches at rows len0 + t.
- *   k_at_sel  (past the indexer budget) one workgroup per token: every
- *             key block's mean-pooled indexer key, rmsnorm + RoPE at the
- *             block start, score sum_heads sum_i relu(q_i p_i) / sqrt(ihd),
- *             invisible blocks -inf; the top budget/compress blocks (value
+ *   k_at_pool one wave per key block completed by the call: the block's
+ *             mean-pooled indexer key, rmsnorm + RoPE at the block start,
+ *             kept in HBM with the layer (a pooled key depends only on its
+ *             block's cached keys, so the reference's per-call recomputation
+ *             gives the same values).
+ *   k_at_score (past the indexer budget) one wave per (token, block): score
+ *             sum_heads sum_i relu(q_i p_i) / sqrt(ihd), invisible blocks
+ *             -inf, as order keys.
+ *   k_at_sel  one workgroup per token: the top budget/compress blocks (value
  *             descending, ties to the lower block) by an 8-bit radix select
  *             -> a bitmap of kept blocks.
- *   k_at_attn one workgroup per (token, head, 256 keys): scores q.k/sqrt(hd)
- *             (kv head = head % kv_heads), the causal mask kk > offset + t and
- *             the block mask, chunk max, sum of exp and exp-weighted v.
+ *   k_at_attn one workgroup per (token, kv head, 256 keys) for up to 8 of the
+ *             query heads that read that kv head: each k and v row is loaded
+ *             once for all of them; scores q.k/sqrt(hd), the causal mask
+ *             kk > offset + t and the block mask, chunk max, sum of exp and
+ *             exp-weighted v per head.
  *   k_at_comb one wave per (token, head): the chunks merged (max, rescaled
  *             sums), times sigmoid(gate).
  * Sums run in parallel orders: outputs match the reference to rounding.
@@ -211,53 +218,83 @@ __global__ __launch_bounds__(64) void k_at_qk(AtQkArgs a) {
 
 #define AT_SEL_T 256
 
-struct AtSelArgs {
+struct AtPoolArgs {
     const float *idx_keys;  /* [cap, ihd] */
     const float *ik_norm;   /* [ihd] */
-    const float *qi;        /* [n, ih, ihd] */
-    uint32_t *keep;         /* [n, kw] */
-    int ih, ihd, comp, nb, btop, offset, rot, kw;
+    float *pooled;          /* [cap/comp, ihd] */
+    int ihd, comp, b0, b1, rot;
     float theta;
+};
+
+/* one wave per block b in [b0, b1): mean of its comp keys, then rmsnorm +
+ * RoPE at the block start (model.c:969-1000) */
+__global__ __launch_bounds__(256) void k_at_pool(AtPoolArgs a) {
+    __shared__ float s_p[4][256];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int b = a.b0 + (int)blockIdx.x * 4 + wave;
+    if (b >= a.b1) return; /* the whole wave; nothing below synchronises the workgroup */
+    float *pw = s_p[wave];
+    for (int i = lane; i < a.ihd; i += 64) {
+        float acc = 0.0f;
+        for (int j = 0; j < a.comp; j++) acc = acc + qk_ld(a.idx_keys + ((size_t)b * a.comp + j) * a.ihd + i);
+        pw[i] = acc / (float)a.comp;
+    }
+    qk_wave_lds_sync();
+    at_norm_rope(pw, a.ik_norm, a.ihd, a.rot, a.theta, b * a.comp, a.pooled + (size_t)b * a.ihd, lane);
+}
+
+struct AtScoreArgs {
+    const float *pooled;    /* [nb, ihd] */
+    const float *qi;        /* [n, ih, ihd] */
+    uint32_t *skey;         /* [n, ldk] order keys of the block scores */
+    int ih, ihd, comp, nb, ldk, offset;
+};
+
+/* grid (n, ceil(nb/4)): one wave per (token, block) */
+__global__ __launch_bounds__(256) void k_at_score(AtScoreArgs a) {
+    extern __shared__ float at_lds[]; /* [ih * ihd] the token's indexer queries */
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, t = blockIdx.x;
+    for (int i = tid; i < a.ih * a.ihd; i += 256) at_lds[i] = qk_ld(a.qi + (size_t)t * a.ih * a.ihd + i);
+    __syncthreads();
+    const int b = (int)blockIdx.y * 4 + wave;
+    if (b >= a.nb) return;
+    const float *pb = a.pooled + (size_t)b * a.ihd;
+    float pv[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) pv[e] = lane + 64 * e < a.ihd ? qk_ld(pb + lane + 64 * e) : 0.0f;
+    float sc = 0.0f;
+    for (int hh = 0; hh < a.ih; hh++) {
+        float dot = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int i = lane + 64 * e;
+            if (i < a.ihd) {
+                const float v = at_lds[hh * a.ihd + i] * pv[e];
+                dot = dot + (v > 0.0f ? v : 0.0f);
+            }
+        }
+        sc = sc + qk_group_sum<64>(dot);
+    }
+    float score = sc * (1.0f / sqrtf((float)a.ihd));
+    if ((long long)b * a.comp + a.comp - 1 > (long long)(a.offset + t)) score = -INFINITY;
+    if (lane == 0) a.skey[(size_t)t * a.ldk + b] = qk_ordkey(score);
+}
+
+struct AtSelArgs {
+    const uint32_t *skey;   /* [n, ldk] */
+    uint32_t *keep;         /* [n, kw] */
+    int nb, btop, kw, ldk;
 };
 
 __global__ __launch_bounds__(AT_SEL_T) void k_at_sel(AtSelArgs a) {
     extern __shared__ float at_lds[];
-    float *s_q = at_lds;                               /* [ih * ihd] */
-    float *s_p = s_q + a.ih * a.ihd;                   /* [4][ihd] per-wave pooled key */
-    uint32_t *s_key = (uint32_t *)(s_p + 4 * a.ihd);   /* [nb] order keys of the scores */
+    uint32_t *s_key = (uint32_t *)at_lds;              /* [nb] order keys of the scores */
     uint32_t *s_bits = s_key + a.nb;                   /* [kw] */
     int *s_hist = (int *)(s_bits + a.kw);              /* [256] */
     int *s_misc = s_hist + 256;                        /* [8] */
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, t = blockIdx.x;
-    const int qpos = a.offset + t;
-    for (int i = tid; i < a.ih * a.ihd; i += AT_SEL_T) s_q[i] = qk_ld(a.qi + (size_t)t * a.ih * a.ihd + i);
     for (int i = tid; i < a.kw; i += AT_SEL_T) s_bits[i] = 0u;
-    __syncthreads();
-    float *pw = s_p + wave * a.ihd;
-    const float inv_sqrt = 1.0f / sqrtf((float)a.ihd);
-    for (int b = wave; b < a.nb; b += 4) {
-        for (int i = lane; i < a.ihd; i += 64) {
-            float acc = 0.0f;
-            for (int j = 0; j < a.comp; j++) acc = acc + qk_ld(a.idx_keys + ((size_t)b * a.comp + j) * a.ihd + i);
-            pw[i] = acc / (float)a.comp;
-        }
-        qk_wave_lds_sync();
-        at_norm_rope(pw, a.ik_norm, a.ihd, a.rot, a.theta, b * a.comp, pw, lane);
-        qk_wave_lds_sync();
-        float sc = 0.0f;
-        for (int hh = 0; hh < a.ih; hh++) {
-            float dot = 0.0f;
-            for (int i = lane; i < a.ihd; i += 64) {
-                const float v = s_q[hh * a.ihd + i] * pw[i];
-                dot = dot + (v > 0.0f ? v : 0.0f);
-            }
-            sc = sc + qk_group_sum<64>(dot);
-        }
-        float score = sc * inv_sqrt;
-        if ((long long)b * a.comp + a.comp - 1 > (long long)qpos) score = -INFINITY;
-        if (lane == 0) s_key[b] = qk_ordkey(score);
-        qk_wave_lds_sync();
-    }
+    for (int b = tid; b < a.nb; b += AT_SEL_T) s_key[b] = qk_ld(a.skey + (size_t)t * a.ldk + b);
     __syncthreads();
     if (a.btop >= a.nb) {
         for (int b = tid; b < a.nb; b += AT_SEL_T) atomicOr(&s_bits[b >> 5], 1u << (b & 31));
@@ -273,14 +310,31 @@ __global__ __launch_bounds__(AT_SEL_T) void k_at_sel(AtSelArgs a) {
                 if ((k & pmask) == prefix) atomicAdd(&s_hist[(k >> shift) & 255], 1);
             }
             __syncthreads();
-            if (tid == 0) {
-                int cum = 0, dg = 0;
-                for (dg = 255; dg > 0; dg--) {
-                    if (cum + s_hist[dg] >= need) break;
-                    cum += s_hist[dg];
+            if (wave == 0) {
+                /* the digit where the count from the top first reaches
+                 * need: lane l holds digits 255-4l .. 252-4l, an exclusive
+                 * scan over the lanes, then the lane holding the crossing */
+                int cnt[4], sum = 0;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    cnt[i] = s_hist[255 - 4 * lane - i];
+                    sum += cnt[i];
                 }
-                s_misc[0] = dg;
-                s_misc[1] = need - cum;
+                int inc = sum;
+                for (int o = 1; o < 64; o <<= 1) {
+                    const int u = __shfl_up(inc, o, QK_WAVE);
+                    if (lane >= o) inc += u;
+                }
+                const int before = inc - sum;
+                if (before < need && inc >= need) {
+                    int cum = before, i = 0;
+                    while (i < 3 && cum + cnt[i] < need) cum += cnt[i++];
+                    s_misc[0] = 255 - 4 * lane - i;
+                    s_misc[1] = need - cum;
+                } else if (lane == 63 && inc < need) { /* fewer keys than need: digit 0 */
+                    s_misc[0] = 0;
+                    s_misc[1] = need - (inc - cnt[3]);
+                }
             }
             __syncthreads();
             prefix |= (uint32_t)s_misc[0] << shift;
@@ -332,77 +386,126 @@ struct AtAttnArgs {
     int h, kvh, hd, kv_total, offset, comp, nb, kw, nchunks;
 };
 
+#define AT_GMAX 8 /* query heads of one kv head per workgroup, at most */
+
+/* grid (n * kvh * ngrp, nchunks): workgroup = (token t, kv head kh, group
+ * of up to AT_GMAX of the heads kh, kh + kvh, ...) over 256 keys; thread
+ * tid owns key c*256 + tid for the scores, wave w the keys w, w+4, .. for
+ * the v sums.  Per head the arithmetic (fma chain of q.k in dimension
+ * order, chunk max, exp, wave tree, the v sums per wave, the waves added in
+ * order) is that of one head alone. */
 __global__ __launch_bounds__(AT_CHUNK) void k_at_attn(AtAttnArgs a) {
-    __shared__ float s_q[256];
-    __shared__ float s_p[AT_CHUNK];
-    __shared__ float s_red[4 * 256];
+    __shared__ float s_q[AT_GMAX][256];
+    __shared__ float s_p[AT_GMAX][AT_CHUNK];
+    __shared__ float s_red[4][AT_GMAX][256];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int t = blockIdx.x / a.h, hh = blockIdx.x - t * a.h, c = blockIdx.y;
-    const int kh = hh % a.kvh, qpos = a.offset + t;
+    const int G = a.h / a.kvh, ngrp = (G + AT_GMAX - 1) / AT_GMAX;
+    const int t = blockIdx.x / (a.kvh * ngrp);
+    const int r = blockIdx.x - t * a.kvh * ngrp, kh = r / ngrp, grp = r - kh * ngrp;
+    const int j0 = grp * AT_GMAX, ng = min(AT_GMAX, G - j0);
+    const int c = blockIdx.y, qpos = a.offset + t;
     const size_t kvw = (size_t)a.kvh * a.hd;
-    for (int i = tid; i < a.hd; i += AT_CHUNK) s_q[i] = qk_ld(a.qn + ((size_t)t * a.h + hh) * a.hd + i);
+    for (int i = tid; i < AT_GMAX * a.hd; i += AT_CHUNK) {
+        const int g = i / a.hd, d = i - g * a.hd;
+        s_q[g][d] = g < ng ? qk_ld(a.qn + ((size_t)t * a.h + kh + (size_t)a.kvh * (j0 + g)) * a.hd + d) : 0.0f;
+    }
     __syncthreads();
     const int kk = c * AT_CHUNK + tid;
-    float sc = -INFINITY;
-    if (kk < a.kv_total) {
-        const float4 *kr = (const float4 *)(a.k_cache + (size_t)kk * kvw + (size_t)kh * a.hd);
-        float acc = 0.0f;
-        for (int i = 0; i < a.hd / 4; i++) {
-            const float4 k4 = qk_ld(kr + i);
-            acc = fmaf(s_q[4 * i], k4.x, acc);
-            acc = fmaf(s_q[4 * i + 1], k4.y, acc);
-            acc = fmaf(s_q[4 * i + 2], k4.z, acc);
-            acc = fmaf(s_q[4 * i + 3], k4.w, acc);
+    bool live = kk < a.kv_total && kk <= qpos;
+    if (live && a.keep) {
+        const int blk = kk / a.comp;
+        bool kp = blk < a.nb && ((qk_ld(a.keep + (size_t)t * a.kw + (blk >> 5)) >> (blk & 31)) & 1u);
+        const long long own = ((long long)(qpos + 1) / a.comp) * a.comp;
+        if (kk >= own) kp = true;
+        live = kp;
+    }
+    float sc[AT_GMAX];
+    {
+        float acc[AT_GMAX];
+#pragma unroll
+        for (int g = 0; g < AT_GMAX; g++) acc[g] = 0.0f;
+        if (kk < a.kv_total) {
+            const float4 *kr = (const float4 *)(a.k_cache + (size_t)kk * kvw + (size_t)kh * a.hd);
+#pragma unroll 4
+            for (int i = 0; i < a.hd / 4; i++) {
+                const float4 k4 = qk_ld(kr + i);
+#pragma unroll
+                for (int g = 0; g < AT_GMAX; g++) {
+                    acc[g] = fmaf(s_q[g][4 * i], k4.x, acc[g]);
+                    acc[g] = fmaf(s_q[g][4 * i + 1], k4.y, acc[g]);
+                    acc[g] = fmaf(s_q[g][4 * i + 2], k4.z, acc[g]);
+                    acc[g] = fmaf(s_q[g][4 * i + 3], k4.w, acc[g]);
+                }
+            }
         }
-        sc = acc * (1.0f / sqrtf((float)a.hd));
-        if (kk > qpos) sc = -INFINITY;
-        if (a.keep) {
-            const int blk = kk / a.comp;
-            bool kp = blk < a.nb && ((qk_ld(a.keep + (size_t)t * a.kw + (blk >> 5)) >> (blk & 31)) & 1u);
-            const long long own = ((long long)(qpos + 1) / a.comp) * a.comp;
-            if (kk >= own && kk <= qpos) kp = true;
-            if (!kp && kk <= qpos) sc = -INFINITY;
+#pragma unroll
+        for (int g = 0; g < AT_GMAX; g++) sc[g] = live ? acc[g] * (1.0f / sqrtf((float)a.hd)) : -INFINITY;
+    }
+    /* per head: chunk max, exp, sum */
+    float mg[AT_GMAX], lg[AT_GMAX];
+#pragma unroll
+    for (int g = 0; g < AT_GMAX; g++) {
+        float m = sc[g];
+        m = fmaxf(m, qk_dpp<QK_DPP_XOR1>(m));
+        m = fmaxf(m, qk_dpp<QK_DPP_XOR2>(m));
+        m = fmaxf(m, qk_dpp<QK_DPP_HALF_MIRROR>(m));
+        m = fmaxf(m, qk_dpp<QK_DPP_MIRROR>(m));
+        m = fmaxf(m, __uint_as_float(qk_xor16_u(__float_as_uint(m))));
+        m = fmaxf(m, __uint_as_float(qk_xor32_u(__float_as_uint(m))));
+        if (lane == 0) s_red[wave][g][0] = m;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < AT_GMAX; g++) {
+        const float m = fmaxf(fmaxf(s_red[0][g][0], s_red[1][g][0]), fmaxf(s_red[2][g][0], s_red[3][g][0]));
+        const float p = m == -INFINITY ? 0.0f : expf(sc[g] - m);
+        s_p[g][tid] = p;
+        mg[g] = m;
+        lg[g] = qk_group_sum<64>(p);
+    }
+    __syncthreads(); /* s_red reused */
+#pragma unroll
+    for (int g = 0; g < AT_GMAX; g++)
+        if (lane == 0) s_red[wave][g][1] = lg[g];
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < AT_GMAX; g++) lg[g] = ((s_red[0][g][1] + s_red[1][g][1]) + s_red[2][g][1]) + s_red[3][g][1];
+    /* exp-weighted v: wave w takes the keys w, w+4, ...; lane the dims lane, lane+64, .. */
+    float o[AT_GMAX][4];
+#pragma unroll
+    for (int g = 0; g < AT_GMAX; g++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) o[g][e] = 0.0f;
+    const int nk = min(AT_CHUNK, a.kv_total - c * AT_CHUNK);
+#pragma unroll 8
+    for (int j = wave; j < nk; j += 4) {
+        const float *vr = a.v_cache + (size_t)(c * AT_CHUNK + j) * kvw + (size_t)kh * a.hd;
+        float vv[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) vv[e] = lane + 64 * e < a.hd ? qk_ld(vr + lane + 64 * e) : 0.0f;
+#pragma unroll
+        for (int g = 0; g < AT_GMAX; g++) {
+            const float pj = s_p[g][j];
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[g][e] = fmaf(pj, vv[e], o[g][e]);
         }
     }
-    /* chunk max */
-    float m = sc;
-    m = fmaxf(m, qk_dpp<QK_DPP_XOR1>(m));
-    m = fmaxf(m, qk_dpp<QK_DPP_XOR2>(m));
-    m = fmaxf(m, qk_dpp<QK_DPP_HALF_MIRROR>(m));
-    m = fmaxf(m, qk_dpp<QK_DPP_MIRROR>(m));
-    m = fmaxf(m, __uint_as_float(qk_xor16_u(__float_as_uint(m))));
-    m = fmaxf(m, __uint_as_float(qk_xor32_u(__float_as_uint(m))));
-    if (lane == 0) s_red[wave] = m;
     __syncthreads();
-    m = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-    const float p = m == -INFINITY ? 0.0f : expf(sc - m);
-    s_p[tid] = p;
-    float l = qk_group_sum<64>(p);
-    __syncthreads(); /* s_red reused */
-    if (lane == 0) s_red[wave] = l;
-    __syncthreads();
-    l = ((s_red[0] + s_red[1]) + s_red[2]) + s_red[3];
-    /* exp-weighted v: wave w takes the keys w, w+4, ...; lane the dims lane, lane+64, .. */
-    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const int nk = min(AT_CHUNK, a.kv_total - c * AT_CHUNK);
-    for (int j = wave; j < nk; j += 4) {
-        const float pj = s_p[j];
-        const float *vr = a.v_cache + (size_t)(c * AT_CHUNK + j) * kvw + (size_t)kh * a.hd;
+#pragma unroll
+    for (int g = 0; g < AT_GMAX; g++)
 #pragma unroll
         for (int e = 0; e < 4; e++)
-            if (lane + 64 * e < a.hd) o[e] = fmaf(pj, qk_ld(vr + lane + 64 * e), o[e]);
-    }
+            if (lane + 64 * e < a.hd) s_red[wave][g][lane + 64 * e] = o[g][e];
     __syncthreads();
-#pragma unroll
-    for (int e = 0; e < 4; e++)
-        if (lane + 64 * e < a.hd) s_red[wave * 256 + lane + 64 * e] = o[e];
-    __syncthreads();
-    float *dst = a.part + (((size_t)t * a.h + hh) * a.nchunks + c) * (a.hd + 2);
-    for (int i = tid; i < a.hd; i += AT_CHUNK)
-        dst[2 + i] = ((s_red[i] + s_red[256 + i]) + s_red[512 + i]) + s_red[768 + i];
-    if (tid == 0) {
-        dst[0] = m;
-        dst[1] = l;
+    for (int g = 0; g < ng; g++) {
+        const int hh = kh + a.kvh * (j0 + g);
+        float *dst = a.part + (((size_t)t * a.h + hh) * a.nchunks + c) * (a.hd + 2);
+        for (int i = tid; i < a.hd; i += AT_CHUNK)
+            dst[2 + i] = ((s_red[0][g][i] + s_red[1][g][i]) + s_red[2][g][i]) + s_red[3][g][i];
+        if (tid == 0) {
+            dst[0] = mg[g];
+            dst[1] = lg[g];
+        }
     }
 }
 
@@ -413,23 +516,44 @@ struct AtCombArgs {
     int h, hd, nchunks;
 };
 
+#define AT_MAXCH 32 /* chunks of 256 keys: kv_cap <= 8192 */
+
+/* one wave per (token, head); lane c holds chunk c's max and sum, every
+ * chunk's partial v sums for the lane's dims are loaded at once; the sums
+ * run over the chunks in order, a chunk with every key masked (max -inf,
+ * sums 0) entering with factor exp(-inf) = 0, which leaves them unchanged */
 __global__ __launch_bounds__(64) void k_at_comb(AtCombArgs a) {
     const int lane = threadIdx.x, th = blockIdx.x;
     const int t = th / a.h, hh = th - t * a.h;
-    const float *pp = a.part + (size_t)th * a.nchunks * (a.hd + 2);
-    float M = -INFINITY;
-    for (int c = 0; c < a.nchunks; c++) M = fmaxf(M, qk_ld(pp + (size_t)c * (a.hd + 2)));
-    float L = 0.0f;
-    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int c = 0; c < a.nchunks; c++) {
-        const float *q = pp + (size_t)c * (a.hd + 2);
-        const float mc = qk_ld(q);
-        if (mc == -INFINITY) continue;
-        const float f = expf(mc - M);
-        L = fmaf(qk_ld(q + 1), f, L);
+    const size_t cw = (size_t)a.hd + 2;
+    const float *pp = a.part + (size_t)th * a.nchunks * cw;
+    const bool cl = lane < a.nchunks;
+    const float mc = cl ? qk_ld(pp + (size_t)lane * cw) : -INFINITY;
+    const float lc = cl ? qk_ld(pp + (size_t)lane * cw + 1) : 0.0f;
+    float v[AT_MAXCH][4];
+#pragma unroll
+    for (int c = 0; c < AT_MAXCH; c++)
 #pragma unroll
         for (int e = 0; e < 4; e++)
-            if (lane + 64 * e < a.hd) o[e] = fmaf(qk_ld(q + 2 + lane + 64 * e), f, o[e]);
+            v[c][e] = (c < a.nchunks && lane + 64 * e < a.hd) ? qk_ld(pp + (size_t)c * cw + 2 + lane + 64 * e) : 0.0f;
+    float M = mc;
+    M = fmaxf(M, qk_dpp<QK_DPP_XOR1>(M));
+    M = fmaxf(M, qk_dpp<QK_DPP_XOR2>(M));
+    M = fmaxf(M, qk_dpp<QK_DPP_HALF_MIRROR>(M));
+    M = fmaxf(M, qk_dpp<QK_DPP_MIRROR>(M));
+    M = fmaxf(M, __uint_as_float(qk_xor16_u(__float_as_uint(M))));
+    M = fmaxf(M, __uint_as_float(qk_xor32_u(__float_as_uint(M))));
+    const float fc = expf(mc - M);
+    float L = 0.0f;
+    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < AT_MAXCH; c++) {
+        if (c < a.nchunks) {
+            const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fc), c));
+            L = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(lc), c)), f, L);
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = fmaf(v[c][e], f, o[e]);
+        }
     }
     const float inv = 1.0f / L;
     const float *g = a.qg + (size_t)t * 2 * a.h * a.hd + (size_t)hh * 2 * a.hd + a.hd;
@@ -475,12 +599,13 @@ extern "C" int qk_at_shape_ok(const qk_at_shape *s) {
 
 extern "C" size_t qk_at_sel_lds(const qk_at_shape *s, int nb) {
     const int kw = (nb + 31) / 32;
-    return ((size_t)s->ih * s->ihd + 4 * (size_t)s->ihd + (size_t)nb + kw + 256 + 8) * 4;
+    (void)s;
+    return ((size_t)nb + kw + 256 + 8) * 4;
 }
 
 extern "C" int qk_launch_at(const qk_at_shape *s, const qk_at_dev *W, const float *x, int n, int offset,
                             int len0, float *out, float *k_cache, float *v_cache, float *idx_keys,
-                            const qk_at_scratch *sc, void *stream) {
+                            float *pooled, const qk_at_scratch *sc, void *stream) {
     if (n <= 0) return 0;
     if (!qk_at_shape_ok(s)) return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)stream;
@@ -512,13 +637,30 @@ extern "C" int qk_launch_at(const qk_at_shape *s, const qk_at_dev *W, const floa
     rc = QK_CHECK_LAUNCH();
     if (rc) return rc;
 
+    /* the pooled keys of the blocks this call completes, whether or not
+     * the block mask runs yet */
+    const int pb0 = len0 / s->comp, pb1 = kv_total / s->comp;
+    if (pb1 > pb0) {
+        AtPoolArgs pa;
+        pa.idx_keys = idx_keys; pa.ik_norm = W->idx_k_norm; pa.pooled = pooled;
+        pa.ihd = ihd; pa.comp = s->comp; pa.b0 = pb0; pa.b1 = pb1; pa.rot = s->rot; pa.theta = s->theta;
+        hipLaunchKernelGGL(k_at_pool, dim3((pb1 - pb0 + 3) / 4), dim3(256), 0, st, pa);
+        rc = QK_CHECK_LAUNCH();
+        if (rc) return rc;
+    }
     const int nb = use_idx ? kv_total / s->comp : 0;
     const int kw = (nb + 31) / 32;
+    const int ldk = s->cap / s->comp;
     if (use_idx && nb > 0) {
+        AtScoreArgs ka;
+        ka.pooled = pooled; ka.qi = sc->qi; ka.skey = sc->skey;
+        ka.ih = ih; ka.ihd = ihd; ka.comp = s->comp; ka.nb = nb; ka.ldk = ldk; ka.offset = offset;
+        hipLaunchKernelGGL(k_at_score, dim3(n, (nb + 3) / 4), dim3(256), (size_t)ih * ihd * 4, st, ka);
+        rc = QK_CHECK_LAUNCH();
+        if (rc) return rc;
         AtSelArgs e;
-        e.idx_keys = idx_keys; e.ik_norm = W->idx_k_norm; e.qi = sc->qi; e.keep = sc->keep;
-        e.ih = ih; e.ihd = ihd; e.comp = s->comp; e.nb = nb; e.btop = s->budget / s->comp;
-        e.offset = offset; e.rot = s->rot; e.kw = kw; e.theta = s->theta;
+        e.skey = sc->skey; e.keep = sc->keep;
+        e.nb = nb; e.btop = s->budget / s->comp; e.kw = kw; e.ldk = ldk;
         hipLaunchKernelGGL(k_at_sel, dim3(n), dim3(AT_SEL_T), qk_at_sel_lds(s, nb), st, e);
         rc = QK_CHECK_LAUNCH();
         if (rc) return rc;
@@ -531,7 +673,8 @@ extern "C" int qk_launch_at(const qk_at_shape *s, const qk_at_dev *W, const floa
     at.h = h; at.kvh = kvh; at.hd = hd; at.kv_total = kv_total; at.offset = offset;
     at.comp = s->comp; at.nb = nb; at.kw = kw;
     at.nchunks = (kv_total + AT_CHUNK - 1) / AT_CHUNK;
-    hipLaunchKernelGGL(k_at_attn, dim3(n * h, at.nchunks), dim3(AT_CHUNK), 0, st, at);
+    const int ngrp = (h / kvh + AT_GMAX - 1) / AT_GMAX;
+    hipLaunchKernelGGL(k_at_attn, dim3(n * kvh * ngrp, at.nchunks), dim3(AT_CHUNK), 0, st, at);
     rc = QK_CHECK_LAUNCH();
     if (rc) return rc;
 

@@ -18,7 +18,7 @@
 
 enum { AT_Q_Q, AT_Q_S, AT_Q_B, AT_K_Q, AT_K_S, AT_K_B, AT_V_Q, AT_V_S, AT_V_B, AT_O_Q, AT_O_S, AT_O_B,
        AT_IDX_W, AT_Q_NORM, AT_K_NORM, AT_IQ_NORM, AT_IK_NORM, AT_K_CACHE, AT_V_CACHE, AT_IDX_KEYS,
-       AT_COUNT };
+       AT_POOLED, AT_COUNT };
 
 typedef struct {
     void *mem;
@@ -92,7 +92,7 @@ int qmoe_attn_create(qmoe_attn_ctx **out, const qmoe_attn_config *cfg, qmoe_err 
         kr * d / 2, kr * (d / 64) * 2, kr * (d / 64) * 2,
         orow * ok / 2, orow * (ok / 64) * 2, orow * (ok / 64) * 2,
         (ih + 1) * ihd * d * 2, hd * 4, hd * 4, ihd * 4, ihd * 4,
-        cap * kr * 4, cap * kr * 4, cap * ihd * 4};
+        cap * kr * 4, cap * kr * 4, cap * ihd * 4, cap / (size_t)s.comp * ihd * 4};
     size_t total = 0;
     for (int i = 0; i < AT_COUNT; i++) {
         c->off[i] = total;
@@ -101,10 +101,11 @@ int qmoe_attn_create(qmoe_attn_ctx **out, const qmoe_attn_config *cfg, qmoe_err 
     }
     const size_t n = (size_t)cfg->max_tokens;
     const size_t nchunks = (cap + 255) / 256, kw = (cap / (size_t)s.comp + 31) / 32 + 1;
-    const size_t ssz[9] = {n * qr * 4, n * kr * 4, n * kr * 4, n * (ih + 1) * ihd * 4, n * h * hd * 4,
-                           n * ih * ihd * 4, n * kw * 4, n * h * nchunks * (hd + 2) * 4, n * h * hd * 4};
-    size_t stot = 0, soff[9];
-    for (int i = 0; i < 9; i++) {
+    const size_t ssz[10] = {n * qr * 4, n * kr * 4, n * kr * 4, n * (ih + 1) * ihd * 4, n * h * hd * 4,
+                            n * ih * ihd * 4, n * kw * 4, n * h * nchunks * (hd + 2) * 4, n * h * hd * 4,
+                            n * (cap / (size_t)s.comp) * 4};
+    size_t stot = 0, soff[10];
+    for (int i = 0; i < 10; i++) {
         soff[i] = stot;
         stot = at_align(stot + ssz[i]);
     }
@@ -124,6 +125,7 @@ int qmoe_attn_create(qmoe_attn_ctx **out, const qmoe_attn_config *cfg, qmoe_err 
     c->sc.keep = (uint32_t *)(b + soff[6]);
     c->sc.part = (float *)(b + soff[7]);
     c->sc.ao = (float *)(b + soff[8]);
+    c->sc.skey = (uint32_t *)(b + soff[9]);
     for (int l = 0; l < cfg->n_layers; l++)
         if (at_hip_fail(err, (int)hipMalloc(&c->layers[l].mem, total), "layer weights")) {
             qmoe_attn_destroy(c);
@@ -246,7 +248,7 @@ int qmoe_attn_forward(qmoe_attn_ctx *c, int layer, const float *x, int n, int of
     W.idx_k_norm = (const float *)at_ptr(c, layer, AT_IK_NORM);
     const int rc = qk_launch_at(&c->shape, &W, x, n, offset, len0, out, (float *)at_ptr(c, layer, AT_K_CACHE),
                                 (float *)at_ptr(c, layer, AT_V_CACHE), (float *)at_ptr(c, layer, AT_IDX_KEYS),
-                                &c->sc, stream);
+                                (float *)at_ptr(c, layer, AT_POOLED), &c->sc, stream);
     if (at_hip_fail(err, rc, "attention launch")) return -1;
     c->layers[layer].len = len0 + n;
     return 0;

@@ -231,14 +231,17 @@ typedef struct {
     uint32_t *keep; /* [n, ceil(cap/comp/32)] */
     float *part;  /* [n, h, ceil(cap/256), hd+2] */
     float *ao;    /* [n, h*hd] */
+    uint32_t *skey; /* [n, cap/comp] order keys of the block scores */
 } qk_at_scratch;
 int qk_at_shape_ok(const qk_at_shape *s);
 size_t qk_at_sel_lds(const qk_at_shape *s, int nb);
 /* x [n, d] f32 at positions offset.. -> out [n, d]; the caches hold len0
- * rows before the call and len0 + n after it (len0 + n <= cap) */
+ * rows before the call and len0 + n after it (len0 + n <= cap); pooled
+ * [cap/comp, ihd] holds the pooled, normed and rotated indexer key of every
+ * complete block, len0/comp of them before the call */
 int qk_launch_at(const qk_at_shape *s, const qk_at_dev *W, const float *x, int n, int offset, int len0,
-                 float *out, float *k_cache, float *v_cache, float *idx_keys, const qk_at_scratch *sc,
-                 void *stream);
+                 float *out, float *k_cache, float *v_cache, float *idx_keys, float *pooled,
+                 const qk_at_scratch *sc, void *stream);
 
 /* the MLP hyper connection (hyper.hip): shapes it takes (hc <= 8, d and R
  * multiples of 64, d <= 2048, R <= 2048) */
