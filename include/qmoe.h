@@ -533,8 +533,8 @@ int qmoe_dn_state(qmoe_dn_ctx *ctx, int layer, float **conv_state, float **rec_s
  *   softmax, weighted sum of v, * sigmoid(gate), o_proj   (model.c:1107-1143)
  * The caches live in HBM with the layer, kv_cap rows; a call that would pass
  * kv_cap is refused (the reference drops the oldest rows of its v and
- * indexer caches there but not of its k cache, model.c:815-821, 863-867,
- * 935-936; that is not reproduced).  Block selection ties go to the lower
+ * indexer caches there but not of its k cache, model.c:815-821, 862-867,
+ * 921; that is not reproduced).  Block selection ties go to the lower
  * block (the reference's quickselect leaves their order open).  Sums run
  * in parallel orders: outputs agree with the reference to rounding.
  * Weights use the checkpoint layout (names model.c:1833-1850). */

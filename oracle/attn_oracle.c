@@ -53,8 +53,8 @@ int orc_attn_forward(const orc_attn *A, orc_attn_state *S, const float *x, int n
     const int idx_out = ih * ihd, qkw = idx_out + ihd;
     if (n <= 0) return 0;
     /* past the capacity the reference drops the oldest rows of the v and
-     * indexer caches but not of the k cache (model.c:815-821, 863-867,
-     * 935-936); only calls that fit are restated */
+     * indexer caches but not of the k cache (model.c:815-821, 862-867,
+     * 921); only calls that fit are restated */
     if (S->kv_len + n > cap || S->idx_len + n > cap) return -2;
     float *qk = (float *)malloc((size_t)n * qkw * sizeof(float));
     float *qbuf = (float *)malloc((size_t)n * h * hd * 2 * sizeof(float));
