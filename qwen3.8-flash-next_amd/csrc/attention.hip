@@ -391,9 +391,9 @@ struct AtAttnArgs {
 /* grid (n * kvh * ngrp, nchunks): workgroup = (token t, kv head kh, group
  * of up to AT_GMAX of the heads kh, kh + kvh, ...) over 256 keys; thread
  * tid owns key c*256 + tid for the scores, wave w the keys w, w+4, .. for
- * the v sums.  Per head the arithmetic (fma chain of q.k in dimension
- * order, chunk max, exp, wave tree, the v sums per wave, the waves added in
- * order) is that of one head alone. */
+ * the v sums; masked keys are not read.  Per head the arithmetic (fma chain
+ * of q.k in dimension order, chunk max, exp, wave tree, the v sums per
+ * wave, the waves added in order) is that of one head alone. */
 __global__ __launch_bounds__(AT_CHUNK) void k_at_attn(AtAttnArgs a) {
     __shared__ float s_q[AT_GMAX][256];
     __shared__ float s_p[AT_GMAX][AT_CHUNK];
@@ -410,7 +410,8 @@ __global__ __launch_bounds__(AT_CHUNK) void k_at_attn(AtAttnArgs a) {
         s_q[g][d] = g < ng ? qk_ld(a.qn + ((size_t)t * a.h + kh + (size_t)a.kvh * (j0 + g)) * a.hd + d) : 0.0f;
     }
     __syncthreads();
-    const int kk = c * AT_CHUNK + tid;
+    const int ck = AT_CHUNK;
+    const int kk = c * ck + tid;
     bool live = kk < a.kv_total && kk <= qpos;
     if (live && a.keep) {
         const int blk = kk / a.comp;
@@ -424,7 +425,7 @@ __global__ __launch_bounds__(AT_CHUNK) void k_at_attn(AtAttnArgs a) {
         float acc[AT_GMAX];
 #pragma unroll
         for (int g = 0; g < AT_GMAX; g++) acc[g] = 0.0f;
-        if (kk < a.kv_total) {
+        if (live) { /* masked keys are not read */
             const float4 *kr = (const float4 *)(a.k_cache + (size_t)kk * kvw + (size_t)kh * a.hd);
 #pragma unroll 4
             for (int i = 0; i < a.hd / 4; i++) {
@@ -476,10 +477,15 @@ __global__ __launch_bounds__(AT_CHUNK) void k_at_attn(AtAttnArgs a) {
     for (int g = 0; g < AT_GMAX; g++)
 #pragma unroll
         for (int e = 0; e < 4; e++) o[g][e] = 0.0f;
-    const int nk = min(AT_CHUNK, a.kv_total - c * AT_CHUNK);
+    const int nk = min(ck, a.kv_total - c * ck);
 #pragma unroll 8
     for (int j = wave; j < nk; j += 4) {
-        const float *vr = a.v_cache + (size_t)(c * AT_CHUNK + j) * kvw + (size_t)kh * a.hd;
+        /* a key with weight 0 for every head adds nothing: its row is not read */
+        bool any = false;
+#pragma unroll
+        for (int g = 0; g < AT_GMAX; g++) any = any || s_p[g][j] != 0.0f;
+        if (!any) continue;
+        const float *vr = a.v_cache + (size_t)(c * ck + j) * kvw + (size_t)kh * a.hd;
         float vv[4];
 #pragma unroll
         for (int e = 0; e < 4; e++) vv[e] = lane + 64 * e < a.hd ? qk_ld(vr + lane + 64 * e) : 0.0f;
@@ -509,6 +515,157 @@ __global__ __launch_bounds__(AT_CHUNK) void k_at_attn(AtAttnArgs a) {
     }
 }
 
+/* Calls of few tokens: chunks of 64 keys, so the cache spreads over many
+ * workgroups (a token at 4096 cached keys: 65 chunks per kv head instead of
+ * 17).  Four adjacent threads share a key, each an fma chain over a quarter
+ * of its dims in order, added by a butterfly; each thread's k quarter and
+ * its v rows (wave w: keys w, w+4, .., 16 of them) are loaded at the start,
+ * with the query and the block mask, so the kernel waits on memory once.
+ * A workgroup takes up to AT_G64 query heads, so a token's work spreads
+ * over twice the workgroups of AT_GMAX.  Rows past the cache are loaded
+ * clamped and never used. */
+#define AT_C64 64
+#define AT_HDMAX 256
+#define AT_G64 4 /* query heads of one kv head per 64-key workgroup, at most */
+
+__global__ __launch_bounds__(256) void k_at_attn64(AtAttnArgs a) {
+    __shared__ float s_q[AT_G64][AT_HDMAX];
+    __shared__ float s_p[AT_G64][AT_C64];
+    __shared__ float s_red[4][AT_G64][AT_HDMAX];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int G = a.h / a.kvh, ngrp = (G + AT_G64 - 1) / AT_G64;
+    const int t = blockIdx.x / (a.kvh * ngrp);
+    const int r = blockIdx.x - t * a.kvh * ngrp, kh = r / ngrp, grp = r - kh * ngrp;
+    const int j0 = grp * AT_G64, ng = min(AT_G64, G - j0);
+    const int c = blockIdx.y, qpos = a.offset + t;
+    const size_t kvw = (size_t)a.kvh * a.hd;
+    const int kl = tid >> 2, part = tid & 3; /* key of the chunk, quarter of its dims */
+    const int kk = c * AT_C64 + kl;
+    const int nq = a.hd >> 4; /* float4 steps of a quarter */
+    /* k quarter of the thread's key */
+    float4 kr[AT_HDMAX / 16];
+    {
+        const float4 *src = (const float4 *)(a.k_cache + (size_t)min(kk, a.kv_total - 1) * kvw +
+                                             (size_t)kh * a.hd) + part * nq;
+#pragma unroll
+        for (int i = 0; i < AT_HDMAX / 16; i++)
+            if (i < nq) kr[i] = qk_ld(src + i);
+    }
+    /* v rows of the wave's keys, the lane's dims lane, lane + 64, .. */
+    const int nk = min(AT_C64, a.kv_total - c * AT_C64);
+    float vr[AT_C64 / 4][AT_HDMAX / 64];
+#pragma unroll
+    for (int i = 0; i < AT_C64 / 4; i++) {
+        const float *src = a.v_cache + (size_t)(c * AT_C64 + min(wave + 4 * i, nk - 1)) * kvw + (size_t)kh * a.hd;
+#pragma unroll
+        for (int e = 0; e < AT_HDMAX / 64; e++)
+            if (lane + 64 * e < a.hd) vr[i][e] = qk_ld(src + lane + 64 * e);
+    }
+    uint32_t kw_word = 0;
+    if (a.keep && kk < a.kv_total && kk / a.comp < a.nb) kw_word = qk_ld(a.keep + (size_t)t * a.kw + ((kk / a.comp) >> 5));
+    for (int i = tid; i < AT_G64 * a.hd; i += 256) {
+        const int g = i / a.hd, d = i - g * a.hd;
+        s_q[g][d] = g < ng ? qk_ld(a.qn + ((size_t)t * a.h + kh + (size_t)a.kvh * (j0 + g)) * a.hd + d) : 0.0f;
+    }
+    __syncthreads();
+    bool live = kk < a.kv_total && kk <= qpos;
+    if (live && a.keep) {
+        const int blk = kk / a.comp;
+        bool kp = blk < a.nb && ((kw_word >> (blk & 31)) & 1u);
+        const long long own = ((long long)(qpos + 1) / a.comp) * a.comp;
+        if (kk >= own) kp = true;
+        live = kp;
+    }
+    float sc[AT_G64];
+    {
+        float acc[AT_G64];
+#pragma unroll
+        for (int g = 0; g < AT_G64; g++) acc[g] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < AT_HDMAX / 16; i++)
+            if (i < nq) {
+                const int d = 4 * (part * nq + i);
+#pragma unroll
+                for (int g = 0; g < AT_G64; g++) {
+                    acc[g] = fmaf(s_q[g][d], kr[i].x, acc[g]);
+                    acc[g] = fmaf(s_q[g][d + 1], kr[i].y, acc[g]);
+                    acc[g] = fmaf(s_q[g][d + 2], kr[i].z, acc[g]);
+                    acc[g] = fmaf(s_q[g][d + 3], kr[i].w, acc[g]);
+                }
+            }
+        /* the four quarters of a key (adjacent lanes), added by a butterfly */
+#pragma unroll
+        for (int g = 0; g < AT_G64; g++) {
+            acc[g] += qk_dpp<QK_DPP_XOR1>(acc[g]);
+            acc[g] += qk_dpp<QK_DPP_XOR2>(acc[g]);
+            sc[g] = live ? acc[g] * (1.0f / sqrtf((float)a.hd)) : -INFINITY;
+        }
+    }
+    float mg[AT_G64], lg[AT_G64];
+#pragma unroll
+    for (int g = 0; g < AT_G64; g++) {
+        float m = sc[g];
+        m = fmaxf(m, qk_dpp<QK_DPP_XOR1>(m));
+        m = fmaxf(m, qk_dpp<QK_DPP_XOR2>(m));
+        m = fmaxf(m, qk_dpp<QK_DPP_HALF_MIRROR>(m));
+        m = fmaxf(m, qk_dpp<QK_DPP_MIRROR>(m));
+        m = fmaxf(m, __uint_as_float(qk_xor16_u(__float_as_uint(m))));
+        m = fmaxf(m, __uint_as_float(qk_xor32_u(__float_as_uint(m))));
+        if (lane == 0) s_red[wave][g][0] = m;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < AT_G64; g++) {
+        const float m = fmaxf(fmaxf(s_red[0][g][0], s_red[1][g][0]), fmaxf(s_red[2][g][0], s_red[3][g][0]));
+        /* the first quarter of each key carries its weight */
+        const float p = (m == -INFINITY || part != 0) ? 0.0f : expf(sc[g] - m);
+        if (part == 0) s_p[g][kl] = p;
+        mg[g] = m;
+        lg[g] = qk_group_sum<64>(p);
+    }
+    __syncthreads(); /* s_red reused, s_p complete */
+#pragma unroll
+    for (int g = 0; g < AT_G64; g++)
+        if (lane == 0) s_red[wave][g][1] = lg[g];
+    float o[AT_G64][AT_HDMAX / 64];
+#pragma unroll
+    for (int g = 0; g < AT_G64; g++)
+#pragma unroll
+        for (int e = 0; e < AT_HDMAX / 64; e++) o[g][e] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < AT_C64 / 4; i++) {
+        const int j = wave + 4 * i;
+        if (j < nk) {
+#pragma unroll
+            for (int g = 0; g < AT_G64; g++) {
+                const float pj = s_p[g][j];
+#pragma unroll
+                for (int e = 0; e < AT_HDMAX / 64; e++) o[g][e] = fmaf(pj, vr[i][e], o[g][e]);
+            }
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < AT_G64; g++) lg[g] = ((s_red[0][g][1] + s_red[1][g][1]) + s_red[2][g][1]) + s_red[3][g][1];
+    __syncthreads(); /* s_red[.][.][1] read before the v sums overwrite it */
+#pragma unroll
+    for (int g = 0; g < AT_G64; g++)
+#pragma unroll
+        for (int e = 0; e < AT_HDMAX / 64; e++)
+            if (lane + 64 * e < a.hd) s_red[wave][g][lane + 64 * e] = o[g][e];
+    __syncthreads();
+    for (int g = 0; g < ng; g++) {
+        const int hh = kh + a.kvh * (j0 + g);
+        float *dst = a.part + (((size_t)t * a.h + hh) * a.nchunks + c) * (a.hd + 2);
+        for (int i = tid; i < a.hd; i += 256)
+            dst[2 + i] = ((s_red[0][g][i] + s_red[1][g][i]) + s_red[2][g][i]) + s_red[3][g][i];
+        if (tid == 0) {
+            dst[0] = mg[g];
+            dst[1] = lg[g];
+        }
+    }
+}
+
 struct AtCombArgs {
     const float *part;      /* [n, h, nchunks, hd + 2] */
     const float *qg;        /* [n, 2h*hd] */
@@ -516,51 +673,70 @@ struct AtCombArgs {
     int h, hd, nchunks;
 };
 
-#define AT_MAXCH 32 /* chunks of 256 keys: kv_cap <= 8192 */
+#define AT_MAXCH 128 /* chunks of 64 keys: kv_cap <= 8192 */
 
-/* one wave per (token, head); lane c holds chunk c's max and sum, every
- * chunk's partial v sums for the lane's dims are loaded at once; the sums
- * run over the chunks in order, a chunk with every key masked (max -inf,
- * sums 0) entering with factor exp(-inf) = 0, which leaves them unchanged */
-__global__ __launch_bounds__(64) void k_at_comb(AtCombArgs a) {
-    const int lane = threadIdx.x, th = blockIdx.x;
+/* one workgroup per (token, head): the chunks' maxima give M; wave w sums
+ * the chunks w, w+4, .. in order, each with factor exp(max - M) (a chunk
+ * with every key masked, max -inf and sums 0, enters with factor 0 and
+ * leaves the sums unchanged), lane the dims lane, lane + 64, ..; the four
+ * waves' sums are added in order */
+template <int CPW> /* chunks per wave, at most: AT_MAXCH / 4 or 8 (256-key chunks) */
+__global__ __launch_bounds__(256) void k_at_comb(AtCombArgs a) {
+    __shared__ float s_m[AT_MAXCH];
+    __shared__ float s_o[4][AT_HDMAX + 1];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, th = blockIdx.x;
     const int t = th / a.h, hh = th - t * a.h;
     const size_t cw = (size_t)a.hd + 2;
     const float *pp = a.part + (size_t)th * a.nchunks * cw;
-    const bool cl = lane < a.nchunks;
-    const float mc = cl ? qk_ld(pp + (size_t)lane * cw) : -INFINITY;
-    const float lc = cl ? qk_ld(pp + (size_t)lane * cw + 1) : 0.0f;
-    float v[AT_MAXCH][4];
-#pragma unroll
-    for (int c = 0; c < AT_MAXCH; c++)
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-            v[c][e] = (c < a.nchunks && lane + 64 * e < a.hd) ? qk_ld(pp + (size_t)c * cw + 2 + lane + 64 * e) : 0.0f;
-    float M = mc;
+    if (tid < AT_MAXCH) s_m[tid] = tid < a.nchunks ? qk_ld(pp + (size_t)tid * cw) : -INFINITY;
+    __syncthreads();
+    float M = fmaxf(s_m[lane], s_m[lane + 64]);
     M = fmaxf(M, qk_dpp<QK_DPP_XOR1>(M));
     M = fmaxf(M, qk_dpp<QK_DPP_XOR2>(M));
     M = fmaxf(M, qk_dpp<QK_DPP_HALF_MIRROR>(M));
     M = fmaxf(M, qk_dpp<QK_DPP_MIRROR>(M));
     M = fmaxf(M, __uint_as_float(qk_xor16_u(__float_as_uint(M))));
     M = fmaxf(M, __uint_as_float(qk_xor32_u(__float_as_uint(M))));
-    const float fc = expf(mc - M);
-    float L = 0.0f;
-    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    /* every partial of the wave's chunks is loaded before the sums start
+     * (a loop over a runtime count would wait for each chunk in turn) */
+    float lv[CPW], vv[CPW][AT_HDMAX / 64];
 #pragma unroll
-    for (int c = 0; c < AT_MAXCH; c++) {
-        if (c < a.nchunks) {
-            const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fc), c));
-            L = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(lc), c)), f, L);
+    for (int i = 0; i < CPW; i++) {
+        const int ci = wave + 4 * i;
+        if (ci < a.nchunks) {
+            const float *q = pp + (size_t)ci * cw;
+            lv[i] = qk_ld(q + 1);
 #pragma unroll
-            for (int e = 0; e < 4; e++) o[e] = fmaf(v[c][e], f, o[e]);
+            for (int e = 0; e < AT_HDMAX / 64; e++)
+                if (lane + 64 * e < a.hd) vv[i][e] = qk_ld(q + 2 + lane + 64 * e);
         }
     }
-    const float inv = 1.0f / L;
-    const float *g = a.qg + (size_t)t * 2 * a.h * a.hd + (size_t)hh * 2 * a.hd + a.hd;
+    float L = 0.0f;
+    float o[AT_HDMAX / 64];
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const int i = lane + 64 * e;
-        if (i < a.hd) a.ao[(size_t)th * a.hd + i] = (o[e] * inv) * (1.0f / (1.0f + expf(-qk_ld(g + i))));
+    for (int e = 0; e < AT_HDMAX / 64; e++) o[e] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPW; i++) {
+        const int ci = wave + 4 * i;
+        if (ci < a.nchunks) {
+            const float f = expf(s_m[ci] - M);
+            L = fmaf(lv[i], f, L);
+#pragma unroll
+            for (int e = 0; e < AT_HDMAX / 64; e++)
+                if (lane + 64 * e < a.hd) o[e] = fmaf(vv[i][e], f, o[e]);
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < AT_HDMAX / 64; e++)
+        if (lane + 64 * e < a.hd) s_o[wave][lane + 64 * e] = o[e];
+    if (lane == 0) s_o[wave][AT_HDMAX] = L;
+    __syncthreads();
+    const float Ls = ((s_o[0][AT_HDMAX] + s_o[1][AT_HDMAX]) + s_o[2][AT_HDMAX]) + s_o[3][AT_HDMAX];
+    const float inv = 1.0f / Ls;
+    const float *g = a.qg + (size_t)t * 2 * a.h * a.hd + (size_t)hh * 2 * a.hd + a.hd;
+    for (int i = tid; i < a.hd; i += 256) {
+        const float v = ((s_o[0][i] + s_o[1][i]) + s_o[2][i]) + s_o[3][i];
+        a.ao[(size_t)th * a.hd + i] = (v * inv) * (1.0f / (1.0f + expf(-qk_ld(g + i))));
     }
 }
 
@@ -672,15 +848,24 @@ extern "C" int qk_launch_at(const qk_at_shape *s, const qk_at_dev *W, const floa
     at.part = sc->part;
     at.h = h; at.kvh = kvh; at.hd = hd; at.kv_total = kv_total; at.offset = offset;
     at.comp = s->comp; at.nb = nb; at.kw = kw;
-    at.nchunks = (kv_total + AT_CHUNK - 1) / AT_CHUNK;
     const int ngrp = (h / kvh + AT_GMAX - 1) / AT_GMAX;
-    hipLaunchKernelGGL(k_at_attn, dim3(n * kvh * ngrp, at.nchunks), dim3(AT_CHUNK), 0, st, at);
+    /* 64-key chunks while 256-key ones leave the grid under 512 workgroups
+     * and the partials of 64-key chunks fit the scratch */
+    const long long n64 = (kv_total + AT_C64 - 1) / AT_C64;
+    const bool c64 = (long long)n * kvh * ngrp * ((kv_total + AT_CHUNK - 1) / AT_CHUNK) < 512 &&
+                     n * n64 <= sc->part_units && n64 <= AT_MAXCH;
+    at.nchunks = c64 ? (int)n64 : (kv_total + AT_CHUNK - 1) / AT_CHUNK;
+    if ((long long)n * at.nchunks > sc->part_units) return (int)hipErrorInvalidValue;
+    const int ngrp64 = (h / kvh + AT_G64 - 1) / AT_G64;
+    if (c64) hipLaunchKernelGGL(k_at_attn64, dim3(n * kvh * ngrp64, at.nchunks), dim3(256), 0, st, at);
+    else hipLaunchKernelGGL(k_at_attn, dim3(n * kvh * ngrp, at.nchunks), dim3(AT_CHUNK), 0, st, at);
     rc = QK_CHECK_LAUNCH();
     if (rc) return rc;
 
     AtCombArgs cb;
     cb.part = sc->part; cb.qg = sc->qg; cb.ao = sc->ao; cb.h = h; cb.hd = hd; cb.nchunks = at.nchunks;
-    hipLaunchKernelGGL(k_at_comb, dim3(n * h), dim3(64), 0, st, cb);
+    if (at.nchunks <= 32) hipLaunchKernelGGL(k_at_comb<8>, dim3(n * h), dim3(256), 0, st, cb);
+    else hipLaunchKernelGGL(k_at_comb<AT_MAXCH / 4>, dim3(n * h), dim3(256), 0, st, cb);
     rc = QK_CHECK_LAUNCH();
     if (rc) return rc;
 

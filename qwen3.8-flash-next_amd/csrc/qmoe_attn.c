@@ -100,9 +100,13 @@ int qmoe_attn_create(qmoe_attn_ctx **out, const qmoe_attn_config *cfg, qmoe_err 
         total = at_align(total + sz[i]);
     }
     const size_t n = (size_t)cfg->max_tokens;
-    const size_t nchunks = (cap + 255) / 256, kw = (cap / (size_t)s.comp + 31) / 32 + 1;
+    /* the attention partials hold max_tokens calls' worth of 256-key chunks,
+     * and at least one token's 64-key chunks (one-token calls split the
+     * cache finer) */
+    const size_t units = n * ((cap + 255) / 256) > (cap + 63) / 64 ? n * ((cap + 255) / 256) : (cap + 63) / 64;
+    const size_t kw = (cap / (size_t)s.comp + 31) / 32 + 1;
     const size_t ssz[10] = {n * qr * 4, n * kr * 4, n * kr * 4, n * (ih + 1) * ihd * 4, n * h * hd * 4,
-                            n * ih * ihd * 4, n * kw * 4, n * h * nchunks * (hd + 2) * 4, n * h * hd * 4,
+                            n * ih * ihd * 4, n * kw * 4, units * h * (hd + 2) * 4, n * h * hd * 4,
                             n * (cap / (size_t)s.comp) * 4};
     size_t stot = 0, soff[10];
     for (int i = 0; i < 10; i++) {
@@ -123,6 +127,7 @@ int qmoe_attn_create(qmoe_attn_ctx **out, const qmoe_attn_config *cfg, qmoe_err 
     c->sc.qn = (float *)(b + soff[4]);
     c->sc.qi = (float *)(b + soff[5]);
     c->sc.keep = (uint32_t *)(b + soff[6]);
+    c->sc.part_units = (long long)units;
     c->sc.part = (float *)(b + soff[7]);
     c->sc.ao = (float *)(b + soff[8]);
     c->sc.skey = (uint32_t *)(b + soff[9]);

@@ -229,9 +229,10 @@ typedef struct {
     float *qn;    /* [n, h*hd] */
     float *qi;    /* [n, ih*ihd] */
     uint32_t *keep; /* [n, ceil(cap/comp/32)] */
-    float *part;  /* [n, h, ceil(cap/256), hd+2] */
+    float *part;  /* [n, h, nchunks, hd+2]: part_units (token, chunk) pairs per head */
     float *ao;    /* [n, h*hd] */
     uint32_t *skey; /* [n, cap/comp] order keys of the block scores */
+    long long part_units; /* capacity of part in (token, key chunk) pairs per head */
 } qk_at_scratch;
 int qk_at_shape_ok(const qk_at_shape *s);
 size_t qk_at_sel_lds(const qk_at_shape *s, int nb);
