@@ -458,6 +458,179 @@ __global__ __launch_bounds__(256) void k_pack_rows(const void *x, size_t nchunks
     if ((i & 7) == 0) gsum[i >> 3] = -128.0f * s;
 }
 
+/*
+ * Down projection of batches of at most MM_NARROW_N tokens, K = 512, on the
+ * dispatch's 16-row task list.  The 64-row kernel waits, every group, on
+ * the chain activation load -> LDS store -> barrier -> LDS read (~1 us per
+ * group at 1..16 rows).  Here the code words of the whole K slice of the
+ * tile (8 groups, 16 bytes per lane and column tile) are loaded into
+ * registers at the start, the chunk's f32 h is staged in LDS at once (hi +
+ * lo planes and the group sums P, the arithmetic of k_pack_rows), and the
+ * K loop reads LDS and registers only, with no barrier.  The products,
+ * their order and the epilogue are those of mm_body: the outputs are
+ * bit-identical.
+ */
+#define MMD_G 8 /* K / 64 of the shapes this kernel takes */
+
+struct MmdSmem {
+    uint4 a[2][MMD_G * 16 * 8]; /* hi, lo: [(g*16 + row)*8 + (kc ^ (row & 7))] */
+    float p[MMD_G][16];         /* P = -128 X_g of the block's rows */
+    uint16_t s[MMD_G][4][16][2]; /* scales, [group][wave][column][tile] */
+};
+
+__global__ __launch_bounds__(256, 2) void k_mm_down16(MmArgs a) {
+    constexpr int G = MMD_G, CT = 2;
+    __shared__ __attribute__((aligned(16))) MmdSmem sm;
+    /* workgroups over the XCDs as for k_mm */
+    const int L = blockIdx.x;
+    const int i8 = L >> 3;
+    const int mt = (i8 / a.ntile) * 8 + (L & 7), nt = i8 - (i8 / a.ntile) * a.ntile;
+    if (mt >= qk_ld(a.tasks)) return;
+    const int4 tk = qk_ld((const int4 *)(a.tasks + MM_TASK_HDR) + mt);
+    const int e = tk.x, p0 = tk.y, m = tk.z, mstart = tk.w * MM_BM16;
+    const int mrows = min(MM_BM16, m - mstart);
+    if (mrows <= 0) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c = lane & 15, kq = lane >> 4;
+    const size_t wrow = (size_t)a.K >> 3;
+    const bool shared = e < 0;
+
+    /* every code word of the tile's K slice: words 2kq, 2kq+1 of each group */
+    uint2 wr[G][CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) {
+        const uint32_t *base = shared ? a.sq[0] : a.q[0] + (size_t)e * a.N * wrow;
+        const uint32_t *wq = base + (size_t)mm_col<true, CT>(nt, wave, ct, c) * wrow + 2 * kq;
+#pragma unroll
+        for (int g = 0; g < G; g++) wr[g][ct] = qk_ld((const uint2 *)(wq + 8 * g));
+    }
+    /* scales of the tile (as mm_body) */
+    const int w2 = tid / (16 * CT), ct2 = (tid >> 4) % CT, c2 = tid & 15;
+    uint4 sv = make_uint4(0, 0, 0, 0);
+    if (tid < 64 * CT) {
+        const uint16_t *sp = (shared ? a.ss[0] : a.s[0] + (size_t)e * a.N * G) +
+                             (size_t)mm_col<true, CT>(nt, w2, ct2, c2) * G;
+        sv = qk_ld((const uint4 *)sp);
+    }
+    /* bias words of the tile (one K step of 32 groups covers G = 8) */
+    qm_bf16x8 bb[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) {
+        const uint16_t *bp = (shared ? a.sb[0] : a.b[0] + (size_t)e * a.N * G) +
+                             (size_t)mm_col<true, CT>(nt, wave, ct, c) * G;
+        const uint4 v = kq == 0 ? qk_ld((const uint4 *)bp) : make_uint4(0, 0, 0, 0);
+        bb[ct] = __builtin_bit_cast(qm_bf16x8, v);
+    }
+
+    /* thread -> row tid/16 of the chunk, 8-column chunks ci = tid%16 + 16 j
+     * of that row (4 per thread) */
+    const int arow = tid >> 4;
+    {
+        const int r0 = 0, brows = mrows;
+        const float *src0 = a.af + (size_t)(p0 + mstart + r0 + min(arow, brows - 1)) * a.K + 8 * (tid & 15);
+        float4 f[G / 2][2];
+#pragma unroll
+        for (int j = 0; j < G / 2; j++) {
+            f[j][0] = qk_ld((const float4 *)(src0 + 128 * j));
+            f[j][1] = qk_ld((const float4 *)(src0 + 128 * j) + 1);
+        }
+#pragma unroll
+        for (int j = 0; j < G / 2; j++) {
+            const int ci = (tid & 15) + 16 * j, g = ci >> 3, kc = ci & 7;
+            /* k_pack_rows' arithmetic: pairs, then the group sum over the 8
+             * chunk-lanes of the group (xor 1, 2, 4) */
+            float v[8] = {f[j][0].x, f[j][0].y, f[j][0].z, f[j][0].w, f[j][1].x, f[j][1].y, f[j][1].z, f[j][1].w};
+            uint32_t hi[4], lo[4];
+            float sg = 0.0f;
+            sg = sg + qk_f32x8_pairs(v, hi, lo);
+            sg += qk_dpp<QK_DPP_XOR1>(sg);
+            sg += qk_dpp<QK_DPP_XOR2>(sg);
+            sg += __shfl_xor(sg, 4, QK_WAVE);
+            const int li = (g * 16 + arow) * 8 + (kc ^ (arow & 7));
+            sm.a[0][li] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+            sm.a[1][li] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+            if (kc == 0) sm.p[g][arow] = -128.0f * sg;
+        }
+        if (tid < 64 * CT) {
+            const uint32_t wv[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                sm.s[2 * j][w2][c2][ct2] = (uint16_t)(wv[j] & 0xFFFFu);
+                sm.s[2 * j + 1][w2][c2][ct2] = (uint16_t)(wv[j] >> 16);
+            }
+        }
+        __syncthreads();
+
+        qm_f32x4 acc[CT];
+#pragma unroll
+        for (int ct = 0; ct < CT; ct++) acc[ct] = qm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            qm_bf16x8 bop[CT][2];
+#pragma unroll
+            for (int ct = 0; ct < CT; ct++) {
+                bop[ct][0] = qm_codes(wr[g][ct].x);
+                bop[ct][1] = qm_codes(wr[g][ct].y);
+            }
+            qm_bf16x8 A[2][2];
+#pragma unroll
+            for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    A[tm][j] = __builtin_bit_cast(qm_bf16x8, sm.a[tm][(g * 16 + c) * 8 + ((2 * kq + j) ^ (c & 7))]);
+            const uint32_t sw = *(const uint32_t *)&sm.s[g][wave][c][0];
+            const float sc[CT] = {qk_bf16_lo(sw), qk_bf16_hi(sw)};
+            const qm_f32x4 xi = *(const qm_f32x4 *)&sm.p[g][4 * kq];
+            qm_f32x4 t[CT];
+#pragma unroll
+            for (int ct = 0; ct < CT; ct++)
+                t[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[0][0], bop[ct][0], xi, 0, 0, 0);
+#pragma unroll
+            for (int tm = 0; tm < 2; tm++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    if (tm == 0 && j == 0) continue;
+#pragma unroll
+                    for (int ct = 0; ct < CT; ct++)
+                        t[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[tm][j], bop[ct][j], t[ct], 0, 0, 0);
+                }
+#pragma unroll
+            for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[ct][i] = fmaf(sc[ct], t[ct][i], acc[ct][i]);
+        }
+        /* bias term (as mm_body): acc += sum_g b[col][g] * X[row][g] */
+        {
+            float xv[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) xv[j] = 8 * kq + j < G ? sm.p[8 * kq + j][c] : 0.0f;
+            uint32_t hi[4], lo[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float x0 = xv[2 * j] * (-1.0f / 128.0f), x1 = xv[2 * j + 1] * (-1.0f / 128.0f);
+                hi[j] = qk_cvt_pk_bf16(x0, x1);
+                lo[j] = qk_cvt_pk_bf16(x0 - qk_bf16_lo(hi[j]), x1 - qk_bf16_hi(hi[j]));
+            }
+            const qm_bf16x8 AH = __builtin_bit_cast(qm_bf16x8, make_uint4(hi[0], hi[1], hi[2], hi[3]));
+            const qm_bf16x8 AL = __builtin_bit_cast(qm_bf16x8, make_uint4(lo[0], lo[1], lo[2], lo[3]));
+#pragma unroll
+            for (int ct = 0; ct < CT; ct++) {
+                acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(AH, bb[ct], acc[ct], 0, 0, 0);
+                acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(AL, bb[ct], acc[ct], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int row = 4 * kq + i;
+            if (row < brows) {
+                float *o = a.out + (size_t)(p0 + mstart + r0 + row) * a.N;
+#pragma unroll
+                for (int ct = 0; ct < CT; ct++) qk_st(o + mm_col<true, CT>(nt, wave, ct, c), acc[ct][i]);
+            }
+        }
+    }
+}
+
 /* the task list as its own launch (mm_tasks.h) */
 __global__ __launch_bounds__(1024) void k_mm_tasks(const int32_t *segtab, int n, int k, int E,
                                                    int min_m, int32_t *tasks, int32_t *small) {
@@ -468,13 +641,21 @@ __global__ __launch_bounds__(1024) void k_mm_tasks(const int32_t *segtab, int n,
  * hold 64-row chunks and give each wave 2 column tiles instead of 4, so a
  * batch of mostly small segments spreads over twice the workgroups (with
  * few rows per task the per-group latency, not the MFMA rate, bounds a
- * workgroup). */
-#define MM_NARROW_N 64
+ * workgroup); the down projection at K = 512 runs on k_mm_down16 over the
+ * 16-row list. */
 
-static int mm_launch(MmArgs &a, bool down, int terms, int max_tasks, hipStream_t st) {
+static int mm_launch(MmArgs &a, bool down, int terms, int max_tasks, hipStream_t st,
+                     const int32_t *list16 = nullptr, int max16 = 0) {
     const bool narrow = a.n <= MM_NARROW_N;
     const int ct = narrow ? 2 : 4;
     a.ntile = a.N / (down ? 64 * ct : 32 * ct);
+    if (narrow && down && list16 && a.K == 64 * MMD_G) {
+        a.tasks = list16;
+        const long long wgs16 = (long long)(max16 + 7) / 8 * 8 * a.ntile;
+        if (wgs16 <= 0) return 0;
+        hipLaunchKernelGGL(k_mm_down16, dim3((unsigned)wgs16), dim3(256), 0, st, a);
+        return QK_CHECK_LAUNCH();
+    }
     /* every (task, column tile) once: 8 * ceil(max_tasks / 8) tasks */
     const long long wgs = (long long)(max_tasks + 7) / 8 * 8 * a.ntile;
     if (wgs <= 0) return 0;
@@ -499,8 +680,16 @@ extern "C" int qk_mfma_max_tasks(qk_shape s, int n) {
     return (int)t;
 }
 
+/* entries of the 16-row list (0 above MM_NARROW_N tokens) */
+static int mm_max_tasks16(qk_shape s, int n) {
+    if (n > MM_NARROW_N) return 0;
+    const long long nk = (long long)n * s.k;
+    return (int)((nk < s.E ? nk : s.E) + nk / MM_BM16 + (n + MM_BM16 - 1) / MM_BM16 + 1);
+}
+
 extern "C" size_t qk_mfma_task_bytes(qk_shape s, int n) {
-    return ((size_t)MM_TASK_HDR + 4 * (size_t)qk_mfma_max_tasks(s, n) + 2 + (size_t)s.E) * 4;
+    const size_t t16 = n <= MM_NARROW_N ? (size_t)MM_TASK_HDR + 4 * (size_t)mm_max_tasks16(s, n) : 0;
+    return ((size_t)MM_TASK_HDR + 4 * (size_t)qk_mfma_max_tasks(s, n) + 2 + (size_t)s.E + t16) * 4;
 }
 
 extern "C" int32_t *qk_mfma_small_list(qk_shape s, int n, int32_t *tasks) {
@@ -584,5 +773,7 @@ extern "C" int qk_launch_down_mfma(const qmoe_layer_weights *W, qk_shape s, cons
     a.N = s.H;
     a.n = n;
     a.k = s.k;
-    return mm_launch(a, true, 2, qk_mfma_max_tasks(s, n), (hipStream_t)stream);
+    return mm_launch(a, true, 2, qk_mfma_max_tasks(s, n), (hipStream_t)stream,
+                     n <= MM_NARROW_N ? qk_mfma_small_list(s, n, (int32_t *)tasks) + 2 + s.E : nullptr,
+                     mm_max_tasks16(s, n));
 }

@@ -13,17 +13,21 @@
 #define MM_BM (16 * MM_MT)   /* rows per chunk */
 #define MM_TASK_HDR 4        /* int32 header before the int4 task entries */
 
-/* Task list: {expert (-1 = shared), first position, rows, chunk} for
- * every segment with at least min_m rows; the shared expert covers all n
- * tokens at positions n*k.. .  tasks[0] = count; entries from
- * tasks + MM_TASK_HDR.  The segments with 1..min_m-1 rows (0 = shared) are
- * listed for the GEMV kernels at `small`: small[0] = count, then ids. */
-static __device__ void mm_tasks_block(const int32_t *segtab, int n, int k, int E, int min_m, int32_t *tasks,
-                               int32_t *small) {
+#define MM_NARROW_N 64       /* batches up to this many tokens also get a 16-row list */
+#define MM_BM16 16
+
+/* One task list: {expert (-1 = shared), first position, rows, chunk} for
+ * every chunk of bm rows of the segments with at least min_m rows; the
+ * shared expert covers all n tokens at positions n*k.. .  list[0] =
+ * count; entries from list + MM_TASK_HDR.  With `small`, the segments with
+ * 1..min_m-1 rows (0 = shared) are listed for the GEMV kernels: small[0] =
+ * count, then ids. */
+static __device__ void mm_tasks_list(const int32_t *segtab, int n, int k, int E, int min_m, int bm,
+                                     int32_t *list, int32_t *small) {
     __shared__ int s_scan[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int U = min(max(qk_ld(segtab), 0), E);
-    int4 *out = (int4 *)(tasks + MM_TASK_HDR);
+    int4 *out = (int4 *)(list + MM_TASK_HDR);
     int base = 0, sbase = 0;
     /* segments 0..U in blocks of 1024; segment 0 is the shared expert */
     for (int s0 = 0; s0 <= U; s0 += 1024) {
@@ -36,7 +40,7 @@ static __device__ void mm_tasks_block(const int32_t *segtab, int n, int k, int E
             p0 = qk_ld(segtab + 3 * sg - 1);
             m = qk_ld(segtab + 3 * sg);
         }
-        const int cnt = m >= min_m && m > 0 ? (m + MM_BM - 1) / MM_BM : 0;
+        const int cnt = m >= min_m && m > 0 ? (m + bm - 1) / bm : 0;
         const int sm = m > 0 && m < min_m ? 1 : 0;
         /* both counts in one scan: chunks in bits 0..19, small segments above */
         const int own = cnt + (sm << 20);
@@ -63,14 +67,23 @@ static __device__ void mm_tasks_block(const int32_t *segtab, int n, int k, int E
             o[2] = m;
             o[3] = ch;
         }
-        if (sm) small[1 + soff] = sg;
+        if (sm && small) small[1 + soff] = sg;
         base += tot & 0xFFFFF;
         sbase += tot >> 20;
     }
     if (tid == 0) {
-        tasks[0] = base;
-        small[0] = sbase;
+        list[0] = base;
+        if (small) small[0] = sbase;
     }
+}
+
+/* The task lists of a dispatch: chunks of MM_BM rows at `tasks` with the
+ * small-segment list at `small`, and, up to MM_NARROW_N tokens, chunks of
+ * MM_BM16 rows at small + 2 + E (the down projection's list there). */
+static __device__ void mm_tasks_block(const int32_t *segtab, int n, int k, int E, int min_m, int32_t *tasks,
+                               int32_t *small) {
+    mm_tasks_list(segtab, n, k, E, min_m, MM_BM, tasks, small);
+    if (n <= MM_NARROW_N) mm_tasks_list(segtab, n, k, E, min_m, MM_BM16, small + 2 + E, nullptr);
 }
 
 #endif
