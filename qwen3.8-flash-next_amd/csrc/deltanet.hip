@@ -276,12 +276,17 @@ struct DnOutArgs {
 
 #define DN_ORW 2 /* out_proj rows per wave */
 
+#define DN_KCMAX 16 /* conv taps at most */
+#define DN_NBU 16   /* sums-of-squares partials per head loaded at once */
+
 /*
  * One wave per DN_ORW rows of out_proj.  The gated norm's head factor
  * r = 1/sqrt(sum(o^2)/dv + eps) comes from the per-block sums of squares
- * of k_dn_rec (dv/16 of them per head); each lane scales its own chunks
- * (32 columns of one head) and splits them into bf16 hi + lo pairs.  No
- * LDS and no barrier.
+ * of k_dn_rec (dv/16 of them per head, loaded together and added in
+ * order); each lane scales its own chunks (32 columns of one head) and
+ * splits them into bf16 hi + lo pairs.  The code words are loaded first;
+ * the conv state moves on at the end (its stores would otherwise hold the
+ * loads back).  No LDS and no barrier.
  */
 template <int P>
 __global__ __launch_bounds__(256) void k_dn_out(DnOutArgs a) {
@@ -289,21 +294,23 @@ __global__ __launch_bounds__(256) void k_dn_out(DnOutArgs a) {
     const int K = a.value_dim, CH = K >> 5, G = K >> 6;
     const size_t wrow = (size_t)K >> 3;
 
-    /* the conv state: channels [c0, c0 + ch_per_wg) move on by n tokens */
-    {
-        const int c = blockIdx.x * a.ch_per_wg + tid;
-        if (tid < a.ch_per_wg && c < a.conv_dim) {
-            for (int j = 0; j < a.kc - 1; j++) {
+    /* the conv state: channels [c0, c0 + ch_per_wg) move on by n tokens;
+     * every new value is read now, written at the end */
+    const int cc = blockIdx.x * a.ch_per_wg + tid;
+    const bool cthr = tid < a.ch_per_wg && cc < a.conv_dim;
+    float cv[DN_KCMAX - 1];
+    if (cthr) {
+#pragma unroll
+        for (int j = 0; j < DN_KCMAX - 1; j++)
+            if (j < a.kc - 1) {
                 const int m = a.n + j;
-                const float v = m < a.kc - 1 ? a.conv_state[(size_t)m * a.conv_dim + c]
-                                             : qk_ld(a.mixed + (size_t)(m - (a.kc - 1)) * a.conv_dim + c);
-                a.conv_state[(size_t)j * a.conv_dim + c] = v;
+                cv[j] = m < a.kc - 1 ? a.conv_state[(size_t)m * a.conv_dim + cc]
+                                     : qk_ld(a.mixed + (size_t)(m - (a.kc - 1)) * a.conv_dim + cc);
             }
-        }
     }
 
     const int r0 = (blockIdx.x * 4 + (tid >> 6)) * DN_ORW;
-    if (r0 >= a.d) return;
+    if (r0 < a.d) {
     uint4 wq[DN_ORW][P];
     float ws[DN_ORW][P], wb[DN_ORW][P];
 #pragma unroll
@@ -331,7 +338,13 @@ __global__ __launch_bounds__(256) void k_dn_out(DnOutArgs a) {
             const int head = (32 * c) / a.dv, nb = a.dv / DN_RB;
             const float *sp = a.ssp + ((size_t)t * (K / a.dv) + head) * nb;
             float ss = 0.0f;
-            for (int j = 0; j < nb; j++) ss = ss + qk_ld(sp + j);
+            for (int j0 = 0; j0 < nb; j0 += DN_NBU) {
+                float pv[DN_NBU];
+#pragma unroll
+                for (int j = 0; j < DN_NBU; j++) pv[j] = qk_ld(sp + min(j0 + j, nb - 1));
+#pragma unroll
+                for (int j = 0; j < DN_NBU; j++) ss = ss + (j0 + j < nb ? pv[j] : 0.0f);
+            }
             const float r = 1.0f / sqrtf(ss / (float)a.dv + 1e-6f);
 #pragma unroll
             for (int w = 0; w < 8; w++) {
@@ -347,6 +360,12 @@ __global__ __launch_bounds__(256) void k_dn_out(DnOutArgs a) {
             const int rr = r0 + j;
             if (lane == 0 && rr < a.d) qk_st(a.out + (size_t)t * a.d + rr, v);
         }
+    }
+    }
+    if (cthr) {
+#pragma unroll
+        for (int j = 0; j < DN_KCMAX - 1; j++)
+            if (j < a.kc - 1) a.conv_state[(size_t)j * a.conv_dim + cc] = cv[j];
     }
 }
 
