@@ -105,6 +105,34 @@ def test_model_shape_long_context(torch_dev):
     run_calls(torch, dev, case, [256, 256, 188, 1, 1, 1], seed=2)
 
 
+WIDE_CASES = [
+    # head_dim 256 (the register arrays' bound), one kv head for 4 heads
+    (512, 4, 1, 256, 2, 64, 4096, 4, 256, 0.25),
+    # 16 query heads on one kv head: several head groups per workgroup row
+    (256, 16, 1, 64, 2, 64, 16, 4, 128, 0.25),
+]
+
+
+@pytest.mark.parametrize("case", WIDE_CASES)
+def test_wide_head_shapes(torch_dev, case):
+    torch, dev = torch_dev
+    say(f"case: attention {case}")
+    run_calls(torch, dev, case, [1, 3, 1, 40, 1, 5, 1])
+
+
+def test_long_cache_decode(torch_dev):
+    """6,000+ cached keys: one-token calls split the cache into ~97 chunks
+    of 64 keys, more than one lane of the combine holds.  The budget covers
+    the cache, so no block mask: with the mask on, 2048-row prefill chunks
+    meet near-ties at the budget boundary, where the GPU's and the oracle's
+    block scores (summed in different orders) can keep different blocks;
+    the selection itself is covered at the model shape above"""
+    torch, dev = torch_dev
+    case = (256, 4, 1, 64, 2, 64, 8192, 4, 8192, 0.25)
+    say(f"case: attention {case}")
+    run_calls(torch, dev, case, [2048, 2048, 2048, 50, 1, 1], seed=4)
+
+
 def test_dense_model_shape(torch_dev):
     torch, dev = torch_dev
     case = (2048, 16, 2, 128, 4, 128, 2048, 4, 2048, 0.25)
