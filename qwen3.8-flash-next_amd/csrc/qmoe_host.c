@@ -753,6 +753,13 @@ int qmoe_router(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n, float
         return -1;
     }
     float *xn = W->norm_w ? (xn_out ? xn_out : c->sc.xn) : NULL;
+    if (!logits_out && qk_route_mfma_ok(c->shape, n))
+        /* only the selection is asked for: MFMA logits, exact where they matter */
+        return hip_fail(err,
+                        qk_launch_route_mfma(W, c->shape, x, x_dtype == QMOE_BF16, n, c->sc.logits, xn,
+                                             c->sc.ahi, c->sc.ag, idx_out, w_out, shared_gate_out,
+                                             stream),
+                        "router");
     if (hip_fail(err, qk_launch_router(W, c->shape, x, x_dtype == QMOE_BF16, n, c->sc.logits, xn,
                                        stream),
                  "router"))
@@ -1028,7 +1035,14 @@ static int layer_core(const stage_env *e, const qmoe_layer_weights *W, int dec_f
                                  residual ? x : NULL, out, hyper, inject, hc, stream);
         return hip_fail(err, rc, "one-token layer");
     }
-    rc = qk_launch_router(W, s, x, xbf, n, sc->logits, xn, stream);
+    /* many tokens: router + top-k on MFMA with the exact logits of the
+     * candidates (the top-k launch below is then skipped) */
+    const int rfast = qk_route_mfma_ok(s, n);
+    if (rfast)
+        rc = qk_launch_route_mfma(W, s, x, xbf, n, sc->logits, xn, sc->ahi, sc->ag, sc->idx, sc->w,
+                                  sc->sg, stream);
+    else
+        rc = qk_launch_router(W, s, x, xbf, n, sc->logits, xn, stream);
     if (hip_fail(err, rc, "router")) return -1;
     const void *xf = W->norm_w ? (const void *)sc->xn : x;
     const int xf_bf = W->norm_w ? 0 : xbf;
@@ -1052,8 +1066,10 @@ static int layer_core(const stage_env *e, const qmoe_layer_weights *W, int dec_f
                                            sc->segtab, mfma_min_m(n), tasks, stream);
         if (hip_fail(err, rc, "topk+dispatch")) return -1;
     } else {
-        rc = qk_launch_topk(s, n, sc->logits, NULL, sc->idx, sc->w, sc->sg, stream);
-        if (hip_fail(err, rc, "topk")) return -1;
+        if (!rfast) {
+            rc = qk_launch_topk(s, n, sc->logits, NULL, sc->idx, sc->w, sc->sg, stream);
+            if (hip_fail(err, rc, "topk")) return -1;
+        }
         rc = qk_launch_dispatch(s, n, sc->idx, sc->offsets, sc->perm, sc->pos, sc->segtab,
                                 sc->bits, sc->wprefix, mfma_min_m(n), tasks, stream);
         if (hip_fail(err, rc, "dispatch")) return -1;
@@ -1801,7 +1817,12 @@ static int layer_forward_streamed(qmoe_ctx *c, int layer, const void *x, int xbf
     hipStream_t st = (hipStream_t)stream;
     int rc;
     float *xn = W->norm_w ? sc->xn : NULL;
-    rc = qk_launch_router(W, s, x, xbf, n, sc->logits, xn, stream);
+    const int rfast = qk_route_mfma_ok(s, n);
+    if (rfast)
+        rc = qk_launch_route_mfma(W, s, x, xbf, n, sc->logits, xn, sc->ahi, sc->ag, sc->idx, sc->w,
+                                  sc->sg, stream);
+    else
+        rc = qk_launch_router(W, s, x, xbf, n, sc->logits, xn, stream);
     if (hip_fail(err, rc, "router")) return -1;
     const void *xf = W->norm_w ? (const void *)sc->xn : x;
     const int xf_bf = W->norm_w ? 0 : xbf;
@@ -1811,8 +1832,10 @@ static int layer_forward_streamed(qmoe_ctx *c, int layer, const void *x, int xbf
                                            sc->segtab, 1, NULL, stream);
         if (hip_fail(err, rc, "topk+dispatch")) return -1;
     } else {
-        rc = qk_launch_topk(s, n, sc->logits, NULL, sc->idx, sc->w, sc->sg, stream);
-        if (hip_fail(err, rc, "topk")) return -1;
+        if (!rfast) {
+            rc = qk_launch_topk(s, n, sc->logits, NULL, sc->idx, sc->w, sc->sg, stream);
+            if (hip_fail(err, rc, "topk")) return -1;
+        }
         rc = qk_launch_dispatch(s, n, sc->idx, sc->offsets, sc->perm, sc->pos, sc->segtab, sc->bits,
                                 sc->wprefix, 1, NULL, stream);
         if (hip_fail(err, rc, "dispatch")) return -1;

@@ -94,6 +94,19 @@ void qh_hc_end(qmoe_ctx *c, int layer);
 int qk_launch_router(const qmoe_layer_weights *W, qk_shape s, const void *x, int x_bf16, int n,
                      float *logits, float *xn, void *stream);
 
+/* router + top-k + renorm + sigmoid for n >= QK_ROUTE_MFMA_MIN_N tokens
+ * (route_mfma.hip): logits on bf16 MFMA with an error bound per (token,
+ * expert), the exact logits recomputed for the experts whose bound reaches
+ * the token's top k; the same idx, w, sg (and xn) as qk_launch_router +
+ * qk_launch_topk.  logits [n, E+1] is scratch here (no exact logits are
+ * left in it); plane [n, H] bf16 and wn2 [E] are scratch.  qk_route_mfma_ok
+ * says whether the shape and n are supported. */
+#define QK_ROUTE_MFMA_MIN_N 256
+int qk_route_mfma_ok(qk_shape s, int n);
+int qk_launch_route_mfma(const qmoe_layer_weights *W, qk_shape s, const void *x, int x_bf16, int n,
+                         float *logits, float *xn, uint16_t *plane, float *wn2, int32_t *idx,
+                         float *w, float *sg, void *stream);
+
 /* top-k + renorm + sigmoid; copies the first E logit columns to logits_out
  * when non-NULL. */
 int qk_launch_topk(qk_shape s, int n, const float *logits, float *logits_out, int32_t *idx,

@@ -384,12 +384,12 @@ class MoeContext:
                                  ctypes.byref(err)), err, "qmoe_router")
         return dict(logits=logits, idx=idx, w=w, shared_gate=sg)
 
-    def router_norm(self, layer, x, stream=None):
+    def router_norm(self, layer, x, want_logits=True, stream=None):
         """router of a layer with a pre-router RMSNorm; also returns the normalised rows"""
         import torch
         n = x.shape[0]
         dev = x.device
-        logits = torch.empty((n, self.E), dtype=torch.float32, device=dev)
+        logits = torch.empty((n, self.E), dtype=torch.float32, device=dev) if want_logits else None
         idx = torch.empty((n, self.k), dtype=torch.int32, device=dev)
         w = torch.empty((n, self.k), dtype=torch.float32, device=dev)
         sg = torch.empty((n,), dtype=torch.float32, device=dev)
