@@ -741,6 +741,8 @@ extern "C" int qk_launch_dec_layer(const qmoe_layer_weights *W, qk_shape s, cons
     a.ra.x = x;
     a.ra.logits = logits;
     a.ra.xn = norm ? xn : nullptr;
+    a.ra.phi = a.ra.plo = nullptr;
+    a.ra.pg = nullptr;
     a.ra.H = s.H;
     a.ra.E = s.E;
     a.ra.n = 1;

@@ -815,8 +815,8 @@ static int mfma_usable(qk_shape s, int n, int stage) {
 static int mfma_min_m(int n) { return n >= QK_MFMA_ALL_N ? 1 : QK_MFMA_MIN_M; }
 
 static int run_gateup(const stage_env *e, const qmoe_layer_weights *W, const void *x, int xbf, int n,
-                      const int32_t *perm, const int32_t *segtab, int tasks_ready, float *h,
-                      void *stream, qmoe_err *err) {
+                      const int32_t *perm, const int32_t *segtab, int tasks_ready, int packed,
+                      float *h, void *stream, qmoe_err *err) {
     const qk_shape s = e->s;
     const qk_scratch *sc = e->sc;
     const int mm = mfma_usable(s, n, xbf ? 0 : 1);
@@ -829,8 +829,10 @@ static int run_gateup(const stage_env *e, const qmoe_layer_weights *W, const voi
             rc = qk_launch_mfma_tasks(s, n, segtab, min_m, sc->tasks, stream);
             if (hip_fail(err, rc, "mfma tasks")) return -1;
         }
-        rc = qk_launch_pack_rows(x, xbf, (size_t)n, s.H, sc->ahi, xbf ? NULL : sc->alo, sc->ag, stream);
-        if (hip_fail(err, rc, "pack x")) return -1;
+        if (!packed) {
+            rc = qk_launch_pack_rows(x, xbf, (size_t)n, s.H, sc->ahi, xbf ? NULL : sc->alo, sc->ag, stream);
+            if (hip_fail(err, rc, "pack x")) return -1;
+        }
     }
     if (mm && gemv && fork(e, stream, err)) return -1;
     if (gemv) {
@@ -928,7 +930,7 @@ int qmoe_expert_gateup(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n
     NEED(segments, "segments");
     NEED(h_out, "h_out");
     const stage_env e = ctx_env(c);
-    return run_gateup(&e, &c->layers[layer].dev, x, x_dtype == QMOE_BF16, n, perm, segments, 0, h_out,
+    return run_gateup(&e, &c->layers[layer].dev, x, x_dtype == QMOE_BF16, n, perm, segments, 0, 0, h_out,
                       stream, err);
 }
 
@@ -1035,17 +1037,23 @@ static int layer_core(const stage_env *e, const qmoe_layer_weights *W, int dec_f
                                  residual ? x : NULL, out, hyper, inject, hc, stream);
         return hip_fail(err, rc, "one-token layer");
     }
+    const void *xf = W->norm_w ? (const void *)sc->xn : x;
+    const int xf_bf = W->norm_w ? 0 : xbf;
     /* many tokens: router + top-k on MFMA with the exact logits of the
-     * candidates (the top-k launch below is then skipped) */
+     * candidates (the top-k launch below is then skipped); else, when the
+     * gate/up runs on MFMA and the tiled router takes n, the router also
+     * writes the gate/up's operand planes (no packing launch) */
     const int rfast = qk_route_mfma_ok(s, n);
+    const int rpack = !rfast && n >= 2 && mfma_usable(s, n, xf_bf ? 0 : 1) && qk_router_packs(s, n);
     if (rfast)
         rc = qk_launch_route_mfma(W, s, x, xbf, n, sc->logits, xn, sc->ahi, sc->ag, sc->idx, sc->w,
                                   sc->sg, stream);
+    else if (rpack)
+        rc = qk_launch_router_pack(W, s, x, xbf, n, sc->logits, xn, sc->ahi, xf_bf ? NULL : sc->alo,
+                                   sc->ag, stream);
     else
         rc = qk_launch_router(W, s, x, xbf, n, sc->logits, xn, stream);
     if (hip_fail(err, rc, "router")) return -1;
-    const void *xf = W->norm_w ? (const void *)sc->xn : x;
-    const int xf_bf = W->norm_w ? 0 : xbf;
     if (n == 1 && qk_gateup_topk_supported(s) && qk_down_combine_lds(s, n) > 0) {
         /* one token: top-k inside the gate/up launch, then down + combine */
         rc = qk_launch_gateup_topk(W, s, xf, xf_bf, sc->logits, sc->idx, sc->w, sc->sg, sc->perm,
@@ -1074,7 +1082,8 @@ static int layer_core(const stage_env *e, const qmoe_layer_weights *W, int dec_f
                                 sc->bits, sc->wprefix, mfma_min_m(n), tasks, stream);
         if (hip_fail(err, rc, "dispatch")) return -1;
     }
-    if (run_gateup(e, W, xf, xf_bf, n, sc->perm, sc->segtab, gu_mm, sc->h, stream, err)) return -1;
+    if (run_gateup(e, W, xf, xf_bf, n, sc->perm, sc->segtab, gu_mm, rpack, sc->h, stream, err))
+        return -1;
     if (!mfma_usable(s, n, 2) && qk_down_combine_lds(s, n) > 0) {
         rc = qk_launch_down_combine(W, s, sc->h, n, sc->segtab, sc->pos, sc->w, sc->sg,
                                     residual ? x : NULL, xbf, out, hyper, inject, hc, stream);
@@ -1788,7 +1797,7 @@ static int streamed_experts(qmoe_ctx *c, const qmoe_layer_weights *W, const void
     qk_scratch *sc = &c->sc;
     const stage_env e = ctx_env(c);
     const int gu_mm = n >= 2 && mfma_usable(s, n, xf_bf ? 0 : 1);
-    int rc = run_gateup(&e, W, xf, xf_bf, n, sc->perm, c->s_segtab, 0, sc->h, stream, err);
+    int rc = run_gateup(&e, W, xf, xf_bf, n, sc->perm, c->s_segtab, 0, 0, sc->h, stream, err);
     if (rc) return rc;
     if (!mfma_usable(s, n, 2) && qk_down_combine_lds(s, n) > 0)
         return hip_fail(err, qk_launch_down_combine(W, s, sc->h, n, c->s_segtab, sc->pos, sc->w, sc->sg,

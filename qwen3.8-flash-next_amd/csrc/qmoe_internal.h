@@ -93,6 +93,14 @@ void qh_hc_end(qmoe_ctx *c, int layer);
  * norm_w set, x is RMS-normalised first and written to xn (if non-NULL) */
 int qk_launch_router(const qmoe_layer_weights *W, qk_shape s, const void *x, int x_bf16, int n,
                      float *logits, float *xn, void *stream);
+/* qk_router_packs: n tokens take the tiled router, which can also write
+ * the MFMA gate/up operand planes of the experts' input (x, or the normed
+ * rows) as qk_launch_pack_rows would: qk_launch_router_pack with phi, pg
+ * (and plo for f32 or normed input) */
+int qk_router_packs(qk_shape s, int n);
+int qk_launch_router_pack(const qmoe_layer_weights *W, qk_shape s, const void *x, int x_bf16, int n,
+                          float *logits, float *xn, uint16_t *phi, uint16_t *plo, float *pg,
+                          void *stream);
 
 /* router + top-k + renorm + sigmoid for n >= QK_ROUTE_MFMA_MIN_N tokens
  * (route_mfma.hip): logits on bf16 MFMA with an error bound per (token,

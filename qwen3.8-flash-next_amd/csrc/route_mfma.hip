@@ -453,6 +453,8 @@ extern "C" int qk_launch_route_mfma(const qmoe_layer_weights *W, qk_shape s, con
     ra.x = x;
     ra.logits = logits;
     ra.xn = xn;
+    ra.phi = ra.plo = nullptr;
+    ra.pg = nullptr;
     ra.H = s.H;
     ra.E = s.E;
     ra.n = n;

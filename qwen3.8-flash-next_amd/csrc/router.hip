@@ -74,6 +74,37 @@ __global__ __launch_bounds__(256, 2) void k_router_tile(RouterArgs a, int rows_p
                 }
             }
         }
+        if (a.phi) {
+            /* the MFMA gate/up operand planes of the experts' input (x, or
+             * the normed rows), k_pack_rows' arithmetic: the 8 chunks of a
+             * 64-column group sit in lanes 8j..8j+7.  The token block's
+             * chunk sets i = 0..NCH-1 go to row slices i % slices, so no
+             * one workgroup carries them all */
+            const bool two = !XBF16 || NORM;
+#pragma unroll
+            for (int i = 0; i < NCH; i++) {
+                if ((int)blockIdx.y != i % (int)gridDim.y) continue;
+                uint32_t ph[4], pl[4];
+                float sg = 0.0f;
+                if (two) {
+                    qk_f32x8_to_pairs(v[t][i], ph, pl, sg);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; j++) ph[j] = qk_cvt_pk_bf16(v[t][i][j], v[t][i][j + 4]);
+#pragma unroll
+                    for (int j = 0; j < 4; j++) sg = qk_dot2(ph[j], QK_BF16_ONES, sg);
+                }
+                sg += qk_dpp<QK_DPP_XOR1>(sg);
+                sg += qk_dpp<QK_DPP_XOR2>(sg);
+                sg += __shfl_xor(sg, 4, QK_WAVE);
+                if (tb + t < a.n) {
+                    const size_t ci = (size_t)(tb + t) * (H / 8) + lane + 64 * i;
+                    ((uint4 *)a.phi)[ci] = make_uint4(ph[0], ph[1], ph[2], ph[3]);
+                    if (two) ((uint4 *)a.plo)[ci] = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+                    if ((lane & 7) == 0) a.pg[ci >> 3] = -128.0f * sg;
+                }
+            }
+        }
     }
 
     /* weight staging: stage row rr, 16-byte chunk q of the row, per thread
@@ -181,9 +212,26 @@ static int router_nch(int H) {
         }                                                                                      \
     } while (0)
 
+extern "C" int qk_router_packs(qk_shape s, int n) {
+    return n >= RTT_MIN_N && s.H % 512 == 0 && s.H <= 2048;
+}
+
+extern "C" int qk_launch_router_pack(const qmoe_layer_weights *W, qk_shape s, const void *x, int x_bf16,
+                                     int n, float *logits, float *xn, uint16_t *phi, uint16_t *plo,
+                                     float *pg, void *stream);
+
 extern "C" int qk_launch_router(const qmoe_layer_weights *W, qk_shape s, const void *x, int x_bf16,
                                 int n, float *logits, float *xn, void *stream) {
+    return qk_launch_router_pack(W, s, x, x_bf16, n, logits, xn, nullptr, nullptr, nullptr, stream);
+}
+
+extern "C" int qk_launch_router_pack(const qmoe_layer_weights *W, qk_shape s, const void *x, int x_bf16,
+                                     int n, float *logits, float *xn, uint16_t *phi, uint16_t *plo,
+                                     float *pg, void *stream) {
     if (n <= 0) return 0;
+    /* the planes come from the tiled router only; lo is there for f32 or normed input */
+    if (phi && (!qk_router_packs(s, n) || !pg || (!plo && (!x_bf16 || W->norm_w))))
+        return (int)hipErrorInvalidValue;
     RouterArgs a;
     a.router_w = W->router_w;
     a.router_bias = W->router_bias;
@@ -192,12 +240,15 @@ extern "C" int qk_launch_router(const qmoe_layer_weights *W, qk_shape s, const v
     a.x = x;
     a.logits = logits;
     a.xn = xn;
+    a.phi = phi;
+    a.plo = plo;
+    a.pg = pg;
     a.H = s.H;
     a.E = s.E;
     a.n = n;
     a.eps = s.eps;
     hipStream_t st = (hipStream_t)stream;
-    if (n >= RTT_MIN_N && s.H % 512 == 0 && s.H <= 2048) {
+    if (qk_router_packs(s, n)) {
         /* tiled: about two workgroups per CU, rows split into slices of whole stages */
         const int tblocks = (n + 4 * RTT_TOK - 1) / (4 * RTT_TOK);
         const int stages = (s.E + 1 + RTT_EB - 1) / RTT_EB;

@@ -24,6 +24,8 @@ struct RouterArgs {
     const void *x;
     float *logits; /* [n, E+1] */
     float *xn;     /* [n, H] or null */
+    uint16_t *phi, *plo; /* k_router_tile, or null: the MFMA gate/up operand planes of the */
+    float *pg;           /* experts' input ([n, H] each, lo null for bf16) and P [n, H/64] */
     int H, E, n;
     float eps;
 };

@@ -399,6 +399,38 @@ def test_stages_compose_to_layer(torch_dev, n, residual):
         assert torch.equal(out, full)
 
 
+@pytest.mark.parametrize("n,x_bf16,norm", [(16, True, False), (64, False, False), (64, True, True),
+                                          (200, False, True), (255, True, False)])
+def test_router_planes_compose_to_layer(torch_dev, n, x_bf16, norm):
+    """from 16 to 255 tokens the tiled router also writes the MFMA gate/up's
+    operand planes of the experts' input (x, or the normed rows), in place of
+    the packing launch: the layer's bits equal the stage chain's, whose
+    gate/up packs its own planes, for bf16 and f32 input, with and without
+    the pre-router norm"""
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    say(f"case: router planes, n={n} x_bf16={x_bf16} norm={norm}")
+    w = pkg.WORKLOADS["batched"]
+    rb = orc.zipf_bias(w.n_experts, w.zipf_s, w.zipf_scale, 3)
+    x = orc.gen_x(n, w.hidden, 7, bf16=x_bf16)
+    with pkg.MoeContext.for_workload(w, max_tokens=n) as ctx:
+        ctx.synth_layer(0, 2, with_norm=norm, router_bias=rb)
+        xt = to_dev(x, torch, dev)
+        full = ctx.layer_forward(0, xt)
+        if norm:
+            rt = ctx.router_norm(0, xt, want_logits=False)
+            xe = rt["xn"]
+        else:
+            rt = ctx.router(0, xt)
+            xe = xt
+        d = ctx.dispatch(rt["idx"])
+        h = ctx.expert_gateup(0, xe, d)
+        y = ctx.expert_down(0, h, n, d)
+        out = ctx.combine(y, d["perm"], rt["w"], rt["shared_gate"], n)
+        torch.cuda.synchronize()
+        assert torch.equal(out, full)
+
+
 def test_gateup_topk_one_token(torch_dev):
     """one-token launch that selects the top-k itself: same routing as the
     oracle (bit-exact ids, dispatch), and the same h as router -> dispatch ->
