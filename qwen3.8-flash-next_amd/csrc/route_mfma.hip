@@ -430,7 +430,8 @@ static int rt_pl(int E) {
 }
 
 extern "C" int qk_route_mfma_ok(qk_shape s, int n) {
-    return n >= QK_ROUTE_MFMA_MIN_N && s.H % 512 == 0 && s.H >= 512 && s.H <= 2048 && rt_pl(s.E) > 0 &&
+    /* instances for H = 512 * NCH, NCH = 1, 2, 4 */
+    return n >= QK_ROUTE_MFMA_MIN_N && (s.H == 512 || s.H == 1024 || s.H == 2048) && rt_pl(s.E) > 0 &&
            s.k >= 1 && s.k <= 64 && s.k <= s.E;
 }
 

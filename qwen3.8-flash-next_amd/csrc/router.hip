@@ -212,8 +212,10 @@ static int router_nch(int H) {
         }                                                                                      \
     } while (0)
 
+/* the tiled router is instantiated for H = 512 * NCH with NCH = 1, 2, 4
+ * (hidden 1536 is a multiple of 512 but has no instance: it takes k_router) */
 extern "C" int qk_router_packs(qk_shape s, int n) {
-    return n >= RTT_MIN_N && s.H % 512 == 0 && s.H <= 2048;
+    return n >= RTT_MIN_N && (s.H == 512 || s.H == 1024 || s.H == 2048);
 }
 
 extern "C" int qk_launch_router_pack(const qmoe_layer_weights *W, qk_shape s, const void *x, int x_bf16,

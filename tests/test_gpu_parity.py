@@ -537,6 +537,31 @@ def test_limits_k64_e1024_small_dims(torch_dev):
         assert_out_close(out.cpu().numpy(), ref["out"], "limits")
 
 
+@pytest.mark.parametrize("n,x_bf16,norm", [(1, True, False), (1, False, True), (37, True, True),
+                                          (300, False, False)])
+def test_fallback_shape_at_scale(torch_dev, n, x_bf16, norm):
+    """hidden 1536 (3 * 512) takes none of the routers' and the one-token
+    fast paths: not the one-token gate/up with top-k nor the one-launch layer
+    (H/32 is not a power of two), not the tiled or the MFMA router (their
+    instances are for hidden 512, 1024, 2048; both once took 1536 and read
+    its rows with the 2048 stride); the grouped GEMMs take it on MFMA.
+    Routing against the oracle on every token, every output row within
+    2e-2 / 1e-3, up to 300 tokens"""
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    H, E, k, I = 1536, 128, 8, 512
+    say(f"case: fallback shape H={H} E={E} k={k} I={I} n={n} x_bf16={x_bf16} norm={norm}")
+    L = orc.Layer(H, E, k, I, seed=11, with_norm=norm)
+    x = orc.gen_x(n, H, 23 + n, bf16=x_bf16)
+    ref = L.forward(x, x_bf16)
+    with pkg.MoeContext(H, E, k, I, max_tokens=n) as ctx:
+        ctx.upload_layer(0, L.arrays())
+        out = ctx.layer_forward(0, to_dev(x, torch, dev))
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(ctx.last_routing(n)["idx"].cpu().numpy(), ref["idx"])
+        assert_out_close(out.cpu().numpy(), ref["out"], "fallback shape")
+
+
 def test_empty_and_errors(torch_dev):
     torch, dev = torch_dev
     pkg = load_pkg()
