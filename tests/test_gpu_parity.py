@@ -562,6 +562,46 @@ def test_fallback_shape_at_scale(torch_dev, n, x_bf16, norm):
         assert_out_close(out.cpu().numpy(), ref["out"], "fallback shape")
 
 
+# (H, E, k, I, n, x_bf16, norm): hidden and intermediate sizes off the
+# powers of two (every multiple of 64 is a valid configuration), odd expert
+# counts, top-1 and top-16, and token counts on both sides of each path's
+# threshold (1 token, the GEMV and mixed MFMA stages, the tiled router from
+# 16, every segment on MFMA from 64, the MFMA router from 256)
+SWEEP = [
+    (768, 60, 6, 320, 1, True, False),
+    (768, 60, 6, 320, 70, False, True),
+    (3072, 96, 4, 512, 1, False, False),
+    (3072, 96, 4, 512, 33, True, False),
+    (4096, 64, 2, 768, 1, True, True),
+    (4096, 64, 2, 768, 20, False, False),
+    (1024, 512, 10, 256, 260, True, False),
+    (1024, 512, 10, 256, 5, False, True),
+    (512, 8, 1, 1024, 300, False, False),
+    (2048, 40, 3, 192, 17, True, True),
+    (2048, 1024, 16, 128, 64, True, False),
+    (1280, 130, 5, 640, 90, False, False),
+]
+
+
+@pytest.mark.parametrize("H,E,k,I,n,x_bf16,norm", SWEEP)
+def test_shape_sweep(torch_dev, H, E, k, I, n, x_bf16, norm):
+    """any valid configuration gives the oracle's routing on every token and
+    every output row within 2e-2 / 1e-3, whichever kernels its shape and
+    token count select"""
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    say(f"case: sweep H={H} E={E} k={k} I={I} n={n} x_bf16={x_bf16} norm={norm}")
+    L = orc.Layer(H, E, k, I, seed=H + E + k, with_norm=norm)
+    x = orc.gen_x(n, H, 31 + n, bf16=x_bf16)
+    ref = L.forward(x, x_bf16)
+    with pkg.MoeContext(H, E, k, I, max_tokens=n) as ctx:
+        ctx.upload_layer(0, L.arrays())
+        out = ctx.layer_forward(0, to_dev(x, torch, dev))
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(ctx.last_routing(n)["idx"].cpu().numpy(), ref["idx"])
+        assert_out_close(out.cpu().numpy(), ref["out"], "sweep")
+
+
 def test_empty_and_errors(torch_dev):
     torch, dev = torch_dev
     pkg = load_pkg()
