@@ -473,7 +473,7 @@ typedef struct {
     int n_k_heads;   /* hk: linear_num_key_heads */
     int n_v_heads;   /* hv: linear_num_value_heads, a multiple of hk */
     int k_head_dim;  /* dk: 32, 64, 128 or 256 */
-    int v_head_dim;  /* dv: a power of two from 32 to 2048; hv*dv <= 8192 */
+    int v_head_dim;  /* dv: a power of two from 32 to 2048; hv*dv a multiple of 64, <= 8192 */
     int conv_kernel; /* linear_conv_kernel_dim, 1..16 */
     int group_size;  /* must be 64 */
     int n_layers;

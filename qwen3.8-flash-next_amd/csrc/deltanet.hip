@@ -381,7 +381,8 @@ extern "C" int qk_dn_shape_ok(const qk_dn_shape *s) {
     if (!(s->dv == 32 || s->dv == 64 || s->dv == 128 || s->dv == 256 || s->dv == 512 ||
           s->dv == 1024 || s->dv == 2048))
         return 0;
-    if (value_dim > 8192) return 0;
+    /* out_proj takes value_dim inputs in q4 groups of 64 */
+    if (value_dim > 8192 || value_dim % 64) return 0;
     if (s->kc < 1 || s->kc > 16) return 0;
     if (conv_dim <= 0) return 0;
     return 1;

@@ -69,7 +69,7 @@ int qmoe_dn_create(qmoe_dn_ctx **out, const qmoe_dn_config *cfg, qmoe_err *err) 
     if (cfg->group_size != 64 || !qk_dn_shape_ok(&s)) {
         dn_set_err(err, "DeltaNet shape unsupported: hidden %d (multiple of 64, <= 8192), heads %d/%d "
                         "(value heads a multiple of key heads), k_head_dim %d (32, 64, 128, 256), "
-                        "v_head_dim %d (a power of two, 32..2048; heads*dim <= 8192), "
+                        "v_head_dim %d (a power of two, 32..2048; heads*dim a multiple of 64, <= 8192), "
                         "conv_kernel %d (1..16), group_size %d (64)",
                    cfg->hidden, cfg->n_k_heads, cfg->n_v_heads, cfg->k_head_dim, cfg->v_head_dim,
                    cfg->conv_kernel, cfg->group_size);

@@ -120,6 +120,27 @@ def test_wide_head_shapes(torch_dev, case):
     run_calls(torch, dev, case, [1, 3, 1, 40, 1, 5, 1])
 
 
+IRREGULAR_CASES = [
+    # hidden 320, 5 query heads on 1 kv head, indexer 3 heads of 68, budget
+    # 12 keys in blocks of 3, full rotary
+    (320, 5, 1, 64, 3, 68, 12, 3, 96, 1.0),
+    # hidden 448, 6 heads on 3 kv heads of 192, compress 1 (every key its own block)
+    (448, 6, 3, 192, 1, 64, 20, 1, 80, 0.25),
+    # hidden 640, 4 heads of 128 on 2 kv heads, indexer 2 heads of 36, blocks of 5
+    (640, 4, 2, 128, 2, 36, 25, 5, 120, 0.25),
+]
+
+
+@pytest.mark.parametrize("case", IRREGULAR_CASES)
+def test_irregular_shapes(torch_dev, case):
+    """valid shapes off the usual ones (odd head counts and hidden sizes,
+    head dim 192, indexer dims 36 and 68, compress 1, 3 and 5, full rotary):
+    one-token calls and chunks, the block mask switching on past the budget"""
+    torch, dev = torch_dev
+    say(f"case: attention irregular {case}")
+    run_calls(torch, dev, case, [1, 4, 1, 17, 1, 30, 1, 2])
+
+
 def test_long_cache_decode(torch_dev):
     """6,000+ cached keys: one-token calls split the cache into ~97 chunks
     of 64 keys, more than one lane of the combine holds.  The budget covers

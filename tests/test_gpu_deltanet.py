@@ -123,6 +123,17 @@ def test_other_shapes_seeded_state(torch_dev, shape):
     run_steps(torch, dev, shape, [1, 3, 1], seed=3, seed_state=True)
 
 
+@pytest.mark.parametrize("shape", [(320, 1, 2, 32, 32, 7), (448, 3, 6, 64, 256, 5),
+                                   (1536, 2, 4, 256, 512, 16), (640, 5, 5, 128, 1024, 2)])
+def test_irregular_shapes(torch_dev, shape):
+    """valid shapes off the usual ones: hidden 320 / 448 / 640 / 1536, odd
+    head counts, value heads 1x to 2x the key heads, value dims 32 to 1024,
+    conv kernels 2 to 16; one-token calls and chunks of 2, 9 and 17"""
+    torch, dev = torch_dev
+    say(f"case: DeltaNet irregular shape {shape}")
+    run_steps(torch, dev, shape, [1, 2, 1, 9, 1, 17, 1], seed=5)
+
+
 def test_tokens_at_once_equal_one_by_one(torch_dev):
     torch, dev = torch_dev
     pkg = load_pkg()
@@ -184,8 +195,9 @@ def test_graph_replay_and_reset(torch_dev):
 def test_errors(torch_dev):
     torch, dev = torch_dev
     pkg = load_pkg()
+    # the last: value_dim 3*32 = 96 is not a multiple of out_proj's q4 group of 64
     for bad in [(100, 1, 1, 64, 64, 4), (256, 2, 3, 64, 64, 4), (256, 1, 1, 48, 64, 4),
-                (256, 1, 1, 64, 8, 4), (256, 1, 1, 64, 64, 0)]:
+                (256, 1, 1, 64, 8, 4), (256, 1, 1, 64, 64, 0), (320, 1, 3, 32, 32, 7)]:
         with pytest.raises(pkg.QmoeError, match="DeltaNet shape unsupported"):
             pkg.DeltaNetContext(*bad)
     with pkg.DeltaNetContext(256, 2, 4, 64, 64, 4, n_layers=1, max_tokens=2) as ctx:
