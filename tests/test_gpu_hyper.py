@@ -132,6 +132,22 @@ def test_decode_shape_hyper_layer(torch_dev, n):
     _case(torch, dev, DECODE, n, seed=7, n_check=6)
 
 
+@pytest.mark.parametrize("shp,n", [
+    (dict(H=768, E=16, k=2, I=128, hc=3, R=192), 1),
+    (dict(H=768, E=16, k=2, I=128, hc=3, R=192), 20),
+    (dict(H=512, E=8, k=1, I=64, hc=1, R=64), 5),
+    (dict(H=1536, E=32, k=4, I=256, hc=8, R=512), 70),
+    (dict(H=2048, E=64, k=4, I=128, hc=2, R=2048), 17),
+])
+def test_hyper_shape_sweep(torch_dev, shp, n):
+    """copy counts 1 to 8, ranks 64 to 2048, hidden 512 to 2048 (1536 =
+    3 * 512 included): mix, layer and update against the oracle on both the
+    GEMV (few tokens) and the MFMA (16 and more) paths"""
+    torch, dev = torch_dev
+    say(f"case: hyper sweep {shp} n={n}")
+    _case(torch, dev, shp, n, seed=9, n_check=n)
+
+
 def test_prefill_hyper_layer(torch_dev):
     torch, dev = torch_dev
     say("case: decode-shape hyper layer n=4096 (16 tokens checked)")
