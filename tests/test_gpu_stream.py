@@ -93,6 +93,25 @@ def test_decode_shape_streamed_with_prefetch(torch_dev):
     stm.close()
 
 
+@pytest.mark.parametrize("prefetch,n", [(4, 1), (0, 70), (-1, 70)])
+def test_odd_shape_streamed(torch_dev, prefetch, n):
+    """hidden 768, 60 experts top-6, intermediate 320: streamed layers (host-
+    and device-resolved) equal the resident ones bit for bit: one token with
+    12 slots (evicting), and 70 tokens on the MFMA path with every expert's
+    slot"""
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    slots = 12 if n == 1 else 60
+    say(f"case: odd shape streamed, {slots} slots of 60 experts, prefetch {prefetch}, n={n}")
+    res, stm = _pair(pkg, 768, 60, 6, 320, 2, n, slots, 2, prefetch, seed=8, zipf=1.1)
+    _run_sequence(torch, dev, res, stm, 2, 6, n, 768, n == 1, seed=70)
+    st = stm.stream_stats()
+    say(f"stats {st}")
+    assert st["hits"] + st["misses"] > 0
+    res.close()
+    stm.close()
+
+
 @pytest.mark.parametrize("prefetch", [0, -1])
 def test_batched_streamed_mfma_path(torch_dev, prefetch):
     """64 tokens route to up to 512 experts: every slot in use, segments

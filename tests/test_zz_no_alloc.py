@@ -57,7 +57,8 @@ def device_weights(pkg, ctx):
     return w
 
 
-SHAPES = {"tiny": (256, 8, 2, 128), "model": (2048, 512, 10, 512)}
+SHAPES = {"tiny": (256, 8, 2, 128), "model": (2048, 512, 10, 512),
+          "odd": (768, 60, 6, 320)}
 
 
 @pytest.mark.parametrize("shape,with_norm,calls", [
@@ -66,6 +67,7 @@ SHAPES = {"tiny": (256, 8, 2, 128), "model": (2048, 512, 10, 512)}
     ("tiny", True, [(64, True, 0), (1, False, 0)]),
     ("model", False, [(300, False, 0), (1, False, 0)]),
     ("model", False, [(64, True, 1), (16, False, 0)]),
+    ("odd", True, [(90, False, 1), (1, True, 0)]),
 ])
 def test_noalloc_matches_layer_forward(torch_dev, shape, with_norm, calls):
     torch, dev = torch_dev
