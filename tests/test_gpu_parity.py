@@ -521,6 +521,53 @@ def test_ties_go_to_lower_expert_id(torch_dev):
     assert ties > 0
 
 
+def test_ties_one_token_decode_shape(torch_dev):
+    """exact ties at the decode shape through the one-token path (the top-k
+    inside the gate/up launch, 8 experts per lane): for each of six tokens
+    its top expert's router row is copied to a second expert (some above,
+    some below it in id), so the two tie for the top; one-token calls must
+    select the oracle's experts in its order (ties to the lower id), and the
+    routing writer's dispatch order must be the sorted ids"""
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    import ctypes
+    w = pkg.WORKLOADS["decode"]
+    H, E, k = w.hidden, w.n_experts, w.top_k
+    say("case: exact ties, one-token calls at the decode shape")
+    L = orc.Layer(H, E, k, w.moe_inter, seed=w.seed, only_experts=[])
+    x = orc.gen_x(6, H, 77, bf16=True)
+    r0 = L.route(x, True)
+    rw = L.t["router_w"].reshape(E, H).copy()
+    used = set(int(v) for v in r0["idx"].reshape(-1))
+    pairs = []
+    for t in range(6):
+        a = int(r0["idx"][t, 0])
+        b = (a + 37 * (t + 1) * (1 if t % 2 else -1)) % E
+        while b in used:
+            b = (b + 1) % E
+        used.add(b)
+        rw[b] = rw[a]
+        pairs.append((a, b))
+    L.t["router_w"] = rw.reshape(-1)
+    L._build()
+    ref = L.route(x, True)
+    assert all(int(ref["idx"][t, 0]) == min(pairs[t]) and int(ref["idx"][t, 1]) == max(pairs[t])
+               for t in range(6)), (pairs, ref["idx"][:, :2])
+    hip = ctypes.CDLL("libamdhip64.so")
+    with pkg.MoeContext.for_workload(w, max_tokens=1, n_layers=1) as ctx:
+        ctx.synth_layer(0, w.seed)
+        rp = ctx.device_weights(0)["router_w"]
+        for a, b in pairs:  # the same row copies on the device (device to device)
+            assert hip.hipMemcpy(ctypes.c_void_p(rp + b * H * 2), ctypes.c_void_p(rp + a * H * 2),
+                                 ctypes.c_size_t(H * 2), 3) == 0
+        for t in range(6):
+            ctx.layer_forward(0, to_dev(x[t:t + 1], torch, dev))
+            torch.cuda.synchronize()
+            lr = ctx.last_routing(1)
+            np.testing.assert_array_equal(lr["idx"].cpu().numpy()[0], ref["idx"][t])
+            np.testing.assert_array_equal(lr["perm"].cpu().numpy(), np.argsort(ref["idx"][t], kind="stable"))
+
+
 def test_limits_k64_e1024_small_dims(torch_dev):
     torch, dev = torch_dev
     pkg = load_pkg()
