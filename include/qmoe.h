@@ -535,8 +535,11 @@ int qmoe_dn_state(qmoe_dn_ctx *ctx, int layer, float **conv_state, float **rec_s
  * kv_cap is refused (the reference drops the oldest rows of its v and
  * indexer caches there but not of its k cache, model.c:815-821, 862-867,
  * 921; that is not reproduced).  Block selection ties go to the lower
- * block (the reference's quickselect leaves their order open).  Sums run
- * in parallel orders: outputs agree with the reference to rounding.
+ * block (the reference's quickselect leaves their order open).  The
+ * indexer path runs in the reference's sequential orders (index_qk_proj in
+ * the router's fixed R64 order), so block scores and kept blocks equal the
+ * C restatement's bit for bit; attention sums run in parallel orders and
+ * agree with the reference to rounding.
  * Weights use the checkpoint layout (names model.c:1833-1850). */
 typedef struct qmoe_attn_ctx qmoe_attn_ctx;
 
@@ -555,7 +558,12 @@ typedef struct {
     float rope_theta;
     int n_layers;
     int max_tokens;
+    int max_position;  /* positions offset + t stay below max(max_position, kv_cap); 0: kv_cap.
+                        * The RoPE table (cos, sin per position) is computed on the host at
+                        * create with the reference's formula; at most QMOE_ATTN_MAX_POSITION */
 } qmoe_attn_config;
+
+#define QMOE_ATTN_MAX_POSITION (1 << 20)
 
 typedef struct {
     const uint32_t *q_q;  /* [2*h*hd, d/8]   q_proj.weight (q | gate per head) */
@@ -587,6 +595,18 @@ int qmoe_attn_forward(qmoe_attn_ctx *ctx, int layer, const float *x, int n, int 
  * keys [kv_cap, idx_hd]) and their current length */
 int qmoe_attn_cache(qmoe_attn_ctx *ctx, int layer, float **k_cache, float **v_cache, float **idx_keys,
                     int *len, qmoe_err *err);
+/* device addresses of the QSA indexer's state, for inspection (the values
+ * the reference computes inside attention_forward, model.c:955-1075): the
+ * layer's pooled, normed and rotated block keys [kv_cap/idx_compress,
+ * idx_hd] (block b valid once the cache holds (b+1)*idx_compress rows),
+ * and, for the context's last forward call that ran the block mask, the
+ * kept-block bitmap [n, keep_words] u32 (bit b%32 of word b/32; keep_words
+ * = ceil(blocks of that call / 32)) and the
+ * block scores as order keys [n, score_ld] u32 (bits of a float s >= 0:
+ * bits | 0x80000000; s < 0: ~bits).  Read them after the call completes
+ * on its stream and before the context's next call. */
+int qmoe_attn_index_state(qmoe_attn_ctx *ctx, int layer, float **pooled, uint32_t **keep, int *keep_words,
+                          uint32_t **score_keys, int *score_ld, qmoe_err *err);
 
 /* ------------------------------------------------- gated residual slots
  * gated_residual (c/src/model.c:728-796) on its own, for the two hyper

@@ -5,8 +5,8 @@
  * nothing in the product links it.
  *
  * Followed step by step, with the arithmetic of model.c and kernel.c:
- *   qk = x.idx_w^T (gemm_bf16); its raw key row appended to the indexer key
- *   cache                                                model.c:807-843
+ *   qk = x.idx_w^T (gemm_bf16, here in the router's R64 order); its raw key
+ *   row appended to the indexer key cache                model.c:807-843
  *   q (+ gate, interleaved per head), k, v = q4 projections;
  *   v appended to its cache                              model.c:847-869
  *   per-head rmsnorm(q_norm / k_norm) then partial RoPE at positions
@@ -16,8 +16,9 @@
  *   past the indexer budget: mean-pooled key blocks (rmsnorm, RoPE at the
  *   block start), per-token indexer queries (rmsnorm, RoPE), block scores
  *   sum_heads sum_i relu(q_i p_i) / sqrt(idx_hd), invisible blocks -inf,
- *   top budget/compress blocks (kernel_topk_indices), keys outside the kept
- *   blocks and the own tail masked                       model.c:969-1104
+ *   top budget/compress blocks (kernel_topk_indices; exact ties at the
+ *   k-th score to the lower block), keys outside the kept blocks and the
+ *   own tail masked                                      model.c:969-1104
  *   softmax, weighted sum of v, * sigmoid(gate), o_proj   model.c:1107-1143
  * Multiply-adds of the form acc += a*b are fma chains (the convention of
  * moe_oracle.c); the ReLU products of the block scores are not contracted.
@@ -48,6 +49,11 @@ static void rope_row(float *x, int n, int d, const float *cs, const float *sn) {
 
 int orc_attn_forward(const orc_attn *A, orc_attn_state *S, const float *x, int n, int offset,
                      float *out) {
+    return orc_attn_forward_dbg(A, S, x, n, offset, out, NULL);
+}
+
+int orc_attn_forward_dbg(const orc_attn *A, orc_attn_state *S, const float *x, int n, int offset,
+                         float *out, const orc_attn_dbg *dbg) {
     const int d = A->hidden, h = A->n_heads, kvh = A->n_kv_heads, hd = A->head_dim;
     const int ih = A->idx_heads, ihd = A->idx_head_dim, cap = A->kv_cap, gs = A->group_size;
     const int idx_out = ih * ihd, qkw = idx_out + ihd;
@@ -69,7 +75,11 @@ int orc_attn_forward(const orc_attn *A, orc_attn_state *S, const float *x, int n
     float *inv = (float *)malloc((size_t)(rot / 2 + 1) * sizeof(float));
     if (!qk || !qbuf || !kbuf || !vbuf || !qn || !kn || !ao || !rc || !rs || !inv) return -1;
 
-    orc_gemm_bf16(n, qkw, d, x, A->idx_w, qk);
+    /* index_qk_proj in the router's fixed R64 order (the reference's
+     * gemm_bf16 leaves its order to BNNS) */
+    for (int t = 0; t < n; t++)
+        for (int r = 0; r < qkw; r++)
+            qk[(size_t)t * qkw + r] = orc_dot_r64_bf16w(x + (size_t)t * d, A->idx_w + (size_t)r * d, d);
     for (int t = 0; t < n; t++)
         memcpy(S->idx_keys + (size_t)(S->idx_len + t) * ihd, qk + (size_t)t * qkw + idx_out,
                (size_t)ihd * sizeof(float));
@@ -136,6 +146,7 @@ int orc_attn_forward(const orc_attn *A, orc_attn_state *S, const float *x, int n
             rope_row(pooled + (size_t)b * ihd, ihd, rot, bc, bs);
         }
         free(tmp);
+        if (dbg && dbg->pooled) memcpy(dbg->pooled, pooled, (size_t)n_blocks * ihd * sizeof(float));
     }
     for (int t = 0; t < n; t++) {
         if (use_idx) {
@@ -144,6 +155,7 @@ int orc_attn_forward(const orc_attn *A, orc_attn_state *S, const float *x, int n
                 rmsnorm_w(qk + (size_t)t * qkw + (size_t)hh * ihd, A->idx_q_norm, ihd, qs + (size_t)hh * ihd);
                 rope_row(qs + (size_t)hh * ihd, ihd, rot, c, s);
             }
+            if (dbg && dbg->qs) memcpy(dbg->qs + (size_t)t * ih * ihd, qs, (size_t)ih * ihd * sizeof(float));
             for (int b = 0; b < n_blocks; b++) {
                 float acc = 0.0f;
                 const float *pb = pooled + (size_t)b * ihd;
@@ -158,9 +170,28 @@ int orc_attn_forward(const orc_attn *A, orc_attn_state *S, const float *x, int n
                 bsc[b] = acc / sqrtf((float)ihd);
                 if ((long long)b * comp + comp - 1 > (long long)offset + t) bsc[b] = -INFINITY;
             }
+            /* kernel_topk_indices (quickselect) fixes the k-th largest
+             * score T; the blocks above T are kept whichever way it
+             * partitions, and among the blocks equal to T (exact ties,
+             * -inf ones included) the lowest ids are kept: the canonical
+             * tie rule, where the reference's choice depends on its
+             * partitioning order */
             orc_topk_quickselect(bsc, n_blocks, btop, top);
             memset(keep_blk, 0, (size_t)n_blocks);
-            for (int b = 0; b < (btop < n_blocks ? btop : n_blocks); b++) keep_blk[top[b]] = 1;
+            if (btop >= n_blocks) {
+                memset(keep_blk, 1, (size_t)n_blocks);
+            } else if (btop > 0) {
+                float T = bsc[top[0]] + 0.0f;
+                for (int j = 1; j < btop; j++)
+                    if (bsc[top[j]] + 0.0f < T) T = bsc[top[j]] + 0.0f;
+                int kept = 0;
+                for (int b = 0; b < n_blocks; b++)
+                    if (bsc[b] + 0.0f > T) keep_blk[b] = 1, kept++;
+                for (int b = 0; b < n_blocks && kept < btop; b++)
+                    if (bsc[b] + 0.0f == T) keep_blk[b] = 1, kept++;
+            }
+            if (dbg && dbg->scores) memcpy(dbg->scores + (size_t)t * n_blocks, bsc, (size_t)n_blocks * sizeof(float));
+            if (dbg && dbg->keep) memcpy(dbg->keep + (size_t)t * n_blocks, keep_blk, (size_t)n_blocks);
         }
         for (int hh = 0; hh < h; hh++) {
             const int kh = hh % kvh;

@@ -262,6 +262,17 @@ typedef struct {
  * -2 when the call would pass the cache capacity */
 int orc_attn_forward(const orc_attn *A, orc_attn_state *S, const float *x, int n, int offset,
                      float *out);
+/* optional copies of the indexer's intermediate values, written when the
+ * call runs the block mask (n_blocks = cached keys / compress after the
+ * call): the pooled keys [n_blocks, idx_hd], each token's normed and
+ * rotated queries [n, idx_heads*idx_hd], block scores [n, n_blocks] and
+ * kept-block flags [n, n_blocks] (1 = among the top budget/compress) */
+typedef struct {
+    float *pooled, *qs, *scores;
+    unsigned char *keep;
+} orc_attn_dbg;
+int orc_attn_forward_dbg(const orc_attn *A, orc_attn_state *S, const float *x, int n, int offset,
+                         float *out, const orc_attn_dbg *dbg);
 
 #ifdef __cplusplus
 }

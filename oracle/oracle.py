@@ -88,6 +88,10 @@ class OrcAttnState(ctypes.Structure):
     _fields_ = [("k_cache", _P), ("v_cache", _P), ("idx_keys", _P), ("kv_len", _I), ("idx_len", _I)]
 
 
+class OrcAttnDbg(ctypes.Structure):
+    _fields_ = [("pooled", _P), ("qs", _P), ("scores", _P), ("keep", _P)]
+
+
 class OrcOpts(ctypes.Structure):
     _fields_ = [("x_is_bf16", _I), ("residual", _I), ("routed_mode", _I), ("n_threads", _I)]
 
@@ -127,6 +131,8 @@ _SIG = {
     "orc_gen_codes": (None, [_P, _SZ, _U64, _U64]),
     "orc_zipf_bias": (None, [_P, _I, ctypes.c_double, ctypes.c_double, _U64]),
     "orc_attn_forward": (_I, [ctypes.POINTER(OrcAttn), ctypes.POINTER(OrcAttnState), _P, _I, _I, _P]),
+    "orc_attn_forward_dbg": (_I, [ctypes.POINTER(OrcAttn), ctypes.POINTER(OrcAttnState), _P, _I, _I, _P,
+                                  ctypes.POINTER(OrcAttnDbg)]),
     "orc_dn_decay": (_F, [_F, _F, _F]),
     "orc_dn_forward": (_I, [ctypes.POINTER(OrcDn), _P, _I, _P, _P, _P, _P]),
     "orc_time_forward": (ctypes.c_double, [ctypes.POINTER(OrcLayer), _P, _I, _P,
@@ -596,19 +602,33 @@ class Attention:
     def new_state(self):
         return Attention.State(self)
 
-    def forward(self, x, state, offset):
-        """x [n, d] f32 at positions offset..offset+n-1 -> out [n, d]; appends to state"""
+    def forward(self, x, state, offset, dbg=False):
+        """x [n, d] f32 at positions offset..offset+n-1 -> out [n, d]; appends to state.
+        With dbg, returns (out, d) where d holds the indexer's pooled keys
+        [nb, ihd], queries [n, ih*ihd], block scores and kept flags [n, nb]
+        when the call runs the block mask (else an empty dict)."""
         x = np.ascontiguousarray(x, dtype=np.float32)
         n = x.shape[0]
         out = np.empty((n, self.d), np.float32)
         S = OrcAttnState(_p(state.k), _p(state.v), _p(state.idx), state.len, state.len)
-        rc = lib().orc_attn_forward(ctypes.byref(self.st), ctypes.byref(S), _p(x), n, offset, _p(out))
+        kv = state.len + n
+        extra = {}
+        D = None
+        if dbg and kv > self.budget:
+            nb = kv // self.compress
+            extra = {"pooled": np.zeros((nb, self.ihd), np.float32),
+                     "qs": np.zeros((n, self.ih * self.ihd), np.float32),
+                     "scores": np.zeros((n, nb), np.float32),
+                     "keep": np.zeros((n, nb), np.uint8)}
+            D = OrcAttnDbg(*(_p(extra[k]) for k in ("pooled", "qs", "scores", "keep")))
+        rc = lib().orc_attn_forward_dbg(ctypes.byref(self.st), ctypes.byref(S), _p(x), n, offset, _p(out),
+                                        ctypes.byref(D) if D is not None else None)
         if rc == -2:
             raise ValueError("the call passes the cache capacity")
         if rc:
             raise MemoryError("orc_attn_forward")
         state.len = S.kv_len
-        return out
+        return (out, extra) if dbg else out
 
 
 def gen_attn_x(n, d, seed, layer=0, std=1.0):

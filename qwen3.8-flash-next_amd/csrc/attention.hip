@@ -9,16 +9,16 @@
  *             o_proj at the end.
  *   k_at_qk   one wave per (token, head): rmsnorm with q_norm / k_norm /
  *             the indexer's q norm, then partial RoPE at position offset+t
- *             (kernel.c:80-93); k, v and the indexer's raw key go into their
- *             caches at rows len0 + t.
+ *             (kernel.c:80-93) from the host's cos / sin table; k, v and
+ *             the indexer's raw key go into their caches at rows len0 + t.
  *   k_at_pool one wave per key block completed by the call: the block's
  *             mean-pooled indexer key, rmsnorm + RoPE at the block start,
  *             kept in HBM with the layer (a pooled key depends only on its
  *             block's cached keys, so the reference's per-call recomputation
  *             gives the same values).
- *   k_at_score (past the indexer budget) one wave per (token, block): score
- *             sum_heads sum_i relu(q_i p_i) / sqrt(ihd), invisible blocks
- *             -inf, as order keys.
+ *   k_at_score (past the indexer budget) one workgroup per (token, 32
+ *             blocks): score sum_heads sum_i relu(q_i p_i) / sqrt(ihd),
+ *             invisible blocks -inf, as order keys.
  *   k_at_sel  one workgroup per token: the top budget/compress blocks (value
  *             descending, ties to the lower block) by an 8-bit radix select
  *             -> a bitmap of kept blocks.
@@ -29,7 +29,11 @@
  *             exp-weighted v per head.
  *   k_at_comb one wave per (token, head): the chunks merged (max, rescaled
  *             sums), times sigmoid(gate).
- * Sums run in parallel orders: outputs match the reference to rounding.
+ * The indexer path (index_qk_proj in the router's R64 order, rmsnorm sums
+ * in index order, the table's cos / sin, the block scores in the
+ * reference's order) has the oracle's bits, so the kept blocks are the
+ * oracle's; the attention sums run in parallel orders and match the
+ * reference to rounding.
  */
 #include "qk_device.h"
 #include "gemv_parts.h"
@@ -99,33 +103,41 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
         }
         return;
     }
+    /* bf16 rows (index_qk_proj): f32 x times the bf16 weights in the
+     * router's R64 order -- 8-element chunk c on lane c % 64, an fma chain
+     * per lane over its chunks in ascending order from +0, the lanes added
+     * by qk_group_sum<64> -- so the indexer's keys and queries have the
+     * oracle's bits (the block selection downstream compares them) */
+    const int C8 = a.K >> 3;
     for (int t = 0; t < a.n; t++) {
-        XRaw<P, false> xr;
-        load_xraw<64, P, false>(a.x, (size_t)t, a.K, lane, xr);
-        XPairs<64, P, false> xp;
-        convert_xraw<64, P, false>(xr, a.K, lane, xp);
+        float acc[AT_RPW];
+#pragma unroll
+        for (int j = 0; j < AT_RPW; j++) acc[j] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4 * P; i++) {
+            const int c0 = lane + 64 * i;
+            const bool ok = c0 < C8;
+            const int c = ok ? c0 : 0;
+            const float4 *xp = (const float4 *)(a.x + (size_t)t * a.K) + 2 * c;
+            const float4 x0 = qk_ld(xp), x1 = qk_ld(xp + 1);
+#pragma unroll
+            for (int j = 0; j < AT_RPW; j++) {
+                const uint4 d = qk_ld((const uint4 *)(S.w + (size_t)(rr + j) * a.K) + c);
+                float a2 = acc[j];
+                a2 = fmaf(x0.x, qk_bf16_lo(d.x), a2);
+                a2 = fmaf(x0.y, qk_bf16_hi(d.x), a2);
+                a2 = fmaf(x0.z, qk_bf16_lo(d.y), a2);
+                a2 = fmaf(x0.w, qk_bf16_hi(d.y), a2);
+                a2 = fmaf(x1.x, qk_bf16_lo(d.z), a2);
+                a2 = fmaf(x1.y, qk_bf16_hi(d.z), a2);
+                a2 = fmaf(x1.z, qk_bf16_lo(d.w), a2);
+                a2 = fmaf(x1.w, qk_bf16_hi(d.w), a2);
+                acc[j] = ok ? a2 : acc[j];
+            }
+        }
 #pragma unroll
         for (int j = 0; j < AT_RPW; j++) {
-            const uint16_t *w = S.w + (size_t)(rr + j) * a.K;
-            float part = 0.0f;
-#pragma unroll
-            for (int ps = 0; ps < P; ps++) {
-                const int c0 = ps * 64 + lane;
-                const bool ok = c0 < CH;
-                const uint4 *src = (const uint4 *)(w + 32 * (size_t)(ok ? c0 : 0));
-#pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    uint32_t wp[4];
-                    qk_bf16x8_to_pairs(qk_ld(src + g), wp);
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const uint32_t w2 = ok ? wp[i] : 0u;
-                        part = qk_dot2(xp.hi[ps][4 * g + i], w2, part);
-                        part = qk_dot2(xp.lo[ps][4 * g + i], w2, part);
-                    }
-                }
-            }
-            const float v = qk_group_sum<64>(part);
+            const float v = qk_group_sum<64>(acc[j]);
             if (lane == 0) qk_st(S.out + (size_t)t * S.ostride + rr + j, v);
         }
     }
@@ -143,32 +155,43 @@ struct AtQkArgs {
     float *k_cache, *v_cache; /* [cap, kvh*hd] */
     float *idx_keys;        /* [cap, ihd] */
     float *qi;              /* [n, ih, ihd], or NULL when the indexer is off */
+    const float2 *rope;     /* [positions, rot/2] (cos, sin) */
     int n, h, kvh, hd, ih, ihd, len0, offset, rot;
-    float theta;
 };
 
 /* rmsnorm (kernel.c:10-20: (x*r)*w) of the L values in s, then partial
- * RoPE of the first rot (kernel.c:80-93) at position pos; one wave */
-__device__ __forceinline__ void at_norm_rope(float *s, const float *w, int L, int rot, float theta,
+ * RoPE of the first rot (kernel.c:80-93) at position pos; one wave.  The
+ * sum of squares is one fma chain in index order (every lane runs it on
+ * the LDS copy), and cos / sin come from the table the host fills with the
+ * reference's formula (cosf / sinf of pos * theta^(-2i/rot)), so the
+ * normed and rotated rows have the oracle's bits. */
+__device__ __forceinline__ void at_norm_rope(float *s, const float *w, int L, int rot, const float2 *rope,
                                              int pos, float *dst, int lane) {
     float ss = 0.0f;
-    for (int i = lane; i < L; i += 64) ss = fmaf(s[i], s[i], ss);
-    ss = qk_group_sum<64>(ss);
+    for (int i = 0; i < L; i += 4) {
+        const float4 v = *(const float4 *)(s + i);
+        ss = fmaf(v.x, v.x, ss);
+        ss = fmaf(v.y, v.y, ss);
+        ss = fmaf(v.z, v.z, ss);
+        ss = fmaf(v.w, v.w, ss);
+    }
     const float r = 1.0f / sqrtf(ss / (float)L + 1e-6f);
+    qk_wave_lds_sync();
     for (int i = lane; i < L; i += 64) s[i] = (s[i] * r) * qk_ld(w + i);
     qk_wave_lds_sync();
     const int half = rot / 2;
+    const float2 *cs = rope + (size_t)pos * half;
     float v[4];
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         const int i = lane + 64 * e;
         if (i >= L) break;
         if (i < half) {
-            const float ang = (float)pos * powf(theta, -(2.0f * (float)i) / (float)rot);
-            v[e] = s[i] * cosf(ang) - s[i + half] * sinf(ang);
+            const float2 c = cs[i];
+            v[e] = s[i] * c.x - s[i + half] * c.y;
         } else if (i < rot) {
-            const float ang = (float)pos * powf(theta, -(2.0f * (float)(i - half)) / (float)rot);
-            v[e] = s[i - half] * sinf(ang) + s[i] * cosf(ang);
+            const float2 c = cs[i - half];
+            v[e] = s[i - half] * c.y + s[i] * c.x;
         } else {
             v[e] = s[i];
         }
@@ -183,14 +206,14 @@ __device__ __forceinline__ void at_norm_rope(float *s, const float *w, int L, in
 }
 
 __global__ __launch_bounds__(64) void k_at_qk(AtQkArgs a) {
-    __shared__ float s[256];
+    __shared__ __align__(16) float s[256];
     const int lane = threadIdx.x, t = blockIdx.x, role = blockIdx.y;
     const int pos = a.offset + t, row = a.len0 + t;
     if (role < a.h) {
         const float *src = a.qg + (size_t)t * 2 * a.h * a.hd + (size_t)role * 2 * a.hd;
         for (int i = lane; i < a.hd; i += 64) s[i] = qk_ld(src + i);
         qk_wave_lds_sync();
-        at_norm_rope(s, a.q_norm, a.hd, a.rot, a.theta, pos, a.qn + ((size_t)t * a.h + role) * a.hd, lane);
+        at_norm_rope(s, a.q_norm, a.hd, a.rot, a.rope, pos, a.qn + ((size_t)t * a.h + role) * a.hd, lane);
     } else if (role < a.h + a.kvh) {
         const int kh = role - a.h;
         const size_t off = (size_t)t * a.kvh * a.hd + (size_t)kh * a.hd;
@@ -203,14 +226,14 @@ __global__ __launch_bounds__(64) void k_at_qk(AtQkArgs a) {
             for (int i = lane; i < a.ihd; i += 64) a.idx_keys[(size_t)row * a.ihd + i] = qk_ld(rk + i);
         }
         qk_wave_lds_sync();
-        at_norm_rope(s, a.k_norm, a.hd, a.rot, a.theta, pos,
+        at_norm_rope(s, a.k_norm, a.hd, a.rot, a.rope, pos,
                      a.k_cache + (size_t)row * a.kvh * a.hd + (size_t)kh * a.hd, lane);
     } else {
         const int ihh = role - a.h - a.kvh;
         const float *src = a.qk + (size_t)t * (a.ih + 1) * a.ihd + (size_t)ihh * a.ihd;
         for (int i = lane; i < a.ihd; i += 64) s[i] = qk_ld(src + i);
         qk_wave_lds_sync();
-        at_norm_rope(s, a.iq_norm, a.ihd, a.rot, a.theta, pos, a.qi + ((size_t)t * a.ih + ihh) * a.ihd, lane);
+        at_norm_rope(s, a.iq_norm, a.ihd, a.rot, a.rope, pos, a.qi + ((size_t)t * a.ih + ihh) * a.ihd, lane);
     }
 }
 
@@ -222,14 +245,14 @@ struct AtPoolArgs {
     const float *idx_keys;  /* [cap, ihd] */
     const float *ik_norm;   /* [ihd] */
     float *pooled;          /* [cap/comp, ihd] */
+    const float2 *rope;     /* [positions, rot/2] (cos, sin) */
     int ihd, comp, b0, b1, rot;
-    float theta;
 };
 
 /* one wave per block b in [b0, b1): mean of its comp keys, then rmsnorm +
  * RoPE at the block start (model.c:969-1000) */
 __global__ __launch_bounds__(256) void k_at_pool(AtPoolArgs a) {
-    __shared__ float s_p[4][256];
+    __shared__ __align__(16) float s_p[4][256];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int b = a.b0 + (int)blockIdx.x * 4 + wave;
     if (b >= a.b1) return; /* the whole wave; nothing below synchronises the workgroup */
@@ -240,7 +263,7 @@ __global__ __launch_bounds__(256) void k_at_pool(AtPoolArgs a) {
         pw[i] = acc / (float)a.comp;
     }
     qk_wave_lds_sync();
-    at_norm_rope(pw, a.ik_norm, a.ihd, a.rot, a.theta, b * a.comp, a.pooled + (size_t)b * a.ihd, lane);
+    at_norm_rope(pw, a.ik_norm, a.ihd, a.rot, a.rope, b * a.comp, a.pooled + (size_t)b * a.ihd, lane);
 }
 
 struct AtScoreArgs {
@@ -250,34 +273,54 @@ struct AtScoreArgs {
     int ih, ihd, comp, nb, ldk, offset;
 };
 
-/* grid (n, ceil(nb/4)): one wave per (token, block) */
+#define AT_SB 32 /* blocks per workgroup of k_at_score */
+
+/* dynamic LDS of k_at_score: the token's queries, a tile of pooled keys
+ * (rows padded by one float), the per-head dots */
+static size_t at_score_lds(int ih, int ihd) {
+    return ((size_t)ih * ihd + (size_t)AT_SB * (ihd + 1) + (size_t)ih * AT_SB) * 4;
+}
+
+/* grid (n, ceil(nb / AT_SB)): workgroup = (token t, AT_SB blocks), thread
+ * (block tid % AT_SB, head slot tid / AT_SB) runs the heads of its slot.
+ * The arithmetic is the reference's order (model.c:1030-1045): per head
+ * one chain dot = dot + relu(q_i * p_i) over i ascending from 0, the heads
+ * added in order from 0, then / sqrt(ihd); so the scores, and the blocks
+ * they keep, are the oracle's bit for bit. */
 __global__ __launch_bounds__(256) void k_at_score(AtScoreArgs a) {
-    extern __shared__ float at_lds[]; /* [ih * ihd] the token's indexer queries */
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, t = blockIdx.x;
-    for (int i = tid; i < a.ih * a.ihd; i += 256) at_lds[i] = qk_ld(a.qi + (size_t)t * a.ih * a.ihd + i);
+    extern __shared__ float at_lds[];
+    const int ih = a.ih, ihd = a.ihd, pl = ihd + 1;
+    float *s_q = at_lds;                       /* [ih * ihd] */
+    float *s_p = s_q + ih * ihd;               /* [AT_SB][ihd + 1] */
+    float *s_d = s_p + AT_SB * pl;             /* [ih][AT_SB] */
+    const int tid = threadIdx.x, t = blockIdx.x, b0 = (int)blockIdx.y * AT_SB;
+    const int nbt = min(AT_SB, a.nb - b0);
+    for (int i = tid; i < ih * ihd; i += 256) s_q[i] = qk_ld(a.qi + (size_t)t * ih * ihd + i);
+    for (int i = tid; i < nbt * ihd; i += 256) {
+        const int bb = i / ihd, ii = i - bb * ihd;
+        s_p[bb * pl + ii] = qk_ld(a.pooled + (size_t)(b0 + bb) * ihd + ii);
+    }
     __syncthreads();
-    const int b = (int)blockIdx.y * 4 + wave;
-    if (b >= a.nb) return;
-    const float *pb = a.pooled + (size_t)b * a.ihd;
-    float pv[4];
-#pragma unroll
-    for (int e = 0; e < 4; e++) pv[e] = lane + 64 * e < a.ihd ? qk_ld(pb + lane + 64 * e) : 0.0f;
-    float sc = 0.0f;
-    for (int hh = 0; hh < a.ih; hh++) {
-        float dot = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int i = lane + 64 * e;
-            if (i < a.ihd) {
-                const float v = at_lds[hh * a.ihd + i] * pv[e];
+    const int bl = tid & (AT_SB - 1);
+    if (bl < nbt)
+        for (int hh = tid / AT_SB; hh < ih; hh += 256 / AT_SB) {
+            const float *q = s_q + hh * ihd, *p = s_p + bl * pl;
+            float dot = 0.0f;
+            for (int i = 0; i < ihd; i++) {
+                const float v = q[i] * p[i];
                 dot = dot + (v > 0.0f ? v : 0.0f);
             }
+            s_d[hh * AT_SB + bl] = dot;
         }
-        sc = sc + qk_group_sum<64>(dot);
+    __syncthreads();
+    if (tid < nbt) {
+        float acc = 0.0f;
+        for (int hh = 0; hh < ih; hh++) acc = acc + s_d[hh * AT_SB + tid];
+        const int b = b0 + tid;
+        float score = acc / sqrtf((float)ihd);
+        if ((long long)b * a.comp + a.comp - 1 > (long long)(a.offset + t)) score = -INFINITY;
+        a.skey[(size_t)t * a.ldk + b] = qk_ordkey(score);
     }
-    float score = sc * (1.0f / sqrtf((float)a.ihd));
-    if ((long long)b * a.comp + a.comp - 1 > (long long)(a.offset + t)) score = -INFINITY;
-    if (lane == 0) a.skey[(size_t)t * a.ldk + b] = qk_ordkey(score);
 }
 
 struct AtSelArgs {
@@ -767,7 +810,7 @@ extern "C" int qk_at_shape_ok(const qk_at_shape *s) {
     if (s->d <= 0 || s->d % 64 || s->d > 8192) return 0;
     if (s->h <= 0 || s->kvh <= 0 || s->h % s->kvh) return 0;
     if (s->hd <= 0 || s->hd % 64 || s->hd > 256 || (s->h * s->hd) % 64 || s->h * s->hd > 8192) return 0;
-    if (s->ih <= 0 || s->ihd <= 0 || s->ihd % 4 || s->ihd > 256) return 0;
+    if (s->ih <= 0 || s->ih > 64 || s->ihd <= 0 || s->ihd % 4 || s->ihd > 256 || s->ih * s->ihd > 8192) return 0;
     if (s->rot < 0 || s->rot % 2 || s->rot > s->hd || s->rot > s->ihd) return 0;
     if (s->cap <= 0 || s->cap > 8192 || s->comp <= 0 || s->budget <= 0) return 0;
     return 1;
@@ -808,7 +851,7 @@ extern "C" int qk_launch_at(const qk_at_shape *s, const qk_at_dev *W, const floa
     q.qn = sc->qn; q.k_cache = k_cache; q.v_cache = v_cache; q.idx_keys = idx_keys;
     q.qi = use_idx ? sc->qi : nullptr;
     q.n = n; q.h = h; q.kvh = kvh; q.hd = hd; q.ih = ih; q.ihd = ihd; q.len0 = len0;
-    q.offset = offset; q.rot = s->rot; q.theta = s->theta;
+    q.offset = offset; q.rot = s->rot; q.rope = (const float2 *)W->rope;
     hipLaunchKernelGGL(k_at_qk, dim3(n, h + kvh + (use_idx ? ih : 0)), dim3(64), 0, st, q);
     rc = QK_CHECK_LAUNCH();
     if (rc) return rc;
@@ -819,7 +862,7 @@ extern "C" int qk_launch_at(const qk_at_shape *s, const qk_at_dev *W, const floa
     if (pb1 > pb0) {
         AtPoolArgs pa;
         pa.idx_keys = idx_keys; pa.ik_norm = W->idx_k_norm; pa.pooled = pooled;
-        pa.ihd = ihd; pa.comp = s->comp; pa.b0 = pb0; pa.b1 = pb1; pa.rot = s->rot; pa.theta = s->theta;
+        pa.ihd = ihd; pa.comp = s->comp; pa.b0 = pb0; pa.b1 = pb1; pa.rot = s->rot; pa.rope = (const float2 *)W->rope;
         hipLaunchKernelGGL(k_at_pool, dim3((pb1 - pb0 + 3) / 4), dim3(256), 0, st, pa);
         rc = QK_CHECK_LAUNCH();
         if (rc) return rc;
@@ -831,7 +874,7 @@ extern "C" int qk_launch_at(const qk_at_shape *s, const qk_at_dev *W, const floa
         AtScoreArgs ka;
         ka.pooled = pooled; ka.qi = sc->qi; ka.skey = sc->skey;
         ka.ih = ih; ka.ihd = ihd; ka.comp = s->comp; ka.nb = nb; ka.ldk = ldk; ka.offset = offset;
-        hipLaunchKernelGGL(k_at_score, dim3(n, (nb + 3) / 4), dim3(256), (size_t)ih * ihd * 4, st, ka);
+        hipLaunchKernelGGL(k_at_score, dim3(n, (nb + AT_SB - 1) / AT_SB), dim3(256), at_score_lds(ih, ihd), st, ka);
         rc = QK_CHECK_LAUNCH();
         if (rc) return rc;
         AtSelArgs e;

@@ -5,6 +5,7 @@
  * Replaces attention_forward (c/src/model.c:798-1144) and the cache state
  * around it (model.c:341-345, 402-406).
  */
+#include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -32,6 +33,9 @@ struct qmoe_attn_ctx {
     at_layer *layers;
     void *scratch;
     qk_at_scratch sc;
+    float *rope;    /* device [rope_rows, rot/2, 2] */
+    int rope_rows;  /* positions the table covers */
+    int last_kw;    /* kept-block bitmap words per token of the last masked call */
 };
 
 static void at_set_err(qmoe_err *err, const char *fmt, ...) {
@@ -50,6 +54,38 @@ static int at_hip_fail(qmoe_err *err, int rc, const char *what) {
 
 static size_t at_align(size_t v) { return (v + AT_ALIGN - 1) / AT_ALIGN * AT_ALIGN; }
 
+/* cos / sin of pos * theta^(-2i/rot) for positions [0, rows) and i < rot/2,
+ * with the reference's formula and float arithmetic (model.c: inv[i] =
+ * powf(theta, -(2i)/rot), a = (float)pos * inv[i], cosf(a), sinf(a)) */
+static int at_rope_table(qmoe_attn_ctx *c, qmoe_err *err) {
+    const int half = c->shape.rot / 2;
+    if (half == 0) return 0;
+    const size_t cnt = (size_t)c->rope_rows * (size_t)half * 2;
+    float *tab = (float *)malloc(cnt * sizeof(float));
+    float *inv = (float *)malloc((size_t)half * sizeof(float));
+    if (!tab || !inv) {
+        free(tab);
+        free(inv);
+        at_set_err(err, "out of host memory");
+        return -1;
+    }
+    for (int i = 0; i < half; i++)
+        inv[i] = powf(c->shape.theta, -(2.0f * (float)i) / (float)c->shape.rot);
+    for (int p = 0; p < c->rope_rows; p++)
+        for (int i = 0; i < half; i++) {
+            const float ang = (float)p * inv[i];
+            tab[((size_t)p * half + i) * 2] = cosf(ang);
+            tab[((size_t)p * half + i) * 2 + 1] = sinf(ang);
+        }
+    int rc = at_hip_fail(err, (int)hipMalloc((void **)&c->rope, cnt * sizeof(float)), "rope table");
+    if (!rc)
+        rc = at_hip_fail(err, (int)hipMemcpy(c->rope, tab, cnt * sizeof(float), hipMemcpyHostToDevice),
+                         "rope table");
+    free(tab);
+    free(inv);
+    return rc;
+}
+
 int qmoe_attn_create(qmoe_attn_ctx **out, const qmoe_attn_config *cfg, qmoe_err *err) {
     if (err) err->msg[0] = 0;
     if (!out || !cfg) {
@@ -64,8 +100,8 @@ int qmoe_attn_create(qmoe_attn_ctx **out, const qmoe_attn_config *cfg, qmoe_err 
         !qk_at_shape_ok(&s)) {
         at_set_err(err, "attention shape unsupported: hidden %d (multiple of 64, <= 8192), heads %d/%d "
                         "(kv heads divide heads), head_dim %d (multiple of 64, <= 256, heads*dim <= 8192), "
-                        "indexer %d heads of %d (dim a multiple of 4, <= 256, >= the rotated dims %d, "
-                        "even), budget %d, compress %d, kv_cap %d (<= 8192), group_size %d (64)",
+                        "indexer %d heads (<= 64) of %d (dim a multiple of 4, <= 256, >= the rotated dims %d, "
+                        "even; heads*dim <= 8192), budget %d, compress %d, kv_cap %d (<= 8192), group_size %d (64)",
                    cfg->hidden, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, cfg->idx_heads,
                    cfg->idx_head_dim, s.rot, cfg->idx_budget, cfg->idx_compress, cfg->kv_cap,
                    cfg->group_size);
@@ -76,6 +112,10 @@ int qmoe_attn_create(qmoe_attn_ctx **out, const qmoe_attn_config *cfg, qmoe_err 
                    cfg->n_layers, cfg->max_tokens, cfg->kv_cap);
         return -1;
     }
+    if (cfg->max_position < 0 || cfg->max_position > QMOE_ATTN_MAX_POSITION) {
+        at_set_err(err, "max_position %d out of range [0, %d]", cfg->max_position, QMOE_ATTN_MAX_POSITION);
+        return -1;
+    }
     qmoe_attn_ctx *c = (qmoe_attn_ctx *)calloc(1, sizeof(*c));
     if (!c) {
         at_set_err(err, "out of host memory");
@@ -83,6 +123,7 @@ int qmoe_attn_create(qmoe_attn_ctx **out, const qmoe_attn_config *cfg, qmoe_err 
     }
     c->cfg = *cfg;
     c->shape = s;
+    c->rope_rows = cfg->max_position > cfg->kv_cap ? cfg->max_position : cfg->kv_cap;
     const size_t d = (size_t)s.d, h = (size_t)s.h, kvh = (size_t)s.kvh, hd = (size_t)s.hd;
     const size_t ih = (size_t)s.ih, ihd = (size_t)s.ihd, cap = (size_t)s.cap;
     const size_t qr = 2 * h * hd, kr = kvh * hd, orow = d, ok = h * hd;
@@ -136,6 +177,10 @@ int qmoe_attn_create(qmoe_attn_ctx **out, const qmoe_attn_config *cfg, qmoe_err 
             qmoe_attn_destroy(c);
             return -1;
         }
+    if (at_rope_table(c, err)) {
+        qmoe_attn_destroy(c);
+        return -1;
+    }
     *out = c;
     return 0;
 }
@@ -145,6 +190,7 @@ void qmoe_attn_destroy(qmoe_attn_ctx *c) {
     if (c->layers)
         for (int l = 0; l < c->cfg.n_layers; l++) hipFree(c->layers[l].mem);
     hipFree(c->scratch);
+    hipFree(c->rope);
     free(c->layers);
     free(c);
 }
@@ -233,6 +279,10 @@ int qmoe_attn_forward(qmoe_attn_ctx *c, int layer, const float *x, int n, int of
         at_set_err(err, "layer %d: %d cached + %d new tokens pass kv_cap %d", layer, len0, n, c->cfg.kv_cap);
         return -1;
     }
+    if ((long long)offset + n > c->rope_rows) {
+        at_set_err(err, "positions %d..%d pass max_position %d", offset, offset + n - 1, c->rope_rows);
+        return -1;
+    }
     qk_at_dev W;
     W.q_q = (const uint32_t *)at_ptr(c, layer, AT_Q_Q);
     W.q_s = (const uint16_t *)at_ptr(c, layer, AT_Q_S);
@@ -251,11 +301,13 @@ int qmoe_attn_forward(qmoe_attn_ctx *c, int layer, const float *x, int n, int of
     W.k_norm = (const float *)at_ptr(c, layer, AT_K_NORM);
     W.idx_q_norm = (const float *)at_ptr(c, layer, AT_IQ_NORM);
     W.idx_k_norm = (const float *)at_ptr(c, layer, AT_IK_NORM);
+    W.rope = c->rope;
     const int rc = qk_launch_at(&c->shape, &W, x, n, offset, len0, out, (float *)at_ptr(c, layer, AT_K_CACHE),
                                 (float *)at_ptr(c, layer, AT_V_CACHE), (float *)at_ptr(c, layer, AT_IDX_KEYS),
                                 (float *)at_ptr(c, layer, AT_POOLED), &c->sc, stream);
     if (at_hip_fail(err, rc, "attention launch")) return -1;
     c->layers[layer].len = len0 + n;
+    if (len0 + n > c->cfg.idx_budget) c->last_kw = ((len0 + n) / c->cfg.idx_compress + 31) / 32;
     return 0;
 }
 
@@ -266,5 +318,16 @@ int qmoe_attn_cache(qmoe_attn_ctx *c, int layer, float **k_cache, float **v_cach
     if (v_cache) *v_cache = (float *)at_ptr(c, layer, AT_V_CACHE);
     if (idx_keys) *idx_keys = (float *)at_ptr(c, layer, AT_IDX_KEYS);
     if (len) *len = c->layers[layer].len;
+    return 0;
+}
+
+int qmoe_attn_index_state(qmoe_attn_ctx *c, int layer, float **pooled, uint32_t **keep, int *keep_words,
+                          uint32_t **score_keys, int *score_ld, qmoe_err *err) {
+    if (at_check_layer(c, layer, err)) return -1;
+    if (pooled) *pooled = (float *)at_ptr(c, layer, AT_POOLED);
+    if (keep) *keep = c->sc.keep;
+    if (keep_words) *keep_words = c->last_kw;
+    if (score_keys) *score_keys = c->sc.skey;
+    if (score_ld) *score_ld = c->cfg.kv_cap / c->cfg.idx_compress;
     return 0;
 }

@@ -241,6 +241,7 @@ typedef struct {
     const uint16_t *q_s, *q_b, *k_s, *k_b, *v_s, *v_b, *o_s, *o_b;
     const uint16_t *idx_w;
     const float *q_norm, *k_norm, *idx_q_norm, *idx_k_norm;
+    const float *rope; /* [positions, rot/2, 2]: cos, sin of pos * theta^(-2i/rot) */
 } qk_at_dev;
 typedef struct {
     float *qg;    /* [n, 2h*hd] */

@@ -83,7 +83,7 @@ class QmoeAttnConfig(ctypes.Structure):
                                             "idx_head_dim", "idx_budget", "idx_compress", "kv_cap",
                                             "group_size")] + \
                [("rotary_factor", ctypes.c_float), ("rope_theta", ctypes.c_float),
-                ("n_layers", ctypes.c_int), ("max_tokens", ctypes.c_int)]
+                ("n_layers", ctypes.c_int), ("max_tokens", ctypes.c_int), ("max_position", ctypes.c_int)]
 
 
 AT_FIELDS = ["q_q", "q_s", "q_b", "k_q", "k_s", "k_b", "v_q", "v_s", "v_b", "o_q", "o_s", "o_b", "idx_w",
@@ -147,6 +147,8 @@ SIGNATURES = {
     "qmoe_attn_forward": (_I, [_P, _I, _P, _I, _I, _P, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_attn_cache": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(_P), ctypes.POINTER(_P),
                              ctypes.POINTER(_I), ctypes.POINTER(QmoeErr)]),
+    "qmoe_attn_index_state": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(_P), ctypes.POINTER(_I),
+                                   ctypes.POINTER(_P), ctypes.POINTER(_I), ctypes.POINTER(QmoeErr)]),
     "qmoe_gr_create": (_I, [ctypes.POINTER(_P), ctypes.POINTER(QmoeGrConfig), ctypes.POINTER(QmoeErr)]),
     "qmoe_gr_destroy": (None, [_P]),
     "qmoe_gr_upload_slot": (_I, [_P, _I, ctypes.POINTER(QmoeHcWeights), ctypes.POINTER(QmoeErr)]),
@@ -740,10 +742,10 @@ class AttentionContext:
 
     def __init__(self, hidden, n_heads, n_kv_heads, head_dim, idx_heads, idx_head_dim, idx_budget,
                  idx_compress, kv_cap=2048, rotary_factor=0.25, rope_theta=1e7, n_layers=1,
-                 max_tokens=1, group_size=64):
+                 max_tokens=1, group_size=64, max_position=0):
         self.cfg = QmoeAttnConfig(hidden, n_heads, n_kv_heads, head_dim, idx_heads, idx_head_dim,
                                   idx_budget, idx_compress, kv_cap, group_size, rotary_factor,
-                                  rope_theta, n_layers, max_tokens)
+                                  rope_theta, n_layers, max_tokens, max_position)
         self.d, self.h, self.kvh, self.hd = hidden, n_heads, n_kv_heads, head_dim
         self.ihd, self.cap = idx_head_dim, kv_cap
         self._h = ctypes.c_void_p()
@@ -812,6 +814,18 @@ class AttentionContext:
         _check(lib().qmoe_attn_cache(self._h, layer, ctypes.byref(k), ctypes.byref(v), ctypes.byref(i),
                                      ctypes.byref(ln), ctypes.byref(err)), err, "qmoe_attn_cache")
         return k.value, v.value, i.value, ln.value
+
+    def index_state(self, layer):
+        """device addresses of the indexer's pooled block keys, the last
+        masked call's kept-block bitmap and block-score order keys, with the
+        bitmap's words and the score keys' row stride"""
+        p, k, s = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+        kw, ld = ctypes.c_int(), ctypes.c_int()
+        err = QmoeErr()
+        _check(lib().qmoe_attn_index_state(self._h, layer, ctypes.byref(p), ctypes.byref(k), ctypes.byref(kw),
+                                           ctypes.byref(s), ctypes.byref(ld), ctypes.byref(err)),
+               err, "qmoe_attn_index_state")
+        return p.value, k.value, kw.value, s.value, ld.value
 
 
 class DeltaNetContext:

@@ -3,10 +3,13 @@ the C ABI) against the oracle (oracle/attn_oracle.c, pinned by
 tests/test_oracle_attn.py).
 
 Bar: per call, outputs within 2e-2 max-abs and 1e-3 relative L2 of the
-oracle run on the same weights and inputs from the same caches; the k, v
-and indexer-key caches within 1e-4 relative L2.  Dense (budget past the
-cache) and sparse (the QSA block mask active) cases, several shapes,
-prefill chunks and one-token steps.
+oracle run on the same weights and inputs from the same caches; the k and v
+caches within 1e-4 relative L2.  The indexer path is index work and is
+compared bit for bit: the raw indexer-key cache, the pooled block keys, the
+block scores of every token (as order keys) and the kept-block set over
+each token's visible blocks.  Dense (budget past the cache) and sparse (the
+QSA block mask active) cases, several shapes, prefill chunks of up to 2048
+tokens and one-token steps, up to 6,000+ cached keys with the mask on.
 """
 import ctypes
 
@@ -34,11 +37,11 @@ def rel(a, b):
 _hip = None
 
 
-def d2h(ptr, shape):
+def d2h(ptr, shape, dtype=np.float32):
     global _hip
     if _hip is None:
         _hip = ctypes.CDLL("libamdhip64.so")
-    buf = np.empty(shape, np.float32)
+    buf = np.empty(shape, dtype)
     assert _hip.hipMemcpy(ctypes.c_void_p(buf.ctypes.data), ctypes.c_void_p(ptr),
                           ctypes.c_size_t(buf.nbytes), 2) == 0
     return buf
@@ -50,18 +53,55 @@ def torch_dev(gpu):
     return torch, gpu
 
 
+def ordkeys(v):
+    """float32 -> the kernels' order keys (-0 as +0)"""
+    b = (np.asarray(v, np.float32) + np.float32(0.0)).view(np.uint32)
+    return np.where(b & 0x80000000, ~b, b | 0x80000000).astype(np.uint32)
+
+
+def check_index(ctx, dbg, case, n, t0, ln):
+    """the indexer's values of the last call against the oracle's, bit for
+    bit: pooled keys, every token's block scores and kept blocks (exact
+    ties at the budget boundary to the lower block on both sides).  Returns
+    the number of tokens whose boundary is such a tie among the blocks the
+    token can see."""
+    d, h, kvh, hd, ih, ihd, budget, comp, cap, rf = case
+    nb, btop = ln // comp, budget // comp
+    pp, kp, kw, sp, ld = ctx.index_state(1)
+    pooled = d2h(pp, (nb, ihd))
+    assert np.array_equal(pooled.view(np.uint32), dbg["pooled"].view(np.uint32)), \
+        ("pooled keys", int((pooled != dbg["pooled"]).sum()))
+    skey = d2h(sp, (n, ld), np.uint32)[:, :nb]
+    okey = ordkeys(dbg["scores"])
+    bad = np.argwhere(skey != okey)
+    assert bad.size == 0, ("block scores differ", bad[:5].tolist(), int(len(bad)))
+    bits = d2h(kp, (n, kw), np.uint32)
+    keep = ((bits[:, np.arange(nb) // 32] >> (np.arange(nb) % 32).astype(np.uint32)) & 1).astype(bool)
+    bad = np.argwhere(keep != dbg["keep"].astype(bool))
+    assert bad.size == 0, ("kept blocks differ", bad[:8].tolist(), int(len(bad)))
+    ties = 0
+    for t in range(n):
+        vis = (np.arange(nb) * comp + comp - 1) <= t0 + t
+        sc = dbg["scores"][t][vis]
+        if btop < sc.size:
+            srt = np.sort(sc)[::-1]
+            ties += int(srt[btop - 1] == srt[btop])
+    return ties
+
+
 def run_calls(torch, dev, case, calls, seed=1):
     d, h, kvh, hd, ih, ihd, budget, comp, cap, rf = case
     pkg = load_pkg()
     A = orc.Attention(d, h, kvh, hd, ih, ihd, budget, comp, kv_cap=cap, rotary_factor=rf, seed=seed)
     st = A.new_state()
     x = orc.gen_attn_x(sum(calls), d, seed + 50)
+    masked = 0
     with pkg.AttentionContext(d, h, kvh, hd, ih, ihd, budget, comp, kv_cap=cap, rotary_factor=rf,
                               n_layers=2, max_tokens=max(calls)) as ctx:
         ctx.upload_layer(1, A.arrays())
         t0 = 0
         for i, n in enumerate(calls):
-            ref = A.forward(x[t0:t0 + n], st, t0)
+            ref, dbg = A.forward(x[t0:t0 + n], st, t0, dbg=True)
             got = ctx.forward(1, torch.from_numpy(x[t0:t0 + n]).to(dev), t0)
             torch.cuda.synchronize()
             g = got.cpu().numpy()
@@ -71,13 +111,18 @@ def run_calls(torch, dev, case, calls, seed=1):
             kc = d2h(kp, (ln, kvh * hd))
             vc = d2h(vp, (ln, kvh * hd))
             ic = d2h(ip, (ln, ihd))
-            rk, rv, ri = rel(kc, st.k[:ln]), rel(vc, st.v[:ln]), rel(ic, st.idx[:ln])
-            say(f"{case} call {i} (n={n}, cached {ln}, mask {'on' if ln > budget else 'off'}): "
+            rk, rv = rel(kc, st.k[:ln]), rel(vc, st.v[:ln])
+            ties = check_index(ctx, dbg, case, n, t0, ln) if dbg else 0
+            masked += n if dbg else 0
+            say(f"{case} call {i} (n={n}, cached {ln}, mask {'on' if dbg else 'off'}): "
                 f"max-abs {err:.2e} rel-L2 {r:.2e} (|ref| max {np.abs(ref).max():.2f}); "
-                f"caches rel {rk:.1e}/{rv:.1e}/{ri:.1e}")
+                f"caches rel {rk:.1e}/{rv:.1e}; indexer keys, pooled keys, scores and kept blocks "
+                f"{'bit-exact' if dbg else 'n/a'}{f' ({ties} exact boundary ties)' if ties else ''}")
+            assert np.array_equal(ic.view(np.uint32), st.idx[:ln].view(np.uint32)), "indexer keys differ"
             assert err < MAX_ABS and r < REL_L2, (i, err, r)
-            assert rk < 1e-4 and rv < 1e-4 and ri < 1e-4, (i, rk, rv, ri)
+            assert rk < 1e-4 and rv < 1e-4, (i, rk, rv)
             t0 += n
+    return masked
 
 
 CASES = [
@@ -142,16 +187,24 @@ def test_irregular_shapes(torch_dev, case):
 
 
 def test_long_cache_decode(torch_dev):
-    """6,000+ cached keys: one-token calls split the cache into ~97 chunks
-    of 64 keys, more than one lane of the combine holds.  The budget covers
-    the cache, so no block mask: with the mask on, 2048-row prefill chunks
-    meet near-ties at the budget boundary, where the GPU's and the oracle's
-    block scores (summed in different orders) can keep different blocks;
-    the selection itself is covered at the model shape above"""
+    """6,000+ cached keys with the block mask on (budget 2048): 2048-token
+    prefill chunks, then one-token calls that split the cache into ~97
+    chunks of 64 keys, more than one lane of the combine holds"""
     torch, dev = torch_dev
-    case = (256, 4, 1, 64, 2, 64, 8192, 4, 8192, 0.25)
+    case = (256, 4, 1, 64, 2, 64, 2048, 4, 8192, 0.25)
     say(f"case: attention {case}")
-    run_calls(torch, dev, case, [2048, 2048, 2048, 50, 1, 1], seed=4)
+    assert run_calls(torch, dev, case, [2048, 2048, 2048, 50, 1, 1], seed=4) == 2048 + 2048 + 50 + 2
+
+
+def test_bench_indexer_setting(torch_dev):
+    """the benchmark's indexer (4 heads of 128, rotary 32 of 128, budget
+    2048, compress 4) with the mask on: 2048-token chunks to 4,096+ cached
+    keys, then one-token steps; hidden 256 and 2 query heads keep the
+    oracle's attention part short"""
+    torch, dev = torch_dev
+    case = (256, 2, 1, 128, 4, 128, 2048, 4, 8192, 0.25)
+    say(f"case: attention {case}")
+    assert run_calls(torch, dev, case, [2048, 2048, 40, 1, 1], seed=5) == 2048 + 40 + 2
 
 
 def test_dense_model_shape(torch_dev):
@@ -165,7 +218,8 @@ def test_errors(torch_dev):
     torch, dev = torch_dev
     pkg = load_pkg()
     for bad in [(100, 4, 2, 64, 2, 64, 8, 2, 64), (256, 4, 3, 64, 2, 64, 8, 2, 64),
-                (256, 4, 2, 96, 2, 64, 8, 2, 64), (256, 4, 2, 64, 2, 8, 8, 2, 64)]:
+                (256, 4, 2, 96, 2, 64, 8, 2, 64), (256, 4, 2, 64, 2, 8, 8, 2, 64),
+                (256, 4, 2, 64, 65, 64, 8, 2, 64), (256, 4, 2, 64, 40, 256, 8, 2, 64)]:
         with pytest.raises(pkg.QmoeError, match="attention shape unsupported"):
             pkg.AttentionContext(*bad)
     with pkg.AttentionContext(256, 4, 2, 64, 2, 64, 8, 2, kv_cap=4, max_tokens=4) as ctx:
@@ -181,3 +235,12 @@ def test_errors(torch_dev):
         ctx.forward(0, x, 0)
         torch.cuda.synchronize()
         assert ctx.cache(0)[3] == 1
+        with pytest.raises(pkg.QmoeError, match="pass max_position"):
+            ctx.forward(0, x, 4)
+    with pkg.AttentionContext(256, 4, 2, 64, 2, 64, 8, 2, kv_cap=4, max_tokens=4, max_position=16) as ctx:
+        ctx.upload_layer(0, A.arrays())
+        ctx.forward(0, x, 15)
+        with pytest.raises(pkg.QmoeError, match="pass max_position"):
+            ctx.forward(0, x, 16)
+    with pytest.raises(pkg.QmoeError, match="max_position"):
+        pkg.AttentionContext(256, 4, 2, 64, 2, 64, 8, 2, kv_cap=4, max_position=-1)
