@@ -282,27 +282,6 @@ int qmoe_layer_forward_noalloc(const qmoe_config *cfg, const qmoe_layer_weights 
                                const void *x, int x_dtype, int n, float *out, int flags,
                                void *stream, qmoe_err *err);
 
-/* enable = 1 runs one-token calls (n = 1) of qmoe_layer_forward and
- * qmoe_hc_layer_forward in ONE launch (hidden 2048 or 4096, moe_inter 512,
- * n_experts <= 1024, (top_k+1)*512 <= 6144): router, shared and routed
- * gate/up, down and the combine, the logits and h handed over inside the
- * launch through tagged words with bounded waits.  The default (enable = 0)
- * is the staged kernels (router; gate/up with top-k; down + combine), which
- * measure faster at the decode shape (17.0 against 19.7 us per layer: each
- * in-kernel hand-off costs more than a kernel boundary on this GPU); both
- * give bit-identical outputs.  No counterpart in the reference (its layer
- * is one CPU call).  enable = 1 on a shape the one-launch path does not
- * take is an error. */
-int qmoe_set_fused_decode(qmoe_ctx *ctx, int enable, qmoe_err *err);
-
-/* Synchronises the device and reports whether a one-launch one-token call
- * gave up a wait (20 ms bound; only possible when other work keeps its
- * gate/up workgroups off the GPU): returns 0 with *flags = 0 when none did;
- * otherwise -1 with *flags != 0, after resetting the hand-off state.  The
- * outputs of the calls since the previous check may then be NaN.  No
- * counterpart in the reference. */
-int qmoe_decode_status(qmoe_ctx *ctx, uint32_t *flags, qmoe_err *err);
-
 /* Copies the routing of the last qmoe_layer_forward call on this context
  * (n must be that call's token count) into caller device buffers, any of
  * which may be NULL: idx [n,k], w [n,k], shared_gate [n], offsets [E+1],

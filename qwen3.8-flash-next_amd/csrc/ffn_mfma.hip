@@ -689,7 +689,7 @@ static int mm_max_tasks16(qk_shape s, int n) {
 
 extern "C" size_t qk_mfma_task_bytes(qk_shape s, int n) {
     const size_t t16 = n <= MM_NARROW_N ? (size_t)MM_TASK_HDR + 4 * (size_t)mm_max_tasks16(s, n) : 0;
-    return ((size_t)MM_TASK_HDR + 4 * (size_t)qk_mfma_max_tasks(s, n) + 2 + (size_t)s.E + t16) * 4;
+    return ((size_t)MM_TASK_HDR + 4 * (size_t)qk_mfma_max_tasks(s, n) + (size_t)MM_SMALL16(s.E) + t16) * 4;
 }
 
 extern "C" int32_t *qk_mfma_small_list(qk_shape s, int n, int32_t *tasks) {
@@ -774,6 +774,6 @@ extern "C" int qk_launch_down_mfma(const qmoe_layer_weights *W, qk_shape s, cons
     a.n = n;
     a.k = s.k;
     return mm_launch(a, true, 2, qk_mfma_max_tasks(s, n), (hipStream_t)stream,
-                     n <= MM_NARROW_N ? qk_mfma_small_list(s, n, (int32_t *)tasks) + 2 + s.E : nullptr,
+                     n <= MM_NARROW_N ? qk_mfma_small_list(s, n, (int32_t *)tasks) + MM_SMALL16(s.E) : nullptr,
                      mm_max_tasks16(s, n));
 }

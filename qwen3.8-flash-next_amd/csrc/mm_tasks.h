@@ -79,11 +79,14 @@ static __device__ void mm_tasks_list(const int32_t *segtab, int n, int k, int E,
 
 /* The task lists of a dispatch: chunks of MM_BM rows at `tasks` with the
  * small-segment list at `small`, and, up to MM_NARROW_N tokens, chunks of
- * MM_BM16 rows at small + 2 + E (the down projection's list there). */
+ * MM_BM16 rows at small + MM_SMALL16(E) (the down projection's list there:
+ * past the small list's 2 + E ints, rounded up to 16 bytes for its int4
+ * entries). */
+#define MM_SMALL16(E) ((2 + (E) + 3) & ~3)
 static __device__ void mm_tasks_block(const int32_t *segtab, int n, int k, int E, int min_m, int32_t *tasks,
                                int32_t *small) {
     mm_tasks_list(segtab, n, k, E, min_m, MM_BM, tasks, small);
-    if (n <= MM_NARROW_N) mm_tasks_list(segtab, n, k, E, min_m, MM_BM16, small + 2 + E, nullptr);
+    if (n <= MM_NARROW_N) mm_tasks_list(segtab, n, k, E, min_m, MM_BM16, small + MM_SMALL16(E), nullptr);
 }
 
 #endif

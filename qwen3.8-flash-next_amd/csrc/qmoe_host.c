@@ -35,7 +35,6 @@ struct qmoe_ctx {
     qmoe_layer_slot *layers;
     size_t layer_bytes;
     int last_n; /* token count of the last qmoe_layer_forward, -1 if none */
-    int dec_fused; /* one-token calls in one launch (qk_launch_dec_layer) when supported */
     /* second stream for the GEMV kernels of small segments, which run beside
      * the MFMA kernels of large ones (fork/join with two events) */
     hipStream_t aux;
@@ -170,17 +169,16 @@ static int check_config(const qmoe_config *c, qmoe_err *err) {
 }
 
 /* the layer scratch for n tokens, carved out of one block: region offsets
- * (QH_SC_COUNT of them) and the total; rep = bytes of the one-token
- * hand-off block (0: none) */
-enum { QH_SC_COUNT = 19 };
-static size_t scratch_plan(qk_shape s, size_t n, size_t rep, size_t offs[QH_SC_COUNT]) {
+ * (QH_SC_COUNT of them) and the total */
+enum { QH_SC_COUNT = 17 };
+static size_t scratch_plan(qk_shape s, size_t n, size_t offs[QH_SC_COUNT]) {
     const size_t E = (size_t)s.E, k = (size_t)s.k, H = (size_t)s.H, I = (size_t)s.I;
     const size_t nw = (n + 31) / 32, rows = n * k + n;
     const size_t plane = n * H > rows * I ? n * H : rows * I;
     const size_t sz[QH_SC_COUNT] = {n * (E + 1) * 4, n * k * 4, n * k * 4, n * 4, (E + 1) * 4, n * k * 4,
                                     n * k * 4, E * nw * 4, E * nw * 4, n * H * 4, rows * I * 4,
                                     rows * H * 4, (3 * E + 1) * 4, qk_mfma_task_bytes(s, (int)n),
-                                    plane * 2, plane * 2, plane / 64 * 4, rep, 4};
+                                    plane * 2, plane * 2, plane / 64 * 4};
     size_t total = 0;
     for (int i = 0; i < QH_SC_COUNT; i++) {
         offs[i] = total;
@@ -189,7 +187,7 @@ static size_t scratch_plan(qk_shape s, size_t n, size_t rep, size_t offs[QH_SC_C
     return total;
 }
 
-static void scratch_bind(qk_scratch *sc, char *b, const size_t offs[QH_SC_COUNT], int with_rep) {
+static void scratch_bind(qk_scratch *sc, char *b, const size_t offs[QH_SC_COUNT]) {
     sc->logits = (float *)(b + offs[0]);
     sc->idx = (int32_t *)(b + offs[1]);
     sc->w = (float *)(b + offs[2]);
@@ -207,8 +205,6 @@ static void scratch_bind(qk_scratch *sc, char *b, const size_t offs[QH_SC_COUNT]
     sc->ahi = (uint16_t *)(b + offs[14]);
     sc->alo = (uint16_t *)(b + offs[15]);
     sc->ag = (float *)(b + offs[16]);
-    sc->rep = with_rep ? (void *)(b + offs[17]) : NULL;
-    sc->status = (uint32_t *)(b + offs[18]);
 }
 
 int qmoe_create(qmoe_ctx **out, const qmoe_config *cfg, qmoe_err *err) {
@@ -244,7 +240,6 @@ int qmoe_create(qmoe_ctx **out, const qmoe_config *cfg, qmoe_err *err) {
     }
     c->layer_bytes = o;
     c->last_n = -1;
-    c->dec_fused = 0;
     c->layers = (qmoe_layer_slot *)calloc((size_t)cfg->n_layers, sizeof(qmoe_layer_slot));
     if (!c->layers) {
         free(c);
@@ -252,23 +247,15 @@ int qmoe_create(qmoe_ctx **out, const qmoe_config *cfg, qmoe_err *err) {
         return -1;
     }
     /* scratch */
-    const size_t rep = qk_dec_supported(c->shape) ? qk_dec_handoff_bytes(c->shape) : 0;
     size_t offs[QH_SC_COUNT];
-    const size_t total = scratch_plan(c->shape, (size_t)cfg->max_tokens, rep, offs);
+    const size_t total = scratch_plan(c->shape, (size_t)cfg->max_tokens, offs);
     c->scratch_bytes = total;
     if (hip_fail(err, (int)hipMalloc(&c->scratch_mem, total), "hipMalloc(scratch)")) {
         free(c->layers);
         free(c);
         return -1;
     }
-    scratch_bind(&c->sc, (char *)c->scratch_mem, offs, rep != 0);
-    if (hip_fail(err, (int)hipMemset(c->sc.status, 0, 4), "clear status") ||
-        (rep && hip_fail(err, (int)hipMemset(c->sc.rep, 0, rep), "clear hand-off"))) {
-        hipFree(c->scratch_mem);
-        free(c->layers);
-        free(c);
-        return -1;
-    }
+    scratch_bind(&c->sc, (char *)c->scratch_mem, offs);
     if (hip_fail(err, (int)hipStreamCreateWithFlags(&c->aux, hipStreamNonBlocking), "stream") ||
         hip_fail(err, (int)hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming), "event") ||
         hip_fail(err, (int)hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming), "event")) {
@@ -1021,22 +1008,14 @@ static int layer_forward_streamed(qmoe_ctx *c, int layer, const void *x, int xbf
                                   float *out, int residual, float *hyper, const float *inject,
                                   void *stream, qmoe_err *err);
 
-/* the layer of resident weights W on the stages of e; dec_fused selects
- * the one-launch one-token path (needs the hand-off block in e's scratch) */
-static int layer_core(const stage_env *e, const qmoe_layer_weights *W, int dec_fused, int hc,
+/* the layer of resident weights W on the stages of e */
+static int layer_core(const stage_env *e, const qmoe_layer_weights *W, int hc,
                       const void *x, int xbf, int n, float *out, int residual, float *hyper,
                       const float *inject, void *stream, qmoe_err *err) {
     const qk_shape s = e->s;
     qk_scratch *sc = e->sc;
     int rc;
     float *xn = W->norm_w ? sc->xn : NULL;
-    if (n == 1 && sc->rep && dec_fused) {
-        /* one token: the whole layer in one launch */
-        rc = qk_launch_dec_layer(W, s, x, xbf, sc->logits, sc->xn, sc->h, sc->rep, sc->status,
-                                 sc->idx, sc->w, sc->sg, sc->perm, sc->pos, sc->segtab,
-                                 residual ? x : NULL, out, hyper, inject, hc, stream);
-        return hip_fail(err, rc, "one-token layer");
-    }
     const void *xf = W->norm_w ? (const void *)sc->xn : x;
     const int xf_bf = W->norm_w ? 0 : xbf;
     /* many tokens: router + top-k on MFMA with the exact logits of the
@@ -1103,7 +1082,7 @@ static int layer_forward(qmoe_ctx *c, int layer, const void *x, int xbf, int n, 
         return layer_forward_streamed(c, layer, x, xbf, n, out, residual, hyper, inject, stream, err);
     c->last_n = n;
     const stage_env e = ctx_env(c);
-    return layer_core(&e, &c->layers[layer].dev, c->dec_fused, hyper ? c->hc : 0, x, xbf, n, out,
+    return layer_core(&e, &c->layers[layer].dev, hyper ? c->hc : 0, x, xbf, n, out,
                       residual, hyper, inject, stream, err);
 }
 
@@ -1139,7 +1118,7 @@ int qmoe_layer_forward_noalloc(const qmoe_config *cfg, const qmoe_layer_weights 
     NEED(out, "out");
     const qk_shape s = {cfg->hidden, cfg->n_experts, cfg->top_k, cfg->moe_inter, cfg->rms_eps};
     size_t offs[QH_SC_COUNT];
-    const size_t bytes = scratch_plan(s, (size_t)n, 0, offs);
+    const size_t bytes = scratch_plan(s, (size_t)n, offs);
     if (bytes > QK_NOALLOC_SCRATCH_BYTES) {
         set_err(err, "n = %d needs %zu bytes of scratch at this shape; the static scratch holds %zu "
                      "(call with fewer tokens)", n, bytes, (size_t)QK_NOALLOC_SCRATCH_BYTES);
@@ -1148,48 +1127,10 @@ int qmoe_layer_forward_noalloc(const qmoe_config *cfg, const qmoe_layer_weights 
     void *base = NULL;
     if (hip_fail(err, qk_noalloc_scratch(&base), "static scratch address")) return -1;
     qk_scratch sc;
-    scratch_bind(&sc, (char *)base, offs, 0);
+    scratch_bind(&sc, (char *)base, offs);
     const stage_env e = {s, &sc, NULL, NULL, NULL}; /* every stage on `stream` */
-    return layer_core(&e, w, 0, 0, x, x_dtype == QMOE_BF16, n, out, (flags & QMOE_RESIDUAL) != 0,
+    return layer_core(&e, w, 0, x, x_dtype == QMOE_BF16, n, out, (flags & QMOE_RESIDUAL) != 0,
                       NULL, NULL, stream, err);
-}
-
-int qmoe_set_fused_decode(qmoe_ctx *c, int enable, qmoe_err *err) {
-    clear_err(err);
-    if (!c) {
-        set_err(err, "ctx is NULL");
-        return -1;
-    }
-    if (enable && !c->sc.rep) {
-        set_err(err, "the one-launch one-token layer does not take this shape (hidden %d, "
-                     "n_experts %d, top_k %d, moe_inter %d)", c->cfg.hidden, c->cfg.n_experts,
-                c->cfg.top_k, c->cfg.moe_inter);
-        return -1;
-    }
-    c->dec_fused = enable != 0;
-    return 0;
-}
-
-int qmoe_decode_status(qmoe_ctx *c, uint32_t *flags, qmoe_err *err) {
-    clear_err(err);
-    if (!c || !flags) {
-        set_err(err, "%s is NULL", c ? "flags" : "ctx");
-        return -1;
-    }
-    *flags = 0;
-    if (hip_fail(err, (int)hipDeviceSynchronize(), "synchronise") ||
-        hip_fail(err, (int)hipMemcpy(flags, c->sc.status, 4, hipMemcpyDeviceToHost), "read status"))
-        return -1;
-    if (*flags == 0) return 0;
-    /* a wait expired: zero the hand-off block (epoch, counter, tagged words) and clear
-     * the status, so later one-token calls start from a clean hand-off */
-    if ((c->sc.rep && hip_fail(err, (int)hipMemset(c->sc.rep, 0, qk_dec_handoff_bytes(c->shape)),
-                               "reset hand-off")) ||
-        hip_fail(err, (int)hipMemset(c->sc.status, 0, 4), "clear status"))
-        return -1;
-    set_err(err, "a one-token layer call waited past its bound for h (flags 0x%x); its output "
-                 "was NaN; the hand-off state is reset", *flags);
-    return -1;
 }
 
 int qmoe_layer_forward(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n, float *out,

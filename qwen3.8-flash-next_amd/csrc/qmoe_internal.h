@@ -46,8 +46,6 @@ typedef struct {
     uint32_t *bits;    /* [E, ceil(n/32)] token membership bitmask (large dispatch) */
     int32_t *wprefix;  /* [E, ceil(n/32)] per-word exclusive popcount prefix */
     float *xn;         /* [n, H] normalised router input */
-    void *rep;         /* one-token hand-off block (qk_dec_handoff_bytes) or NULL */
-    uint32_t *status;  /* [1] expired waits of the one-token launch */
     float *h;          /* [n*k+n, I] */
     float *y;          /* [n*k+n, H] */
 } qk_scratch;
@@ -195,22 +193,6 @@ int qk_launch_down_combine(const qmoe_layer_weights *W, qk_shape s, const float 
 int qk_launch_combine(qk_shape s, int n, const float *y, const int32_t *pos, const float *w,
                       const float *sg, const void *x_res, int x_bf16, float *out, float *hyper,
                       const float *inject, int hc, void *stream);
-
-/* one token in one launch (decode_layer.hip): router, shared and routed
- * gate/up, down + combine, handing the logits and h over inside the launch
- * through tagged words in `handoff` (qk_dec_handoff_bytes, zero before the
- * first call) and recording an expired wait in *status.  Bit-identical to
- * the staged kernels. */
-#define QK_DEC_WAIT_TICKS 2000000ull /* 20 ms of the 100 MHz s_memrealtime clock */
-#define QK_DEC_ERR_WAIT 1u
-int qk_dec_supported(qk_shape s);
-size_t qk_dec_lds(qk_shape s);
-size_t qk_dec_handoff_bytes(qk_shape s);
-int qk_launch_dec_layer(const qmoe_layer_weights *W, qk_shape s, const void *x, int x_bf16,
-                        float *logits, float *xn, float *h, void *handoff, uint32_t *status,
-                        int32_t *idx, float *w, float *sg, int32_t *perm, int32_t *pos,
-                        int32_t *segtab, const void *x_res, float *out, float *hyper,
-                        const float *inject, int hc, void *stream);
 
 /* the gated DeltaNet mixer (deltanet.hip) */
 typedef struct {

@@ -139,7 +139,6 @@ SIGNATURES = {
     "qmoe_layer_forward_noalloc": (_I, [ctypes.POINTER(QmoeConfig), ctypes.POINTER(QmoeLayerWeights), _P,
                                         _I, _I, _P, _I, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_moe_forward_host": (_I, [_P, _I, _P, _I, _P, ctypes.POINTER(QmoeErr)]),
-    "qmoe_set_fused_decode": (_I, [_P, _I, ctypes.POINTER(QmoeErr)]),
     "qmoe_attn_create": (_I, [ctypes.POINTER(_P), ctypes.POINTER(QmoeAttnConfig), ctypes.POINTER(QmoeErr)]),
     "qmoe_attn_destroy": (None, [_P]),
     "qmoe_attn_upload_layer": (_I, [_P, _I, ctypes.POINTER(QmoeAttnWeights), ctypes.POINTER(QmoeErr)]),
@@ -160,7 +159,6 @@ SIGNATURES = {
     "qmoe_dn_reset_state": (_I, [_P, _I, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_dn_forward": (_I, [_P, _I, _P, _I, _P, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_dn_state": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(_P), ctypes.POINTER(QmoeErr)]),
-    "qmoe_decode_status": (_I, [_P, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(QmoeErr)]),
     "qmoe_last_routing": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_scratch_bytes": (ctypes.c_size_t, [_P]),
     "qmoe_layer_bytes": (ctypes.c_size_t, [_P]),
@@ -497,22 +495,6 @@ class MoeContext:
         rc = lib().qmoe_layer_forward(self._h, layer, x_ptr, x_dtype, n, out_ptr, flags,
                                       stream_handle, ctypes.byref(err))
         return rc, err.msg.decode(errors="replace")
-
-    def set_fused_decode(self, enable: bool):
-        """one-token calls in one launch (True) or through the staged
-        kernels (False, the default); the outputs are bit-identical"""
-        err = QmoeErr()
-        _check(lib().qmoe_set_fused_decode(self._h, 1 if enable else 0, ctypes.byref(err)), err,
-               "qmoe_set_fused_decode")
-
-    def decode_status(self):
-        """synchronises; raises QmoeError if a one-launch one-token call gave
-        up its wait for h since the last check (its outputs were NaN)"""
-        flags = ctypes.c_uint32(0)
-        err = QmoeErr()
-        _check(lib().qmoe_decode_status(self._h, ctypes.byref(flags), ctypes.byref(err)), err,
-               "qmoe_decode_status")
-        return int(flags.value)
 
     def last_routing(self, n, stream=None):
         """routing of the last layer_forward call (device tensors)"""

@@ -588,7 +588,7 @@ def test_limits_k64_e1024_small_dims(torch_dev):
                                           (300, False, False)])
 def test_fallback_shape_at_scale(torch_dev, n, x_bf16, norm):
     """hidden 1536 (3 * 512) takes none of the routers' and the one-token
-    fast paths: not the one-token gate/up with top-k nor the one-launch layer
+    fast paths: not the one-token gate/up with top-k
     (H/32 is not a power of two), not the tiled or the MFMA router (their
     instances are for hidden 512, 1024, 2048; both once took 1536 and read
     its rows with the 2048 stride); the grouped GEMMs take it on MFMA.
