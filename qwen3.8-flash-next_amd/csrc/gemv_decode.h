@@ -70,7 +70,8 @@ struct DecRouteOut {
  *         router logits themselves (wave 0, WaveTopk<PL>, broadcast through
  *         LDS) instead of waiting for a separate top-k launch.  Segment j
  *         computes the expert of slot j-1: wave 0 runs the selection rounds
- *         up to that slot, every wave starts its weight loads, and wave 0
+ *         (two slots a round) up to that slot, every wave starts its weight
+ *         loads, and wave 0
  *         runs the remaining rounds under the loads to find the expert's
  *         dispatch position (its rank among the selected ids), which only
  *         the stores need.  Workgroup (segment 1, block 0) writes the
@@ -121,16 +122,21 @@ __global__ __launch_bounds__(256) void k_gateup_dec(DecArgs a, const int32_t *__
         if (!shared) {
             if (wave == 0) {
                 tks.init(ro.logits, a.E, lane);
+                /* two slots a round, up to the round that yields this slot */
                 int es = 0;
-                for (int r = 0; r <= slot; r++) {
-                    uint32_t m;
-                    int ei;
-                    tks.next(lane, m, ei);
-                    if (lane == r) {
-                        my_key = m;
-                        my_id = ei;
+                for (int r = 0; 2 * r <= slot; r++) {
+                    uint32_t m1, m2;
+                    int ea, eb;
+                    tks.next2(lane, m1, ea, m2, eb);
+                    if (lane == 2 * r) {
+                        my_key = m1;
+                        my_id = ea;
                     }
-                    es = ei;
+                    if (lane == 2 * r + 1 && 2 * r + 1 < a.k) {
+                        my_key = m2;
+                        my_id = eb;
+                    }
+                    es = (2 * r == slot) ? ea : eb;
                 }
                 if (lane == 0) s_ep[0] = es;
             }
@@ -179,15 +185,7 @@ __global__ __launch_bounds__(256) void k_gateup_dec(DecArgs a, const int32_t *__
     if (TK > 0 && !shared) {
         /* under the loads: the remaining rounds, then this slot's rank */
         if (wave == 0) {
-            for (int r = slot + 1; r < a.k; r++) {
-                uint32_t m;
-                int ei;
-                tks.next(lane, m, ei);
-                if (lane == r) {
-                    my_key = m;
-                    my_id = ei;
-                }
-            }
+            topk_rounds(tks, slot / 2 + 1, (a.k + 1) / 2, a.k, lane, my_key, my_id);
             const int rank = (int)__popcll(__ballot(my_id < e));
             if (lane == 0) s_ep[1] = rank;
             if (seg == 1 && rb == 0) {

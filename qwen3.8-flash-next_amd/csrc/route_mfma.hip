@@ -403,15 +403,7 @@ __global__ __launch_bounds__(256) void k_rt_exact(RtExactArgs a) {
         for (int i = 0; i < PL; i++) lv[i] = row[lane * PL + i];
         WaveTopk<PL> st;
         st.init_vals(lv, E, lane);
-        for (int r = 0; r < a.k; r++) {
-            uint32_t m;
-            int e;
-            st.next(lane, m, e);
-            if (lane == r) {
-                my_key = m;
-                my_id = e;
-            }
-        }
+        topk_rounds(st, 0, (a.k + 1) / 2, a.k, lane, my_key, my_id);
     }
     const float my_w = topk_weight(my_key, a.k, lane);
     if (lane < a.k) {
