@@ -495,6 +495,122 @@ def bench_attention(pkg, torch, layers, steps, warmup, context=AT_CONTEXT):
     return sec
 
 
+def hc_token_bytes(d, hc, R, inject):
+    """algorithmic HBM bytes of one token through one hyper connection
+    (gated_residual): the q4 down [R, hc*d] and up [hc*d, R] mix matrices,
+    the f32 hc_norm, the bf16 inject matrix [hc, hc*d] when the connection
+    has one, the hyper state read, the mixed row written and, with inject,
+    the update's read and write of the hyper state"""
+    q4 = lambda rows, cols: rows * cols // 2 + rows * (cols // 64) * 4
+    b = q4(R, hc * d) + q4(hc * d, R) + hc * d * 4 + hc * d * 4 + d * 4
+    if inject:
+        b += hc * hc * d * 2 + 2 * hc * d * 4
+    return b
+
+
+STACK_LAYERS = 48  # the model's text stack: DeltaNet : attention = 3 : 1
+STACK_CONTEXT = 4096  # cached tokens in each attention layer before the timed tokens
+
+
+def stack_token_bytes(w, layers, context):
+    """algorithmic HBM bytes of one token through the decoder stack: per
+    layer the attention-block hyper connection, its mixer (DeltaNet or
+    attention at `context` cached), the MLP hyper connection and the MoE
+    layer on the f32 mixed row; then the final mixer"""
+    types = [("attn" if (l + 1) % 4 == 0 else "dn") for l in range(layers)]
+    moe = layer_token_bytes(w) + 2 * w.hidden  # f32 mixed row in instead of bf16
+    total = 0
+    for t in types:
+        total += hc_token_bytes(w.hidden, HC_COUNT, HC_LOWRANK, True) * 2 + moe
+        total += dn_token_bytes(DN_SHAPE) if t == "dn" else at_token_bytes(AT_SHAPE, context)
+    return total + hc_token_bytes(w.hidden, HC_COUNT, HC_LOWRANK, False)
+
+
+def bench_stack(pkg, torch, w, tokens, warmup, layers=STACK_LAYERS, context=STACK_CONTEXT):
+    """one token per step through the decoder stack (qmoe.DecoderStack): 48
+    layers, gated DeltaNet and full attention at 3 : 1, both hyper
+    connections of every layer (hc 4, rank 320), the MoE layers of the
+    decode workload (hidden 2048, 512 experts top-10, all resident), and the
+    final mixer.  The attention layers' caches are first filled with
+    `context` tokens (their mixer alone, random inputs); the DeltaNet
+    states start empty.  `warmup` eager tokens, then `tokens` tokens
+    captured in one HIP graph, replayed once untimed, then timed.  Random
+    weights (device synthesis for the MoE and MLP hyper layers, numpy for
+    the mixers and the attention-block hyper connections, the same host
+    arrays in every slot).  Returns seconds per token."""
+    import numpy as np
+    types = pkg.decoder_layer_types(layers)
+    d = w.hidden
+    rng = np.random.default_rng(3)
+    bf = lambda n, std: ((rng.normal(0, std, n).astype(np.float32).view(np.uint32) + 0x8000) >> 16).astype(np.uint16)
+    codes = lambda n: rng.integers(0, 2**32, n, dtype=np.uint32)
+    chunk = 256
+    moe = pkg.MoeContext.for_workload(w, n_layers=layers, max_tokens=chunk)
+    moe.hc_enable(HC_COUNT, HC_LOWRANK)
+    for l in range(layers):
+        moe.synth_layer(l, w.seed)
+        moe.hc_synth_layer(l, w.seed)
+    hcd = HC_COUNT * d
+    ghost = dict(hc_norm=(1 + rng.normal(0, 0.1, hcd)).astype(np.float32),
+                 down_q=codes(HC_LOWRANK * hcd // 8), down_s=bf(HC_LOWRANK * hcd // 64, 0.02),
+                 down_b=bf(HC_LOWRANK * hcd // 64, 0.01), up_q=codes(hcd * HC_LOWRANK // 8),
+                 up_s=bf(hcd * HC_LOWRANK // 64, 0.02), up_b=bf(hcd * HC_LOWRANK // 64, 0.01),
+                 inject_w=bf(HC_COUNT * hcd, 0.02))
+    gr = pkg.GatedResidualContext(d, HC_COUNT, HC_LOWRANK, n_slots=layers + 1, max_tokens=chunk)
+    for l in range(layers):
+        gr.upload_slot(l, ghost)
+    gr.upload_slot(layers, {k: v for k, v in ghost.items() if k != "inject_w"})
+    _, hk, hv, dk, dv, kc = DN_SHAPE
+    kd, vd = hk * dk, hv * dv
+    cd = 2 * kd + vd
+    dnw = dict(qkv_q=codes(cd * d // 8), qkv_s=bf(cd * d // 64, 0.02), qkv_b=bf(cd * d // 64, 0.01),
+               z_q=codes(vd * d // 8), z_s=bf(vd * d // 64, 0.02), z_b=bf(vd * d // 64, 0.01),
+               a_w=bf(hv * d, 0.02), b_w=bf(hv * d, 0.02),
+               out_q=codes(d * vd // 8), out_s=bf(d * vd // 64, 0.02), out_b=bf(d * vd // 64, 0.01),
+               conv_w=bf(cd * kc, 0.5), norm_w=(1 + rng.normal(0, 0.1, dv)).astype(np.float32),
+               a_log=rng.normal(0, 1, hv).astype(np.float32), dt_bias=rng.normal(0, 1, hv).astype(np.float32))
+    dn = pkg.DeltaNetContext(d, hk, hv, dk, dv, kc, n_layers=layers, max_tokens=chunk)
+    _, h, kvh, hd, ih, ihd, budget, comp = AT_SHAPE
+    q4 = lambda rows, cols: (codes(rows * cols // 8), bf(rows * cols // 64, 0.02), bf(rows * cols // 64, 0.01))
+    atw = {}
+    for nm, (rows, cols) in (("q", (2 * h * hd, d)), ("k", (kvh * hd, d)), ("v", (kvh * hd, d)), ("o", (d, h * hd))):
+        atw[nm + "_q"], atw[nm + "_s"], atw[nm + "_b"] = q4(rows, cols)
+    atw["idx_w"] = bf((ih + 1) * ihd * d, 0.02)
+    for nm, n in (("q_norm", hd), ("k_norm", hd), ("idx_q_norm", ihd), ("idx_k_norm", ihd)):
+        atw[nm] = (1 + rng.normal(0, 0.1, n)).astype(np.float32)
+    cap = context + warmup + tokens + chunk
+    at = pkg.AttentionContext(d, h, kvh, hd, ih, ihd, budget, comp, kv_cap=cap, n_layers=layers,
+                              max_tokens=chunk)
+    xs = torch.randn((chunk, d), device="cuda") * 0.5
+    for l, t in enumerate(types):
+        if t == "dn":
+            dn.upload_layer(l, dnw)
+        else:
+            at.upload_layer(l, atw)
+            for t0 in range(0, context, chunk):
+                at.forward(l, xs, t0)
+    torch.cuda.synchronize()
+    stack = pkg.DecoderStack(gr, moe, dn, at, types, 1)
+    hyper = torch.empty((1, hcd), dtype=torch.float32, device="cuda")
+    pkg.synth_fill(hyper, 1, 78, 0, pkg.TAGS["HYPER"], stddev=1.0)
+    for i in range(warmup):
+        stack.step(hyper, context + i)
+    torch.cuda.synchronize()
+
+    def run():
+        for i in range(tokens):
+            stack.step(hyper, context + warmup + i)
+    g = capture(torch, run, warm=False)
+    time_graph(torch, g, GRAPH_WARM_REPLAYS)
+    sec = time_graph(torch, g, 1) / tokens
+    ok = bool(torch.isfinite(stack.final).all().item())
+    for c in (moe, gr, dn, at):
+        c.close()
+    if not ok:
+        raise RuntimeError("decoder stack output is not finite")
+    return sec
+
+
 def bench_depth(pkg, torch, w, tokens, warmup):
     """48 stacked layers, one token: h <- h + MoE(RMSNorm(h)) layer after
     layer (f32 residual stream), captured as one graph per token; returns
@@ -715,6 +831,9 @@ def main():
     ap.add_argument("--stream", default="16,64,16", metavar="LAYERS,SLOTS,PREFETCH",
                     help="also time Zipf decode with streamed experts (pinned host store, SLOTS "
                          "of 512 HBM expert slots per layer); empty: skip")
+    ap.add_argument("--stack", type=int, default=1,
+                    help=f"also time one token through the {STACK_LAYERS}-layer decoder stack "
+                         f"(DeltaNet : attention 3 : 1, hyper connections, final mixer; 0: skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 8 plain copies of MIB MiB (counter calibration) and exit")
     args = ap.parse_args()
@@ -798,6 +917,20 @@ def main():
         log(f"{name}: {s_e * 1e3:.4f} ms/step -> {we.n_tokens / s_e:.0f} tokens/s")
         free(torch, st)
         del st
+    if args.stack:
+        ws = pkg.WORKLOADS["decode"]
+        s_s = bench_stack(pkg, torch, ws, 20, 4)
+        b = stack_token_bytes(ws, STACK_LAYERS, STACK_CONTEXT)
+        extra["decoder_stack"] = dict(
+            us_per_token=s_s * 1e6, tokens_per_s=1.0 / s_s, layers=STACK_LAYERS,
+            deltanet_layers=sum(1 for l in range(STACK_LAYERS) if (l + 1) % 4),
+            attention_context=STACK_CONTEXT, tokens=20, algorithmic_bytes_per_token=b,
+            hbm_fraction=round(b / s_s / 1e9 / HBM_PEAK_GBS, 4),
+            note="one f32 hyper-state token through 48 decoder layers (attention-block hyper "
+                 "connection, gated DeltaNet or QSA attention at 3 : 1, inject, MLP hyper connection "
+                 "+ MoE layer + inject) and the final mixer, 20 tokens in one HIP graph")
+        log(f"decoder stack: {s_s * 1e6:.1f} us/token -> {b / s_s / 1e9:.0f} GB/s")
+        torch.cuda.empty_cache()
     if args.deltanet:
         nl = 16
         s_d = bench_deltanet(pkg, torch, nl, 256, 32)

@@ -964,6 +964,52 @@ class GatedResidualContext:
         return hyper
 
 
+def decoder_layer_types(n_layers, full_attention_interval=4):
+    """per-layer mixer kinds of the model's text stack: every
+    full_attention_interval-th layer full attention, the others gated
+    DeltaNet (src/colibri_runtime/model.py:138-143, c/src/model.c:124)"""
+    return ["attn" if (l + 1) % full_attention_interval == 0 else "dn" for l in range(n_layers)]
+
+
+class DecoderStack:
+    """The decoder layer loop of model_forward (c/src/model.c:1644-1745) on
+    the library's parts, for n tokens of hyper state [n, hc*d] f32 updated
+    in place.  Layer l: the attention block's hyper connection (slot l of
+    `gr`: gated_residual with inject, model.c:1671-1672), its mixer (gated
+    DeltaNet, layer l of `dn`, or full attention with the QSA indexer,
+    layer l of `at`, at positions offset..), the inject update hyper +=
+    inject (x) out (model.c:1699-1707), then the MLP hyper connection, the
+    MoE layer and its inject update (layer l of `moe`,
+    qmoe_hc_layer_forward, model.c:1710-1731).  After the last layer the
+    final mixer (slot len(types) of `gr`, no inject, model.c:1743-1745)
+    gives the LM head's input.  Buffers are allocated once, so a HIP graph
+    can capture step()."""
+
+    def __init__(self, gr, moe, dn, at, types, n, device="cuda"):
+        import torch
+        self.gr, self.moe, self.dn, self.at, self.types = gr, moe, dn, at, list(types)
+        d, hc = gr.d, gr.hc
+        self.mixed = torch.empty((n, d), dtype=torch.float32, device=device)
+        self.inject = torch.empty((n, hc), dtype=torch.float32, device=device)
+        self.out = torch.empty((n, d), dtype=torch.float32, device=device)
+        self.final = torch.empty((n, d), dtype=torch.float32, device=device)
+
+    def step(self, hyper, offset):
+        """hyper [n, hc*d] at positions offset.. through every layer; returns
+        the final mixer's output [n, d] (a buffer reused by the next step)"""
+        L = len(self.types)
+        for l, t in enumerate(self.types):
+            self.gr.mix(l, hyper, mixed=self.mixed, inject=self.inject, want_inject=True)
+            if t == "dn":
+                self.dn.forward(l, self.mixed, out=self.out)
+            else:
+                self.at.forward(l, self.mixed, offset, out=self.out)
+            self.gr.inject(self.inject, self.out, hyper)
+            self.moe.hc_layer_forward(l, hyper, want_out=False)
+        self.gr.mix(L, hyper, mixed=self.final, want_inject=False)
+        return self.final
+
+
 def synth_fill(t, kind: int, seed: int, layer: int, tag: int, start=0, stddev=1.0, stream=None):
     """fill a torch CUDA tensor with a synthetic stream (kind 0 bf16 normal, 1 f32 normal, 2 codes)"""
     err = QmoeErr()

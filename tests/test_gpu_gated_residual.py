@@ -266,3 +266,36 @@ def test_layer_loop(torch_dev, shape, types, calls, seed):
             off += n
     finally:
         ch.close()
+
+
+def test_decoder_stack(torch_dev):
+    """the benchmark's decoder stack (qmoe.DecoderStack: gated DeltaNet and
+    full attention at 3 : 1 by the model's layer types, both hyper
+    connections of every layer, the final mixer) at 4 of its 48 layers and
+    the model's shapes, end to end against the oracle's own chain from the
+    same hyper states: a 4-token prefill call, then one-token calls.  The
+    final mixer output and the hyper state after the last layer within
+    2e-2 max-abs and 1e-3 relative L2."""
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    types = tuple(pkg.decoder_layer_types(4))
+    assert types == ("dn", "dn", "dn", "attn")
+    seed, calls = 5, (4, 1, 1)
+    say(f"case: decoder stack {types} calls {calls}")
+    ch = Chain(torch, dev, MODEL, types, seed, max(calls))
+    try:
+        h0 = orc.gen_hyper(sum(calls), MODEL["hc"], MODEL["d"], seed=seed + 70)
+        off = 0
+        for i, n in enumerate(calls):
+            tag = f"stack call {i} (n={n}, offset {off})"
+            stack = pkg.DecoderStack(ch.gr, ch.ctx, ch.dn, ch.at, types, n)
+            h = torch.from_numpy(h0[off:off + n].copy()).to(dev)
+            fin = stack.step(h, off)
+            torch.cuda.synchronize()
+            ref, href, _ = ch.step_oracle(h0[off:off + n], off)
+            assert_close(fin.cpu().numpy(), ref, f"{tag} final mixer")
+            assert_close(h.cpu().numpy(), href, f"{tag} hyper state")
+            say(f"{tag}: final mixer and hyper state within bounds")
+            off += n
+    finally:
+        ch.close()
