@@ -511,9 +511,10 @@ int qmoe_dn_state(qmoe_dn_ctx *ctx, int layer, float **conv_state, float **rec_s
  *   blocks and the token's own block tail kept            (model.c:969-1104)
  *   softmax, weighted sum of v, * sigmoid(gate), o_proj   (model.c:1107-1143)
  * The caches live in HBM with the layer, kv_cap rows; a call that would pass
- * kv_cap is refused (the reference drops the oldest rows of its v and
+ * kv_cap is refused, or with slide = 1 drops the oldest rows of all three
+ * caches together (the reference drops the oldest rows of its v and
  * indexer caches there but not of its k cache, model.c:815-821, 862-867,
- * 921; that is not reproduced).  Block selection ties go to the lower
+ * 921, which misaligns k and v; that is not reproduced).  Block selection ties go to the lower
  * block (the reference's quickselect leaves their order open).  The
  * indexer path runs in the reference's sequential orders (index_qk_proj in
  * the router's fixed R64 order), so block scores and kept blocks equal the
@@ -540,6 +541,14 @@ typedef struct {
     int max_position;  /* positions offset + t stay below max(max_position, kv_cap); 0: kv_cap.
                         * The RoPE table (cos, sin per position) is computed on the host at
                         * create with the reference's formula; at most QMOE_ATTN_MAX_POSITION */
+    int slide;         /* 0: a call past kv_cap is refused.  1: sliding window -- a call that
+                        * would pass kv_cap first drops the oldest rows of the k, v and
+                        * indexer-key caches together (and the pooled keys of the blocks they
+                        * made), a multiple of idx_compress of them so blocks stay aligned;
+                        * positions are absolute, calls continue at position window start +
+                        * cached rows, and kv_cap must be a multiple of idx_compress.  Unlike
+                        * the reference's drop (model.c:815-821, 862-867), k stays aligned
+                        * with v. */
 } qmoe_attn_config;
 
 #define QMOE_ATTN_MAX_POSITION (1 << 20)
@@ -570,8 +579,9 @@ int qmoe_attn_reset(qmoe_attn_ctx *ctx, int layer, qmoe_err *err);
  * cache length is host state, so calls on one layer run in call order. */
 int qmoe_attn_forward(qmoe_attn_ctx *ctx, int layer, const float *x, int n, int offset, float *out,
                       void *stream, qmoe_err *err);
-/* device addresses of a layer's caches (k and v [kv_cap, kvh*hd], indexer
- * keys [kv_cap, idx_hd]) and their current length */
+/* device addresses of a layer's caches (k and v [len, kvh*hd], indexer
+ * keys [len, idx_hd]; with slide, the window's first row) and their current
+ * length */
 int qmoe_attn_cache(qmoe_attn_ctx *ctx, int layer, float **k_cache, float **v_cache, float **idx_keys,
                     int *len, qmoe_err *err);
 /* device addresses of the QSA indexer's state, for inspection (the values

@@ -60,7 +60,28 @@ int orc_attn_forward_dbg(const orc_attn *A, orc_attn_state *S, const float *x, i
     if (n <= 0) return 0;
     /* past the capacity the reference drops the oldest rows of the v and
      * indexer caches but not of the k cache (model.c:815-821, 862-867,
-     * 921); only calls that fit are restated */
+     * 921), which misaligns k and v.  Without slide only calls that fit
+     * are restated; with slide the oldest rows of all three caches go
+     * together, idx_compress rows at a time, and positions are absolute
+     * (base + row) */
+    int pos0 = 0;
+    if (A->slide) {
+        if (offset != S->base + S->kv_len || S->kv_len != S->idx_len) return -3;
+        if (S->kv_len + n > cap) {
+            const int over = S->kv_len + n - cap;
+            const int drop = (over + A->idx_compress - 1) / A->idx_compress * A->idx_compress;
+            if (drop > S->kv_len) return -2;
+            const size_t kr = (size_t)kvh * hd;
+            memmove(S->k_cache, S->k_cache + (size_t)drop * kr, (size_t)(S->kv_len - drop) * kr * sizeof(float));
+            memmove(S->v_cache, S->v_cache + (size_t)drop * kr, (size_t)(S->kv_len - drop) * kr * sizeof(float));
+            memmove(S->idx_keys, S->idx_keys + (size_t)drop * ihd,
+                    (size_t)(S->idx_len - drop) * ihd * sizeof(float));
+            S->kv_len -= drop;
+            S->idx_len -= drop;
+            S->base += drop;
+        }
+        pos0 = S->base;
+    }
     if (S->kv_len + n > cap || S->idx_len + n > cap) return -2;
     float *qk = (float *)malloc((size_t)n * qkw * sizeof(float));
     float *qbuf = (float *)malloc((size_t)n * h * hd * 2 * sizeof(float));
@@ -139,7 +160,7 @@ int orc_attn_forward_dbg(const orc_attn *A, orc_attn_state *S, const float *x, i
             rmsnorm_w(tmp, A->idx_k_norm, ihd, pooled + (size_t)b * ihd);
             float bc[512], bs[512];
             for (int i = 0; i < rot / 2; i++) {
-                const float ang = (float)(b * comp) * inv[i];
+                const float ang = (float)(pos0 + b * comp) * inv[i];
                 bc[i] = cosf(ang);
                 bs[i] = sinf(ang);
             }
@@ -168,7 +189,7 @@ int orc_attn_forward_dbg(const orc_attn *A, orc_attn_state *S, const float *x, i
                     acc = acc + dot;
                 }
                 bsc[b] = acc / sqrtf((float)ihd);
-                if ((long long)b * comp + comp - 1 > (long long)offset + t) bsc[b] = -INFINITY;
+                if ((long long)pos0 + (long long)b * comp + comp - 1 > (long long)offset + t) bsc[b] = -INFINITY;
             }
             /* kernel_topk_indices (quickselect) fixes the k-th largest
              * score T; the blocks above T are kept whichever way it
@@ -201,15 +222,15 @@ int orc_attn_forward_dbg(const orc_attn *A, orc_attn_state *S, const float *x, i
                 float acc = 0.0f;
                 for (int i = 0; i < hd; i++) acc = fmaf(q[i], k[i], acc);
                 sc[kk] = acc * (1.0f / sqrtf((float)hd));
-                if (kk > offset + t) sc[kk] = -INFINITY;
+                if (pos0 + kk > offset + t) sc[kk] = -INFINITY;
             }
             if (use_idx) {
                 const long long own_start = ((long long)(offset + t + 1) / comp) * comp;
                 for (int kk = 0; kk < kv_total; kk++) {
                     const int blk = kk / comp;
                     int keep = blk < n_blocks && keep_blk[blk];
-                    if (kk >= own_start && kk <= offset + t) keep = 1;
-                    if (!keep && kk <= offset + t) sc[kk] = -INFINITY;
+                    if (pos0 + kk >= own_start && pos0 + kk <= offset + t) keep = 1;
+                    if (!keep && pos0 + kk <= offset + t) sc[kk] = -INFINITY;
                 }
             }
             /* kernel_softmax (kernel.c:61-71) */

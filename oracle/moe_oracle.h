@@ -252,14 +252,21 @@ typedef struct {
     const uint16_t *idx_w;                              /* index_qk_proj [idx_heads*idx_hd + idx_hd, d] bf16 */
     const float *q_norm, *k_norm;                       /* [hd] */
     const float *idx_q_norm, *idx_k_norm;               /* [idx_hd] */
+    int slide; /* 0: refuse calls past kv_cap; 1: sliding window (see orc_attn_forward) */
 } orc_attn;
 typedef struct {
     float *k_cache, *v_cache; /* [kv_cap, kvh*hd] */
     float *idx_keys;          /* [kv_cap, idx_hd] */
     int kv_len, idx_len;
+    int base;                 /* sliding window: position of cache row 0 */
 } orc_attn_state;
 /* x [n, d] f32 at positions offset.. -> out [n, d]; appends to the caches;
- * -2 when the call would pass the cache capacity */
+ * -2 when the call would pass the cache capacity.  With slide, a call that
+ * would pass it first drops the oldest rows of the k, v and indexer-key
+ * caches together, a multiple of idx_compress of them (so blocks stay
+ * aligned), and base advances by as many; every mask and block position
+ * is then the absolute position base + row, and offset must equal base +
+ * kv_len (-3 otherwise; -2 when the drop would exceed the cached rows) */
 int orc_attn_forward(const orc_attn *A, orc_attn_state *S, const float *x, int n, int offset,
                      float *out);
 /* optional copies of the indexer's intermediate values, written when the

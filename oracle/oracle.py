@@ -81,11 +81,13 @@ class OrcAttn(ctypes.Structure):
         ("q_q", _P), ("q_s", _P), ("q_b", _P), ("k_q", _P), ("k_s", _P), ("k_b", _P),
         ("v_q", _P), ("v_s", _P), ("v_b", _P), ("o_q", _P), ("o_s", _P), ("o_b", _P),
         ("idx_w", _P), ("q_norm", _P), ("k_norm", _P), ("idx_q_norm", _P), ("idx_k_norm", _P),
+        ("slide", _I),
     ]
 
 
 class OrcAttnState(ctypes.Structure):
-    _fields_ = [("k_cache", _P), ("v_cache", _P), ("idx_keys", _P), ("kv_len", _I), ("idx_len", _I)]
+    _fields_ = [("k_cache", _P), ("v_cache", _P), ("idx_keys", _P), ("kv_len", _I), ("idx_len", _I),
+                ("base", _I)]
 
 
 class OrcAttnDbg(ctypes.Structure):
@@ -554,7 +556,8 @@ class Attention:
             "idx_w", "q_norm", "k_norm", "idx_q_norm", "idx_k_norm")
 
     def __init__(self, d, h, kvh, hd, idx_heads, idx_hd, budget, compress, kv_cap=2048,
-                 rotary_factor=0.25, rope_theta=1e7, seed=0, layer=0, group_size=64):
+                 rotary_factor=0.25, rope_theta=1e7, seed=0, layer=0, group_size=64, slide=False):
+        self.slide = bool(slide)
         self.d, self.h, self.kvh, self.hd = d, h, kvh, hd
         self.ih, self.ihd, self.budget, self.compress = idx_heads, idx_hd, budget, compress
         self.cap, self.rf, self.theta, self.g = kv_cap, rotary_factor, rope_theta, group_size
@@ -585,6 +588,7 @@ class Attention:
         st.hidden, st.n_heads, st.n_kv_heads, st.head_dim = self.d, self.h, self.kvh, self.hd
         st.idx_heads, st.idx_head_dim, st.idx_budget, st.idx_compress = self.ih, self.ihd, self.budget, self.compress
         st.kv_cap, st.group_size, st.rotary_factor, st.rope_theta = self.cap, self.g, self.rf, self.theta
+        st.slide = 1 if getattr(self, "slide", False) else 0
         for f, a in self.t.items():
             setattr(st, f, _p(a))
         self.st = st
@@ -598,6 +602,7 @@ class Attention:
             self.v = np.zeros((A.cap, A.kvh * A.hd), np.float32)
             self.idx = np.zeros((A.cap, A.ihd), np.float32)
             self.len = 0
+            self.base = 0  # sliding window: position of row 0
 
     def new_state(self):
         return Attention.State(self)
@@ -610,8 +615,10 @@ class Attention:
         x = np.ascontiguousarray(x, dtype=np.float32)
         n = x.shape[0]
         out = np.empty((n, self.d), np.float32)
-        S = OrcAttnState(_p(state.k), _p(state.v), _p(state.idx), state.len, state.len)
+        S = OrcAttnState(_p(state.k), _p(state.v), _p(state.idx), state.len, state.len, state.base)
         kv = state.len + n
+        if self.slide and kv > self.cap:  # the window after the drop (a multiple of compress)
+            kv -= (kv - self.cap + self.compress - 1) // self.compress * self.compress
         extra = {}
         D = None
         if dbg and kv > self.budget:
@@ -625,9 +632,12 @@ class Attention:
                                         ctypes.byref(D) if D is not None else None)
         if rc == -2:
             raise ValueError("the call passes the cache capacity")
+        if rc == -3:
+            raise ValueError("a sliding call must continue at position base + cached rows")
         if rc:
             raise MemoryError("orc_attn_forward")
         state.len = S.kv_len
+        state.base = S.base
         return (out, extra) if dbg else out
 
 

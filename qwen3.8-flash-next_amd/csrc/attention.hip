@@ -246,7 +246,7 @@ struct AtPoolArgs {
     const float *ik_norm;   /* [ihd] */
     float *pooled;          /* [cap/comp, ihd] */
     const float2 *rope;     /* [positions, rot/2] (cos, sin) */
-    int ihd, comp, b0, b1, rot;
+    int ihd, comp, b0, b1, rot, pos0; /* pos0: position of cache row 0 */
 };
 
 /* one wave per block b in [b0, b1): mean of its comp keys, then rmsnorm +
@@ -263,7 +263,7 @@ __global__ __launch_bounds__(256) void k_at_pool(AtPoolArgs a) {
         pw[i] = acc / (float)a.comp;
     }
     qk_wave_lds_sync();
-    at_norm_rope(pw, a.ik_norm, a.ihd, a.rot, a.rope, b * a.comp, a.pooled + (size_t)b * a.ihd, lane);
+    at_norm_rope(pw, a.ik_norm, a.ihd, a.rot, a.rope, a.pos0 + b * a.comp, a.pooled + (size_t)b * a.ihd, lane);
 }
 
 struct AtScoreArgs {
@@ -823,7 +823,7 @@ extern "C" size_t qk_at_sel_lds(const qk_at_shape *s, int nb) {
 }
 
 extern "C" int qk_launch_at(const qk_at_shape *s, const qk_at_dev *W, const float *x, int n, int offset,
-                            int len0, float *out, float *k_cache, float *v_cache, float *idx_keys,
+                            int pos0, int len0, float *out, float *k_cache, float *v_cache, float *idx_keys,
                             float *pooled, const qk_at_scratch *sc, void *stream) {
     if (n <= 0) return 0;
     if (!qk_at_shape_ok(s)) return (int)hipErrorInvalidValue;
@@ -863,6 +863,7 @@ extern "C" int qk_launch_at(const qk_at_shape *s, const qk_at_dev *W, const floa
         AtPoolArgs pa;
         pa.idx_keys = idx_keys; pa.ik_norm = W->idx_k_norm; pa.pooled = pooled;
         pa.ihd = ihd; pa.comp = s->comp; pa.b0 = pb0; pa.b1 = pb1; pa.rot = s->rot; pa.rope = (const float2 *)W->rope;
+        pa.pos0 = pos0;
         hipLaunchKernelGGL(k_at_pool, dim3((pb1 - pb0 + 3) / 4), dim3(256), 0, st, pa);
         rc = QK_CHECK_LAUNCH();
         if (rc) return rc;
@@ -873,7 +874,7 @@ extern "C" int qk_launch_at(const qk_at_shape *s, const qk_at_dev *W, const floa
     if (use_idx && nb > 0) {
         AtScoreArgs ka;
         ka.pooled = pooled; ka.qi = sc->qi; ka.skey = sc->skey;
-        ka.ih = ih; ka.ihd = ihd; ka.comp = s->comp; ka.nb = nb; ka.ldk = ldk; ka.offset = offset;
+        ka.ih = ih; ka.ihd = ihd; ka.comp = s->comp; ka.nb = nb; ka.ldk = ldk; ka.offset = offset - pos0;
         hipLaunchKernelGGL(k_at_score, dim3(n, (nb + AT_SB - 1) / AT_SB), dim3(256), at_score_lds(ih, ihd), st, ka);
         rc = QK_CHECK_LAUNCH();
         if (rc) return rc;
@@ -889,7 +890,7 @@ extern "C" int qk_launch_at(const qk_at_shape *s, const qk_at_dev *W, const floa
     at.qn = sc->qn; at.k_cache = k_cache; at.v_cache = v_cache;
     at.keep = use_idx ? sc->keep : nullptr;
     at.part = sc->part;
-    at.h = h; at.kvh = kvh; at.hd = hd; at.kv_total = kv_total; at.offset = offset;
+    at.h = h; at.kvh = kvh; at.hd = hd; at.kv_total = kv_total; at.offset = offset - pos0;
     at.comp = s->comp; at.nb = nb; at.kw = kw;
     const int ngrp = (h / kvh + AT_GMAX - 1) / AT_GMAX;
     /* 64-key chunks while 256-key ones leave the grid under 512 workgroups

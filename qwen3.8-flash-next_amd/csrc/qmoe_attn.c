@@ -24,6 +24,8 @@ enum { AT_Q_Q, AT_Q_S, AT_Q_B, AT_K_Q, AT_K_S, AT_K_B, AT_V_Q, AT_V_S, AT_V_B, A
 typedef struct {
     void *mem;
     int ready, len;
+    int start; /* sliding window: first row of the window in the cache buffers */
+    int base;  /* sliding window: position of the window's first row */
 } at_layer;
 
 struct qmoe_attn_ctx {
@@ -112,6 +114,11 @@ int qmoe_attn_create(qmoe_attn_ctx **out, const qmoe_attn_config *cfg, qmoe_err 
                    cfg->n_layers, cfg->max_tokens, cfg->kv_cap);
         return -1;
     }
+    if (cfg->slide != 0 && (cfg->slide != 1 || cfg->kv_cap % cfg->idx_compress != 0)) {
+        at_set_err(err, "slide %d: 0 or 1, and 1 needs kv_cap %d a multiple of idx_compress %d",
+                   cfg->slide, cfg->kv_cap, cfg->idx_compress);
+        return -1;
+    }
     if (cfg->max_position < 0 || cfg->max_position > QMOE_ATTN_MAX_POSITION) {
         at_set_err(err, "max_position %d out of range [0, %d]", cfg->max_position, QMOE_ATTN_MAX_POSITION);
         return -1;
@@ -127,13 +134,16 @@ int qmoe_attn_create(qmoe_attn_ctx **out, const qmoe_attn_config *cfg, qmoe_err 
     const size_t d = (size_t)s.d, h = (size_t)s.h, kvh = (size_t)s.kvh, hd = (size_t)s.hd;
     const size_t ih = (size_t)s.ih, ihd = (size_t)s.ihd, cap = (size_t)s.cap;
     const size_t qr = 2 * h * hd, kr = kvh * hd, orow = d, ok = h * hd;
+    /* a sliding window moves through buffers of twice the capacity and is
+     * copied back to their start when it reaches their end */
+    const size_t phys = cfg->slide ? 2 * cap : cap;
     const size_t sz[AT_COUNT] = {
         qr * d / 2, qr * (d / 64) * 2, qr * (d / 64) * 2,
         kr * d / 2, kr * (d / 64) * 2, kr * (d / 64) * 2,
         kr * d / 2, kr * (d / 64) * 2, kr * (d / 64) * 2,
         orow * ok / 2, orow * (ok / 64) * 2, orow * (ok / 64) * 2,
         (ih + 1) * ihd * d * 2, hd * 4, hd * 4, ihd * 4, ihd * 4,
-        cap * kr * 4, cap * kr * 4, cap * ihd * 4, cap / (size_t)s.comp * ihd * 4};
+        phys * kr * 4, phys * kr * 4, phys * ihd * 4, phys / (size_t)s.comp * ihd * 4};
     size_t total = 0;
     for (int i = 0; i < AT_COUNT; i++) {
         c->off[i] = total;
@@ -234,7 +244,7 @@ int qmoe_attn_upload_layer(qmoe_attn_ctx *c, int layer, const qmoe_attn_weights 
         if (at_hip_fail(err, (int)hipMemcpy(at_ptr(c, layer, i), src[i], c->bytes[i], hipMemcpyHostToDevice),
                         names[i]))
             return -1;
-    c->layers[layer].len = 0;
+    c->layers[layer].len = c->layers[layer].start = c->layers[layer].base = 0;
     c->layers[layer].ready = 1;
     return 0;
 }
@@ -246,11 +256,11 @@ int qmoe_attn_reset(qmoe_attn_ctx *c, int layer, qmoe_err *err) {
         return -1;
     }
     if (layer == -1) {
-        for (int l = 0; l < c->cfg.n_layers; l++) c->layers[l].len = 0;
+        for (int l = 0; l < c->cfg.n_layers; l++) c->layers[l].len = c->layers[l].start = c->layers[l].base = 0;
         return 0;
     }
     if (at_check_layer(c, layer, err)) return -1;
-    c->layers[layer].len = 0;
+    c->layers[layer].len = c->layers[layer].start = c->layers[layer].base = 0;
     return 0;
 }
 
@@ -274,15 +284,56 @@ int qmoe_attn_forward(qmoe_attn_ctx *c, int layer, const float *x, int n, int of
         at_set_err(err, "%s is NULL", x ? "out" : "x");
         return -1;
     }
-    const int len0 = c->layers[layer].len;
-    if (len0 + n > c->cfg.kv_cap) {
-        at_set_err(err, "layer %d: %d cached + %d new tokens pass kv_cap %d", layer, len0, n, c->cfg.kv_cap);
+    at_layer *L = &c->layers[layer];
+    int len0 = L->len, drop = 0;
+    const int comp = c->cfg.idx_compress, cap = c->cfg.kv_cap;
+    if (c->cfg.slide) {
+        if (offset != L->base + len0) {
+            at_set_err(err, "layer %d: a sliding window continues at position %d (window from %d, "
+                            "%d cached), not %d", layer, L->base + len0, L->base, len0, offset);
+            return -1;
+        }
+        if (len0 + n > cap) {
+            drop = (len0 + n - cap + comp - 1) / comp * comp;
+            if (drop > len0) {
+                at_set_err(err, "layer %d: %d new tokens would drop %d rows of the %d cached (calls of "
+                                "at most kv_cap - idx_compress + 1 = %d tokens always fit)",
+                           layer, n, drop, len0, cap - comp + 1);
+                return -1;
+            }
+        }
+    } else if (len0 + n > cap) {
+        at_set_err(err, "layer %d: %d cached + %d new tokens pass kv_cap %d", layer, len0, n, cap);
         return -1;
     }
     if ((long long)offset + n > c->rope_rows) {
         at_set_err(err, "positions %d..%d pass max_position %d", offset, offset + n - 1, c->rope_rows);
         return -1;
     }
+    if (drop) { /* the oldest rows leave the window */
+        L->start += drop;
+        L->base += drop;
+        len0 -= drop;
+        L->len = len0;
+    }
+    const size_t kr = (size_t)c->shape.kvh * c->shape.hd, ihd = (size_t)c->shape.ihd;
+    float *kc = (float *)at_ptr(c, layer, AT_K_CACHE), *vc = (float *)at_ptr(c, layer, AT_V_CACHE);
+    float *ic = (float *)at_ptr(c, layer, AT_IDX_KEYS), *pc = (float *)at_ptr(c, layer, AT_POOLED);
+    if (c->cfg.slide && L->start + len0 + n > 2 * cap) {
+        /* the window back to the buffers' start: rows [start, start + len0) to [0, len0),
+         * disjoint because start > cap >= len0 + n; the pooled keys of its complete blocks too */
+        hipStream_t st = (hipStream_t)stream;
+        const size_t s0 = (size_t)L->start;
+        int rc = (int)hipMemcpyAsync(kc, kc + s0 * kr, (size_t)len0 * kr * 4, hipMemcpyDeviceToDevice, st);
+        if (!rc) rc = (int)hipMemcpyAsync(vc, vc + s0 * kr, (size_t)len0 * kr * 4, hipMemcpyDeviceToDevice, st);
+        if (!rc) rc = (int)hipMemcpyAsync(ic, ic + s0 * ihd, (size_t)len0 * ihd * 4, hipMemcpyDeviceToDevice, st);
+        if (!rc)
+            rc = (int)hipMemcpyAsync(pc, pc + s0 / comp * ihd, (size_t)(len0 / comp) * ihd * 4,
+                                     hipMemcpyDeviceToDevice, st);
+        if (at_hip_fail(err, rc, "window copy")) return -1;
+        L->start = 0;
+    }
+    const size_t w0 = (size_t)L->start;
     qk_at_dev W;
     W.q_q = (const uint32_t *)at_ptr(c, layer, AT_Q_Q);
     W.q_s = (const uint16_t *)at_ptr(c, layer, AT_Q_S);
@@ -302,11 +353,10 @@ int qmoe_attn_forward(qmoe_attn_ctx *c, int layer, const float *x, int n, int of
     W.idx_q_norm = (const float *)at_ptr(c, layer, AT_IQ_NORM);
     W.idx_k_norm = (const float *)at_ptr(c, layer, AT_IK_NORM);
     W.rope = c->rope;
-    const int rc = qk_launch_at(&c->shape, &W, x, n, offset, len0, out, (float *)at_ptr(c, layer, AT_K_CACHE),
-                                (float *)at_ptr(c, layer, AT_V_CACHE), (float *)at_ptr(c, layer, AT_IDX_KEYS),
-                                (float *)at_ptr(c, layer, AT_POOLED), &c->sc, stream);
+    const int rc = qk_launch_at(&c->shape, &W, x, n, offset, c->cfg.slide ? L->base : 0, len0, out,
+                                kc + w0 * kr, vc + w0 * kr, ic + w0 * ihd, pc + w0 / comp * ihd, &c->sc, stream);
     if (at_hip_fail(err, rc, "attention launch")) return -1;
-    c->layers[layer].len = len0 + n;
+    L->len = len0 + n;
     if (len0 + n > c->cfg.idx_budget) c->last_kw = ((len0 + n) / c->cfg.idx_compress + 31) / 32;
     return 0;
 }
@@ -314,9 +364,11 @@ int qmoe_attn_forward(qmoe_attn_ctx *c, int layer, const float *x, int n, int of
 int qmoe_attn_cache(qmoe_attn_ctx *c, int layer, float **k_cache, float **v_cache, float **idx_keys,
                     int *len, qmoe_err *err) {
     if (at_check_layer(c, layer, err)) return -1;
-    if (k_cache) *k_cache = (float *)at_ptr(c, layer, AT_K_CACHE);
-    if (v_cache) *v_cache = (float *)at_ptr(c, layer, AT_V_CACHE);
-    if (idx_keys) *idx_keys = (float *)at_ptr(c, layer, AT_IDX_KEYS);
+    const size_t w0 = (size_t)c->layers[layer].start;
+    const size_t kr = (size_t)c->shape.kvh * c->shape.hd;
+    if (k_cache) *k_cache = (float *)at_ptr(c, layer, AT_K_CACHE) + w0 * kr;
+    if (v_cache) *v_cache = (float *)at_ptr(c, layer, AT_V_CACHE) + w0 * kr;
+    if (idx_keys) *idx_keys = (float *)at_ptr(c, layer, AT_IDX_KEYS) + w0 * (size_t)c->shape.ihd;
     if (len) *len = c->layers[layer].len;
     return 0;
 }
@@ -324,7 +376,9 @@ int qmoe_attn_cache(qmoe_attn_ctx *c, int layer, float **k_cache, float **v_cach
 int qmoe_attn_index_state(qmoe_attn_ctx *c, int layer, float **pooled, uint32_t **keep, int *keep_words,
                           uint32_t **score_keys, int *score_ld, qmoe_err *err) {
     if (at_check_layer(c, layer, err)) return -1;
-    if (pooled) *pooled = (float *)at_ptr(c, layer, AT_POOLED);
+    if (pooled)
+        *pooled = (float *)at_ptr(c, layer, AT_POOLED) +
+                  (size_t)(c->layers[layer].start / c->cfg.idx_compress) * c->shape.ihd;
     if (keep) *keep = c->sc.keep;
     if (keep_words) *keep_words = c->last_kw;
     if (score_keys) *score_keys = c->sc.skey;

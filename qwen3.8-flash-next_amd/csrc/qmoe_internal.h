@@ -243,9 +243,11 @@ size_t qk_at_sel_lds(const qk_at_shape *s, int nb);
 /* x [n, d] f32 at positions offset.. -> out [n, d]; the caches hold len0
  * rows before the call and len0 + n after it (len0 + n <= cap); pooled
  * [cap/comp, ihd] holds the pooled, normed and rotated indexer key of every
- * complete block, len0/comp of them before the call */
-int qk_launch_at(const qk_at_shape *s, const qk_at_dev *W, const float *x, int n, int offset, int len0,
-                 float *out, float *k_cache, float *v_cache, float *idx_keys, float *pooled,
+ * complete block, len0/comp of them before the call.  pos0 (a multiple of
+ * comp) is the position of cache row 0: the masks compare rows with
+ * offset - pos0 and block b's pooled key is rotated to pos0 + b*comp. */
+int qk_launch_at(const qk_at_shape *s, const qk_at_dev *W, const float *x, int n, int offset, int pos0,
+                 int len0, float *out, float *k_cache, float *v_cache, float *idx_keys, float *pooled,
                  const qk_at_scratch *sc, void *stream);
 
 /* the MLP hyper connection (hyper.hip): shapes it takes (hc <= 8, d and R

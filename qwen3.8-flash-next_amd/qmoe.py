@@ -83,7 +83,8 @@ class QmoeAttnConfig(ctypes.Structure):
                                             "idx_head_dim", "idx_budget", "idx_compress", "kv_cap",
                                             "group_size")] + \
                [("rotary_factor", ctypes.c_float), ("rope_theta", ctypes.c_float),
-                ("n_layers", ctypes.c_int), ("max_tokens", ctypes.c_int), ("max_position", ctypes.c_int)]
+                ("n_layers", ctypes.c_int), ("max_tokens", ctypes.c_int), ("max_position", ctypes.c_int),
+                ("slide", ctypes.c_int)]
 
 
 AT_FIELDS = ["q_q", "q_s", "q_b", "k_q", "k_s", "k_b", "v_q", "v_s", "v_b", "o_q", "o_s", "o_b", "idx_w",
@@ -724,10 +725,10 @@ class AttentionContext:
 
     def __init__(self, hidden, n_heads, n_kv_heads, head_dim, idx_heads, idx_head_dim, idx_budget,
                  idx_compress, kv_cap=2048, rotary_factor=0.25, rope_theta=1e7, n_layers=1,
-                 max_tokens=1, group_size=64, max_position=0):
+                 max_tokens=1, group_size=64, max_position=0, slide=False):
         self.cfg = QmoeAttnConfig(hidden, n_heads, n_kv_heads, head_dim, idx_heads, idx_head_dim,
                                   idx_budget, idx_compress, kv_cap, group_size, rotary_factor,
-                                  rope_theta, n_layers, max_tokens, max_position)
+                                  rope_theta, n_layers, max_tokens, max_position, 1 if slide else 0)
         self.d, self.h, self.kvh, self.hd = hidden, n_heads, n_kv_heads, head_dim
         self.ihd, self.cap = idx_head_dim, kv_cap
         self._h = ctypes.c_void_p()

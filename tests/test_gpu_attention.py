@@ -89,15 +89,17 @@ def check_index(ctx, dbg, case, n, t0, ln):
     return ties
 
 
-def run_calls(torch, dev, case, calls, seed=1):
+def run_calls(torch, dev, case, calls, seed=1, slide=False):
     d, h, kvh, hd, ih, ihd, budget, comp, cap, rf = case
     pkg = load_pkg()
-    A = orc.Attention(d, h, kvh, hd, ih, ihd, budget, comp, kv_cap=cap, rotary_factor=rf, seed=seed)
+    A = orc.Attention(d, h, kvh, hd, ih, ihd, budget, comp, kv_cap=cap, rotary_factor=rf, seed=seed,
+                      slide=slide)
     st = A.new_state()
     x = orc.gen_attn_x(sum(calls), d, seed + 50)
     masked = 0
     with pkg.AttentionContext(d, h, kvh, hd, ih, ihd, budget, comp, kv_cap=cap, rotary_factor=rf,
-                              n_layers=2, max_tokens=max(calls)) as ctx:
+                              n_layers=2, max_tokens=max(calls), slide=slide,
+                              max_position=sum(calls) if slide else 0) as ctx:
         ctx.upload_layer(1, A.arrays())
         t0 = 0
         for i, n in enumerate(calls):
@@ -107,14 +109,14 @@ def run_calls(torch, dev, case, calls, seed=1):
             g = got.cpu().numpy()
             err, r = float(np.abs(g - ref).max()), rel(g, ref)
             kp, vp, ip, ln = ctx.cache(1)
-            assert ln == t0 + n
+            assert ln == st.len and (slide or ln == t0 + n), (ln, st.len, t0 + n)
             kc = d2h(kp, (ln, kvh * hd))
             vc = d2h(vp, (ln, kvh * hd))
             ic = d2h(ip, (ln, ihd))
             rk, rv = rel(kc, st.k[:ln]), rel(vc, st.v[:ln])
             ties = check_index(ctx, dbg, case, n, t0, ln) if dbg else 0
             masked += n if dbg else 0
-            say(f"{case} call {i} (n={n}, cached {ln}, mask {'on' if dbg else 'off'}): "
+            say(f"{case} call {i} (n={n}, cached {ln} from position {st.base}, mask {'on' if dbg else 'off'}): "
                 f"max-abs {err:.2e} rel-L2 {r:.2e} (|ref| max {np.abs(ref).max():.2f}); "
                 f"caches rel {rk:.1e}/{rv:.1e}; indexer keys, pooled keys, scores and kept blocks "
                 f"{'bit-exact' if dbg else 'n/a'}{f' ({ties} exact boundary ties)' if ties else ''}")
@@ -205,6 +207,59 @@ def test_bench_indexer_setting(torch_dev):
     case = (256, 2, 1, 128, 4, 128, 2048, 4, 8192, 0.25)
     say(f"case: attention {case}")
     assert run_calls(torch, dev, case, [2048, 2048, 40, 1, 1], seed=5) == 2048 + 40 + 2
+
+
+SLIDE_CASES = [
+    # d, h, kvh, hd, idx heads, idx hd, budget, compress, cap, rotary factor
+    (256, 4, 2, 64, 2, 64, 8, 2, 16, 0.25),      # the block mask inside a 16-row window
+    (256, 4, 1, 64, 2, 64, 8, 4, 20, 0.5),       # blocks of 4, one kv head
+    (192, 2, 1, 64, 2, 32, 4096, 3, 12, 0.5),    # dense window, blocks of 3
+]
+
+
+@pytest.mark.parametrize("case", SLIDE_CASES)
+def test_sliding_window(torch_dev, case):
+    """slide = 1: calls past kv_cap drop the oldest rows of k, v and the
+    indexer keys together, compress rows at a time; the window moves
+    through buffers of twice the capacity and is copied back when it
+    reaches their end (several times here).  Against the oracle with the
+    same option (pinned by tests/test_oracle_attn.py against a float64
+    statement over the full history): outputs, the window's k and v, and
+    the indexer bit for bit"""
+    torch, dev = torch_dev
+    say(f"case: sliding attention {case}")
+    calls = [5, 7, 1, 1, 6, 1, 9, 1, 1, 8, 1, 3, 1] * 3
+    run_calls(torch, dev, case, calls, seed=6, slide=True)
+
+
+def test_sliding_window_model_shape(torch_dev):
+    """the model's attention shape in a 1024-row window with the benchmark's
+    indexer budget and compress (mask on from 513 keys): 256-token chunks
+    past the capacity, then one-token steps"""
+    torch, dev = torch_dev
+    case = (2048, 16, 2, 128, 4, 128, 512, 4, 1024, 0.25)
+    say(f"case: sliding attention {case}")
+    run_calls(torch, dev, case, [256] * 6 + [1, 1, 1], seed=7, slide=True)
+
+
+def test_sliding_errors(torch_dev):
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    with pytest.raises(pkg.QmoeError, match="slide"):
+        pkg.AttentionContext(256, 4, 2, 64, 2, 64, 8, 3, kv_cap=16, slide=True)  # 16 % 3
+    A = orc.Attention(256, 4, 2, 64, 2, 64, 8, 4, kv_cap=8, slide=True)
+    with pkg.AttentionContext(256, 4, 2, 64, 2, 64, 8, 4, kv_cap=8, max_tokens=8, slide=True,
+                              max_position=64) as ctx:
+        ctx.upload_layer(0, A.arrays())
+        ctx.forward(0, torch.zeros((3, 256), device=dev), 0)
+        with pytest.raises(pkg.QmoeError, match="continues at position 3"):
+            ctx.forward(0, torch.zeros((1, 256), device=dev), 5)
+        with pytest.raises(pkg.QmoeError, match="would drop 4 rows of the 3 cached"):
+            ctx.forward(0, torch.zeros((8, 256), device=dev), 3)
+        ctx.forward(0, torch.zeros((5, 256), device=dev), 3)   # fills the window
+        ctx.forward(0, torch.zeros((1, 256), device=dev), 8)   # slides by 4
+        torch.cuda.synchronize()
+        assert ctx.cache(0)[3] == 5
 
 
 def test_dense_model_shape(torch_dev):

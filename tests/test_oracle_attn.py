@@ -63,7 +63,10 @@ class F64:
         self.V = np.zeros((0, kvh, hd))
         self.I = np.zeros((0, A.ihd))
 
-    def forward(self, x, offset):
+    def forward(self, x, offset, base=0):
+        """x at positions offset..; with base > 0 only keys at positions >=
+        base (and key blocks starting there) are attended: the sliding
+        window stated over the full history"""
         A, t = self.A, self.A.t
         h, kvh, hd, ih, ihd = A.h, A.kvh, A.hd, A.ih, A.ihd
         rot = int(hd * A.rf)
@@ -82,8 +85,8 @@ class F64:
         kk = np.arange(L)
         out = np.zeros((n, h, hd))
         for ti in range(n):
-            allowed = kk <= offset + ti
-            if L > A.budget:
+            allowed = (kk <= offset + ti) & (kk >= base)
+            if L - base > A.budget:
                 c = A.compress
                 nb = L // c
                 pooled = self.I[:nb * c].reshape(nb, c, ihd).mean(1)
@@ -91,7 +94,8 @@ class F64:
                 qi = rope(rms(qk[ti, :ih * ihd].reshape(ih, ihd), t["idx_q_norm"]), pos[ti], rot, A.theta)
                 sc = np.maximum(qi[:, None, :] * pooled[None], 0).sum((0, 2)) / np.sqrt(ihd)
                 sc[np.arange(nb) * c + c - 1 > offset + ti] = -np.inf
-                order = sorted(range(nb), key=lambda b: (-sc[b], b))[:A.budget // c]
+                cand = [b for b in range(nb) if b * c >= base]
+                order = sorted(cand, key=lambda b: (-sc[b], b))[:A.budget // c]
                 keep = np.isin(kk // c, order) & (kk // c < nb)
                 own = (offset + ti + 1) // c * c
                 keep |= (kk >= own) & (kk <= offset + ti)
@@ -166,3 +170,48 @@ def test_capacity_refused():
     A.forward(orc.gen_attn_x(4, 256, 1), st, 0)
     with pytest.raises(ValueError, match="capacity"):
         A.forward(orc.gen_attn_x(1, 256, 2), st, 4)
+
+
+SLIDE_CASES = [
+    # d, h, kvh, hd, idx heads, idx hd, budget, compress, cap, rotary factor
+    (256, 4, 2, 64, 2, 64, 8, 2, 16, 0.25),      # the indexer masks inside the window
+    (256, 4, 1, 64, 2, 64, 8, 4, 20, 0.5),       # blocks of 4, one kv head
+    (192, 2, 1, 32, 2, 32, 4096, 3, 12, 1.0),    # dense window, blocks of 3
+]
+
+
+@pytest.mark.parametrize("case", SLIDE_CASES)
+def test_sliding_window_matches_float64(case):
+    """past kv_cap the sliding oracle drops the oldest rows of k, v and the
+    indexer keys together, compress rows at a time; it must equal the
+    float64 mixer over the whole history with every key (and key block)
+    before the window's first position masked, where that position is
+    round_up(tokens - cap, compress) -- stated here without the oracle's
+    bookkeeping.  Calls cross the capacity several times, in chunks and
+    one token at a time."""
+    d, h, kvh, hd, ih, ihd, budget, comp, cap, rf = case
+    A = orc.Attention(d, h, kvh, hd, ih, ihd, budget, comp, kv_cap=cap, rotary_factor=rf, seed=3,
+                      slide=True)
+    st = A.new_state()
+    ref = F64(A)
+    x = orc.gen_attn_x(64, d, 4)
+    t0 = 0
+    for n in (5, 7, 1, 1, 6, 1, 9, 1, 1, 8, 1, 3, 1):
+        got = A.forward(x[t0:t0 + n], st, t0)
+        total = t0 + n
+        base = max(0, -(-(total - cap) // comp) * comp)
+        exp = ref.forward(x[t0:t0 + n], t0, base)
+        assert st.base == base and st.len == total - base, (t0, n, st.base, st.len, base)
+        assert rel(got, exp) < 1e-5, (t0, n, rel(got, exp))
+        t0 += n
+    assert st.base > 0
+
+
+def test_sliding_window_refusals():
+    A = orc.Attention(256, 4, 2, 64, 2, 64, 4096, 4, kv_cap=8, seed=7, slide=True)
+    st = A.new_state()
+    A.forward(orc.gen_attn_x(3, 256, 1), st, 0)
+    with pytest.raises(ValueError, match="base"):   # positions must continue the window
+        A.forward(orc.gen_attn_x(1, 256, 2), st, 5)
+    with pytest.raises(ValueError, match="capacity"):  # the drop would exceed the 3 cached rows
+        A.forward(orc.gen_attn_x(8, 256, 2), st, 3)
