@@ -658,13 +658,18 @@ def cpu_model():
     return "unknown"
 
 
-def _timed(fn, budget_s, max_iters=10, warm=3):
-    """median of up to max_iters runs after up to `warm` warm-ups, fitted to
-    a time budget (at least 1 run)"""
-    one = fn(0, 1)
-    iters = max(1, min(max_iters, int(budget_s / max(one, 1e-6))))
-    wu = min(warm, max(0, iters - 1))
-    return fn(wu, iters), iters, wu
+def _timed_runs(make_fn, n_max, budget_s, runs=10, warm=3):
+    """the median of `runs` timed runs after `warm` warm-ups; when
+    runs + warm runs of n_max tokens would take longer than budget_s, the
+    token sample shrinks to fit (never the run count).
+    make_fn(n) -> fn(warmups, iters) returning the median seconds.  Returns
+    (median, tokens per run, runs, warm-ups)."""
+    n = n_max
+    one = make_fn(n)(1, 1)  # a warm run: the first touches the weights
+    per = budget_s / (runs + warm)
+    if one > per and n > 1:
+        n = max(1, int(n * per / one))
+    return make_fn(n)(warm, runs), n, runs, warm
 
 
 def cpu_baselines(pkg, names, threads, budget_s):
@@ -676,6 +681,7 @@ def cpu_baselines(pkg, names, threads, budget_s):
     layers with only the routed experts generated (no other expert is
     touched).  Prefill runs on a token sample (stated); the 48-layer stack
     is q4 only (a warm fp32 cache of 48 layers does not fit host memory)."""
+    import numpy as np
     sys.path.insert(0, ROOT)
     from oracle import oracle as orc
     res = {}
@@ -698,19 +704,19 @@ def cpu_baselines(pkg, names, threads, budget_s):
         L = orc.Layer(w.hidden, w.n_experts, w.top_k, w.moe_inter, seed=w.seed, router_bias=rb,
                       only_experts=ids, group_size=w.group_size)
         warm = orc.Warm(L, ids, n_threads=threads)
-        entry = dict(sample_tokens_all_threads=n_all, sample_tokens_one_thread=n_one,
-                     warm_fp32_bytes=warm.nbytes)
+        entry = dict(warm_fp32_bytes=warm.nbytes)
         for mode in ("warm_fp32", "q4"):
             row = {}
-            for th, n in ((threads, n_all), (1, n_one)):
-                xs = x[:n]
-                if mode == "warm_fp32":
-                    fn = lambda wu, it, xs=xs, th=th: warm.time_forward(xs, w.x_bf16, th, wu, it)  # noqa: E731
-                else:
-                    fn = lambda wu, it, xs=xs, th=th: L.time_forward(xs, w.x_bf16, th, wu, it)  # noqa: E731
-                med, iters, wu = _timed(fn, budget_s if th > 1 else budget_s / 2)
+            for th, n_max in ((threads, n_all), (1, n_one)):
+                def make_fn(n, th=th, mode=mode):
+                    xs = np.ascontiguousarray(x[:n])
+                    if mode == "warm_fp32":
+                        return lambda wu, it: warm.time_forward(xs, w.x_bf16, th, wu, it)
+                    return lambda wu, it: L.time_forward(xs, w.x_bf16, th, wu, it)
+                med, n, iters, wu = _timed_runs(make_fn, n_max, budget_s)
                 key = "all" if th > 1 else "1"
                 row[f"tokens_per_s_{key}"] = n / med
+                row[f"sample_tokens_{key}"] = n
                 row[f"runs_{key}"] = iters
                 row[f"warmups_{key}"] = wu
                 if name == "prefill":
@@ -750,17 +756,17 @@ def cpu_depth(orc, w, threads, budget_s, sample_layers=8):
     for th, key in ((threads, "all"), (1, "1")):
         tot = 0.0
         for L, hin in layers:
-            med, _, _ = _timed(lambda wu, it: L.time_forward(np.ascontiguousarray(hin), False, th,
-                                                             wu, it, residual=True),
-                               per_layer if th > 1 else per_layer / 2, max_iters=10, warm=3)
+            med, _, _, _ = _timed_runs(lambda n, L=L, hin=hin: (lambda wu, it: L.time_forward(
+                np.ascontiguousarray(hin), False, th, wu, it, residual=True)), 1, per_layer)
             tot += med
         tot *= w.n_layers / len(layers)
         out[f"tokens_per_s_{key}"] = 1.0 / tot
         out[f"gbs_{key}"] = layer_token_bytes(w) * w.n_layers / tot / 1e9
     return dict(q4=out, sample_tokens=1, sample_layers=len(layers),
+                runs=10, warmups=3,
                 note=f"one token through the first {len(layers)} of the {w.n_layers} layers as a "
-                     f"chain, per-layer medians summed and scaled to {w.n_layers} layers; only the "
-                     f"routed experts of each layer generated")
+                     f"chain, per-layer medians (10 runs after 3 warm-ups) summed and scaled to "
+                     f"{w.n_layers} layers; only the routed experts of each layer generated")
 
 
 def copy_calibration(torch, mib):
@@ -812,8 +818,9 @@ def main():
     ap.add_argument("--layers", type=int, default=48,
                     help="resident layers rotated over (defeats the Infinity Cache)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=2.0,
-                    help="seconds of CPU timing per (workload, mode, thread count)")
+    ap.add_argument("--cpu-budget", type=float, default=12.0,
+                    help="at most this many seconds of CPU timing per (workload, mode, thread "
+                         "count): past it the token sample shrinks, the 10 runs after 3 warm-ups stay")
     ap.add_argument("--cpu", default="tiny,decode,batched,prefill,depth48",
                     help="workloads timed on the CPU (the oracle)")
     ap.add_argument("--extra", default="tiny,batched,prefill,depth48",
@@ -1015,8 +1022,9 @@ def main():
                    cpu_model=cpu_model(),
                    sample=f"the {w.name} workload through oracle/moe_oracle.c (the C restatement of "
                           f"the reference C port's moe_forward) with warm fp32-dequantised routed "
-                          f"experts (weight mode i, gemm_fp32), median of the runs that fit "
-                          f"{args.cpu_budget:.0f} s after up to 3 warm-ups; {threads} OpenMP threads "
+                          f"experts (weight mode i, gemm_fp32), median of 10 runs after 3 warm-ups "
+                          f"(the token sample per run shrunk to fit {args.cpu_budget:.0f} s, as "
+                          f"per_config's sample_tokens_* give); {threads} OpenMP threads "
                           f"(value_1thread: 1 thread); per_config holds every workload in both weight "
                           f"modes (q4: gemm_q4 for every expert)",
                    per_config=per)
