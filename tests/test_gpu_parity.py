@@ -372,11 +372,12 @@ def test_depth48_stack_norm_residual(torch_dev):
         assert err < nl * MAX_ABS and rel < REL_L2, (err, rel)
 
 
-@pytest.mark.parametrize("n,residual", [(64, False), (1, False), (1, True), (5, True)])
+@pytest.mark.parametrize("n,residual", [(64, False), (1, False), (1, True), (5, True), (1024, False)])
 def test_stages_compose_to_layer(torch_dev, n, residual):
     """the stage entry points chained by hand give the layer's bits (n <= 8
     exercises the layer's fused down+combine kernel, n = 64 the separate
-    down and combine kernels)"""
+    down and combine kernels on the narrow MFMA tiles, n = 1024 on the
+    full tiles with several chunks per expert)"""
     torch, dev = torch_dev
     pkg = load_pkg()
     say(f"case: router -> dispatch -> ffn -> combine == layer_forward, n={n} residual={residual}")
