@@ -212,6 +212,91 @@ static int router_nch(int H) {
         }                                                                                      \
     } while (0)
 
+/*
+ * One token: one workgroup of 4 waves per row (E+1 workgroups, 4(E+1)
+ * waves: two or more per SIMD where a wave per row would leave half the
+ * SIMDs idle).  Wave w runs the R64 chains of lanes 16w..16w+15 (its lanes
+ * 16..63 repeat lanes 0..15 and are ignored), sums them over l^1..l^8 as
+ * qk_group_sum<64> does, and the l^16, l^32 levels of the tree are added
+ * from LDS in the same order: (S0 + S1) + (S2 + S3).  With NORM the sum of
+ * squares takes the same route, every wave forms r and the normalised row
+ * itself (router_rows' arithmetic), and row 0's workgroup writes xn.  The
+ * logits are the bits of k_router's.
+ */
+template <bool XBF16, bool NORM, int NCH>
+__global__ __launch_bounds__(256) void k_router_one(RouterArgs a) {
+    const int row = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int vl = 16 * wave + (lane & 15);
+    const int chunks = a.H >> 3;
+    const uint16_t *wrow = row < a.E ? a.router_w + (size_t)row * a.H : a.sh_gate_w;
+    __shared__ float s_g[2][4];
+    uint4 wv[NCH];
+    bool cv[NCH];
+    int cc[NCH];
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+        const int c = vl + 64 * i;
+        cv[i] = c < chunks;
+        cc[i] = cv[i] ? c : 0;
+        wv[i] = qk_ld((const uint4 *)wrow + cc[i]);
+    }
+    float v[NCH][8];
+#pragma unroll
+    for (int i = 0; i < NCH; i++) load_x8<XBF16>(a.x, 0, cc[i], v[i]);
+    if (NORM) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NCH; i++) {
+            float s2 = ss;
+#pragma unroll
+            for (int j = 0; j < 8; j++) s2 = fmaf(v[i][j], v[i][j], s2);
+            ss = cv[i] ? s2 : ss;
+        }
+        ss = qk_group_sum<16>(ss);
+        if (lane == 0) s_g[0][wave] = ss;
+        __syncthreads();
+        ss = (s_g[0][0] + s_g[0][1]) + (s_g[0][2] + s_g[0][3]);
+        const float r = 1.0f / sqrtf(ss / (float)a.H + a.eps);
+#pragma unroll
+        for (int i = 0; i < NCH; i++) {
+            const float4 *nw = (const float4 *)a.norm_w + 2 * cc[i];
+            const float4 w0 = qk_ld(nw), w1 = qk_ld(nw + 1);
+            const float wn[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[i][j] = (v[i][j] * r) * wn[j];
+            if (row == 0 && a.xn && cv[i] && lane < 16) {
+                float4 *o = (float4 *)a.xn + 2 * cc[i];
+                o[0] = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
+                o[1] = make_float4(v[i][4], v[i][5], v[i][6], v[i][7]);
+            }
+        }
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+        const uint4 d = wv[i];
+        float a2 = acc;
+        a2 = fmaf(v[i][0], qk_bf16_lo(d.x), a2);
+        a2 = fmaf(v[i][1], qk_bf16_hi(d.x), a2);
+        a2 = fmaf(v[i][2], qk_bf16_lo(d.y), a2);
+        a2 = fmaf(v[i][3], qk_bf16_hi(d.y), a2);
+        a2 = fmaf(v[i][4], qk_bf16_lo(d.z), a2);
+        a2 = fmaf(v[i][5], qk_bf16_hi(d.z), a2);
+        a2 = fmaf(v[i][6], qk_bf16_lo(d.w), a2);
+        a2 = fmaf(v[i][7], qk_bf16_hi(d.w), a2);
+        acc = cv[i] ? a2 : acc;
+    }
+    acc = qk_group_sum<16>(acc);
+    if (lane == 0) s_g[1][wave] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float l = (s_g[1][0] + s_g[1][1]) + (s_g[1][2] + s_g[1][3]);
+        if (row < a.E && a.router_bias) l = l + a.router_bias[row];
+        a.logits[row] = l;
+    }
+}
+
 /* the tiled router is instantiated for H = 512 * NCH with NCH = 1, 2, 4
  * (hidden 1536 is a multiple of 512 but has no instance: it takes k_router) */
 extern "C" int qk_router_packs(qk_shape s, int n) {
@@ -273,6 +358,25 @@ extern "C" int qk_launch_router_pack(const qmoe_layer_weights *W, qk_shape s, co
         }
 #undef RTT_N
 #undef RTT_L
+        return QK_CHECK_LAUNCH();
+    }
+    if (n == 1 && router_nch(s.H) <= 4) {
+        const int nch = router_nch(s.H);
+        const bool nrm = W->norm_w != nullptr;
+#define R1_L(XB, NR)                                                                                      \
+    do {                                                                                                  \
+        if (nch == 1) hipLaunchKernelGGL((k_router_one<XB, NR, 1>), dim3(s.E + 1), dim3(256), 0, st, a); \
+        else if (nch == 2) hipLaunchKernelGGL((k_router_one<XB, NR, 2>), dim3(s.E + 1), dim3(256), 0, st, a); \
+        else hipLaunchKernelGGL((k_router_one<XB, NR, 4>), dim3(s.E + 1), dim3(256), 0, st, a);          \
+    } while (0)
+        if (x_bf16) {
+            if (nrm) R1_L(true, true);
+            else R1_L(true, false);
+        } else {
+            if (nrm) R1_L(false, true);
+            else R1_L(false, false);
+        }
+#undef R1_L
         return QK_CHECK_LAUNCH();
     }
     /* one wave per (row, block of RT_TB tokens); RT_WPB waves per workgroup
