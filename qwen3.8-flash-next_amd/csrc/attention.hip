@@ -16,7 +16,7 @@
  *             kept in HBM with the layer (a pooled key depends only on its
  *             block's cached keys, so the reference's per-call recomputation
  *             gives the same values).
- *   k_at_score (past the indexer budget) one workgroup per (token, 32
+ *   k_at_score (past the indexer budget) one workgroup per (token, 16
  *             blocks): score sum_heads sum_i relu(q_i p_i) / sqrt(ihd),
  *             invisible blocks -inf, as order keys.
  *   k_at_sel  one workgroup per token: the top budget/compress blocks (value
@@ -167,6 +167,20 @@ struct AtQkArgs {
  * normed and rotated rows have the oracle's bits. */
 __device__ __forceinline__ void at_norm_rope(float *s, const float *w, int L, int rot, const float2 *rope,
                                              int pos, float *dst, int lane) {
+    /* the norm weights and this position's cos / sin are loaded first, so
+     * they arrive while the sum of squares runs */
+    const int half = rot / 2;
+    const float2 *cs = rope + (size_t)pos * half;
+    float wv[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) wv[e] = qk_ld(w + min(lane + 64 * e, L - 1));
+    float2 c[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int i = lane + 64 * e;
+        const int ci = i < half ? i : (i < rot ? i - half : 0);
+        c[e] = half > 0 ? cs[ci] : make_float2(1.0f, 0.0f);
+    }
     float ss = 0.0f;
     for (int i = 0; i < L; i += 4) {
         const float4 v = *(const float4 *)(s + i);
@@ -177,24 +191,20 @@ __device__ __forceinline__ void at_norm_rope(float *s, const float *w, int L, in
     }
     const float r = 1.0f / sqrtf(ss / (float)L + 1e-6f);
     qk_wave_lds_sync();
-    for (int i = lane; i < L; i += 64) s[i] = (s[i] * r) * qk_ld(w + i);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int i = lane + 64 * e;
+        if (i < L) s[i] = (s[i] * r) * wv[e];
+    }
     qk_wave_lds_sync();
-    const int half = rot / 2;
-    const float2 *cs = rope + (size_t)pos * half;
     float v[4];
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         const int i = lane + 64 * e;
         if (i >= L) break;
-        if (i < half) {
-            const float2 c = cs[i];
-            v[e] = s[i] * c.x - s[i + half] * c.y;
-        } else if (i < rot) {
-            const float2 c = cs[i - half];
-            v[e] = s[i - half] * c.y + s[i] * c.x;
-        } else {
-            v[e] = s[i];
-        }
+        if (i < half) v[e] = s[i] * c[e].x - s[i + half] * c[e].y;
+        else if (i < rot) v[e] = s[i - half] * c[e].y + s[i] * c[e].x;
+        else v[e] = s[i];
     }
     qk_wave_lds_sync(); /* dst may be s itself */
 #pragma unroll
@@ -205,33 +215,50 @@ __device__ __forceinline__ void at_norm_rope(float *s, const float *w, int L, in
     }
 }
 
+/* the first L <= 256 floats of src for this lane (elements lane + 64 e),
+ * all four loads issued together (a loop with a runtime trip count would
+ * wait on each); past L the last element is read again and not used */
+__device__ __forceinline__ void at_ld4(const float *src, int L, int lane, float v[4]) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = qk_ld(src + min(lane + 64 * e, L - 1));
+}
+__device__ __forceinline__ void at_st4(float *dst, int L, int lane, const float v[4]) {
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        if (lane + 64 * e < L) dst[lane + 64 * e] = v[e];
+}
+
 __global__ __launch_bounds__(64) void k_at_qk(AtQkArgs a) {
     __shared__ __align__(16) float s[256];
     const int lane = threadIdx.x, t = blockIdx.x, role = blockIdx.y;
     const int pos = a.offset + t, row = a.len0 + t;
     if (role < a.h) {
         const float *src = a.qg + (size_t)t * 2 * a.h * a.hd + (size_t)role * 2 * a.hd;
-        for (int i = lane; i < a.hd; i += 64) s[i] = qk_ld(src + i);
+        float v[4];
+        at_ld4(src, a.hd, lane, v);
+        at_st4(s, a.hd, lane, v);
         qk_wave_lds_sync();
         at_norm_rope(s, a.q_norm, a.hd, a.rot, a.rope, pos, a.qn + ((size_t)t * a.h + role) * a.hd, lane);
     } else if (role < a.h + a.kvh) {
         const int kh = role - a.h;
         const size_t off = (size_t)t * a.kvh * a.hd + (size_t)kh * a.hd;
-        for (int i = lane; i < a.hd; i += 64) {
-            s[i] = qk_ld(a.kraw + off + i);
-            a.v_cache[(size_t)row * a.kvh * a.hd + (size_t)kh * a.hd + i] = qk_ld(a.vraw + off + i);
-        }
-        if (kh == 0) {
-            const float *rk = a.qk + (size_t)t * (a.ih + 1) * a.ihd + (size_t)a.ih * a.ihd;
-            for (int i = lane; i < a.ihd; i += 64) a.idx_keys[(size_t)row * a.ihd + i] = qk_ld(rk + i);
-        }
+        float kv[4], vv[4], iv[4];
+        at_ld4(a.kraw + off, a.hd, lane, kv);
+        at_ld4(a.vraw + off, a.hd, lane, vv);
+        const float *rk = a.qk + (size_t)t * (a.ih + 1) * a.ihd + (size_t)a.ih * a.ihd;
+        at_ld4(rk, a.ihd, lane, iv); /* every kv head loads it; head 0 stores it */
+        at_st4(s, a.hd, lane, kv);
+        at_st4(a.v_cache + (size_t)row * a.kvh * a.hd + (size_t)kh * a.hd, a.hd, lane, vv);
+        if (kh == 0) at_st4(a.idx_keys + (size_t)row * a.ihd, a.ihd, lane, iv);
         qk_wave_lds_sync();
         at_norm_rope(s, a.k_norm, a.hd, a.rot, a.rope, pos,
                      a.k_cache + (size_t)row * a.kvh * a.hd + (size_t)kh * a.hd, lane);
     } else {
         const int ihh = role - a.h - a.kvh;
         const float *src = a.qk + (size_t)t * (a.ih + 1) * a.ihd + (size_t)ihh * a.ihd;
-        for (int i = lane; i < a.ihd; i += 64) s[i] = qk_ld(src + i);
+        float v[4];
+        at_ld4(src, a.ihd, lane, v);
+        at_st4(s, a.ihd, lane, v);
         qk_wave_lds_sync();
         at_norm_rope(s, a.iq_norm, a.ihd, a.rot, a.rope, pos, a.qi + ((size_t)t * a.ih + ihh) * a.ihd, lane);
     }
@@ -257,11 +284,23 @@ __global__ __launch_bounds__(256) void k_at_pool(AtPoolArgs a) {
     const int b = a.b0 + (int)blockIdx.x * 4 + wave;
     if (b >= a.b1) return; /* the whole wave; nothing below synchronises the workgroup */
     float *pw = s_p[wave];
-    for (int i = lane; i < a.ihd; i += 64) {
-        float acc = 0.0f;
-        for (int j = 0; j < a.comp; j++) acc = acc + qk_ld(a.idx_keys + ((size_t)b * a.comp + j) * a.ihd + i);
-        pw[i] = acc / (float)a.comp;
+    /* the block's keys four at a time, every load of a round in flight;
+     * each element summed over j in ascending order */
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j0 = 0; j0 < a.comp; j0 += 4) {
+        float v[4][4];
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            at_ld4(a.idx_keys + ((size_t)b * a.comp + min(j0 + u, a.comp - 1)) * a.ihd, a.ihd, lane, v[u]);
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (j0 + u < a.comp)
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[e] = acc[e] + v[u][e];
     }
+#pragma unroll
+    for (int e = 0; e < 4; e++) acc[e] = acc[e] / (float)a.comp;
+    at_st4(pw, a.ihd, lane, acc);
     qk_wave_lds_sync();
     at_norm_rope(pw, a.ik_norm, a.ihd, a.rot, a.rope, a.pos0 + b * a.comp, a.pooled + (size_t)b * a.ihd, lane);
 }
@@ -273,49 +312,75 @@ struct AtScoreArgs {
     int ih, ihd, comp, nb, ldk, offset;
 };
 
-#define AT_SB 32 /* blocks per workgroup of k_at_score */
+#define AT_SB 16 /* blocks per workgroup of k_at_score (16 beat 32 and 64 at one token) */
 
-/* dynamic LDS of k_at_score: the token's queries, a tile of pooled keys
- * (rows padded by one float), the per-head dots */
+/* dynamic LDS of k_at_score: the token's queries, a tile of AT_SB pooled
+ * keys (rows padded by 4 floats: 16-byte aligned, banks staggered), the
+ * per-head dots; at most 53 KB (ih * ihd <= 8192, ihd <= 256) */
 static size_t at_score_lds(int ih, int ihd) {
-    return ((size_t)ih * ihd + (size_t)AT_SB * (ihd + 1) + (size_t)ih * AT_SB) * 4;
+    return ((size_t)ih * ihd + (size_t)AT_SB * (ihd + 4) + (size_t)ih * AT_SB) * 4;
 }
 
 /* grid (n, ceil(nb / AT_SB)): workgroup = (token t, AT_SB blocks), thread
- * (block tid % AT_SB, head slot tid / AT_SB) runs the heads of its slot.
- * The arithmetic is the reference's order (model.c:1030-1045): per head
- * one chain dot = dot + relu(q_i * p_i) over i ascending from 0, the heads
- * added in order from 0, then / sqrt(ihd); so the scores, and the blocks
- * they keep, are the oracle's bit for bit. */
+ * (block tid % AT_SB, head slot tid / AT_SB) runs the heads of its slot, reading
+ * four query and key values per LDS access.  The arithmetic is the
+ * reference's order (model.c:1030-1045): per head one chain dot = dot +
+ * relu(q_i * p_i) over i ascending from 0, the heads added in order from
+ * 0, then / sqrt(ihd); so the scores, and the blocks they keep, are the
+ * oracle's bit for bit. */
 __global__ __launch_bounds__(256) void k_at_score(AtScoreArgs a) {
+    constexpr int SB = AT_SB;
     extern __shared__ float at_lds[];
-    const int ih = a.ih, ihd = a.ihd, pl = ihd + 1;
+    const int ih = a.ih, ihd = a.ihd, pl = ihd + 4;
     float *s_q = at_lds;                       /* [ih * ihd] */
-    float *s_p = s_q + ih * ihd;               /* [AT_SB][ihd + 1] */
-    float *s_d = s_p + AT_SB * pl;             /* [ih][AT_SB] */
-    const int tid = threadIdx.x, t = blockIdx.x, b0 = (int)blockIdx.y * AT_SB;
-    const int nbt = min(AT_SB, a.nb - b0);
-    for (int i = tid; i < ih * ihd; i += 256) s_q[i] = qk_ld(a.qi + (size_t)t * ih * ihd + i);
-    for (int i = tid; i < nbt * ihd; i += 256) {
-        const int bb = i / ihd, ii = i - bb * ihd;
-        s_p[bb * pl + ii] = qk_ld(a.pooled + (size_t)(b0 + bb) * ihd + ii);
+    float *s_p = s_q + ih * ihd;               /* [SB][ihd + 4] */
+    float *s_d = s_p + SB * pl;                /* [ih][SB] */
+    const int tid = threadIdx.x, t = blockIdx.x, b0 = (int)blockIdx.y * SB;
+    const int nbt = min(SB, a.nb - b0);
+    /* staging in float4s, four loads in flight per thread and round (a
+     * loop with a runtime trip count would wait on each load) */
+    const int q4 = ih * ihd / 4, r4 = ihd / 4, p4 = nbt * r4;
+    const float4 *qsrc = (const float4 *)(a.qi + (size_t)t * ih * ihd);
+    const float4 *psrc = (const float4 *)(a.pooled + (size_t)b0 * ihd);
+    for (int j0 = tid; j0 < q4 + p4; j0 += 4 * 256) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int j = min(j0 + 256 * u, q4 + p4 - 1);
+            v[u] = j < q4 ? qk_ld(qsrc + j) : qk_ld(psrc + (j - q4));
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int j = j0 + 256 * u;
+            if (j < q4) {
+                *(float4 *)(s_q + 4 * j) = v[u];
+            } else if (j < q4 + p4) {
+                const int bb = (j - q4) / r4, c4 = (j - q4) - bb * r4;
+                *(float4 *)(s_p + bb * pl + 4 * c4) = v[u];
+            }
+        }
     }
     __syncthreads();
-    const int bl = tid & (AT_SB - 1);
+    const int bl = tid % SB;
     if (bl < nbt)
-        for (int hh = tid / AT_SB; hh < ih; hh += 256 / AT_SB) {
-            const float *q = s_q + hh * ihd, *p = s_p + bl * pl;
+        for (int hh = tid / SB; hh < ih; hh += 256 / SB) {
+            const float4 *q = (const float4 *)(s_q + hh * ihd), *p = (const float4 *)(s_p + bl * pl);
             float dot = 0.0f;
-            for (int i = 0; i < ihd; i++) {
-                const float v = q[i] * p[i];
-                dot = dot + (v > 0.0f ? v : 0.0f);
+#pragma unroll 4
+            for (int i = 0; i < ihd / 4; i++) {
+                const float4 qv = q[i], pv = p[i];
+                const float v0 = qv.x * pv.x, v1 = qv.y * pv.y, v2 = qv.z * pv.z, v3 = qv.w * pv.w;
+                dot = dot + (v0 > 0.0f ? v0 : 0.0f);
+                dot = dot + (v1 > 0.0f ? v1 : 0.0f);
+                dot = dot + (v2 > 0.0f ? v2 : 0.0f);
+                dot = dot + (v3 > 0.0f ? v3 : 0.0f);
             }
-            s_d[hh * AT_SB + bl] = dot;
+            s_d[hh * SB + bl] = dot;
         }
     __syncthreads();
     if (tid < nbt) {
         float acc = 0.0f;
-        for (int hh = 0; hh < ih; hh++) acc = acc + s_d[hh * AT_SB + tid];
+        for (int hh = 0; hh < ih; hh++) acc = acc + s_d[hh * SB + tid];
         const int b = b0 + tid;
         float score = acc / sqrtf((float)ihd);
         if ((long long)b * a.comp + a.comp - 1 > (long long)(a.offset + t)) score = -INFINITY;
@@ -337,7 +402,17 @@ __global__ __launch_bounds__(AT_SEL_T) void k_at_sel(AtSelArgs a) {
     int *s_misc = s_hist + 256;                        /* [8] */
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, t = blockIdx.x;
     for (int i = tid; i < a.kw; i += AT_SEL_T) s_bits[i] = 0u;
-    for (int b = tid; b < a.nb; b += AT_SEL_T) s_key[b] = qk_ld(a.skey + (size_t)t * a.ldk + b);
+    /* four key loads in flight per thread and round (a loop with a runtime
+     * trip count would wait on each load) */
+    const uint32_t *ksrc = a.skey + (size_t)t * a.ldk;
+    for (int b0 = tid; b0 < a.nb; b0 += 4 * AT_SEL_T) {
+        uint32_t v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = qk_ld(ksrc + min(b0 + AT_SEL_T * u, a.nb - 1));
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (b0 + AT_SEL_T * u < a.nb) s_key[b0 + AT_SEL_T * u] = v[u];
+    }
     __syncthreads();
     if (a.btop >= a.nb) {
         for (int b = tid; b < a.nb; b += AT_SEL_T) atomicOr(&s_bits[b >> 5], 1u << (b & 31));
