@@ -152,17 +152,37 @@ struct DnRecArgs {
     int n, hk, hv, dk, dv, kc, conv_dim;
 };
 
-/* silu(conv) of channel c at token t: sum over taps i of w[c, i] * seq[t+i, c]
- * with seq = [conv_state rows; mixed rows] */
-__device__ __forceinline__ float dn_conv_silu(const DnRecArgs &a, int t, int c) {
-    float acc = 0.0f;
-    for (int i = 0; i < a.kc; i++) {
-        const int j = t + i;
-        const float s = j < a.kc - 1 ? qk_ld(a.conv_state + (size_t)j * a.conv_dim + c)
-                                     : qk_ld(a.mixed + (size_t)(j - (a.kc - 1)) * a.conv_dim + c);
-        acc = fmaf(s, qk_bf16(qk_ld(a.conv_w + (size_t)c * a.kc + i)), acc);
+/* silu(conv) of channels ch[0..NC) at token t: sum over taps i of
+ * w[c, i] * seq[t+i, c] with seq = [conv_state rows; mixed rows], the fma
+ * chain over i ascending.  The taps come four at a time with every load of
+ * a round (all NC channels) in flight: a loop with a runtime trip count
+ * would wait on each load.  Past kc the last tap is read again, unused. */
+template <int NC>
+__device__ __forceinline__ void dn_conv_silu(const DnRecArgs &a, int t, const int (&ch)[NC], float (&out)[NC]) {
+    float acc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; c++) acc[c] = 0.0f;
+    for (int i0 = 0; i0 < a.kc; i0 += 4) {
+        float sv[NC][4];
+        uint16_t wv[NC][4];
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int i = min(i0 + u, a.kc - 1), j = t + i;
+                const float *src = j < a.kc - 1 ? a.conv_state + (size_t)j * a.conv_dim + ch[c]
+                                                : a.mixed + (size_t)(j - (a.kc - 1)) * a.conv_dim + ch[c];
+                sv[c][u] = qk_ld(src);
+                wv[c][u] = qk_ld(a.conv_w + (size_t)ch[c] * a.kc + i);
+            }
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                if (i0 + u < a.kc) acc[c] = fmaf(sv[c][u], qk_bf16(wv[c][u]), acc[c]);
     }
-    return qk_silu(acc);
+#pragma unroll
+    for (int c = 0; c < NC; c++) out[c] = qk_silu(acc[c]);
 }
 
 template <int EPL>
@@ -191,11 +211,28 @@ __global__ __launch_bounds__(256) void k_dn_rec(DnRecArgs a) {
     const float al = expf(qk_ld(a.a_log + h)), dtb = qk_ld(a.dt_bias + h);
     const float scale_q = 1.0f / sqrtf((float)DK);
     for (int t = 0; t < a.n; t++) {
-        for (int c = tid; c < 2 * DK + DN_RB; c += 256) {
-            const int ch = c < DK ? kh * DK + c
-                         : c < 2 * DK ? key_dim + kh * DK + (c - DK)
-                                      : 2 * key_dim + h * a.dv + rb + (c - 2 * DK);
-            s_ch[c] = dn_conv_silu(a, t, ch);
+        /* what the token's later steps read, loaded with the channels' taps
+         * (every thread loads them; the addresses are shared) */
+        const size_t zi = (size_t)t * value_dim + (size_t)h * a.dv + row;
+        const float zv = qk_ld(a.z + zi), nwv = qk_ld(a.norm_w + row);
+        const float av = qk_ld(a.a + (size_t)t * a.hv + h), bv = qk_ld(a.b + (size_t)t * a.hv + h);
+        {
+            /* the block's q, k, v channels, NCC per thread (all their loads
+             * in flight); past the last one a thread repeats it */
+            constexpr int NCC = (2 * DK + DN_RB + 255) / 256;
+            int ch[NCC];
+#pragma unroll
+            for (int u = 0; u < NCC; u++) {
+                const int c = min(tid + 256 * u, 2 * DK + DN_RB - 1);
+                ch[u] = c < DK ? kh * DK + c
+                      : c < 2 * DK ? key_dim + kh * DK + (c - DK)
+                                   : 2 * key_dim + h * a.dv + rb + (c - 2 * DK);
+            }
+            float v[NCC];
+            dn_conv_silu<NCC>(a, t, ch, v);
+#pragma unroll
+            for (int u = 0; u < NCC; u++)
+                if (tid + 256 * u < 2 * DK + DN_RB) s_ch[tid + 256 * u] = v[u];
         }
         __syncthreads();
         if (wave < 2) {
@@ -208,7 +245,6 @@ __global__ __launch_bounds__(256) void k_dn_rec(DnRecArgs a) {
             ss = qk_group_sum<64>(ss);
             if (lane == 0) s_sc[wave] = 1.0f / sqrtf(ss + 1e-6f);
         } else if (tid == 128) {
-            const float av = qk_ld(a.a + (size_t)t * a.hv + h), bv = qk_ld(a.b + (size_t)t * a.hv + h);
             s_sc[2] = expf(-al * log1pf(expf(av + dtb)));
             s_sc[3] = 1.0f / (1.0f + expf(-bv));
         }
@@ -238,9 +274,7 @@ __global__ __launch_bounds__(256) void k_dn_rec(DnRecArgs a) {
         if ((tid & 15) == 0) {
             /* the gated norm's row factors here, its head factor (from the
              * sums of squares) in k_dn_out */
-            const size_t i = (size_t)t * value_dim + (size_t)h * a.dv + row;
-            const float zv = qk_ld(a.z + i);
-            qk_st(a.core + i, (o * qk_ld(a.norm_w + row)) * (1.0f / (1.0f + expf(-zv))));
+            qk_st(a.core + zi, (o * nwv) * (1.0f / (1.0f + expf(-zv))));
             s_o[tid >> 4] = o;
         }
         __syncthreads();
