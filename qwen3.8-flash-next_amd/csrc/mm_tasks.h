@@ -16,17 +16,27 @@
 #define MM_NARROW_N 64       /* batches up to this many tokens also get a 16-row list */
 #define MM_BM16 16
 
+/* a segment-table word: from LDS (the table this workgroup just built,
+ * mirrored there) or from global memory */
+template <bool LDS>
+__device__ __forceinline__ int mm_seg_ld(const int32_t *p) {
+    if (LDS) return *p;
+    return qk_ld(p);
+}
+
 /* One task list: {expert (-1 = shared), first position, rows, chunk} for
  * every chunk of bm rows of the segments with at least min_m rows; the
  * shared expert covers all n tokens at positions n*k.. .  list[0] =
  * count; entries from list + MM_TASK_HDR.  With `small`, the segments with
  * 1..min_m-1 rows (0 = shared) are listed for the GEMV kernels: small[0] =
- * count, then ids. */
+ * count, then ids.  LDS: segtab is the workgroup's LDS mirror of the
+ * table (no global round trip). */
+template <bool LDS>
 static __device__ void mm_tasks_list(const int32_t *segtab, int n, int k, int E, int min_m, int bm,
                                      int32_t *list, int32_t *small) {
     __shared__ int s_scan[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int U = min(max(qk_ld(segtab), 0), E);
+    const int U = min(max(mm_seg_ld<LDS>(segtab), 0), E);
     int4 *out = (int4 *)(list + MM_TASK_HDR);
     int base = 0, sbase = 0;
     /* segments 0..U in blocks of 1024; segment 0 is the shared expert */
@@ -36,9 +46,9 @@ static __device__ void mm_tasks_list(const int32_t *segtab, int n, int k, int E,
         if (sg == 0) {
             m = n;
         } else if (sg <= U) {
-            e = qk_ld(segtab + 3 * sg - 2);
-            p0 = qk_ld(segtab + 3 * sg - 1);
-            m = qk_ld(segtab + 3 * sg);
+            e = mm_seg_ld<LDS>(segtab + 3 * sg - 2);
+            p0 = mm_seg_ld<LDS>(segtab + 3 * sg - 1);
+            m = mm_seg_ld<LDS>(segtab + 3 * sg);
         }
         const int cnt = m >= min_m && m > 0 ? (m + bm - 1) / bm : 0;
         const int sm = m > 0 && m < min_m ? 1 : 0;
@@ -83,10 +93,11 @@ static __device__ void mm_tasks_list(const int32_t *segtab, int n, int k, int E,
  * past the small list's 2 + E ints, rounded up to 16 bytes for its int4
  * entries). */
 #define MM_SMALL16(E) ((2 + (E) + 3) & ~3)
+template <bool LDS = false>
 static __device__ void mm_tasks_block(const int32_t *segtab, int n, int k, int E, int min_m, int32_t *tasks,
                                int32_t *small) {
-    mm_tasks_list(segtab, n, k, E, min_m, MM_BM, tasks, small);
-    if (n <= MM_NARROW_N) mm_tasks_list(segtab, n, k, E, min_m, MM_BM16, small + MM_SMALL16(E), nullptr);
+    mm_tasks_list<LDS>(segtab, n, k, E, min_m, MM_BM, tasks, small);
+    if (n <= MM_NARROW_N) mm_tasks_list<LDS>(segtab, n, k, E, min_m, MM_BM16, small + MM_SMALL16(E), nullptr);
 }
 
 #endif

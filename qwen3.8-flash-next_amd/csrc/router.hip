@@ -490,9 +490,11 @@ __device__ int block_exscan(int v, int *lds /* >= NT/64 ints */, int &total) {
 /* per-expert counts (cnt[j] for experts e = threadIdx.x*PER + j) ->
  * offsets and segtab; lds_off gets offsets when non-null; returns the
  * total count (in every thread) */
+/* the segment table goes to segtab and, when s_seg is given, to that LDS
+ * mirror (for the task lists built next by the same workgroup) */
 template <int NT>
 __device__ int counts_to_offsets(const int *cnt, int E, int *lds_scan, int32_t *offsets,
-                                  int32_t *segtab, int *lds_off) {
+                                  int32_t *segtab, int *lds_off, int32_t *s_seg) {
     constexpr int PER = QK_MAX_EXPERTS / NT;
     int csum = 0, asum = 0;
 #pragma unroll
@@ -516,6 +518,11 @@ __device__ int counts_to_offsets(const int *cnt, int E, int *lds_scan, int32_t *
                 segtab[1 + 3 * uoff] = e;
                 segtab[2 + 3 * uoff] = off;
                 segtab[3 + 3 * uoff] = cnt[j];
+                if (s_seg) {
+                    s_seg[1 + 3 * uoff] = e;
+                    s_seg[2 + 3 * uoff] = off;
+                    s_seg[3 + 3 * uoff] = cnt[j];
+                }
                 uoff++;
             }
             off += cnt[j];
@@ -524,6 +531,7 @@ __device__ int counts_to_offsets(const int *cnt, int E, int *lds_scan, int32_t *
     if (threadIdx.x == 0) {
         offsets[E] = total;
         segtab[0] = ntot;
+        if (s_seg) s_seg[0] = ntot;
     }
     return total;
 }
@@ -532,7 +540,7 @@ __device__ int counts_to_offsets(const int *cnt, int E, int *lds_scan, int32_t *
  * run by one NT-thread workgroup */
 template <int NT>
 __device__ void dispatch_block(const int32_t *s_idx, int n, int k, int E, int32_t *offsets,
-                               int32_t *perm, int32_t *pos, int32_t *segtab) {
+                               int32_t *perm, int32_t *pos, int32_t *segtab, int32_t *s_seg) {
     __shared__ uint32_t s_bits[QK_MAX_EXPERTS * (QK_SMALL_N / 32)];
     __shared__ int32_t s_wpre[QK_MAX_EXPERTS * (QK_SMALL_N / 32)];
     __shared__ int32_t s_off[QK_MAX_EXPERTS];
@@ -558,7 +566,7 @@ __device__ void dispatch_block(const int32_t *s_idx, int n, int k, int E, int32_
                 cnt[j] += __popc(s_bits[e * NW + wd]);
             }
     }
-    counts_to_offsets<NT>(cnt, E, s_scan, offsets, segtab, s_off);
+    counts_to_offsets<NT>(cnt, E, s_scan, offsets, segtab, s_off, s_seg);
     __syncthreads();
     for (int f = tid; f < n * k; f += NT) {
         const int t = f / k, e = s_idx[f], wd = t >> 5;
@@ -624,13 +632,14 @@ __global__ __launch_bounds__(64) void k_topk_dispatch_one(SmallDispArgs a) {
 template <int PL>
 __global__ __launch_bounds__(1024) void k_topk_dispatch_small(SmallDispArgs a) {
     __shared__ int32_t s_idx[QK_SMALL_NK];
+    __shared__ int32_t s_seg[1 + 3 * QK_MAX_EXPERTS]; /* the segment table, mirrored */
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     for (int t = wave; t < a.tk.n; t += 16) topk_token<PL>(a.tk, t, lane, s_idx);
     __syncthreads();
-    dispatch_block<1024>(s_idx, a.tk.n, a.tk.k, a.tk.E, a.offsets, a.perm, a.pos, a.segtab);
+    dispatch_block<1024>(s_idx, a.tk.n, a.tk.k, a.tk.E, a.offsets, a.perm, a.pos, a.segtab, s_seg);
     if (a.tasks) {
         __syncthreads(); /* the segment table, written by this workgroup */
-        mm_tasks_block(a.segtab, a.tk.n, a.tk.k, a.tk.E, a.min_m, a.tasks, a.small);
+        mm_tasks_block<true>(s_seg, a.tk.n, a.tk.k, a.tk.E, a.min_m, a.tasks, a.small);
     }
 }
 
@@ -641,12 +650,13 @@ __global__ __launch_bounds__(1024) void k_dispatch_small(const int32_t *idx, int
                                                          int32_t *pos, int32_t *segtab, int min_m,
                                                          int32_t *tasks, int32_t *small) {
     __shared__ int32_t s_idx[QK_SMALL_NK];
+    __shared__ int32_t s_seg[1 + 3 * QK_MAX_EXPERTS]; /* the segment table, mirrored */
     for (int f = threadIdx.x; f < n * k; f += 1024) s_idx[f] = qk_ld(idx + f);
     __syncthreads();
-    dispatch_block<1024>(s_idx, n, k, E, offsets, perm, pos, segtab);
+    dispatch_block<1024>(s_idx, n, k, E, offsets, perm, pos, segtab, s_seg);
     if (tasks) {
         __syncthreads();
-        mm_tasks_block(segtab, n, k, E, min_m, tasks, small);
+        mm_tasks_block<true>(s_seg, n, k, E, min_m, tasks, small);
     }
 }
 
@@ -726,14 +736,15 @@ __global__ __launch_bounds__(1024) void k_count_offsets(int E, int32_t *offsets,
                                                         int32_t *perm, int nk, int n, int k,
                                                         int min_m, int32_t *tasks, int32_t *small) {
     __shared__ int s_scan[16];
+    __shared__ int32_t s_seg[1 + 3 * QK_MAX_EXPERTS]; /* the segment table, mirrored */
     const int tid = threadIdx.x;
     int cnt[1] = {tid < E ? offsets[tid] : 0};
     __syncthreads();
-    const int total = counts_to_offsets<1024>(cnt, E, s_scan, offsets, segtab, nullptr);
+    const int total = counts_to_offsets<1024>(cnt, E, s_scan, offsets, segtab, nullptr, s_seg);
     for (int i = total + tid; i < nk; i += 1024) perm[i] = -1;
     if (tasks) {
         __syncthreads(); /* the segment table, written by this workgroup */
-        mm_tasks_block(segtab, n, k, E, min_m, tasks, small);
+        mm_tasks_block<true>(s_seg, n, k, E, min_m, tasks, small);
     }
 }
 
