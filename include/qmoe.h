@@ -487,6 +487,15 @@ int qmoe_dn_reset_state(qmoe_dn_ctx *ctx, int layer, void *stream, qmoe_err *err
  * the layer's states.  Asynchronous on `stream`. */
 int qmoe_dn_forward(qmoe_dn_ctx *ctx, int layer, const float *x, int n, float *out, void *stream,
                     qmoe_err *err);
+/* qmoe_dn_forward followed by the gated residual's update of the mixer's
+ * output into the hyper state, hyper[t, j, :] += inject[t, j] * out[t, :]
+ * for j < hc (qmoe_gr_inject, model.c:1699-1707), done in the mixer's last
+ * launch with the same arithmetic: one launch fewer per layer.  hyper [n,
+ * hc, d] and inject [n, hc] f32 device, 1 <= hc <= 8; out may be NULL (not
+ * written).  No counterpart in the reference: its layer loop calls the
+ * mixer and the update separately (model.c:1683-1688, 1699-1707). */
+int qmoe_dn_forward_inject(qmoe_dn_ctx *ctx, int layer, const float *x, int n, float *out, float *hyper,
+                           const float *inject, int hc, void *stream, qmoe_err *err);
 /* device addresses of a layer's states: conv [conv_kernel-1, conv_dim] and
  * recurrent [hv, dv, dk] f32 (for inspection and for seeding a state) */
 int qmoe_dn_state(qmoe_dn_ctx *ctx, int layer, float **conv_state, float **rec_state,
@@ -579,6 +588,12 @@ int qmoe_attn_reset(qmoe_attn_ctx *ctx, int layer, qmoe_err *err);
  * cache length is host state, so calls on one layer run in call order. */
 int qmoe_attn_forward(qmoe_attn_ctx *ctx, int layer, const float *x, int n, int offset, float *out,
                       void *stream, qmoe_err *err);
+/* qmoe_attn_forward with the gated residual's update fused into o_proj's
+ * launch, as qmoe_dn_forward_inject (hyper [n, hc, d], inject [n, hc],
+ * 1 <= hc <= 8, out may be NULL).  No counterpart in the reference
+ * (model.c:1683-1688 calls the mixer, 1699-1707 the update). */
+int qmoe_attn_forward_inject(qmoe_attn_ctx *ctx, int layer, const float *x, int n, int offset, float *out,
+                             float *hyper, const float *inject, int hc, void *stream, qmoe_err *err);
 /* device addresses of a layer's caches (k and v [len, kvh*hd], indexer
  * keys [len, idx_hd]; with slide, the window's first row) and their current
  * length */

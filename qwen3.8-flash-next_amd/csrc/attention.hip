@@ -58,9 +58,12 @@ struct RowsArgs {
     int nseg;
     const float *x;             /* [n, K] */
     int K, n;
+    float *hyper;               /* INJ (one q4 segment): hyper[t, j] += inject[t, j] * out[t], */
+    const float *inject;        /* [n, hc, ostride] and [n, hc] */
+    int hc;
 };
 
-template <int P>
+template <int P, bool INJ>
 __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
     const int lane = threadIdx.x & 63;
     const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * AT_RPW;
@@ -91,6 +94,20 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
             }
         }
         for (int t = 0; t < a.n; t++) {
+            /* INJ: the token's inject weights and the hyper values of this
+             * wave's rows, loaded with x (clamped addresses) */
+            float iv[INJ ? QK_INJECT_MAX_HC : 1], hv[INJ ? AT_RPW : 1][INJ ? QK_INJECT_MAX_HC : 1];
+            if (INJ) {
+#pragma unroll
+                for (int q = 0; q < QK_INJECT_MAX_HC; q++) {
+                    const int qc = min(q, a.hc - 1);
+                    iv[INJ ? q : 0] = qk_ld(a.inject + (size_t)t * a.hc + qc);
+#pragma unroll
+                    for (int j = 0; j < AT_RPW; j++)
+                        hv[INJ ? j : 0][INJ ? q : 0] =
+                            qk_ld(a.hyper + ((size_t)t * a.hc + qc) * S.ostride + min(rr + j, S.rows - 1));
+                }
+            }
             XRaw<P, false> xr;
             load_xraw<64, P, false>(a.x, (size_t)t, a.K, lane, xr);
             XPairs<64, P, false> xp;
@@ -98,7 +115,15 @@ __global__ __launch_bounds__(256) void k_rows(RowsArgs a) {
 #pragma unroll
             for (int j = 0; j < AT_RPW; j++) {
                 const float v = qk_group_sum<64>(row_part<64, P, false>(wq[j], ws[j], wb[j], xp));
-                if (lane == 0) qk_st(S.out + (size_t)t * S.ostride + rr + j, v);
+                if (lane == 0) {
+                    if (S.out) qk_st(S.out + (size_t)t * S.ostride + rr + j, v);
+                    if (INJ)
+#pragma unroll
+                        for (int q = 0; q < QK_INJECT_MAX_HC; q++)
+                            if (q < a.hc)
+                                qk_st(a.hyper + ((size_t)t * a.hc + q) * S.ostride + rr + j,
+                                      fmaf(iv[INJ ? q : 0], v, hv[INJ ? j : 0][INJ ? q : 0]));
+                }
             }
         }
         return;
@@ -864,12 +889,19 @@ static int at_rows_launch(RowsArgs &r, hipStream_t st) {
     const int rows = r.start[r.nseg];
     const int waves = (rows + AT_RPW - 1) / AT_RPW;
     const dim3 grid((waves + 3) / 4);
+    const bool inj = r.hyper != nullptr;
+#define AT_ROWS_L(P)                                                                  \
+    do {                                                                              \
+        if (inj) hipLaunchKernelGGL((k_rows<P, true>), grid, dim3(256), 0, st, r);    \
+        else hipLaunchKernelGGL((k_rows<P, false>), grid, dim3(256), 0, st, r);       \
+    } while (0)
     switch ((r.K / 32 + 63) / 64) {
-    case 1: hipLaunchKernelGGL(k_rows<1>, grid, dim3(256), 0, st, r); break;
-    case 2: hipLaunchKernelGGL(k_rows<2>, grid, dim3(256), 0, st, r); break;
-    case 3: hipLaunchKernelGGL(k_rows<3>, grid, dim3(256), 0, st, r); break;
-    default: hipLaunchKernelGGL(k_rows<4>, grid, dim3(256), 0, st, r); break;
+    case 1: AT_ROWS_L(1); break;
+    case 2: AT_ROWS_L(2); break;
+    case 3: AT_ROWS_L(3); break;
+    default: AT_ROWS_L(4); break;
     }
+#undef AT_ROWS_L
     return QK_CHECK_LAUNCH();
 }
 
@@ -899,8 +931,10 @@ extern "C" size_t qk_at_sel_lds(const qk_at_shape *s, int nb) {
 
 extern "C" int qk_launch_at(const qk_at_shape *s, const qk_at_dev *W, const float *x, int n, int offset,
                             int pos0, int len0, float *out, float *k_cache, float *v_cache, float *idx_keys,
-                            float *pooled, const qk_at_scratch *sc, void *stream) {
+                            float *pooled, const qk_at_scratch *sc, const qk_inject *inj, void *stream) {
     if (n <= 0) return 0;
+    if (inj && inj->hyper && (inj->hc < 1 || inj->hc > QK_INJECT_MAX_HC || !inj->inject))
+        return (int)hipErrorInvalidValue;
     if (!qk_at_shape_ok(s)) return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)stream;
     const int h = s->h, kvh = s->kvh, hd = s->hd, ih = s->ih, ihd = s->ihd;
@@ -913,6 +947,9 @@ extern "C" int qk_launch_at(const qk_at_shape *s, const qk_at_dev *W, const floa
     r.x = x;
     r.K = s->d;
     r.n = n;
+    r.hyper = nullptr;
+    r.inject = nullptr;
+    r.hc = 1;
     at_seg(r, W->q_q, W->q_s, W->q_b, nullptr, 2 * h * hd, sc->qg, 2 * h * hd);
     at_seg(r, W->k_q, W->k_s, W->k_b, nullptr, kvh * hd, sc->kraw, kvh * hd);
     at_seg(r, W->v_q, W->v_s, W->v_b, nullptr, kvh * hd, sc->vraw, kvh * hd);
@@ -994,6 +1031,9 @@ extern "C" int qk_launch_at(const qk_at_shape *s, const qk_at_dev *W, const floa
     o.x = sc->ao;
     o.K = h * hd;
     o.n = n;
+    o.hyper = inj ? inj->hyper : nullptr;
+    o.inject = inj ? inj->inject : nullptr;
+    o.hc = inj && inj->hyper ? inj->hc : 1;
     at_seg(o, W->o_q, W->o_s, W->o_b, nullptr, s->d, out, s->d);
     return at_rows_launch(o, st);
 }

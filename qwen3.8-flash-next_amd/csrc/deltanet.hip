@@ -305,7 +305,9 @@ struct DnOutArgs {
     const float *mixed;        /* [n, conv_dim] */
     float *conv_state;         /* [kc-1, conv_dim], moved on by n tokens */
     float *out;                /* [n, d] */
-    int n, d, value_dim, dv, kc, conv_dim, ch_per_wg;
+    float *hyper;              /* INJ: [n, hc, d], hyper[t, j] += inject[t, j] * out[t] */
+    const float *inject;       /* INJ: [n, hc] */
+    int n, d, value_dim, dv, kc, conv_dim, ch_per_wg, hc;
 };
 
 #define DN_ORW 2 /* out_proj rows per wave */
@@ -322,7 +324,7 @@ struct DnOutArgs {
  * the conv state moves on at the end (its stores would otherwise hold the
  * loads back).  No LDS and no barrier.
  */
-template <int P>
+template <int P, bool INJ>
 __global__ __launch_bounds__(256) void k_dn_out(DnOutArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int K = a.value_dim, CH = K >> 5, G = K >> 6;
@@ -362,6 +364,20 @@ __global__ __launch_bounds__(256) void k_dn_out(DnOutArgs a) {
         }
     }
     for (int t = 0; t < a.n; t++) {
+        /* INJ: the token's inject weights and the hyper values of this
+         * wave's rows, loaded before the row sums (clamped addresses) */
+        float iv[INJ ? QK_INJECT_MAX_HC : 1], hv[INJ ? DN_ORW : 1][INJ ? QK_INJECT_MAX_HC : 1];
+        if (INJ) {
+#pragma unroll
+            for (int j = 0; j < QK_INJECT_MAX_HC; j++) {
+                const int jc = min(j, a.hc - 1);
+                iv[INJ ? j : 0] = qk_ld(a.inject + (size_t)t * a.hc + jc);
+#pragma unroll
+                for (int q = 0; q < DN_ORW; q++)
+                    hv[INJ ? q : 0][INJ ? j : 0] =
+                        qk_ld(a.hyper + ((size_t)t * a.hc + jc) * a.d + min(r0 + q, a.d - 1));
+            }
+        }
         XRaw<P, false> xr;
 #pragma unroll
         for (int ps = 0; ps < P; ps++) {
@@ -392,7 +408,15 @@ __global__ __launch_bounds__(256) void k_dn_out(DnOutArgs a) {
         for (int j = 0; j < DN_ORW; j++) {
             const float v = qk_group_sum<64>(row_part<64, P, false>(wq[j], ws[j], wb[j], xp));
             const int rr = r0 + j;
-            if (lane == 0 && rr < a.d) qk_st(a.out + (size_t)t * a.d + rr, v);
+            if (lane == 0 && rr < a.d) {
+                if (a.out) qk_st(a.out + (size_t)t * a.d + rr, v);
+                if (INJ)
+#pragma unroll
+                    for (int q = 0; q < QK_INJECT_MAX_HC; q++)
+                        if (q < a.hc)
+                            qk_st(a.hyper + ((size_t)t * a.hc + q) * a.d + rr,
+                                  fmaf(iv[INJ ? q : 0], v, hv[INJ ? j : 0][INJ ? q : 0]));
+            }
         }
     }
     }
@@ -424,7 +448,7 @@ extern "C" int qk_dn_shape_ok(const qk_dn_shape *s) {
 
 extern "C" int qk_launch_dn(const qk_dn_shape *s, const qk_dn_dev *W, const float *x, int n, float *out,
                             float *conv_state, float *rec_state, float *mixed, float *z, float *av,
-                            float *bv, float *core, float *ssp, void *stream) {
+                            float *bv, float *core, float *ssp, const qk_inject *inj_in, void *stream) {
     if (n <= 0) return 0;
     if (!qk_dn_shape_ok(s)) return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)stream;
@@ -472,6 +496,11 @@ extern "C" int qk_launch_dn(const qk_dn_shape *s, const qk_dn_dev *W, const floa
     oa.out_q = W->out_q; oa.out_s = W->out_s; oa.out_b = W->out_b;
     oa.core = core; oa.ssp = ssp; oa.mixed = mixed;
     oa.conv_state = conv_state; oa.out = out;
+    const bool inj = inj_in && inj_in->hyper;
+    if (inj && (inj_in->hc < 1 || inj_in->hc > QK_INJECT_MAX_HC || !inj_in->inject)) return (int)hipErrorInvalidValue;
+    oa.hyper = inj ? inj_in->hyper : nullptr;
+    oa.inject = inj ? inj_in->inject : nullptr;
+    oa.hc = inj ? inj_in->hc : 1;
     oa.n = n; oa.d = s->d; oa.value_dim = value_dim; oa.dv = s->dv; oa.kc = s->kc;
     oa.conv_dim = conv_dim;
     const int owgs = (s->d + 4 * DN_ORW - 1) / (4 * DN_ORW);
@@ -479,10 +508,16 @@ extern "C" int qk_launch_dn(const qk_dn_shape *s, const qk_dn_dev *W, const floa
     if (oa.ch_per_wg > 256) return (int)hipErrorInvalidValue;
     const int p_out = (value_dim / 32 + 63) / 64;
     switch (p_out) {
-    case 1: hipLaunchKernelGGL(k_dn_out<1>, dim3(owgs), dim3(256), 0, st, oa); break;
-    case 2: hipLaunchKernelGGL(k_dn_out<2>, dim3(owgs), dim3(256), 0, st, oa); break;
-    case 3: hipLaunchKernelGGL(k_dn_out<3>, dim3(owgs), dim3(256), 0, st, oa); break;
-    default: hipLaunchKernelGGL(k_dn_out<4>, dim3(owgs), dim3(256), 0, st, oa); break;
+#define DN_OUT_L(P)                                                                          \
+    do {                                                                                     \
+        if (inj) hipLaunchKernelGGL((k_dn_out<P, true>), dim3(owgs), dim3(256), 0, st, oa);  \
+        else hipLaunchKernelGGL((k_dn_out<P, false>), dim3(owgs), dim3(256), 0, st, oa);     \
+    } while (0)
+    case 1: DN_OUT_L(1); break;
+    case 2: DN_OUT_L(2); break;
+    case 3: DN_OUT_L(3); break;
+    default: DN_OUT_L(4); break;
+#undef DN_OUT_L
     }
     return QK_CHECK_LAUNCH();
 }

@@ -264,8 +264,8 @@ int qmoe_attn_reset(qmoe_attn_ctx *c, int layer, qmoe_err *err) {
     return 0;
 }
 
-int qmoe_attn_forward(qmoe_attn_ctx *c, int layer, const float *x, int n, int offset, float *out,
-                      void *stream, qmoe_err *err) {
+static int attn_forward(qmoe_attn_ctx *c, int layer, const float *x, int n, int offset, float *out,
+                        const qk_inject *inj, void *stream, qmoe_err *err) {
     if (at_check_layer(c, layer, err)) return -1;
     if (n < 0 || n > c->cfg.max_tokens) {
         at_set_err(err, "n = %d out of range [0, max_tokens = %d]", n, c->cfg.max_tokens);
@@ -280,7 +280,7 @@ int qmoe_attn_forward(qmoe_attn_ctx *c, int layer, const float *x, int n, int of
         return -1;
     }
     if (n == 0) return 0;
-    if (!x || !out) {
+    if (!x || (!out && !inj)) {
         at_set_err(err, "%s is NULL", x ? "out" : "x");
         return -1;
     }
@@ -354,11 +354,31 @@ int qmoe_attn_forward(qmoe_attn_ctx *c, int layer, const float *x, int n, int of
     W.idx_k_norm = (const float *)at_ptr(c, layer, AT_IK_NORM);
     W.rope = c->rope;
     const int rc = qk_launch_at(&c->shape, &W, x, n, offset, c->cfg.slide ? L->base : 0, len0, out,
-                                kc + w0 * kr, vc + w0 * kr, ic + w0 * ihd, pc + w0 / comp * ihd, &c->sc, stream);
+                                kc + w0 * kr, vc + w0 * kr, ic + w0 * ihd, pc + w0 / comp * ihd, &c->sc, inj,
+                                stream);
     if (at_hip_fail(err, rc, "attention launch")) return -1;
     L->len = len0 + n;
     if (len0 + n > c->cfg.idx_budget) c->last_kw = ((len0 + n) / c->cfg.idx_compress + 31) / 32;
     return 0;
+}
+
+int qmoe_attn_forward(qmoe_attn_ctx *c, int layer, const float *x, int n, int offset, float *out,
+                      void *stream, qmoe_err *err) {
+    return attn_forward(c, layer, x, n, offset, out, NULL, stream, err);
+}
+
+int qmoe_attn_forward_inject(qmoe_attn_ctx *c, int layer, const float *x, int n, int offset, float *out,
+                             float *hyper, const float *inject, int hc, void *stream, qmoe_err *err) {
+    if (!hyper || !inject) {
+        at_set_err(err, "%s is NULL", hyper ? "inject" : "hyper");
+        return -1;
+    }
+    if (hc < 1 || hc > QK_INJECT_MAX_HC) {
+        at_set_err(err, "hc = %d out of range [1, %d]", hc, QK_INJECT_MAX_HC);
+        return -1;
+    }
+    const qk_inject inj = {hyper, inject, hc};
+    return attn_forward(c, layer, x, n, offset, out, &inj, stream, err);
 }
 
 int qmoe_attn_cache(qmoe_attn_ctx *c, int layer, float **k_cache, float **v_cache, float **idx_keys,

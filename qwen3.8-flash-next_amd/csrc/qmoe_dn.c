@@ -215,8 +215,8 @@ int qmoe_dn_reset_state(qmoe_dn_ctx *c, int layer, void *stream, qmoe_err *err) 
     return dn_zero_states(c, layer, (hipStream_t)stream, err);
 }
 
-int qmoe_dn_forward(qmoe_dn_ctx *c, int layer, const float *x, int n, float *out, void *stream,
-                    qmoe_err *err) {
+static int dn_forward(qmoe_dn_ctx *c, int layer, const float *x, int n, float *out,
+                      const qk_inject *inj, void *stream, qmoe_err *err) {
     if (dn_check_layer(c, layer, err)) return -1;
     if (n < 0 || n > c->cfg.max_tokens) {
         dn_set_err(err, "n = %d out of range [0, max_tokens = %d]", n, c->cfg.max_tokens);
@@ -227,7 +227,7 @@ int qmoe_dn_forward(qmoe_dn_ctx *c, int layer, const float *x, int n, float *out
         return -1;
     }
     if (n == 0) return 0;
-    if (!x || !out) {
+    if (!x || (!out && !inj)) {
         dn_set_err(err, "%s is NULL", x ? "out" : "x");
         return -1;
     }
@@ -249,8 +249,27 @@ int qmoe_dn_forward(qmoe_dn_ctx *c, int layer, const float *x, int n, float *out
     W.dt_bias = (const float *)dn_ptr(c, layer, DT_DT_BIAS);
     const int rc = qk_launch_dn(&c->shape, &W, x, n, out, (float *)dn_ptr(c, layer, DT_CONV_STATE),
                                 (float *)dn_ptr(c, layer, DT_REC_STATE), c->mixed, c->z, c->a, c->b,
-                                c->core, c->ssp, stream);
+                                c->core, c->ssp, inj, stream);
     return dn_hip_fail(err, rc, "DeltaNet launch");
+}
+
+int qmoe_dn_forward(qmoe_dn_ctx *c, int layer, const float *x, int n, float *out, void *stream,
+                    qmoe_err *err) {
+    return dn_forward(c, layer, x, n, out, NULL, stream, err);
+}
+
+int qmoe_dn_forward_inject(qmoe_dn_ctx *c, int layer, const float *x, int n, float *out, float *hyper,
+                           const float *inject, int hc, void *stream, qmoe_err *err) {
+    if (!hyper || !inject) {
+        dn_set_err(err, "%s is NULL", hyper ? "inject" : "hyper");
+        return -1;
+    }
+    if (hc < 1 || hc > QK_INJECT_MAX_HC) {
+        dn_set_err(err, "hc = %d out of range [1, %d]", hc, QK_INJECT_MAX_HC);
+        return -1;
+    }
+    const qk_inject inj = {hyper, inject, hc};
+    return dn_forward(c, layer, x, n, out, &inj, stream, err);
 }
 
 int qmoe_dn_state(qmoe_dn_ctx *c, int layer, float **conv_state, float **rec_state, qmoe_err *err) {

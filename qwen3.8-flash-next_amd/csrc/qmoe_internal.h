@@ -208,9 +208,19 @@ int qk_dn_shape_ok(const qk_dn_shape *s);
 /* x [n, d] f32 -> out [n, d]; conv_state and rec_state are updated;
  * mixed [n, conv_dim], z [n, value_dim], a, b [n, hv], core [n, value_dim]
  * and ssp [n, hv, dv/16] are scratch */
+/* the gated residual's update after a mixer, fused into the mixer's last
+ * launch: hyper[t, j] = fma(inject[t, j], out[t], hyper[t, j]) for j < hc,
+ * the arithmetic of qk_launch_hc_inject (hyper NULL or no struct: none) */
+#define QK_INJECT_MAX_HC 8
+typedef struct {
+    float *hyper;         /* [n, hc, d] */
+    const float *inject;  /* [n, hc] */
+    int hc;
+} qk_inject;
+
 int qk_launch_dn(const qk_dn_shape *s, const qk_dn_dev *W, const float *x, int n, float *out,
                  float *conv_state, float *rec_state, float *mixed, float *z, float *a, float *b,
-                 float *core, float *ssp, void *stream);
+                 float *core, float *ssp, const qk_inject *inj, void *stream);
 int qk_launch_dn_zero(float *p, size_t count, void *stream);
 
 /* the full-attention mixer with the QSA indexer (attention.hip) */
@@ -248,7 +258,7 @@ size_t qk_at_sel_lds(const qk_at_shape *s, int nb);
  * offset - pos0 and block b's pooled key is rotated to pos0 + b*comp. */
 int qk_launch_at(const qk_at_shape *s, const qk_at_dev *W, const float *x, int n, int offset, int pos0,
                  int len0, float *out, float *k_cache, float *v_cache, float *idx_keys, float *pooled,
-                 const qk_at_scratch *sc, void *stream);
+                 const qk_at_scratch *sc, const qk_inject *inj, void *stream);
 
 /* the MLP hyper connection (hyper.hip): shapes it takes (hc <= 8, d and R
  * multiples of 64, d <= 2048, R <= 2048) */

@@ -145,6 +145,7 @@ SIGNATURES = {
     "qmoe_attn_upload_layer": (_I, [_P, _I, ctypes.POINTER(QmoeAttnWeights), ctypes.POINTER(QmoeErr)]),
     "qmoe_attn_reset": (_I, [_P, _I, ctypes.POINTER(QmoeErr)]),
     "qmoe_attn_forward": (_I, [_P, _I, _P, _I, _I, _P, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_attn_forward_inject": (_I, [_P, _I, _P, _I, _I, _P, _P, _P, _I, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_attn_cache": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(_P), ctypes.POINTER(_P),
                              ctypes.POINTER(_I), ctypes.POINTER(QmoeErr)]),
     "qmoe_attn_index_state": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(_P), ctypes.POINTER(_I),
@@ -159,6 +160,7 @@ SIGNATURES = {
     "qmoe_dn_upload_layer": (_I, [_P, _I, ctypes.POINTER(QmoeDnWeights), ctypes.POINTER(QmoeErr)]),
     "qmoe_dn_reset_state": (_I, [_P, _I, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_dn_forward": (_I, [_P, _I, _P, _I, _P, _P, ctypes.POINTER(QmoeErr)]),
+    "qmoe_dn_forward_inject": (_I, [_P, _I, _P, _I, _P, _P, _P, _I, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_dn_state": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(_P), ctypes.POINTER(QmoeErr)]),
     "qmoe_last_routing": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, ctypes.POINTER(QmoeErr)]),
     "qmoe_scratch_bytes": (ctypes.c_size_t, [_P]),
@@ -783,6 +785,18 @@ class AttentionContext:
                                        ctypes.byref(err)), err, "qmoe_attn_forward")
         return out
 
+    def forward_inject(self, layer, x, offset, hyper, inject, out=None, stream=None):
+        """forward, then hyper[t, j] += inject[t, j] * out[t] (the gated
+        residual's update) in the same launches; hyper [n, hc*d] and inject
+        [n, hc] f32 CUDA tensors; out is written only when given"""
+        n, hc = x.shape[0], inject.shape[1]
+        err = QmoeErr()
+        _check(lib().qmoe_attn_forward_inject(self._h, layer, _ptr(x), n, offset,
+                                              _ptr(out), _ptr(hyper),
+                                              _ptr(inject), hc, _stream(stream), ctypes.byref(err)),
+               err, "qmoe_attn_forward_inject")
+        return out
+
     def forward_raw(self, layer, x_ptr, n, offset, out_ptr, stream_handle):
         err = QmoeErr()
         rc = lib().qmoe_attn_forward(self._h, layer, x_ptr, n, offset, out_ptr, stream_handle,
@@ -873,6 +887,18 @@ class DeltaNetContext:
         err = QmoeErr()
         _check(lib().qmoe_dn_forward(self._h, layer, _ptr(x), n, _ptr(out), _stream(stream),
                                      ctypes.byref(err)), err, "qmoe_dn_forward")
+        return out
+
+    def forward_inject(self, layer, x, hyper, inject, out=None, stream=None):
+        """forward, then hyper[t, j] += inject[t, j] * out[t] (the gated
+        residual's update) in the same launches; hyper [n, hc*d] and inject
+        [n, hc] f32 CUDA tensors; out is written only when given"""
+        n, hc = x.shape[0], inject.shape[1]
+        err = QmoeErr()
+        _check(lib().qmoe_dn_forward_inject(self._h, layer, _ptr(x), n,
+                                            _ptr(out), _ptr(hyper),
+                                            _ptr(inject), hc, _stream(stream), ctypes.byref(err)),
+               err, "qmoe_dn_forward_inject")
         return out
 
     def forward_raw(self, layer, x_ptr, n, out_ptr, stream_handle):
@@ -978,8 +1004,9 @@ class DecoderStack:
     in place.  Layer l: the attention block's hyper connection (slot l of
     `gr`: gated_residual with inject, model.c:1671-1672), its mixer (gated
     DeltaNet, layer l of `dn`, or full attention with the QSA indexer,
-    layer l of `at`, at positions offset..), the inject update hyper +=
-    inject (x) out (model.c:1699-1707), then the MLP hyper connection, the
+    layer l of `at`, at positions offset..) with the inject update hyper +=
+    inject (x) out (model.c:1699-1707) fused into its last launch
+    (forward_inject), then the MLP hyper connection, the
     MoE layer and its inject update (layer l of `moe`,
     qmoe_hc_layer_forward, model.c:1710-1731).  After the last layer the
     final mixer (slot len(types) of `gr`, no inject, model.c:1743-1745)
@@ -992,7 +1019,6 @@ class DecoderStack:
         d, hc = gr.d, gr.hc
         self.mixed = torch.empty((n, d), dtype=torch.float32, device=device)
         self.inject = torch.empty((n, hc), dtype=torch.float32, device=device)
-        self.out = torch.empty((n, d), dtype=torch.float32, device=device)
         self.final = torch.empty((n, d), dtype=torch.float32, device=device)
 
     def step(self, hyper, offset):
@@ -1001,11 +1027,11 @@ class DecoderStack:
         L = len(self.types)
         for l, t in enumerate(self.types):
             self.gr.mix(l, hyper, mixed=self.mixed, inject=self.inject, want_inject=True)
+            # the mixer with the gated residual's update fused into its last launch
             if t == "dn":
-                self.dn.forward(l, self.mixed, out=self.out)
+                self.dn.forward_inject(l, self.mixed, hyper, self.inject)
             else:
-                self.at.forward(l, self.mixed, offset, out=self.out)
-            self.gr.inject(self.inject, self.out, hyper)
+                self.at.forward_inject(l, self.mixed, offset, hyper, self.inject)
             self.moe.hc_layer_forward(l, hyper, want_out=False)
         self.gr.mix(L, hyper, mixed=self.final, want_inject=False)
         return self.final

@@ -268,6 +268,62 @@ def test_layer_loop(torch_dev, shape, types, calls, seed):
         ch.close()
 
 
+@pytest.mark.parametrize("shape", ["tiny", "model"])
+@pytest.mark.parametrize("n", [1, 3])
+def test_mixer_forward_inject(torch_dev, shape, n):
+    """qmoe_dn_forward_inject / qmoe_attn_forward_inject (the gated
+    residual's update fused into the mixer's last launch) against the
+    separate mixer call + qmoe_gr_inject from the same state: out and the
+    hyper state bit-identical, the update bit-exact against the oracle's
+    inject_update of the GPU's out; and with out NULL the same hyper
+    state"""
+    torch, dev = torch_dev
+    shp = TINY if shape == "tiny" else MODEL
+    types = ("dn", "attn")
+    say(f"case: mixer forward_inject {shape} n={n}")
+    ch = Chain(torch, dev, shp, types, 7, 4)
+    try:
+        h0 = torch.from_numpy(orc.gen_hyper(n, shp["hc"], shp["d"], seed=71)).to(dev)
+        for l, t in enumerate(types):
+            tag = f"{shape} n={n} {t}"
+            m, inj = ch.gr.mix(l, h0)
+
+            def fwd(**kw):
+                if t == "dn":
+                    ch.dn.reset_state(l)
+                    return ch.dn.forward_inject(l, m, **kw) if "hyper" in kw else ch.dn.forward(l, m, **kw)
+                ch.at.reset(l)
+                return (ch.at.forward_inject(l, m, 0, **kw) if "hyper" in kw else ch.at.forward(l, m, 0, **kw))
+
+            out_a = fwd()
+            h_a = ch.gr.inject(inj, out_a, h0.clone())
+            out_b = torch.empty_like(out_a)
+            h_b = h0.clone()
+            fwd(hyper=h_b, inject=inj, out=out_b)
+            h_c = h0.clone()
+            fwd(hyper=h_c, inject=inj)
+            torch.cuda.synchronize()
+            assert torch.equal(out_a, out_b), tag
+            assert torch.equal(h_a, h_b), tag
+            assert torch.equal(h_a, h_c), tag
+            np.testing.assert_array_equal(
+                h_b.cpu().numpy(), ch.ah[l].inject_update(h0.cpu().numpy(), inj.cpu().numpy(),
+                                                          out_b.cpu().numpy()))
+            say(f"{tag}: out and hyper bit-identical to the separate update, update exact")
+        # refusals: hc out of range, missing hyper / inject
+        bad_inj = torch.zeros((n, 9), device=dev)
+        with pytest.raises(pkg_error()):
+            ch.dn.forward_inject(0, m, h0, bad_inj)
+        with pytest.raises(pkg_error()):
+            ch.at.forward_inject(1, m, 0, h0, bad_inj)
+    finally:
+        ch.close()
+
+
+def pkg_error():
+    return load_pkg().QmoeError
+
+
 def test_decoder_stack(torch_dev):
     """the benchmark's decoder stack (qmoe.DecoderStack: gated DeltaNet and
     full attention at 3 : 1 by the model's layer types, both hyper
