@@ -54,11 +54,14 @@ enum {
  * The reference requires the shared expert's intermediate size to equal
  * moe_intermediate_size (model.c:1391-1395 passes moe_inter as N). */
 typedef struct {
-    int hidden;      /* H: hidden_size; multiple of group_size */
+    int hidden;      /* H: hidden_size; multiple of 64 */
     int n_experts;   /* E: num_experts, <= 1024 */
     int top_k;       /* k: num_experts_per_tok, 1 <= k <= min(E, 64) */
-    int moe_inter;   /* I: moe_intermediate_size; multiple of group_size */
-    int group_size;  /* g: quantization group size; must be 64 */
+    int moe_inter;   /* I: moe_intermediate_size; multiple of 64 */
+    int group_size;  /* g: the experts' quantization group size (experts_load,
+                        model.c:646-651): 64, or 32, which the GEMV kernels
+                        take (a group-32 layer runs every segment on them; the
+                        MFMA grouped GEMMs take groups of 64) */
     int n_layers;    /* number of resident layers */
     int max_tokens;  /* largest n accepted per call; sizes the scratch */
     float rms_eps;   /* pre-router RMSNorm epsilon (used only when norm_w is set) */

@@ -26,7 +26,7 @@
 
 struct GemvArgs {
     const uint32_t *q[2];   /* routed [E, N, K/8] */
-    const uint16_t *s[2];   /* routed [E, N, K/64] */
+    const uint16_t *s[2];   /* routed [E, N, K/g] (g = 32 << (gsh == 1)) */
     const uint16_t *b[2];
     const uint32_t *sq[2];  /* shared [N, K/8] */
     const uint16_t *ss[2];
@@ -38,6 +38,7 @@ struct GemvArgs {
     int max_m;              /* skip segments with >= max_m rows (0: none skipped) */
     const int32_t *seglist; /* null, or [count, segment...]: only these segments */
     int in_by_pos;          /* input row = dispatch position (down) instead of token */
+    int gsh;                /* log2(group size / 32): 32-column chunk c is in group c >> gsh */
 };
 
 #define GV_RITER 2
@@ -49,7 +50,7 @@ __global__ __launch_bounds__(256) void k_q4gemv(GemvArgs a) {
     constexpr int RB = 4 * RPWAVE;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int sub = lane % LPR, rsub = lane / LPR;
-    const int CH = a.K >> 5, G = a.K >> 6;
+    const int CH = a.K >> 5, G = a.K >> (5 + a.gsh);
     const size_t wrow = (size_t)a.K >> 3; /* u32 words per weight row */
     const int tps = (a.N + RB - 1) / RB;
     const int u_raw = a.segtab[0];
@@ -132,8 +133,8 @@ __global__ __launch_bounds__(256) void k_q4gemv(GemvArgs a) {
 #pragma unroll
                 for (int mt = 0; mt < NMAT; mt++) {
                     wq[mt][it][ps] = qk_ld((const uint4 *)(q[mt] + (size_t)r * wrow) + c);
-                    rs[mt][it][ps] = qk_ld(sc[mt] + (size_t)r * G + (c >> 1));
-                    rbi[mt][it][ps] = qk_ld(bi[mt] + (size_t)r * G + (c >> 1));
+                    rs[mt][it][ps] = qk_ld(sc[mt] + (size_t)r * G + (c >> a.gsh));
+                    rbi[mt][it][ps] = qk_ld(bi[mt] + (size_t)r * G + (c >> a.gsh));
                 }
             }
         }
@@ -202,6 +203,7 @@ struct DcArgs {
     float *hyper;                 /* [n, hc, N] or null: hyper[t, j] += inject[t, j] * out[t] */
     const float *inject;          /* [n, hc] */
     int K, N, n, k, E, xbf16, hc;
+    int gsh;                      /* log2(group size / 32), as GemvArgs */
 };
 
 #define DC_WAVES 16
@@ -222,7 +224,7 @@ __global__ __launch_bounds__(64 * DC_WAVES) void k_down_combine(DcArgs a,
     uint32_t *s_x = (uint32_t *)dc_lds + ((((nk + a.n) * RB + 2 * nk) + 3) & ~3);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int sub = lane % LPR, rsub = lane / LPR;
-    const int CH = a.K >> 5, G = a.K >> 6;
+    const int CH = a.K >> 5, G = a.K >> (5 + a.gsh);
     const size_t wrow = (size_t)a.K >> 3;
     const int r0 = blockIdx.x * RB;
     const int u_raw = segtab[0];
@@ -295,8 +297,8 @@ __global__ __launch_bounds__(64 * DC_WAVES) void k_down_combine(DcArgs a,
                 const int c0 = ps * LPR + sub;
                 const int c = c0 < CH ? c0 : 0;
                 wq[it][ps] = qk_ld((const uint4 *)(q + (size_t)r * wrow) + c);
-                rs[it][ps] = qk_ld(sc + (size_t)r * G + (c >> 1));
-                rbi[it][ps] = qk_ld(bi + (size_t)r * G + (c >> 1));
+                rs[it][ps] = qk_ld(sc + (size_t)r * G + (c >> a.gsh));
+                rbi[it][ps] = qk_ld(bi + (size_t)r * G + (c >> a.gsh));
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -371,7 +373,8 @@ static int launch_gateup_topk_pl(const DecArgs &a, int cpl, dim3 grid, const Dec
 
 extern "C" int qk_gateup_topk_supported(qk_shape s) {
     const int ch = s.H / 32;
-    return ch >= 64 && ch <= 256 && (ch & (ch - 1)) == 0 && s.E <= 64 * 16 && s.k <= QK_MAX_TOPK;
+    return ch >= 64 && ch <= 256 && (ch & (ch - 1)) == 0 && s.E <= 64 * 16 && s.k <= QK_MAX_TOPK &&
+           !s.g32;
 }
 
 extern "C" int qk_launch_gateup_topk(const qmoe_layer_weights *W, qk_shape s, const void *x,
@@ -444,6 +447,7 @@ extern "C" int qk_launch_down_combine(const qmoe_layer_weights *W, qk_shape s, c
     a.hyper = hyper;
     a.inject = inject;
     a.hc = hc;
+    a.gsh = s.g32 ? 0 : 1;
     a.K = s.I;
     a.N = s.H;
     a.n = n;
@@ -483,7 +487,7 @@ static int pick_lpr(int K) {
 template <bool XBF16>
 static int launch_gateup_dec(const GemvArgs &g, hipStream_t st) {
     const int ch = g.K / 32;
-    if (ch < 2 || ch > 256 || (ch & (ch - 1)) != 0) return -1;
+    if (ch < 2 || ch > 256 || (ch & (ch - 1)) != 0 || g.gsh != 1) return -1; /* groups of 64 only */
     DecArgs a;
     for (int mt = 0; mt < 2; mt++) {
         a.q[mt] = g.q[mt]; a.s[mt] = g.s[mt]; a.b[mt] = g.b[mt];
@@ -562,6 +566,7 @@ extern "C" int qk_launch_gateup(const qmoe_layer_weights *W, qk_shape s, const v
     a.max_m = max_m;
     a.seglist = seglist;
     a.in_by_pos = 0;
+    a.gsh = s.g32 ? 0 : 1;
     const int max_seg = n * s.k < s.E ? n * s.k : s.E;
     hipStream_t st = (hipStream_t)stream;
     if (n == 1) {
@@ -594,6 +599,7 @@ extern "C" int qk_launch_down(const qmoe_layer_weights *W, qk_shape s, const flo
     a.max_m = max_m;
     a.seglist = seglist;
     a.in_by_pos = 1;
+    a.gsh = s.g32 ? 0 : 1;
     const int max_seg = n * s.k < s.E ? n * s.k : s.E;
     return launch_gemv<1, false>(a, max_seg, (hipStream_t)stream);
 }

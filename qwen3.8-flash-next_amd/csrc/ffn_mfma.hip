@@ -701,12 +701,12 @@ extern "C" int32_t *qk_mfma_small_list(qk_shape s, int n, int32_t *tasks) {
  * tables of scales and group sums). */
 extern "C" int qk_mfma_gateup_ok(qk_shape s, int x_bf16) {
     const int G = s.H / 64;
-    return s.H % 512 == 0 && s.I % 128 == 0 && G <= MM_MAXG;
+    return s.H % 512 == 0 && s.I % 128 == 0 && G <= MM_MAXG && !s.g32;
 }
 
 extern "C" int qk_mfma_down_ok(qk_shape s) {
     const int G = s.I / 64;
-    return s.I % 512 == 0 && s.H % 256 == 0 && G <= MM_MAXG;
+    return s.I % 512 == 0 && s.H % 256 == 0 && G <= MM_MAXG && !s.g32;
 }
 
 extern "C" int qk_launch_mfma_tasks(qk_shape s, int n, const int32_t *segtab, int min_m,

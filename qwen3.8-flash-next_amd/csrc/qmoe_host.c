@@ -132,8 +132,9 @@ static int check_config(const qmoe_config *c, qmoe_err *err) {
         set_err(err, "config is NULL");
         return -1;
     }
-    if (c->group_size != QK_GROUP) {
-        set_err(err, "group_size %d unsupported (this build needs %d)", c->group_size, QK_GROUP);
+    if (c->group_size != QK_GROUP && c->group_size != 32) {
+        set_err(err, "group_size %d unsupported (this build takes %d, or 32 on the GEMV kernels)",
+                c->group_size, QK_GROUP);
         return -1;
     }
     if (c->hidden <= 0 || c->hidden % QK_GROUP || c->hidden > 8192) {
@@ -226,6 +227,7 @@ int qmoe_create(qmoe_ctx **out, const qmoe_config *cfg, qmoe_err *err) {
     c->shape.k = cfg->top_k;
     c->shape.I = cfg->moe_inter;
     c->shape.eps = cfg->rms_eps;
+    c->shape.g32 = cfg->group_size == 32;
     if (hip_fail(err, (int)hipGetDevice(&c->device), "hipGetDevice")) {
         free(c);
         return -1;
@@ -1116,7 +1118,8 @@ int qmoe_layer_forward_noalloc(const qmoe_config *cfg, const qmoe_layer_weights 
     if (n == 0) return 0;
     NEED(x, "x");
     NEED(out, "out");
-    const qk_shape s = {cfg->hidden, cfg->n_experts, cfg->top_k, cfg->moe_inter, cfg->rms_eps};
+    const qk_shape s = {cfg->hidden, cfg->n_experts, cfg->top_k, cfg->moe_inter, cfg->rms_eps,
+                        cfg->group_size == 32};
     size_t offs[QH_SC_COUNT];
     const size_t bytes = scratch_plan(s, (size_t)n, offs);
     if (bytes > QK_NOALLOC_SCRATCH_BYTES) {

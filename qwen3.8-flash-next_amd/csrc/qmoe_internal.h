@@ -27,6 +27,7 @@ extern "C" {
 typedef struct {
     int H, E, k, I;
     float eps;
+    int g32; /* 1: the experts' q4 groups are 32 columns (GEMV kernels only), 0: 64 */
 } qk_shape;
 
 /* device scratch carved out of one allocation by the host */

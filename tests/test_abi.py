@@ -61,7 +61,7 @@ def test_null_and_bad_arguments_return_errors():
         assert rc == -1 and b"ctx is NULL" in err.msg
     # config validation happens before any device call
     h = ctypes.c_void_p()
-    for bad, msg in (((256, 8, 2, 128, 32, 1, 4, 1e-6), b"group_size"),
+    for bad, msg in (((256, 8, 2, 128, 128, 1, 4, 1e-6), b"group_size"),
                      ((250, 8, 2, 128, 64, 1, 4, 1e-6), b"hidden"),
                      ((256, 8, 9, 128, 64, 1, 4, 1e-6), b"top_k"),
                      ((256, 2000, 2, 128, 64, 1, 4, 1e-6), b"n_experts"),

@@ -650,6 +650,55 @@ def test_shape_sweep(torch_dev, H, E, k, I, n, x_bf16, norm):
         assert_out_close(out.cpu().numpy(), ref["out"], "sweep")
 
 
+# (H, E, k, I, n, x_bf16, norm, layers): q4 groups of 32 columns (the
+# reference's integration model), on every GEMV path: the one-token layer,
+# the fused down + combine (n <= 8), the grouped GEMV for every segment
+# (no MFMA stage takes groups of 32), the tiled and the MFMA router; and a
+# residual chain of layers with the pre-router norm
+G32 = [
+    (2048, 64, 4, 512, 1, True, False, 1),
+    (2048, 64, 4, 512, 5, False, True, 1),
+    (1024, 48, 6, 256, 37, True, False, 1),
+    (2048, 128, 8, 512, 300, False, False, 1),
+    (768, 40, 3, 320, 64, True, True, 1),
+    (1024, 32, 4, 256, 1, False, True, 4),
+]
+
+
+@pytest.mark.parametrize("H,E,k,I,n,x_bf16,norm,layers", G32)
+def test_group_size_32(torch_dev, H, E, k, I, n, x_bf16, norm, layers):
+    """expert weights quantised in groups of 32 columns (w = q*s + b per 32
+    columns, model.c:646-651 with the checkpoint's group_size): the
+    oracle's routing on every token and every output row within 2e-2 /
+    1e-3; with several layers, the residual chain layer by layer"""
+    torch, dev = torch_dev
+    pkg = load_pkg()
+    say(f"case: group 32 H={H} E={E} k={k} I={I} n={n} x_bf16={x_bf16} norm={norm} layers={layers}")
+    Ls = [orc.Layer(H, E, k, I, seed=H + E + n + l, layer=l, with_norm=norm, group_size=32)
+          for l in range(layers)]
+    x = orc.gen_x(n, H, 41 + n, bf16=x_bf16)
+    with pkg.MoeContext(H, E, k, I, n_layers=layers, max_tokens=n, group_size=32) as ctx:
+        for l, L in enumerate(Ls):
+            ctx.upload_layer(l, L.arrays())
+        if layers == 1:
+            ref = Ls[0].forward(x, x_bf16)
+            out = ctx.layer_forward(0, to_dev(x, torch, dev))
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(ctx.last_routing(n)["idx"].cpu().numpy(), ref["idx"])
+            assert_out_close(out.cpu().numpy(), ref["out"], "group 32")
+            return
+        hn = np.asarray(x, np.float32)  # the chain's cases feed f32 rows
+        h = to_dev(hn, torch, dev)
+        for l, L in enumerate(Ls):
+            ref = L.forward(hn, False, residual=True)
+            h = ctx.layer_forward(l, h, residual=True)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(ctx.last_routing(n)["idx"].cpu().numpy(), ref["idx"])
+            got = h.cpu().numpy()
+            assert_out_close(got, ref["out"], f"group 32 layer {l}")
+            hn = got
+
+
 def test_empty_and_errors(torch_dev):
     torch, dev = torch_dev
     pkg = load_pkg()
@@ -670,7 +719,8 @@ def test_empty_and_errors(torch_dev):
             ctx.layer_forward(1, x5[:1])
         with pytest.raises(pkg.QmoeError, match="no norm"):
             ctx.router_norm(0, x5[:1])
-    with pytest.raises(pkg.QmoeError, match="group_size"):
-        pkg.MoeContext(256, 8, 2, 128, group_size=32)
+    for gs in (16, 128):
+        with pytest.raises(pkg.QmoeError, match="group_size"):
+            pkg.MoeContext(256, 8, 2, 128, group_size=gs)
     with pytest.raises(pkg.QmoeError, match="top_k"):
         pkg.MoeContext(256, 8, 9, 128)
