@@ -1,7 +1,6 @@
 /*
  * router_rows.h -- one router row (one wavefront) for a block of tokens,
- * shared by the router kernels (router.hip) and the one-token layer's
- * front launch (decode_layer.hip).
+ * shared by the router kernels (router.hip, route_mfma.hip).
  *
  * Router reduction order ("R64", bit-exact with the oracle): for one
  * (token, expert) dot product the K axis is cut into 8-element chunks, chunk
