@@ -43,32 +43,19 @@ struct HcDownArgs {
     float eps;
 };
 
-#define HD_RW 2 /* weight rows per workgroup */
+#define HD_RW 2 /* down-matrix rows per workgroup */
 
-/*
- * Workgroup = hc waves; wave h owns copy h (columns h*d .. h*d+d) of the
- * hyper state, P chunks of 32 columns per lane, so the copy's RMSNorm is a
- * wave sum and needs no other wave: normed = (x * r) * w with
- * r = 1/sqrt(ss/d + eps) (kernel_rmsnorm_grouped, kernel.c:22-36).  A task
- * is (block of tb tokens, block of HD_RW rows) of either the down matrix
- * (q4) or the inject matrix (bf16; no inject blocks when inject_w is NULL); per token each wave leaves its copy's
- * partial row sums in LDS (double-buffered by token parity) and the first
- * threads add the copies in order and apply the activation: silu(v / hc)
- * for down rows (kernel_scale + kernel_silu, model.c:757-758), 2 *
- * sigmoid(v / hc) for inject rows (model.c:790-792).
- */
-template <int P>
-__global__ __launch_bounds__(64 * HC_MAX) void k_hc_down(HcDownArgs a) {
+/* one task of k_hc_down: INJ = one row of the inject matrix, else HD_RW
+ * rows of the down matrix */
+template <int P, bool INJ>
+__device__ __forceinline__ void hc_down_body(const HcDownArgs &a, int tblk, int rb, int nrb) {
+    constexpr int RW = INJ ? 1 : HD_RW; /* rows of this task */
     __shared__ float s_part[2][HC_MAX][HD_RW];
     const int lane = threadIdx.x & 63, h = threadIdx.x >> 6;
     const int D = a.hc * a.d, CPC = a.d >> 5, G = D >> 6;
     const size_t wrow = (size_t)D >> 3;
-    const int nrb = (a.R + HD_RW - 1) / HD_RW;
-    const int nblk = nrb + (a.inject_w ? (a.hc + HD_RW - 1) / HD_RW : 0);
-    const int tblk = blockIdx.x / nblk, rb = blockIdx.x - tblk * nblk;
-    const bool inj = rb >= nrb;
-    const int r0 = inj ? (rb - nrb) * HD_RW : rb * HD_RW;
-    const int nrows = inj ? a.hc : a.R;
+    const int r0 = INJ ? rb - nrb : rb * HD_RW;
+    const int nrows = INJ ? a.hc : a.R;
     const int t0 = tblk * a.tb, m = min(a.tb, a.n - t0);
     if (m <= 0) return;
     const float inv_hc = 1.0f / (float)a.hc;
@@ -82,29 +69,28 @@ __global__ __launch_bounds__(64 * HC_MAX) void k_hc_down(HcDownArgs a) {
         cok[ps] = cc < CPC;
         gc[ps] = h * CPC + (cok[ps] ? cc : 0);
     }
-    /* weights: q4 rows (codes, scale, bias) or bf16 rows (32 weights a chunk) */
-    uint4 wq[HD_RW][P];
-    float ws[HD_RW][P], wb[HD_RW][P];
-    uint4 wi[HD_RW][P][4];
-#pragma unroll
-    for (int it = 0; it < HD_RW; it++) {
-        const int r = min(r0 + it, nrows - 1);
+    /* weights: q4 rows (codes, scale, bias) or one bf16 row (32 weights a chunk) */
+    uint4 wq[RW][P];
+    float ws[RW][P], wb[RW][P];
+    uint4 wi[P][4];
+    if (INJ) {
 #pragma unroll
         for (int ps = 0; ps < P; ps++) {
-            const bool ok = cok[ps] && r0 + it < nrows;
-            if (inj) {
-                const uint4 *src = (const uint4 *)(a.inject_w + (size_t)r * D) + 4 * gc[ps];
+            const uint4 *src = (const uint4 *)(a.inject_w + (size_t)r0 * D) + 4 * gc[ps];
 #pragma unroll
-                for (int v = 0; v < 4; v++) wi[it][ps][v] = ok ? qk_ld(src + v) : make_uint4(0u, 0u, 0u, 0u);
-                wq[it][ps] = make_uint4(0u, 0u, 0u, 0u);
-                ws[it][ps] = wb[it][ps] = 0.0f;
-            } else {
+            for (int v = 0; v < 4; v++) wi[ps][v] = cok[ps] ? qk_ld(src + v) : make_uint4(0u, 0u, 0u, 0u);
+        }
+    } else {
+#pragma unroll
+        for (int it = 0; it < RW; it++) {
+            const int r = min(r0 + it, nrows - 1);
+#pragma unroll
+            for (int ps = 0; ps < P; ps++) {
+                const bool ok = cok[ps] && r0 + it < nrows;
                 wq[it][ps] = ok ? qk_ld((const uint4 *)(a.q + (size_t)r * wrow) + gc[ps])
                                 : make_uint4(0u, 0u, 0u, 0u);
                 ws[it][ps] = ok ? qk_bf16(qk_ld(a.s + (size_t)r * G + (gc[ps] >> 1))) : 0.0f;
                 wb[it][ps] = ok ? qk_bf16(qk_ld(a.b + (size_t)r * G + (gc[ps] >> 1))) : 0.0f;
-#pragma unroll
-                for (int v = 0; v < 4; v++) wi[it][ps][v] = make_uint4(0u, 0u, 0u, 0u);
             }
         }
     }
@@ -114,7 +100,7 @@ __global__ __launch_bounds__(64 * HC_MAX) void k_hc_down(HcDownArgs a) {
 #pragma unroll
         for (int v = 0; v < 8; v++)
             wn[ps][v] = qk_ld((const float4 *)(a.norm_w + (size_t)gc[ps] * 32) + v);
-    const bool store_normed = rb == 0;
+    const bool store_normed = !INJ && rb == 0;
 
     float4 xr[P][8];
     auto load_x = [&](int t) {
@@ -170,16 +156,16 @@ __global__ __launch_bounds__(64 * HC_MAX) void k_hc_down(HcDownArgs a) {
                 qk_f32x8_to_pairs(&xv[ps][8 * w], &xp.hi[ps][4 * w], &xp.lo[ps][4 * w], xp.xs[ps]);
         }
 #pragma unroll
-        for (int it = 0; it < HD_RW; it++) {
+        for (int it = 0; it < RW; it++) {
             float part;
-            if (inj) {
+            if (INJ) {
                 part = 0.0f;
 #pragma unroll
                 for (int ps = 0; ps < P; ps++)
 #pragma unroll
                     for (int v = 0; v < 4; v++) {
                         uint32_t pr[4];
-                        qk_bf16x8_to_pairs(wi[it][ps][v], pr);
+                        qk_bf16x8_to_pairs(wi[ps][v], pr);
 #pragma unroll
                         for (int i = 0; i < 4; i++) {
                             part = qk_dot2(xp.hi[ps][4 * v + i], pr[i], part);
@@ -193,14 +179,37 @@ __global__ __launch_bounds__(64 * HC_MAX) void k_hc_down(HcDownArgs a) {
             if (lane == 0) s_part[j & 1][h][it] = v;
         }
         __syncthreads();
-        if ((int)threadIdx.x < HD_RW && r0 + (int)threadIdx.x < nrows) {
+        if ((int)threadIdx.x < RW && r0 + (int)threadIdx.x < nrows) {
             const int it = threadIdx.x;
             float acc = 0.0f;
             for (int hh = 0; hh < a.hc; hh++) acc += s_part[j & 1][hh][it];
-            if (inj) a.inject[(size_t)t * a.hc + r0 + it] = 2.0f * qk_sigmoid(acc * inv_hc);
+            if (INJ) a.inject[(size_t)t * a.hc + r0 + it] = 2.0f * qk_sigmoid(acc * inv_hc);
             else a.w[(size_t)t * a.R + r0 + it] = qk_silu(acc * inv_hc);
         }
     }
+}
+
+/*
+ * Workgroup = hc waves; wave h owns copy h (columns h*d .. h*d+d) of the
+ * hyper state, P chunks of 32 columns per lane, so the copy's RMSNorm is a
+ * wave sum and needs no other wave: normed = (x * r) * w with
+ * r = 1/sqrt(ss/d + eps) (kernel_rmsnorm_grouped, kernel.c:22-36).  A task
+ * is (block of tb tokens, block of HD_RW rows of the down matrix (q4) or
+ * one row of the inject matrix (bf16; no inject tasks when inject_w is
+ * NULL)); per token each wave leaves its copy's partial row sums in LDS
+ * (double-buffered by token parity) and the first threads add the copies
+ * in order and apply the activation: silu(v / hc) for down rows
+ * (kernel_scale + kernel_silu, model.c:757-758), 2 * sigmoid(v / hc) for
+ * inject rows (model.c:790-792).  The two task kinds are separate bodies,
+ * so neither carries the other's weight registers.
+ */
+template <int P>
+__global__ __launch_bounds__(64 * HC_MAX) void k_hc_down(HcDownArgs a) {
+    const int nrb = (a.R + HD_RW - 1) / HD_RW;
+    const int nblk = nrb + (a.inject_w ? a.hc : 0);
+    const int tblk = blockIdx.x / nblk, rb = blockIdx.x - tblk * nblk;
+    if (rb >= nrb) hc_down_body<P, true>(a, tblk, rb, nrb);
+    else hc_down_body<P, false>(a, tblk, rb, nrb);
 }
 
 /* ------------------------------------------------------- up + mean mix */
@@ -215,7 +224,7 @@ struct HcUpArgs {
     int hc, d, R, n, tb;
 };
 
-#define HU_RIT 4
+#define HU_RIT 2 /* row steps per wave: 2 * 64/LPR columns per workgroup */
 
 /*
  * Workgroup = hc waves (wave h computes rows h*d + i of the up projection)
@@ -352,7 +361,7 @@ extern "C" int qk_launch_hc_down(const float *hyper, const float *norm_w, const 
     if (!qk_hc_shape_ok(hc, d, R)) return (int)hipErrorInvalidValue;
     if (inject_w && !inject) return (int)hipErrorInvalidValue;
     /* no inject matrix (the final mixer): the down row blocks alone */
-    const int nblk = (R + HD_RW - 1) / HD_RW + (inject_w ? (hc + HD_RW - 1) / HD_RW : 0);
+    const int nblk = (R + HD_RW - 1) / HD_RW + (inject_w ? hc : 0);
     const int tb = hc_tokens_per_task(n, nblk);
     HcDownArgs a{hyper, norm_w, q, s, b, inject_w, normed, w, inject, hc, d, R, n, tb, eps};
     const dim3 grid((unsigned)(((n + tb - 1) / tb) * nblk)), blk(64 * hc);
