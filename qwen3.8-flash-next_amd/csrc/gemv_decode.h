@@ -94,23 +94,52 @@ __global__ __launch_bounds__(256) void k_gateup_dec(DecArgs a, const int32_t *__
     const int c0 = sub * CPL;     /* first chunk of this lane */
     const int g0 = (c0 >> 1);     /* first scale group of this lane */
 
-    /* activations: no routing dependence, issued first */
-    uint4 xd[XBF16 ? CPL : 1][4];
-    float4 xf[XBF16 ? 1 : CPL][8];
+    /* Activations, staged once per workgroup: the K/8 groups of 8 values
+     * are loaded in address order (a wave's load covers one contiguous
+     * run), converted to (x_i, x_{i+4}) bf16 pairs (f32: hi and lo pairs and
+     * the group sum) and left in LDS for every lane's chunk.  In routed
+     * workgroups of the fused top-k, wave 0 stages nothing, so its logit
+     * loads are not queued behind activation loads. */
+    constexpr int NG = 4 * LPR * CPL;            /* groups of 8 activations */
+    constexpr int NSTG = (NG + 191) / 192;       /* groups per staging thread, at most */
+    __shared__ uint4 s_xh[NG];
+    __shared__ uint4 s_xl[XBF16 ? 1 : NG];
+    __shared__ float s_xg[XBF16 ? 1 : NG];
+    const bool shared = seg == 0;
+    const int st0 = (TK > 0 && !shared) ? 64 : 0; /* first staging thread */
+    const int sts = 256 - st0;
+    uint4 xd[XBF16 ? NSTG : 1];
+    float4 xf[XBF16 ? 1 : NSTG][2];
 #pragma unroll
-    for (int c = 0; c < CPL; c++) {
-        if (XBF16) {
-            const uint4 *src = (const uint4 *)((const uint16_t *)a.x) + 4 * (c0 + c);
-#pragma unroll
-            for (int w = 0; w < 4; w++) xd[XBF16 ? c : 0][w] = qk_ld(src + w);
-        } else {
-            const float4 *src = (const float4 *)((const float *)a.x) + 8 * (c0 + c);
-#pragma unroll
-            for (int w = 0; w < 8; w++) xf[XBF16 ? 0 : c][w] = qk_ld(src + w);
+    for (int j = 0; j < NSTG; j++) {
+        const int gi = min(max((int)threadIdx.x - st0, 0) + j * sts, NG - 1);
+        if (XBF16) xd[XBF16 ? j : 0] = qk_ld((const uint4 *)a.x + gi);
+        else {
+            xf[XBF16 ? 0 : j][0] = qk_ld((const float4 *)a.x + 2 * gi);
+            xf[XBF16 ? 0 : j][1] = qk_ld((const float4 *)a.x + 2 * gi + 1);
         }
     }
+    /* groups -> LDS slots, XOR-swizzled within runs of four */
+    auto xslot = [](int gi) { return gi ^ ((gi >> 2) & 3); };
+    auto stage_x = [&]() {
+#pragma unroll
+        for (int j = 0; j < NSTG; j++) {
+            const int gi = (int)threadIdx.x - st0 + j * sts;
+            if ((int)threadIdx.x < st0 || gi >= NG) continue;
+            uint32_t hp4[4];
+            if (XBF16) {
+                qk_bf16x8_to_pairs(xd[XBF16 ? j : 0], hp4);
+            } else {
+                const float4 a0 = xf[XBF16 ? 0 : j][0], a1 = xf[XBF16 ? 0 : j][1];
+                const float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+                uint32_t lp4[4];
+                s_xg[XBF16 ? 0 : gi] = qk_f32x8_pairs(v, hp4, lp4);
+                s_xl[XBF16 ? 0 : xslot(gi)] = make_uint4(lp4[0], lp4[1], lp4[2], lp4[3]);
+            }
+            s_xh[xslot(gi)] = make_uint4(hp4[0], hp4[1], hp4[2], hp4[3]);
+        }
+    };
 
-    const bool shared = seg == 0;
     const int slot = seg - 1;
     bool valid;
     int e, p0;
@@ -120,6 +149,7 @@ __global__ __launch_bounds__(256) void k_gateup_dec(DecArgs a, const int32_t *__
     int my_id = 0x7FFFFFFF;
     if (TK > 0) {
         if (!shared) {
+            if (wave != 0) stage_x();
             if (wave == 0) {
                 tks.init(ro.logits, a.E, lane);
                 /* two slots a round, up to the round that yields this slot */
@@ -141,6 +171,8 @@ __global__ __launch_bounds__(256) void k_gateup_dec(DecArgs a, const int32_t *__
                 if (lane == 0) s_ep[0] = es;
             }
             __syncthreads();
+        } else {
+            stage_x(); /* read after the barrier below, under the weight loads */
         }
         valid = true;
         e = shared ? 0 : s_ep[0];
@@ -150,6 +182,7 @@ __global__ __launch_bounds__(256) void k_gateup_dec(DecArgs a, const int32_t *__
         const int s1 = shared ? 1 : seg;
         const int u = segtab[0];
         const int e_raw = segtab[3 * s1 - 2], p_raw = segtab[3 * s1 - 1], m_raw = segtab[3 * s1];
+        stage_x();
         valid = shared | ((seg <= u) & (e_raw >= 0) & (e_raw < a.E) & (p_raw >= 0) & (p_raw < a.k) &
                           (m_raw == 1));
         e = (valid && !shared) ? e_raw : 0;
@@ -207,31 +240,40 @@ __global__ __launch_bounds__(256) void k_gateup_dec(DecArgs a, const int32_t *__
                 }
             }
         }
-        __syncthreads();
+        qk_lds_barrier(); /* s_ep[1]; the weight loads stay in flight */
         p0 = s_ep[1];
     }
 
-    /* activation pairs (x_i, x_{i+4}) per 8 columns, and chunk sums */
+    if (!(TK > 0 && !shared)) qk_lds_barrier(); /* the staged groups; weight loads stay in flight */
+
+    /* this lane's chunks from the staged groups: pairs (x_i, x_{i+4}) per 8
+     * columns and the chunk sums (bf16: v_dot2 chain over the 16 pairs from
+     * 0; f32: 0 + g0 + g1 + g2 + g3 over the four group sums, left to right) */
     uint32_t hp[CPL][16];
     uint32_t lp[XBF16 ? 1 : CPL][XBF16 ? 1 : 16];
     float xs[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; c++) {
-        if (XBF16) {
 #pragma unroll
-            for (int w = 0; w < 4; w++) qk_bf16x8_to_pairs(xd[XBF16 ? c : 0][w], &hp[c][4 * w]);
+        for (int w = 0; w < 4; w++) {
+            const int gi = 4 * (c0 + c) + w;
+            const uint4 h4 = s_xh[xslot(gi)];
+            hp[c][4 * w] = h4.x; hp[c][4 * w + 1] = h4.y; hp[c][4 * w + 2] = h4.z; hp[c][4 * w + 3] = h4.w;
+            if (!XBF16) {
+                const uint4 l4 = s_xl[XBF16 ? 0 : xslot(gi)];
+                uint32_t *l = lp[XBF16 ? 0 : c];
+                l[XBF16 ? 0 : 4 * w] = l4.x; l[XBF16 ? 0 : 4 * w + 1] = l4.y;
+                l[XBF16 ? 0 : 4 * w + 2] = l4.z; l[XBF16 ? 0 : 4 * w + 3] = l4.w;
+            }
+        }
+        if (XBF16) {
             float s = 0.0f;
 #pragma unroll
             for (int i = 0; i < 16; i++) s = qk_dot2(hp[c][i], QK_BF16_ONES, s);
             xs[c] = s;
         } else {
-            xs[c] = 0.0f;
-#pragma unroll
-            for (int w = 0; w < 4; w++) {
-                const float4 a0 = xf[XBF16 ? 0 : c][2 * w], a1 = xf[XBF16 ? 0 : c][2 * w + 1];
-                const float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-                qk_f32x8_to_pairs(v, &hp[c][4 * w], &lp[XBF16 ? 0 : c][XBF16 ? 0 : 4 * w], xs[c]);
-            }
+            const float4 g4 = *(const float4 *)&s_xg[XBF16 ? 0 : 4 * (c0 + c)];
+            xs[c] = (((0.0f + g4.x) + g4.y) + g4.z) + g4.w;
         }
     }
 

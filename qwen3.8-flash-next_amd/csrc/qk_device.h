@@ -142,6 +142,15 @@ __device__ __forceinline__ void qk_f32x8_to_pairs(const float x[8], uint32_t hi[
     xsum = xsum + qk_f32x8_pairs(x, hi, lo);
 }
 
+/* workgroup barrier that orders LDS only: the fences are limited to the
+ * local address space, so global loads in flight are not waited for (a
+ * plain __syncthreads waits for every outstanding load first) */
+__device__ __forceinline__ void qk_lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ float qk_silu(float v) { return v / (1.0f + expf(-v)); }
 __device__ __forceinline__ float qk_sigmoid(float v) { return 1.0f / (1.0f + expf(-v)); }
 /* silu with the hardware exp2 and reciprocal (a few ulp): for epilogues
