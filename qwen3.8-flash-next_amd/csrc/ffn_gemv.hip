@@ -229,8 +229,11 @@ __global__ __launch_bounds__(64 * DC_WAVES) void k_down_combine(DcArgs a,
     const int r0 = blockIdx.x * RB;
     const int u_raw = segtab[0];
 
-    /* each token's slots ranked by dispatch position (invalid last) */
-    for (int t = wave; t < a.n; t += DC_WAVES) {
+    /* each token's slots ranked by dispatch position (invalid last), by the
+     * waves counted from the last: the first waves start their segments'
+     * loads at once (wave 0 holds the shared expert, which needs no table),
+     * and with k + 1 < DC_WAVES segments the last waves have none */
+    for (int t = DC_WAVES - 1 - wave; t < a.n; t += DC_WAVES) {
         int p = 0x7FFFFFFF;
         float wt = 0.0f;
         if (lane < a.k) {
