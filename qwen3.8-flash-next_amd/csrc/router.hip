@@ -137,8 +137,12 @@ __global__ __launch_bounds__(256, 2) void k_router_tile(RouterArgs a, int rows_p
     store_rows(0);
     if (r0 + RTT_EB < r1) load_rows(r0 + RTT_EB);
     __syncthreads();
+    const int rs_d = qk_rs16_index(lane); /* this lane's (token, row) after the reduction */
     for (int rb = r0, it = 0; rb < r1; rb += RTT_EB, it++) {
         const int buf = it & 1;
+        /* the bias of this lane's row, loaded before the sums: loaded at the
+         * store, the barrier that ends the stage would wait for it */
+        const float bv = a.router_bias ? qk_ld(a.router_bias + min(rb + rs_d % RTT_EB, a.E - 1)) : 0.0f;
         /* partial sums of this lane, d = t*RTT_EB + rr */
         float part[RTT_TOK * RTT_EB];
 #pragma unroll
@@ -163,11 +167,11 @@ __global__ __launch_bounds__(256, 2) void k_router_tile(RouterArgs a, int rows_p
         /* the 16 wave sums, each in the R64 tree's pairing, spread over lanes */
         const float val = qk_reduce_scatter16(part, lane);
         {
-            const int d = qk_rs16_index(lane);
+            const int d = rs_d;
             const int t = d / RTT_EB, row = rb + d % RTT_EB;
             if (lane < 16 && row < r1 && tb + t < a.n) {
                 float o = val;
-                if (row < a.E && a.router_bias) o = o + a.router_bias[row];
+                if (row < a.E && a.router_bias) o = o + bv;
                 a.logits[(size_t)(tb + t) * (a.E + 1) + row] = o;
             }
         }
@@ -231,6 +235,10 @@ __global__ __launch_bounds__(256) void k_router_one(RouterArgs a) {
     const int chunks = a.H >> 3;
     const uint16_t *wrow = row < a.E ? a.router_w + (size_t)row * a.H : a.sh_gate_w;
     __shared__ float s_g[2][4];
+    /* the bias, loaded now: after the last barrier it would cost a load
+     * round trip of its own */
+    const bool has_bias = row < a.E && a.router_bias;
+    const float bias = (threadIdx.x == 0 && has_bias) ? qk_ld(a.router_bias + row) : 0.0f;
     uint4 wv[NCH];
     bool cv[NCH];
     int cc[NCH];
@@ -292,7 +300,7 @@ __global__ __launch_bounds__(256) void k_router_one(RouterArgs a) {
     __syncthreads();
     if (threadIdx.x == 0) {
         float l = (s_g[1][0] + s_g[1][1]) + (s_g[1][2] + s_g[1][3]);
-        if (row < a.E && a.router_bias) l = l + a.router_bias[row];
+        if (has_bias) l = l + bias;
         a.logits[row] = l;
     }
 }
