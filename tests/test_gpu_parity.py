@@ -628,6 +628,11 @@ SWEEP = [
     (2048, 40, 3, 192, 17, True, True),
     (2048, 1024, 16, 128, 64, True, False),
     (1280, 130, 5, 640, 90, False, False),
+    # one token on the fused top-k + gate/up launch with 2 and 4 chunks per
+    # lane (activations staged per workgroup in 3 and 6 passes)
+    (4096, 64, 2, 256, 1, True, False),
+    (8192, 32, 2, 128, 1, True, False),
+    (8192, 32, 3, 128, 1, False, True),
 ]
 
 
