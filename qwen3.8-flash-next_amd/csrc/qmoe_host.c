@@ -747,7 +747,7 @@ int qmoe_router(qmoe_ctx *c, int layer, const void *x, int x_dtype, int n, float
         return hip_fail(err,
                         qk_launch_route_mfma(W, c->shape, x, x_dtype == QMOE_BF16, n, c->sc.logits, xn,
                                              c->sc.ahi, c->sc.ag, idx_out, w_out, shared_gate_out,
-                                             stream),
+                                             NULL, NULL, NULL, NULL, stream),
                         "router");
     if (hip_fail(err, qk_launch_router(W, c->shape, x, x_dtype == QMOE_BF16, n, c->sc.logits, xn,
                                        stream),
@@ -898,7 +898,7 @@ int qmoe_dispatch(qmoe_ctx *c, const int32_t *idx, int n, int32_t *offsets_out, 
     NEED(idx, "idx");
     NEED(perm_out, "perm_out");
     return hip_fail(err, qk_launch_dispatch(c->shape, n, idx, offsets_out, perm_out, c->sc.pos,
-                                            segments_out, c->sc.bits, c->sc.wprefix, 0,
+                                            segments_out, c->sc.bits, 0, c->sc.wprefix, 0,
                                             NULL, stream),
                     "dispatch");
 }
@@ -1026,9 +1026,15 @@ static int layer_core(const stage_env *e, const qmoe_layer_weights *W, int hc,
      * writes the gate/up's operand planes (no packing launch) */
     const int rfast = qk_route_mfma_ok(s, n);
     const int rpack = !rfast && n >= 2 && mfma_usable(s, n, xf_bf ? 0 : 1) && qk_router_packs(s, n);
+    /* the MFMA router's last launch also writes the gate/up's operand planes
+     * when the gate/up runs on MFMA, and the dispatch's token bitmask (its
+     * n >= QK_ROUTE_MFMA_MIN_N always takes qk_launch_dispatch below); its
+     * wn2 scratch then goes to h, which the gate/up writes later */
+    const int rmm = rfast && mfma_usable(s, n, xf_bf ? 0 : 1);
     if (rfast)
-        rc = qk_launch_route_mfma(W, s, x, xbf, n, sc->logits, xn, sc->ahi, sc->ag, sc->idx, sc->w,
-                                  sc->sg, stream);
+        rc = qk_launch_route_mfma(W, s, x, xbf, n, sc->logits, xn, sc->ahi, rmm ? sc->h : sc->ag, sc->idx,
+                                  sc->w, sc->sg, sc->bits, rmm ? sc->ahi : NULL,
+                                  rmm && !xf_bf ? sc->alo : NULL, rmm ? sc->ag : NULL, stream);
     else if (rpack)
         rc = qk_launch_router_pack(W, s, x, xbf, n, sc->logits, xn, sc->ahi, xf_bf ? NULL : sc->alo,
                                    sc->ag, stream);
@@ -1060,10 +1066,10 @@ static int layer_core(const stage_env *e, const qmoe_layer_weights *W, int hc,
             if (hip_fail(err, rc, "topk")) return -1;
         }
         rc = qk_launch_dispatch(s, n, sc->idx, sc->offsets, sc->perm, sc->pos, sc->segtab,
-                                sc->bits, sc->wprefix, mfma_min_m(n), tasks, stream);
+                                sc->bits, rfast, sc->wprefix, mfma_min_m(n), tasks, stream);
         if (hip_fail(err, rc, "dispatch")) return -1;
     }
-    if (run_gateup(e, W, xf, xf_bf, n, sc->perm, sc->segtab, gu_mm, rpack, sc->h, stream, err))
+    if (run_gateup(e, W, xf, xf_bf, n, sc->perm, sc->segtab, gu_mm, rpack || rmm, sc->h, stream, err))
         return -1;
     if (!mfma_usable(s, n, 2) && qk_down_combine_lds(s, n) > 0) {
         rc = qk_launch_down_combine(W, s, sc->h, n, sc->segtab, sc->pos, sc->w, sc->sg,
@@ -1773,7 +1779,7 @@ static int layer_forward_streamed(qmoe_ctx *c, int layer, const void *x, int xbf
     const int rfast = qk_route_mfma_ok(s, n);
     if (rfast)
         rc = qk_launch_route_mfma(W, s, x, xbf, n, sc->logits, xn, sc->ahi, sc->ag, sc->idx, sc->w,
-                                  sc->sg, stream);
+                                  sc->sg, sc->bits, NULL, NULL, NULL, stream);
     else
         rc = qk_launch_router(W, s, x, xbf, n, sc->logits, xn, stream);
     if (hip_fail(err, rc, "router")) return -1;
@@ -1790,7 +1796,7 @@ static int layer_forward_streamed(qmoe_ctx *c, int layer, const void *x, int xbf
             if (hip_fail(err, rc, "topk")) return -1;
         }
         rc = qk_launch_dispatch(s, n, sc->idx, sc->offsets, sc->perm, sc->pos, sc->segtab, sc->bits,
-                                sc->wprefix, 1, NULL, stream);
+                                rfast, sc->wprefix, 1, NULL, stream);
         if (hip_fail(err, rc, "dispatch")) return -1;
     }
     if (c->s_dev) {

@@ -107,12 +107,18 @@ int qk_launch_router_pack(const qmoe_layer_weights *W, qk_shape s, const void *x
  * the token's top k; the same idx, w, sg (and xn) as qk_launch_router +
  * qk_launch_topk.  logits [n, E+1] is scratch here (no exact logits are
  * left in it); plane [n, H] bf16 and wn2 [E] are scratch.  qk_route_mfma_ok
- * says whether the shape and n are supported. */
+ * says whether the shape and n are supported.  With bits set, the launch
+ * also leaves the dispatch's token bitmask [E][(n+31)/32] as k_fill_u32 +
+ * k_setbits would (qk_launch_dispatch with bits_set then skips both); with
+ * phi set, the grouped GEMM's operand planes of the rows the gate/up reads
+ * (x, or xn with a norm): phi, plo (f32 rows), pg as qk_launch_pack_rows
+ * writes them.  wn2 must not overlap them. */
 #define QK_ROUTE_MFMA_MIN_N 256
 int qk_route_mfma_ok(qk_shape s, int n);
 int qk_launch_route_mfma(const qmoe_layer_weights *W, qk_shape s, const void *x, int x_bf16, int n,
                          float *logits, float *xn, uint16_t *plane, float *wn2, int32_t *idx,
-                         float *w, float *sg, void *stream);
+                         float *w, float *sg, uint32_t *bits, uint16_t *phi, uint16_t *plo, float *pg,
+                         void *stream);
 
 /* top-k + renorm + sigmoid; copies the first E logit columns to logits_out
  * when non-NULL. */
@@ -126,9 +132,10 @@ int qk_launch_topk_dispatch_small(qk_shape s, int n, const float *logits, float 
                                   int32_t *idx, float *w, float *sg, int32_t *offsets,
                                   int32_t *perm, int32_t *pos, int32_t *segtab, int min_m,
                                   int32_t *tasks, void *stream);
-/* dispatch from idx alone (any n); tasks as for qk_launch_topk_dispatch_small */
+/* dispatch from idx alone (any n); tasks as for qk_launch_topk_dispatch_small;
+ * bits_set: the token bitmask in bits is already built (qk_launch_route_mfma) */
 int qk_launch_dispatch(qk_shape s, int n, const int32_t *idx, int32_t *offsets, int32_t *perm,
-                       int32_t *pos, int32_t *segtab, uint32_t *bits, int32_t *wprefix,
+                       int32_t *pos, int32_t *segtab, uint32_t *bits, int bits_set, int32_t *wprefix,
                        int min_m, int32_t *tasks, void *stream);
 /* offsets [E+1] from a segment table */
 int qk_launch_offsets_from_segtab(qk_shape s, const int32_t *segtab, int32_t *offsets,

@@ -23,6 +23,13 @@
  *               canonical top-k and softmax of router.hip's k_topk on the
  *               row that holds those exact logits and -inf elsewhere.
  *
+ * Two jobs of the following launches ride along when the caller asks: the
+ * dispatch's token bitmask (k_rt_mm clears it, k_rt_exact sets the bits of
+ * the token's k experts, as router.hip's k_fill_u32 + k_setbits), and the
+ * grouped GEMM's operand planes of the rows k_rt_exact reads (pair-order
+ * bf16 hi (+ lo for f32 rows) and P = -128 x group sums, k_pack_rows'
+ * arithmetic term for term).
+ *
  * Why the selection is the exact one: l_j >= a_j - eps_j for every j, so
  * the k-th largest exact logit is >= T, and every expert of the exact top
  * k has l_e >= T, hence a_e + eps_e >= T: it is recomputed.  An expert that
@@ -108,6 +115,8 @@ struct RtMmArgs {
     const float *bias;    /* [E] or null */
     float *logits;        /* [n, E+1]: columns 0..E-1 written */
     float *wn2;           /* [E] squared norms of the router rows */
+    uint4 *bits;          /* null, or the dispatch bitmask to clear */
+    int nbits4;           /* its size in uint4 */
     int n, E, tiles, per; /* tiles of 64 tokens x 64 experts; per = ceil(tiles / 8) */
 };
 
@@ -115,8 +124,29 @@ struct RtMmSmem {
     float p[4][64][65]; /* the four K quarters' partial tiles, [row][column] */
 };
 
+/* squared norm of router row e, one wave (lane sums, then the wave's tree) */
+template <int NCH>
+__device__ __forceinline__ float rt_row_norm2(const uint16_t *w, int e, int lane) {
+    constexpr int H = 512 * NCH;
+    uint4 d[NCH];
+#pragma unroll
+    for (int i = 0; i < NCH; i++) d[i] = qk_ld((const uint4 *)(w + (size_t)e * H) + lane + 64 * i);
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+        const uint32_t u[4] = {d[i].x, d[i].y, d[i].z, d[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float lo = qk_bf16_lo(u[j]), hi = qk_bf16_hi(u[j]);
+            ss = fmaf(lo, lo, ss);
+            ss = fmaf(hi, hi, ss);
+        }
+    }
+    return qk_group_sum<64>(ss);
+}
+
 /*
- * Grid: 8 * per tile workgroups, then E/32 norm workgroups.  Tile
+ * Grid: 8 * per tile workgroups.  Tile
  * workgroup L runs on XCD L % 8 and takes tile (L % 8) * per + L / 8, so an
  * XCD holds a contiguous range of tiles (tiles are token-major: a range is
  * a few token blocks against every expert, whose rows stay in its L2).
@@ -124,7 +154,10 @@ struct RtMmSmem {
  * (16 MFMA per K-step), and the quarters are summed through LDS in order.
  * 16x16x32 lane layout: A lane l holds token l%16, B lane l expert l%16,
  * both with K elements [8*(l/16), +8) of the step; D lane l holds expert
- * l%16 of tokens 4*(l/16) + i.
+ * l%16 of tokens 4*(l/16) + i.  After its logits a tile workgroup also
+ * writes the squared norms of ceil(64 / token blocks) of its 64 router rows
+ * (rows its B operand just brought into L2): every row once, with no
+ * workgroups of their own at the end of the grid.
  */
 template <int NCH>
 __global__ __launch_bounds__(256, 2) void k_rt_mm(RtMmArgs a) {
@@ -132,33 +165,8 @@ __global__ __launch_bounds__(256, 2) void k_rt_mm(RtMmArgs a) {
     constexpr int S = H / 128; /* K-steps of 32 per wave */
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int L = blockIdx.x;
-    if (L >= 8 * a.per) {
-        /* squared norms: 32 rows per workgroup, 8 per wave */
-        const int r0 = (L - 8 * a.per) * 32 + wave * 8;
-        uint4 d[8][NCH];
-#pragma unroll
-        for (int q = 0; q < 8; q++)
-#pragma unroll
-            for (int i = 0; i < NCH; i++)
-                d[q][i] = qk_ld((const uint4 *)(a.w + (size_t)min(r0 + q, a.E - 1) * H) + lane + 64 * i);
-#pragma unroll
-        for (int q = 0; q < 8; q++) {
-            float ss = 0.0f;
-#pragma unroll
-            for (int i = 0; i < NCH; i++) {
-                const uint32_t u[4] = {d[q][i].x, d[q][i].y, d[q][i].z, d[q][i].w};
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const float lo = qk_bf16_lo(u[j]), hi = qk_bf16_hi(u[j]);
-                    ss = fmaf(lo, lo, ss);
-                    ss = fmaf(hi, hi, ss);
-                }
-            }
-            ss = qk_group_sum<64>(ss);
-            if (lane == 0 && r0 + q < a.E) a.wn2[r0 + q] = ss;
-        }
-        return;
-    }
+    if (a.bits)
+        for (int i = L * 256 + tid; i < a.nbits4; i += (int)gridDim.x * 256) a.bits[i] = make_uint4(0u, 0u, 0u, 0u);
     const int tl = (L & 7) * a.per + (L >> 3);
     if (tl >= a.tiles) return;
     __shared__ __attribute__((aligned(16))) RtMmSmem sm;
@@ -219,6 +227,12 @@ __global__ __launch_bounds__(256, 2) void k_rt_mm(RtMmArgs a) {
         const float v = ((sm.p[0][row][c] + sm.p[1][row][c]) + sm.p[2][row][c]) + sm.p[3][row][c];
         if (t0 + row < a.n) a.logits[(size_t)(t0 + row) * (a.E + 1) + e0 + c] = a.bias ? v + b : v;
     }
+    /* rows e0 + tt * rpw .. of this expert block, one per wave in turn */
+    const int ntt = a.tiles / net, rpw = (64 + ntt - 1) / ntt;
+    for (int j = wave; j < rpw && tt * rpw + j < 64; j += 4) {
+        const float ss = rt_row_norm2<NCH>(a.w, e0 + tt * rpw + j, lane);
+        if (lane == 0) a.wn2[e0 + tt * rpw + j] = ss;
+    }
 }
 
 /* ------------------------------------------------------------ exact top-k */
@@ -233,7 +247,10 @@ struct RtExactArgs {
     int32_t *idx;
     float *wt;
     float *sg;
-    int n, E, k;
+    uint32_t *bits;         /* null, or the dispatch bitmask [E][NW] (cleared by k_rt_mm) */
+    uint16_t *phi, *plo;    /* null, or the operand planes of x: hi; lo for f32 rows */
+    float *pg;              /* with phi: P = -128 x the group sums, [n, H/64] */
+    int n, E, k, NW;
     float coef;             /* 2^-8 for rounded MFMA rows, 2^-12 for bf16 input */
 };
 
@@ -273,6 +290,32 @@ __global__ __launch_bounds__(256) void k_rt_exact(RtExactArgs a) {
     float v[NCH][8];
 #pragma unroll
     for (int i = 0; i < NCH; i++) load_x8<XBF16>(a.x, (size_t)t * H, lane + 64 * i, v[i]);
+    if (a.phi) {
+        /* the grouped GEMM's planes of this row: chunk lane + 64 i holds
+         * columns 8 (lane + 64 i) .. +7, so the 8 lanes of a 64-column group
+         * are adjacent, as the threads of k_pack_rows */
+#pragma unroll
+        for (int i = 0; i < NCH; i++) {
+            uint32_t ph[4], pl[4];
+            float gs = 0.0f;
+            if (XBF16) {
+                /* the rows' own bf16 (v holds them exactly) */
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    ph[j] = (__float_as_uint(v[i][j]) >> 16) | (__float_as_uint(v[i][j + 4]) & 0xFFFF0000u);
+#pragma unroll
+                for (int j = 0; j < 4; j++) gs = qk_dot2(ph[j], QK_BF16_ONES, gs);
+            } else {
+                qk_f32x8_to_pairs(v[i], ph, pl, gs);
+                ((uint4 *)a.plo)[(size_t)t * (H / 8) + lane + 64 * i] = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+            }
+            ((uint4 *)a.phi)[(size_t)t * (H / 8) + lane + 64 * i] = make_uint4(ph[0], ph[1], ph[2], ph[3]);
+            gs += qk_dpp<QK_DPP_XOR1>(gs);
+            gs += qk_dpp<QK_DPP_XOR2>(gs);
+            gs += __shfl_xor(gs, 4, QK_WAVE);
+            if ((lane & 7) == 0) a.pg[(size_t)t * (H / 64) + (lane >> 3) + 8 * i] = -128.0f * gs;
+        }
+    }
     float xs = 0.0f;
 #pragma unroll
     for (int i = 0; i < NCH; i++)
@@ -409,6 +452,8 @@ __global__ __launch_bounds__(256) void k_rt_exact(RtExactArgs a) {
     if (lane < a.k) {
         a.idx[(size_t)t * a.k + lane] = my_id;
         a.wt[(size_t)t * a.k + lane] = my_w;
+        /* ids outside [0, E) are not dispatched, as in k_setbits */
+        if (a.bits && (unsigned)my_id < (unsigned)a.E) atomicOr(&a.bits[(size_t)my_id * a.NW + (t >> 5)], 1u << (t & 31));
     }
     if (lane == 0) a.sg[t] = qk_sigmoid(res[C]);
 }
@@ -429,7 +474,8 @@ extern "C" int qk_route_mfma_ok(qk_shape s, int n) {
 
 extern "C" int qk_launch_route_mfma(const qmoe_layer_weights *W, qk_shape s, const void *x, int x_bf16,
                                     int n, float *logits, float *xn, uint16_t *plane, float *wn2,
-                                    int32_t *idx, float *w, float *sg, void *stream) {
+                                    int32_t *idx, float *w, float *sg, uint32_t *bits, uint16_t *phi,
+                                    uint16_t *plo, float *pg, void *stream) {
     if (n <= 0) return 0;
     if (!qk_route_mfma_ok(s, n)) return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)stream;
@@ -437,6 +483,9 @@ extern "C" int qk_launch_route_mfma(const qmoe_layer_weights *W, qk_shape s, con
     const bool norm = W->norm_w != nullptr;
     const bool as_is = x_bf16 && !norm; /* the MFMA reads x itself */
     if (norm && !xn) return (int)hipErrorInvalidValue;
+    /* the planes are of the rows k_rt_exact reads: f32 ones need lo too */
+    if (phi && (!pg || (!as_is && !plo))) return (int)hipErrorInvalidValue;
+    const int NW = (n + 31) / 32;
 
     RouterArgs ra;
     ra.router_w = W->router_w;
@@ -472,11 +521,13 @@ extern "C" int qk_launch_route_mfma(const qmoe_layer_weights *W, qk_shape s, con
     ma.bias = W->router_bias;
     ma.logits = logits;
     ma.wn2 = wn2;
+    ma.bits = (uint4 *)bits;
+    ma.nbits4 = bits ? s.E * NW / 4 : 0; /* E is a multiple of 64 */
     ma.n = n;
     ma.E = s.E;
     ma.tiles = (n + 63) / 64 * (s.E / 64);
     ma.per = (ma.tiles + 7) / 8;
-    const dim3 mgrid(8 * ma.per + (s.E + 31) / 32);
+    const dim3 mgrid(8 * ma.per);
     if (nch == 1) hipLaunchKernelGGL(k_rt_mm<1>, mgrid, dim3(256), 0, st, ma);
     else if (nch == 2) hipLaunchKernelGGL(k_rt_mm<2>, mgrid, dim3(256), 0, st, ma);
     else hipLaunchKernelGGL(k_rt_mm<4>, mgrid, dim3(256), 0, st, ma);
@@ -493,9 +544,14 @@ extern "C" int qk_launch_route_mfma(const qmoe_layer_weights *W, qk_shape s, con
     ea.idx = idx;
     ea.wt = w;
     ea.sg = sg;
+    ea.bits = bits;
+    ea.phi = phi;
+    ea.plo = as_is ? nullptr : plo;
+    ea.pg = pg;
     ea.n = n;
     ea.E = s.E;
     ea.k = s.k;
+    ea.NW = NW;
     ea.coef = as_is ? 0x1p-12f : 0x1p-8f;
     const dim3 egrid((n + 3) / 4);
 #define RTE_L(XB, NC, PL) hipLaunchKernelGGL((k_rt_exact<XB, NC, PL>), egrid, dim3(256), 0, st, ea)

@@ -774,16 +774,18 @@ __global__ void k_scatter(const int32_t *idx, int n, int k, int E, int NW, const
 
 extern "C" int qk_launch_dispatch(qk_shape s, int n, const int32_t *idx, int32_t *offsets,
                                   int32_t *perm, int32_t *pos, int32_t *segtab,
-                                  uint32_t *bits, int32_t *wprefix, int min_m, int32_t *tasks,
-                                  void *stream) {
+                                  uint32_t *bits, int bits_set, int32_t *wprefix, int min_m,
+                                  int32_t *tasks, void *stream) {
     hipStream_t st = (hipStream_t)stream;
     if (n <= 0) return 0;
     const int NW = (n + 31) / 32;
     const size_t nb = (size_t)s.E * NW;
-    hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, st, bits, nb, 0u);
     const int nk = n * s.k;
-    hipLaunchKernelGGL(k_setbits, dim3((nk + 255) / 256), dim3(256), 0, st, idx, n, s.k, s.E, NW,
-                       bits);
+    if (!bits_set) {
+        hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, st, bits, nb, 0u);
+        hipLaunchKernelGGL(k_setbits, dim3((nk + 255) / 256), dim3(256), 0, st, idx, n, s.k, s.E, NW,
+                           bits);
+    }
     hipLaunchKernelGGL(k_word_prefix, dim3((s.E + 15) / 16), dim3(1024), 0, st, (const uint32_t *)bits,
                        wprefix, s.E, NW, offsets);
     hipLaunchKernelGGL(k_count_offsets, dim3(1), dim3(1024), 0, st, s.E, offsets, segtab, perm, nk, n,
